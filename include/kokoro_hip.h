@@ -1,0 +1,184 @@
+/*
+ * kokoro_hip.h -- C ABI of the MI355X (gfx950) batched ragged Kokoro-82M decoder + iSTFTNet
+ * generator path.
+ *
+ * This library stands in for the reference's `crate::gpu` module (src/gpu.rs + src/gpu_batch.rs)
+ * on the path from the predicted durations to the audio.  Plain pointers and sizes only; every
+ * entry returns KK_OK (0) or a negative KK_ERR_* status and, where a buffer is given, a message.
+ * No entry aborts the process: device allocation failure is KK_ERR_OOM so a caller can split its
+ * batch and retry as Engine::synth_batch does (src/engine.rs:229-234).
+ *
+ * Threading: a context may be created on one thread and used from another (the reference creates
+ * its Gpu on a helper thread, src/engine.rs:92-96); every entry selects the context's device
+ * itself.  Calls on one context must not overlap (the reference engine is not shared,
+ * src/cli.rs:625-626).
+ */
+#ifndef KOKORO_HIP_H
+#define KOKORO_HIP_H
+#include <stddef.h>
+#include <stdint.h>
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KK_OK 0
+#define KK_ERR_INVALID (-1) /* bad argument or shape (src/gpu_batch.rs:181-187, src/gpu.rs:494-498) */
+#define KK_ERR_HIP (-2)     /* HIP runtime error */
+#define KK_ERR_OOM (-3)     /* device allocation failed */
+#define KK_ERR_STATE (-4)   /* model not uploaded / plan not run */
+
+typedef struct kk_ctx kk_ctx;
+typedef struct kk_plan kk_plan;
+
+/* ------------------------------------------------------------------ context (Gpu) */
+
+/* Gpu::new(ordinal) (src/gpu.rs:81-105): open device `ordinal`, create the stream, upload the
+ * STFT twiddles and window.  Refuses devices that are not gfx950. */
+int kk_open(int ordinal, kk_ctx** out, char* err, size_t errlen);
+void kk_close(kk_ctx* ctx);
+/* Gpu::device_name (src/gpu.rs:107-109). */
+int kk_device_name(const kk_ctx* ctx, char* buf, size_t len);
+/* Numerical identity of the engine, part of output provenance / resume keys
+ * (KERNEL_ROUNDING src/gpu.rs:29, Engine::identity src/engine.rs:109-111). */
+const char* kk_identity(void);
+
+/* ------------------------------------------------------------------ model (GpuKokoro::with_gpu) */
+
+/* One host tensor of the decoder + generator, by checkpoint state-dict name with weight_norm
+ * already resolved (the values the reference's host structs hold, src/vocoder.rs:54-111,
+ * src/nn.rs:25-166; e.g. "decoder.generator.resblocks.0.convs1.0.weight", f32, row-major). */
+typedef struct {
+    const char* name;
+    const float* data;
+    int64_t numel;
+} kk_tensor;
+
+/* GpuKokoro::with_gpu (src/gpu.rs:685-724), decoder + generator part: validates every shape,
+ * packs the conv weights into the MFMA operand layout (bf16), copies everything to the device.
+ * The tensors are copied; the caller keeps ownership. */
+int kk_upload_model(kk_ctx* ctx, const kk_tensor* tensors, int n, char* err, size_t errlen);
+
+/* ------------------------------------------------------------------ batch items */
+
+#define KK_NOISE_COUNTER 0 /* ItemNoise::Counter(seed) (src/gpu_batch.rs:15) */
+#define KK_NOISE_FIXED 1   /* ItemNoise::Fixed { rand_ini, sine } (src/gpu_batch.rs:16) */
+
+/* One item at the point where forward_batch enters the decoder (src/gpu_batch.rs:244-297): its
+ * predicted durations (pred_dur, src/model.rs:90-99), the text-encoder features of its tokens
+ * (t_en columns, channel-major [512][n_tok]), the F0 and energy curves at 2N (the predictor's
+ * F0/N outputs), its style ref_s (BatchItem::ref_s, 256 values; the decoder uses [0,128)) and its
+ * noise source. */
+typedef struct {
+    const int64_t* dur;   /* [n_tok], each >= 1; N = sum(dur) */
+    int32_t n_tok;
+    const float* t_en;    /* [512][n_tok] */
+    const float* f0;      /* [2N] */
+    const float* energy;  /* [2N] */
+    const float* ref_s;   /* [256] */
+    int32_t noise_kind;   /* KK_NOISE_* */
+    uint64_t seed;        /* counter seed (KK_NOISE_COUNTER) */
+    const float* rand_ini;/* [9]        (KK_NOISE_FIXED) */
+    const float* sine;    /* [600N * 9] (KK_NOISE_FIXED) */
+    int64_t sine_len;
+} kk_decoder_item;
+
+/* Output (src/model.rs:101-104): the item's audio, 600 N samples at 24 kHz, malloc'ed by the
+ * library and released by kk_output_free. */
+typedef struct {
+    float* audio;
+    int64_t n_samples;
+} kk_output;
+
+/* The decoder + generator part of GpuKokoro::forward_batch (src/gpu_batch.rs:250-420): ragged
+ * layout, duration expansion, decoder, harmonic source + STFT, generator, iSTFT, per-item audio in
+ * input order.  `out` is a caller array of n entries. */
+int kk_forward_decoder_batch(kk_ctx* ctx, const kk_decoder_item* items, int n, kk_output* out, char* err,
+                             size_t errlen);
+void kk_output_free(kk_output* out, int n);
+
+/* ------------------------------------------------------------------ plans (device-resident runs)
+ * kk_forward_decoder_batch = kk_plan_create + kk_plan_run + kk_plan_fetch + kk_plan_free.
+ * A plan builds the layout, uploads the inputs and allocates every device buffer once; kk_plan_run
+ * only enqueues kernels on the context's stream (no allocation, no host synchronization), so it
+ * can be timed with inputs already resident in HBM and run repeatedly. */
+int kk_plan_create(kk_ctx* ctx, const kk_decoder_item* items, int n, kk_plan** out, char* err, size_t errlen);
+/* Generator-only plan: per item the decoder output x [512][2N] channel-major,
+ * F0 [2N], ref_s [256], noise. */
+typedef struct {
+    const float* x;       /* [512][2N] */
+    int32_t n_frames;     /* N */
+    const float* f0;      /* [2N] */
+    const float* ref_s;   /* [256] */
+    int32_t noise_kind;
+    uint64_t seed;
+    const float* rand_ini;
+    const float* sine;
+    int64_t sine_len;
+} kk_generator_item;
+int kk_plan_create_generator(kk_ctx* ctx, const kk_generator_item* items, int n, kk_plan** out, char* err,
+                             size_t errlen);
+/* Snake-block plan: one AdaINResBlock1 (`prefix`, e.g.
+ * "decoder.generator.resblocks.1") over n ragged items x_b [C][t_b], packed with `gap` zero
+ * columns (snake_b, src/gpu_batch.rs:140-154). */
+int kk_plan_create_snake(kk_ctx* ctx, const char* prefix, const float* const* x, const int64_t* t,
+                         const float* const* ref_s, int n, int gap, kk_plan** out, char* err, size_t errlen);
+/* Enqueue the plan's kernels; `until` = KK_STAGE_ALL or an earlier stage (for stage taps). */
+#define KK_STAGE_DECODER 1
+#define KK_STAGE_SOURCE 2
+#define KK_STAGE_GEN0 3
+#define KK_STAGE_GEN1 4
+#define KK_STAGE_POST 5
+#define KK_STAGE_ALL 6
+int kk_plan_run(kk_plan* plan, int until, char* err, size_t errlen);
+int kk_plan_sync(kk_plan* plan, char* err, size_t errlen);
+/* Copy each item's result to the host (audio for decoder/generator plans, [C][t_b] for snake
+ * plans, as kk_output with n_samples = element count). */
+int kk_plan_fetch(kk_plan* plan, kk_output* out, char* err, size_t errlen);
+/* Copy a named device buffer of the last run to the host, per item and channel-major like the
+ * reference's host tensors: "asr" [512][N], "decoder" [512][2N], "spec" [22][120N+1],
+ * "gen0" [256][20N], "post" [22][120N+1], "audio" [600N].  `dst` receives item `item` only;
+ * `count` is its element count. */
+int kk_plan_tap(kk_plan* plan, const char* name, int item, float* dst, int64_t count, char* err, size_t errlen);
+typedef struct {
+    int64_t n_items;
+    int64_t ln;             /* frame-layout width (sum of N_b + 2) */
+    int64_t frames;         /* sum of N_b */
+    int64_t samples;        /* sum of 600 N_b */
+    double conv_flop;       /* algorithmic conv FLOP of one run (valid columns, 2 per MAC) */
+    double snake_flop;      /* of which in the Snake-block convs */
+    int64_t device_bytes;   /* device memory held by the plan */
+    int64_t launches;       /* kernels per run */
+} kk_plan_info;
+int kk_plan_get_info(const kk_plan* plan, kk_plan_info* info);
+void kk_plan_free(kk_plan* plan);
+
+/* ------------------------------------------------------------------ measurement
+ * With profiling on, kk_plan_run brackets every MFMA conv launch with HIP events on the
+ * context's stream; kk_profile_read reports, per kernel class, the summed event time and the
+ * algorithmic FLOP of those launches (classes: "snake_conv", "decoder_conv", "convt", "post_conv"). */
+int kk_set_profiling(kk_ctx* ctx, int on);
+typedef struct {
+    char name[32];
+    int64_t launches;
+    double ms;
+    double flop;
+} kk_profile_entry;
+int kk_profile_read(kk_ctx* ctx, kk_profile_entry* out, int max, int* n_out, char* err, size_t errlen);
+
+/* ------------------------------------------------------------------ host rules (bit-exact)
+ * durations_from_logits (src/model.rs:90-99): d_i = max(1, round_half_even(sum_j sigmoid(l_ij) /
+ * speed)) over [t][50] logits. */
+int kk_durations_from_logits(const float* logits, int t, float speed, int64_t* out);
+/* Frame layout (src/gpu_batch.rs:250-263): a[b] = sum_{j<b}(N_j + 2), returns ln. */
+int64_t kk_layout_frames(const int64_t* nfs, int n, int64_t* a_out);
+/* col_item of a domain of width l with item spans [start_b, start_b + len_b) (Dom::new,
+ * src/gpu_batch.rs:42-54); KK_ERR_INVALID on overflow or overlap. */
+int kk_layout_col_item(int64_t l, const int64_t* start, const int64_t* len, int n, int32_t* col_item);
+/* Frame -> token-row expansion table (src/gpu_batch.rs:265-276). */
+int kk_layout_src_row(const int64_t* const* dur, const int32_t* n_tok, int n, const int64_t* tstart,
+                      const int64_t* a, int64_t ln, int32_t* src_row);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,1269 @@
+// kk_engine.hip -- host side of the gfx950 decoder + generator path: context, model hydration,
+// ragged batch plans and the launch sequence, behind the C ABI of include/kokoro_hip.h.
+//
+// Reference structure being replaced: src/gpu.rs (Gpu, GConv/GConvT/GAdaIn/GResBlk/GSnakeBlk
+// hydration) and src/gpu_batch.rs (Dom layout and forward_batch from the durations on).
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "kk_common.h"
+#include "kk_kernels.h"
+#include "kokoro_hip.h"
+
+namespace kk {
+
+struct Err {
+    int code;
+    std::string msg;
+};
+
+[[noreturn]] static void fail(int code, const std::string& m) { throw Err{code, m}; }
+static void check(bool ok, const std::string& m) {
+    if (!ok) fail(KK_ERR_INVALID, m);
+}
+#define KK_HIP(x)                                                                                             \
+    do {                                                                                                      \
+        hipError_t e_ = (x);                                                                                  \
+        if (e_ != hipSuccess)                                                                                 \
+            ::kk::fail(e_ == hipErrorOutOfMemory ? KK_ERR_OOM : KK_ERR_HIP,                                   \
+                       std::string(#x) + ": " + hipGetErrorString(e_));                                       \
+    } while (0)
+
+// ------------------------------------------------------------------ device buffers
+struct DevBuf {
+    void* p = nullptr;
+    size_t bytes = 0;
+    DevBuf() = default;
+    DevBuf(const DevBuf&) = delete;
+    DevBuf& operator=(const DevBuf&) = delete;
+    DevBuf(DevBuf&& o) noexcept : p(o.p), bytes(o.bytes) { o.p = nullptr, o.bytes = 0; }
+    DevBuf& operator=(DevBuf&& o) noexcept {
+        release();
+        p = o.p, bytes = o.bytes;
+        o.p = nullptr, o.bytes = 0;
+        return *this;
+    }
+    ~DevBuf() { release(); }
+    void release() {
+        if (p) (void)hipFree(p);
+        p = nullptr, bytes = 0;
+    }
+    void alloc(size_t n) {
+        release();
+        if (n == 0) n = 16;
+        hipError_t e = hipMalloc(&p, n);
+        if (e != hipSuccess) {
+            p = nullptr;
+            (void)hipGetLastError();
+            fail(e == hipErrorOutOfMemory ? KK_ERR_OOM : KK_ERR_HIP,
+                 "hipMalloc(" + std::to_string(n) + " bytes): " + hipGetErrorString(e));
+        }
+        bytes = n;
+    }
+    template <class T>
+    void upload(const T* h, size_t count) {
+        alloc(count * sizeof(T));
+        if (count) KK_HIP(hipMemcpy(p, h, count * sizeof(T), hipMemcpyHostToDevice));
+    }
+    template <class T>
+    void upload(const std::vector<T>& v) {
+        upload(v.data(), v.size());
+    }
+    template <class T>
+    T* as() const {
+        return (T*)p;
+    }
+};
+
+static uint16_t bf16_bits(float f) {
+    uint32_t u;
+    std::memcpy(&u, &f, 4);
+    if ((u & 0x7f800000u) == 0x7f800000u) {
+        if (u & 0x007fffffu) u |= 0x00400000u;
+        return (uint16_t)(u >> 16);
+    }
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+static uint64_t splitmix_at(uint64_t seed, uint64_t ctr) {
+    uint64_t x = seed + (ctr + 1ull) * 0x9E3779B97F4A7C15ull;
+    x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+    x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+    return x ^ (x >> 31);
+}
+
+// ------------------------------------------------------------------ model on the device
+struct MConv {
+    DevBuf w, b;
+    int cin = 0, cin_pad = 0, cout = 0, m = 0, m_pad = 0, k = 0, dil = 1, pad = 0, shape = 0;
+    bool bias = false;
+};
+struct MAdain {
+    DevBuf nw, nb;
+    int c = 0, gb_off = 0;
+};
+struct MSnake {
+    MConv c1[3], c2[3];
+    MAdain a1[3], a2[3];
+    DevBuf ar1[3], ai1[3], ar2[3], ai2[3];
+    int c = 0;
+};
+struct MResblk {
+    MConv conv1, conv2, conv1x1;
+    bool has1x1 = false, up = false;
+    MAdain n1, n2;
+    DevBuf pool_w, pool_b;
+    int din = 0, dout = 0;
+};
+struct MNoiseConv {
+    DevBuf w, b;
+    int cout = 0, k = 0, stride = 1, pad = 0;
+};
+struct Model {
+    MResblk encode, decode[4];
+    DevBuf f0w, f0b, nw_, nb_;
+    MConv asr_res;
+    DevBuf lw;
+    float lb = 0.f;
+    MNoiseConv nc[2];
+    MSnake noise_res[2];
+    MConv ups[2];
+    int ups_stride[2] = {10, 6}, ups_pad[2] = {5, 3}, ups_cin[2] = {512, 256}, ups_cout[2] = {256, 128};
+    MSnake rb[6];
+    MConv post;
+    DevBuf style_wt, style_b;
+    int style_rows = 0;
+    bool ready = false;
+};
+
+struct ProfRec {
+    int cls;
+    double flop;
+    hipEvent_t e0, e1;
+};
+static const char* kProfNames[4] = {"snake_conv", "decoder_conv", "convt", "post_conv"};
+enum { PC_SNAKE = 0, PC_DECODER = 1, PC_CONVT = 2, PC_POST = 3 };
+
+}  // namespace kk
+
+struct kk_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::string name;
+    kk::Model model;
+    bool profiling = false;
+    std::vector<kk::ProfRec> prof;
+    std::vector<hipEvent_t> event_pool;
+};
+
+namespace kk {
+
+static int round_up(int v, int m) { return (v + m - 1) / m * m; }
+
+// Weight table lookup (names as the checkpoint's state dict).
+struct Table {
+    std::map<std::string, const kk_tensor*> byname;
+    const float* get(const std::string& name, int64_t numel) const {
+        auto it = byname.find(name);
+        check(it != byname.end(), "missing tensor " + name);
+        check(it->second->numel == numel, "tensor " + name + " has " + std::to_string(it->second->numel) +
+                                              " values, expected " + std::to_string(numel));
+        check(it->second->data != nullptr, "tensor " + name + " has no data");
+        return it->second->data;
+    }
+};
+
+// A stride-1 conv, w [cout][cin][k] -> packed [k][cin_pad/32][m_pad][32] bf16.
+static void load_conv(MConv& c, const Table& t, const std::string& p, int cin, int cout, int k, int pad, int dil,
+                      bool bias, int shape) {
+    c.cin = cin, c.cout = cout, c.k = k, c.pad = pad, c.dil = dil, c.shape = shape, c.bias = bias;
+    c.cin_pad = round_up(cin, 64);
+    c.m = cout;
+    c.m_pad = round_up(cout, conv_block_m(shape));
+    const float* w = t.get(p + ".weight", (int64_t)cout * cin * k);
+    const int ncc = c.cin_pad / 32;
+    std::vector<uint16_t> pk((size_t)k * ncc * c.m_pad * 32, 0);
+    for (int co = 0; co < cout; co++)
+        for (int ci = 0; ci < cin; ci++)
+            for (int kk = 0; kk < k; kk++)
+                pk[(((size_t)kk * ncc + ci / 32) * c.m_pad + co) * 32 + (ci & 31)] =
+                    bf16_bits(w[((size_t)co * cin + ci) * k + kk]);
+    c.w.upload(pk);
+    if (bias) {
+        std::vector<float> b(round_up(cout, 4), 0.f);
+        std::memcpy(b.data(), t.get(p + ".bias", cout), sizeof(float) * cout);
+        c.b.upload(b);
+    }
+}
+
+// ConvTranspose1d with K = 2 * stride as a 2-tap conv over input rows (i - 1, i) whose GEMM row
+// m = phase * cout + co produces output column stride * i + phase - pad (see kk_conv.hip).
+static void load_convt(MConv& c, const Table& t, const std::string& p, int cin, int cout, int kw, int stride) {
+    check(kw == 2 * stride, p + ": polyphase ConvT needs K = 2 * stride");
+    c.cin = cin, c.cout = cout, c.k = 2, c.pad = 1, c.dil = 1, c.shape = SHAPE_W4x2, c.bias = true;
+    c.cin_pad = round_up(cin, 64);
+    c.m = stride * cout;
+    c.m_pad = round_up(c.m, conv_block_m(c.shape));
+    const float* w = t.get(p + ".weight", (int64_t)cin * cout * kw);
+    const int ncc = c.cin_pad / 32;
+    std::vector<uint16_t> pk((size_t)2 * ncc * c.m_pad * 32, 0);
+    for (int tap = 0; tap < 2; tap++)
+        for (int r = 0; r < stride; r++)
+            for (int co = 0; co < cout; co++) {
+                const int m = r * cout + co, kk = tap == 0 ? r + stride : r;
+                for (int ci = 0; ci < cin; ci++)
+                    pk[(((size_t)tap * ncc + ci / 32) * c.m_pad + m) * 32 + (ci & 31)] =
+                        bf16_bits(w[((size_t)ci * cout + co) * kw + kk]);
+            }
+    c.w.upload(pk);
+    std::vector<float> b(round_up(cout, 4), 0.f);
+    std::memcpy(b.data(), t.get(p + ".bias", cout), sizeof(float) * cout);
+    c.b.upload(b);
+}
+
+struct StyleRows {
+    std::vector<float> wt_rows;  // [rows][128] (transposed at upload)
+    std::vector<float> bias;
+    int rows = 0;
+};
+
+static void load_adain(MAdain& a, const Table& t, const std::string& p, int c, StyleRows& sr) {
+    a.c = c;
+    a.nw.upload(t.get(p + ".norm.weight", c), c);
+    a.nb.upload(t.get(p + ".norm.bias", c), c);
+    const float* fw = t.get(p + ".fc.weight", (int64_t)2 * c * kStyleDim);
+    const float* fb = t.get(p + ".fc.bias", 2 * c);
+    a.gb_off = sr.rows;
+    sr.wt_rows.insert(sr.wt_rows.end(), fw, fw + (size_t)2 * c * kStyleDim);
+    sr.bias.insert(sr.bias.end(), fb, fb + 2 * c);
+    sr.rows += 2 * c;
+}
+
+// AdaInResBlock1::load (src/nn.rs:154-165): convs1 pad (k d - d) / 2 dil d; convs2 pad (k - 1) / 2.
+static void load_snake(MSnake& s, const Table& t, const std::string& p, int c, int k, StyleRows& sr) {
+    static const int dil[3] = {1, 3, 5};
+    s.c = c;
+    const int shape = c >= 256 ? SHAPE_W4x2 : SHAPE_W2x4;
+    for (int i = 0; i < 3; i++) {
+        const std::string si = std::to_string(i);
+        load_conv(s.c1[i], t, p + ".convs1." + si, c, c, k, (k * dil[i] - dil[i]) / 2, dil[i], true, shape);
+        load_conv(s.c2[i], t, p + ".convs2." + si, c, c, k, (k - 1) / 2, 1, true, shape);
+        load_adain(s.a1[i], t, p + ".adain1." + si, c, sr);
+        load_adain(s.a2[i], t, p + ".adain2." + si, c, sr);
+        for (int j = 0; j < 2; j++) {
+            const float* al = t.get(p + (j ? ".alpha2." : ".alpha1.") + si, c);
+            std::vector<float> rev(c), inv(c);
+            for (int ch = 0; ch < c; ch++) {
+                check(al[ch] != 0.f && std::isfinite(al[ch]), p + ": Snake alpha must be finite and nonzero");
+                rev[ch] = (float)((double)al[ch] / (2.0 * M_PI));
+                inv[ch] = 1.0f / al[ch];
+            }
+            (j ? s.ar2[i] : s.ar1[i]).upload(rev);
+            (j ? s.ai2[i] : s.ai1[i]).upload(inv);
+        }
+    }
+}
+
+// AdainResBlk1d::load (src/nn.rs:119-140).
+static void load_resblk(MResblk& r, const Table& t, const std::string& p, int din, int dout, bool up,
+                        StyleRows& sr) {
+    r.din = din, r.dout = dout, r.up = up;
+    load_conv(r.conv1, t, p + ".conv1", din, dout, 3, 1, 1, true, SHAPE_W4x2);
+    load_conv(r.conv2, t, p + ".conv2", dout, dout, 3, 1, 1, true, SHAPE_W4x2);
+    load_adain(r.n1, t, p + ".norm1", din, sr);
+    load_adain(r.n2, t, p + ".norm2", dout, sr);
+    r.has1x1 = din != dout;
+    if (r.has1x1) load_conv(r.conv1x1, t, p + ".conv1x1", din, dout, 1, 0, 1, false, SHAPE_W4x2);
+    if (up) {
+        r.pool_w.upload(t.get(p + ".pool.weight", (int64_t)din * 3), (size_t)din * 3);
+        r.pool_b.upload(t.get(p + ".pool.bias", din), din);
+    }
+}
+
+static void load_model(kk_ctx* ctx, const kk_tensor* tensors, int n) {
+    Table t;
+    for (int i = 0; i < n; i++) {
+        check(tensors[i].name != nullptr, "tensor without a name");
+        t.byname[tensors[i].name] = &tensors[i];
+    }
+    Model& m = ctx->model;
+    m.ready = false;
+    StyleRows sr;
+    // Shapes: Decoder::load / Generator::load (src/vocoder.rs:54-111).
+    load_resblk(m.encode, t, "decoder.encode", 514, 1024, false, sr);
+    for (int i = 0; i < 4; i++)
+        load_resblk(m.decode[i], t, "decoder.decode." + std::to_string(i), 1090, i == 3 ? 512 : 1024, i == 3, sr);
+    m.f0w.upload(t.get("decoder.F0_conv.weight", 3), 3);
+    m.f0b.upload(t.get("decoder.F0_conv.bias", 1), 1);
+    m.nw_.upload(t.get("decoder.N_conv.weight", 3), 3);
+    m.nb_.upload(t.get("decoder.N_conv.bias", 1), 1);
+    load_conv(m.asr_res, t, "decoder.asr_res.0", 512, 64, 1, 0, 1, true, SHAPE_W1x4);
+    const std::string g = "decoder.generator";
+    m.lw.upload(t.get(g + ".m_source.l_linear.weight", kHarmonics), kHarmonics);
+    m.lb = t.get(g + ".m_source.l_linear.bias", 1)[0];
+    const int nc_cout[2] = {256, 128}, nc_k[2] = {12, 1}, nc_s[2] = {6, 1}, nc_p[2] = {3, 0};
+    for (int i = 0; i < 2; i++) {
+        const std::string p = g + ".noise_convs." + std::to_string(i);
+        MNoiseConv& c = m.nc[i];
+        c.cout = nc_cout[i], c.k = nc_k[i], c.stride = nc_s[i], c.pad = nc_p[i];
+        c.w.upload(t.get(p + ".weight", (int64_t)c.cout * 22 * c.k), (size_t)c.cout * 22 * c.k);
+        c.b.upload(t.get(p + ".bias", c.cout), c.cout);
+    }
+    load_snake(m.noise_res[0], t, g + ".noise_res.0", 256, 7, sr);
+    load_snake(m.noise_res[1], t, g + ".noise_res.1", 128, 11, sr);
+    load_convt(m.ups[0], t, g + ".ups.0", 512, 256, 20, 10);
+    load_convt(m.ups[1], t, g + ".ups.1", 256, 128, 12, 6);
+    static const int ks[3] = {3, 7, 11};
+    for (int i = 0; i < 6; i++)
+        load_snake(m.rb[i], t, g + ".resblocks." + std::to_string(i), i < 3 ? 256 : 128, ks[i % 3], sr);
+    load_conv(m.post, t, g + ".conv_post", 128, 22, 7, 3, 1, true, SHAPE_W1x4);
+    // style projections of every AdaIN, transposed [128][rows]
+    std::vector<float> wt((size_t)kStyleDim * sr.rows);
+    for (int r = 0; r < sr.rows; r++)
+        for (int k = 0; k < kStyleDim; k++) wt[(size_t)k * sr.rows + r] = sr.wt_rows[(size_t)r * kStyleDim + k];
+    m.style_wt.upload(wt);
+    m.style_b.upload(sr.bias);
+    m.style_rows = sr.rows;
+    KK_HIP(hipDeviceSynchronize());
+    m.ready = true;
+}
+
+// ------------------------------------------------------------------ plans
+struct Dom {
+    int64_t l = 0;
+    std::vector<int64_t> start, len;
+    std::vector<int32_t> col;
+    DevBuf col_d, start_d, len_d;
+    int64_t valid() const {
+        int64_t s = 0;
+        for (auto v : len) s += v;
+        return s;
+    }
+    // Dom::new (src/gpu_batch.rs:42-54): col_item per column, overflow / overlap are errors.
+    void build(int64_t l_, std::vector<int64_t> st, std::vector<int64_t> ln) {
+        l = l_, start = std::move(st), len = std::move(ln);
+        col.assign(l, -1);
+        for (size_t b = 0; b < start.size(); b++) {
+            check(start[b] >= 0 && len[b] >= 0 && start[b] + len[b] <= l, "layout overflow");
+            for (int64_t t = start[b]; t < start[b] + len[b]; t++) {
+                check(col[t] < 0, "overlapping item spans");
+                col[t] = (int32_t)b;
+            }
+        }
+        col_d.upload(col);
+        start_d.upload(start);
+        len_d.upload(len);
+    }
+    DomDev dev() const { return DomDev{l, col_d.as<int32_t>(), start_d.as<int64_t>(), len_d.as<int64_t>(), (int)start.size()}; }
+};
+
+enum PlanKind { PLAN_DECODER = 0, PLAN_GENERATOR = 1, PLAN_SNAKE = 2 };
+
+}  // namespace kk
+
+struct kk_plan {
+    kk_ctx* ctx = nullptr;
+    int kind = 0;
+    int nb = 0;
+    std::vector<int64_t> nfr;  // N_b
+    std::vector<int64_t> a;    // frame layout starts
+    int64_t ln = 0;
+    kk::Dom dn, d2, d20, d120, ds;
+    // snake plans
+    const kk::MSnake* sblk = nullptr;
+    int sc = 0;
+    // inputs
+    kk::DevBuf t_en, src_row, f0, en, style, seeds, kinds, rand_ini, fixed_noise;
+    int64_t t_rows = 0;
+    // intermediates
+    kk::DevBuf gb, xcat, xin_a, xin_b, hdec, pool, sc_half, dec_out, pp, spec, B[6], post, audio, audio_start;
+    kk::DevBuf sums, coef[3];
+    kk::DevBuf src_item, src_f0, ist_item, ist_s0;
+    int64_t n_src = 0, n_ist = 0;
+    int64_t dev_bytes = 0;
+    double conv_flop = 0, snake_flop = 0;
+    int64_t launches = 0;
+    int last_until = 0;
+    std::vector<kk::DevBuf*> owned() {
+        return {&t_en, &src_row, &f0, &en, &style, &seeds, &kinds, &rand_ini, &fixed_noise, &gb, &xcat, &xin_a,
+                &xin_b, &hdec, &pool, &sc_half, &dec_out, &pp, &spec, &B[0], &B[1], &B[2], &B[3], &B[4], &B[5],
+                &post, &audio, &audio_start, &sums, &coef[0], &coef[1], &coef[2], &src_item, &src_f0, &ist_item,
+                &ist_s0};
+    }
+};
+
+namespace kk {
+
+constexpr int kGapN = 2;  // GAP_N (src/gpu_batch.rs:27)
+constexpr int kGapT = 2;  // GAP_T (src/gpu_batch.rs:29)
+constexpr int64_t kXcatLd = 576, kXinLd = 1152, kSpecLd = 32, kPostLd = 32;
+
+static void alloc_zero(kk_plan* p, DevBuf& b, size_t bytes) {
+    b.alloc(bytes);
+    KK_HIP(launch_zero(b.p, (int64_t)((bytes + 3) / 4 * 4), p->ctx->stream));
+}
+
+// Layout shared by decoder and generator plans (src/gpu_batch.rs:250-263).
+static void build_frame_layout(kk_plan* p) {
+    p->a.resize(p->nb);
+    int64_t ln = 0;
+    for (int b = 0; b < p->nb; b++) {
+        p->a[b] = ln;
+        ln += p->nfr[b] + kGapN;
+    }
+    p->ln = ln;
+    auto scale = [&](int64_t f) {
+        std::vector<int64_t> v(p->nb);
+        for (int b = 0; b < p->nb; b++) v[b] = p->a[b] * f;
+        return v;
+    };
+    auto lens = [&](int64_t f, int64_t add) {
+        std::vector<int64_t> v(p->nb);
+        for (int b = 0; b < p->nb; b++) v[b] = p->nfr[b] * f + add;
+        return v;
+    };
+    p->dn.build(ln, scale(1), lens(1, 0));
+    p->d2.build(2 * ln, scale(2), lens(2, 0));
+    p->d20.build(20 * ln, scale(20), lens(20, 0));
+    p->d120.build(120 * ln + 1, scale(120), lens(120, 1));
+}
+
+struct NoiseIn {
+    int32_t kind;
+    uint64_t seed;
+    const float* rand_ini;
+    const float* sine;
+    int64_t sine_len;
+};
+
+// Generator inputs: F0 at d2, styles, noise (src/gpu_batch.rs:319-341) and all generator buffers.
+static void setup_generator(kk_plan* p, const std::vector<const float*>& f0s, const std::vector<const float*>& ref_s,
+                            const std::vector<NoiseIn>& noise) {
+    const int nb = p->nb;
+    const int64_t ln = p->ln, l2 = 2 * ln, l20 = 20 * ln, l120 = 120 * ln + 1;
+    hipStream_t s = p->ctx->stream;
+    std::vector<float> f0h(l2, 0.f);
+    for (int b = 0; b < nb; b++) std::memcpy(&f0h[2 * p->a[b]], f0s[b], sizeof(float) * 2 * p->nfr[b]);
+    p->f0.upload(f0h);
+    std::vector<float> st((size_t)nb * kStyleDim);
+    for (int b = 0; b < nb; b++) std::memcpy(&st[(size_t)b * kStyleDim], ref_s[b], sizeof(float) * kStyleDim);
+    p->style.upload(st);
+    std::vector<uint64_t> seeds(nb);
+    std::vector<int32_t> kinds(nb);
+    std::vector<float> ri((size_t)nb * kHarmonics);
+    bool any_fixed = false;
+    for (int b = 0; b < nb; b++) {
+        seeds[b] = noise[b].seed;
+        kinds[b] = noise[b].kind;
+        if (noise[b].kind == KK_NOISE_COUNTER) {
+            // RngNoise::rand_ini (src/vocoder.rs:34-40)
+            for (int h = 0; h < kHarmonics; h++)
+                ri[(size_t)b * kHarmonics + h] =
+                    (float)(splitmix_at(noise[b].seed, (uint64_t)h) >> 40) * (1.0f / 16777216.0f);
+        } else {
+            any_fixed = true;
+            std::memcpy(&ri[(size_t)b * kHarmonics], noise[b].rand_ini, sizeof(float) * kHarmonics);
+        }
+    }
+    p->seeds.upload(seeds);
+    p->kinds.upload(kinds);
+    p->rand_ini.upload(ri);
+    if (any_fixed) {
+        std::vector<float> fx((size_t)600 * ln * kHarmonics, 0.f);
+        for (int b = 0; b < nb; b++)
+            if (noise[b].kind == KK_NOISE_FIXED)
+                std::memcpy(&fx[(size_t)600 * p->a[b] * kHarmonics], noise[b].sine,
+                            sizeof(float) * 600 * p->nfr[b] * kHarmonics);
+        p->fixed_noise.upload(fx);
+    }
+    // work lists of the one-launch source+STFT and iSTFT kernels
+    std::vector<int64_t> si, sf, ii, is;
+    for (int b = 0; b < nb; b++) {
+        const int64_t frames = 120 * p->nfr[b] + 1, samples = 600 * p->nfr[b];
+        for (int64_t f = 0; f < frames; f += kSourceFrames) si.push_back(b), sf.push_back(f);
+        for (int64_t q = 0; q < samples; q += kIstftSamples) ii.push_back(b), is.push_back(q);
+    }
+    p->n_src = (int64_t)si.size(), p->n_ist = (int64_t)ii.size();
+    p->src_item.upload(si), p->src_f0.upload(sf), p->ist_item.upload(ii), p->ist_s0.upload(is);
+    std::vector<int64_t> as(nb);
+    for (int b = 0; b < nb; b++) as[b] = 600 * p->a[b];
+    p->audio_start.upload(as);
+
+    p->gb.alloc((size_t)nb * p->ctx->model.style_rows * sizeof(float));
+    p->pp.alloc((size_t)kHarmonics * l2 * sizeof(float));
+    alloc_zero(p, p->spec, (size_t)l120 * kSpecLd * sizeof(float));
+    const size_t big = (size_t)std::max(l20 * 256, l120 * 128) * sizeof(float);
+    for (int i = 0; i < 6; i++) alloc_zero(p, p->B[i], big);
+    alloc_zero(p, p->post, (size_t)l120 * kPostLd * sizeof(float));
+    alloc_zero(p, p->audio, (size_t)600 * ln * sizeof(float));
+    alloc_zero(p, p->sums, (size_t)nb * kXinLd * 2 * sizeof(double));
+    for (int i = 0; i < 3; i++) p->coef[i].alloc((size_t)nb * kXinLd * sizeof(Coef));
+}
+
+static void finish_plan(kk_plan* p) {
+    KK_HIP(hipStreamSynchronize(p->ctx->stream));
+    p->dev_bytes = 0;
+    for (DevBuf* b : p->owned()) p->dev_bytes += (int64_t)b->bytes;
+    for (kk::Dom* d : {&p->dn, &p->d2, &p->d20, &p->d120, &p->ds})
+        p->dev_bytes += (int64_t)(d->col_d.bytes + d->start_d.bytes + d->len_d.bytes);
+}
+
+static void check_noise(const NoiseIn& nz, int64_t n_frames, int b) {
+    const std::string sb = std::to_string(b);
+    check(nz.kind == KK_NOISE_COUNTER || nz.kind == KK_NOISE_FIXED, "item " + sb + ": unknown noise kind");
+    if (nz.kind == KK_NOISE_FIXED) {
+        check(nz.rand_ini && nz.sine, "item " + sb + ": fixed noise needs rand_ini and sine");
+        // src/gpu_batch.rs:338: fixed noise size mismatch is an error
+        check(nz.sine_len == 600 * n_frames * kHarmonics, "fixed noise size mismatch for item " + sb);
+    }
+}
+
+static kk_plan* create_decoder_plan(kk_ctx* ctx, const kk_decoder_item* items, int n) {
+    check(ctx->model.ready, "no model uploaded");
+    check(items != nullptr && n > 0, "empty batch");
+    auto p = std::make_unique<kk_plan>();
+    p->ctx = ctx, p->kind = PLAN_DECODER, p->nb = n;
+    std::vector<int64_t> tstart(n);
+    int64_t rows = 0;
+    for (int b = 0; b < n; b++) {
+        const kk_decoder_item& it = items[b];
+        const std::string sb = std::to_string(b);
+        check(it.dur && it.t_en && it.f0 && it.energy && it.ref_s, "item " + sb + ": null input");
+        check(it.n_tok >= 1, "item " + sb + ": no tokens");
+        int64_t nf = 0;
+        for (int i = 0; i < it.n_tok; i++) {
+            check(it.dur[i] >= 1, "item " + sb + ": durations must be >= 1");
+            nf += it.dur[i];
+        }
+        check(nf <= (int64_t)1 << 22, "item " + sb + ": too many frames");
+        check_noise(NoiseIn{it.noise_kind, it.seed, it.rand_ini, it.sine, it.sine_len}, nf, b);
+        p->nfr.push_back(nf);
+        tstart[b] = rows;  // token layout (src/gpu_batch.rs:188-197)
+        rows += it.n_tok + kGapT;
+    }
+    build_frame_layout(p.get());
+    const int64_t ln = p->ln;
+    // t_en in the token layout, channel-major [512][rows] (text_encoder_b output convention)
+    p->t_rows = rows;
+    {
+        std::vector<float> te((size_t)512 * rows, 0.f);
+        for (int b = 0; b < n; b++)
+            for (int c = 0; c < 512; c++)
+                std::memcpy(&te[(size_t)c * rows + tstart[b]], items[b].t_en + (size_t)c * items[b].n_tok,
+                            sizeof(float) * items[b].n_tok);
+        p->t_en.upload(te);
+    }
+    // frame -> token row table (src/gpu_batch.rs:265-276)
+    {
+        std::vector<int32_t> sr(ln, -1);
+        for (int b = 0; b < n; b++) {
+            int64_t f = p->a[b];
+            for (int tok = 0; tok < items[b].n_tok; tok++)
+                for (int64_t r = 0; r < items[b].dur[tok]; r++) sr[f++] = (int32_t)(tstart[b] + tok);
+        }
+        p->src_row.upload(sr);
+    }
+    {
+        std::vector<float> eh(2 * ln, 0.f);
+        for (int b = 0; b < n; b++) std::memcpy(&eh[2 * p->a[b]], items[b].energy, sizeof(float) * 2 * p->nfr[b]);
+        p->en.upload(eh);
+    }
+    std::vector<const float*> f0s(n), refs(n);
+    std::vector<NoiseIn> nz(n);
+    for (int b = 0; b < n; b++) {
+        f0s[b] = items[b].f0, refs[b] = items[b].ref_s;
+        nz[b] = NoiseIn{items[b].noise_kind, items[b].seed, items[b].rand_ini, items[b].sine, items[b].sine_len};
+    }
+    setup_generator(p.get(), f0s, refs, nz);
+    alloc_zero(p.get(), p->xcat, (size_t)ln * kXcatLd * sizeof(float));
+    alloc_zero(p.get(), p->xin_a, (size_t)ln * kXinLd * sizeof(float));
+    alloc_zero(p.get(), p->xin_b, (size_t)ln * kXinLd * sizeof(float));
+    alloc_zero(p.get(), p->hdec, (size_t)ln * 1024 * sizeof(float));
+    alloc_zero(p.get(), p->pool, (size_t)2 * ln * kXinLd * sizeof(uint16_t));
+    alloc_zero(p.get(), p->sc_half, (size_t)ln * 512 * sizeof(float));
+    alloc_zero(p.get(), p->dec_out, (size_t)2 * ln * 512 * sizeof(float));
+    finish_plan(p.get());
+    return p.release();
+}
+
+static kk_plan* create_generator_plan(kk_ctx* ctx, const kk_generator_item* items, int n) {
+    check(ctx->model.ready, "no model uploaded");
+    check(items != nullptr && n > 0, "empty batch");
+    auto p = std::make_unique<kk_plan>();
+    p->ctx = ctx, p->kind = PLAN_GENERATOR, p->nb = n;
+    for (int b = 0; b < n; b++) {
+        const std::string sb = std::to_string(b);
+        check(items[b].x && items[b].f0 && items[b].ref_s, "item " + sb + ": null input");
+        check(items[b].n_frames >= 1 && items[b].n_frames <= (1 << 22), "item " + sb + ": frames out of range");
+        check_noise(NoiseIn{items[b].noise_kind, items[b].seed, items[b].rand_ini, items[b].sine, items[b].sine_len},
+                    items[b].n_frames, b);
+        p->nfr.push_back(items[b].n_frames);
+    }
+    build_frame_layout(p.get());
+    std::vector<const float*> f0s(n), refs(n);
+    std::vector<NoiseIn> nz(n);
+    for (int b = 0; b < n; b++) {
+        f0s[b] = items[b].f0, refs[b] = items[b].ref_s;
+        nz[b] = NoiseIn{items[b].noise_kind, items[b].seed, items[b].rand_ini, items[b].sine, items[b].sine_len};
+    }
+    setup_generator(p.get(), f0s, refs, nz);
+    // decoder output x [512][2N] per item -> time-major d2 rows
+    const int64_t l2 = 2 * p->ln;
+    std::vector<float> xh((size_t)l2 * 512, 0.f);
+    for (int b = 0; b < n; b++) {
+        const int64_t t2 = 2 * p->nfr[b];
+        for (int c = 0; c < 512; c++)
+            for (int64_t t = 0; t < t2; t++) xh[(size_t)(2 * p->a[b] + t) * 512 + c] = items[b].x[(size_t)c * t2 + t];
+    }
+    p->dec_out.upload(xh);
+    finish_plan(p.get());
+    return p.release();
+}
+
+static const MSnake* find_snake(const Model& m, const std::string& prefix) {
+    for (int i = 0; i < 2; i++)
+        if (prefix == "decoder.generator.noise_res." + std::to_string(i)) return &m.noise_res[i];
+    for (int i = 0; i < 6; i++)
+        if (prefix == "decoder.generator.resblocks." + std::to_string(i)) return &m.rb[i];
+    return nullptr;
+}
+
+static kk_plan* create_snake_plan(kk_ctx* ctx, const char* prefix, const float* const* x, const int64_t* t,
+                                  const float* const* ref_s, int n, int gap) {
+    check(ctx->model.ready, "no model uploaded");
+    check(prefix && x && t && ref_s && n > 0 && gap >= 0, "bad arguments");
+    const MSnake* blk = find_snake(ctx->model, prefix);
+    check(blk != nullptr, std::string("no Snake block named ") + prefix);
+    auto p = std::make_unique<kk_plan>();
+    p->ctx = ctx, p->kind = PLAN_SNAKE, p->nb = n, p->sblk = blk, p->sc = blk->c;
+    // receptive field of one dilation step: (k - 1) * 5 / 2 + (k - 1) / 2 columns
+    const int k = blk->c1[0].k;
+    check(gap >= (k - 1) * 5 / 2, "gap narrower than the block's conv reach");
+    std::vector<int64_t> st(n), ln(n);
+    int64_t l = 0;
+    for (int b = 0; b < n; b++) {
+        check(x[b] && ref_s[b] && t[b] >= 1, "item " + std::to_string(b) + ": bad input");
+        st[b] = l, ln[b] = t[b];
+        p->nfr.push_back(t[b]);
+        l += t[b] + gap;
+    }
+    p->ds.build(l, st, ln);
+    const int c = blk->c;
+    std::vector<float> xh((size_t)l * c, 0.f);
+    for (int b = 0; b < n; b++)
+        for (int ch = 0; ch < c; ch++)
+            for (int64_t i = 0; i < t[b]; i++) xh[(size_t)(st[b] + i) * c + ch] = x[b][(size_t)ch * t[b] + i];
+    p->B[0].upload(xh);
+    std::vector<float> sth((size_t)n * kStyleDim);
+    for (int b = 0; b < n; b++) std::memcpy(&sth[(size_t)b * kStyleDim], ref_s[b], sizeof(float) * kStyleDim);
+    p->style.upload(sth);
+    p->gb.alloc((size_t)n * ctx->model.style_rows * sizeof(float));
+    alloc_zero(p.get(), p->B[1], (size_t)l * c * sizeof(float));
+    alloc_zero(p.get(), p->sums, (size_t)n * c * 2 * sizeof(double));
+    p->coef[0].alloc((size_t)n * c * sizeof(Coef));
+    finish_plan(p.get());
+    return p.release();
+}
+
+// ------------------------------------------------------------------ the launch sequence
+struct Runner {
+    kk_plan* p;
+    kk_ctx* ctx;
+    const Model& m;
+    hipStream_t s;
+    double flop = 0, snake_flop = 0;
+    int64_t launches = 0;
+    int64_t gb_ld() const { return m.style_rows; }
+
+    hipEvent_t ev() {
+        if (!ctx->event_pool.empty()) {
+            hipEvent_t e = ctx->event_pool.back();
+            ctx->event_pool.pop_back();
+            return e;
+        }
+        hipEvent_t e;
+        KK_HIP(hipEventCreate(&e));
+        return e;
+    }
+
+    void stats_fin(const float* x, int64_t ld, int c, const Dom& d, const MAdain& a, Coef* coef, bool stats = true,
+                   int reset = 1) {
+        if (stats) {
+            KK_HIP(launch_stats(x, ld, c, d.dev(), p->sums.as<double>(), s));
+            launches++;
+        }
+        KK_HIP(launch_finalize(x, ld, c, d.dev(), p->sums.as<double>(), p->gb.as<float>(), gb_ld(), a.gb_off,
+                               a.nw.as<float>(), a.nb.as<float>(), coef, reset, s));
+        launches++;
+    }
+
+    // One MFMA conv launch; `valid` = algorithmic columns (FLOP accounting).
+    void conv(const MConv& c, int pro, int epi, const void* x, int64_t x_ld, int64_t l_in, const int32_t* col_in,
+              float* y, int64_t y_ld, int64_t n_out, double valid, int cls, const Coef* coef = nullptr,
+              const DevBuf* ar = nullptr, const DevBuf* ai = nullptr, float slope = 0.f, const float* r0 = nullptr,
+              const float* r1 = nullptr, const float* r2 = nullptr, int64_t r0_ld = 0, float scale = 1.f,
+              int stride_t = 1, int pad_t = 0, int64_t l_convt = 0, const Dom* dpad = nullptr) {
+        ConvParams q{};
+        q.x = x, q.x_ld = x_ld, q.l_in = l_in, q.cin = c.cin, q.cin_pad = c.cin_pad, q.col_in = col_in;
+        q.coef = coef, q.alpha_rev = ar ? ar->as<float>() : nullptr, q.alpha_inv = ai ? ai->as<float>() : nullptr;
+        q.slope = slope, q.w = c.w.as<uint16_t>(), q.bias = c.bias ? c.b.as<float>() : nullptr;
+        q.m = c.m, q.m_pad = c.m_pad, q.k = c.k, q.dil = c.dil, q.pad = c.pad;
+        q.y = y, q.y_ld = y_ld, q.cout = c.cout, q.n_out = n_out;
+        q.r0 = r0, q.r1 = r1, q.r2 = r2, q.r0_ld = r0_ld, q.scale = scale;
+        q.stride_t = stride_t, q.pad_t = pad_t, q.l_convt = l_convt;
+        q.col_out = dpad ? dpad->col_d.as<int32_t>() : nullptr;
+        q.start_out = dpad ? dpad->start_d.as<int64_t>() : nullptr;
+        // ConvT (K = 2 stride): every input column feeds K x cout outputs = 2 m MACs per channel
+        const bool convt = epi == EPI_CONVT || epi == EPI_CONVT_REFLECT;
+        const double f = 2.0 * (double)c.cin * valid * (convt ? 2.0 * c.m : (double)c.cout * c.k);
+        flop += f;
+        if (cls == PC_SNAKE) snake_flop += f;
+        hipEvent_t e0 = nullptr, e1 = nullptr;
+        if (ctx->profiling) {
+            e0 = ev(), e1 = ev();
+            KK_HIP(hipEventRecord(e0, s));
+        }
+        KK_HIP(launch_conv(q, pro, epi, c.shape, s));
+        launches++;
+        if (ctx->profiling) {
+            KK_HIP(hipEventRecord(e1, s));
+            ctx->prof.push_back(ProfRec{cls, f, e0, e1});
+        }
+    }
+
+    // snake_b (src/gpu_batch.rs:140-154) in place on X.
+    void snake_block(const MSnake& blk, float* X, float* h, const Dom& d) {
+        const int c = blk.c;
+        const double valid = (double)d.valid();
+        Coef* cf = p->coef[0].as<Coef>();
+        for (int i = 0; i < 3; i++) {
+            stats_fin(X, c, c, d, blk.a1[i], cf);
+            conv(blk.c1[i], PRO_ADAIN_SNAKE, EPI_STORE, X, c, d.l, d.col_d.as<int32_t>(), h, c, d.l, valid, PC_SNAKE,
+                 cf, &blk.ar1[i], &blk.ai1[i]);
+            stats_fin(h, c, c, d, blk.a2[i], cf);
+            conv(blk.c2[i], PRO_ADAIN_SNAKE, EPI_ACCUM, h, c, d.l, d.col_d.as<int32_t>(), X, c, d.l, valid, PC_SNAKE,
+                 cf, &blk.ar2[i], &blk.ai2[i]);
+        }
+    }
+
+    // x = (rb0(y) + rb1(y) + rb2(y)) / 3 (src/gpu_batch.rs:395-401); result in X[2].
+    void resblock_mean(const MSnake* rbs, const float* y, float* X[3], float* h, const Dom& d) {
+        const int c = rbs[0].c;
+        const double valid = (double)d.valid();
+        const int32_t* col = d.col_d.as<int32_t>();
+        // the three blocks' first AdaIN share one statistics pass over y
+        KK_HIP(launch_stats(y, c, c, d.dev(), p->sums.as<double>(), s));
+        launches++;
+        for (int j = 0; j < 3; j++) stats_fin(y, c, c, d, rbs[j].a1[0], p->coef[j].as<Coef>(), false, j == 2);
+        Coef* cf = p->coef[0].as<Coef>();
+        for (int j = 0; j < 3; j++) {
+            const MSnake& blk = rbs[j];
+            for (int i = 0; i < 3; i++) {
+                const float* in = i == 0 ? y : X[j];
+                const Coef* c1 = i == 0 ? p->coef[j].as<Coef>() : cf;
+                if (i > 0) stats_fin(X[j], c, c, d, blk.a1[i], cf);
+                conv(blk.c1[i], PRO_ADAIN_SNAKE, EPI_STORE, in, c, d.l, col, h, c, d.l, valid, PC_SNAKE, c1,
+                     &blk.ar1[i], &blk.ai1[i]);
+                // coef[0] may still hold the shared coefficients of block 0 (used above): the
+                // conv1 launch has been enqueued before this overwrite, stream order keeps it safe
+                stats_fin(h, c, c, d, blk.a2[i], cf);
+                int epi = EPI_ACCUM;
+                const float *r0 = nullptr, *r1 = nullptr, *r2 = nullptr;
+                if (i == 0) epi = EPI_ADD_FROM, r0 = y;
+                if (j == 2 && i == 2) epi = EPI_MEAN3, r0 = X[0], r1 = X[1], r2 = X[2];
+                conv(blk.c2[i], PRO_ADAIN_SNAKE, epi, h, c, d.l, col, X[j], c, d.l, valid, PC_SNAKE, cf, &blk.ar2[i],
+                     &blk.ai2[i], 0.f, r0, r1, r2, c);
+            }
+        }
+    }
+
+    // AdainResBlk1d (src/gpu_batch.rs:104-135) without upsampling: in [ln][in_ld] -> out[:, 0:dout].
+    void resblk(const MResblk& r, const float* in, int64_t in_ld, float* out, int64_t out_ld) {
+        const Dom& d = p->dn;
+        const double valid = (double)d.valid();
+        const int32_t* col = d.col_d.as<int32_t>();
+        Coef* cf = p->coef[0].as<Coef>();
+        float* h = p->hdec.as<float>();
+        stats_fin(in, in_ld, r.din, d, r.n1, cf);
+        conv(r.conv1, PRO_ADAIN_LEAKY, EPI_STORE, in, in_ld, d.l, col, h, r.dout, d.l, valid, PC_DECODER, cf,
+             nullptr, nullptr, 0.2f);
+        conv(r.conv1x1, PRO_F32, EPI_STORE, in, in_ld, d.l, col, out, out_ld, d.l, valid, PC_DECODER);
+        stats_fin(h, r.dout, r.dout, d, r.n2, cf);
+        conv(r.conv2, PRO_ADAIN_LEAKY, EPI_RESID, h, r.dout, d.l, col, out, out_ld, d.l, valid, PC_DECODER, cf,
+             nullptr, nullptr, 0.2f, nullptr, nullptr, nullptr, 0, 1.0f / sqrtf(2.0f));
+    }
+
+    void decoder() {
+        const Dom& dn = p->dn;
+        const Dom& d2 = p->d2;
+        const int64_t ln = p->ln;
+        const int32_t* col = dn.col_d.as<int32_t>();
+        float* xcat = p->xcat.as<float>();
+        float* xa = p->xin_a.as<float>();
+        float* xb = p->xin_b.as<float>();
+        // asr = t_en expanded by the durations; F0 / N convs (src/gpu_batch.rs:295-302)
+        KK_HIP(launch_expand(p->t_en.as<float>(), p->t_rows, p->src_row.as<int32_t>(), ln, xcat, kXcatLd, s));
+        KK_HIP(launch_f0n_conv(p->f0.as<float>(), p->en.as<float>(), 2 * ln, m.f0w.as<float>(), m.f0b.as<float>(),
+                               m.nw_.as<float>(), m.nb_.as<float>(), xcat, kXcatLd, 512, 513, col, ln, s));
+        launches += 2;
+        resblk(m.encode, xcat, kXcatLd, xa, kXinLd);
+        // asr_res (512 -> 64, k1) into channels [1024, 1088); F0n, Nn into 1088, 1089
+        conv(m.asr_res, PRO_F32, EPI_STORE, xcat, kXcatLd, ln, col, xa + 1024, kXinLd, ln, (double)dn.valid(),
+             PC_DECODER);
+        KK_HIP(launch_copy_cols(xcat + 512, kXcatLd, 2, xa, kXinLd, 1088, col, ln, s));
+        KK_HIP(launch_copy_cols(xa + 1024, kXinLd, 66, xb, kXinLd, 1024, col, ln, s));
+        launches += 2;
+        resblk(m.decode[0], xa, kXinLd, xb, kXinLd);
+        resblk(m.decode[1], xb, kXinLd, xa, kXinLd);
+        resblk(m.decode[2], xa, kXinLd, xb, kXinLd);
+        // decode.3: upsample block to 2N (src/gpu_batch.rs:106-133)
+        const MResblk& r = m.decode[3];
+        Coef* cf = p->coef[0].as<Coef>();
+        stats_fin(xb, kXinLd, r.din, dn, r.n1, cf);
+        KK_HIP(launch_adain_pool(xb, kXinLd, r.din, cf, col, ln, r.pool_w.as<float>(), r.pool_b.as<float>(),
+                                 d2.col_d.as<int32_t>(), p->pool.as<uint16_t>(), kXinLd, s));
+        launches++;
+        float* h = p->hdec.as<float>();
+        const double v2 = (double)d2.valid();
+        conv(r.conv1, PRO_BF16, EPI_STORE, p->pool.p, kXinLd, d2.l, d2.col_d.as<int32_t>(), h, 512, d2.l, v2,
+             PC_DECODER);
+        // shortcut conv1x1(nearest x2 (x)) = nearest x2 (conv1x1(x)) for a 1x1 conv: computed at N
+        conv(r.conv1x1, PRO_F32, EPI_STORE, xb, kXinLd, ln, col, p->sc_half.as<float>(), 512, ln, v2, PC_DECODER);
+        stats_fin(h, 512, 512, d2, r.n2, cf);
+        conv(r.conv2, PRO_ADAIN_LEAKY, EPI_RESID_UP2, h, 512, d2.l, d2.col_d.as<int32_t>(), p->dec_out.as<float>(), 512,
+             d2.l, v2, PC_DECODER, cf, nullptr, nullptr, 0.2f, p->sc_half.as<float>(), nullptr, nullptr, 512,
+             1.0f / sqrtf(2.0f));
+    }
+
+    void source() {
+        KK_HIP(launch_phase_pre(p->f0.as<float>(), p->d2.start_d.as<int64_t>(), p->d2.len_d.as<int64_t>(), p->nb,
+                                p->rand_ini.as<float>(), p->pp.as<float>(), 2 * p->ln, s));
+        SourceParams q{};
+        q.f0 = p->f0.as<float>(), q.start2 = p->d2.start_d.as<int64_t>(), q.len2 = p->d2.len_d.as<int64_t>();
+        q.pp = p->pp.as<float>(), q.pp_ld = 2 * p->ln, q.seeds = p->seeds.as<uint64_t>();
+        q.fixed_noise = p->fixed_noise.as<float>(), q.noise_kind = p->kinds.as<int32_t>();
+        q.lw = m.lw.as<float>(), q.lb = m.lb;
+        q.start120 = p->d120.start_d.as<int64_t>(), q.f_len = p->d120.len_d.as<int64_t>();
+        q.blk_item = p->src_item.as<int64_t>(), q.blk_f0 = p->src_f0.as<int64_t>(), q.n_blocks = p->n_src;
+        q.spec = p->spec.as<float>(), q.spec_ld = kSpecLd;
+        KK_HIP(launch_source_stft(q, s));
+        launches += 2;
+    }
+
+    void gen_stage(int i) {
+        const Dom& din = i == 0 ? p->d2 : p->d20;
+        const Dom& dout = i == 0 ? p->d20 : p->d120;
+        const int c = m.ups[i].cout;
+        float* B[6];
+        for (int j = 0; j < 6; j++) B[j] = p->B[j].as<float>();
+        // xs = noise_res[i](noise_convs[i](masked spec)) (src/gpu_batch.rs:362-375)
+        const MNoiseConv& nc = m.nc[i];
+        KK_HIP(launch_noise_conv(p->spec.as<float>(), kSpecLd, p->d120.l, p->d120.col_d.as<int32_t>(),
+                                 nc.w.as<float>(), nc.b.as<float>(), nc.cout, nc.k, nc.stride, nc.pad, B[1], c,
+                                 dout.l, s));
+        launches++;
+        snake_block(m.noise_res[i], B[1], B[2], dout);
+        // y = ups[i](leaky_0.1(x) masked) (+ reflect pad on stage 1) + xs
+        const float* x = i == 0 ? p->dec_out.as<float>() : B[0];
+        const int64_t x_ld = i == 0 ? 512 : 256;
+        const int64_t l_convt = i == 0 ? dout.l : dout.l - 1;
+        conv(m.ups[i], PRO_LEAKY, i == 0 ? EPI_CONVT : EPI_CONVT_REFLECT, x, x_ld, din.l, din.col_d.as<int32_t>(),
+             B[3], c, din.l + 1, (double)din.valid(), PC_CONVT, nullptr, nullptr, nullptr, 0.1f, B[1], nullptr,
+             nullptr, c, 1.f, m.ups_stride[i], m.ups_pad[i], l_convt, i == 0 ? nullptr : &dout);
+        float* X[3] = {B[4], B[5], B[0]};
+        resblock_mean(&m.rb[3 * i], B[3], X, B[2], dout);
+    }
+
+    void post_istft() {
+        const Dom& d = p->d120;
+        conv(m.post, PRO_LEAKY, EPI_STORE, p->B[0].p, 128, d.l, d.col_d.as<int32_t>(), p->post.as<float>(), kPostLd,
+             d.l, (double)d.valid(), PC_POST, nullptr, nullptr, nullptr, 0.01f);
+    }
+
+    void istft() {
+        IstftParams q{};
+        q.post = p->post.as<float>(), q.post_ld = kPostLd;
+        q.start120 = p->d120.start_d.as<int64_t>(), q.f_len = p->d120.len_d.as<int64_t>();
+        q.blk_item = p->ist_item.as<int64_t>(), q.blk_s0 = p->ist_s0.as<int64_t>(), q.n_blocks = p->n_ist;
+        q.audio = p->audio.as<float>(), q.audio_start = p->audio_start.as<int64_t>();
+        KK_HIP(launch_istft(q, s));
+        launches++;
+    }
+
+    void run(int until) {
+        KK_HIP(launch_style_fc(m.style_wt.as<float>(), m.style_b.as<float>(), m.style_rows, p->style.as<float>(),
+                               p->nb, p->gb.as<float>(), s));
+        launches++;
+        if (p->kind == PLAN_SNAKE) {
+            snake_block(*p->sblk, p->B[0].as<float>(), p->B[1].as<float>(), p->ds);
+            return;
+        }
+        if (p->kind == PLAN_DECODER) decoder();
+        if (until <= KK_STAGE_DECODER) return;
+        source();
+        if (until <= KK_STAGE_SOURCE) return;
+        gen_stage(0);
+        if (until <= KK_STAGE_GEN0) return;
+        gen_stage(1);
+        if (until <= KK_STAGE_GEN1) return;
+        post_istft();
+        if (until <= KK_STAGE_POST) return;
+        istft();
+    }
+};
+
+static void set_err(char* err, size_t errlen, const std::string& m) {
+    if (err && errlen) {
+        std::snprintf(err, errlen, "%s", m.c_str());
+    }
+}
+
+template <class F>
+static int guard(char* err, size_t errlen, F&& f) {
+    try {
+        f();
+        return KK_OK;
+    } catch (const Err& e) {
+        set_err(err, errlen, e.msg);
+        return e.code;
+    } catch (const std::bad_alloc&) {
+        set_err(err, errlen, "host allocation failed");
+        return KK_ERR_OOM;
+    } catch (const std::exception& e) {
+        set_err(err, errlen, e.what());
+        return KK_ERR_INVALID;
+    }
+}
+
+static void use_device(const kk_ctx* ctx) { KK_HIP(hipSetDevice(ctx->device)); }
+
+// Copy rows [r0, r0 + rows) x channels [0, c) of a time-major buffer and transpose to [c][rows].
+static void tap_rows(const void* dev, int64_t ld, int64_t r0, int64_t rows, int c, float* dst) {
+    std::vector<float> h((size_t)rows * ld);
+    KK_HIP(hipMemcpy(h.data(), (const float*)dev + r0 * ld, sizeof(float) * rows * ld, hipMemcpyDeviceToHost));
+    for (int ch = 0; ch < c; ch++)
+        for (int64_t t = 0; t < rows; t++) dst[(size_t)ch * rows + t] = h[(size_t)t * ld + ch];
+}
+
+}  // namespace kk
+
+using namespace kk;
+
+extern "C" {
+
+const char* kk_identity(void) { return "hip-gfx950 bf16-mfma f32-acc"; }
+
+int kk_open(int ordinal, kk_ctx** out, char* err, size_t errlen) {
+    if (!out) return KK_ERR_INVALID;
+    *out = nullptr;
+    return guard(err, errlen, [&] {
+        int n = 0;
+        KK_HIP(hipGetDeviceCount(&n));
+        check(ordinal >= 0 && ordinal < n, "device ordinal " + std::to_string(ordinal) + " out of range (" +
+                                               std::to_string(n) + " devices visible)");
+        hipDeviceProp_t prop;
+        KK_HIP(hipGetDeviceProperties(&prop, ordinal));
+        check(std::strncmp(prop.gcnArchName, "gfx950", 6) == 0,
+              std::string("device ") + std::to_string(ordinal) + " is " + prop.gcnArchName +
+                  "; this build carries gfx950 code only");
+        auto ctx = std::make_unique<kk_ctx>();
+        ctx->device = ordinal;
+        ctx->name = prop.name;
+        KK_HIP(hipSetDevice(ordinal));
+        KK_HIP(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking));
+        // twiddles and periodic Hann window in f64 (src/gpu.rs:93-101)
+        double cs[220], sn[220];
+        float win[20];
+        for (int k = 0; k < 11; k++)
+            for (int j = 0; j < 20; j++) {
+                const double a = 2.0 * M_PI * (double)((k * j) % 20) / 20.0;
+                cs[k * 20 + j] = std::cos(a);
+                sn[k * 20 + j] = std::sin(a);
+            }
+        for (int j = 0; j < 20; j++) win[j] = (float)(0.5 - 0.5 * std::cos(2.0 * M_PI * (double)j / 20.0));
+        KK_HIP(upload_stft_tables(cs, sn, win));
+        *out = ctx.release();
+    });
+}
+
+void kk_close(kk_ctx* ctx) {
+    if (!ctx) return;
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
+    for (auto& r : ctx->prof) {
+        (void)hipEventDestroy(r.e0);
+        (void)hipEventDestroy(r.e1);
+    }
+    for (auto e : ctx->event_pool) (void)hipEventDestroy(e);
+    ctx->model = Model();
+    (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+}
+
+int kk_device_name(const kk_ctx* ctx, char* buf, size_t len) {
+    if (!ctx || !buf || !len) return KK_ERR_INVALID;
+    std::snprintf(buf, len, "%s", ctx->name.c_str());
+    return KK_OK;
+}
+
+int kk_upload_model(kk_ctx* ctx, const kk_tensor* tensors, int n, char* err, size_t errlen) {
+    if (!ctx || (!tensors && n > 0)) return KK_ERR_INVALID;
+    return guard(err, errlen, [&] {
+        use_device(ctx);
+        load_model(ctx, tensors, n);
+    });
+}
+
+int kk_plan_create(kk_ctx* ctx, const kk_decoder_item* items, int n, kk_plan** out, char* err, size_t errlen) {
+    if (!ctx || !out) return KK_ERR_INVALID;
+    *out = nullptr;
+    return guard(err, errlen, [&] {
+        use_device(ctx);
+        *out = create_decoder_plan(ctx, items, n);
+    });
+}
+
+int kk_plan_create_generator(kk_ctx* ctx, const kk_generator_item* items, int n, kk_plan** out, char* err,
+                             size_t errlen) {
+    if (!ctx || !out) return KK_ERR_INVALID;
+    *out = nullptr;
+    return guard(err, errlen, [&] {
+        use_device(ctx);
+        *out = create_generator_plan(ctx, items, n);
+    });
+}
+
+int kk_plan_create_snake(kk_ctx* ctx, const char* prefix, const float* const* x, const int64_t* t,
+                         const float* const* ref_s, int n, int gap, kk_plan** out, char* err, size_t errlen) {
+    if (!ctx || !out) return KK_ERR_INVALID;
+    *out = nullptr;
+    return guard(err, errlen, [&] {
+        use_device(ctx);
+        *out = create_snake_plan(ctx, prefix, x, t, ref_s, n, gap);
+    });
+}
+
+int kk_plan_run(kk_plan* plan, int until, char* err, size_t errlen) {
+    if (!plan) return KK_ERR_INVALID;
+    return guard(err, errlen, [&] {
+        use_device(plan->ctx);
+        check(plan->ctx->model.ready, "no model uploaded");
+        Runner r{plan, plan->ctx, plan->ctx->model, plan->ctx->stream};
+        r.run(until);
+        plan->conv_flop = r.flop, plan->snake_flop = r.snake_flop, plan->launches = r.launches;
+        plan->last_until = until;
+    });
+}
+
+int kk_plan_sync(kk_plan* plan, char* err, size_t errlen) {
+    if (!plan) return KK_ERR_INVALID;
+    return guard(err, errlen, [&] {
+        use_device(plan->ctx);
+        KK_HIP(hipStreamSynchronize(plan->ctx->stream));
+    });
+}
+
+int kk_plan_fetch(kk_plan* plan, kk_output* out, char* err, size_t errlen) {
+    if (!plan || !out) return KK_ERR_INVALID;
+    for (int b = 0; b < plan->nb; b++) out[b] = kk_output{nullptr, 0};
+    int rc = guard(err, errlen, [&] {
+        use_device(plan->ctx);
+        check(plan->last_until >= KK_STAGE_ALL || plan->kind == PLAN_SNAKE, "plan has not run to the end");
+        KK_HIP(hipStreamSynchronize(plan->ctx->stream));
+        for (int b = 0; b < plan->nb; b++) {
+            if (plan->kind == PLAN_SNAKE) {
+                const int64_t t = plan->ds.len[b];
+                out[b].n_samples = t * plan->sc;
+                out[b].audio = (float*)std::malloc(sizeof(float) * out[b].n_samples);
+                if (!out[b].audio) throw std::bad_alloc();
+                tap_rows(plan->B[0].p, plan->sc, plan->ds.start[b], t, plan->sc, out[b].audio);
+            } else {
+                const int64_t ns = 600 * plan->nfr[b];
+                out[b].n_samples = ns;
+                out[b].audio = (float*)std::malloc(sizeof(float) * ns);
+                if (!out[b].audio) throw std::bad_alloc();
+                KK_HIP(hipMemcpy(out[b].audio, plan->audio.as<float>() + 600 * plan->a[b], sizeof(float) * ns,
+                                 hipMemcpyDeviceToHost));
+            }
+        }
+    });
+    if (rc != KK_OK) kk_output_free(out, plan->nb);
+    return rc;
+}
+
+int kk_plan_tap(kk_plan* plan, const char* name, int item, float* dst, int64_t count, char* err, size_t errlen) {
+    if (!plan || !name || !dst) return KK_ERR_INVALID;
+    return guard(err, errlen, [&] {
+        use_device(plan->ctx);
+        check(item >= 0 && item < plan->nb, "item out of range");
+        check(plan->kind != PLAN_SNAKE, "snake plans have no taps");
+        KK_HIP(hipStreamSynchronize(plan->ctx->stream));
+        const std::string n(name);
+        const int64_t N = plan->nfr[item], a = plan->a[item];
+        auto need = [&](int64_t c) { check(count == c, "tap " + n + " holds " + std::to_string(c) + " values"); };
+        if (n == "asr") {
+            check(plan->kind == PLAN_DECODER, "asr exists in decoder plans only");
+            need(512 * N);
+            tap_rows(plan->xcat.p, kXcatLd, a, N, 512, dst);
+        } else if (n == "decoder") {
+            need(512 * 2 * N);
+            tap_rows(plan->dec_out.p, 512, 2 * a, 2 * N, 512, dst);
+        } else if (n == "spec") {
+            need(22 * (120 * N + 1));
+            tap_rows(plan->spec.p, kSpecLd, 120 * a, 120 * N + 1, 22, dst);
+        } else if (n == "gen0") {
+            check(plan->last_until == KK_STAGE_GEN0, "gen0 is valid after a run until KK_STAGE_GEN0");
+            need(256 * 20 * N);
+            tap_rows(plan->B[0].p, 256, 20 * a, 20 * N, 256, dst);
+        } else if (n == "post") {
+            need(22 * (120 * N + 1));
+            tap_rows(plan->post.p, kPostLd, 120 * a, 120 * N + 1, 22, dst);
+        } else if (n == "audio") {
+            need(600 * N);
+            KK_HIP(hipMemcpy(dst, plan->audio.as<float>() + 600 * a, sizeof(float) * 600 * N, hipMemcpyDeviceToHost));
+        } else {
+            fail(KK_ERR_INVALID, "unknown tap " + n);
+        }
+    });
+}
+
+int kk_plan_get_info(const kk_plan* plan, kk_plan_info* info) {
+    if (!plan || !info) return KK_ERR_INVALID;
+    info->n_items = plan->nb;
+    info->ln = plan->ln;
+    int64_t fr = 0;
+    for (auto v : plan->nfr) fr += v;
+    info->frames = fr;
+    info->samples = plan->kind == PLAN_SNAKE ? 0 : 600 * fr;
+    info->conv_flop = plan->conv_flop;
+    info->snake_flop = plan->snake_flop;
+    info->device_bytes = plan->dev_bytes;
+    info->launches = plan->launches;
+    return KK_OK;
+}
+
+void kk_plan_free(kk_plan* plan) {
+    if (!plan) return;
+    (void)hipSetDevice(plan->ctx->device);
+    (void)hipStreamSynchronize(plan->ctx->stream);
+    delete plan;
+}
+
+int kk_forward_decoder_batch(kk_ctx* ctx, const kk_decoder_item* items, int n, kk_output* out, char* err,
+                             size_t errlen) {
+    if (!ctx || !out) return KK_ERR_INVALID;
+    kk_plan* plan = nullptr;
+    int rc = kk_plan_create(ctx, items, n, &plan, err, errlen);
+    if (rc != KK_OK) return rc;
+    rc = kk_plan_run(plan, KK_STAGE_ALL, err, errlen);
+    if (rc == KK_OK) rc = kk_plan_fetch(plan, out, err, errlen);
+    kk_plan_free(plan);
+    return rc;
+}
+
+void kk_output_free(kk_output* out, int n) {
+    if (!out) return;
+    for (int b = 0; b < n; b++) {
+        std::free(out[b].audio);
+        out[b].audio = nullptr;
+        out[b].n_samples = 0;
+    }
+}
+
+int kk_set_profiling(kk_ctx* ctx, int on) {
+    if (!ctx) return KK_ERR_INVALID;
+    ctx->profiling = on != 0;
+    return KK_OK;
+}
+
+int kk_profile_read(kk_ctx* ctx, kk_profile_entry* out, int max, int* n_out, char* err, size_t errlen) {
+    if (!ctx || !out || !n_out) return KK_ERR_INVALID;
+    return guard(err, errlen, [&] {
+        use_device(ctx);
+        KK_HIP(hipStreamSynchronize(ctx->stream));
+        kk_profile_entry acc[4];
+        for (int i = 0; i < 4; i++) {
+            std::memset(&acc[i], 0, sizeof(acc[i]));
+            std::snprintf(acc[i].name, sizeof(acc[i].name), "%s", kProfNames[i]);
+        }
+        for (auto& r : ctx->prof) {
+            float ms = 0.f;
+            KK_HIP(hipEventElapsedTime(&ms, r.e0, r.e1));
+            acc[r.cls].launches++;
+            acc[r.cls].ms += ms;
+            acc[r.cls].flop += r.flop;
+            ctx->event_pool.push_back(r.e0);
+            ctx->event_pool.push_back(r.e1);
+        }
+        ctx->prof.clear();
+        int k = 0;
+        for (int i = 0; i < 4 && k < max; i++) out[k++] = acc[i];
+        *n_out = k;
+    });
+}
+
+int kk_durations_from_logits(const float* logits, int t, float speed, int64_t* out) {
+    if (!logits || !out || t < 0 || !(speed > 0.f) || !std::isfinite(speed)) return KK_ERR_INVALID;
+    // src/model.rs:90-99 with src/ops.rs:49-51: f32 sigmoid, left-to-right f32 sum, ties to even
+    for (int i = 0; i < t; i++) {
+        float s = 0.f;
+        for (int j = 0; j < 50; j++) {
+            volatile float e = std::exp(-logits[i * 50 + j]);
+            s = s + 1.0f / (1.0f + (float)e);
+        }
+        const float d = std::nearbyint(s / speed);
+        const int64_t di = (int64_t)d;
+        out[i] = di < 1 ? 1 : di;
+    }
+    return KK_OK;
+}
+
+int64_t kk_layout_frames(const int64_t* nfs, int n, int64_t* a_out) {
+    if (!nfs || !a_out || n <= 0) return KK_ERR_INVALID;
+    int64_t ln = 0;
+    for (int b = 0; b < n; b++) {
+        if (nfs[b] < 0) return KK_ERR_INVALID;
+        a_out[b] = ln;
+        ln += nfs[b] + kGapN;
+    }
+    return ln;
+}
+
+int kk_layout_col_item(int64_t l, const int64_t* start, const int64_t* len, int n, int32_t* col_item) {
+    if (!start || !len || !col_item || l < 0) return KK_ERR_INVALID;
+    for (int64_t t = 0; t < l; t++) col_item[t] = -1;
+    for (int b = 0; b < n; b++) {
+        if (start[b] < 0 || len[b] < 0 || start[b] + len[b] > l) return KK_ERR_INVALID;
+        for (int64_t t = start[b]; t < start[b] + len[b]; t++) {
+            if (col_item[t] >= 0) return KK_ERR_INVALID;
+            col_item[t] = b;
+        }
+    }
+    return KK_OK;
+}
+
+int kk_layout_src_row(const int64_t* const* dur, const int32_t* n_tok, int n, const int64_t* tstart, const int64_t* a,
+                      int64_t ln, int32_t* src_row) {
+    if (!dur || !n_tok || !tstart || !a || !src_row) return KK_ERR_INVALID;
+    for (int64_t t = 0; t < ln; t++) src_row[t] = -1;
+    for (int b = 0; b < n; b++) {
+        int64_t f = a[b];
+        for (int tok = 0; tok < n_tok[b]; tok++)
+            for (int64_t r = 0; r < dur[b][tok]; r++) {
+                if (f >= ln) return KK_ERR_INVALID;
+                src_row[f++] = (int32_t)(tstart[b] + tok);
+            }
+    }
+    return KK_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,554 @@
+// kk_misc.hip -- bandwidth-bound kernels of the decoder + generator path (gfx950).
+//
+// All activations are time-major [rows][ld] f32 with items packed along the rows (see
+// kk_common.h).  Each kernel cites the reference kernel / host step whose semantics it restates.
+#include "kk_common.h"
+#include "kk_kernels.h"
+
+namespace kk {
+
+// Periodic Hann(20) window and DFT twiddles, computed in f64 on the host exactly as
+// src/gpu.rs:93-101 does (uploaded once per context).
+__constant__ double c_cos[11][20];
+__constant__ double c_sin[11][20];
+__constant__ float c_win[20];
+
+namespace {
+
+constexpr float kPiF = 3.14159274101257324f;  // (float)M_PI, kernels/kokoro.cu:9
+
+// ------------------------------------------------------------------ AdaIN statistics
+// chan_stats_seg (kernels/kokoro.cu:779-810): per (item, channel) sums of x - x[first row of the
+// item], accumulated in f64 and combined with f64 atomics.  One wave covers 64 channels of a run of
+// rows; the item of a row is wave-uniform, so item changes flush the partial sums.
+__global__ __launch_bounds__(256) void stats_kernel(const float* __restrict__ x, int64_t ld, int c, DomDev d,
+                                                    double* __restrict__ sums, int64_t rows_per_wave) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int ch = blockIdx.y * 64 + lane;
+    const bool live = ch < c;
+    const int64_t r_begin = ((int64_t)blockIdx.x * 4 + wave) * rows_per_wave;
+    if (r_begin >= d.l) return;
+    const int64_t r_end = min(r_begin + rows_per_wave, d.l);
+    int cur = -1;
+    float shift = 0.f;
+    double s = 0.0, s2 = 0.0;
+    for (int64_t r = r_begin; r < r_end; r++) {
+        const int b = d.col_item[r];
+        if (b != cur) {
+            if (cur >= 0 && live) {
+                unsafeAtomicAdd(&sums[((int64_t)cur * c + ch) * 2], s);
+                unsafeAtomicAdd(&sums[((int64_t)cur * c + ch) * 2 + 1], s2);
+            }
+            cur = b;
+            s = s2 = 0.0;
+            if (b >= 0 && live) shift = x[d.start[b] * ld + ch];
+        }
+        if (b >= 0 && live) {
+            const float v = x[r * ld + ch] - shift;
+            s += (double)v;
+            s2 += (double)v * (double)v;
+        }
+    }
+    if (cur >= 0 && live) {
+        unsafeAtomicAdd(&sums[((int64_t)cur * c + ch) * 2], s);
+        unsafeAtomicAdd(&sums[((int64_t)cur * c + ch) * 2 + 1], s2);
+    }
+}
+
+// mean / rstd exactly as chan_stats_seg's epilogue, then the AdaIN affine of adain_apply_seg
+// (kernels/kokoro.cu:318-334) folded into v = x * sc + sh.  With `reset`, zeroes the sums for the
+// next statistics pass (several AdaIN layers may share one pass).
+__global__ void finalize_kernel(const float* __restrict__ x, int64_t ld, int c, DomDev d, double* sums,
+                                const float* __restrict__ gb, int64_t gb_ld, int gb_off, const float* __restrict__ nw,
+                                const float* __restrict__ nbias, Coef* __restrict__ coef, int reset) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (int64_t)d.nb * c) return;
+    const int b = (int)(i / c), ch = (int)(i - (int64_t)b * c);
+    const double s = sums[i * 2], s2 = sums[i * 2 + 1];
+    if (reset) {
+        sums[i * 2] = 0.0;
+        sums[i * 2 + 1] = 0.0;
+    }
+    const int64_t n = d.len[b];
+    if (n <= 0) {
+        coef[i] = Coef{0.f, 0.f};
+        return;
+    }
+    const float shift = x[d.start[b] * ld + ch];
+    const double dm = s / (double)n;
+    double var = s2 / (double)n - dm * dm;
+    if (var < 0.0) var = 0.0;
+    const float mean = (float)((double)shift + dm);
+    const float rstd = 1.0f / sqrtf((float)var + 1e-5f);
+    const double g1 = 1.0 + (double)gb[b * gb_ld + gb_off + ch];
+    const double beta = gb[b * gb_ld + gb_off + c + ch];
+    const double a = (double)rstd * (double)nw[ch];
+    coef[i] = Coef{(float)(a * g1), (float)(((double)nbias[ch] - (double)mean * a) * g1 + beta)};
+}
+
+// ------------------------------------------------------------------ style projections
+// GLinear of every AdaIN (src/gpu_batch.rs:84): gb[b][j] = bias[j] + sum_k W[j][k] style[b][k].
+// W is stored transposed [128][rows] so consecutive threads read consecutive rows.
+__global__ __launch_bounds__(256) void style_fc_kernel(const float* __restrict__ wt, const float* __restrict__ bias,
+                                                       int rows, const float* __restrict__ style, int nb,
+                                                       float* __restrict__ gb) {
+    __shared__ float st[16][kStyleDim];
+    const int j = blockIdx.x * 256 + threadIdx.x;
+    for (int b0 = 0; b0 < nb; b0 += 16) {
+        const int cnt = min(16, nb - b0);
+        __syncthreads();
+        for (int i = threadIdx.x; i < cnt * kStyleDim; i += 256) st[i / kStyleDim][i % kStyleDim] = style[(int64_t)b0 * kStyleDim + i];
+        __syncthreads();
+        if (j < rows) {
+            double acc[16];
+#pragma unroll
+            for (int e = 0; e < 16; e++) acc[e] = 0.0;
+            for (int k = 0; k < kStyleDim; k++) {
+                const double w = wt[(int64_t)k * rows + j];
+#pragma unroll
+                for (int e = 0; e < 16; e++) acc[e] += w * (double)st[e][k];
+            }
+            for (int e = 0; e < cnt; e++) gb[(int64_t)(b0 + e) * rows + j] = (float)(acc[e] + (double)bias[j]);
+        }
+    }
+}
+
+// ------------------------------------------------------------------ duration expansion
+// gather_cols (kernels/kokoro.cu:393-398; src/gpu_batch.rs:295-297): exact copies, gaps -> 0.
+__global__ void expand_kernel(const float* __restrict__ t_en, int64_t t_rows, const int32_t* __restrict__ src_row,
+                              int64_t l, float* __restrict__ asr, int64_t ld) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= l * 512) return;
+    const int64_t t = i >> 9;
+    const int ch = (int)(i & 511);
+    const int32_t r = src_row[t];
+    asr[t * ld + ch] = r < 0 ? 0.0f : t_en[(int64_t)ch * t_rows + r];
+}
+
+// F0_conv / N_conv (src/vocoder.rs:106-107): Conv1d 1->1 k3 s2 p1, d2 -> dn, f32; gap rows -> 0.
+__global__ void f0n_kernel(const float* __restrict__ f0, const float* __restrict__ en, int64_t l2,
+                           const float* __restrict__ wf, const float* __restrict__ bf, const float* __restrict__ wn,
+                           const float* __restrict__ bn, float* __restrict__ out, int64_t ld, int col_f0, int col_n,
+                           const int32_t* __restrict__ col, int64_t ln) {
+#pragma clang fp contract(off)
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= ln) return;
+    float a = bf[0], b = bn[0];
+    for (int k = 0; k < 3; k++) {
+        const int64_t i = 2 * t - 1 + k;
+        if (i < 0 || i >= l2) continue;
+        a = a + wf[k] * f0[i];
+        b = b + wn[k] * en[i];
+    }
+    const bool gap = col[t] < 0;
+    out[t * ld + col_f0] = gap ? 0.f : a;
+    out[t * ld + col_n] = gap ? 0.f : b;
+}
+
+__global__ void copy_cols_kernel(const float* __restrict__ src, int64_t src_ld, int c, float* __restrict__ dst,
+                                 int64_t dst_ld, int dst_c0, const int32_t* __restrict__ col, int64_t l) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= l * c) return;
+    const int64_t t = i / c;
+    const int ch = (int)(i - t * c);
+    dst[t * dst_ld + dst_c0 + ch] = col[t] < 0 ? 0.f : src[t * src_ld + ch];
+}
+
+// Decoder upsample block (src/gpu_batch.rs:106-117): AdaIN + leaky 0.2 (adain_apply_seg, gaps -> 0)
+// followed by the depthwise ConvTranspose1d k3 s2 p1 op1 (dw_convT_k3s2, kernels/kokoro.cu:150-166:
+// bias, then ascending contributing inputs), masked on d2 and rounded to bf16 for conv1.
+__global__ void adain_pool_kernel(const float* __restrict__ x, int64_t ld, int c, const Coef* __restrict__ coef,
+                                  const int32_t* __restrict__ col_n, int64_t ln, const float* __restrict__ pw,
+                                  const float* __restrict__ pb, const int32_t* __restrict__ col_2,
+                                  uint16_t* __restrict__ out, int64_t out_ld) {
+#pragma clang fp contract(off)
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= 2 * ln * out_ld) return;
+    const int64_t o = i / out_ld;
+    const int ch = (int)(i - o * out_ld);
+    float v = 0.f;
+    if (ch < c && col_2[o] >= 0) {
+        float acc = pb[ch];
+        for (int64_t t = (o - 1) / 2 - 1; t <= (o + 1) / 2; t++) {
+            if (t < 0 || t >= ln) continue;
+            const int64_t k = o + 1 - 2 * t;
+            if (k < 0 || k >= 3) continue;
+            const int b = col_n[t];
+            float a = 0.f;
+            if (b >= 0) {
+                const Coef cf = coef[(int64_t)b * c + ch];
+                a = __builtin_fmaf(x[t * ld + ch], cf.sc, cf.sh);
+                a = a < 0.f ? a * 0.2f : a;
+            }
+            acc = acc + pw[ch * 3 + k] * a;
+        }
+        v = acc;
+    }
+    out[o * out_ld + ch] = f32_to_bf16_bits(v);
+}
+
+// ------------------------------------------------------------------ noise convolutions (f32)
+// conv1d_strided / conv_direct_tiled semantics (kernels/kokoro.cu:517-617): y = b + sum_k sum_ci
+// w x with the spectrum's gap rows zeroed first (src/gpu_batch.rs:363-365).  A block computes
+// kNcRows output rows x all output channels (one channel per thread); the input window sits in LDS.
+constexpr int kNcRows = 32;
+__global__ __launch_bounds__(256) void noise_conv_kernel(const float* __restrict__ spec, int64_t spec_ld, int64_t l_in,
+                                                         const int32_t* __restrict__ col_in,
+                                                         const float* __restrict__ w, const float* __restrict__ b,
+                                                         int cout, int k, int stride, int pad, float* __restrict__ y,
+                                                         int64_t y_ld, int64_t l_out) {
+    __shared__ float xs[(kNcRows - 1) * 6 + 12][22];
+    const int64_t t0 = (int64_t)blockIdx.x * kNcRows;
+    const int win = (kNcRows - 1) * stride + k;
+    const int64_t in0 = t0 * stride - pad;
+    for (int i = threadIdx.x; i < win * 22; i += blockDim.x) {
+        const int r = i / 22, ci = i - r * 22;
+        const int64_t row = in0 + r;
+        float v = 0.f;
+        if (row >= 0 && row < l_in && col_in[row] >= 0) v = spec[row * spec_ld + ci];
+        xs[r][ci] = v;
+    }
+    __syncthreads();
+    const int co = threadIdx.x;
+    if (co >= cout) return;
+    const int nrows = (int)min((int64_t)kNcRows, l_out - t0);
+    float acc[kNcRows];
+    const float bias = b[co];
+#pragma unroll
+    for (int r = 0; r < kNcRows; r++) acc[r] = bias;
+    for (int kk = 0; kk < k; kk++) {
+        for (int ci = 0; ci < 22; ci++) {
+            const float wv = w[((int64_t)co * 22 + ci) * k + kk];
+#pragma unroll
+            for (int r = 0; r < kNcRows; r++) acc[r] = __builtin_fmaf(wv, xs[r * stride + kk][ci], acc[r]);
+        }
+    }
+    for (int r = 0; r < nrows; r++) y[(t0 + r) * y_ld + co] = acc[r];
+}
+
+// ------------------------------------------------------------------ SineGen (kernels/kokoro.cu:188-254)
+__device__ __forceinline__ float remainder1(float a) {
+    float m = fmodf(a, 1.0f);
+    if (m != 0.0f && m < 0.0f) m = m + 1.0f;
+    return m;
+}
+
+__device__ __forceinline__ float sine_rad(const float* f0c, int l, float near_scale, int t, int h,
+                                          const float* rand_ini) {
+#pragma clang fp contract(off)
+    int src = (int)floorf((float)t * near_scale);
+    if (src > l - 1) src = l - 1;
+    float r = remainder1(f0c[src] * (float)(h + 1) / 24000.0f);
+    if (t == 0 && h > 0) r = r + rand_ini[h];
+    return r;
+}
+
+// phase_pre[h][d] = (float(cumsum_f64(v)) * 2 * pi) * 300 where v is the ×1/300 linear downsample of
+// rad (sine_phase_pre, kernels/kokoro.cu:206-226).  One block per (item, harmonic); the sequential
+// f64 cumulative sum becomes a block scan in f64.
+__global__ __launch_bounds__(256) void phase_pre_kernel(const float* __restrict__ f0, const int64_t* __restrict__ start2,
+                                                        const int64_t* __restrict__ len2,
+                                                        const float* __restrict__ rand_ini, float* __restrict__ pp,
+                                                        int64_t pp_ld) {
+#pragma clang fp contract(off)
+    __shared__ double wsum[4];
+    const int b = blockIdx.x / kHarmonics, h = blockIdx.x % kHarmonics;
+    const int l = (int)len2[b];
+    const float* f0c = f0 + start2[b];
+    const float* ri = rand_ini + b * kHarmonics;
+    const int s = l * 300;
+    const int d_len = (int)floor((double)s * (1.0 / 300.0));
+    const float near_scale = (float)(1.0 / 300.0);
+    const float down_scale = (float)(1.0 / (1.0 / 300.0));
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    double carry = 0.0;
+    for (int d0 = 0; d0 < d_len; d0 += 256) {
+        const int d = d0 + threadIdx.x;
+        double v = 0.0;
+        if (d < d_len) {
+            float real = __builtin_fmaf(down_scale, (float)d + 0.5f, -0.5f);
+            if (real < 0.0f) real = 0.0f;
+            int i0 = (int)floorf(real);
+            if (i0 > s - 1) i0 = s - 1;
+            const float l1 = fminf(fmaxf(real - (float)i0, 0.0f), 1.0f);
+            const int i1 = i0 < s - 1 ? i0 + 1 : i0;
+            const float l0 = 1.0f - l1;
+            v = (double)__builtin_fmaf(sine_rad(f0c, l, near_scale, i0, h, ri), l0,
+                                       sine_rad(f0c, l, near_scale, i1, h, ri) * l1);
+        }
+        // inclusive wave scan in f64
+        for (int off = 1; off < 64; off <<= 1) {
+            const double u = __shfl_up(v, off, 64);
+            if (lane >= off) v += u;
+        }
+        if (lane == 63) wsum[wave] = v;
+        __syncthreads();
+        double pre = carry;
+        for (int w = 0; w < wave; w++) pre += wsum[w];
+        const double tot = wsum[0] + wsum[1] + wsum[2] + wsum[3];
+        __syncthreads();
+        v += pre;
+        if (d < d_len) pp[(int64_t)h * pp_ld + start2[b] + d] = (((float)v) * 2.0f * kPiF) * 300.0f;
+        carry += tot;
+    }
+}
+
+__device__ __forceinline__ uint64_t splitmix_at(uint64_t seed, uint64_t ctr) {
+    uint64_t x = seed + (ctr + 1ull) * 0x9E3779B97F4A7C15ull;
+    x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+    x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+    return x ^ (x >> 31);
+}
+
+// Box-Muller pair i of the counter stream (gen_noise, kernels/kokoro.cu:291-302).
+__device__ __forceinline__ void noise_pair(uint64_t seed, uint64_t i, float& n0, float& n1) {
+#pragma clang fp contract(off)
+    const uint64_t x = splitmix_at(seed, 1024ull + i);
+    const float u1 = (float)((x >> 40) + 1ull) * (1.0f / 16777216.0f);
+    const float u2 = (float)((x >> 16) & 0xFFFFFFull) * (1.0f / 16777216.0f);
+    const float r = sqrtf(-2.0f * logf(u1));
+    const float th = 6.2831855f * u2;
+    n0 = r * cosf(th);
+    n1 = r * sinf(th);
+}
+
+// har[t] of one item (sine_har_source, kernels/kokoro.cu:228-254).
+__device__ float har_sample(const SourceParams& p, int b, int t) {
+#pragma clang fp contract(off)
+    const int l = (int)p.len2[b];
+    const int d_len = l;
+    const float* f0c = p.f0 + p.start2[b];
+    const float near_scale = (float)(1.0 / 300.0);
+    const float up_scale = (float)(1.0 / 300.0);
+    int src = (int)floorf((float)t * near_scale);
+    if (src > l - 1) src = l - 1;
+    const float f0 = f0c[src];
+    const float uv = f0 > 10.0f ? 1.0f : 0.0f;
+    const float noise_amp = uv * 0.003f + (1.0f - uv) * 0.1f / 3.0f;
+    float real = __builtin_fmaf(up_scale, (float)t + 0.5f, -0.5f);
+    if (real < 0.0f) real = 0.0f;
+    int i0 = (int)floorf(real);
+    if (i0 > d_len - 1) i0 = d_len - 1;
+    const float l1 = fminf(fmaxf(real - (float)i0, 0.0f), 1.0f);
+    const int i1 = i0 < d_len - 1 ? i0 + 1 : i0;
+    const float l0 = 1.0f - l1;
+    float nz[kHarmonics + 1];
+    const int64_t base = (int64_t)t * kHarmonics;
+    if (p.noise_kind[b] == 0) {
+        const uint64_t seed = p.seeds[b];
+        const int64_t first = base >> 1;
+#pragma unroll
+        for (int q = 0; q < 5; q++) {
+            float n0, n1;
+            noise_pair(seed, (uint64_t)(first + q), n0, n1);
+            const int64_t i0n = 2 * (first + q) - base;  // harmonic index of n0 (may be -1)
+            if (i0n >= 0 && i0n < kHarmonics) nz[i0n] = n0;
+            if (i0n + 1 >= 0 && i0n + 1 < kHarmonics) nz[i0n + 1] = n1;
+        }
+    } else {
+        const float* fx = p.fixed_noise + (300 * p.start2[b]) * kHarmonics + base;
+#pragma unroll
+        for (int h = 0; h < kHarmonics; h++) nz[h] = fx[h];
+    }
+    const float* pp = p.pp + p.start2[b];
+    float acc = 0.0f;
+#pragma unroll
+    for (int h = 0; h < kHarmonics; h++) {
+        const float ph = __builtin_fmaf(pp[h * p.pp_ld + i0], l0, pp[h * p.pp_ld + i1] * l1);
+        const float sine = sinf(ph) * 0.1f;
+        const float v = sine * uv + noise_amp * nz[h];
+        acc = acc + p.lw[h] * v;
+    }
+    return tanhf(acc + p.lb);
+}
+
+// Harmonic source + STFT (stft20_ld, kernels/kokoro.cu:470-490) over a run of frames of one item:
+// the frames' reflect-padded samples are synthesized into LDS, then each (frame, bin) computes
+// its f64 DFT.  One launch covers every item (work list blk_item / blk_f0).
+__global__ __launch_bounds__(256) void source_stft_kernel(SourceParams p) {
+#pragma clang fp contract(off)
+    __shared__ float har[kSourceFrames * 5 + 15];
+    const int64_t blk = blockIdx.x;
+    const int b = (int)p.blk_item[blk];
+    const int64_t f_begin = p.blk_f0[blk];
+    const int64_t nf_item = p.f_len[b];
+    const int nf = (int)min((int64_t)kSourceFrames, nf_item - f_begin);
+    const int s_len = (int)(300 * p.len2[b]);
+    const int64_t p0 = 5 * f_begin - 10;
+    const int nsamp = 5 * (nf - 1) + 20;
+    for (int i = threadIdx.x; i < nsamp; i += blockDim.x) {
+        const int64_t pos = p0 + i;
+        const int src = (int)(pos < 0 ? -pos : (pos >= s_len ? 2 * (int64_t)s_len - 2 - pos : pos));
+        har[i] = har_sample(p, b, src);
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < nf * 11; i += blockDim.x) {
+        const int fl = i / 11, k = i - fl * 11;
+        double re = 0.0, im = 0.0;
+        for (int n = 0; n < 20; n++) {
+            const double v = (double)(har[fl * 5 + n] * c_win[n]);
+            re += v * c_cos[k][n];
+            im -= v * c_sin[k][n];
+        }
+        if (k == 0 || k == 10) im = 0.0;
+        const float rf = (float)re, imf = (float)im;
+        float* dst = p.spec + (p.start120[b] + f_begin + fl) * p.spec_ld;
+        dst[k] = hypotf(rf, imf);
+        dst[11 + k] = atan2f(imf, rf);
+    }
+}
+
+// ------------------------------------------------------------------ iSTFT (kernels/kokoro.cu:264-280, 492-508)
+constexpr int kIstftFrames = kIstftSamples / 5 + 5;
+__global__ __launch_bounds__(256) void istft_kernel(IstftParams p) {
+#pragma clang fp contract(off)
+    __shared__ double re[kIstftFrames][11];
+    __shared__ double im[kIstftFrames][11];
+    __shared__ double fr[kIstftFrames][20];
+    const int64_t blk = blockIdx.x;
+    const int b = (int)p.blk_item[blk];
+    const int64_t s0 = p.blk_s0[blk];
+    const int64_t nframes = p.f_len[b];
+    const int64_t len = 5 * (nframes - 1);
+    const int64_t s1 = min(s0 + kIstftSamples, len);
+    // frames touched by samples [s0, s1): j = i + 10, f in [(j-19+4)/5, j/5]
+    const int64_t jl = s0 + 10;
+    const int64_t f_first = jl - 19 > 0 ? (jl - 19 + 4) / 5 : 0;
+    const int64_t f_last = min((s1 - 1 + 10) / 5, nframes - 1);
+    const int nfr = (int)(f_last - f_first + 1);
+    const float* post = p.post + (p.start120[b] + f_first) * p.post_ld;
+    for (int i = threadIdx.x; i < nfr * 11; i += blockDim.x) {
+        const int q = i / 11, k = i - q * 11;
+        const float m = expf(post[q * p.post_ld + k]);
+        const float ph = sinf(post[q * p.post_ld + 11 + k]);
+        re[q][k] = (double)(m * cosf(ph));
+        im[q][k] = (double)(m * sinf(ph));
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < nfr * 20; i += blockDim.x) {
+        const int q = i / 20, n = i - q * 20;
+        double v = re[q][0] + re[q][10] * ((n % 2 == 0) ? 1.0 : -1.0);
+        for (int k = 1; k < 10; k++) v += 2.0 * (re[q][k] * c_cos[k][n] - im[q][k] * c_sin[k][n]);
+        v = v / 20.0;
+        fr[q][n] = v * (double)c_win[n];
+    }
+    __syncthreads();
+    float* out = p.audio + p.audio_start[b];
+    for (int64_t i = s0 + threadIdx.x; i < s1; i += blockDim.x) {
+        const int64_t j = i + 10;
+        const int64_t f_lo = j - 19 > 0 ? (j - 19 + 4) / 5 : 0;
+        int64_t f_hi = j / 5;
+        if (f_hi > nframes - 1) f_hi = nframes - 1;
+        double acc = 0.0, env = 0.0;
+        for (int64_t f = f_lo; f <= f_hi; f++) {
+            const int n = (int)(j - 5 * f);
+            acc += fr[f - f_first][n];
+            const double w = (double)c_win[n];
+            env += w * w;
+        }
+        out[i] = (float)(acc / env);
+    }
+}
+
+__global__ void zero_kernel(uint32_t* p, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0u;
+}
+
+unsigned blocks_for(int64_t n, int per) { return (unsigned)ceil_div(n, per); }
+
+}  // namespace
+
+hipError_t upload_stft_tables(const double* cosv, const double* sinv, const float* win) {
+    hipError_t e = hipMemcpyToSymbol(HIP_SYMBOL(c_cos), cosv, sizeof(double) * 220);
+    if (e != hipSuccess) return e;
+    e = hipMemcpyToSymbol(HIP_SYMBOL(c_sin), sinv, sizeof(double) * 220);
+    if (e != hipSuccess) return e;
+    return hipMemcpyToSymbol(HIP_SYMBOL(c_win), win, sizeof(float) * 20);
+}
+
+hipError_t launch_stats(const float* x, int64_t ld, int c, DomDev d, double* sums, hipStream_t s) {
+    const int64_t cblk = ceil_div(c, 64);
+    int64_t rpw = ceil_div(d.l * cblk, 16384);
+    if (rpw < 64) rpw = 64;
+    const int64_t waves = ceil_div(d.l, rpw);
+    dim3 grid(blocks_for(waves, 4), (unsigned)cblk);
+    hipLaunchKernelGGL(stats_kernel, grid, dim3(256), 0, s, x, ld, c, d, sums, rpw);
+    return hipGetLastError();
+}
+
+hipError_t launch_finalize(const float* x, int64_t ld, int c, DomDev d, double* sums, const float* gb, int64_t gb_ld,
+                           int gb_off, const float* nw, const float* nb, Coef* coef, int reset, hipStream_t s) {
+    hipLaunchKernelGGL(finalize_kernel, dim3(blocks_for((int64_t)d.nb * c, 256)), dim3(256), 0, s, x, ld, c, d, sums,
+                       gb, gb_ld, gb_off, nw, nb, coef, reset);
+    return hipGetLastError();
+}
+
+hipError_t launch_style_fc(const float* w, const float* bias, int rows, const float* style, int nb, float* gb,
+                           hipStream_t s) {
+    hipLaunchKernelGGL(style_fc_kernel, dim3(blocks_for(rows, 256)), dim3(256), 0, s, w, bias, rows, style, nb, gb);
+    return hipGetLastError();
+}
+
+hipError_t launch_expand(const float* t_en, int64_t t_rows, const int32_t* src_row, int64_t l, float* asr, int64_t ld,
+                         hipStream_t s) {
+    hipLaunchKernelGGL(expand_kernel, dim3(blocks_for(l * 512, 256)), dim3(256), 0, s, t_en, t_rows, src_row, l, asr,
+                       ld);
+    return hipGetLastError();
+}
+
+hipError_t launch_f0n_conv(const float* f0, const float* en, int64_t l2, const float* w_f0, const float* b_f0,
+                           const float* w_n, const float* b_n, float* out, int64_t ld, int col_f0, int col_n,
+                           const int32_t* col, int64_t ln, hipStream_t s) {
+    hipLaunchKernelGGL(f0n_kernel, dim3(blocks_for(ln, 256)), dim3(256), 0, s, f0, en, l2, w_f0, b_f0, w_n, b_n, out,
+                       ld, col_f0, col_n, col, ln);
+    return hipGetLastError();
+}
+
+hipError_t launch_copy_cols(const float* src, int64_t src_ld, int c, float* dst, int64_t dst_ld, int dst_c0,
+                            const int32_t* col, int64_t l, hipStream_t s) {
+    hipLaunchKernelGGL(copy_cols_kernel, dim3(blocks_for(l * c, 256)), dim3(256), 0, s, src, src_ld, c, dst, dst_ld,
+                       dst_c0, col, l);
+    return hipGetLastError();
+}
+
+hipError_t launch_adain_pool(const float* x, int64_t ld, int c, const Coef* coef, const int32_t* col_n, int64_t ln,
+                             const float* pw, const float* pb, const int32_t* col_2, uint16_t* out, int64_t out_ld,
+                             hipStream_t s) {
+    hipLaunchKernelGGL(adain_pool_kernel, dim3(blocks_for(2 * ln * out_ld, 256)), dim3(256), 0, s, x, ld, c, coef,
+                       col_n, ln, pw, pb, col_2, out, out_ld);
+    return hipGetLastError();
+}
+
+hipError_t launch_noise_conv(const float* spec, int64_t spec_ld, int64_t l_in, const int32_t* col_in, const float* w,
+                             const float* b, int cout, int k, int stride, int pad, float* y, int64_t y_ld,
+                             int64_t l_out, hipStream_t s) {
+    if (cout > 256 || (kNcRows - 1) * stride + k > (kNcRows - 1) * 6 + 12) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(noise_conv_kernel, dim3(blocks_for(l_out, kNcRows)), dim3(256), 0, s, spec, spec_ld, l_in,
+                       col_in, w, b, cout, k, stride, pad, y, y_ld, l_out);
+    return hipGetLastError();
+}
+
+hipError_t launch_phase_pre(const float* f0, const int64_t* start2, const int64_t* len2, int nb, const float* rand_ini,
+                            float* pp, int64_t pp_ld, hipStream_t s) {
+    hipLaunchKernelGGL(phase_pre_kernel, dim3(nb * kHarmonics), dim3(256), 0, s, f0, start2, len2, rand_ini, pp, pp_ld);
+    return hipGetLastError();
+}
+
+hipError_t launch_source_stft(const SourceParams& p, hipStream_t s) {
+    hipLaunchKernelGGL(source_stft_kernel, dim3((unsigned)p.n_blocks), dim3(256), 0, s, p);
+    return hipGetLastError();
+}
+
+hipError_t launch_istft(const IstftParams& p, hipStream_t s) {
+    hipLaunchKernelGGL(istft_kernel, dim3((unsigned)p.n_blocks), dim3(256), 0, s, p);
+    return hipGetLastError();
+}
+
+hipError_t launch_zero(void* p, int64_t bytes, hipStream_t s) {
+    const int64_t n = bytes / 4;
+    hipLaunchKernelGGL(zero_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, s, (uint32_t*)p, n);
+    return hipGetLastError();
+}
+
+}  // namespace kk

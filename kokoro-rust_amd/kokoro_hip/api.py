@@ -1,0 +1,329 @@
+"""ctypes binding of libkokoro_hip.so (the C ABI declared in include/kokoro_hip.h).
+
+The library is the product; this module only marshals numpy arrays into the ABI's plain pointers.
+It raises if the library is missing: there is no CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(os.path.dirname(HERE), "lib", "libkokoro_hip.so")
+
+KK_OK = 0
+KK_NOISE_COUNTER = 0
+KK_NOISE_FIXED = 1
+STAGES = {"decoder": 1, "source": 2, "gen0": 3, "gen1": 4, "post": 5, "all": 6}
+EXPORTS = [
+    "kk_open", "kk_close", "kk_device_name", "kk_identity", "kk_upload_model", "kk_forward_decoder_batch",
+    "kk_output_free", "kk_plan_create", "kk_plan_create_generator", "kk_plan_create_snake", "kk_plan_run",
+    "kk_plan_sync", "kk_plan_fetch", "kk_plan_tap", "kk_plan_get_info", "kk_plan_free", "kk_set_profiling",
+    "kk_profile_read", "kk_durations_from_logits", "kk_layout_frames", "kk_layout_col_item", "kk_layout_src_row",
+]
+
+
+class KKError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__(f"kokoro_hip error {code}: {msg}")
+        self.code = code
+
+
+class Tensor(C.Structure):
+    _fields_ = [("name", C.c_char_p), ("data", C.c_void_p), ("numel", C.c_int64)]
+
+
+class DecoderItem(C.Structure):
+    _fields_ = [("dur", C.c_void_p), ("n_tok", C.c_int32), ("t_en", C.c_void_p), ("f0", C.c_void_p),
+                ("energy", C.c_void_p), ("ref_s", C.c_void_p), ("noise_kind", C.c_int32), ("seed", C.c_uint64),
+                ("rand_ini", C.c_void_p), ("sine", C.c_void_p), ("sine_len", C.c_int64)]
+
+
+class GeneratorItem(C.Structure):
+    _fields_ = [("x", C.c_void_p), ("n_frames", C.c_int32), ("f0", C.c_void_p), ("ref_s", C.c_void_p),
+                ("noise_kind", C.c_int32), ("seed", C.c_uint64), ("rand_ini", C.c_void_p), ("sine", C.c_void_p),
+                ("sine_len", C.c_int64)]
+
+
+class Output(C.Structure):
+    _fields_ = [("audio", C.POINTER(C.c_float)), ("n_samples", C.c_int64)]
+
+
+class PlanInfo(C.Structure):
+    _fields_ = [("n_items", C.c_int64), ("ln", C.c_int64), ("frames", C.c_int64), ("samples", C.c_int64),
+                ("conv_flop", C.c_double), ("snake_flop", C.c_double), ("device_bytes", C.c_int64),
+                ("launches", C.c_int64)]
+
+
+class ProfileEntry(C.Structure):
+    _fields_ = [("name", C.c_char * 32), ("launches", C.c_int64), ("ms", C.c_double), ("flop", C.c_double)]
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: build it with __graft_entry__.build() "
+                               "(there is no CPU fallback)")
+        L = C.CDLL(LIB_PATH)
+        vp, i32, i64, sz, cp = C.c_void_p, C.c_int, C.c_int64, C.c_size_t, C.c_char_p
+        L.kk_open.argtypes = [i32, C.POINTER(vp), cp, sz]
+        L.kk_close.argtypes = [vp]
+        L.kk_close.restype = None
+        L.kk_device_name.argtypes = [vp, cp, sz]
+        L.kk_identity.restype = C.c_char_p
+        L.kk_upload_model.argtypes = [vp, C.POINTER(Tensor), i32, cp, sz]
+        L.kk_forward_decoder_batch.argtypes = [vp, C.POINTER(DecoderItem), i32, C.POINTER(Output), cp, sz]
+        L.kk_output_free.argtypes = [C.POINTER(Output), i32]
+        L.kk_output_free.restype = None
+        L.kk_plan_create.argtypes = [vp, C.POINTER(DecoderItem), i32, C.POINTER(vp), cp, sz]
+        L.kk_plan_create_generator.argtypes = [vp, C.POINTER(GeneratorItem), i32, C.POINTER(vp), cp, sz]
+        L.kk_plan_create_snake.argtypes = [vp, cp, C.POINTER(vp), C.POINTER(C.c_int64), C.POINTER(vp), i32, i32,
+                                           C.POINTER(vp), cp, sz]
+        L.kk_plan_run.argtypes = [vp, i32, cp, sz]
+        L.kk_plan_sync.argtypes = [vp, cp, sz]
+        L.kk_plan_fetch.argtypes = [vp, C.POINTER(Output), cp, sz]
+        L.kk_plan_tap.argtypes = [vp, cp, i32, vp, i64, cp, sz]
+        L.kk_plan_get_info.argtypes = [vp, C.POINTER(PlanInfo)]
+        L.kk_plan_free.argtypes = [vp]
+        L.kk_plan_free.restype = None
+        L.kk_set_profiling.argtypes = [vp, i32]
+        L.kk_profile_read.argtypes = [vp, C.POINTER(ProfileEntry), i32, C.POINTER(C.c_int), cp, sz]
+        L.kk_durations_from_logits.argtypes = [vp, i32, C.c_float, vp]
+        L.kk_layout_frames.argtypes = [vp, i32, vp]
+        L.kk_layout_frames.restype = i64
+        L.kk_layout_col_item.argtypes = [i64, vp, vp, i32, vp]
+        L.kk_layout_src_row.argtypes = [C.POINTER(vp), vp, i32, vp, vp, i64, vp]
+        _lib = L
+    return _lib
+
+
+def _err():
+    return C.create_string_buffer(1024)
+
+
+def _check(rc, err):
+    if rc != KK_OK:
+        raise KKError(rc, err.value.decode(errors="replace"))
+
+
+def _p(a):
+    return C.c_void_p(a.ctypes.data) if a is not None else C.c_void_p()
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def identity():
+    return lib().kk_identity().decode()
+
+
+# ------------------------------------------------------------------ host rules
+
+
+def durations_from_logits(logits, speed):
+    logits = _f32(logits)
+    out = np.zeros(logits.shape[0], np.int64)
+    rc = lib().kk_durations_from_logits(_p(logits), logits.shape[0], float(speed), _p(out))
+    if rc != KK_OK:
+        raise KKError(rc, "durations_from_logits")
+    return out
+
+
+def layout_frames(nfs):
+    nfs = np.ascontiguousarray(nfs, np.int64)
+    a = np.zeros(len(nfs), np.int64)
+    ln = lib().kk_layout_frames(_p(nfs), len(nfs), _p(a))
+    if ln < 0:
+        raise KKError(int(ln), "layout_frames")
+    return a, int(ln)
+
+
+def layout_col_item(l, start, length):
+    start = np.ascontiguousarray(start, np.int64)
+    length = np.ascontiguousarray(length, np.int64)
+    out = np.zeros(l, np.int32)
+    rc = lib().kk_layout_col_item(l, _p(start), _p(length), len(start), _p(out))
+    if rc != KK_OK:
+        raise KKError(rc, "layout_col_item")
+    return out
+
+
+def layout_src_row(durs, tstart, a, ln):
+    durs = [np.ascontiguousarray(d, np.int64) for d in durs]
+    ptrs = (C.c_void_p * len(durs))(*[d.ctypes.data for d in durs])
+    ntok = np.asarray([len(d) for d in durs], np.int32)
+    out = np.zeros(ln, np.int32)
+    tstart = np.ascontiguousarray(tstart, np.int64)
+    a = np.ascontiguousarray(a, np.int64)
+    rc = lib().kk_layout_src_row(ptrs, _p(ntok), len(durs), _p(tstart), _p(a), ln, _p(out))
+    if rc != KK_OK:
+        raise KKError(rc, "layout_src_row")
+    return out
+
+
+# ------------------------------------------------------------------ device objects
+
+
+class Context:
+    """Gpu::new + GpuKokoro::with_gpu (src/gpu.rs:81-105, 685-724) for the decoder + generator."""
+
+    def __init__(self, ordinal=0):
+        h = C.c_void_p()
+        err = _err()
+        _check(lib().kk_open(ordinal, C.byref(h), err, len(err)), err)
+        self.h = h
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().kk_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def device_name(self):
+        buf = C.create_string_buffer(256)
+        lib().kk_device_name(self.h, buf, 256)
+        return buf.value.decode()
+
+    def upload_model(self, weights: dict):
+        names = list(weights.keys())
+        arrs = [_f32(weights[n]).reshape(-1) for n in names]
+        enc = [n.encode() for n in names]
+        tab = (Tensor * len(names))(*[Tensor(e, a.ctypes.data, a.size) for e, a in zip(enc, arrs)])
+        err = _err()
+        _check(lib().kk_upload_model(self.h, tab, len(names), err, len(err)), err)
+
+    def set_profiling(self, on):
+        lib().kk_set_profiling(self.h, int(bool(on)))
+
+    def profile_read(self):
+        ents = (ProfileEntry * 8)()
+        n = C.c_int()
+        err = _err()
+        _check(lib().kk_profile_read(self.h, ents, 8, C.byref(n), err, len(err)), err)
+        return {e.name.decode(): {"launches": e.launches, "ms": e.ms, "flop": e.flop} for e in ents[: n.value]}
+
+    # -------------------------------------------------------------- batch entry points
+    def forward_decoder_batch(self, items):
+        """kk_forward_decoder_batch: list of workloads.DecoderItem -> list of audio arrays."""
+        arr, keep = _decoder_items(items)
+        outs = (Output * len(items))()
+        err = _err()
+        _check(lib().kk_forward_decoder_batch(self.h, arr, len(items), outs, err, len(err)), err)
+        res = [np.ctypeslib.as_array(o.audio, shape=(o.n_samples,)).copy() for o in outs]
+        lib().kk_output_free(outs, len(items))
+        del keep
+        return res
+
+    def plan(self, items):
+        return Plan.decoder(self, items)
+
+
+def _decoder_items(items):
+    keep = []
+    arr = (DecoderItem * len(items))()
+    for i, it in enumerate(items):
+        dur = np.ascontiguousarray(it.dur, np.int64)
+        t_en, f0, en, rs = _f32(it.t_en), _f32(it.f0), _f32(it.energy), _f32(it.ref_s)
+        keep += [dur, t_en, f0, en, rs]
+        d = arr[i]
+        d.dur, d.n_tok, d.t_en, d.f0, d.energy, d.ref_s = dur.ctypes.data, len(dur), t_en.ctypes.data, \
+            f0.ctypes.data, en.ctypes.data, rs.ctypes.data
+        if it.sine is not None:
+            ri, sn = _f32(it.rand_ini), _f32(it.sine)
+            keep += [ri, sn]
+            d.noise_kind, d.rand_ini, d.sine, d.sine_len = KK_NOISE_FIXED, ri.ctypes.data, sn.ctypes.data, sn.size
+        else:
+            d.noise_kind, d.seed = KK_NOISE_COUNTER, int(it.seed) & 0xFFFFFFFFFFFFFFFF
+    return arr, keep
+
+
+class Plan:
+    def __init__(self, ctx, h, n, kind):
+        self.ctx, self.h, self.n, self.kind = ctx, h, n, kind
+
+    @classmethod
+    def decoder(cls, ctx, items):
+        arr, keep = _decoder_items(items)
+        h = C.c_void_p()
+        err = _err()
+        _check(lib().kk_plan_create(ctx.h, arr, len(items), C.byref(h), err, len(err)), err)
+        return cls(ctx, h, len(items), "decoder")
+
+    @classmethod
+    def generator(cls, ctx, xs, f0s, ref_ss, seeds):
+        """Generator-only plan: x [512, 2N], f0 [2N], ref_s [>=128], counter seeds."""
+        keep = []
+        arr = (GeneratorItem * len(xs))()
+        for i, (x, f0, rs, sd) in enumerate(zip(xs, f0s, ref_ss, seeds)):
+            x, f0 = _f32(x), _f32(f0)
+            rs = _f32(np.pad(np.asarray(rs, np.float32), (0, max(0, 256 - len(rs)))))
+            keep += [x, f0, rs]
+            g = arr[i]
+            g.x, g.n_frames, g.f0, g.ref_s = x.ctypes.data, x.shape[1] // 2, f0.ctypes.data, rs.ctypes.data
+            g.noise_kind, g.seed = KK_NOISE_COUNTER, int(sd) & 0xFFFFFFFFFFFFFFFF
+        h = C.c_void_p()
+        err = _err()
+        _check(lib().kk_plan_create_generator(ctx.h, arr, len(xs), C.byref(h), err, len(err)), err)
+        return cls(ctx, h, len(xs), "generator")
+
+    @classmethod
+    def snake(cls, ctx, prefix, xs, ref_ss, gap=40):
+        xs = [_f32(x) for x in xs]
+        rss = [_f32(np.pad(np.asarray(r, np.float32), (0, max(0, 256 - len(r))))) for r in ref_ss]
+        xp = (C.c_void_p * len(xs))(*[x.ctypes.data for x in xs])
+        rp = (C.c_void_p * len(xs))(*[r.ctypes.data for r in rss])
+        ts = (C.c_int64 * len(xs))(*[x.shape[1] for x in xs])
+        h = C.c_void_p()
+        err = _err()
+        _check(lib().kk_plan_create_snake(ctx.h, prefix.encode(), xp, ts, rp, len(xs), gap, C.byref(h), err,
+                                          len(err)), err)
+        p = cls(ctx, h, len(xs), "snake")
+        p.shapes = [x.shape for x in xs]
+        return p
+
+    def run(self, until="all"):
+        err = _err()
+        _check(lib().kk_plan_run(self.h, STAGES[until] if isinstance(until, str) else int(until), err, len(err)),
+               err)
+
+    def sync(self):
+        err = _err()
+        _check(lib().kk_plan_sync(self.h, err, len(err)), err)
+
+    def fetch(self):
+        outs = (Output * self.n)()
+        err = _err()
+        _check(lib().kk_plan_fetch(self.h, outs, err, len(err)), err)
+        res = [np.ctypeslib.as_array(o.audio, shape=(o.n_samples,)).copy() for o in outs]
+        lib().kk_output_free(outs, self.n)
+        if self.kind == "snake":
+            res = [r.reshape(s) for r, s in zip(res, self.shapes)]
+        return res
+
+    def tap(self, name, item, shape):
+        out = np.zeros(shape, np.float32)
+        err = _err()
+        _check(lib().kk_plan_tap(self.h, name.encode(), item, _p(out), out.size, err, len(err)), err)
+        return out
+
+    def info(self):
+        inf = PlanInfo()
+        lib().kk_plan_get_info(self.h, C.byref(inf))
+        return {k: getattr(inf, k) for k, _ in PlanInfo._fields_}
+
+    def free(self):
+        if getattr(self, "h", None):
+            lib().kk_plan_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.free()

@@ -1,0 +1,104 @@
+/*
+ * kk_oracle.h -- CPU fp32 restatement of kokoro-rust's batched decoder + iSTFTNet generator path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the checker the HIP path is compared against; only
+ * tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it.  The product path
+ * (kokoro-rust_amd/) never links, loads or calls it.
+ *
+ * Layout: per item, channel-major [C][T] float arrays (the reference's host convention,
+ * src/nn.rs:1-2).  Ragged packing is restated separately (ko_layout_*) so its tables can be
+ * compared bit-for-bit; the forward functions run one item at a time, which the reference's
+ * gap-masked packed layout reproduces exactly (docs/design/BATCHING.md:16-42).
+ *
+ * Precision: fp32 storage and arithmetic, f64 where the reference accumulates in f64
+ * (statistics, SineGen cumulative sum, STFT/iSTFT).  Compiled with -ffp-contract=off; fused
+ * multiply-adds appear only where the reference writes fmaf() explicitly.
+ *
+ * Every function returns 0 on success, a negative value on a shape error.
+ */
+#ifndef KK_ORACLE_H
+#define KK_ORACLE_H
+#include <stddef.h>
+#include <stdint.h>
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---------------------------------------------------------------- numerics switches */
+/* When set, every input operand and weight of the layers the HIP path runs on bf16 MFMA is rounded
+ * to bf16 (round-to-nearest-even) before the fp32 product; accumulation stays fp32.  Used to
+ * predict the GPU's error budget; the default (0) is the fp32 reference path. */
+void ko_set_bf16_emulation(int on);
+int ko_get_bf16_emulation(void);
+/* Error-budget analysis: fmt 0 off, 1 bf16, 2 fp16; groups = OR of KO_GROUP_*. */
+#define KO_GROUP_DECODER 1
+#define KO_GROUP_SNAKE 2
+#define KO_GROUP_POST 4
+#define KO_GROUP_UPS 8
+void ko_set_operand_emulation(int fmt, int groups);
+float ko_fp16_round(float x);
+void ko_set_threads(int n);
+float ko_bf16_round(float x);
+
+/* ---------------------------------------------------------------- ragged layout (a1-a3) */
+/* Frame layout (src/gpu_batch.rs:250-263): a[b] = sum_{j<b}(N_j + gap); ln = sum(N_b + gap).
+ * col_item (length l) = item index on [start_b, start_b + len_b), -1 elsewhere. */
+int ko_layout_frames(const int64_t* nfs, int nb, int gap, int64_t* a_out, int64_t* ln_out);
+int ko_layout_col_item(int64_t l, const int64_t* start, const int64_t* len, int nb, int32_t* col_item);
+/* Duration expansion table (src/gpu_batch.rs:265-276): src_row[a_b + f] = tstart_b + tok. */
+int ko_layout_src_row(const int64_t* const* dur, const int64_t* ntok, int nb, const int64_t* tstart,
+                      const int64_t* a, int64_t ln, int32_t* src_row);
+/* durations_from_logits (src/model.rs:90-99): d = max(1, rint_half_even(sum_j sigmoid(l_ij) / speed)). */
+void ko_durations_from_logits(const float* logits, int t, float speed, int64_t* out);
+
+/* ---------------------------------------------------------------- primitives */
+/* Conv1d: y[co][o] = b[co] + sum_k sum_ci w[co][ci][k] * x[ci][o*s + k*d - p] (zero outside [0,T)). */
+int ko_conv1d(const float* x, int cin, int t, const float* w, const float* b, int cout, int k, int stride,
+              int pad, int dil, float* y, int tout);
+/* ConvTranspose1d, w [cin][cout][k]; tout = (t-1)*s + k - 2p (kernels/kokoro.cu:169-185). */
+int ko_conv_transpose1d(const float* x, int cin, int t, const float* w, const float* b, int cout, int k,
+                        int stride, int pad, float* y, int tout);
+/* Per-channel instance statistics (kernels/kokoro.cu:779-810): biased variance, eps 1e-5. */
+void ko_chan_stats(const float* x, int c, int t, float* mean, float* rstd);
+/* Style projection gb[2C] = fc_w[2C][128] * s + fc_b (src/gpu_batch.rs:84). */
+void ko_style_fc(const float* fc_w, const float* fc_b, int c2, const float* s, float* gb);
+/* AdaIN apply + activation: mode 0 = leaky(slope), 1 = Snake with alpha[c]. */
+void ko_adain_apply(const float* x, int c, int t, const float* mean, const float* rstd, const float* nw,
+                    const float* nb, const float* gb, int mode, float slope, const float* alpha, float* y);
+/* SineGen noise (src/vocoder.rs:17-41, kernels/kokoro.cu:284-302). */
+uint64_t ko_splitmix_at(uint64_t seed, uint64_t ctr);
+void ko_rand_ini(uint64_t seed, float* out9);
+void ko_gen_noise(uint64_t seed, float* out, int64_t n);
+/* Harmonic source (kernels/kokoro.cu:188-254): f0c [L] -> har [300 L]. noise [300 L * 9]. */
+int ko_sine_source(const float* f0c, int l, const float* rand_ini, const float* noise, const float* lw, float lb,
+                   float* phase_pre /* [9][L] or NULL */, float* har);
+/* STFT n_fft 20 hop 5 (kernels/kokoro.cu:470-490): x [L] -> out [22][F], F = 1 + L/5. */
+int ko_stft20(const float* x, int l, float* out, int f);
+/* iSTFT (kernels/kokoro.cu:264-280, 492-508): post [22][F] -> audio [5(F-1)]. */
+int ko_istft20(const float* post, int f, float* audio);
+
+/* ---------------------------------------------------------------- model */
+typedef struct ko_model ko_model;
+/* Weight table by checkpoint name (weight_norm already resolved). */
+int ko_model_create(int n, const char* const* names, const float* const* data, const int64_t* numel,
+                    ko_model** out, char* err, size_t errlen);
+void ko_model_free(ko_model* m);
+
+/* Decoder (src/gpu_batch.rs:299-317): asr [512][N], f0 [2N], en [2N], style [128] -> x [512][2N]. */
+int ko_decoder_forward(const ko_model* m, const float* asr, const float* f0, const float* en, const float* style,
+                       int n, float* x_out);
+/* Generator (src/gpu_batch.rs:319-420): x [512][2N], f0 [2N], style [128], noise [600N*9], rand_ini[9]
+ * -> audio [600N]. spec_out [22][120N+1] and post_out [22][120N+1] are optional taps. */
+int ko_generator_forward(const ko_model* m, const float* x, const float* f0, const float* style, int n,
+                         const float* rand_ini, const float* noise, float* audio, float* spec_out, float* post_out);
+/* One AdaINResBlock1 (src/gpu_batch.rs:140-154): x [C][T] -> out [C][T] (x + three dilation steps). */
+int ko_snake_block_forward(const ko_model* m, const char* prefix, const float* x, int t, const float* style,
+                           float* out);
+/* One AdainResBlk1d (src/gpu_batch.rs:104-135): x [Cin][T] -> out [Cout][T or 2T]. */
+int ko_resblk_forward(const ko_model* m, const char* prefix, const float* x, int t, const float* style,
+                      float* out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
