@@ -886,18 +886,11 @@ static void resblock_mean(const ko_model* m, int first, const float* y, int t, c
     free(r);
 }
 
-/* Generator (src/gpu_batch.rs:319-420), one item. */
-int ko_generator_forward(const ko_model* m, const float* x_in, const float* f0, const float* style, int n,
-                         const float* rand_ini, const float* noise, float* audio, float* spec_out, float* post_out) {
+/* Generator stages after the source (src/gpu_batch.rs:358-420), one item, from spec [22][120N+1]. */
+int ko_generator_from_spec(const ko_model* m, const float* x_in, const float* spec, const float* style, int n,
+                           float* audio, float* post_out) {
     if (n <= 0) return -1;
-    const int l2 = 2 * n, s = 600 * n, f = 120 * n + 1, t0 = 20 * n, t1 = 120 * n + 1;
-    float* har = (float*)malloc((size_t)s * sizeof(float));
-    ko_sine_source(f0, l2, rand_ini, noise, m->l_w, m->l_b, NULL, har);
-    float* spec = (float*)malloc((size_t)22 * f * sizeof(float));
-    ko_stft20(har, s, spec, f);
-    free(har);
-    if (spec_out) memcpy(spec_out, spec, (size_t)22 * f * sizeof(float));
-
+    const int l2 = 2 * n, f = 120 * n + 1, t0 = 20 * n, t1 = 120 * n + 1;
     /* stage 0 */
     float* x = (float*)malloc((size_t)512 * l2 * sizeof(float));
     memcpy(x, x_in, (size_t)512 * l2 * sizeof(float));
@@ -944,6 +937,21 @@ int ko_generator_forward(const ko_model* m, const float* x_in, const float* f0, 
     ko_istft20(post, t1, audio);
     free(x2);
     free(post);
-    free(spec);
     return 0;
+}
+
+/* Generator (src/gpu_batch.rs:319-420), one item: source + STFT, then the stages above. */
+int ko_generator_forward(const ko_model* m, const float* x_in, const float* f0, const float* style, int n,
+                         const float* rand_ini, const float* noise, float* audio, float* spec_out, float* post_out) {
+    if (n <= 0) return -1;
+    const int l2 = 2 * n, s = 600 * n, f = 120 * n + 1;
+    float* har = (float*)malloc((size_t)s * sizeof(float));
+    ko_sine_source(f0, l2, rand_ini, noise, m->l_w, m->l_b, NULL, har);
+    float* spec = (float*)malloc((size_t)22 * f * sizeof(float));
+    ko_stft20(har, s, spec, f);
+    free(har);
+    if (spec_out) memcpy(spec_out, spec, (size_t)22 * f * sizeof(float));
+    int rc = ko_generator_from_spec(m, x_in, spec, style, n, audio, post_out);
+    free(spec);
+    return rc;
 }

@@ -91,6 +91,9 @@ int ko_decoder_forward(const ko_model* m, const float* asr, const float* f0, con
  * -> audio [600N]. spec_out [22][120N+1] and post_out [22][120N+1] are optional taps. */
 int ko_generator_forward(const ko_model* m, const float* x, const float* f0, const float* style, int n,
                          const float* rand_ini, const float* noise, float* audio, float* spec_out, float* post_out);
+/* The generator stages after the source + STFT, from a given spec [22][120N+1]. */
+int ko_generator_from_spec(const ko_model* m, const float* x, const float* spec, const float* style, int n,
+                           float* audio, float* post_out);
 /* One AdaINResBlock1 (src/gpu_batch.rs:140-154): x [C][T] -> out [C][T] (x + three dilation steps). */
 int ko_snake_block_forward(const ko_model* m, const char* prefix, const float* x, int t, const float* style,
                            float* out);

@@ -54,6 +54,7 @@ def lib():
         L.ko_decoder_forward.argtypes = [C.c_void_p, _f32p, _f32p, _f32p, _f32p, C.c_int, _f32p]
         L.ko_generator_forward.argtypes = [C.c_void_p, _f32p, _f32p, _f32p, C.c_int, _f32p, _f32p, _f32p,
                                            C.c_void_p, C.c_void_p]
+        L.ko_generator_from_spec.argtypes = [C.c_void_p, _f32p, _f32p, _f32p, C.c_int, _f32p, C.c_void_p]
         L.ko_snake_block_forward.argtypes = [C.c_void_p, C.c_char_p, _f32p, C.c_int, _f32p, _f32p]
         L.ko_resblk_forward.argtypes = [C.c_void_p, C.c_char_p, _f32p, C.c_int, _f32p, _f32p]
         _lib = L
@@ -258,6 +259,15 @@ class Model:
                                         audio, spec.ctypes.data if taps else None,
                                         post.ctypes.data if taps else None), "generator")
         return (audio, spec, post) if taps else audio
+
+    def generator_from_spec(self, x, spec, style):
+        x = _f32(x)
+        n = x.shape[1] // 2
+        audio = np.zeros(600 * n, np.float32)
+        post = np.zeros((22, 120 * n + 1), np.float32)
+        _chk(lib().ko_generator_from_spec(self.h, x, _f32(spec), _f32(style[:128]), n, audio, post.ctypes.data),
+             "generator_from_spec")
+        return audio, post
 
     def snake_block(self, prefix, x, style):
         x = _f32(x)
