@@ -10,8 +10,10 @@
 #include <cstdlib>
 #include <cstring>
 #include <map>
+#include <set>
 #include <memory>
 #include <string>
+#include <tuple>
 #include <vector>
 
 #include "kk_common.h"
@@ -155,8 +157,11 @@ enum { PC_SNAKE = 0, PC_DECODER = 1, PC_CONVT = 2, PC_POST = 3 };
 
 }  // namespace kk
 
+struct kk_plan;
 struct kk_ctx {
     int device = 0;
+    int n_cu = 1;
+    std::set<kk_plan*> plans;  // live plans: released (and orphaned) by kk_close
     hipStream_t stream = nullptr;
     std::string name;
     kk::Model model;
@@ -188,7 +193,7 @@ static void load_conv(MConv& c, const Table& t, const std::string& p, int cin, i
     c.cin = cin, c.cout = cout, c.k = k, c.pad = pad, c.dil = dil, c.shape = shape, c.bias = bias;
     c.cin_pad = round_up(cin, 64);
     c.m = cout;
-    c.m_pad = round_up(cout, conv_block_m(shape));
+    c.m_pad = round_up(cout, kShapeM[shape]);
     const float* w = t.get(p + ".weight", (int64_t)cout * cin * k);
     const int ncc = c.cin_pad / 32;
     std::vector<uint16_t> pk((size_t)k * ncc * c.m_pad * 32, 0);
@@ -209,10 +214,10 @@ static void load_conv(MConv& c, const Table& t, const std::string& p, int cin, i
 // m = phase * cout + co produces output column stride * i + phase - pad (see kk_conv.hip).
 static void load_convt(MConv& c, const Table& t, const std::string& p, int cin, int cout, int kw, int stride) {
     check(kw == 2 * stride, p + ": polyphase ConvT needs K = 2 * stride");
-    c.cin = cin, c.cout = cout, c.k = 2, c.pad = 1, c.dil = 1, c.shape = SHAPE_W4x2, c.bias = true;
+    c.cin = cin, c.cout = cout, c.k = 2, c.pad = 1, c.dil = 1, c.shape = SHAPE_256x128, c.bias = true;
     c.cin_pad = round_up(cin, 64);
     c.m = stride * cout;
-    c.m_pad = round_up(c.m, conv_block_m(c.shape));
+    c.m_pad = round_up(c.m, kShapeM[c.shape]);
     const float* w = t.get(p + ".weight", (int64_t)cin * cout * kw);
     const int ncc = c.cin_pad / 32;
     std::vector<uint16_t> pk((size_t)2 * ncc * c.m_pad * 32, 0);
@@ -252,7 +257,7 @@ static void load_adain(MAdain& a, const Table& t, const std::string& p, int c, S
 static void load_snake(MSnake& s, const Table& t, const std::string& p, int c, int k, StyleRows& sr) {
     static const int dil[3] = {1, 3, 5};
     s.c = c;
-    const int shape = c >= 256 ? SHAPE_W4x2 : SHAPE_W2x4;
+    const int shape = c >= 256 ? SHAPE_256x128 : SHAPE_128x256;
     for (int i = 0; i < 3; i++) {
         const std::string si = std::to_string(i);
         load_conv(s.c1[i], t, p + ".convs1." + si, c, c, k, (k * dil[i] - dil[i]) / 2, dil[i], true, shape);
@@ -277,12 +282,12 @@ static void load_snake(MSnake& s, const Table& t, const std::string& p, int c, i
 static void load_resblk(MResblk& r, const Table& t, const std::string& p, int din, int dout, bool up,
                         StyleRows& sr) {
     r.din = din, r.dout = dout, r.up = up;
-    load_conv(r.conv1, t, p + ".conv1", din, dout, 3, 1, 1, true, SHAPE_W4x2);
-    load_conv(r.conv2, t, p + ".conv2", dout, dout, 3, 1, 1, true, SHAPE_W4x2);
+    load_conv(r.conv1, t, p + ".conv1", din, dout, 3, 1, 1, true, SHAPE_256x128);
+    load_conv(r.conv2, t, p + ".conv2", dout, dout, 3, 1, 1, true, SHAPE_256x128);
     load_adain(r.n1, t, p + ".norm1", din, sr);
     load_adain(r.n2, t, p + ".norm2", dout, sr);
     r.has1x1 = din != dout;
-    if (r.has1x1) load_conv(r.conv1x1, t, p + ".conv1x1", din, dout, 1, 0, 1, false, SHAPE_W4x2);
+    if (r.has1x1) load_conv(r.conv1x1, t, p + ".conv1x1", din, dout, 1, 0, 1, false, SHAPE_256x128);
     if (up) {
         r.pool_w.upload(t.get(p + ".pool.weight", (int64_t)din * 3), (size_t)din * 3);
         r.pool_b.upload(t.get(p + ".pool.bias", din), din);
@@ -306,7 +311,7 @@ static void load_model(kk_ctx* ctx, const kk_tensor* tensors, int n) {
     m.f0b.upload(t.get("decoder.F0_conv.bias", 1), 1);
     m.nw_.upload(t.get("decoder.N_conv.weight", 3), 3);
     m.nb_.upload(t.get("decoder.N_conv.bias", 1), 1);
-    load_conv(m.asr_res, t, "decoder.asr_res.0", 512, 64, 1, 0, 1, true, SHAPE_W1x4);
+    load_conv(m.asr_res, t, "decoder.asr_res.0", 512, 64, 1, 0, 1, true, SHAPE_64x256);
     const std::string g = "decoder.generator";
     m.lw.upload(t.get(g + ".m_source.l_linear.weight", kHarmonics), kHarmonics);
     m.lb = t.get(g + ".m_source.l_linear.bias", 1)[0];
@@ -325,7 +330,7 @@ static void load_model(kk_ctx* ctx, const kk_tensor* tensors, int n) {
     static const int ks[3] = {3, 7, 11};
     for (int i = 0; i < 6; i++)
         load_snake(m.rb[i], t, g + ".resblocks." + std::to_string(i), i < 3 ? 256 : 128, ks[i % 3], sr);
-    load_conv(m.post, t, g + ".conv_post", 128, 22, 7, 3, 1, true, SHAPE_W1x4);
+    load_conv(m.post, t, g + ".conv_post", 128, 22, 7, 3, 1, true, SHAPE_64x256);
     // style projections of every AdaIN, transposed [128][rows]
     std::vector<float> wt((size_t)kStyleDim * sr.rows);
     for (int r = 0; r < sr.rows; r++)
@@ -366,6 +371,35 @@ struct Dom {
     DomDev dev() const { return DomDev{l, col_d.as<int32_t>(), start_d.as<int64_t>(), len_d.as<int64_t>(), (int)start.size()}; }
 };
 
+// Item-aligned GEMM-column tiles of a domain (see TilesDev in kk_kernels.h).
+struct Tiles {
+    DevBuf item, t0, n, lo, hi;
+    int64_t count = 0;
+    int width = 0;
+    TilesDev dev() const {
+        return TilesDev{item.as<int32_t>(), t0.as<int64_t>(), n.as<int32_t>(), lo.as<int32_t>(), hi.as<int32_t>(),
+                        count};
+    }
+    // tiles of width `w` over [start_b, start_b + len_b + extra) for every item (extra = 1: the
+    // ConvT GEMM column one past the item's last input)
+    void build(const Dom& d, int w, int extra) {
+        std::vector<int32_t> it, nn, lo(d.start.size()), hi(d.start.size());
+        std::vector<int64_t> t;
+        for (size_t b = 0; b < d.start.size(); b++) {
+            lo[b] = (int32_t)it.size();
+            const int64_t len = d.len[b] + extra;
+            for (int64_t j = 0; j < len; j += w) {
+                it.push_back((int32_t)b);
+                t.push_back(d.start[b] + j);
+                nn.push_back((int32_t)std::min<int64_t>(w, len - j));
+            }
+            hi[b] = (int32_t)it.size();
+        }
+        count = (int64_t)it.size(), width = w;
+        item.upload(it), t0.upload(t), n.upload(nn), this->lo.upload(lo), this->hi.upload(hi);
+    }
+};
+
 enum PlanKind { PLAN_DECODER = 0, PLAN_GENERATOR = 1, PLAN_SNAKE = 2 };
 
 }  // namespace kk
@@ -386,7 +420,20 @@ struct kk_plan {
     int64_t t_rows = 0;
     // intermediates
     kk::DevBuf gb, xcat, xin_a, xin_b, hdec, pool, sc_half, dec_out, pp, spec, B[6], post, audio, audio_start;
-    kk::DevBuf sums, coef[3];
+    kk::DevBuf part, coef[5];
+    int64_t part_bytes = 0;
+    std::map<std::tuple<const kk::Dom*, int, int>, std::unique_ptr<kk::Tiles>> tiles;
+    // item-aligned tiles of domain d, width w (built on first use, at plan creation)
+    const kk::Tiles& tl(const kk::Dom& d, int w, int extra = 0) {
+        auto key = std::make_tuple(&d, w, extra);
+        auto it = tiles.find(key);
+        if (it == tiles.end()) {
+            auto t = std::make_unique<kk::Tiles>();
+            t->build(d, w, extra);
+            it = tiles.emplace(key, std::move(t)).first;
+        }
+        return *it->second;
+    }
     kk::DevBuf src_item, src_f0, ist_item, ist_s0;
     int64_t n_src = 0, n_ist = 0;
     int64_t dev_bytes = 0;
@@ -396,8 +443,8 @@ struct kk_plan {
     std::vector<kk::DevBuf*> owned() {
         return {&t_en, &src_row, &f0, &en, &style, &seeds, &kinds, &rand_ini, &fixed_noise, &gb, &xcat, &xin_a,
                 &xin_b, &hdec, &pool, &sc_half, &dec_out, &pp, &spec, &B[0], &B[1], &B[2], &B[3], &B[4], &B[5],
-                &post, &audio, &audio_start, &sums, &coef[0], &coef[1], &coef[2], &src_item, &src_f0, &ist_item,
-                &ist_s0};
+                &post, &audio, &audio_start, &part, &coef[0], &coef[1], &coef[2], &coef[3], &coef[4], &src_item,
+                &src_f0, &ist_item, &ist_s0};
     }
 };
 
@@ -505,16 +552,28 @@ static void setup_generator(kk_plan* p, const std::vector<const float*>& f0s, co
     for (int i = 0; i < 6; i++) alloc_zero(p, p->B[i], big);
     alloc_zero(p, p->post, (size_t)l120 * kPostLd * sizeof(float));
     alloc_zero(p, p->audio, (size_t)600 * ln * sizeof(float));
-    alloc_zero(p, p->sums, (size_t)nb * kXinLd * 2 * sizeof(double));
-    for (int i = 0; i < 3; i++) p->coef[i].alloc((size_t)nb * kXinLd * sizeof(Coef));
+    for (int i = 0; i < 5; i++) p->coef[i].alloc((size_t)nb * kXinLd * sizeof(Coef));
+    // statistics partials: every partial covers at most 128 columns of one item
+    auto bound = [&](int64_t l, int64_t c) { return (l / 128 + 2 * (int64_t)nb + 2) * c; };
+    const int64_t np = std::max({bound(ln, 1152), bound(2 * ln, 512), bound(l20, 256), bound(l120, 128)});
+    p->part.alloc((size_t)np * sizeof(StatPart));
+    p->part_bytes = (int64_t)p->part.bytes;
 }
 
+struct Runner;
+static void prebuild_tiles(kk_plan* p);
+
 static void finish_plan(kk_plan* p) {
+    prebuild_tiles(p);
     KK_HIP(hipStreamSynchronize(p->ctx->stream));
     p->dev_bytes = 0;
     for (DevBuf* b : p->owned()) p->dev_bytes += (int64_t)b->bytes;
     for (kk::Dom* d : {&p->dn, &p->d2, &p->d20, &p->d120, &p->ds})
         p->dev_bytes += (int64_t)(d->col_d.bytes + d->start_d.bytes + d->len_d.bytes);
+    for (auto& kv : p->tiles) {
+        const kk::Tiles& t = *kv.second;
+        p->dev_bytes += (int64_t)(t.item.bytes + t.t0.bytes + t.n.bytes + t.lo.bytes + t.hi.bytes);
+    }
 }
 
 static void check_noise(const NoiseIn& nz, int64_t n_frames, int b) {
@@ -592,6 +651,7 @@ static kk_plan* create_decoder_plan(kk_ctx* ctx, const kk_decoder_item* items, i
     alloc_zero(p.get(), p->sc_half, (size_t)ln * 512 * sizeof(float));
     alloc_zero(p.get(), p->dec_out, (size_t)2 * ln * 512 * sizeof(float));
     finish_plan(p.get());
+    ctx->plans.insert(p.get());
     return p.release();
 }
 
@@ -626,6 +686,7 @@ static kk_plan* create_generator_plan(kk_ctx* ctx, const kk_generator_item* item
     }
     p->dec_out.upload(xh);
     finish_plan(p.get());
+    ctx->plans.insert(p.get());
     return p.release();
 }
 
@@ -668,21 +729,30 @@ static kk_plan* create_snake_plan(kk_ctx* ctx, const char* prefix, const float* 
     p->style.upload(sth);
     p->gb.alloc((size_t)n * ctx->model.style_rows * sizeof(float));
     alloc_zero(p.get(), p->B[1], (size_t)l * c * sizeof(float));
-    alloc_zero(p.get(), p->sums, (size_t)n * c * 2 * sizeof(double));
-    p->coef[0].alloc((size_t)n * c * sizeof(Coef));
+    for (int i = 0; i < 2; i++) p->coef[i].alloc((size_t)n * c * sizeof(Coef));
+    p->part.alloc((size_t)(l / 128 + 2 * (int64_t)n + 2) * c * sizeof(StatPart));
+    p->part_bytes = (int64_t)p->part.bytes;
     finish_plan(p.get());
+    ctx->plans.insert(p.get());
     return p.release();
 }
 
 // ------------------------------------------------------------------ the launch sequence
+#define KK_LAUNCH(x)                  \
+    do {                              \
+        if (!dry) KK_HIP(x);          \
+    } while (0)
+
 struct Runner {
     kk_plan* p;
     kk_ctx* ctx;
     const Model& m;
     hipStream_t s;
+    bool dry = false;  // build the plan's tile lists only, launch nothing
     double flop = 0, snake_flop = 0;
     int64_t launches = 0;
     int64_t gb_ld() const { return m.style_rows; }
+    Coef* cf(int i) const { return p->coef[i].as<Coef>(); }
 
     hipEvent_t ev() {
         if (!ctx->event_pool.empty()) {
@@ -695,93 +765,132 @@ struct Runner {
         return e;
     }
 
-    void stats_fin(const float* x, int64_t ld, int c, const Dom& d, const MAdain& a, Coef* coef, bool stats = true,
-                   int reset = 1) {
-        if (stats) {
-            KK_HIP(launch_stats(x, ld, c, d.dev(), p->sums.as<double>(), s));
-            launches++;
-        }
-        KK_HIP(launch_finalize(x, ld, c, d.dev(), p->sums.as<double>(), p->gb.as<float>(), gb_ld(), a.gb_off,
-                               a.nw.as<float>(), a.nb.as<float>(), coef, reset, s));
-        launches++;
+    void need_part(int64_t n) {
+        check(n * (int64_t)sizeof(StatPart) <= p->part_bytes, "statistics partials buffer too small");
     }
 
-    // One MFMA conv launch; `valid` = algorithmic columns (FLOP accounting).
-    void conv(const MConv& c, int pro, int epi, const void* x, int64_t x_ld, int64_t l_in, const int32_t* col_in,
-              float* y, int64_t y_ld, int64_t n_out, double valid, int cls, const Coef* coef = nullptr,
-              const DevBuf* ar = nullptr, const DevBuf* ai = nullptr, float slope = 0.f, const float* r0 = nullptr,
-              const float* r1 = nullptr, const float* r2 = nullptr, int64_t r0_ld = 0, float scale = 1.f,
-              int stride_t = 1, int pad_t = 0, int64_t l_convt = 0, const Dom* dpad = nullptr) {
+    // Standalone statistics partials of x over domain d (tiles of kStatTile rows).
+    const Tiles& stats(const float* x, int64_t ld, int c, const Dom& d) {
+        const Tiles& t = p->tl(d, kStatTile);
+        need_part(t.count * c);
+        KK_LAUNCH(launch_stats_tiles(x, ld, c, t.dev(), p->part.as<StatPart>(), s));
+        launches++;
+        return t;
+    }
+    // Partials -> coefficients of AdaIN layer a.
+    void fin(const Tiles& t, int wn, int wcols, int c, const MAdain& a, Coef* coef) {
+        KK_LAUNCH(launch_finalize(p->part.as<StatPart>(), c, wn, wcols, t.dev(), p->nb, p->gb.as<float>(), gb_ld(),
+                               a.gb_off, a.nw.as<float>(), a.nb.as<float>(), coef, s));
+        launches++;
+    }
+    void stats_fin(const float* x, int64_t ld, int c, const Dom& d, const MAdain& a, Coef* coef) {
+        fin(stats(x, ld, c, d), 1, kStatTile, c, a, coef);
+    }
+
+    // One MFMA conv launch.
+    struct Op {
+        int pro = PRO_F32, epi = EPI_STORE;
+        const void* x = nullptr;
+        int64_t x_ld = 0;
+        const Dom* din = nullptr;   // input domain: rows outside the tile's item read as 0
+        float* y = nullptr;
+        int64_t y_ld = 0;
+        const Dom* dout = nullptr;  // output domain (tiles of stride-1 convs)
+        const Coef* coef = nullptr;
+        const DevBuf* ar = nullptr;
+        const DevBuf* ai = nullptr;
+        float slope = 0.f;
+        const float *r0 = nullptr, *r1 = nullptr, *r2 = nullptr;
+        int64_t r0_ld = 0;
+        float scale = 1.f;
+        bool stats = false;
+        int cls = PC_DECODER;
+        bool convt = false;
+        int stride = 1, pad_t = 0;
+        bool in_h = false, out_h = false;  // fp16 input / output (the Snake steps' h)
+    };
+    const Tiles& conv(const MConv& c, const Op& o) {
+        const int wn = kShapeWN[c.shape], bn = kShapeN[c.shape];
+        const Tiles& t = o.convt ? p->tl(*o.din, bn, 1) : p->tl(*o.dout, bn);
         ConvParams q{};
-        q.x = x, q.x_ld = x_ld, q.l_in = l_in, q.cin = c.cin, q.cin_pad = c.cin_pad, q.col_in = col_in;
-        q.coef = coef, q.alpha_rev = ar ? ar->as<float>() : nullptr, q.alpha_inv = ai ? ai->as<float>() : nullptr;
-        q.slope = slope, q.w = c.w.as<uint16_t>(), q.bias = c.bias ? c.b.as<float>() : nullptr;
+        q.x = o.x, q.x_ld = o.x_ld, q.l_in = o.din->l, q.cin = c.cin, q.cin_pad = c.cin_pad;
+        q.in_start = o.din->start_d.as<int64_t>(), q.in_len = o.din->len_d.as<int64_t>();
+        q.tiles = t.dev();
+        q.coef = o.coef, q.alpha_rev = o.ar ? o.ar->as<float>() : nullptr;
+        q.alpha_inv = o.ai ? o.ai->as<float>() : nullptr, q.slope = o.slope;
+        q.w = c.w.as<uint16_t>(), q.bias = c.bias ? c.b.as<float>() : nullptr;
         q.m = c.m, q.m_pad = c.m_pad, q.k = c.k, q.dil = c.dil, q.pad = c.pad;
-        q.y = y, q.y_ld = y_ld, q.cout = c.cout, q.n_out = n_out;
-        q.r0 = r0, q.r1 = r1, q.r2 = r2, q.r0_ld = r0_ld, q.scale = scale;
-        q.stride_t = stride_t, q.pad_t = pad_t, q.l_convt = l_convt;
-        q.col_out = dpad ? dpad->col_d.as<int32_t>() : nullptr;
-        q.start_out = dpad ? dpad->start_d.as<int64_t>() : nullptr;
-        // ConvT (K = 2 stride): every input column feeds K x cout outputs = 2 m MACs per channel
-        const bool convt = epi == EPI_CONVT || epi == EPI_CONVT_REFLECT;
-        const double f = 2.0 * (double)c.cin * valid * (convt ? 2.0 * c.m : (double)c.cout * c.k);
+        q.y = o.y, q.y_ld = o.y_ld, q.cout = c.cout;
+        q.r0 = o.r0, q.r1 = o.r1, q.r2 = o.r2, q.r0_ld = o.r0_ld, q.scale = o.scale;
+        q.stride_t = o.stride, q.pad_t = o.pad_t;
+        q.out_start = o.dout->start_d.as<int64_t>(), q.out_len = o.dout->len_d.as<int64_t>();
+        if (o.stats) {
+            need_part(t.count * wn * c.cout);
+            q.part = p->part.as<StatPart>();
+        }
+        // algorithmic FLOP over valid columns; ConvT (K = 2 stride): each input column feeds
+        // K x cout outputs = 2 m MACs per input channel
+        const double valid = (double)(o.convt ? o.din->valid() : o.dout->valid());
+        const double f = 2.0 * (double)c.cin * valid * (o.convt ? 2.0 * c.m : (double)c.cout * c.k);
         flop += f;
-        if (cls == PC_SNAKE) snake_flop += f;
+        if (o.cls == PC_SNAKE) snake_flop += f;
         hipEvent_t e0 = nullptr, e1 = nullptr;
-        if (ctx->profiling) {
+        if (ctx->profiling && !dry) {
             e0 = ev(), e1 = ev();
             KK_HIP(hipEventRecord(e0, s));
         }
-        KK_HIP(launch_conv(q, pro, epi, c.shape, s));
+        KK_LAUNCH(launch_conv(q, o.pro, o.epi, c.shape, o.stats, o.in_h, o.out_h, ctx->n_cu, s));
         launches++;
-        if (ctx->profiling) {
+        if (ctx->profiling && !dry) {
             KK_HIP(hipEventRecord(e1, s));
-            ctx->prof.push_back(ProfRec{cls, f, e0, e1});
+            ctx->prof.push_back(ProfRec{o.cls, f, e0, e1});
         }
+        return t;
     }
 
-    // snake_b (src/gpu_batch.rs:140-154) in place on X.
+    Op snake_op(const MSnake& blk, const Dom& d, const void* x, float* y, int epi, const Coef* coef, int i,
+                bool second, bool stats) {
+        Op o;
+        o.pro = PRO_ADAIN_SNAKE, o.epi = epi, o.x = x, o.x_ld = blk.c, o.din = o.dout = &d, o.y = y;
+        o.y_ld = blk.c, o.coef = coef, o.stats = stats, o.cls = PC_SNAKE;
+        o.ar = second ? &blk.ar2[i] : &blk.ar1[i];
+        o.ai = second ? &blk.ai2[i] : &blk.ai1[i];
+        // conv1 writes h in fp16, conv2 reads it
+        o.out_h = !second, o.in_h = second;
+        return o;
+    }
+
+    // snake_b (src/gpu_batch.rs:140-154) in place on X.  The statistics of each conv's output are
+    // reduced in its epilogue; only the block input needs a statistics pass.
     void snake_block(const MSnake& blk, float* X, float* h, const Dom& d) {
-        const int c = blk.c;
-        const double valid = (double)d.valid();
-        Coef* cf = p->coef[0].as<Coef>();
+        const int c = blk.c, wn = kShapeWN[blk.c1[0].shape];
+        stats_fin(X, c, c, d, blk.a1[0], cf(0));
         for (int i = 0; i < 3; i++) {
-            stats_fin(X, c, c, d, blk.a1[i], cf);
-            conv(blk.c1[i], PRO_ADAIN_SNAKE, EPI_STORE, X, c, d.l, d.col_d.as<int32_t>(), h, c, d.l, valid, PC_SNAKE,
-                 cf, &blk.ar1[i], &blk.ai1[i]);
-            stats_fin(h, c, c, d, blk.a2[i], cf);
-            conv(blk.c2[i], PRO_ADAIN_SNAKE, EPI_ACCUM, h, c, d.l, d.col_d.as<int32_t>(), X, c, d.l, valid, PC_SNAKE,
-                 cf, &blk.ar2[i], &blk.ai2[i]);
+            const Tiles& t = conv(blk.c1[i], snake_op(blk, d, X, h, EPI_STORE, cf(0), i, false, true));
+            fin(t, wn, 128, c, blk.a2[i], cf(1));
+            conv(blk.c2[i], snake_op(blk, d, h, X, EPI_ACCUM, cf(1), i, true, i < 2));
+            if (i < 2) fin(t, wn, 128, c, blk.a1[i + 1], cf(0));
         }
     }
 
     // x = (rb0(y) + rb1(y) + rb2(y)) / 3 (src/gpu_batch.rs:395-401); result in X[2].
     void resblock_mean(const MSnake* rbs, const float* y, float* X[3], float* h, const Dom& d) {
-        const int c = rbs[0].c;
-        const double valid = (double)d.valid();
-        const int32_t* col = d.col_d.as<int32_t>();
+        const int c = rbs[0].c, wn = kShapeWN[rbs[0].c1[0].shape];
         // the three blocks' first AdaIN share one statistics pass over y
-        KK_HIP(launch_stats(y, c, c, d.dev(), p->sums.as<double>(), s));
-        launches++;
-        for (int j = 0; j < 3; j++) stats_fin(y, c, c, d, rbs[j].a1[0], p->coef[j].as<Coef>(), false, j == 2);
-        Coef* cf = p->coef[0].as<Coef>();
+        const Tiles& ts = stats(y, c, c, d);
+        for (int j = 0; j < 3; j++) fin(ts, 1, kStatTile, c, rbs[j].a1[0], cf(2 + j));
         for (int j = 0; j < 3; j++) {
             const MSnake& blk = rbs[j];
             for (int i = 0; i < 3; i++) {
                 const float* in = i == 0 ? y : X[j];
-                const Coef* c1 = i == 0 ? p->coef[j].as<Coef>() : cf;
-                if (i > 0) stats_fin(X[j], c, c, d, blk.a1[i], cf);
-                conv(blk.c1[i], PRO_ADAIN_SNAKE, EPI_STORE, in, c, d.l, col, h, c, d.l, valid, PC_SNAKE, c1,
-                     &blk.ar1[i], &blk.ai1[i]);
-                // coef[0] may still hold the shared coefficients of block 0 (used above): the
-                // conv1 launch has been enqueued before this overwrite, stream order keeps it safe
-                stats_fin(h, c, c, d, blk.a2[i], cf);
-                int epi = EPI_ACCUM;
-                const float *r0 = nullptr, *r1 = nullptr, *r2 = nullptr;
-                if (i == 0) epi = EPI_ADD_FROM, r0 = y;
-                if (j == 2 && i == 2) epi = EPI_MEAN3, r0 = X[0], r1 = X[1], r2 = X[2];
-                conv(blk.c2[i], PRO_ADAIN_SNAKE, epi, h, c, d.l, col, X[j], c, d.l, valid, PC_SNAKE, cf, &blk.ar2[i],
-                     &blk.ai2[i], 0.f, r0, r1, r2, c);
+                const Tiles& t =
+                    conv(blk.c1[i], snake_op(blk, d, in, h, EPI_STORE, i == 0 ? cf(2 + j) : cf(0), i, false, true));
+                fin(t, wn, 128, c, blk.a2[i], cf(1));
+                Op o2 = snake_op(blk, d, h, X[j], EPI_ACCUM, cf(1), i, true, i < 2);
+                if (i == 0) o2.epi = EPI_ADD_FROM, o2.r0 = y, o2.r0_ld = c;
+                if (j == 2 && i == 2) o2.epi = EPI_MEAN3, o2.r0 = X[0], o2.r1 = X[1], o2.r2 = X[2], o2.r0_ld = c;
+                conv(blk.c2[i], o2);
+                if (i < 2) fin(t, wn, 128, c, blk.a1[i + 1], cf(0));
             }
         }
     }
@@ -789,17 +898,20 @@ struct Runner {
     // AdainResBlk1d (src/gpu_batch.rs:104-135) without upsampling: in [ln][in_ld] -> out[:, 0:dout].
     void resblk(const MResblk& r, const float* in, int64_t in_ld, float* out, int64_t out_ld) {
         const Dom& d = p->dn;
-        const double valid = (double)d.valid();
-        const int32_t* col = d.col_d.as<int32_t>();
-        Coef* cf = p->coef[0].as<Coef>();
         float* h = p->hdec.as<float>();
-        stats_fin(in, in_ld, r.din, d, r.n1, cf);
-        conv(r.conv1, PRO_ADAIN_LEAKY, EPI_STORE, in, in_ld, d.l, col, h, r.dout, d.l, valid, PC_DECODER, cf,
-             nullptr, nullptr, 0.2f);
-        conv(r.conv1x1, PRO_F32, EPI_STORE, in, in_ld, d.l, col, out, out_ld, d.l, valid, PC_DECODER);
-        stats_fin(h, r.dout, r.dout, d, r.n2, cf);
-        conv(r.conv2, PRO_ADAIN_LEAKY, EPI_RESID, h, r.dout, d.l, col, out, out_ld, d.l, valid, PC_DECODER, cf,
-             nullptr, nullptr, 0.2f, nullptr, nullptr, nullptr, 0, 1.0f / sqrtf(2.0f));
+        stats_fin(in, in_ld, r.din, d, r.n1, cf(0));
+        Op o1;
+        o1.pro = PRO_ADAIN_LEAKY, o1.x = in, o1.x_ld = in_ld, o1.din = o1.dout = &d, o1.y = h, o1.y_ld = r.dout;
+        o1.coef = cf(0), o1.slope = 0.2f, o1.stats = true;
+        const Tiles& t = conv(r.conv1, o1);
+        fin(t, kShapeWN[r.conv1.shape], 128, r.dout, r.n2, cf(1));
+        Op os;
+        os.x = in, os.x_ld = in_ld, os.din = os.dout = &d, os.y = out, os.y_ld = out_ld;
+        conv(r.conv1x1, os);
+        Op o2;
+        o2.pro = PRO_ADAIN_LEAKY, o2.epi = EPI_RESID, o2.x = h, o2.x_ld = r.dout, o2.din = o2.dout = &d;
+        o2.y = out, o2.y_ld = out_ld, o2.coef = cf(1), o2.slope = 0.2f, o2.scale = 1.0f / sqrtf(2.0f);
+        conv(r.conv2, o2);
     }
 
     void decoder() {
@@ -811,41 +923,46 @@ struct Runner {
         float* xa = p->xin_a.as<float>();
         float* xb = p->xin_b.as<float>();
         // asr = t_en expanded by the durations; F0 / N convs (src/gpu_batch.rs:295-302)
-        KK_HIP(launch_expand(p->t_en.as<float>(), p->t_rows, p->src_row.as<int32_t>(), ln, xcat, kXcatLd, s));
-        KK_HIP(launch_f0n_conv(p->f0.as<float>(), p->en.as<float>(), 2 * ln, m.f0w.as<float>(), m.f0b.as<float>(),
+        KK_LAUNCH(launch_expand(p->t_en.as<float>(), p->t_rows, p->src_row.as<int32_t>(), ln, xcat, kXcatLd, s));
+        KK_LAUNCH(launch_f0n_conv(p->f0.as<float>(), p->en.as<float>(), 2 * ln, m.f0w.as<float>(), m.f0b.as<float>(),
                                m.nw_.as<float>(), m.nb_.as<float>(), xcat, kXcatLd, 512, 513, col, ln, s));
         launches += 2;
         resblk(m.encode, xcat, kXcatLd, xa, kXinLd);
         // asr_res (512 -> 64, k1) into channels [1024, 1088); F0n, Nn into 1088, 1089
-        conv(m.asr_res, PRO_F32, EPI_STORE, xcat, kXcatLd, ln, col, xa + 1024, kXinLd, ln, (double)dn.valid(),
-             PC_DECODER);
-        KK_HIP(launch_copy_cols(xcat + 512, kXcatLd, 2, xa, kXinLd, 1088, col, ln, s));
-        KK_HIP(launch_copy_cols(xa + 1024, kXinLd, 66, xb, kXinLd, 1024, col, ln, s));
+        Op oa;
+        oa.x = xcat, oa.x_ld = kXcatLd, oa.din = oa.dout = &dn, oa.y = xa + 1024, oa.y_ld = kXinLd;
+        conv(m.asr_res, oa);
+        KK_LAUNCH(launch_copy_cols(xcat + 512, kXcatLd, 2, xa, kXinLd, 1088, col, ln, s));
+        KK_LAUNCH(launch_copy_cols(xa + 1024, kXinLd, 66, xb, kXinLd, 1024, col, ln, s));
         launches += 2;
         resblk(m.decode[0], xa, kXinLd, xb, kXinLd);
         resblk(m.decode[1], xb, kXinLd, xa, kXinLd);
         resblk(m.decode[2], xa, kXinLd, xb, kXinLd);
         // decode.3: upsample block to 2N (src/gpu_batch.rs:106-133)
         const MResblk& r = m.decode[3];
-        Coef* cf = p->coef[0].as<Coef>();
-        stats_fin(xb, kXinLd, r.din, dn, r.n1, cf);
-        KK_HIP(launch_adain_pool(xb, kXinLd, r.din, cf, col, ln, r.pool_w.as<float>(), r.pool_b.as<float>(),
+        stats_fin(xb, kXinLd, r.din, dn, r.n1, cf(0));
+        KK_LAUNCH(launch_adain_pool(xb, kXinLd, r.din, cf(0), col, ln, r.pool_w.as<float>(), r.pool_b.as<float>(),
                                  d2.col_d.as<int32_t>(), p->pool.as<uint16_t>(), kXinLd, s));
         launches++;
         float* h = p->hdec.as<float>();
-        const double v2 = (double)d2.valid();
-        conv(r.conv1, PRO_BF16, EPI_STORE, p->pool.p, kXinLd, d2.l, d2.col_d.as<int32_t>(), h, 512, d2.l, v2,
-             PC_DECODER);
+        Op o1;
+        o1.pro = PRO_BF16, o1.x = p->pool.p, o1.x_ld = kXinLd, o1.din = o1.dout = &d2, o1.y = h, o1.y_ld = 512;
+        o1.stats = true;
+        const Tiles& t = conv(r.conv1, o1);
+        fin(t, kShapeWN[r.conv1.shape], 128, 512, r.n2, cf(1));
         // shortcut conv1x1(nearest x2 (x)) = nearest x2 (conv1x1(x)) for a 1x1 conv: computed at N
-        conv(r.conv1x1, PRO_F32, EPI_STORE, xb, kXinLd, ln, col, p->sc_half.as<float>(), 512, ln, v2, PC_DECODER);
-        stats_fin(h, 512, 512, d2, r.n2, cf);
-        conv(r.conv2, PRO_ADAIN_LEAKY, EPI_RESID_UP2, h, 512, d2.l, d2.col_d.as<int32_t>(), p->dec_out.as<float>(), 512,
-             d2.l, v2, PC_DECODER, cf, nullptr, nullptr, 0.2f, p->sc_half.as<float>(), nullptr, nullptr, 512,
-             1.0f / sqrtf(2.0f));
+        Op os;
+        os.x = xb, os.x_ld = kXinLd, os.din = os.dout = &dn, os.y = p->sc_half.as<float>(), os.y_ld = 512;
+        conv(r.conv1x1, os);
+        Op o2;
+        o2.pro = PRO_ADAIN_LEAKY, o2.epi = EPI_RESID_UP2, o2.x = h, o2.x_ld = 512, o2.din = o2.dout = &d2;
+        o2.y = p->dec_out.as<float>(), o2.y_ld = 512, o2.coef = cf(1), o2.slope = 0.2f;
+        o2.r0 = p->sc_half.as<float>(), o2.r0_ld = 512, o2.scale = 1.0f / sqrtf(2.0f);
+        conv(r.conv2, o2);
     }
 
     void source() {
-        KK_HIP(launch_phase_pre(p->f0.as<float>(), p->d2.start_d.as<int64_t>(), p->d2.len_d.as<int64_t>(), p->nb,
+        KK_LAUNCH(launch_phase_pre(p->f0.as<float>(), p->d2.start_d.as<int64_t>(), p->d2.len_d.as<int64_t>(), p->nb,
                                 p->rand_ini.as<float>(), p->pp.as<float>(), 2 * p->ln, s));
         SourceParams q{};
         q.f0 = p->f0.as<float>(), q.start2 = p->d2.start_d.as<int64_t>(), q.len2 = p->d2.len_d.as<int64_t>();
@@ -855,7 +972,7 @@ struct Runner {
         q.start120 = p->d120.start_d.as<int64_t>(), q.f_len = p->d120.len_d.as<int64_t>();
         q.blk_item = p->src_item.as<int64_t>(), q.blk_f0 = p->src_f0.as<int64_t>(), q.n_blocks = p->n_src;
         q.spec = p->spec.as<float>(), q.spec_ld = kSpecLd;
-        KK_HIP(launch_source_stft(q, s));
+        KK_LAUNCH(launch_source_stft(q, s));
         launches += 2;
     }
 
@@ -867,26 +984,28 @@ struct Runner {
         for (int j = 0; j < 6; j++) B[j] = p->B[j].as<float>();
         // xs = noise_res[i](noise_convs[i](masked spec)) (src/gpu_batch.rs:362-375)
         const MNoiseConv& nc = m.nc[i];
-        KK_HIP(launch_noise_conv(p->spec.as<float>(), kSpecLd, p->d120.l, p->d120.col_d.as<int32_t>(),
+        KK_LAUNCH(launch_noise_conv(p->spec.as<float>(), kSpecLd, p->d120.l, p->d120.col_d.as<int32_t>(),
                                  nc.w.as<float>(), nc.b.as<float>(), nc.cout, nc.k, nc.stride, nc.pad, B[1], c,
                                  dout.l, s));
         launches++;
         snake_block(m.noise_res[i], B[1], B[2], dout);
-        // y = ups[i](leaky_0.1(x) masked) (+ reflect pad on stage 1) + xs
-        const float* x = i == 0 ? p->dec_out.as<float>() : B[0];
-        const int64_t x_ld = i == 0 ? 512 : 256;
-        const int64_t l_convt = i == 0 ? dout.l : dout.l - 1;
-        conv(m.ups[i], PRO_LEAKY, i == 0 ? EPI_CONVT : EPI_CONVT_REFLECT, x, x_ld, din.l, din.col_d.as<int32_t>(),
-             B[3], c, din.l + 1, (double)din.valid(), PC_CONVT, nullptr, nullptr, nullptr, 0.1f, B[1], nullptr,
-             nullptr, c, 1.f, m.ups_stride[i], m.ups_pad[i], l_convt, i == 0 ? nullptr : &dout);
+        // y = ups[i](leaky_0.1(x) masked) (+ per-item reflect pad on stage 1) + xs
+        Op ou;
+        ou.pro = PRO_LEAKY, ou.epi = i == 0 ? EPI_CONVT : EPI_CONVT_REFLECT, ou.slope = 0.1f;
+        ou.x = i == 0 ? (const void*)p->dec_out.p : (const void*)B[0], ou.x_ld = i == 0 ? 512 : 256;
+        ou.din = &din, ou.dout = &dout, ou.y = B[3], ou.y_ld = c, ou.r0 = B[1], ou.r0_ld = c;
+        ou.convt = true, ou.stride = m.ups_stride[i], ou.pad_t = m.ups_pad[i], ou.cls = PC_CONVT;
+        conv(m.ups[i], ou);
         float* X[3] = {B[4], B[5], B[0]};
         resblock_mean(&m.rb[3 * i], B[3], X, B[2], dout);
     }
 
     void post_istft() {
         const Dom& d = p->d120;
-        conv(m.post, PRO_LEAKY, EPI_STORE, p->B[0].p, 128, d.l, d.col_d.as<int32_t>(), p->post.as<float>(), kPostLd,
-             d.l, (double)d.valid(), PC_POST, nullptr, nullptr, nullptr, 0.01f);
+        Op o;
+        o.pro = PRO_LEAKY, o.slope = 0.01f, o.x = p->B[0].p, o.x_ld = 128, o.din = o.dout = &d;
+        o.y = p->post.as<float>(), o.y_ld = kPostLd, o.cls = PC_POST;
+        conv(m.post, o);
     }
 
     void istft() {
@@ -895,12 +1014,12 @@ struct Runner {
         q.start120 = p->d120.start_d.as<int64_t>(), q.f_len = p->d120.len_d.as<int64_t>();
         q.blk_item = p->ist_item.as<int64_t>(), q.blk_s0 = p->ist_s0.as<int64_t>(), q.n_blocks = p->n_ist;
         q.audio = p->audio.as<float>(), q.audio_start = p->audio_start.as<int64_t>();
-        KK_HIP(launch_istft(q, s));
+        KK_LAUNCH(launch_istft(q, s));
         launches++;
     }
 
     void run(int until) {
-        KK_HIP(launch_style_fc(m.style_wt.as<float>(), m.style_b.as<float>(), m.style_rows, p->style.as<float>(),
+        KK_LAUNCH(launch_style_fc(m.style_wt.as<float>(), m.style_b.as<float>(), m.style_rows, p->style.as<float>(),
                                p->nb, p->gb.as<float>(), s));
         launches++;
         if (p->kind == PLAN_SNAKE) {
@@ -920,6 +1039,24 @@ struct Runner {
         istft();
     }
 };
+
+// Every tile list a run needs is built (and uploaded) here, so kk_plan_run allocates nothing.
+static void prebuild_tiles(kk_plan* p) {
+    Runner r{p, p->ctx, p->ctx->model, p->ctx->stream};
+    r.dry = true;
+    r.run(KK_STAGE_ALL);
+}
+
+static void release_plan_device(kk_plan* p) {
+    for (DevBuf* b : p->owned()) b->release();
+    for (kk::Dom* d : {&p->dn, &p->d2, &p->d20, &p->d120, &p->ds}) {
+        d->col_d.release();
+        d->start_d.release();
+        d->len_d.release();
+    }
+    p->tiles.clear();
+    p->ctx = nullptr;
+}
 
 static void set_err(char* err, size_t errlen, const std::string& m) {
     if (err && errlen) {
@@ -977,7 +1114,8 @@ int kk_open(int ordinal, kk_ctx** out, char* err, size_t errlen) {
                   "; this build carries gfx950 code only");
         auto ctx = std::make_unique<kk_ctx>();
         ctx->device = ordinal;
-        ctx->name = prop.name;
+        ctx->name = prop.name[0] ? prop.name : prop.gcnArchName;
+        ctx->n_cu = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 1;
         KK_HIP(hipSetDevice(ordinal));
         KK_HIP(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking));
         // twiddles and periodic Hann window in f64 (src/gpu.rs:93-101)
@@ -999,6 +1137,10 @@ void kk_close(kk_ctx* ctx) {
     if (!ctx) return;
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
+    // plans still alive lose their device memory now and become orphans: kk_plan_free later only
+    // releases the host object, and every other entry on them reports KK_ERR_STATE
+    for (kk_plan* p : ctx->plans) release_plan_device(p);
+    ctx->plans.clear();
     for (auto& r : ctx->prof) {
         (void)hipEventDestroy(r.e0);
         (void)hipEventDestroy(r.e1);
@@ -1054,6 +1196,10 @@ int kk_plan_create_snake(kk_ctx* ctx, const char* prefix, const float* const* x,
 
 int kk_plan_run(kk_plan* plan, int until, char* err, size_t errlen) {
     if (!plan) return KK_ERR_INVALID;
+    if (!plan->ctx) {
+        set_err(err, errlen, "plan outlived its context");
+        return KK_ERR_STATE;
+    }
     return guard(err, errlen, [&] {
         use_device(plan->ctx);
         check(plan->ctx->model.ready, "no model uploaded");
@@ -1066,6 +1212,10 @@ int kk_plan_run(kk_plan* plan, int until, char* err, size_t errlen) {
 
 int kk_plan_sync(kk_plan* plan, char* err, size_t errlen) {
     if (!plan) return KK_ERR_INVALID;
+    if (!plan->ctx) {
+        set_err(err, errlen, "plan outlived its context");
+        return KK_ERR_STATE;
+    }
     return guard(err, errlen, [&] {
         use_device(plan->ctx);
         KK_HIP(hipStreamSynchronize(plan->ctx->stream));
@@ -1074,6 +1224,10 @@ int kk_plan_sync(kk_plan* plan, char* err, size_t errlen) {
 
 int kk_plan_fetch(kk_plan* plan, kk_output* out, char* err, size_t errlen) {
     if (!plan || !out) return KK_ERR_INVALID;
+    if (!plan->ctx) {
+        set_err(err, errlen, "plan outlived its context");
+        return KK_ERR_STATE;
+    }
     for (int b = 0; b < plan->nb; b++) out[b] = kk_output{nullptr, 0};
     int rc = guard(err, errlen, [&] {
         use_device(plan->ctx);
@@ -1102,6 +1256,10 @@ int kk_plan_fetch(kk_plan* plan, kk_output* out, char* err, size_t errlen) {
 
 int kk_plan_tap(kk_plan* plan, const char* name, int item, float* dst, int64_t count, char* err, size_t errlen) {
     if (!plan || !name || !dst) return KK_ERR_INVALID;
+    if (!plan->ctx) {
+        set_err(err, errlen, "plan outlived its context");
+        return KK_ERR_STATE;
+    }
     return guard(err, errlen, [&] {
         use_device(plan->ctx);
         check(item >= 0 && item < plan->nb, "item out of range");
@@ -1153,8 +1311,11 @@ int kk_plan_get_info(const kk_plan* plan, kk_plan_info* info) {
 
 void kk_plan_free(kk_plan* plan) {
     if (!plan) return;
-    (void)hipSetDevice(plan->ctx->device);
-    (void)hipStreamSynchronize(plan->ctx->stream);
+    if (plan->ctx) {  // an orphan's device memory went with its context (kk_close)
+        (void)hipSetDevice(plan->ctx->device);
+        (void)hipStreamSynchronize(plan->ctx->stream);
+        plan->ctx->plans.erase(plan);
+    }
     delete plan;
 }
 

@@ -4,11 +4,31 @@
 
 namespace kk {
 
+// ---------------------------------------------------------------- tiles
+// Convolutions and statistics run over item-aligned tiles: tile i covers GEMM columns
+// [t0[i], t0[i] + n[i]) of item item[i] (n[i] <= the kernel's tile width), so no tile mixes items
+// and gap columns are never computed.  Tiles of one item are consecutive; item b owns tiles
+// [lo[b], hi[b]).
+struct TilesDev {
+    const int32_t* item;
+    const int64_t* t0;
+    const int32_t* n;
+    const int32_t* lo;
+    const int32_t* hi;
+    int64_t count;
+};
+
+// Per-(partial, channel) statistics record: sums of (v - shift) and (v - shift)^2 over n columns,
+// shift = the first of those columns' value (exact local centring; Chan's combination in finalize).
+struct StatPart {
+    float s1, s2, shift;
+};
+
 // ---------------------------------------------------------------- MFMA convolution
 enum Prologue {
-    PRO_BF16 = 0,         // input already bf16 [L][ld], gap rows -> 0
-    PRO_F32 = 1,          // f32 input -> bf16, gap rows -> 0
-    PRO_LEAKY = 2,        // leaky ReLU(slope), gap rows -> 0
+    PRO_BF16 = 0,         // input already bf16 [L][ld]
+    PRO_F32 = 1,          // f32 input -> bf16
+    PRO_LEAKY = 2,        // leaky ReLU(slope)
     PRO_ADAIN_LEAKY = 3,  // AdaIN (per item, per channel affine) + leaky ReLU(slope)
     PRO_ADAIN_SNAKE = 4,  // AdaIN + Snake x + sin^2(a x)/a
 };
@@ -23,17 +43,22 @@ enum Epilogue {
     EPI_CONVT_REFLECT = 7,  // ConvT scatter with per-item ReflectionPad1d((1,0)), + r0
 };
 enum BlockShape {
-    SHAPE_W4x2 = 0,  // 256 (M) x 128 (N), 8 waves
-    SHAPE_W2x4 = 1,  // 128 x 256, 8 waves
-    SHAPE_W1x4 = 2,  // 64 x 256, 4 waves
+    SHAPE_256x128 = 0,  // 4 waves (4 x 1), wave tile 64 x 128
+    SHAPE_128x256 = 1,  // 4 waves (2 x 2)
+    SHAPE_64x256 = 2,   // 2 waves (1 x 2)
 };
+constexpr int kShapeM[3] = {256, 128, 64};
+constexpr int kShapeN[3] = {128, 256, 256};
+constexpr int kShapeWN[3] = {1, 2, 2};
 
 struct ConvParams {
-    const void* x;           // input [l_in][x_ld] (f32 or bf16)
+    const void* x;           // input [l_in][x_ld] (f32, fp16 or bf16)
     int64_t x_ld;
     int64_t l_in;
     int cin, cin_pad;        // real and padded (multiple of 64) input channels
-    const int32_t* col_in;   // input domain col_item (null: no gap masking)
+    const int64_t* in_start; // input domain item spans (rows outside an item's span read as 0)
+    const int64_t* in_len;
+    TilesDev tiles;          // GEMM-column tiles (output domain for convs, input domain for ConvT)
     const Coef* coef;        // [nb][cin]
     const float* alpha_rev;  // [cin] alpha / 2 pi
     const float* alpha_inv;  // [cin] 1 / alpha
@@ -42,39 +67,38 @@ struct ConvParams {
     const float* bias;       // [cout] or null
     int m, m_pad;            // GEMM rows (cout, or stride * cout for ConvT), padded to the block
     int k, dil, pad;
-    float* y;                // output [rows][y_ld]
+    float* y;                // output [rows][y_ld] (f32, or fp16 for the Snake steps' h)
     int64_t y_ld;
     int cout;
-    int64_t n_out;           // GEMM columns
     const float* r0;         // epilogue operands
     const float* r1;
     const float* r2;
     int64_t r0_ld;
     float scale;
     int stride_t, pad_t;     // ConvT stride / padding
-    int64_t l_convt;         // ConvT output length (before the reflect pad)
-    const int32_t* col_out;  // padded output domain (reflect epilogue)
-    const int64_t* start_out;
+    const int64_t* out_start;// ConvT: output domain item spans
+    const int64_t* out_len;
+    StatPart* part;          // epilogue statistics [tiles * WN][cout] (null: none)
 };
 
-int conv_block_m(int shape);
-int conv_block_n(int shape);
-hipError_t launch_conv(const ConvParams& p, int pro, int epi, int shape, hipStream_t s);
+// in_h / out_h: fp16 input (conv2 of a Snake step) / fp16 output (conv1 of a Snake step).
+hipError_t launch_conv(const ConvParams& p, int pro, int epi, int shape, bool stats, bool in_h, bool out_h, int n_cu,
+                       hipStream_t s);
 
 // ---------------------------------------------------------------- bandwidth kernels (kk_misc.hip)
-// AdaIN statistics: per-(item, channel) shifted sums accumulated in f64 (sums [nb][C][2]).
-hipError_t launch_stats(const float* x, int64_t ld, int c, DomDev d, double* sums, hipStream_t s);
-// sums -> AdaIN coefficients (and sums reset to zero for the next use).
-hipError_t launch_finalize(const float* x, int64_t ld, int c, DomDev d, double* sums, const float* gb,
-                           int64_t gb_ld, int gb_off, const float* nw, const float* nb, Coef* coef, int reset,
-                           hipStream_t s);
+// Statistics partials of x [l][ld] over tiles (one partial per tile and channel).
+hipError_t launch_stats_tiles(const float* x, int64_t ld, int c, TilesDev t, StatPart* part, hipStream_t s);
+// Partials -> per-(item, channel) mean / rstd (chan_stats_seg semantics) -> AdaIN coefficients.
+// `wn` partials per tile; partial (tile, w) covers columns [w*wcols, (w+1)*wcols) of the tile.
+hipError_t launch_finalize(const StatPart* part, int c, int wn, int wcols, TilesDev t, int nb, const float* gb,
+                           int64_t gb_ld, int gb_off, const float* nw, const float* nb_, Coef* coef, hipStream_t s);
 // gb[b][j] = W[j] . style[b] + bias[j] for every AdaIN layer at once.
 hipError_t launch_style_fc(const float* w, const float* bias, int rows, const float* style, int nb, float* gb,
                            hipStream_t s);
 // asr[t][c] = t_en[c][src_row[t]] (0 in gaps), time-major [l][ld] with channels [0, 512).
 hipError_t launch_expand(const float* t_en, int64_t t_rows, const int32_t* src_row, int64_t l, float* asr,
                          int64_t ld, hipStream_t s);
-// F0_conv / N_conv: 1 -> 1 channel, k3 s2 p1 on d2 -> dn; out at column `col` of [ln][ld].
+// F0_conv / N_conv: 1 -> 1 channel, k3 s2 p1 on d2 -> dn; out at columns col_f0 / col_n of [ln][ld].
 hipError_t launch_f0n_conv(const float* f0, const float* en, int64_t l2, const float* w_f0, const float* b_f0,
                            const float* w_n, const float* b_n, float* out, int64_t ld, int col_f0, int col_n,
                            const int32_t* col, int64_t ln, hipStream_t s);
@@ -126,11 +150,12 @@ struct IstftParams {
     const int64_t* audio_start;
 };
 hipError_t launch_istft(const IstftParams& p, hipStream_t s);
-// Zero a float buffer (a kernel, so the sequence stays capturable in a graph).
+// Zero a buffer (a kernel, so the sequence stays capturable in a graph).
 hipError_t launch_zero(void* p, int64_t bytes, hipStream_t s);
 
 constexpr int kSourceFrames = 128;  // STFT frames per source block
 constexpr int kIstftSamples = 512;  // output samples per iSTFT block
+constexpr int kStatTile = 256;      // rows per tile of the standalone statistics pass
 hipError_t upload_stft_tables(const double* cosv, const double* sinv, const float* win);
 
 }  // namespace kk

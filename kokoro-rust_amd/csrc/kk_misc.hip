@@ -18,72 +18,96 @@ namespace {
 constexpr float kPiF = 3.14159274101257324f;  // (float)M_PI, kernels/kokoro.cu:9
 
 // ------------------------------------------------------------------ AdaIN statistics
-// chan_stats_seg (kernels/kokoro.cu:779-810): per (item, channel) sums of x - x[first row of the
-// item], accumulated in f64 and combined with f64 atomics.  One wave covers 64 channels of a run of
-// rows; the item of a row is wave-uniform, so item changes flush the partial sums.
-__global__ __launch_bounds__(256) void stats_kernel(const float* __restrict__ x, int64_t ld, int c, DomDev d,
-                                                    double* __restrict__ sums, int64_t rows_per_wave) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+// Statistics partials of x over item-aligned tiles: per (tile, channel) the sums of (v - shift) and
+// (v - shift)^2 with shift = the tile's first value (the centring of chan_stats_seg,
+// kernels/kokoro.cu:779-810, applied per tile).  One wave per 64 channels and row phase.
+__global__ __launch_bounds__(256) void stats_tiles_kernel(const float* __restrict__ x, int64_t ld, int c, TilesDev t,
+                                                          StatPart* __restrict__ part) {
+    __shared__ float sa[4][64], sb[4][64];
+    const int lane = threadIdx.x & 63, g = threadIdx.x >> 6;
     const int ch = blockIdx.y * 64 + lane;
-    const bool live = ch < c;
-    const int64_t r_begin = ((int64_t)blockIdx.x * 4 + wave) * rows_per_wave;
-    if (r_begin >= d.l) return;
-    const int64_t r_end = min(r_begin + rows_per_wave, d.l);
-    int cur = -1;
-    float shift = 0.f;
-    double s = 0.0, s2 = 0.0;
-    for (int64_t r = r_begin; r < r_end; r++) {
-        const int b = d.col_item[r];
-        if (b != cur) {
-            if (cur >= 0 && live) {
-                unsafeAtomicAdd(&sums[((int64_t)cur * c + ch) * 2], s);
-                unsafeAtomicAdd(&sums[((int64_t)cur * c + ch) * 2 + 1], s2);
-            }
-            cur = b;
-            s = s2 = 0.0;
-            if (b >= 0 && live) shift = x[d.start[b] * ld + ch];
-        }
-        if (b >= 0 && live) {
-            const float v = x[r * ld + ch] - shift;
-            s += (double)v;
-            s2 += (double)v * (double)v;
+    const int64_t tile = blockIdx.x;
+    const int64_t t0 = t.t0[tile];
+    const int n = t.n[tile];
+    float shift = 0.f, s1 = 0.f, s2 = 0.f;
+    if (ch < c) {
+        shift = x[t0 * ld + ch];
+#pragma unroll 8
+        for (int r = g; r < n; r += 4) {
+            const float d = x[(t0 + r) * ld + ch] - shift;
+            s1 += d;
+            s2 = __builtin_fmaf(d, d, s2);
         }
     }
-    if (cur >= 0 && live) {
-        unsafeAtomicAdd(&sums[((int64_t)cur * c + ch) * 2], s);
-        unsafeAtomicAdd(&sums[((int64_t)cur * c + ch) * 2 + 1], s2);
+    sa[g][lane] = s1;
+    sb[g][lane] = s2;
+    __syncthreads();
+    if (g == 0 && ch < c) {
+        s1 = ((sa[0][lane] + sa[1][lane]) + sa[2][lane]) + sa[3][lane];
+        s2 = ((sb[0][lane] + sb[1][lane]) + sb[2][lane]) + sb[3][lane];
+        part[tile * c + ch] = StatPart{s1, s2, shift};
     }
 }
 
-// mean / rstd exactly as chan_stats_seg's epilogue, then the AdaIN affine of adain_apply_seg
-// (kernels/kokoro.cu:318-334) folded into v = x * sc + sh.  With `reset`, zeroes the sums for the
-// next statistics pass (several AdaIN layers may share one pass).
-__global__ void finalize_kernel(const float* __restrict__ x, int64_t ld, int c, DomDev d, double* sums,
-                                const float* __restrict__ gb, int64_t gb_ld, int gb_off, const float* __restrict__ nw,
-                                const float* __restrict__ nbias, Coef* __restrict__ coef, int reset) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (int64_t)d.nb * c) return;
-    const int b = (int)(i / c), ch = (int)(i - (int64_t)b * c);
-    const double s = sums[i * 2], s2 = sums[i * 2 + 1];
-    if (reset) {
-        sums[i * 2] = 0.0;
-        sums[i * 2 + 1] = 0.0;
+// Per (item, channel): combine the item's partials in a fixed order, then mean / rstd exactly as
+// chan_stats_seg's epilogue (biased variance, eps 1e-5, rstd = 1 / sqrtf((float)var + eps)) and the
+// AdaIN affine of adain_apply_seg (kernels/kokoro.cu:318-334) folded into v = x * sc + sh.
+// Every partial is re-centred on one reference per (item, channel) -- the item's first partial's
+// shift, a value of the data -- so the f64 sums need no division per partial and the final
+// E[d^2] - E[d]^2 cancels only over a few standard deviations.  16 threads per (item, channel)
+// reduce in a fixed tree: deterministic, no atomics.
+constexpr int kFinSub = 16;
+__global__ __launch_bounds__(256) void finalize_kernel(const StatPart* __restrict__ part, int c, int wn, int wcols,
+                                                       TilesDev t, const float* __restrict__ gb, int64_t gb_ld,
+                                                       int gb_off, const float* __restrict__ nw,
+                                                       const float* __restrict__ nbias, Coef* __restrict__ coef) {
+    __shared__ double sa[kFinSub][16], sb[kFinSub][16], sn[kFinSub][16];
+    const int cl = threadIdx.x & 15, sub = threadIdx.x >> 4;
+    const int b = blockIdx.x;
+    const int ch = blockIdx.y * 16 + cl;
+    const int64_t lo = (int64_t)t.lo[b] * wn, hi = (int64_t)t.hi[b] * wn;
+    double a1 = 0.0, a2 = 0.0, n = 0.0, ref = 0.0;
+    if (ch < c && lo < hi) {
+        ref = (double)part[lo * c + ch].shift;
+        for (int64_t pi = lo + sub; pi < hi; pi += kFinSub) {
+            const int64_t tile = pi / wn;
+            const int w = (int)(pi - tile * wn);
+            const int nt = min(max(t.n[tile] - w * wcols, 0), wcols);
+            if (nt <= 0) continue;
+            const StatPart q = part[pi * c + ch];
+            const double dn = (double)nt, d = (double)q.shift - ref, s1 = (double)q.s1;
+            // sums of (v - ref) and (v - ref)^2 over the partial's columns
+            a1 += s1 + dn * d;
+            a2 += (double)q.s2 + 2.0 * d * s1 + dn * d * d;
+            n += dn;
+        }
     }
-    const int64_t n = d.len[b];
-    if (n <= 0) {
+    sa[sub][cl] = a1, sb[sub][cl] = a2, sn[sub][cl] = n;
+    __syncthreads();
+    for (int k = kFinSub / 2; k > 0; k >>= 1) {
+        if (sub < k) {
+            sa[sub][cl] += sa[sub + k][cl];
+            sb[sub][cl] += sb[sub + k][cl];
+            sn[sub][cl] += sn[sub + k][cl];
+        }
+        __syncthreads();
+    }
+    if (sub != 0 || ch >= c) return;
+    a1 = sa[0][cl], a2 = sb[0][cl], n = sn[0][cl];
+    const int64_t i = (int64_t)b * c + ch;
+    if (n <= 0.0) {
         coef[i] = Coef{0.f, 0.f};
         return;
     }
-    const float shift = x[d.start[b] * ld + ch];
-    const double dm = s / (double)n;
-    double var = s2 / (double)n - dm * dm;
+    const double dm = a1 / n;
+    double var = a2 / n - dm * dm;
     if (var < 0.0) var = 0.0;
-    const float mean = (float)((double)shift + dm);
+    const float meanf = (float)(ref + dm);
     const float rstd = 1.0f / sqrtf((float)var + 1e-5f);
     const double g1 = 1.0 + (double)gb[b * gb_ld + gb_off + ch];
     const double beta = gb[b * gb_ld + gb_off + c + ch];
     const double a = (double)rstd * (double)nw[ch];
-    coef[i] = Coef{(float)(a * g1), (float)(((double)nbias[ch] - (double)mean * a) * g1 + beta)};
+    coef[i] = Coef{(float)(a * g1), (float)(((double)nbias[ch] - (double)meanf * a) * g1 + beta)};
 }
 
 // ------------------------------------------------------------------ style projections
@@ -467,20 +491,17 @@ hipError_t upload_stft_tables(const double* cosv, const double* sinv, const floa
     return hipMemcpyToSymbol(HIP_SYMBOL(c_win), win, sizeof(float) * 20);
 }
 
-hipError_t launch_stats(const float* x, int64_t ld, int c, DomDev d, double* sums, hipStream_t s) {
-    const int64_t cblk = ceil_div(c, 64);
-    int64_t rpw = ceil_div(d.l * cblk, 16384);
-    if (rpw < 64) rpw = 64;
-    const int64_t waves = ceil_div(d.l, rpw);
-    dim3 grid(blocks_for(waves, 4), (unsigned)cblk);
-    hipLaunchKernelGGL(stats_kernel, grid, dim3(256), 0, s, x, ld, c, d, sums, rpw);
+hipError_t launch_stats_tiles(const float* x, int64_t ld, int c, TilesDev t, StatPart* part, hipStream_t s) {
+    if (t.count == 0) return hipSuccess;
+    dim3 grid((unsigned)t.count, (unsigned)ceil_div(c, 64));
+    hipLaunchKernelGGL(stats_tiles_kernel, grid, dim3(256), 0, s, x, ld, c, t, part);
     return hipGetLastError();
 }
 
-hipError_t launch_finalize(const float* x, int64_t ld, int c, DomDev d, double* sums, const float* gb, int64_t gb_ld,
-                           int gb_off, const float* nw, const float* nb, Coef* coef, int reset, hipStream_t s) {
-    hipLaunchKernelGGL(finalize_kernel, dim3(blocks_for((int64_t)d.nb * c, 256)), dim3(256), 0, s, x, ld, c, d, sums,
-                       gb, gb_ld, gb_off, nw, nb, coef, reset);
+hipError_t launch_finalize(const StatPart* part, int c, int wn, int wcols, TilesDev t, int nb, const float* gb,
+                           int64_t gb_ld, int gb_off, const float* nw, const float* nb_, Coef* coef, hipStream_t s) {
+    dim3 grid((unsigned)nb, (unsigned)ceil_div(c, 16));
+    hipLaunchKernelGGL(finalize_kernel, grid, dim3(256), 0, s, part, c, wn, wcols, t, gb, gb_ld, gb_off, nw, nb_, coef);
     return hipGetLastError();
 }
 

@@ -325,5 +325,11 @@ class Plan:
             lib().kk_plan_free(self.h)
             self.h = None
 
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.free()
+
     def __del__(self):
         self.free()

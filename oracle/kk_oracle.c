@@ -740,6 +740,9 @@ static void snake_block(const snake_t* s, const float* x, int t, const float* st
     for (int i = 0; i < 3; i++) {
         adain_act(&s->a1[i], out, t, style, 1, 0.0f, s->al1[i], u);
         conv_layer(&s->c1[i], u, t, h, t);
+        /* the HIP path stores conv1's output (the input of adain2) in fp16 */
+        if (g_bf16 && (g_groups & KO_GROUP_H16))
+            for (size_t j = 0; j < n; j++) h[j] = ko_fp16_round(h[j]);
         adain_act(&s->a2[i], h, t, style, 1, 0.0f, s->al2[i], u);
         conv_layer(&s->c2[i], u, t, h, t);
         for (size_t j = 0; j < n; j++) out[j] = out[j] + h[j];

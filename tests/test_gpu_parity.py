@@ -29,10 +29,9 @@ def test_snake_block_ragged(gpu_ctx, oracle_model):
     xs = [rng.standard_normal((256, t)).astype(np.float32) for t in ts]
     styles = [rng.standard_normal(256).astype(np.float32) for _ in ts]
     _print("snake block resblocks.1, T =", ts)
-    plan = api.Plan.snake(gpu_ctx, "decoder.generator.resblocks.1", xs, styles, gap=40)
-    plan.run()
-    outs = plan.fetch()
-    plan.free()
+    with api.Plan.snake(gpu_ctx, "decoder.generator.resblocks.1", xs, styles, gap=40) as plan:
+        plan.run()
+        outs = plan.fetch()
     for x, s, y in zip(xs, styles, outs):
         ref = oracle_model.snake_block("decoder.generator.resblocks.1", x, s)
         with O.bf16_emulation():
@@ -50,9 +49,9 @@ def test_snake_block_128(gpu_ctx, oracle_model):
     ts = [300, 141]
     xs = [rng.standard_normal((128, t)).astype(np.float32) for t in ts]
     styles = [rng.standard_normal(256).astype(np.float32) for _ in ts]
-    plan = api.Plan.snake(gpu_ctx, "decoder.generator.noise_res.1", xs, styles, gap=40)
-    plan.run()
-    outs = plan.fetch()
+    with api.Plan.snake(gpu_ctx, "decoder.generator.noise_res.1", xs, styles, gap=40) as plan:
+        plan.run()
+        outs = plan.fetch()
     for x, s, y in zip(xs, styles, outs):
         with O.bf16_emulation():
             emu = oracle_model.snake_block("decoder.generator.noise_res.1", x, s)
@@ -66,15 +65,15 @@ def decoder_run(gpu_ctx, oracle_model):
     from oracle import oracle as O
     items = workloads.small_items(31, [9, 23, 14])
     _print("decoder batch, N =", [it.n_frames for it in items])
-    plan = api.Plan.decoder(gpu_ctx, items)
-    plan.run()
-    audio = plan.fetch()
-    taps = []
-    for b, it in enumerate(items):
-        n = it.n_frames
-        taps.append({"asr": plan.tap("asr", b, (512, n)), "decoder": plan.tap("decoder", b, (512, 2 * n)),
-                     "spec": plan.tap("spec", b, (22, 120 * n + 1)), "post": plan.tap("post", b, (22, 120 * n + 1))})
-    plan.free()
+    with api.Plan.decoder(gpu_ctx, items) as plan:
+        plan.run()
+        audio = plan.fetch()
+        taps = []
+        for b, it in enumerate(items):
+            n = it.n_frames
+            taps.append({"asr": plan.tap("asr", b, (512, n)), "decoder": plan.tap("decoder", b, (512, 2 * n)),
+                         "spec": plan.tap("spec", b, (22, 120 * n + 1)),
+                         "post": plan.tap("post", b, (22, 120 * n + 1))})
     refs, emus = [], []
     for it in items:
         refs.append(O.synth_item(oracle_model, it, taps=True))
@@ -131,10 +130,24 @@ def test_generator_only(gpu_ctx, oracle_model):
     from kokoro_hip import api, workloads
     from oracle import oracle as O
     x, f0, style, seed = workloads.config1_generator_input(seed=5, n_frames=12)
-    plan = api.Plan.generator(gpu_ctx, [x], [f0], [style], [seed])
-    plan.run()
-    (a,) = plan.fetch()
+    with api.Plan.generator(gpu_ctx, [x], [f0], [style], [seed]) as plan:
+        plan.run()
+        (a,) = plan.fetch()
     ref = oracle_model.generator(x, f0, style, O.rand_ini(seed), O.gen_noise(seed, 600 * 12 * 9))
     _print("  generator-only fp32 snr", snr_db(ref, a), "maxabs", np.abs(a - ref).max())
     assert np.abs(a - ref).max() <= 2e-3
     assert snr_db(ref, a) >= 40.0
+
+
+def test_plan_outliving_its_context(weights):
+    """A plan freed after its context is closed releases nothing twice and reports KK_ERR_STATE
+    (Engine ownership: src/engine.rs owns GpuKokoro; a caller may drop them in any order)."""
+    from kokoro_hip import api, workloads
+    ctx = api.Context(0)
+    ctx.upload_model(weights)
+    plan = api.Plan.decoder(ctx, workloads.small_items(41, [3]))
+    ctx.close()
+    with pytest.raises(api.KKError) as e:
+        plan.run()
+    assert e.value.code == -4
+    plan.free()
