@@ -1,4 +1,4 @@
-// kk_conv.hip -- bf16 implicit-GEMM convolution on CDNA4 MFMA (v_mfma_f32_16x16x32_bf16).
+// kk_conv.hip -- bf16 implicit-GEMM convolution on CDNA4 MFMA (v_mfma_f32_32x32x16_bf16).
 //
 // One kernel family serves every MFMA layer of the path:
 //   * stride-1 Conv1d with any K / dilation (decoder conv1/conv2/conv1x1/asr_res, the 48 Snake-block
@@ -8,29 +8,30 @@
 //     (phase, out-channel) pairs (replaces the f32 sgemm + convT_gather of src/gpu.rs:527-537).
 //
 // GEMM view: M = output channels (x phases), N = time columns, K = input channels x taps.
-// * Blocks run over item-aligned tiles (kk_kernels.h TilesDev): a tile never mixes items, so the
-//   per-item zero padding of the reference's gap masking (src/gpu_batch.rs:62-79) is a row-range
-//   test and the AdaIN coefficients are constants of the block.
-// * A (weights) is pre-packed as [tap][cin/32][M_pad][32] bf16: one A fragment (16 rows x 32
-//   channels) is a contiguous 1 KB, loaded straight into registers one (tap, 32-channel) step
-//   ahead of its use.
-// * B (activations) is staged per 64-channel slab into LDS as [time][64 + 8 pad] bf16 (144-byte
-//   rows: a 16-lane B-fragment read touches distinct banks); every tap reads the same slab at a
-//   row offset.  The layer's prologue (AdaIN affine + Snake or leaky ReLU, f32 -> bf16 with the
-//   hardware round-to-nearest-even convert) runs once per staged element.
-// * Warp specialization: half of a block's waves are producers, half consumers.  Producers stage
-//   (global loads + prologue VALU) the next 64-channel slab into one of two LDS buffers while the
-//   consumers run the MFMAs of the current slab from the other, so VALU and MFMA co-execute on
-//   every SIMD.  Blocks are persistent: each walks a strided list of (tile, M-block) units, and the
-//   slab stream runs across unit boundaries, so the epilogue of one unit overlaps the staging of
-//   the next.
-// * Each consumer wave owns a 64 x 128 output tile (4 x 8 MFMA tiles, 128 accumulator registers);
-//   A fragments are prefetched two (tap, 32-channel) steps ahead, across slab and unit boundaries.
+// * Work units are (tile, M-block) pairs.  Tiles are item-aligned (kk_kernels.h TilesDev): a tile
+//   never mixes items, so the per-item zero padding of the reference's gap masking
+//   (src/gpu_batch.rs:62-79) is a row-range test and the AdaIN coefficients are constants of the
+//   unit.  One persistent block per CU walks a strided list of units; the M-blocks of one tile run
+//   side by side on one XCD and share its L2 copy of the tile's input.
+// * Warp specialization.  Producer waves stream the input through LDS in 64-channel slabs
+//   ([time][64 + 8 pad] bf16, 144-byte rows: the 16 rows of a B-fragment read fall on distinct
+//   banks): global loads of slab g + 2 are in flight while slab g + 1 is converted, and the layer's
+//   prologue (AdaIN affine + Snake or leaky ReLU, f32 -> bf16 with the hardware round-to-nearest-
+//   even convert) runs once per staged element.  Consumer waves run the MFMAs of slab g from the
+//   other LDS buffer; one barrier per slab hands the buffers over.  Vector-memory counters complete
+//   in issue order, so keeping the HBM stream in the producer waves keeps the consumers' waits to
+//   their own weight loads (L2 hits), and the producers' VALU work co-issues with the MFMAs.
+// * The consumers issue v_mfma_f32_32x32x16_bf16: one wave per SIMD sustains the matrix core's
+//   rate with the 32x32 shape (the 16x16x32 shape needs two).  Each consumer wave owns a 64 x 128
+//   output tile (2 x 4 MFMA tiles, 128 accumulator registers).
+// * A (weights) is pre-packed as [tap][cin/16][M_pad][16] bf16: one A fragment (32 rows x 16
+//   channels) is a contiguous 1 KB, loaded into registers a full tap ahead of its use; B fragments
+//   are read from LDS one 16-channel step ahead.
 // * The epilogue adds the bias, applies the layer's residual rule in f32 and, when asked, reduces
 //   the instance-norm statistics of the values it stores: per (tile, wave, channel) sums of
 //   (v - v_first), written to a partials buffer that finalize combines in a fixed order.
-// * The Snake blocks' conv1 output (input of conv2's AdaIN) is stored as fp16 (PRO_*_H / EPI_STORE_H):
-//   half the HBM traffic of f32, 8x the precision of bf16 operands; the residual stream stays f32.
+// * The Snake blocks' conv1 output (input of conv2's AdaIN) is stored as fp16: half the HBM
+//   traffic of f32, 8x the precision of the bf16 operands; the residual stream stays f32.
 #include "kk_common.h"
 #include "kk_kernels.h"
 
@@ -40,11 +41,14 @@ namespace kk {
 
 namespace {
 
-constexpr int kCK = 64;       // input channels staged per slab
-constexpr int kRS = kCK + 8;  // LDS row stride (bf16 elements)
+constexpr int kCK = 64;       // input channels per LDS slab
+constexpr int kRS = kCK + 8;  // LDS row stride (bf16 elements, 144 bytes)
 constexpr int kNJ = 8;        // 16-column MFMA tiles per wave (wave N = 128)
+constexpr int kMaxHalo = 64;  // largest (k - 1) * dil the staging covers
+constexpr int kNP = 256;      // producer threads per block
 
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
@@ -58,327 +62,477 @@ __device__ __forceinline__ float snake(float v, float a_rev, float a_inv) {
     return __builtin_fmaf(s * s, a_inv, v);
 }
 
-// Stage rows [in0, in0 + tw) x channels [c0, c0 + 64) of the input into LDS as bf16, applying the
-// prologue.  Producer thread pt owns channel octet (pt % 8) of rows pt / 8, pt / 8 + NP / 8, ...;
-// RB rows' global loads are issued before any of them is converted.
-template <int PRO, bool IN_H, int NP>
-__device__ __forceinline__ void stage_slab(const ConvParams& p, uint16_t* xs, int64_t in0, int tw, int c0,
-                                           int64_t i_lo, int64_t i_hi, int item, int pt) {
-    const int q = (pt & 7) * 8;
-    const int c = c0 + q;
-    constexpr int RP = NP / 8;  // rows per pass
-    constexpr int RB = NP >= 256 ? 10 : 9;
-    if constexpr (PRO == PRO_BF16) {
-        const uint16_t* x = (const uint16_t*)p.x;
-        for (int r = pt >> 3; r < tw; r += RP) {
-            const int64_t row = in0 + r;
-            uint4 v = make_uint4(0, 0, 0, 0);
-            if (row >= i_lo && row < i_hi) v = *(const uint4*)(x + row * p.x_ld + c);
-            *(uint4*)(xs + r * kRS + q) = v;
-        }
-        return;
-    } else {
-        // per-thread constants of this slab: AdaIN coefficients of the unit's item, Snake alphas
-        float sc[8], sh[8], ar[8], ai[8];
+// One (tile, M-block) unit of work.  Rows fit in 32 bits (checked on the host).
+struct Unit {
+    int tile, n0, in0, i_lo, i_hi, m0, item, nv;
+};
+
+// Producer side: one slab = rows [in0, in0 + tw) x channels [c0, c0 + 64) of the input.  Producer
+// thread pt owns channel octet q = (pt % 8) * 8 of rows pt / 8 + j * RP (j < RB).  load() issues the
+// global loads into registers; convert() applies the prologue and writes bf16 rows into an LDS
+// buffer.  Rows outside the unit's item, and channels >= cin, are staged as 0 (the conv's zero
+// padding of the activated signal).
+template <int PRO, bool IN_H, int BN>
+struct Stager {
+    static constexpr int RP = kNP / 8;                        // rows per pass
+    static constexpr int RB = (BN + kMaxHalo + RP - 1) / RP;  // passes
+    static constexpr bool WIDE = PRO != PRO_BF16 && !IN_H;    // f32 source: 8 dwords per octet
+    static constexpr int NW = WIDE ? 8 : 4;
+    uint32_t raw[RB][NW];
+
+    __device__ __forceinline__ static bool live(const ConvParams& p, const Unit& u, int r, int tw, int c) {
+        const int row = u.in0 + r;
+        return r < tw && row >= u.i_lo && row < u.i_hi && c < p.cin;
+    }
+
+    __device__ __forceinline__ void load(const ConvParams& p, const Unit& u, int c0, int tw, int q, int rr) {
+        const int c = c0 + q;
 #pragma unroll
-        for (int e = 0; e < 8; e++) {
-            const bool live = c + e < p.cin;
-            sc[e] = 1.f, sh[e] = 0.f, ar[e] = 0.f, ai[e] = 0.f;
-            if constexpr (PRO == PRO_ADAIN_LEAKY || PRO == PRO_ADAIN_SNAKE) {
-                if (live) {
-                    const Coef k = p.coef[(int64_t)item * p.cin + c + e];
-                    sc[e] = k.sc, sh[e] = k.sh;
-                }
-            }
-            if constexpr (PRO == PRO_ADAIN_SNAKE) {
-                if (live) ar[e] = p.alpha_rev[c + e], ai[e] = p.alpha_inv[c + e];
-            }
-        }
-        for (int rb = pt >> 3; rb < tw; rb += RB * RP) {
-            float v[RB][8];
-            bool ok[RB];
+        for (int j = 0; j < RB; j++) {
+            const int r = rr + j * RP;
 #pragma unroll
-            for (int j = 0; j < RB; j++) {
-                const int r = rb + j * RP;
-                const int64_t row = in0 + r;
-                ok[j] = r < tw && row >= i_lo && row < i_hi && c < p.cin;
-                if constexpr (IN_H) {
-                    uint4 h = make_uint4(0, 0, 0, 0);
-                    if (ok[j]) h = *(const uint4*)((const uint16_t*)p.x + row * p.x_ld + c);
-                    const uint32_t hw[4] = {h.x, h.y, h.z, h.w};
-#pragma unroll
-                    for (int e = 0; e < 4; e++) {
-                        const _Float16 lo = __builtin_bit_cast(_Float16, (uint16_t)(hw[e] & 0xffffu));
-                        const _Float16 hi = __builtin_bit_cast(_Float16, (uint16_t)(hw[e] >> 16));
-                        v[j][2 * e] = (float)lo, v[j][2 * e + 1] = (float)hi;
-                    }
+            for (int e = 0; e < NW; e++) raw[j][e] = 0u;
+            if (live(p, u, r, tw, c)) {
+                const int64_t row = u.in0 + r;
+                if constexpr (WIDE) {
+                    const uint4* xp = (const uint4*)((const float*)p.x + row * p.x_ld + c);
+                    const uint4 x0 = xp[0], x1 = xp[1];
+                    raw[j][0] = x0.x, raw[j][1] = x0.y, raw[j][2] = x0.z, raw[j][3] = x0.w;
+                    raw[j][4] = x1.x, raw[j][5] = x1.y, raw[j][6] = x1.z, raw[j][7] = x1.w;
                 } else {
-                    float4 x0 = make_float4(0.f, 0.f, 0.f, 0.f), x1 = x0;
-                    if (ok[j]) {
-                        const float* xp = (const float*)p.x + row * p.x_ld + c;
-                        x0 = *(const float4*)xp;
-                        x1 = *(const float4*)(xp + 4);
+                    const uint4 h = *(const uint4*)((const uint16_t*)p.x + row * p.x_ld + c);
+                    raw[j][0] = h.x, raw[j][1] = h.y, raw[j][2] = h.z, raw[j][3] = h.w;
+                }
+            }
+        }
+    }
+
+    __device__ __forceinline__ void convert(const ConvParams& p, uint16_t* xs, const Unit& u, int c0, int tw, int q,
+                                            int rr) const {
+        const int c = c0 + q;
+        if constexpr (PRO == PRO_BF16) {
+            // bf16 input: channels >= cin of the source buffer hold 0
+#pragma unroll
+            for (int j = 0; j < RB; j++) {
+                const int r = rr + j * RP;
+                if (r < tw) *(uint4*)(xs + r * kRS + q) = make_uint4(raw[j][0], raw[j][1], raw[j][2], raw[j][3]);
+            }
+            return;
+        } else {
+            // per-thread constants: AdaIN coefficients of the unit's item, Snake alphas
+            float sc[8], sh[8], ar[8], ai[8];
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const bool in = c + e < p.cin;
+                sc[e] = 1.f, sh[e] = 0.f, ar[e] = 0.f, ai[e] = 0.f;
+                if constexpr (PRO == PRO_ADAIN_LEAKY || PRO == PRO_ADAIN_SNAKE) {
+                    if (in) {
+                        const Coef k = p.coef[(int64_t)u.item * p.cin + c + e];
+                        sc[e] = k.sc, sh[e] = k.sh;
                     }
-                    v[j][0] = x0.x, v[j][1] = x0.y, v[j][2] = x0.z, v[j][3] = x0.w;
-                    v[j][4] = x1.x, v[j][5] = x1.y, v[j][6] = x1.z, v[j][7] = x1.w;
+                }
+                if constexpr (PRO == PRO_ADAIN_SNAKE) {
+                    if (in) ar[e] = p.alpha_rev[c + e], ai[e] = p.alpha_inv[c + e];
                 }
             }
 #pragma unroll
             for (int j = 0; j < RB; j++) {
-                const int r = rb + j * RP;
+                const int r = rr + j * RP;
                 if (r >= tw) break;
                 uint4 out = make_uint4(0, 0, 0, 0);
-                if (ok[j]) {
-                    float u[8];
+                if (live(p, u, r, tw, c)) {
+                    float v[8];
+                    if constexpr (WIDE) {
+#pragma unroll
+                        for (int e = 0; e < 8; e++) v[e] = __uint_as_float(raw[j][e]);
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; e++) {
+                            v[2 * e] = (float)__builtin_bit_cast(_Float16, (uint16_t)(raw[j][e] & 0xffffu));
+                            v[2 * e + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(raw[j][e] >> 16));
+                        }
+                    }
+                    float w[8];
 #pragma unroll
                     for (int e = 0; e < 8; e++) {
-                        float w = v[j][e];
+                        float x = v[e];
                         if constexpr (PRO == PRO_LEAKY) {
-                            w = w < 0.f ? w * p.slope : w;
+                            x = x < 0.f ? x * p.slope : x;
                         } else if constexpr (PRO == PRO_ADAIN_LEAKY) {
-                            w = __builtin_fmaf(w, sc[e], sh[e]);
-                            w = w < 0.f ? w * p.slope : w;
+                            x = __builtin_fmaf(x, sc[e], sh[e]);
+                            x = x < 0.f ? x * p.slope : x;
                         } else if constexpr (PRO == PRO_ADAIN_SNAKE) {
-                            w = snake(__builtin_fmaf(w, sc[e], sh[e]), ar[e], ai[e]);
+                            x = snake(__builtin_fmaf(x, sc[e], sh[e]), ar[e], ai[e]);
                         }
-                        u[e] = c + e < p.cin ? w : 0.f;
+                        w[e] = c + e < p.cin ? x : 0.f;
                     }
-                    out.x = pack_bf16x2(u[0], u[1]);
-                    out.y = pack_bf16x2(u[2], u[3]);
-                    out.z = pack_bf16x2(u[4], u[5]);
-                    out.w = pack_bf16x2(u[6], u[7]);
+                    out.x = pack_bf16x2(w[0], w[1]);
+                    out.y = pack_bf16x2(w[2], w[3]);
+                    out.z = pack_bf16x2(w[4], w[5]);
+                    out.w = pack_bf16x2(w[6], w[7]);
                 }
                 *(uint4*)(xs + r * kRS + q) = out;
             }
         }
     }
-}
+};
 
-// Store 4 consecutive GEMM rows m..m+3 of GEMM column t; returns the stored values (statistics).
-template <int EPI, bool OUT_H>
-__device__ __forceinline__ float4 store4(const ConvParams& p, int item, int64_t t, int m, float4 v) {
-    if constexpr (EPI == EPI_CONVT || EPI == EPI_CONVT_REFLECT) {
-        const int ph = m / p.cout, co = m - ph * p.cout;
-        const int64_t o = (int64_t)p.stride_t * t + ph - p.pad_t;  // ConvT output column
-        const int64_t os = p.out_start[item];
-        const int64_t ol = EPI == EPI_CONVT ? p.out_len[item] : p.out_len[item] - 1;
-        if (o < os || o >= os + ol) return v;
-        const float4 b = *(const float4*)(p.bias + co);
-        v.x += b.x, v.y += b.y, v.z += b.z, v.w += b.w;
-        // EPI_CONVT_REFLECT: ReflectionPad1d((1,0)) per item on the padded domain
-        // (kernels/kokoro.cu:452-467): padded[s] = ups[s + 1], padded[s + 1 + j] = ups[s + j].
-        const int64_t dest = EPI == EPI_CONVT ? o : o + 1;
-        const float4 r = *(const float4*)(p.r0 + dest * p.r0_ld + co);
-        *(float4*)(p.y + dest * p.y_ld + co) = make_float4(v.x + r.x, v.y + r.y, v.z + r.z, v.w + r.w);
-        if (EPI == EPI_CONVT_REFLECT && o == os + 1) {
-            const float4 r2 = *(const float4*)(p.r0 + os * p.r0_ld + co);
-            *(float4*)(p.y + os * p.y_ld + co) = make_float4(v.x + r2.x, v.y + r2.y, v.z + r2.z, v.w + r2.w);
-        }
-        return v;
-    } else {
-        const float4 b = p.bias ? *(const float4*)(p.bias + m) : make_float4(0.f, 0.f, 0.f, 0.f);
-        v.x += b.x, v.y += b.y, v.z += b.z, v.w += b.w;
-        if constexpr (OUT_H) {
-            // fp16 storage; the statistics describe the rounded values the next layer reads
-            const _Float16 h0 = (_Float16)v.x, h1 = (_Float16)v.y, h2 = (_Float16)v.z, h3 = (_Float16)v.w;
-            uint2 pk;
-            pk.x = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
-            pk.y = (uint32_t)__builtin_bit_cast(uint16_t, h2) | ((uint32_t)__builtin_bit_cast(uint16_t, h3) << 16);
-            *(uint2*)((uint16_t*)p.y + t * p.y_ld + m) = pk;
-            return make_float4((float)h0, (float)h1, (float)h2, (float)h3);
-        }
-        float* dst = p.y + t * p.y_ld + m;
-        float4 o = v;
-        if constexpr (EPI == EPI_ACCUM) {
-            const float4 y = *(const float4*)dst;
-            o = make_float4(y.x + v.x, y.y + v.y, y.z + v.z, y.w + v.w);
-        } else if constexpr (EPI == EPI_RESID) {
-            const float4 y = *(const float4*)dst;
-            const float s = p.scale;
-            o = make_float4((v.x + y.x) * s, (v.y + y.y) * s, (v.z + y.z) * s, (v.w + y.w) * s);
-        } else if constexpr (EPI == EPI_RESID_UP2) {
-            const float4 y = *(const float4*)(p.r0 + (t >> 1) * p.r0_ld + m);
-            const float s = p.scale;
-            o = make_float4((v.x + y.x) * s, (v.y + y.y) * s, (v.z + y.z) * s, (v.w + y.w) * s);
-        } else if constexpr (EPI == EPI_ADD_FROM) {
-            const float4 y = *(const float4*)(p.r0 + t * p.r0_ld + m);
-            o = make_float4(y.x + v.x, y.y + v.y, y.z + v.z, y.w + v.w);
-        } else if constexpr (EPI == EPI_MEAN3) {
-            // ((rb0 + rb1) + (rb2_resid + conv)) / 3   (src/gpu_batch.rs:395-401)
-            const float4 a = *(const float4*)(p.r0 + t * p.r0_ld + m);
-            const float4 b1 = *(const float4*)(p.r1 + t * p.r0_ld + m);
-            const float4 c = *(const float4*)(p.r2 + t * p.r0_ld + m);
-            o = make_float4(((a.x + b1.x) + (c.x + v.x)) / 3.0f, ((a.y + b1.y) + (c.y + v.y)) / 3.0f,
-                            ((a.z + b1.z) + (c.z + v.z)) / 3.0f, ((a.w + b1.w) + (c.w + v.w)) / 3.0f);
-        }
-        *(float4*)dst = o;
-        return o;
+// ConvT epilogue: scatter 4 consecutive GEMM rows m..m+3 (phase, channel) of input column t.
+template <int EPI>
+__device__ __forceinline__ void store_convt(const ConvParams& p, int item, int64_t t, int m, float4 v) {
+    const int ph = m / p.cout, co = m - ph * p.cout;
+    const int64_t o = (int64_t)p.stride_t * t + ph - p.pad_t;  // ConvT output column
+    const int64_t os = p.out_start[item];
+    const int64_t ol = EPI == EPI_CONVT ? p.out_len[item] : p.out_len[item] - 1;
+    if (o < os || o >= os + ol) return;
+    const float4 b = *(const float4*)(p.bias + co);
+    v.x += b.x, v.y += b.y, v.z += b.z, v.w += b.w;
+    // EPI_CONVT_REFLECT: ReflectionPad1d((1,0)) per item on the padded domain
+    // (kernels/kokoro.cu:452-467): padded[s] = ups[s + 1], padded[s + 1 + j] = ups[s + j].
+    const int64_t dest = EPI == EPI_CONVT ? o : o + 1;
+    const float4 r = *(const float4*)(p.r0 + dest * p.r0_ld + co);
+    *(float4*)(p.y + dest * p.y_ld + co) = make_float4(v.x + r.x, v.y + r.y, v.z + r.z, v.w + r.w);
+    if (EPI == EPI_CONVT_REFLECT && o == os + 1) {
+        const float4 r2 = *(const float4*)(p.r0 + os * p.r0_ld + co);
+        *(float4*)(p.y + os * p.y_ld + co) = make_float4(v.x + r2.x, v.y + r2.y, v.z + r2.z, v.w + r2.w);
     }
 }
 
-// Sum over the 16 lanes of a DPP row (row_ror 1, 2, 4, 8): every lane of the row gets the total.
-__device__ __forceinline__ float row_sum16(float v) {
-    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x121, 0xf, 0xf, false));
-    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x122, 0xf, 0xf, false));
-    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x124, 0xf, 0xf, false));
-    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x128, 0xf, 0xf, false));
-    return v;
+// Residual operands a stride-1 epilogue reads per 4 output rows.
+template <int EPI>
+constexpr int kNumRes = EPI == EPI_MEAN3 ? 3
+                        : (EPI == EPI_ACCUM || EPI == EPI_RESID || EPI == EPI_RESID_UP2 || EPI == EPI_ADD_FROM) ? 1
+                                                                                                                 : 0;
+
+template <int EPI>
+__device__ __forceinline__ void load_res(const ConvParams& p, int64_t t, int m, float4* r) {
+    if constexpr (EPI == EPI_ACCUM || EPI == EPI_RESID) {
+        r[0] = *(const float4*)(p.y + t * p.y_ld + m);
+    } else if constexpr (EPI == EPI_RESID_UP2) {
+        r[0] = *(const float4*)(p.r0 + (t >> 1) * p.r0_ld + m);
+    } else if constexpr (EPI == EPI_ADD_FROM) {
+        r[0] = *(const float4*)(p.r0 + t * p.r0_ld + m);
+    } else if constexpr (EPI == EPI_MEAN3) {
+        r[0] = *(const float4*)(p.r0 + t * p.r0_ld + m);
+        r[1] = *(const float4*)(p.r1 + t * p.r0_ld + m);
+        r[2] = *(const float4*)(p.r2 + t * p.r0_ld + m);
+    }
+}
+
+// Stride-1 epilogue of rows m..m+3 of column t: v = conv + bias, combined with the residuals r;
+// returns the stored values (the statistics describe what the next layer reads).
+template <int EPI, bool OUT_H>
+__device__ __forceinline__ float4 finish4(const ConvParams& p, int64_t t, int m, float4 v, const float4* r) {
+    if constexpr (OUT_H) {
+        // fp16 storage
+        const _Float16 h0 = (_Float16)v.x, h1 = (_Float16)v.y, h2 = (_Float16)v.z, h3 = (_Float16)v.w;
+        uint2 pk;
+        pk.x = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+        pk.y = (uint32_t)__builtin_bit_cast(uint16_t, h2) | ((uint32_t)__builtin_bit_cast(uint16_t, h3) << 16);
+        *(uint2*)((uint16_t*)p.y + t * p.y_ld + m) = pk;
+        return make_float4((float)h0, (float)h1, (float)h2, (float)h3);
+    }
+    float4 o = v;
+    if constexpr (EPI == EPI_ACCUM || EPI == EPI_ADD_FROM) {
+        const float4 y = r[0];
+        o = make_float4(y.x + v.x, y.y + v.y, y.z + v.z, y.w + v.w);
+    } else if constexpr (EPI == EPI_RESID || EPI == EPI_RESID_UP2) {
+        const float4 y = r[0];
+        const float s = p.scale;
+        o = make_float4((v.x + y.x) * s, (v.y + y.y) * s, (v.z + y.z) * s, (v.w + y.w) * s);
+    } else if constexpr (EPI == EPI_MEAN3) {
+        // ((rb0 + rb1) + (rb2_resid + conv)) / 3   (src/gpu_batch.rs:395-401)
+        const float4 a = r[0], b1 = r[1], c = r[2];
+        o = make_float4(((a.x + b1.x) + (c.x + v.x)) / 3.0f, ((a.y + b1.y) + (c.y + v.y)) / 3.0f,
+                        ((a.z + b1.z) + (c.z + v.z)) / 3.0f, ((a.w + b1.w) + (c.w + v.w)) / 3.0f);
+    }
+    *(float4*)(p.y + t * p.y_ld + m) = o;
+    return o;
+}
+
+constexpr int kScrLd = 64 + 4;  // epilogue LDS scratch row stride (f32): one time column, 64 channels
+
+// Epilogue of one unit: bias, residual rule, stores, statistics partials; zeroes the accumulators.
+// The MFMA layout gives each lane 4 channels of one column (D of tile (i, j): rows i*32 + 8 g + 4 lh
+// + r of column j*32 + l32), so stores straight from it would scatter 8-16 byte pieces over 32
+// rows.  Instead the wave transposes each 32-column slice through its LDS scratch ([32][kScrLd]
+// f32): afterwards 16 lanes hold one column's 64 channels (lane group cg = column, cq = channel
+// quad), so every store and residual load covers whole 256-byte column rows, and the statistics
+// accumulate per lane over columns with one cross-group reduction at the end.
+template <int EPI, int WM, int WN, bool STATS, bool OUT_H>
+__device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32x16 (&acc)[2][4], int wm, int wn,
+                                         int lane, float* scr) {
+    constexpr bool CONVT = EPI == EPI_CONVT || EPI == EPI_CONVT_REFLECT;
+    constexpr int NR = CONVT ? 0 : kNumRes<EPI>;
+    constexpr int NRA = NR > 0 ? NR : 1;
+    constexpr int QB = NR > 1 ? 2 : 8;  // column groups per residual batch
+    const int l32 = lane & 31, lh = lane >> 5;
+    const int cq = lane & 15, cg = lane >> 4;
+    const int wcol0 = wn * 128;                // this wave's first column within the tile
+    const int m = u.m0 + wm * 64 + 4 * cq;     // this lane's 4 output rows after the transpose
+    const bool mok = m < p.m;
+    float4 b = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (!CONVT && p.bias && mok) b = *(const float4*)(p.bias + m);
+    float s1[4] = {0.f, 0.f, 0.f, 0.f}, s2[4] = {0.f, 0.f, 0.f, 0.f}, sft[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int g = 0; g < 4; g++)
+                *(float4*)(scr + l32 * kScrLd + i * 32 + 8 * g + 4 * lh) =
+                    make_float4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int q0 = 0; q0 < 8; q0 += QB) {
+            float4 res[QB][NRA];
+            if constexpr (NR > 0) {
+#pragma unroll
+                for (int qq = 0; qq < QB; qq++) {
+                    const int col = wcol0 + j * 32 + 4 * (q0 + qq) + cg;
+#pragma unroll
+                    for (int e = 0; e < NRA; e++) res[qq][e] = make_float4(0.f, 0.f, 0.f, 0.f);
+                    if (col < u.nv && mok) load_res<EPI>(p, u.n0 + col, m, res[qq]);
+                }
+            }
+#pragma unroll
+            for (int qq = 0; qq < QB; qq++) {
+                const int q = q0 + qq;
+                const int col = wcol0 + j * 32 + 4 * q + cg;
+                const bool valid = col < u.nv;
+                float4 v = *(const float4*)(scr + (4 * q + cg) * kScrLd + 4 * cq);
+                float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (valid && mok) {
+                    if constexpr (CONVT) {
+                        store_convt<EPI>(p, u.item, u.n0 + col, m, v);
+                    } else {
+                        v.x += b.x, v.y += b.y, v.z += b.z, v.w += b.w;
+                        o = finish4<EPI, OUT_H>(p, u.n0 + col, m, v, res[qq]);
+                    }
+                }
+                if constexpr (STATS) {
+                    const float ov[4] = {o.x, o.y, o.z, o.w};
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        if (j == 0 && q == 0) sft[r] = __shfl(ov[r], cq, 64);  // the wave's first column
+                        const float d = valid ? ov[r] - sft[r] : 0.f;
+                        s1[r] += d;
+                        s2[r] = __builtin_fmaf(d, d, s2[r]);
+                    }
+                }
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+    if constexpr (STATS) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            s1[r] += __shfl_xor(s1[r], 16, 64);
+            s2[r] += __shfl_xor(s2[r], 16, 64);
+            s1[r] += __shfl_xor(s1[r], 32, 64);
+            s2[r] += __shfl_xor(s2[r], 32, 64);
+        }
+        if (cg == 0 && wcol0 < u.nv) {
+            StatPart* dst = p.part + ((int64_t)u.tile * WN + wn) * p.cout;
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+                if (m + r < p.cout) dst[m + r] = StatPart{s1[r], s2[r], sft[r]};
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) acc[i][j][e] = 0.f;
 }
 
 template <int PRO, int EPI, int WM, int WN, bool STATS, bool IN_H, bool OUT_H>
-__global__ __launch_bounds__(128 * WM * WN) void conv_mfma_kernel(ConvParams p) {
+__global__ __launch_bounds__(64 * WM * WN + kNP) void conv_mfma_kernel(ConvParams p) {
     constexpr int BM = 64 * WM, BN = 16 * kNJ * WN, NC = 64 * WM * WN;
     extern __shared__ __align__(16) uint16_t xs[];
+    const int mblocks = p.m_pad / BM;
     const int tw = BN + (p.k - 1) * p.dil;
     const int slab_elems = tw * kRS;
-    const int nslab = p.cin_pad / kCK;
-    const int mblocks = p.m_pad / BM;
-    const int64_t units = p.tiles.count * mblocks;
-    const int64_t my_units = units > blockIdx.x ? (units - blockIdx.x + gridDim.x - 1) / gridDim.x : 0;
-    const int64_t steps = my_units * nslab;
-    auto unit_of = [&](int64_t g) { return (int64_t)blockIdx.x + (g / nslab) * gridDim.x; };
+    const int nsl = p.cin_pad / kCK;
+
+    // Units: U = g * 8 * mblocks + w * 8 + x is M-block w of tile g * 8 + x.  Block b runs units
+    // b, b + G, b + 2G, ... (G = gridDim.x, a multiple of 8 * mblocks, so b keeps its w and x).
+    // Workgroup slots go to the 8 XCDs round-robin: block b stays on XCD x.
+    const int grp_units = 8 * mblocks;
+    auto unit_at = [&](int U, Unit& u) -> bool {
+        const int g = U / grp_units;
+        const int within = U - g * grp_units;
+        u.tile = g * 8 + (within & 7);
+        if (u.tile >= p.tiles.count) return false;
+        u.m0 = (within >> 3) * BM;
+        u.item = p.tiles.item[u.tile];
+        u.n0 = (int)p.tiles.t0[u.tile];
+        u.nv = p.tiles.n[u.tile];
+        u.i_lo = (int)p.in_start[u.item];
+        u.i_hi = u.i_lo + (int)p.in_len[u.item];
+        u.in0 = u.n0 - p.pad;
+        return true;
+    };
+    // slabs this block runs: units b + i G with tile g_i * 8 + x < count, g_i = g_0 + i * (G / grp)
+    int n_units = 0;
+    {
+        const int b = blockIdx.x;
+        const int g0 = b / grp_units, x = (b - g0 * grp_units) & 7;
+        const int gmax = ((int)p.tiles.count - 1 - x) >> 3;  // last group whose tile g*8+x exists
+        if (p.tiles.count > x && gmax >= g0) n_units = (gmax - g0) / ((int)gridDim.x / grp_units) + 1;
+    }
+    const int G = n_units * nsl;
+    if (G == 0) return;
 
     if (threadIdx.x >= NC) {
         // ------------------------------------------------------------ producer waves
         const int pt = threadIdx.x - NC;
-        auto stage = [&](int64_t g) {
-            const int64_t u = unit_of(g);
-            const int64_t tile = u / mblocks;
-            const int item = p.tiles.item[tile];
-            const int64_t i_lo = p.in_start[item], i_hi = i_lo + p.in_len[item];
-            stage_slab<PRO, IN_H, NC>(p, xs + (g & 1) * slab_elems, p.tiles.t0[tile] - p.pad, tw,
-                                      (int)(g % nslab) * kCK, i_lo, i_hi, item, pt);
+        const int q = (pt & 7) * 8, rr = pt >> 3;
+        Stager<PRO, IN_H, BN> st;
+        int U = blockIdx.x, sl = 0;  // iterator over (unit, slab) steps
+        Unit u;
+        unit_at(U, u);
+        auto advance = [&]() {
+            if (++sl == nsl) {
+                sl = 0;
+                U += gridDim.x;
+                unit_at(U, u);
+            }
         };
-        if (steps > 0) stage(0);
+        st.load(p, u, 0, tw, q, rr);
+        st.convert(p, xs, u, 0, tw, q, rr);
+        advance();
+        if (G > 1) st.load(p, u, sl * kCK, tw, q, rr);
         __syncthreads();
-        for (int64_t g = 0; g < steps; g++) {
-            if (g + 1 < steps) stage(g + 1);
+        for (int g = 0; g < G; g++) {
+            // the iterator is at step g + 1: convert it (its loads were issued during step g - 1),
+            // then issue the loads of step g + 2
+            if (g + 1 < G) {
+                st.convert(p, xs + ((g + 1) & 1) * slab_elems, u, sl * kCK, tw, q, rr);
+                advance();
+                if (g + 2 < G) st.load(p, u, sl * kCK, tw, q, rr);
+            }
             __syncthreads();
         }
         return;
     }
 
     // ---------------------------------------------------------------- consumer waves
+    // v_mfma_f32_32x32x16_bf16 lane layouts (l32 = lane % 32, lh = lane / 32): A[l32][8 lh + e],
+    // B[8 lh + e][l32], D[8 (r / 4) + 4 lh + r % 4][l32] for r < 16.  One wave issuing 32x32 MFMAs
+    // back to back keeps the matrix core busy; the 16x16 shape needs two waves per SIMD.
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int wm = wave % WM, wn = wave / WM;
-    const int lr = lane & 15, lg = lane >> 4;
-    const int ncc = p.cin_pad >> 5;
-    const int64_t total = steps * p.k;  // flattened (slab step, tap) stream
-    const int64_t a_step = (int64_t)p.m_pad * 4;
-    // A fragments of flattened iteration f = g * k + tap: [half cs][i] for the unit's M block and slab
-    bf16x8 a_cur[2][4], a_nxt[2][4];
-    auto load_a = [&](bf16x8 (&dst)[2][4], int64_t f) {
-        if (f >= total) return;
-        const int64_t g = f / p.k;
-        const int kk = (int)(f - g * p.k);
-        const int mb = (int)(unit_of(g) % mblocks);
-        const bf16x8* ap = (const bf16x8*)p.w + (int64_t)(mb * BM + wm * 64 + lr) * 4 + lg +
-                           ((int64_t)kk * ncc + (g % nslab) * 2) * a_step;
-#pragma unroll
-        for (int cs = 0; cs < 2; cs++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) dst[cs][i] = ap[cs * a_step + i * 64];
+    const int l32 = lane & 31, lh = lane >> 5;
+    // this wave's epilogue scratch, after the two slab buffers
+    float* scr = (float*)(xs + 2 * slab_elems) + wave * 32 * kScrLd;
+    const int n16 = p.cin_pad / 16;               // 16-channel groups
+    const int64_t a_step = (int64_t)p.m_pad * 2;  // one 16-channel group of A, in bf16x8
+    const bf16x8* w_lane = (const bf16x8*)p.w + (int64_t)(wm * 64 + l32) * 2 + lh;
+    // A fragments of tap kk, 16-channel group c16: rows m0 + wm*64 + i*32 + l32 (i < 2)
+    auto load_a = [&](bf16x8 (&dst)[2], int m0, int kk, int c16) {
+        const bf16x8* ap = w_lane + (int64_t)m0 * 2 + ((int64_t)kk * n16 + c16) * a_step;
+        dst[0] = ap[0];
+        dst[1] = ap[64];
     };
-    f32x4 acc[4][kNJ];
+    // B fragments of tap kk, 16-channel step kc of the slab: columns wn*128 + j*32 + l32 (j < 4)
+    auto read_b = [&](bf16x8 (&dst)[4], const uint16_t* buf, int kk, int kc) {
+        const uint16_t* bp = buf + (wn * 128 + kk * p.dil + l32) * kRS + kc * 16 + lh * 8;
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+        for (int j = 0; j < 4; j++) dst[j] = *(const bf16x8*)(bp + j * 32 * kRS);
+    };
+    f32x16 acc[2][4];
 #pragma unroll
-        for (int j = 0; j < kNJ; j++) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) acc[i][j][e] = 0.f;
+    auto mfma_step = [&](const bf16x8 (&a)[2], const bf16x8 (&b)[4]) {
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+    };
 
-    load_a(a_cur, 0);
+    int U = blockIdx.x, sl = 0;
+    Unit cu, nu;
+    unit_at(U, cu);
+    bool has_next = unit_at(U + gridDim.x, nu);
+    // A of the current tap, one register set per 16-channel step; each set is refilled with the
+    // next tap's fragments right after its MFMAs issue (a full tap of lead time for the L2 loads).
+    bf16x8 A[4][2], B0[4], B1[4];
+#pragma unroll
+    for (int kc = 0; kc < 4; kc++) load_a(A[kc], cu.m0, 0, kc);
     __syncthreads();  // slab 0 staged
-    for (int64_t g = 0; g < steps; g++) {
+    for (int g = 0; g < G; g++) {
         const uint16_t* buf = xs + (g & 1) * slab_elems;
+        const bool last = sl + 1 == nsl;
+        read_b(B0, buf, 0, 0);
         for (int kk = 0; kk < p.k; kk++) {
-            load_a(a_nxt, g * p.k + kk + 1);  // one tap ahead, across slab and unit boundaries
-            const int rb = wn * 128 + kk * p.dil + lr;
-#pragma unroll
-            for (int cs = 0; cs < 2; cs++) {
-                const int col = cs * 32 + lg * 8;
-#pragma unroll
-                for (int j = 0; j < kNJ; j += 2) {
-                    const bf16x8 b0 = *(const bf16x8*)(buf + (rb + j * 16) * kRS + col);
-                    const bf16x8 b1 = *(const bf16x8*)(buf + (rb + j * 16 + 16) * kRS + col);
-#pragma unroll
-                    for (int i = 0; i < 4; i++)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_cur[cs][i], b0, acc[i][j], 0, 0, 0);
-#pragma unroll
-                    for (int i = 0; i < 4; i++)
-                        acc[i][j + 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_cur[cs][i], b1, acc[i][j + 1], 0, 0, 0);
-                }
+            // the tap after this one: same slab, first tap of the next slab, or of the next unit
+            int n_m0 = cu.m0, n_kk = kk + 1, n_c16 = 4 * sl;
+            bool have = true;
+            if (kk + 1 == p.k) {
+                if (!last) n_kk = 0, n_c16 = 4 * sl + 4;
+                else if (has_next) n_m0 = nu.m0, n_kk = 0, n_c16 = 0;
+                else have = false;
             }
 #pragma unroll
-            for (int cs = 0; cs < 2; cs++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) a_cur[cs][i] = a_nxt[cs][i];
-        }
-        if (g % nslab == nslab - 1) {
-            // the unit's last slab: epilogue, then fresh accumulators for the next unit
-            const int64_t u = unit_of(g);
-            const int64_t tile = u / mblocks;
-            const int m0 = (int)(u % mblocks) * BM;
-            const int item = p.tiles.item[tile];
-            const int64_t n0 = p.tiles.t0[tile];
-            const int nv = p.tiles.n[tile];
-            // D[i][j] lane layout: row (output channel) = 4 * (lane / 16) + r, column = lane % 16.
-            const int wcol0 = wn * 128;
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int m = m0 + wm * 64 + i * 16 + lg * 4;
-                float s1[4] = {0.f, 0.f, 0.f, 0.f}, s2[4] = {0.f, 0.f, 0.f, 0.f}, sft[4];
-#pragma unroll
-                for (int j = 0; j < kNJ; j++) {
-                    const int col = wcol0 + j * 16 + lr;
-                    const bool valid = col < nv;
-                    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-                    if (valid && m < p.m)
-                        o = store4<EPI, OUT_H>(p, item, n0 + col, m,
-                                               make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]));
-                    acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
-                    if constexpr (STATS) {
-                        const float ov[4] = {o.x, o.y, o.z, o.w};
-#pragma unroll
-                        for (int r = 0; r < 4; r++) {
-                            if (j == 0) sft[r] = __shfl(ov[r], lane & 48, 64);  // the wave's first column
-                            const float d = valid ? ov[r] - sft[r] : 0.f;
-                            s1[r] += d;
-                            s2[r] = __builtin_fmaf(d, d, s2[r]);
-                        }
-                    }
-                }
-                if constexpr (STATS) {
-                    if (wcol0 < nv) {
-                        StatPart* dst = p.part + (tile * WN + wn) * (int64_t)p.cout;
-#pragma unroll
-                        for (int r = 0; r < 4; r++) {
-                            const float sa = row_sum16(s1[r]);
-                            const float sb = row_sum16(s2[r]);
-                            if (lr == 0 && m + r < p.cout) dst[m + r] = StatPart{sa, sb, sft[r]};
-                        }
-                    }
-                }
+            for (int kc = 0; kc < 4; kc++) {
+                bf16x8(&bc)[4] = (kc & 1) ? B1 : B0;
+                bf16x8(&bn)[4] = (kc & 1) ? B0 : B1;
+                if (kc < 3) read_b(bn, buf, kk, kc + 1);
+                else if (kk + 1 < p.k) read_b(bn, buf, kk + 1, 0);
+                __builtin_amdgcn_sched_barrier(0);
+                mfma_step(A[kc], bc);
+                __builtin_amdgcn_sched_barrier(0);
+                if (have) load_a(A[kc], n_m0, n_kk, n_c16 + kc);
             }
         }
+        if (last) epilogue<EPI, WM, WN, STATS, OUT_H>(p, cu, acc, wm, wn, lane, scr);
         __syncthreads();  // hand the slab buffer back to the producers
+        if (last) {
+            sl = 0;
+            U += gridDim.x;
+            cu = nu;
+            has_next = unit_at(U + gridDim.x, nu);
+        } else {
+            sl++;
+        }
     }
 }
 
 template <int PRO, int EPI, int WM, int WN, bool STATS, bool IN_H, bool OUT_H>
 hipError_t launch_t(const ConvParams& p, int n_cu, hipStream_t s) {
-    constexpr int BM = 64 * WM, BN = 16 * kNJ * WN;
-    const int tw = BN + (p.k - 1) * p.dil;
-    const size_t smem = 2 * (size_t)tw * kRS * sizeof(uint16_t);
-    if (p.m_pad % BM != 0 || p.cin_pad % kCK != 0 || smem > 160 * 1024) return hipErrorInvalidValue;
+    constexpr int BM = 64 * WM, BN = 16 * kNJ * WN, NT = 64 * WM * WN + kNP;
+    const int halo = (p.k - 1) * p.dil;
+    constexpr size_t scr_bytes = (size_t)WM * WN * 32 * kScrLd * sizeof(float);
+    const size_t smem = 2 * (size_t)(BN + halo) * kRS * sizeof(uint16_t) + scr_bytes;
+    constexpr size_t smem_max = 2 * (size_t)(BN + kMaxHalo) * kRS * sizeof(uint16_t) + scr_bytes;
+    static_assert(smem_max <= 160 * 1024, "LDS budget");
+    if (p.m_pad % BM != 0 || p.cin_pad % kCK != 0 || halo < 0 || halo > kMaxHalo) return hipErrorInvalidValue;
+    if (p.l_in >= (int64_t)1 << 30 || p.tiles.count >= (int64_t)1 << 28) return hipErrorInvalidValue;  // 32-bit rows
     auto kern = conv_mfma_kernel<PRO, EPI, WM, WN, STATS, IN_H, OUT_H>;
-    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
-    if (e != hipSuccess) return e;
-    int per_cu = 0;
-    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, 128 * WM * WN, smem);
-    if (e != hipSuccess) return e;
-    if (per_cu < 1) return hipErrorInvalidConfiguration;
-    const int64_t units = p.tiles.count * (p.m_pad / BM);
-    const int64_t grid = std::min<int64_t>(units, (int64_t)per_cu * n_cu);
-    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(128 * WM * WN), smem, s, p);
+    static bool attr = false;
+    if (!attr) {
+        const hipError_t e =
+            hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem_max);
+        if (e != hipSuccess) return e;
+        attr = true;
+    }
+    // one persistent block per CU; the grid is a multiple of 8 * mblocks
+    const int64_t grp = 8 * (int64_t)(p.m_pad / BM);
+    const int64_t units = ceil_div(p.tiles.count, 8) * grp;  // padded unit count
+    const int64_t fit = std::max<int64_t>(1, n_cu / grp) * grp;
+    const int64_t grid = std::min(units, fit);
+    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(NT), smem, s, p);
     return hipGetLastError();
 }
 

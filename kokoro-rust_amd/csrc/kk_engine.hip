@@ -187,7 +187,8 @@ struct Table {
     }
 };
 
-// A stride-1 conv, w [cout][cin][k] -> packed [k][cin_pad/32][m_pad][32] bf16.
+// A stride-1 conv, w [cout][cin][k] -> packed [k][cin_pad/16][m_pad][16] bf16 (one MFMA A fragment,
+// 32 rows x 16 channels, is a contiguous 1 KB).
 static void load_conv(MConv& c, const Table& t, const std::string& p, int cin, int cout, int k, int pad, int dil,
                       bool bias, int shape) {
     c.cin = cin, c.cout = cout, c.k = k, c.pad = pad, c.dil = dil, c.shape = shape, c.bias = bias;
@@ -195,12 +196,12 @@ static void load_conv(MConv& c, const Table& t, const std::string& p, int cin, i
     c.m = cout;
     c.m_pad = round_up(cout, kShapeM[shape]);
     const float* w = t.get(p + ".weight", (int64_t)cout * cin * k);
-    const int ncc = c.cin_pad / 32;
-    std::vector<uint16_t> pk((size_t)k * ncc * c.m_pad * 32, 0);
+    const int n16 = c.cin_pad / 16;
+    std::vector<uint16_t> pk((size_t)k * n16 * c.m_pad * 16, 0);
     for (int co = 0; co < cout; co++)
         for (int ci = 0; ci < cin; ci++)
             for (int kk = 0; kk < k; kk++)
-                pk[(((size_t)kk * ncc + ci / 32) * c.m_pad + co) * 32 + (ci & 31)] =
+                pk[(((size_t)kk * n16 + ci / 16) * c.m_pad + co) * 16 + (ci & 15)] =
                     bf16_bits(w[((size_t)co * cin + ci) * k + kk]);
     c.w.upload(pk);
     if (bias) {
@@ -219,14 +220,14 @@ static void load_convt(MConv& c, const Table& t, const std::string& p, int cin, 
     c.m = stride * cout;
     c.m_pad = round_up(c.m, kShapeM[c.shape]);
     const float* w = t.get(p + ".weight", (int64_t)cin * cout * kw);
-    const int ncc = c.cin_pad / 32;
-    std::vector<uint16_t> pk((size_t)2 * ncc * c.m_pad * 32, 0);
+    const int n16 = c.cin_pad / 16;
+    std::vector<uint16_t> pk((size_t)2 * n16 * c.m_pad * 16, 0);
     for (int tap = 0; tap < 2; tap++)
         for (int r = 0; r < stride; r++)
             for (int co = 0; co < cout; co++) {
                 const int m = r * cout + co, kk = tap == 0 ? r + stride : r;
                 for (int ci = 0; ci < cin; ci++)
-                    pk[(((size_t)tap * ncc + ci / 32) * c.m_pad + m) * 32 + (ci & 31)] =
+                    pk[(((size_t)tap * n16 + ci / 16) * c.m_pad + m) * 16 + (ci & 15)] =
                         bf16_bits(w[((size_t)ci * cout + co) * kw + kk]);
             }
     c.w.upload(pk);

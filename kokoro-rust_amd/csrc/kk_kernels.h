@@ -63,7 +63,7 @@ struct ConvParams {
     const float* alpha_rev;  // [cin] alpha / 2 pi
     const float* alpha_inv;  // [cin] 1 / alpha
     float slope;
-    const uint16_t* w;       // packed bf16 [k][cin_pad/32][m_pad][32]
+    const uint16_t* w;       // packed bf16 [k][cin_pad/16][m_pad][16]
     const float* bias;       // [cout] or null
     int m, m_pad;            // GEMM rows (cout, or stride * cout for ConvT), padded to the block
     int k, dil, pad;
@@ -82,6 +82,7 @@ struct ConvParams {
 };
 
 // in_h / out_h: fp16 input (conv2 of a Snake step) / fp16 output (conv1 of a Snake step).
+// n_cu: compute units of the device (persistent grid size).
 hipError_t launch_conv(const ConvParams& p, int pro, int epi, int shape, bool stats, bool in_h, bool out_h, int n_cu,
                        hipStream_t s);
 
