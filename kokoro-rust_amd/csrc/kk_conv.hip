@@ -62,23 +62,49 @@ __device__ __forceinline__ float snake(float v, float a_rev, float a_inv) {
     return __builtin_fmaf(s * s, a_inv, v);
 }
 
+// Read-only tables (tiles, item spans) through the constant address space: uniform indices become
+// scalar loads, which leave the vector-memory counter -- and the producers' prefetch -- alone.
+template <typename T>
+__device__ __forceinline__ T ld_const(const T* p, int64_t i) {
+    return ((const __attribute__((address_space(4))) T*)p)[i];
+}
+
 // One (tile, M-block) unit of work.  Rows fit in 32 bits (checked on the host).
 struct Unit {
     int tile, n0, in0, i_lo, i_hi, m0, item, nv;
 };
 
+// An empty asm that reads its operands: whatever produces them (e.g. their loads) completes here,
+// once and outside any branch.  Without it, a first use inside a branch that may be skipped makes
+// the wait-count pass (whose state merges conservatively at join points) wait for every later load.
+__device__ __forceinline__ void ready(const float4& v) { asm volatile("" ::"v"(v.x), "v"(v.y), "v"(v.z), "v"(v.w)); }
+__device__ __forceinline__ void ready(uint32_t v) { asm volatile("" ::"v"(v)); }
+// Copy a (uniform) value into a VGPR, so it is not rematerialized from memory inside a loop.
+__device__ __forceinline__ int vgpr(int x) {
+    int v;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(v) : "s"(x));
+    return v;
+}
+__device__ __forceinline__ float vgpr_f(float x) { return __int_as_float(vgpr(__float_as_int(x))); }
+
 // Producer side: one slab = rows [in0, in0 + tw) x channels [c0, c0 + 64) of the input.  Producer
-// thread pt owns channel octet q = (pt % 8) * 8 of rows pt / 8 + j * RP (j < RB).  load() issues the
-// global loads into registers; convert() applies the prologue and writes bf16 rows into an LDS
-// buffer.  Rows outside the unit's item, and channels >= cin, are staged as 0 (the conv's zero
-// padding of the activated signal).
+// thread pt owns channel quad q = (pt % 16) * 4 of rows pt / 16 + j * RP (j < RB).  A Slot holds one
+// slab's raw input and the per-channel prologue constants in registers; load() issues every global
+// load of the slab (addresses outside the unit's item are clamped to a row of the item, so the
+// number of loads is fixed and the producers' wait counts are static), convert() applies the
+// prologue and writes bf16 rows into an LDS buffer.  Rows outside the item, and channels >= cin,
+// are staged as 0 (the conv's zero padding of the activated signal).
 template <int PRO, bool IN_H, int BN>
-struct Stager {
-    static constexpr int RP = kNP / 8;                        // rows per pass
+struct Slot {
+    static constexpr int RP = kNP / 16;                       // rows per pass
     static constexpr int RB = (BN + kMaxHalo + RP - 1) / RP;  // passes
-    static constexpr bool WIDE = PRO != PRO_BF16 && !IN_H;    // f32 source: 8 dwords per octet
-    static constexpr int NW = WIDE ? 8 : 4;
+    static constexpr bool WIDE = PRO != PRO_BF16 && !IN_H;    // f32 source: 4 dwords per quad
+    static constexpr int NW = WIDE ? 4 : 2;
+    static constexpr bool ADAIN = PRO == PRO_ADAIN_LEAKY || PRO == PRO_ADAIN_SNAKE;
+    static constexpr bool SNAKE = PRO == PRO_ADAIN_SNAKE;
     uint32_t raw[RB][NW];
+    float4 k01, k23;  // AdaIN coefficients (sc, sh) of channels c..c+1 and c+2..c+3
+    float4 ar, ai;    // Snake alpha / (2 pi) and 1 / alpha
 
     __device__ __forceinline__ static bool live(const ConvParams& p, const Unit& u, int r, int tw, int c) {
         const int row = u.in0 + r;
@@ -87,92 +113,84 @@ struct Stager {
 
     __device__ __forceinline__ void load(const ConvParams& p, const Unit& u, int c0, int tw, int q, int rr) {
         const int c = c0 + q;
+        const int cl = c < p.cin ? c : 0;
 #pragma unroll
         for (int j = 0; j < RB; j++) {
             const int r = rr + j * RP;
-#pragma unroll
-            for (int e = 0; e < NW; e++) raw[j][e] = 0u;
-            if (live(p, u, r, tw, c)) {
-                const int64_t row = u.in0 + r;
-                if constexpr (WIDE) {
-                    const uint4* xp = (const uint4*)((const float*)p.x + row * p.x_ld + c);
-                    const uint4 x0 = xp[0], x1 = xp[1];
-                    raw[j][0] = x0.x, raw[j][1] = x0.y, raw[j][2] = x0.z, raw[j][3] = x0.w;
-                    raw[j][4] = x1.x, raw[j][5] = x1.y, raw[j][6] = x1.z, raw[j][7] = x1.w;
-                } else {
-                    const uint4 h = *(const uint4*)((const uint16_t*)p.x + row * p.x_ld + c);
-                    raw[j][0] = h.x, raw[j][1] = h.y, raw[j][2] = h.z, raw[j][3] = h.w;
-                }
+            const int64_t row = live(p, u, r, tw, c) ? u.in0 + r : u.i_lo;
+            if constexpr (WIDE) {
+                const uint4 x = *(const uint4*)((const float*)p.x + row * p.x_ld + cl);
+                raw[j][0] = x.x, raw[j][1] = x.y, raw[j][2] = x.z, raw[j][3] = x.w;
+            } else {
+                const uint2 h = *(const uint2*)((const uint16_t*)p.x + row * p.x_ld + cl);
+                raw[j][0] = h.x, raw[j][1] = h.y;
             }
+        }
+        if constexpr (ADAIN) {
+            const float4* kp = (const float4*)(p.coef + (int64_t)u.item * p.cin + cl);
+            k01 = kp[0], k23 = kp[1];
+        }
+        if constexpr (SNAKE) {
+            ar = *(const float4*)(p.alpha_rev + cl);
+            ai = *(const float4*)(p.alpha_inv + cl);
         }
     }
 
     __device__ __forceinline__ void convert(const ConvParams& p, uint16_t* xs, const Unit& u, int c0, int tw, int q,
                                             int rr) const {
         const int c = c0 + q;
-        if constexpr (PRO == PRO_BF16) {
-            // bf16 input: channels >= cin of the source buffer hold 0
 #pragma unroll
-            for (int j = 0; j < RB; j++) {
-                const int r = rr + j * RP;
-                if (r < tw) *(uint4*)(xs + r * kRS + q) = make_uint4(raw[j][0], raw[j][1], raw[j][2], raw[j][3]);
-            }
-            return;
-        } else {
-            // per-thread constants: AdaIN coefficients of the unit's item, Snake alphas
-            float sc[8], sh[8], ar[8], ai[8];
+        for (int j = 0; j < RB; j++)
 #pragma unroll
-            for (int e = 0; e < 8; e++) {
-                const bool in = c + e < p.cin;
-                sc[e] = 1.f, sh[e] = 0.f, ar[e] = 0.f, ai[e] = 0.f;
-                if constexpr (PRO == PRO_ADAIN_LEAKY || PRO == PRO_ADAIN_SNAKE) {
-                    if (in) {
-                        const Coef k = p.coef[(int64_t)u.item * p.cin + c + e];
-                        sc[e] = k.sc, sh[e] = k.sh;
-                    }
-                }
-                if constexpr (PRO == PRO_ADAIN_SNAKE) {
-                    if (in) ar[e] = p.alpha_rev[c + e], ai[e] = p.alpha_inv[c + e];
-                }
-            }
+            for (int e = 0; e < NW; e++) ready(raw[j][e]);
+        if constexpr (ADAIN) ready(k01), ready(k23);
+        if constexpr (SNAKE) ready(ar), ready(ai);
+        const float sc[4] = {k01.x, k01.z, k23.x, k23.z}, sh[4] = {k01.y, k01.w, k23.y, k23.w};
+        const float arv[4] = {ar.x, ar.y, ar.z, ar.w}, aiv[4] = {ai.x, ai.y, ai.z, ai.w};
+        // Per-slab limits, held in VGPRs for the whole loop (the kernel is short of SGPRs, and a
+        // limit rematerialized from the kernel arguments costs a scalar load and a wait per row):
+        // live rows r in [r_lo, r_hi), live channels e < n_ch of this quad.
+        const int r_lo = vgpr(u.i_lo - u.in0), r_hi = vgpr(min(tw, u.i_hi - u.in0)), n_ch = p.cin - c;
+        const float slope = vgpr_f(p.slope);
 #pragma unroll
-            for (int j = 0; j < RB; j++) {
-                const int r = rr + j * RP;
-                if (r >= tw) break;
-                uint4 out = make_uint4(0, 0, 0, 0);
-                if (live(p, u, r, tw, c)) {
-                    float v[8];
+        for (int j = 0; j < RB; j++) {
+            const int r = rr + j * RP;
+            if (r >= tw) break;
+            uint2 out = make_uint2(0, 0);
+            if (r >= r_lo && r < r_hi && n_ch > 0) {
+                if constexpr (PRO == PRO_BF16) {
+                    out = make_uint2(raw[j][0], raw[j][1]);  // bf16 input: channels >= cin hold 0
+                } else {
+                    float v[4];
                     if constexpr (WIDE) {
 #pragma unroll
-                        for (int e = 0; e < 8; e++) v[e] = __uint_as_float(raw[j][e]);
+                        for (int e = 0; e < 4; e++) v[e] = __uint_as_float(raw[j][e]);
                     } else {
 #pragma unroll
-                        for (int e = 0; e < 4; e++) {
+                        for (int e = 0; e < 2; e++) {
                             v[2 * e] = (float)__builtin_bit_cast(_Float16, (uint16_t)(raw[j][e] & 0xffffu));
                             v[2 * e + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(raw[j][e] >> 16));
                         }
                     }
-                    float w[8];
+                    float w[4];
 #pragma unroll
-                    for (int e = 0; e < 8; e++) {
+                    for (int e = 0; e < 4; e++) {
                         float x = v[e];
                         if constexpr (PRO == PRO_LEAKY) {
-                            x = x < 0.f ? x * p.slope : x;
+                            x = x < 0.f ? x * slope : x;
                         } else if constexpr (PRO == PRO_ADAIN_LEAKY) {
                             x = __builtin_fmaf(x, sc[e], sh[e]);
-                            x = x < 0.f ? x * p.slope : x;
+                            x = x < 0.f ? x * slope : x;
                         } else if constexpr (PRO == PRO_ADAIN_SNAKE) {
-                            x = snake(__builtin_fmaf(x, sc[e], sh[e]), ar[e], ai[e]);
+                            x = snake(__builtin_fmaf(x, sc[e], sh[e]), arv[e], aiv[e]);
                         }
-                        w[e] = c + e < p.cin ? x : 0.f;
+                        w[e] = e < n_ch ? x : 0.f;
                     }
                     out.x = pack_bf16x2(w[0], w[1]);
                     out.y = pack_bf16x2(w[2], w[3]);
-                    out.z = pack_bf16x2(w[4], w[5]);
-                    out.w = pack_bf16x2(w[6], w[7]);
                 }
-                *(uint4*)(xs + r * kRS + q) = out;
             }
+            *(uint2*)(xs + r * kRS + q) = out;
         }
     }
 };
@@ -272,7 +290,10 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
     const int m = u.m0 + wm * 64 + 4 * cq;     // this lane's 4 output rows after the transpose
     const bool mok = m < p.m;
     float4 b = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (!CONVT && p.bias && mok) b = *(const float4*)(p.bias + m);
+    if (!CONVT && p.bias) b = *(const float4*)(p.bias + (mok ? m : 0));
+    // Consume the loaded values once, outside any branch: stores issued later then never make the
+    // wait-count pass wait for them again (its state merges conservatively after skipped branches).
+    ready(b);
     float s1[4] = {0.f, 0.f, 0.f, 0.f}, s2[4] = {0.f, 0.f, 0.f, 0.f}, sft[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < 4; j++) {
@@ -282,20 +303,21 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
             for (int g = 0; g < 4; g++)
                 *(float4*)(scr + l32 * kScrLd + i * 32 + 8 * g + 4 * lh) =
                     make_float4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]);
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        __builtin_amdgcn_wave_barrier();  // LDS operations of one wave execute in order
 #pragma unroll
         for (int q0 = 0; q0 < 8; q0 += QB) {
             float4 res[QB][NRA];
             if constexpr (NR > 0) {
+                // unconditional loads (invalid columns / rows read column 0 / row 0 of the tile)
 #pragma unroll
                 for (int qq = 0; qq < QB; qq++) {
                     const int col = wcol0 + j * 32 + 4 * (q0 + qq) + cg;
-#pragma unroll
-                    for (int e = 0; e < NRA; e++) res[qq][e] = make_float4(0.f, 0.f, 0.f, 0.f);
-                    if (col < u.nv && mok) load_res<EPI>(p, u.n0 + col, m, res[qq]);
+                    load_res<EPI>(p, u.n0 + (col < u.nv ? col : 0), mok ? m : u.m0, res[qq]);
                 }
+#pragma unroll
+                for (int qq = 0; qq < QB; qq++)
+#pragma unroll
+                    for (int e = 0; e < NRA; e++) ready(res[qq][e]);
             }
 #pragma unroll
             for (int qq = 0; qq < QB; qq++) {
@@ -324,9 +346,7 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
                 }
             }
         }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        __builtin_amdgcn_wave_barrier();  // LDS operations of one wave execute in order
     }
     if constexpr (STATS) {
 #pragma unroll
@@ -370,11 +390,11 @@ __global__ __launch_bounds__(64 * WM * WN + kNP) void conv_mfma_kernel(ConvParam
         u.tile = g * 8 + (within & 7);
         if (u.tile >= p.tiles.count) return false;
         u.m0 = (within >> 3) * BM;
-        u.item = p.tiles.item[u.tile];
-        u.n0 = (int)p.tiles.t0[u.tile];
-        u.nv = p.tiles.n[u.tile];
-        u.i_lo = (int)p.in_start[u.item];
-        u.i_hi = u.i_lo + (int)p.in_len[u.item];
+        u.item = ld_const(p.tiles.item, u.tile);
+        u.n0 = (int)ld_const(p.tiles.t0, u.tile);
+        u.nv = ld_const(p.tiles.n, u.tile);
+        u.i_lo = (int)ld_const(p.in_start, u.item);
+        u.i_hi = u.i_lo + (int)ld_const(p.in_len, u.item);
         u.in0 = u.n0 - p.pad;
         return true;
     };
@@ -391,32 +411,58 @@ __global__ __launch_bounds__(64 * WM * WN + kNP) void conv_mfma_kernel(ConvParam
 
     if (threadIdx.x >= NC) {
         // ------------------------------------------------------------ producer waves
+        // Two register slots: the loads of step n + 2 are in flight while step n + 1 is converted.
+        // Every load is issued unconditionally (past the last step the load iterator repeats its
+        // last unit), so the number of loads in flight is the same at every wait.
         const int pt = threadIdx.x - NC;
-        const int q = (pt & 7) * 8, rr = pt >> 3;
-        Stager<PRO, IN_H, BN> st;
-        int U = blockIdx.x, sl = 0;  // iterator over (unit, slab) steps
-        Unit u;
-        unit_at(U, u);
-        auto advance = [&]() {
-            if (++sl == nsl) {
-                sl = 0;
-                U += gridDim.x;
-                unit_at(U, u);
+        const int q = (pt & 15) * 4, rr = pt >> 4;
+        Slot<PRO, IN_H, BN> s0, s1;
+        // iterators over (unit, slab) steps: load and convert
+        int lU = blockIdx.x, ls = 0, cU = blockIdx.x, cs = 0;
+        Unit lu, cuv;
+        unit_at(lU, lu);
+        cuv = lu;
+        auto adv_l = [&]() {
+            if (++ls == nsl) {
+                Unit t;
+                ls = 0;
+                lU += gridDim.x;
+                if (unit_at(lU, t)) lu = t;
             }
         };
-        st.load(p, u, 0, tw, q, rr);
-        st.convert(p, xs, u, 0, tw, q, rr);
-        advance();
-        if (G > 1) st.load(p, u, sl * kCK, tw, q, rr);
-        __syncthreads();
-        for (int g = 0; g < G; g++) {
-            // the iterator is at step g + 1: convert it (its loads were issued during step g - 1),
-            // then issue the loads of step g + 2
-            if (g + 1 < G) {
-                st.convert(p, xs + ((g + 1) & 1) * slab_elems, u, sl * kCK, tw, q, rr);
-                advance();
-                if (g + 2 < G) st.load(p, u, sl * kCK, tw, q, rr);
+        auto adv_c = [&]() {
+            if (++cs == nsl) {
+                cs = 0;
+                cU += gridDim.x;
+                unit_at(cU, cuv);
             }
+        };
+        s0.load(p, lu, ls * kCK, tw, q, rr);
+        adv_l();
+        s1.load(p, lu, ls * kCK, tw, q, rr);
+        adv_l();
+        s0.convert(p, xs, cuv, cs * kCK, tw, q, rr);
+        adv_c();
+        s0.load(p, lu, ls * kCK, tw, q, rr);
+        adv_l();
+        __syncthreads();
+        for (int g = 0; g < G; g += 2) {
+            // step g: convert step g + 1 (slot 1), then load step g + 3 into slot 1
+            if (g + 1 < G) {
+                s1.convert(p, xs + slab_elems, cuv, cs * kCK, tw, q, rr);
+                adv_c();
+            }
+            s1.load(p, lu, ls * kCK, tw, q, rr);
+            adv_l();
+            __syncthreads();
+            if (g + 1 >= G) break;
+            // step g + 1: convert step g + 2 (slot 0), then load step g + 4 into slot 0
+            if (g + 2 < G) {
+                s0.convert(p, xs, cuv, cs * kCK, tw, q, rr);
+                adv_c();
+            }
+            s0.load(p, lu, ls * kCK, tw, q, rr);
+            adv_l();
             __syncthreads();
         }
         return;
@@ -477,12 +523,12 @@ __global__ __launch_bounds__(64 * WM * WN + kNP) void conv_mfma_kernel(ConvParam
         read_b(B0, buf, 0, 0);
         for (int kk = 0; kk < p.k; kk++) {
             // the tap after this one: same slab, first tap of the next slab, or of the next unit
+            // (the very last tap reloads tap 0 of this slab: a harmless load keeps the count static)
             int n_m0 = cu.m0, n_kk = kk + 1, n_c16 = 4 * sl;
-            bool have = true;
             if (kk + 1 == p.k) {
-                if (!last) n_kk = 0, n_c16 = 4 * sl + 4;
-                else if (has_next) n_m0 = nu.m0, n_kk = 0, n_c16 = 0;
-                else have = false;
+                n_kk = 0;
+                if (!last) n_c16 = 4 * sl + 4;
+                else if (has_next) n_m0 = nu.m0, n_c16 = 0;
             }
 #pragma unroll
             for (int kc = 0; kc < 4; kc++) {
@@ -493,7 +539,7 @@ __global__ __launch_bounds__(64 * WM * WN + kNP) void conv_mfma_kernel(ConvParam
                 __builtin_amdgcn_sched_barrier(0);
                 mfma_step(A[kc], bc);
                 __builtin_amdgcn_sched_barrier(0);
-                if (have) load_a(A[kc], n_m0, n_kk, n_c16 + kc);
+                load_a(A[kc], n_m0, n_kk, n_c16 + kc);
             }
         }
         if (last) epilogue<EPI, WM, WN, STATS, OUT_H>(p, cu, acc, wm, wn, lane, scr);
