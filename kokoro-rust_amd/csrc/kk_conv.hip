@@ -356,11 +356,13 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
             s1[r] += __shfl_xor(s1[r], 32, 64);
             s2[r] += __shfl_xor(s2[r], 32, 64);
         }
-        if (cg == 0 && wcol0 < u.nv) {
+        // every wave writes its record, an empty one (n = 0) when the tile ends before its columns
+        if (cg == 0) {
             StatPart* dst = p.part + ((int64_t)u.tile * WN + wn) * p.cout;
+            const float nc = (float)max(min(u.nv - wcol0, 128), 0);
 #pragma unroll
             for (int r = 0; r < 4; r++)
-                if (m + r < p.cout) dst[m + r] = StatPart{s1[r], s2[r], sft[r]};
+                if (m + r < p.cout) dst[m + r] = nc > 0.f ? StatPart{s1[r], s2[r], sft[r], nc} : StatPart{0.f, 0.f, 0.f, 0.f};
         }
     }
 #pragma unroll

@@ -321,7 +321,14 @@ static void load_model(kk_ctx* ctx, const kk_tensor* tensors, int n) {
         const std::string p = g + ".noise_convs." + std::to_string(i);
         MNoiseConv& c = m.nc[i];
         c.cout = nc_cout[i], c.k = nc_k[i], c.stride = nc_s[i], c.pad = nc_p[i];
-        c.w.upload(t.get(p + ".weight", (int64_t)c.cout * 22 * c.k), (size_t)c.cout * 22 * c.k);
+        // transposed to [k][22][cout] (one coalesced float4 per 4 output channels in the kernel)
+        const float* w = t.get(p + ".weight", (int64_t)c.cout * 22 * c.k);
+        std::vector<float> wt((size_t)c.cout * 22 * c.k);
+        for (int co = 0; co < c.cout; co++)
+            for (int ci = 0; ci < 22; ci++)
+                for (int kk = 0; kk < c.k; kk++)
+                    wt[((size_t)kk * 22 + ci) * c.cout + co] = w[((size_t)co * 22 + ci) * c.k + kk];
+        c.w.upload(wt);
         c.b.upload(t.get(p + ".bias", c.cout), c.cout);
     }
     load_snake(m.noise_res[0], t, g + ".noise_res.0", 256, 7, sr);
@@ -779,13 +786,13 @@ struct Runner {
         return t;
     }
     // Partials -> coefficients of AdaIN layer a.
-    void fin(const Tiles& t, int wn, int wcols, int c, const MAdain& a, Coef* coef) {
-        KK_LAUNCH(launch_finalize(p->part.as<StatPart>(), c, wn, wcols, t.dev(), p->nb, p->gb.as<float>(), gb_ld(),
+    void fin(const Tiles& t, int wn, int c, const MAdain& a, Coef* coef) {
+        KK_LAUNCH(launch_finalize(p->part.as<StatPart>(), c, wn, t.dev(), p->nb, p->gb.as<float>(), gb_ld(),
                                a.gb_off, a.nw.as<float>(), a.nb.as<float>(), coef, s));
         launches++;
     }
     void stats_fin(const float* x, int64_t ld, int c, const Dom& d, const MAdain& a, Coef* coef) {
-        fin(stats(x, ld, c, d), 1, kStatTile, c, a, coef);
+        fin(stats(x, ld, c, d), 1, c, a, coef);
     }
 
     // One MFMA conv launch.
@@ -868,9 +875,9 @@ struct Runner {
         stats_fin(X, c, c, d, blk.a1[0], cf(0));
         for (int i = 0; i < 3; i++) {
             const Tiles& t = conv(blk.c1[i], snake_op(blk, d, X, h, EPI_STORE, cf(0), i, false, true));
-            fin(t, wn, 128, c, blk.a2[i], cf(1));
+            fin(t, wn, c, blk.a2[i], cf(1));
             conv(blk.c2[i], snake_op(blk, d, h, X, EPI_ACCUM, cf(1), i, true, i < 2));
-            if (i < 2) fin(t, wn, 128, c, blk.a1[i + 1], cf(0));
+            if (i < 2) fin(t, wn, c, blk.a1[i + 1], cf(0));
         }
     }
 
@@ -879,19 +886,19 @@ struct Runner {
         const int c = rbs[0].c, wn = kShapeWN[rbs[0].c1[0].shape];
         // the three blocks' first AdaIN share one statistics pass over y
         const Tiles& ts = stats(y, c, c, d);
-        for (int j = 0; j < 3; j++) fin(ts, 1, kStatTile, c, rbs[j].a1[0], cf(2 + j));
+        for (int j = 0; j < 3; j++) fin(ts, 1, c, rbs[j].a1[0], cf(2 + j));
         for (int j = 0; j < 3; j++) {
             const MSnake& blk = rbs[j];
             for (int i = 0; i < 3; i++) {
                 const float* in = i == 0 ? y : X[j];
                 const Tiles& t =
                     conv(blk.c1[i], snake_op(blk, d, in, h, EPI_STORE, i == 0 ? cf(2 + j) : cf(0), i, false, true));
-                fin(t, wn, 128, c, blk.a2[i], cf(1));
+                fin(t, wn, c, blk.a2[i], cf(1));
                 Op o2 = snake_op(blk, d, h, X[j], EPI_ACCUM, cf(1), i, true, i < 2);
                 if (i == 0) o2.epi = EPI_ADD_FROM, o2.r0 = y, o2.r0_ld = c;
                 if (j == 2 && i == 2) o2.epi = EPI_MEAN3, o2.r0 = X[0], o2.r1 = X[1], o2.r2 = X[2], o2.r0_ld = c;
                 conv(blk.c2[i], o2);
-                if (i < 2) fin(t, wn, 128, c, blk.a1[i + 1], cf(0));
+                if (i < 2) fin(t, wn, c, blk.a1[i + 1], cf(0));
             }
         }
     }
@@ -905,7 +912,7 @@ struct Runner {
         o1.pro = PRO_ADAIN_LEAKY, o1.x = in, o1.x_ld = in_ld, o1.din = o1.dout = &d, o1.y = h, o1.y_ld = r.dout;
         o1.coef = cf(0), o1.slope = 0.2f, o1.stats = true;
         const Tiles& t = conv(r.conv1, o1);
-        fin(t, kShapeWN[r.conv1.shape], 128, r.dout, r.n2, cf(1));
+        fin(t, kShapeWN[r.conv1.shape], r.dout, r.n2, cf(1));
         Op os;
         os.x = in, os.x_ld = in_ld, os.din = os.dout = &d, os.y = out, os.y_ld = out_ld;
         conv(r.conv1x1, os);
@@ -950,7 +957,7 @@ struct Runner {
         o1.pro = PRO_BF16, o1.x = p->pool.p, o1.x_ld = kXinLd, o1.din = o1.dout = &d2, o1.y = h, o1.y_ld = 512;
         o1.stats = true;
         const Tiles& t = conv(r.conv1, o1);
-        fin(t, kShapeWN[r.conv1.shape], 128, 512, r.n2, cf(1));
+        fin(t, kShapeWN[r.conv1.shape], 512, r.n2, cf(1));
         // shortcut conv1x1(nearest x2 (x)) = nearest x2 (conv1x1(x)) for a 1x1 conv: computed at N
         Op os;
         os.x = xb, os.x_ld = kXinLd, os.din = os.dout = &dn, os.y = p->sc_half.as<float>(), os.y_ld = 512;

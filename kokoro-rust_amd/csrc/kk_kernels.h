@@ -20,8 +20,8 @@ struct TilesDev {
 
 // Per-(partial, channel) statistics record: sums of (v - shift) and (v - shift)^2 over n columns,
 // shift = the first of those columns' value (exact local centring; Chan's combination in finalize).
-struct StatPart {
-    float s1, s2, shift;
+struct __align__(16) StatPart {
+    float s1, s2, shift, n;
 };
 
 // ---------------------------------------------------------------- MFMA convolution
@@ -90,9 +90,9 @@ hipError_t launch_conv(const ConvParams& p, int pro, int epi, int shape, bool st
 // Statistics partials of x [l][ld] over tiles (one partial per tile and channel).
 hipError_t launch_stats_tiles(const float* x, int64_t ld, int c, TilesDev t, StatPart* part, hipStream_t s);
 // Partials -> per-(item, channel) mean / rstd (chan_stats_seg semantics) -> AdaIN coefficients.
-// `wn` partials per tile; partial (tile, w) covers columns [w*wcols, (w+1)*wcols) of the tile.
-hipError_t launch_finalize(const StatPart* part, int c, int wn, int wcols, TilesDev t, int nb, const float* gb,
-                           int64_t gb_ld, int gb_off, const float* nw, const float* nb_, Coef* coef, hipStream_t s);
+// `wn` partials per tile (records [tile * wn + w][c]).
+hipError_t launch_finalize(const StatPart* part, int c, int wn, TilesDev t, int nb, const float* gb, int64_t gb_ld,
+                           int gb_off, const float* nw, const float* nb_, Coef* coef, hipStream_t s);
 // gb[b][j] = W[j] . style[b] + bias[j] for every AdaIN layer at once.
 hipError_t launch_style_fc(const float* w, const float* bias, int rows, const float* style, int nb, float* gb,
                            hipStream_t s);
@@ -110,9 +110,10 @@ hipError_t launch_copy_cols(const float* src, int64_t src_ld, int c, float* dst,
 hipError_t launch_adain_pool(const float* x, int64_t ld, int c, const Coef* coef, const int32_t* col_n,
                              int64_t ln, const float* pw, const float* pb, const int32_t* col_2, uint16_t* out,
                              int64_t out_ld, hipStream_t s);
-// Strided f32 conv 22 -> cout (noise_convs.0: k12 s6 p3; noise_convs.1: k1) on the masked spectrum.
+// Strided f32 conv 22 -> cout (noise_convs.0: k12 s6 p3; noise_convs.1: k1) on the masked spectrum;
+// wt is the weight transposed to [k][22][cout], cout 128 or 256.
 hipError_t launch_noise_conv(const float* spec, int64_t spec_ld, int64_t l_in, const int32_t* col_in,
-                             const float* w, const float* b, int cout, int k, int stride, int pad, float* y,
+                             const float* wt, const float* b, int cout, int k, int stride, int pad, float* y,
                              int64_t y_ld, int64_t l_out, hipStream_t s);
 // SineGen phase_pre: per item and harmonic, f64 cumulative sum of the 1/300-downsampled rad values.
 hipError_t launch_phase_pre(const float* f0, const int64_t* start2, const int64_t* len2, int nb,

@@ -45,7 +45,7 @@ __global__ __launch_bounds__(256) void stats_tiles_kernel(const float* __restric
     if (g == 0 && ch < c) {
         s1 = ((sa[0][lane] + sa[1][lane]) + sa[2][lane]) + sa[3][lane];
         s2 = ((sb[0][lane] + sb[1][lane]) + sb[2][lane]) + sb[3][lane];
-        part[tile * c + ch] = StatPart{s1, s2, shift};
+        part[tile * c + ch] = StatPart{s1, s2, shift, (float)n};
     }
 }
 
@@ -57,30 +57,35 @@ __global__ __launch_bounds__(256) void stats_tiles_kernel(const float* __restric
 // E[d^2] - E[d]^2 cancels only over a few standard deviations.  16 threads per (item, channel)
 // reduce in a fixed tree: deterministic, no atomics.
 constexpr int kFinSub = 16;
-__global__ __launch_bounds__(256) void finalize_kernel(const StatPart* __restrict__ part, int c, int wn, int wcols,
-                                                       TilesDev t, const float* __restrict__ gb, int64_t gb_ld,
-                                                       int gb_off, const float* __restrict__ nw,
-                                                       const float* __restrict__ nbias, Coef* __restrict__ coef) {
+__global__ __launch_bounds__(256) void finalize_kernel(const StatPart* __restrict__ part, int c, int wn, TilesDev t,
+                                                       const float* __restrict__ gb, int64_t gb_ld, int gb_off,
+                                                       const float* __restrict__ nw, const float* __restrict__ nbias,
+                                                       Coef* __restrict__ coef) {
     __shared__ double sa[kFinSub][16], sb[kFinSub][16], sn[kFinSub][16];
     const int cl = threadIdx.x & 15, sub = threadIdx.x >> 4;
     const int b = blockIdx.x;
     const int ch = blockIdx.y * 16 + cl;
     const int64_t lo = (int64_t)t.lo[b] * wn, hi = (int64_t)t.hi[b] * wn;
     double a1 = 0.0, a2 = 0.0, n = 0.0, ref = 0.0;
-    if (ch < c && lo < hi) {
-        ref = (double)part[lo * c + ch].shift;
-        for (int64_t pi = lo + sub; pi < hi; pi += kFinSub) {
-            const int64_t tile = pi / wn;
-            const int w = (int)(pi - tile * wn);
-            const int nt = min(max(t.n[tile] - w * wcols, 0), wcols);
-            if (nt <= 0) continue;
-            const StatPart q = part[pi * c + ch];
-            const double dn = (double)nt, d = (double)q.shift - ref, s1 = (double)q.s1;
+    auto add = [&](const StatPart& q) {
+        if (q.n > 0.f) {
+            const double dn = (double)q.n, d = (double)q.shift - ref, s1 = (double)q.s1;
             // sums of (v - ref) and (v - ref)^2 over the partial's columns
             a1 += s1 + dn * d;
             a2 += (double)q.s2 + 2.0 * d * s1 + dn * d * d;
             n += dn;
         }
+    };
+    if (ch < c && lo < hi) {
+        ref = (double)part[lo * c + ch].shift;
+        // partials lo + sub, lo + sub + 16, ... in increasing order, four loads in flight
+        int64_t pi = lo + sub;
+        for (; pi + 3 * kFinSub < hi; pi += 4 * kFinSub) {
+            const StatPart q0 = part[pi * c + ch], q1 = part[(pi + kFinSub) * c + ch];
+            const StatPart q2 = part[(pi + 2 * kFinSub) * c + ch], q3 = part[(pi + 3 * kFinSub) * c + ch];
+            add(q0), add(q1), add(q2), add(q3);
+        }
+        for (; pi < hi; pi += kFinSub) add(part[pi * c + ch]);
     }
     sa[sub][cl] = a1, sb[sub][cl] = a2, sn[sub][cl] = n;
     __syncthreads();
@@ -214,14 +219,22 @@ __global__ void adain_pool_kernel(const float* __restrict__ x, int64_t ld, int c
 // ------------------------------------------------------------------ noise convolutions (f32)
 // conv1d_strided / conv_direct_tiled semantics (kernels/kokoro.cu:517-617): y = b + sum_k sum_ci
 // w x with the spectrum's gap rows zeroed first (src/gpu_batch.rs:363-365).  A block computes
-// kNcRows output rows x all output channels (one channel per thread); the input window sits in LDS.
-constexpr int kNcRows = 32;
+// noise_convs (22 -> COUT channels, f32 like the reference's sgemm route).  A block computes 64
+// output rows x COUT channels; thread = 4 consecutive channels x TT rows, so every weight load is
+// one coalesced float4 across the wave and every input value is a wave-uniform LDS broadcast.
+// Weights are pre-transposed to [k][22][COUT].  Accumulation order per output: bias, then taps
+// ascending, channels ascending within a tap (f32 FMA).
+constexpr int kNcRows = 64;
+constexpr int kNcMaxWin = (kNcRows - 1) * 6 + 12;
+template <int COUT, int TT>
 __global__ __launch_bounds__(256) void noise_conv_kernel(const float* __restrict__ spec, int64_t spec_ld, int64_t l_in,
                                                          const int32_t* __restrict__ col_in,
-                                                         const float* __restrict__ w, const float* __restrict__ b,
-                                                         int cout, int k, int stride, int pad, float* __restrict__ y,
+                                                         const float* __restrict__ wt, const float* __restrict__ b,
+                                                         int k, int stride, int pad, float* __restrict__ y,
                                                          int64_t y_ld, int64_t l_out) {
-    __shared__ float xs[(kNcRows - 1) * 6 + 12][22];
+    constexpr int CQ = COUT / 4, TG = 256 / CQ;
+    static_assert(TG * TT == kNcRows, "rows per block");
+    __shared__ float xs[kNcMaxWin][22];
     const int64_t t0 = (int64_t)blockIdx.x * kNcRows;
     const int win = (kNcRows - 1) * stride + k;
     const int64_t in0 = t0 * stride - pad;
@@ -233,21 +246,30 @@ __global__ __launch_bounds__(256) void noise_conv_kernel(const float* __restrict
         xs[r][ci] = v;
     }
     __syncthreads();
-    const int co = threadIdx.x;
-    if (co >= cout) return;
-    const int nrows = (int)min((int64_t)kNcRows, l_out - t0);
-    float acc[kNcRows];
-    const float bias = b[co];
+    const int cq = threadIdx.x % CQ, tg = threadIdx.x / CQ;
+    const float4 bias = *(const float4*)(b + cq * 4);
+    float4 acc[TT];
 #pragma unroll
-    for (int r = 0; r < kNcRows; r++) acc[r] = bias;
+    for (int tt = 0; tt < TT; tt++) acc[tt] = bias;
+    const int rb = tg * TT * stride;
     for (int kk = 0; kk < k; kk++) {
         for (int ci = 0; ci < 22; ci++) {
-            const float wv = w[((int64_t)co * 22 + ci) * k + kk];
+            const float4 wv = *(const float4*)(wt + ((int64_t)kk * 22 + ci) * COUT + cq * 4);
 #pragma unroll
-            for (int r = 0; r < kNcRows; r++) acc[r] = __builtin_fmaf(wv, xs[r * stride + kk][ci], acc[r]);
+            for (int tt = 0; tt < TT; tt++) {
+                const float x = xs[rb + tt * stride + kk][ci];
+                acc[tt].x = __builtin_fmaf(wv.x, x, acc[tt].x);
+                acc[tt].y = __builtin_fmaf(wv.y, x, acc[tt].y);
+                acc[tt].z = __builtin_fmaf(wv.z, x, acc[tt].z);
+                acc[tt].w = __builtin_fmaf(wv.w, x, acc[tt].w);
+            }
         }
     }
-    for (int r = 0; r < nrows; r++) y[(t0 + r) * y_ld + co] = acc[r];
+#pragma unroll
+    for (int tt = 0; tt < TT; tt++) {
+        const int64_t row = t0 + tg * TT + tt;
+        if (row < l_out) *(float4*)(y + row * y_ld + cq * 4) = acc[tt];
+    }
 }
 
 // ------------------------------------------------------------------ SineGen (kernels/kokoro.cu:188-254)
@@ -498,10 +520,10 @@ hipError_t launch_stats_tiles(const float* x, int64_t ld, int c, TilesDev t, Sta
     return hipGetLastError();
 }
 
-hipError_t launch_finalize(const StatPart* part, int c, int wn, int wcols, TilesDev t, int nb, const float* gb,
-                           int64_t gb_ld, int gb_off, const float* nw, const float* nb_, Coef* coef, hipStream_t s) {
+hipError_t launch_finalize(const StatPart* part, int c, int wn, TilesDev t, int nb, const float* gb, int64_t gb_ld,
+                           int gb_off, const float* nw, const float* nb_, Coef* coef, hipStream_t s) {
     dim3 grid((unsigned)nb, (unsigned)ceil_div(c, 16));
-    hipLaunchKernelGGL(finalize_kernel, grid, dim3(256), 0, s, part, c, wn, wcols, t, gb, gb_ld, gb_off, nw, nb_, coef);
+    hipLaunchKernelGGL(finalize_kernel, grid, dim3(256), 0, s, part, c, wn, t, gb, gb_ld, gb_off, nw, nb_, coef);
     return hipGetLastError();
 }
 
@@ -541,12 +563,19 @@ hipError_t launch_adain_pool(const float* x, int64_t ld, int c, const Coef* coef
     return hipGetLastError();
 }
 
-hipError_t launch_noise_conv(const float* spec, int64_t spec_ld, int64_t l_in, const int32_t* col_in, const float* w,
+hipError_t launch_noise_conv(const float* spec, int64_t spec_ld, int64_t l_in, const int32_t* col_in, const float* wt,
                              const float* b, int cout, int k, int stride, int pad, float* y, int64_t y_ld,
                              int64_t l_out, hipStream_t s) {
-    if (cout > 256 || (kNcRows - 1) * stride + k > (kNcRows - 1) * 6 + 12) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(noise_conv_kernel, dim3(blocks_for(l_out, kNcRows)), dim3(256), 0, s, spec, spec_ld, l_in,
-                       col_in, w, b, cout, k, stride, pad, y, y_ld, l_out);
+    if ((kNcRows - 1) * stride + k > kNcMaxWin) return hipErrorInvalidValue;
+    const dim3 grid(blocks_for(l_out, kNcRows));
+    if (cout == 256)
+        hipLaunchKernelGGL((noise_conv_kernel<256, 16>), grid, dim3(256), 0, s, spec, spec_ld, l_in, col_in, wt, b, k,
+                           stride, pad, y, y_ld, l_out);
+    else if (cout == 128)
+        hipLaunchKernelGGL((noise_conv_kernel<128, 8>), grid, dim3(256), 0, s, spec, spec_ld, l_in, col_in, wt, b, k,
+                           stride, pad, y, y_ld, l_out);
+    else
+        return hipErrorInvalidValue;
     return hipGetLastError();
 }
 
