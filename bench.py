@@ -6,7 +6,9 @@ over the batch (kk_plan_run: duration expansion -> decoder -> harmonic source + 
 iSTFT), with every input already resident in HBM.  `value` = audio seconds synthesized per wall
 second.  The roofline block reports the dominant kernel (the Snake-block MFMA convolutions):
 algorithmic FLOP / summed HIP-event time of those launches in the timed region, against the bf16
-dense MFMA peak.  The CPU baseline is the oracle (a CPU restatement of the same path) on a bounded
+dense MFMA peak; its `traffic` is the HBM bytes per launch measured by the FETCH_SIZE / WRITE_SIZE
+counters (profiles/conv_mfma_snake_config3_traffic.json, made with --calibrate-copy-mib and
+kokoro_hip/profsum.py).  The CPU baseline is the oracle (a CPU restatement of the same path) on a bounded
 sample of the same batch.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--config 3|5]
@@ -46,6 +48,16 @@ def cpu_baseline(weights, items, budget_s=12.0):
                       f"of the same batch: {done_audio:.1f} audio-s in {done_s:.1f} s"}
 
 
+def _traffic(config):
+    """HBM bytes per Snake-conv launch (FETCH_SIZE + WRITE_SIZE, copy-calibrated) from the committed
+    PMC summary of the config-3 workload; None for other workloads or when it is absent."""
+    path = os.path.join(ROOT, "profiles", "conv_mfma_snake_config3_traffic.json")
+    if config != 3 or not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return round(json.load(f)["traffic_bytes_per_launch"])
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -54,6 +66,8 @@ def main():
     ap.add_argument("--config", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-events", action="store_true", help="time without the per-launch HIP events")
+    ap.add_argument("--calibrate-copy-mib", type=int, default=0,
+                    help="first run one plain copy kernel over this many MiB (reference for PMC byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only: the path is data-parallel over independent items and this "
@@ -63,6 +77,18 @@ def main():
 
     import numpy as np
     from kokoro_hip import api, model_spec, workloads
+
+    if args.calibrate_copy_mib:
+        # one elementwise kernel that reads and writes exactly M MiB: the FETCH_SIZE / WRITE_SIZE
+        # counters of this dispatch scale those of the conv kernels to bytes
+        import torch
+        a = torch.ones(args.calibrate_copy_mib << 18, device="cuda:0")
+        b = torch.empty_like(a)
+        torch.cuda.synchronize()
+        torch.mul(a, 1.0, out=b)
+        torch.cuda.synchronize()
+        del a, b
+        print(f"# calibration copy: {args.calibrate_copy_mib} MiB", file=sys.stderr, flush=True)
 
     weights = model_spec.random_weights(seed=0)
     if args.config == 5:
@@ -107,7 +133,7 @@ def main():
         sn = prof["snake_conv"]
         achieved = sn["flop"] / (sn["ms"] / 1e3) / 1e12
         roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": _traffic(args.config),
                 "kernel": "conv_mfma_kernel<PRO_ADAIN_SNAKE> (48 Snake-block convs per step)",
                 "avg_launch_ms": round(sn["ms"] / max(sn["launches"], 1), 4),
                 "flop_per_launch": sn["flop"] / max(sn["launches"], 1)}

@@ -222,32 +222,44 @@ constexpr int kNumRes = EPI == EPI_MEAN3 ? 3
                         : (EPI == EPI_ACCUM || EPI == EPI_RESID || EPI == EPI_RESID_UP2 || EPI == EPI_ADD_FROM) ? 1
                                                                                                                  : 0;
 
+// Row pointers of one unit: every tensor the epilogue touches, advanced to the unit's first row
+// (uniform), so a lane's element offset within the unit fits 32 bits.
+struct EpiBase {
+    void* y;
+    const float *r0, *r1, *r2;
+};
+
+// Residual operands of output row t, channels m..m+3 (`yo`, `ro`: element offsets from the unit's
+// first row in y and r0..r2).
 template <int EPI>
-__device__ __forceinline__ void load_res(const ConvParams& p, int64_t t, int m, float4* r) {
+__device__ __forceinline__ void load_res(const ConvParams& p, const EpiBase& eb, uint32_t yo, uint32_t ro, int64_t t,
+                                         int m, float4* r) {
     if constexpr (EPI == EPI_ACCUM || EPI == EPI_RESID) {
-        r[0] = *(const float4*)(p.y + t * p.y_ld + m);
+        r[0] = *(const float4*)((const float*)eb.y + yo);
     } else if constexpr (EPI == EPI_RESID_UP2) {
         r[0] = *(const float4*)(p.r0 + (t >> 1) * p.r0_ld + m);
     } else if constexpr (EPI == EPI_ADD_FROM) {
-        r[0] = *(const float4*)(p.r0 + t * p.r0_ld + m);
+        r[0] = *(const float4*)(eb.r0 + ro);
     } else if constexpr (EPI == EPI_MEAN3) {
-        r[0] = *(const float4*)(p.r0 + t * p.r0_ld + m);
-        r[1] = *(const float4*)(p.r1 + t * p.r0_ld + m);
-        r[2] = *(const float4*)(p.r2 + t * p.r0_ld + m);
+        r[0] = *(const float4*)(eb.r0 + ro);
+        r[1] = *(const float4*)(eb.r1 + ro);
+        r[2] = *(const float4*)(eb.r2 + ro);
     }
 }
 
-// Stride-1 epilogue of rows m..m+3 of column t: v = conv + bias, combined with the residuals r;
-// returns the stored values (the statistics describe what the next layer reads).
+// Applies the residual rule to v (conv + bias) of 4 channels of one output row and stores the
+// result at element offset `yo` from the unit's first row of y; returns the stored values (the
+// statistics describe what the next layer reads).
 template <int EPI, bool OUT_H>
-__device__ __forceinline__ float4 finish4(const ConvParams& p, int64_t t, int m, float4 v, const float4* r) {
+__device__ __forceinline__ float4 finish4(const ConvParams& p, const EpiBase& eb, uint32_t yo, float4 v,
+                                          const float4* r) {
     if constexpr (OUT_H) {
         // fp16 storage
         const _Float16 h0 = (_Float16)v.x, h1 = (_Float16)v.y, h2 = (_Float16)v.z, h3 = (_Float16)v.w;
         uint2 pk;
         pk.x = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
         pk.y = (uint32_t)__builtin_bit_cast(uint16_t, h2) | ((uint32_t)__builtin_bit_cast(uint16_t, h3) << 16);
-        *(uint2*)((uint16_t*)p.y + t * p.y_ld + m) = pk;
+        *(uint2*)((uint16_t*)eb.y + yo) = pk;
         return make_float4((float)h0, (float)h1, (float)h2, (float)h3);
     }
     float4 o = v;
@@ -264,7 +276,7 @@ __device__ __forceinline__ float4 finish4(const ConvParams& p, int64_t t, int m,
         o = make_float4(((a.x + b1.x) + (c.x + v.x)) / 3.0f, ((a.y + b1.y) + (c.y + v.y)) / 3.0f,
                         ((a.z + b1.z) + (c.z + v.z)) / 3.0f, ((a.w + b1.w) + (c.w + v.w)) / 3.0f);
     }
-    *(float4*)(p.y + t * p.y_ld + m) = o;
+    *(float4*)((float*)eb.y + yo) = o;
     return o;
 }
 
@@ -289,11 +301,24 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
     const int wcol0 = wn * 128;                // this wave's first column within the tile
     const int m = u.m0 + wm * 64 + 4 * cq;     // this lane's 4 output rows after the transpose
     const bool mok = m < p.m;
+    // every stride-1 MFMA layer has a bias vector (zeros for a layer without one)
     float4 b = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (!CONVT && p.bias) b = *(const float4*)(p.bias + (mok ? m : 0));
+    if constexpr (!CONVT) b = *(const float4*)(p.bias + (mok ? m : 0));
     // Consume the loaded values once, outside any branch: stores issued later then never make the
     // wait-count pass wait for them again (its state merges conservatively after skipped branches).
     ready(b);
+    // Row pointers at the unit's first row (uniform) and this lane's 32-bit element offsets of its
+    // first output row (column wcol0 + cg); row wcol0 + cg + c adds c * ld, one 24-bit multiply
+    // with ld held in a VGPR (uniform products of every c would occupy scalar registers).
+    EpiBase eb;
+    const int64_t n0 = u.n0;
+    eb.y = OUT_H ? (void*)((uint16_t*)p.y + n0 * p.y_ld) : (void*)(p.y + n0 * p.y_ld);
+    eb.r0 = eb.r1 = eb.r2 = nullptr;
+    if constexpr (EPI == EPI_ADD_FROM || EPI == EPI_MEAN3) eb.r0 = p.r0 + n0 * p.r0_ld;
+    if constexpr (EPI == EPI_MEAN3) eb.r1 = p.r1 + n0 * p.r0_ld, eb.r2 = p.r2 + n0 * p.r0_ld;
+    const uint32_t yld = (uint32_t)vgpr((int)p.y_ld), rld = (uint32_t)vgpr((int)p.r0_ld);
+    const uint32_t yo0 = (uint32_t)(wcol0 + cg) * yld + m, ro0 = (uint32_t)(wcol0 + cg) * rld + m;
+    const uint32_t yz = u.m0, rz = u.m0;  // clamped operand of an invalid row: row 0 of the unit
     float s1[4] = {0.f, 0.f, 0.f, 0.f}, s2[4] = {0.f, 0.f, 0.f, 0.f}, sft[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < 4; j++) {
@@ -311,27 +336,34 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
                 // unconditional loads (invalid columns / rows read column 0 / row 0 of the tile)
 #pragma unroll
                 for (int qq = 0; qq < QB; qq++) {
-                    const int col = wcol0 + j * 32 + 4 * (q0 + qq) + cg;
-                    load_res<EPI>(p, u.n0 + (col < u.nv ? col : 0), mok ? m : u.m0, res[qq]);
+                    const int c = j * 32 + 4 * (q0 + qq);
+                    const bool ok = wcol0 + c + cg < u.nv && mok;
+                    load_res<EPI>(p, eb, ok ? yo0 + __umul24(c, yld) : yz, ok ? ro0 + __umul24(c, rld) : rz,
+                                  ok ? n0 + wcol0 + cg + c : n0, ok ? m : u.m0, res[qq]);
                 }
 #pragma unroll
                 for (int qq = 0; qq < QB; qq++)
 #pragma unroll
                     for (int e = 0; e < NRA; e++) ready(res[qq][e]);
             }
+            // all LDS reads of the batch first, one wait, then the arithmetic and the stores
+            float4 v[QB];
+#pragma unroll
+            for (int qq = 0; qq < QB; qq++) v[qq] = *(const float4*)(scr + (4 * (q0 + qq) + cg) * kScrLd + 4 * cq);
+#pragma unroll
+            for (int qq = 0; qq < QB; qq++) ready(v[qq]);
 #pragma unroll
             for (int qq = 0; qq < QB; qq++) {
                 const int q = q0 + qq;
                 const int col = wcol0 + j * 32 + 4 * q + cg;
                 const bool valid = col < u.nv;
-                float4 v = *(const float4*)(scr + (4 * q + cg) * kScrLd + 4 * cq);
                 float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
                 if (valid && mok) {
                     if constexpr (CONVT) {
-                        store_convt<EPI>(p, u.item, u.n0 + col, m, v);
+                        store_convt<EPI>(p, u.item, u.n0 + col, m, v[qq]);
                     } else {
-                        v.x += b.x, v.y += b.y, v.z += b.z, v.w += b.w;
-                        o = finish4<EPI, OUT_H>(p, u.n0 + col, m, v, res[qq]);
+                        const float4 w = make_float4(v[qq].x + b.x, v[qq].y + b.y, v[qq].z + b.z, v[qq].w + b.w);
+                        o = finish4<EPI, OUT_H>(p, eb, yo0 + __umul24(j * 32 + 4 * q, yld), w, res[qq]);
                     }
                 }
                 if constexpr (STATS) {
@@ -565,7 +597,7 @@ hipError_t launch_t(const ConvParams& p, int n_cu, hipStream_t s) {
     const size_t smem = 2 * (size_t)(BN + halo) * kRS * sizeof(uint16_t) + scr_bytes;
     constexpr size_t smem_max = 2 * (size_t)(BN + kMaxHalo) * kRS * sizeof(uint16_t) + scr_bytes;
     static_assert(smem_max <= 160 * 1024, "LDS budget");
-    if (p.m_pad % BM != 0 || p.cin_pad % kCK != 0 || halo < 0 || halo > kMaxHalo) return hipErrorInvalidValue;
+    if (p.m_pad % BM != 0 || p.cin_pad % kCK != 0 || halo < 0 || halo > kMaxHalo || !p.bias) return hipErrorInvalidValue;
     if (p.l_in >= (int64_t)1 << 30 || p.tiles.count >= (int64_t)1 << 28) return hipErrorInvalidValue;  // 32-bit rows
     auto kern = conv_mfma_kernel<PRO, EPI, WM, WN, STATS, IN_H, OUT_H>;
     static bool attr = false;

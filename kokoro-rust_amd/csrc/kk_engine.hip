@@ -204,11 +204,10 @@ static void load_conv(MConv& c, const Table& t, const std::string& p, int cin, i
                 pk[(((size_t)kk * n16 + ci / 16) * c.m_pad + co) * 16 + (ci & 15)] =
                     bf16_bits(w[((size_t)co * cin + ci) * k + kk]);
     c.w.upload(pk);
-    if (bias) {
-        std::vector<float> b(round_up(cout, 4), 0.f);
-        std::memcpy(b.data(), t.get(p + ".bias", cout), sizeof(float) * cout);
-        c.b.upload(b);
-    }
+    // a layer without a bias gets a zero vector: the conv epilogue always reads one
+    std::vector<float> b(round_up(cout, 4), 0.f);
+    if (bias) std::memcpy(b.data(), t.get(p + ".bias", cout), sizeof(float) * cout);
+    c.b.upload(b);
 }
 
 // ConvTranspose1d with K = 2 * stride as a 2-tap conv over input rows (i - 1, i) whose GEMM row
@@ -826,7 +825,7 @@ struct Runner {
         q.tiles = t.dev();
         q.coef = o.coef, q.alpha_rev = o.ar ? o.ar->as<float>() : nullptr;
         q.alpha_inv = o.ai ? o.ai->as<float>() : nullptr, q.slope = o.slope;
-        q.w = c.w.as<uint16_t>(), q.bias = c.bias ? c.b.as<float>() : nullptr;
+        q.w = c.w.as<uint16_t>(), q.bias = c.b.as<float>();
         q.m = c.m, q.m_pad = c.m_pad, q.k = c.k, q.dil = c.dil, q.pad = c.pad;
         q.y = o.y, q.y_ld = o.y_ld, q.cout = c.cout;
         q.r0 = o.r0, q.r1 = o.r1, q.r2 = o.r2, q.r0_ld = o.r0_ld, q.scale = o.scale;

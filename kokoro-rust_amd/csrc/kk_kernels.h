@@ -64,7 +64,7 @@ struct ConvParams {
     const float* alpha_inv;  // [cin] 1 / alpha
     float slope;
     const uint16_t* w;       // packed bf16 [k][cin_pad/16][m_pad][16]
-    const float* bias;       // [cout] or null
+    const float* bias;       // [cout] (zeros for a layer without bias)
     int m, m_pad;            // GEMM rows (cout, or stride * cout for ConvT), padded to the block
     int k, dil, pad;
     float* y;                // output [rows][y_ld] (f32, or fp16 for the Snake steps' h)
