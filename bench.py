@@ -4,8 +4,10 @@ Workload (the metric's config): 32 ragged items, N ~ U
 frames each, seeded synthetic inputs and random-init weights.  One step = one pass of the hot path
 over the batch (kk_plan_run: duration expansion -> decoder -> harmonic source + STFT -> generator ->
 iSTFT), with every input already resident in HBM.  `value` = audio seconds synthesized per wall
-second.  The roofline block reports the dominant kernel (the Snake-block MFMA convolutions):
-algorithmic FLOP / summed HIP-event time of those launches in the timed region, against the bf16
+second, timed without per-launch instrumentation.  The roofline block reports the dominant kernel
+(the Snake-block MFMA convolutions): algorithmic FLOP / summed HIP-event time of those launches over
+a second timed pass of the same K steps with an event pair around every conv launch on the
+library's stream, against the bf16
 dense MFMA peak; its `traffic` is the HBM bytes per launch measured by the FETCH_SIZE / WRITE_SIZE
 counters (profiles/conv_mfma_snake_config3_traffic.json, made with --calibrate-copy-mib and
 kokoro_hip/profsum.py).  The CPU baseline is the oracle (a CPU restatement of the same path) on a bounded
@@ -108,19 +110,25 @@ def main():
     for _ in range(args.warmup):
         plan.run()
     plan.sync()
-    ctx.set_profiling(not args.no_events)
-    ctx.profile_read()  # drop warmup records
-    plan.sync()
     t0 = time.perf_counter()
     for _ in range(args.steps):
         plan.run()
     plan.sync()
     t1 = time.perf_counter()
-    prof = ctx.profile_read() if not args.no_events else {}
-    ctx.set_profiling(False)
     info = plan.info()
     ms = (t1 - t0) * 1e3 / args.steps
     value = audio_s / (ms / 1e3)
+    # per-kernel durations: the same K steps again, launched one by one with a HIP event pair
+    # around every conv launch on the library's stream
+    prof = {}
+    if not args.no_events:
+        ctx.set_profiling(True)
+        ctx.profile_read()
+        for _ in range(args.steps):
+            plan.run()
+        plan.sync()
+        prof = ctx.profile_read()
+        ctx.set_profiling(False)
 
     # parity spot check of the measured batch's first item is done by the test suite; here only a
     # sanity check that the output is finite
