@@ -20,7 +20,7 @@ SNAKE = re.compile(r"conv_mfma_kernel<4,")
 COPY = re.compile(r"elementwise_kernel<.*MulFunctor")  # torch's out = a * 1 over M MiB of float32
 
 
-def _layers():
+def snake_layers():
     """The 48 Snake-block convs of one config-3 step in launch order: per stage the noise resblock,
     then resblocks k3, k7, k11; per block dilations 1, 3, 5; per dilation conv1 then conv2."""
     from kokoro_hip import workloads
@@ -67,7 +67,7 @@ def stats(trace_dir):
     lines = ["| kernel | calls | total ms | avg us | % |", "|---|---:|---:|---:|---:|"]
     for k, v in sorted(per.items(), key=lambda kv: -sum(kv[1])):
         lines.append(f"| `{k}` | {len(v)} | {sum(v) / 1e3:.2f} | {sum(v) / len(v):.1f} | {100 * sum(v) / total:.2f} |")
-    layers, frames = _layers()
+    layers, frames = snake_layers()
     sn = [r for r in rows if SNAKE.search(r["Kernel_Name"])]
     n_steps = len(sn) // len(layers)
     lines += ["", f"Snake-block convs, per layer (config 3: {frames} frames; average over {n_steps} steps):", "",
@@ -96,7 +96,7 @@ def _per_dispatch(run_dir, counter):
 def traffic(fetch_dir, write_dir, mib):
     """FETCH_SIZE and WRITE_SIZE are in KiB per dispatch; the copy kernel moves M MiB each way."""
     res = {}
-    layers, _ = _layers()
+    layers, _ = snake_layers()
     for key, d, counter in [("fetch", fetch_dir, "FETCH_SIZE"), ("write", write_dir, "WRITE_SIZE")]:
         disp = _per_dispatch(d, counter)
         copies = [v for n, v in disp if COPY.search(n)]
