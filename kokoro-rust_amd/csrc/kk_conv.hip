@@ -50,9 +50,15 @@ constexpr int kNP = 256;      // producer threads per block
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
     const bf16x2_t v = __builtin_convertvector((f32x2_t){a, b}, bf16x2_t);  // v_cvt_pk_bf16_f32 (RNE)
+    return __builtin_bit_cast(uint32_t, v);
+}
+
+__device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
+    const f16x2_t v = __builtin_convertvector((f32x2_t){a, b}, f16x2_t);  // v_cvt_pk_f16_f32 (RNE)
     return __builtin_bit_cast(uint32_t, v);
 }
 
@@ -247,20 +253,17 @@ __device__ __forceinline__ void load_res(const ConvParams& p, const EpiBase& eb,
     }
 }
 
-// Applies the residual rule to v (conv + bias) of 4 channels of one output row and stores the
-// result at element offset `yo` from the unit's first row of y; returns the stored values (the
-// statistics describe what the next layer reads).
+// The residual rule applied to v (conv + bias) of 4 channels of one output row: the values to
+// store (the statistics describe these: what the next layer reads).  With fp16 output, `pk` gets
+// the fp16 bits and the returned values are their f32 images.
 template <int EPI, bool OUT_H>
-__device__ __forceinline__ float4 finish4(const ConvParams& p, const EpiBase& eb, uint32_t yo, float4 v,
-                                          const float4* r) {
+__device__ __forceinline__ float4 finish4(const ConvParams& p, float4 v, const float4* r, uint2& pk) {
     if constexpr (OUT_H) {
-        // fp16 storage
-        const _Float16 h0 = (_Float16)v.x, h1 = (_Float16)v.y, h2 = (_Float16)v.z, h3 = (_Float16)v.w;
-        uint2 pk;
-        pk.x = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
-        pk.y = (uint32_t)__builtin_bit_cast(uint16_t, h2) | ((uint32_t)__builtin_bit_cast(uint16_t, h3) << 16);
-        *(uint2*)((uint16_t*)eb.y + yo) = pk;
-        return make_float4((float)h0, (float)h1, (float)h2, (float)h3);
+        pk = make_uint2(pack_f16x2(v.x, v.y), pack_f16x2(v.z, v.w));
+        return make_float4((float)__builtin_bit_cast(_Float16, (uint16_t)(pk.x & 0xffffu)),
+                           (float)__builtin_bit_cast(_Float16, (uint16_t)(pk.x >> 16)),
+                           (float)__builtin_bit_cast(_Float16, (uint16_t)(pk.y & 0xffffu)),
+                           (float)__builtin_bit_cast(_Float16, (uint16_t)(pk.y >> 16)));
     }
     float4 o = v;
     if constexpr (EPI == EPI_ACCUM || EPI == EPI_ADD_FROM) {
@@ -276,8 +279,17 @@ __device__ __forceinline__ float4 finish4(const ConvParams& p, const EpiBase& eb
         o = make_float4(((a.x + b1.x) + (c.x + v.x)) / 3.0f, ((a.y + b1.y) + (c.y + v.y)) / 3.0f,
                         ((a.z + b1.z) + (c.z + v.z)) / 3.0f, ((a.w + b1.w) + (c.w + v.w)) / 3.0f);
     }
-    *(float4*)((float*)eb.y + yo) = o;
     return o;
+}
+
+// Stores one row's result at element offset `yo` from the unit's first row of y.
+template <bool OUT_H>
+__device__ __forceinline__ void store4(const EpiBase& eb, uint32_t yo, float4 o, uint2 pk) {
+    if constexpr (OUT_H) {
+        *(uint2*)((uint16_t*)eb.y + yo) = pk;
+    } else {
+        *(float4*)((float*)eb.y + yo) = o;
+    }
 }
 
 constexpr int kScrLd = 64 + 4;  // epilogue LDS scratch row stride (f32): one time column, 64 channels
@@ -357,14 +369,16 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
                 const int q = q0 + qq;
                 const int col = wcol0 + j * 32 + 4 * q + cg;
                 const bool valid = col < u.nv;
+                // the values are computed for every row (they feed the statistics, masked there);
+                // only the store is conditional
                 float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-                if (valid && mok) {
-                    if constexpr (CONVT) {
-                        store_convt<EPI>(p, u.item, u.n0 + col, m, v[qq]);
-                    } else {
-                        const float4 w = make_float4(v[qq].x + b.x, v[qq].y + b.y, v[qq].z + b.z, v[qq].w + b.w);
-                        o = finish4<EPI, OUT_H>(p, eb, yo0 + __umul24(j * 32 + 4 * q, yld), w, res[qq]);
-                    }
+                if constexpr (CONVT) {
+                    if (valid && mok) store_convt<EPI>(p, u.item, u.n0 + col, m, v[qq]);
+                } else {
+                    const float4 w = make_float4(v[qq].x + b.x, v[qq].y + b.y, v[qq].z + b.z, v[qq].w + b.w);
+                    uint2 pk;
+                    o = finish4<EPI, OUT_H>(p, w, res[qq], pk);
+                    if (valid && mok) store4<OUT_H>(eb, yo0 + __umul24(j * 32 + 4 * q, yld), o, pk);
                 }
                 if constexpr (STATS) {
                     const float ov[4] = {o.x, o.y, o.z, o.w};
@@ -540,6 +554,7 @@ __global__ __launch_bounds__(64 * WM * WN + kNP) void conv_mfma_kernel(ConvParam
             for (int i = 0; i < 2; i++)
                 acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
     };
+
 
     int U = blockIdx.x, sl = 0;
     Unit cu, nu;
