@@ -112,23 +112,26 @@ struct Slot {
     float4 k01, k23;  // AdaIN coefficients (sc, sh) of channels c..c+1 and c+2..c+3
     float4 ar, ai;    // Snake alpha / (2 pi) and 1 / alpha
 
-    __device__ __forceinline__ static bool live(const ConvParams& p, const Unit& u, int r, int tw, int c) {
-        const int row = u.in0 + r;
-        return r < tw && row >= u.i_lo && row < u.i_hi && c < p.cin;
-    }
-
+    // Slab (u, c0): row in0 + r (r = rr + j RP) is read clamped into the item's rows and channel c0 + q
+    // as channel 0 past cin (the conversion zeroes both).  Addresses are 32-bit byte offsets from
+    // the item's first row (a uniform base), one clamp and one 24-bit multiply-add per row.
     __device__ __forceinline__ void load(const ConvParams& p, const Unit& u, int c0, int tw, int q, int rr) {
         const int c = c0 + q;
         const int cl = c < p.cin ? c : 0;
+        constexpr int ES = WIDE ? 4 : 2;  // bytes per element
+        const char* base = (const char*)p.x + (int64_t)u.i_lo * p.x_ld * ES;
+        const uint32_t ld = (uint32_t)p.x_ld;
+        const int r0 = u.in0 - u.i_lo, rmax = u.i_hi - 1 - u.i_lo;  // row offsets from the item start
 #pragma unroll
         for (int j = 0; j < RB; j++) {
             const int r = rr + j * RP;
-            const int64_t row = live(p, u, r, tw, c) ? u.in0 + r : u.i_lo;
+            const uint32_t row = (uint32_t)max(min(r0 + r, rmax), 0);
+            const uint32_t off = (__umul24(row, ld) + (uint32_t)cl) * ES;
             if constexpr (WIDE) {
-                const uint4 x = *(const uint4*)((const float*)p.x + row * p.x_ld + cl);
+                const uint4 x = *(const uint4*)(base + off);
                 raw[j][0] = x.x, raw[j][1] = x.y, raw[j][2] = x.z, raw[j][3] = x.w;
             } else {
-                const uint2 h = *(const uint2*)((const uint16_t*)p.x + row * p.x_ld + cl);
+                const uint2 h = *(const uint2*)(base + off);
                 raw[j][0] = h.x, raw[j][1] = h.y;
             }
         }
@@ -142,6 +145,8 @@ struct Slot {
         }
     }
 
+    // Converts the slab into LDS rows [r][kRS]: the layer's prologue once per element, rows outside
+    // the item (gap masking) and channels past cin as zero, branch-free per row.
     __device__ __forceinline__ void convert(const ConvParams& p, uint16_t* xs, const Unit& u, int c0, int tw, int q,
                                             int rr) const {
         const int c = c0 + q;
@@ -157,46 +162,52 @@ struct Slot {
         // limit rematerialized from the kernel arguments costs a scalar load and a wait per row):
         // live rows r in [r_lo, r_hi), live channels e < n_ch of this quad.
         const int r_lo = vgpr(u.i_lo - u.in0), r_hi = vgpr(min(tw, u.i_hi - u.in0)), n_ch = p.cin - c;
+        const uint32_t r_n = (uint32_t)(r_hi - r_lo);
         const float slope = vgpr_f(p.slope);
+        uint16_t* xrow = xs + rr * kRS + q;
 #pragma unroll
         for (int j = 0; j < RB; j++) {
             const int r = rr + j * RP;
-            if (r >= tw) break;
-            uint2 out = make_uint2(0, 0);
-            if (r >= r_lo && r < r_hi && n_ch > 0) {
-                if constexpr (PRO == PRO_BF16) {
-                    out = make_uint2(raw[j][0], raw[j][1]);  // bf16 input: channels >= cin hold 0
+            const bool live = (uint32_t)(r - r_lo) < r_n;
+            uint2 out;
+            if constexpr (PRO == PRO_BF16) {
+                out = make_uint2(raw[j][0], raw[j][1]);  // bf16 input: channels >= cin hold 0
+            } else {
+                float v[4];
+                if constexpr (WIDE) {
+#pragma unroll
+                    for (int e = 0; e < 4; e++) v[e] = __uint_as_float(raw[j][e]);
                 } else {
-                    float v[4];
-                    if constexpr (WIDE) {
 #pragma unroll
-                        for (int e = 0; e < 4; e++) v[e] = __uint_as_float(raw[j][e]);
-                    } else {
-#pragma unroll
-                        for (int e = 0; e < 2; e++) {
-                            v[2 * e] = (float)__builtin_bit_cast(_Float16, (uint16_t)(raw[j][e] & 0xffffu));
-                            v[2 * e + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(raw[j][e] >> 16));
-                        }
+                    for (int e = 0; e < 2; e++) {
+                        v[2 * e] = (float)__builtin_bit_cast(_Float16, (uint16_t)(raw[j][e] & 0xffffu));
+                        v[2 * e + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(raw[j][e] >> 16));
                     }
-                    float w[4];
-#pragma unroll
-                    for (int e = 0; e < 4; e++) {
-                        float x = v[e];
-                        if constexpr (PRO == PRO_LEAKY) {
-                            x = x < 0.f ? x * slope : x;
-                        } else if constexpr (PRO == PRO_ADAIN_LEAKY) {
-                            x = __builtin_fmaf(x, sc[e], sh[e]);
-                            x = x < 0.f ? x * slope : x;
-                        } else if constexpr (PRO == PRO_ADAIN_SNAKE) {
-                            x = snake(__builtin_fmaf(x, sc[e], sh[e]), arv[e], aiv[e]);
-                        }
-                        w[e] = e < n_ch ? x : 0.f;
-                    }
-                    out.x = pack_bf16x2(w[0], w[1]);
-                    out.y = pack_bf16x2(w[2], w[3]);
                 }
+                float w[4];
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    float x = v[e];
+                    if constexpr (PRO == PRO_LEAKY) {
+                        x = x < 0.f ? x * slope : x;
+                    } else if constexpr (PRO == PRO_ADAIN_LEAKY) {
+                        x = __builtin_fmaf(x, sc[e], sh[e]);
+                        x = x < 0.f ? x * slope : x;
+                    } else if constexpr (PRO == PRO_ADAIN_SNAKE) {
+                        x = snake(__builtin_fmaf(x, sc[e], sh[e]), arv[e], aiv[e]);
+                    }
+                    // the Snake layers' cin is a multiple of the slab width (checked on the host)
+                    if constexpr (!SNAKE) x = e < n_ch ? x : 0.f;
+                    w[e] = x;
+                }
+                out = make_uint2(pack_bf16x2(w[0], w[1]), pack_bf16x2(w[2], w[3]));
             }
-            *(uint2*)(xs + r * kRS + q) = out;
+            if constexpr (PRO == PRO_BF16) {
+                if (!live) out = make_uint2(0, 0);
+            } else {
+                if (!live || n_ch <= 0) out = make_uint2(0, 0);
+            }
+            if (r < tw) *(uint2*)(xrow + j * RP * kRS) = out;
         }
     }
 };
@@ -613,7 +624,10 @@ hipError_t launch_t(const ConvParams& p, int n_cu, hipStream_t s) {
     constexpr size_t smem_max = 2 * (size_t)(BN + kMaxHalo) * kRS * sizeof(uint16_t) + scr_bytes;
     static_assert(smem_max <= 160 * 1024, "LDS budget");
     if (p.m_pad % BM != 0 || p.cin_pad % kCK != 0 || halo < 0 || halo > kMaxHalo || !p.bias) return hipErrorInvalidValue;
+    if (PRO == PRO_ADAIN_SNAKE && p.cin % kCK != 0) return hipErrorInvalidValue;  // no channel mask there
     if (p.l_in >= (int64_t)1 << 30 || p.tiles.count >= (int64_t)1 << 28) return hipErrorInvalidValue;  // 32-bit rows
+    // producer loads: 32-bit byte offsets within one item's rows
+    if (p.in_max_len * p.x_ld * (PRO != PRO_BF16 && !IN_H ? 4 : 2) >= (int64_t)1 << 32) return hipErrorInvalidValue;
     auto kern = conv_mfma_kernel<PRO, EPI, WM, WN, STATS, IN_H, OUT_H>;
     static bool attr = false;
     if (!attr) {

@@ -5,6 +5,7 @@
 // hydration) and src/gpu_batch.rs (Dom layout and forward_batch from the durations on).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -821,6 +822,7 @@ struct Runner {
         const Tiles& t = o.convt ? p->tl(*o.din, bn, 1) : p->tl(*o.dout, bn);
         ConvParams q{};
         q.x = o.x, q.x_ld = o.x_ld, q.l_in = o.din->l, q.cin = c.cin, q.cin_pad = c.cin_pad;
+        q.in_max_len = o.din->len.empty() ? 0 : *std::max_element(o.din->len.begin(), o.din->len.end());
         q.in_start = o.din->start_d.as<int64_t>(), q.in_len = o.din->len_d.as<int64_t>();
         q.tiles = t.dev();
         q.coef = o.coef, q.alpha_rev = o.ar ? o.ar->as<float>() : nullptr;

@@ -55,6 +55,7 @@ struct ConvParams {
     const void* x;           // input [l_in][x_ld] (f32, fp16 or bf16)
     int64_t x_ld;
     int64_t l_in;
+    int64_t in_max_len;      // longest item span of the input domain (rows)
     int cin, cin_pad;        // real and padded (multiple of 64) input channels
     const int64_t* in_start; // input domain item spans (rows outside an item's span read as 0)
     const int64_t* in_len;
