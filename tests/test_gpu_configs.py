@@ -1,0 +1,93 @@
+"""The benchmark configurations at their full sizes on the GPU, through the C ABI.
+
+- Config 1 (generator only, one item of 100 decoder frames): against the fp32 oracle.
+- Config 2 (one 256-channel k7 Snake block, 16 ragged items of 500-2000 columns): the whole batch
+  on the GPU; the three shortest items against the bf16-emulated oracle (the block's increment,
+  >= 55 dB) and the fp32 oracle (>= 40 dB); the longest item alone is bit-identical to its copy in
+  the batch.
+- Config 5 (128 items, generator frames log-uniform in [80, 4000], ~27 GiB of plan): size-
+  independent properties at full size: every item finite with the right length, two items (the
+  shortest and the longest) bit-identical to runs of themselves alone, and the shortest against
+  the fp32 oracle.
+"""
+import numpy as np
+import pytest
+
+from conftest import snr_db
+from test_gpu_properties import _check_vs_oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def _print(*a):
+    print(*a, flush=True)
+
+
+def test_config1_generator(gpu_ctx, oracle_model):
+    """End to end against the oracle, or from the GPU's own spectrum when a bin sits on atan2's
+    branch cut (see test_gpu_properties._check_vs_oracle)."""
+    from kokoro_hip import api, workloads
+    from oracle import oracle as O
+    x, f0, style, seed = workloads.config1_generator_input()
+    n = x.shape[1] // 2
+    with api.Plan.generator(gpu_ctx, [x], [f0], [style], [seed]) as plan:
+        plan.run()
+        (a,) = plan.fetch()
+        g = plan.tap("spec", 0, (22, 120 * n + 1))
+    ref, spec, _ = oracle_model.generator(x, f0, style, O.rand_ini(seed), O.gen_noise(seed, 600 * n * 9), taps=True)
+    mag_err = np.abs(g[:11] - spec[:11]).max() / max(np.abs(spec[:11]).max(), 1e-6)
+    energetic = spec[:11] > 1e-4 * spec[:11].max()
+    dphi = np.angle(np.exp(1j * (g[11:].astype(np.float64) - spec[11:])))
+    flips = int((np.abs(g[11:] - spec[11:]) > np.pi).sum())
+    assert mag_err < 1e-4 and np.abs(dphi[energetic]).max() < 1e-3
+    if flips:
+        ref, _ = oracle_model.generator_from_spec(x, g, style)
+    _print("  config 1: N", n, "branch-cut bins", flips, "snr", snr_db(ref, a), "maxabs", np.abs(a - ref).max())
+    assert a.shape == (600 * n,)
+    assert np.abs(a - ref).max() <= 2e-3
+    assert snr_db(ref, a) >= 40.0
+
+
+def test_config2_snake_block(gpu_ctx, oracle_model):
+    from kokoro_hip import api, workloads
+    from oracle import oracle as O
+    prefix = "decoder.generator.resblocks.1"  # 256 channels, k 7, dilations 1 / 3 / 5
+    xs, styles = workloads.config2_snake_items()
+    _print("  config 2: T =", [x.shape[1] for x in xs])
+    with api.Plan.snake(gpu_ctx, prefix, xs, styles, gap=40) as plan:
+        plan.run()
+        outs = plan.fetch()
+    order = np.argsort([x.shape[1] for x in xs])
+    for i in order[:3]:
+        x, s, y = xs[i], styles[i], outs[i]
+        ref = oracle_model.snake_block(prefix, x, s)
+        with O.bf16_emulation():
+            emu = oracle_model.snake_block(prefix, x, s)
+        _print("  T", x.shape[1], "fp32 snr", snr_db(ref - x, y - x), "emu snr", snr_db(emu - x, y - x))
+        assert snr_db(emu - x, y - x) >= 55.0
+        assert snr_db(ref - x, y - x) >= 40.0
+    j = int(order[-1])
+    with api.Plan.snake(gpu_ctx, prefix, [xs[j]], [styles[j]], gap=40) as plan:
+        plan.run()
+        (alone,) = plan.fetch()
+    assert np.array_equal(alone, outs[j])
+
+
+def test_config5_full_size(gpu_ctx, oracle_model):
+    from kokoro_hip import api, workloads
+    items = workloads.config5_items()
+    ns = [it.n_frames for it in items]
+    _print("  config 5:", len(items), "items, frames", sum(ns), "samples", 600 * sum(ns))
+    with api.Plan.decoder(gpu_ctx, items) as plan:
+        plan.run()
+        outs = plan.fetch()
+    for it, a in zip(items, outs):
+        assert a.shape == (600 * it.n_frames,) and np.isfinite(a).all()
+    lo, hi = int(np.argmin(ns)), int(np.argmax(ns))
+    # the shortest item alone, against the oracle (spectrum and audio, as in the property tests)
+    _, (alone,) = _check_vs_oracle(gpu_ctx, oracle_model, [items[lo]], "config 5 shortest")
+    assert np.array_equal(alone, outs[lo])
+    with api.Plan.decoder(gpu_ctx, [items[hi]]) as plan:
+        plan.run()
+        (alone,) = plan.fetch()
+    assert np.array_equal(alone, outs[hi]), f"item {hi} (N {ns[hi]})"
