@@ -266,10 +266,12 @@ __device__ __forceinline__ void load_res(const ConvParams& p, const EpiBase& eb,
 
 // The residual rule applied to v (conv + bias) of 4 channels of one output row: the values to
 // store (the statistics describe these: what the next layer reads).  With fp16 output, `pk` gets
-// the fp16 bits and the returned values are their f32 images.
+// the fp16 bits.
 template <int EPI, bool OUT_H>
 __device__ __forceinline__ float4 finish4(const ConvParams& p, float4 v, const float4* r, uint2& pk) {
     if constexpr (OUT_H) {
+        // fp16 storage; the statistics use the f32 values (the fp16 rounding moves the mean and
+        // variance by ~2^-12 relative, far below the next layer's bf16 operand rounding)
         pk = make_uint2(pack_f16x2(v.x, v.y), pack_f16x2(v.z, v.w));
         return make_float4((float)__builtin_bit_cast(_Float16, (uint16_t)(pk.x & 0xffffu)),
                            (float)__builtin_bit_cast(_Float16, (uint16_t)(pk.x >> 16)),
@@ -304,8 +306,29 @@ __device__ __forceinline__ void store4(const EpiBase& eb, uint32_t yo, float4 o,
 }
 
 constexpr int kScrLd = 64 + 4;  // epilogue LDS scratch row stride (f32): one time column, 64 channels
+constexpr int kMaxBias = 1152;  // bias vector staged in LDS (output rows, M_pad)
 
-// Epilogue of one unit: bias, residual rule, stores, statistics partials; zeroes the accumulators.
+// Starts a unit's accumulators at its bias (stride-1 layers): element 4 g + r of MFMA tile (i, j)
+// is output row i 32 + 8 g + 4 lh + r of the wave's 64 rows, for every column.  ConvT layers
+// (bias per output channel of a phase, added in their scatter) start from zero.
+template <bool BIAS>
+__device__ __forceinline__ void init_acc(f32x16 (&acc)[2][4], const float* bias_s, int m0, int wm, int lane) {
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            float4 bv = make_float4(0.f, 0.f, 0.f, 0.f);
+            if constexpr (BIAS) bv = *(const float4*)(bias_s + m0 + wm * 64 + i * 32 + 8 * g + 4 * (lane >> 5));
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                acc[i][j][4 * g] = bv.x, acc[i][j][4 * g + 1] = bv.y;
+                acc[i][j][4 * g + 2] = bv.z, acc[i][j][4 * g + 3] = bv.w;
+            }
+        }
+}
+
+// Epilogue of one unit: residual rule, stores, statistics partials; then starts the accumulators of
+// the block's next unit (at its bias, or zero for ConvT).
 // The MFMA layout gives each lane 4 channels of one column (D of tile (i, j): rows i*32 + 8 g + 4 lh
 // + r of column j*32 + l32), so stores straight from it would scatter 8-16 byte pieces over 32
 // rows.  Instead the wave transposes each 32-column slice through its LDS scratch ([32][kScrLd]
@@ -314,7 +337,7 @@ constexpr int kScrLd = 64 + 4;  // epilogue LDS scratch row stride (f32): one ti
 // accumulate per lane over columns with one cross-group reduction at the end.
 template <int EPI, int WM, int WN, bool STATS, bool OUT_H>
 __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32x16 (&acc)[2][4], int wm, int wn,
-                                         int lane, float* scr) {
+                                         int lane, float* scr, const float* bias_s, int next_m0) {
     constexpr bool CONVT = EPI == EPI_CONVT || EPI == EPI_CONVT_REFLECT;
     constexpr int NR = CONVT ? 0 : kNumRes<EPI>;
     constexpr int NRA = NR > 0 ? NR : 1;
@@ -324,12 +347,6 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
     const int wcol0 = wn * 128;                // this wave's first column within the tile
     const int m = u.m0 + wm * 64 + 4 * cq;     // this lane's 4 output rows after the transpose
     const bool mok = m < p.m;
-    // every stride-1 MFMA layer has a bias vector (zeros for a layer without one)
-    float4 b = make_float4(0.f, 0.f, 0.f, 0.f);
-    if constexpr (!CONVT) b = *(const float4*)(p.bias + (mok ? m : 0));
-    // Consume the loaded values once, outside any branch: stores issued later then never make the
-    // wait-count pass wait for them again (its state merges conservatively after skipped branches).
-    ready(b);
     // Row pointers at the unit's first row (uniform) and this lane's 32-bit element offsets of its
     // first output row (column wcol0 + cg); row wcol0 + cg + c adds c * ld, one 24-bit multiply
     // with ld held in a VGPR (uniform products of every c would occupy scalar registers).
@@ -386,9 +403,8 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
                 if constexpr (CONVT) {
                     if (valid && mok) store_convt<EPI>(p, u.item, u.n0 + col, m, v[qq]);
                 } else {
-                    const float4 w = make_float4(v[qq].x + b.x, v[qq].y + b.y, v[qq].z + b.z, v[qq].w + b.w);
-                    uint2 pk;
-                    o = finish4<EPI, OUT_H>(p, w, res[qq], pk);
+                    uint2 pk;  // v = conv + bias (the accumulators started at the bias)
+                    o = finish4<EPI, OUT_H>(p, v[qq], res[qq], pk);
                     if (valid && mok) store4<OUT_H>(eb, yo0 + __umul24(j * 32 + 4 * q, yld), o, pk);
                 }
                 if constexpr (STATS) {
@@ -422,12 +438,7 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
                 if (m + r < p.cout) dst[m + r] = nc > 0.f ? StatPart{s1[r], s2[r], sft[r], nc} : StatPart{0.f, 0.f, 0.f, 0.f};
         }
     }
-#pragma unroll
-    for (int i = 0; i < 2; i++)
-#pragma unroll
-        for (int j = 0; j < 4; j++)
-#pragma unroll
-            for (int e = 0; e < 16; e++) acc[i][j][e] = 0.f;
+    init_acc<!CONVT>(acc, bias_s, next_m0, wm, lane);  // the next unit starts at its bias
 }
 
 template <int PRO, int EPI, int WM, int WN, bool STATS, bool IN_H, bool OUT_H>
@@ -551,13 +562,13 @@ __global__ __launch_bounds__(64 * WM * WN + kNP) void conv_mfma_kernel(ConvParam
 #pragma unroll
         for (int j = 0; j < 4; j++) dst[j] = *(const bf16x8*)(bp + j * 32 * kRS);
     };
+    // the layer's bias in LDS (after the scratch), read when each unit's accumulators start
+    constexpr bool CONVT = EPI == EPI_CONVT || EPI == EPI_CONVT_REFLECT;
+    float* bias_s = (float*)(xs + 2 * slab_elems) + NC / 64 * 32 * kScrLd;
+    if constexpr (!CONVT) {
+        for (int i = threadIdx.x; i < p.m_pad; i += NC) bias_s[i] = i < p.m ? p.bias[i] : 0.f;
+    }
     f32x16 acc[2][4];
-#pragma unroll
-    for (int i = 0; i < 2; i++)
-#pragma unroll
-        for (int j = 0; j < 4; j++)
-#pragma unroll
-            for (int e = 0; e < 16; e++) acc[i][j][e] = 0.f;
     auto mfma_step = [&](const bf16x8 (&a)[2], const bf16x8 (&b)[4]) {
 #pragma unroll
         for (int j = 0; j < 4; j++)
@@ -576,7 +587,8 @@ __global__ __launch_bounds__(64 * WM * WN + kNP) void conv_mfma_kernel(ConvParam
     bf16x8 A[4][2], B0[4], B1[4];
 #pragma unroll
     for (int kc = 0; kc < 4; kc++) load_a(A[kc], cu.m0, 0, kc);
-    __syncthreads();  // slab 0 staged
+    __syncthreads();  // slab 0 and the bias staged
+    init_acc<!CONVT>(acc, bias_s, cu.m0, wm, lane);
     for (int g = 0; g < G; g++) {
         const uint16_t* buf = xs + (g & 1) * slab_elems;
         const bool last = sl + 1 == nsl;
@@ -602,7 +614,7 @@ __global__ __launch_bounds__(64 * WM * WN + kNP) void conv_mfma_kernel(ConvParam
                 load_a(A[kc], n_m0, n_kk, n_c16 + kc);
             }
         }
-        if (last) epilogue<EPI, WM, WN, STATS, OUT_H>(p, cu, acc, wm, wn, lane, scr);
+        if (last) epilogue<EPI, WM, WN, STATS, OUT_H>(p, cu, acc, wm, wn, lane, scr, bias_s, has_next ? nu.m0 : cu.m0);
         __syncthreads();  // hand the slab buffer back to the producers
         if (last) {
             sl = 0;
@@ -619,11 +631,13 @@ template <int PRO, int EPI, int WM, int WN, bool STATS, bool IN_H, bool OUT_H>
 hipError_t launch_t(const ConvParams& p, int n_cu, hipStream_t s) {
     constexpr int BM = 64 * WM, BN = 16 * kNJ * WN, NT = 64 * WM * WN + kNP;
     const int halo = (p.k - 1) * p.dil;
-    constexpr size_t scr_bytes = (size_t)WM * WN * 32 * kScrLd * sizeof(float);
+    constexpr size_t scr_bytes = (size_t)WM * WN * 32 * kScrLd * sizeof(float) + kMaxBias * sizeof(float);
     const size_t smem = 2 * (size_t)(BN + halo) * kRS * sizeof(uint16_t) + scr_bytes;
     constexpr size_t smem_max = 2 * (size_t)(BN + kMaxHalo) * kRS * sizeof(uint16_t) + scr_bytes;
     static_assert(smem_max <= 160 * 1024, "LDS budget");
+    constexpr bool CONVT = EPI == EPI_CONVT || EPI == EPI_CONVT_REFLECT;
     if (p.m_pad % BM != 0 || p.cin_pad % kCK != 0 || halo < 0 || halo > kMaxHalo || !p.bias) return hipErrorInvalidValue;
+    if (!CONVT && p.m_pad > kMaxBias) return hipErrorInvalidValue;  // the bias staged in LDS
     if (PRO == PRO_ADAIN_SNAKE && p.cin % kCK != 0) return hipErrorInvalidValue;  // no channel mask there
     if (p.l_in >= (int64_t)1 << 30 || p.tiles.count >= (int64_t)1 << 28) return hipErrorInvalidValue;  // 32-bit rows
     // producer loads: 32-bit byte offsets within one item's rows
