@@ -212,26 +212,16 @@ struct Slot {
     }
 };
 
-// ConvT epilogue: scatter 4 consecutive GEMM rows m..m+3 (phase, channel) of input column t.
-template <int EPI>
-__device__ __forceinline__ void store_convt(const ConvParams& p, int item, int64_t t, int m, float4 v) {
-    const int ph = m / p.cout, co = m - ph * p.cout;
-    const int64_t o = (int64_t)p.stride_t * t + ph - p.pad_t;  // ConvT output column
-    const int64_t os = p.out_start[item];
-    const int64_t ol = EPI == EPI_CONVT ? p.out_len[item] : p.out_len[item] - 1;
-    if (o < os || o >= os + ol) return;
-    const float4 b = *(const float4*)(p.bias + co);
-    v.x += b.x, v.y += b.y, v.z += b.z, v.w += b.w;
-    // EPI_CONVT_REFLECT: ReflectionPad1d((1,0)) per item on the padded domain
-    // (kernels/kokoro.cu:452-467): padded[s] = ups[s + 1], padded[s + 1 + j] = ups[s + j].
-    const int64_t dest = EPI == EPI_CONVT ? o : o + 1;
-    const float4 r = *(const float4*)(p.r0 + dest * p.r0_ld + co);
-    *(float4*)(p.y + dest * p.y_ld + co) = make_float4(v.x + r.x, v.y + r.y, v.z + r.z, v.w + r.w);
-    if (EPI == EPI_CONVT_REFLECT && o == os + 1) {
-        const float4 r2 = *(const float4*)(p.r0 + os * p.r0_ld + co);
-        *(float4*)(p.y + os * p.y_ld + co) = make_float4(v.x + r2.x, v.y + r2.y, v.z + r2.z, v.w + r2.w);
-    }
-}
+// ConvT epilogue geometry (kernels/kokoro.cu:452-467 for the reflection pad).  GEMM row m = phase
+// ph x cout + co of input column t is output column o = stride t + ph - pad; the wave's 64 rows lie in
+// one phase (cout is a multiple of 64).  EPI_CONVT writes y[o] = conv + b + r0[o] for o in the
+// item's output span; EPI_CONVT_REFLECT applies ReflectionPad1d((1,0)) per item on the padded
+// domain (padded[s] = ups[s + 1], padded[s + 1 + j] = ups[s + j]): it writes row o + 1 for
+// o < len - 1, and the item's first row again from o = 1.
+struct ConvTGeo {
+    int64_t os, ol;  // the item's output span (rows written from ups: [os, os + ol))
+    int ph, co;      // this lane's phase and first output channel
+};
 
 // Residual operands a stride-1 epilogue reads per 4 output rows.
 template <int EPI>
@@ -339,14 +329,32 @@ template <int EPI, int WM, int WN, bool STATS, bool OUT_H>
 __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32x16 (&acc)[2][4], int wm, int wn,
                                          int lane, float* scr, const float* bias_s, int next_m0) {
     constexpr bool CONVT = EPI == EPI_CONVT || EPI == EPI_CONVT_REFLECT;
-    constexpr int NR = CONVT ? 0 : kNumRes<EPI>;
+    constexpr int NR = CONVT ? 1 : kNumRes<EPI>;
     constexpr int NRA = NR > 0 ? NR : 1;
-    constexpr int QB = NR > 1 ? 2 : 8;  // column groups per residual batch
+    constexpr int QB = NR > 1 ? 2 : (CONVT ? 4 : 8);  // column groups per residual batch
     const int l32 = lane & 31, lh = lane >> 5;
     const int cq = lane & 15, cg = lane >> 4;
     const int wcol0 = wn * 128;                // this wave's first column within the tile
     const int m = u.m0 + wm * 64 + 4 * cq;     // this lane's 4 output rows after the transpose
     const bool mok = m < p.m;
+    // ConvT: the item's output span (uniform, scalar loads), the lane's phase / channel and bias,
+    // all once per unit
+    ConvTGeo cg_ = {0, 0, 0, 0};
+    float4 cb = make_float4(0.f, 0.f, 0.f, 0.f);
+    if constexpr (CONVT) {
+        cg_.os = ld_const(p.out_start, u.item);
+        cg_.ol = ld_const(p.out_len, u.item) - (EPI == EPI_CONVT_REFLECT ? 1 : 0);
+        const int mm = mok ? m : u.m0;
+        cg_.ph = mm / p.cout, cg_.co = mm - cg_.ph * p.cout;
+        cb = *(const float4*)(p.bias + cg_.co);
+        ready(cb);
+    }
+    // ConvT output column of tile column col, whether this lane writes it, and the row written
+    auto convt_dest = [&](int col, bool& ok) -> int64_t {
+        const int64_t o = (int64_t)p.stride_t * (u.n0 + col) + cg_.ph - p.pad_t;
+        ok = col < u.nv && mok && o >= cg_.os && o < cg_.os + cg_.ol;
+        return ok ? (EPI == EPI_CONVT ? o : o + 1) : cg_.os;
+    };
     // Row pointers at the unit's first row (uniform) and this lane's 32-bit element offsets of its
     // first output row (column wcol0 + cg); row wcol0 + cg + c adds c * ld, one 24-bit multiply
     // with ld held in a VGPR (uniform products of every c would occupy scalar registers).
@@ -377,9 +385,15 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
 #pragma unroll
                 for (int qq = 0; qq < QB; qq++) {
                     const int c = j * 32 + 4 * (q0 + qq);
-                    const bool ok = wcol0 + c + cg < u.nv && mok;
-                    load_res<EPI>(p, eb, ok ? yo0 + __umul24(c, yld) : yz, ok ? ro0 + __umul24(c, rld) : rz,
-                                  ok ? n0 + wcol0 + cg + c : n0, ok ? m : u.m0, res[qq]);
+                    if constexpr (CONVT) {
+                        bool ok;
+                        const int64_t d = convt_dest(wcol0 + c + cg, ok);
+                        res[qq][0] = *(const float4*)(p.r0 + d * p.r0_ld + cg_.co);
+                    } else {
+                        const bool ok = wcol0 + c + cg < u.nv && mok;
+                        load_res<EPI>(p, eb, ok ? yo0 + __umul24(c, yld) : yz, ok ? ro0 + __umul24(c, rld) : rz,
+                                      ok ? n0 + wcol0 + cg + c : n0, ok ? m : u.m0, res[qq]);
+                    }
                 }
 #pragma unroll
                 for (int qq = 0; qq < QB; qq++)
@@ -401,7 +415,17 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
                 // only the store is conditional
                 float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
                 if constexpr (CONVT) {
-                    if (valid && mok) store_convt<EPI>(p, u.item, u.n0 + col, m, v[qq]);
+                    bool ok;
+                    const int64_t d = convt_dest(col, ok);
+                    const float4 w = make_float4(v[qq].x + cb.x, v[qq].y + cb.y, v[qq].z + cb.z, v[qq].w + cb.w);
+                    const float4 r = res[qq][0];
+                    if (ok) *(float4*)(p.y + d * p.y_ld + cg_.co) = make_float4(w.x + r.x, w.y + r.y, w.z + r.z, w.w + r.w);
+                    if (EPI == EPI_CONVT_REFLECT && ok && d == cg_.os + 2) {
+                        // o = os + 1 also fills the item's first row (the reflected sample)
+                        const float4 r2 = *(const float4*)(p.r0 + cg_.os * p.r0_ld + cg_.co);
+                        *(float4*)(p.y + cg_.os * p.y_ld + cg_.co) =
+                            make_float4(w.x + r2.x, w.y + r2.y, w.z + r2.z, w.w + r2.w);
+                    }
                 } else {
                     uint2 pk;  // v = conv + bias (the accumulators started at the bias)
                     o = finish4<EPI, OUT_H>(p, v[qq], res[qq], pk);
