@@ -238,12 +238,30 @@ __global__ __launch_bounds__(256) void noise_conv_kernel(const float* __restrict
     const int64_t t0 = (int64_t)blockIdx.x * kNcRows;
     const int win = (kNcRows - 1) * stride + k;
     const int64_t in0 = t0 * stride - pad;
-    for (int i = threadIdx.x; i < win * 22; i += blockDim.x) {
-        const int r = i / 22, ci = i - r * 22;
-        const int64_t row = in0 + r;
-        float v = 0.f;
-        if (row >= 0 && row < l_in && col_in[row] >= 0) v = spec[row * spec_ld + ci];
-        xs[r][ci] = v;
+    // Stage the input window: every load of a thread is issued before the first is used (rows
+    // clamped into the buffer, the gap / range mask applied afterwards), so the window costs one
+    // memory latency rather than one per element.
+    constexpr int kPer = (kNcMaxWin * 22 + 255) / 256;
+    {
+        float sv[kPer];
+        int cv[kPer];
+#pragma unroll
+        for (int kk = 0; kk < kPer; kk++) {
+            if (kk * 256 >= win * 22) break;  // uniform
+            const int i = threadIdx.x + kk * 256;
+            const int r = i / 22, ci = i - r * 22;
+            const int64_t row = min(max(in0 + r, (int64_t)0), l_in - 1);
+            cv[kk] = col_in[row];
+            sv[kk] = spec[row * spec_ld + ci];
+        }
+#pragma unroll
+        for (int kk = 0; kk < kPer; kk++) {
+            if (kk * 256 >= win * 22) break;
+            const int i = threadIdx.x + kk * 256;
+            const int r = i / 22, ci = i - r * 22;
+            const int64_t row = in0 + r;
+            if (i < win * 22) xs[r][ci] = (row >= 0 && row < l_in && cv[kk] >= 0) ? sv[kk] : 0.f;
+        }
     }
     __syncthreads();
     const int cq = threadIdx.x % CQ, tg = threadIdx.x / CQ;
