@@ -226,7 +226,7 @@ __global__ void adain_pool_kernel(const float* __restrict__ x, int64_t ld, int c
 // ascending, channels ascending within a tap (f32 FMA).
 constexpr int kNcRows = 64;
 constexpr int kNcMaxWin = (kNcRows - 1) * 6 + 12;
-template <int COUT, int TT>
+template <int COUT, int TT, int WIN>
 __global__ __launch_bounds__(256) void noise_conv_kernel(const float* __restrict__ spec, int64_t spec_ld, int64_t l_in,
                                                          const int32_t* __restrict__ col_in,
                                                          const float* __restrict__ wt, const float* __restrict__ b,
@@ -234,14 +234,14 @@ __global__ __launch_bounds__(256) void noise_conv_kernel(const float* __restrict
                                                          int64_t y_ld, int64_t l_out) {
     constexpr int CQ = COUT / 4, TG = 256 / CQ;
     static_assert(TG * TT == kNcRows, "rows per block");
-    __shared__ float xs[kNcMaxWin][22];
+    __shared__ float xs[WIN][22];  // the input window (its size sets how many blocks share a CU)
     const int64_t t0 = (int64_t)blockIdx.x * kNcRows;
     const int win = (kNcRows - 1) * stride + k;
     const int64_t in0 = t0 * stride - pad;
     // Stage the input window: every load of a thread is issued before the first is used (rows
     // clamped into the buffer, the gap / range mask applied afterwards), so the window costs one
     // memory latency rather than one per element.
-    constexpr int kPer = (kNcMaxWin * 22 + 255) / 256;
+    constexpr int kPer = (WIN * 22 + 255) / 256;
     {
         float sv[kPer];
         int cv[kPer];
@@ -584,14 +584,20 @@ hipError_t launch_adain_pool(const float* x, int64_t ld, int c, const Coef* coef
 hipError_t launch_noise_conv(const float* spec, int64_t spec_ld, int64_t l_in, const int32_t* col_in, const float* wt,
                              const float* b, int cout, int k, int stride, int pad, float* y, int64_t y_ld,
                              int64_t l_out, hipStream_t s) {
-    if ((kNcRows - 1) * stride + k > kNcMaxWin) return hipErrorInvalidValue;
+    const int win = (kNcRows - 1) * stride + k;
+    if (win > kNcMaxWin) return hipErrorInvalidValue;
     const dim3 grid(blocks_for(l_out, kNcRows));
+    // noise_convs.0 (k 12, stride 6) stages a 390-row window; noise_convs.1 (k 1) 64 rows, small
+    // enough for 16 blocks per CU
     if (cout == 256)
-        hipLaunchKernelGGL((noise_conv_kernel<256, 16>), grid, dim3(256), 0, s, spec, spec_ld, l_in, col_in, wt, b, k,
-                           stride, pad, y, y_ld, l_out);
+        hipLaunchKernelGGL((noise_conv_kernel<256, 16, kNcMaxWin>), grid, dim3(256), 0, s, spec, spec_ld, l_in, col_in,
+                           wt, b, k, stride, pad, y, y_ld, l_out);
+    else if (cout == 128 && win <= kNcRows)
+        hipLaunchKernelGGL((noise_conv_kernel<128, 8, kNcRows>), grid, dim3(256), 0, s, spec, spec_ld, l_in, col_in, wt,
+                           b, k, stride, pad, y, y_ld, l_out);
     else if (cout == 128)
-        hipLaunchKernelGGL((noise_conv_kernel<128, 8>), grid, dim3(256), 0, s, spec, spec_ld, l_in, col_in, wt, b, k,
-                           stride, pad, y, y_ld, l_out);
+        hipLaunchKernelGGL((noise_conv_kernel<128, 8, kNcMaxWin>), grid, dim3(256), 0, s, spec, spec_ld, l_in, col_in,
+                           wt, b, k, stride, pad, y, y_ld, l_out);
     else
         return hipErrorInvalidValue;
     return hipGetLastError();
