@@ -112,9 +112,10 @@ struct Slot {
     float4 k01, k23;  // AdaIN coefficients (sc, sh) of channels c..c+1 and c+2..c+3
     float4 ar, ai;    // Snake alpha / (2 pi) and 1 / alpha
 
-    // Slab (u, c0): row in0 + r (r = rr + j RP) is read clamped into the item's rows and channel c0 + q
-    // as channel 0 past cin (the conversion zeroes both).  Addresses are 32-bit byte offsets from
-    // the item's first row (a uniform base), one clamp and one 24-bit multiply-add per row.
+    // Slab (u, c0): row in0 + r (r = rr + j RP < tw) is read clamped into the item's rows and
+    // channel c0 + q as channel 0 past cin (the conversion zeroes both).  Addresses are 32-bit byte
+    // offsets from the item's first row (a uniform base), one clamp and one 24-bit multiply-add per
+    // row.
     __device__ __forceinline__ void load(const ConvParams& p, const Unit& u, int c0, int tw, int q, int rr) {
         const int c = c0 + q;
         const int cl = c < p.cin ? c : 0;
@@ -124,7 +125,8 @@ struct Slot {
         const int r0 = u.in0 - u.i_lo, rmax = u.i_hi - 1 - u.i_lo;  // row offsets from the item start
 #pragma unroll
         for (int j = 0; j < RB; j++) {
-            const int r = rr + j * RP;
+            // rows past the slab's window re-read its first row (a cache hit, no HBM traffic)
+            const int r = rr + j * RP < tw ? rr + j * RP : 0;
             const uint32_t row = (uint32_t)max(min(r0 + r, rmax), 0);
             const uint32_t off = (__umul24(row, ld) + (uint32_t)cl) * ES;
             if constexpr (WIDE) {
