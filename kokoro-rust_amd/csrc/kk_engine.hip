@@ -128,7 +128,7 @@ struct MResblk {
     int din = 0, dout = 0;
 };
 struct MNoiseConv {
-    DevBuf w, b;
+    DevBuf w, b, wp;  // wp: f32 matrix-core packing (noise_convs.0)
     int cout = 0, k = 0, stride = 1, pad = 0;
 };
 struct Model {
@@ -330,6 +330,18 @@ static void load_model(kk_ctx* ctx, const kk_tensor* tensors, int n) {
                     wt[((size_t)kk * 22 + ci) * c.cout + co] = w[((size_t)co * 22 + ci) * c.k + kk];
         c.w.upload(wt);
         c.b.upload(t.get(p + ".bias", c.cout), c.cout);
+        if (c.cout == 256 && c.k == 12 && c.stride == 6) {
+            // [32-row tile mt][h][row i][tap][cp < 11, one pad] = W[32 mt + i][channel 2 cp + h][tap]
+            std::vector<float> wp((size_t)c.cout * 2 * 12 * 12, 0.f);
+            for (int mt = 0; mt < c.cout / 32; mt++)
+                for (int h = 0; h < 2; h++)
+                    for (int i = 0; i < 32; i++)
+                        for (int kk = 0; kk < 12; kk++)
+                            for (int cp = 0; cp < 11; cp++)
+                                wp[((((size_t)mt * 2 + h) * 32 + i) * 12 + kk) * 12 + cp] =
+                                    w[((size_t)(32 * mt + i) * 22 + 2 * cp + h) * c.k + kk];
+            c.wp.upload(wp);
+        }
     }
     load_snake(m.noise_res[0], t, g + ".noise_res.0", 256, 7, sr);
     load_snake(m.noise_res[1], t, g + ".noise_res.1", 128, 11, sr);
@@ -994,7 +1006,8 @@ struct Runner {
         // xs = noise_res[i](noise_convs[i](masked spec)) (src/gpu_batch.rs:362-375)
         const MNoiseConv& nc = m.nc[i];
         KK_LAUNCH(launch_noise_conv(p->spec.as<float>(), kSpecLd, p->d120.l, p->d120.col_d.as<int32_t>(),
-                                 nc.w.as<float>(), nc.b.as<float>(), nc.cout, nc.k, nc.stride, nc.pad, B[1], c,
+                                 nc.w.as<float>(), nc.wp.p ? nc.wp.as<float>() : nullptr, nc.b.as<float>(), nc.cout,
+                                 nc.k, nc.stride, nc.pad, B[1], c,
                                  dout.l, s));
         launches++;
         snake_block(m.noise_res[i], B[1], B[2], dout);

@@ -290,6 +290,121 @@ __global__ __launch_bounds__(256) void noise_conv_kernel(const float* __restrict
     }
 }
 
+// noise_convs.0 (22 -> 256, k 12, stride 6) on the f32 matrix cores (v_mfma_f32_32x32x2_f32:
+// exact f32 products, f32 accumulation, like the reference's f32 sgemm route).  GEMM view per
+// block: 256 output channels x 64 output columns, K = 12 taps x 22 channels = 264 in steps of 2
+// (tap, channel pair).  Wave w owns channels 64 w .. 64 w + 63 (2 x 2 tiles of 32 x 32).
+//   A (weights) lane (i = l % 32, h = l / 32) of step (tap, cp): W[row i][channel 2 cp + h][tap],
+//     pre-packed as [32-row tile][h][i][tap][12] (cp < 11, one pad) so a tap is three float4 per lane;
+//   B (input window in LDS, channel-major) lane (j, h): x[channel 2 cp + h][row 6 j + tap].
+// Accumulators start at the bias; the epilogue stores each lane's 4 consecutive channels.
+constexpr int kNc0Win = (kNcRows - 1) * 6 + 12;  // 390 input rows per 64 output columns
+constexpr int kNc0Ld = kNc0Win + 2;               // channel-major window row stride (floats)
+__global__ __launch_bounds__(256) void noise_conv0_mfma_kernel(const float* __restrict__ spec, int64_t spec_ld,
+                                                               int64_t l_in, const int32_t* __restrict__ col_in,
+                                                               const float4* __restrict__ wp, const float* __restrict__ b,
+                                                               int pad, float* __restrict__ y, int64_t y_ld,
+                                                               int64_t l_out) {
+    typedef float f32x16 __attribute__((ext_vector_type(16)));
+    __shared__ float xs[22 * kNc0Ld];
+    const int64_t t0 = (int64_t)blockIdx.x * kNcRows;
+    const int64_t in0 = t0 * 6 - pad;
+    // the window in batches of 12 loads per thread, each batch in flight before its first use (rows
+    // clamped, the gap / range mask applied afterwards)
+    constexpr int kPer = (kNc0Win * 22 + 255) / 256, kBatch = 12;
+#pragma unroll 1
+    for (int k0 = 0; k0 < kPer; k0 += kBatch) {
+        float sv[kBatch];
+        int cv[kBatch];
+#pragma unroll
+        for (int kk = 0; kk < kBatch; kk++) {
+            const int i = min((int)threadIdx.x + (k0 + kk) * 256, kNc0Win * 22 - 1);
+            const int r = i / 22, ci = i - r * 22;
+            const int64_t row = min(max(in0 + r, (int64_t)0), l_in - 1);
+            cv[kk] = col_in[row];
+            sv[kk] = spec[row * spec_ld + ci];
+        }
+#pragma unroll
+        for (int kk = 0; kk < kBatch; kk++) {
+            const int i = threadIdx.x + (k0 + kk) * 256;
+            if (i < kNc0Win * 22) {
+                const int r = i / 22, ci = i - r * 22;
+                const int64_t row = in0 + r;
+                xs[ci * kNc0Ld + r] = (row >= 0 && row < l_in && cv[kk] >= 0) ? sv[kk] : 0.f;
+            }
+        }
+    }
+    __syncthreads();
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, l32 = lane & 31, h = lane >> 5;
+    f32x16 acc[2][2];
+#pragma unroll
+    for (int mi = 0; mi < 2; mi++) {
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            const float4 bv = *(const float4*)(b + wave * 64 + mi * 32 + 8 * g + 4 * h);
+#pragma unroll
+            for (int ni = 0; ni < 2; ni++) {
+                acc[mi][ni][4 * g] = bv.x, acc[mi][ni][4 * g + 1] = bv.y;
+                acc[mi][ni][4 * g + 2] = bv.z, acc[mi][ni][4 * g + 3] = bv.w;
+            }
+        }
+    }
+    // this lane's weights: tile 2 wave + mi, half h, row l32; per tap 12 floats (11 channel pairs
+    // and a pad), three float4
+    const float4* wa[2];
+#pragma unroll
+    for (int mi = 0; mi < 2; mi++) wa[mi] = wp + ((int64_t)((2 * wave + mi) * 2 + h) * 32 + l32) * 36;
+    const float* xb = xs + h * kNc0Ld + 6 * l32;  // channel h, output column l32 (ni = 0)
+    // Tap by tap: the next tap's weights are in flight while this tap's 11 steps (44 MFMAs per
+    // wave) run; scheduling barriers keep the loads where they are issued.
+    float4 ac[2][3], an[2][3];
+#pragma unroll
+    for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+        for (int q = 0; q < 3; q++) ac[mi][q] = wa[mi][q];
+#pragma unroll 1
+    for (int tap = 0; tap < 12; tap++) {
+        const int tn = min(tap + 1, 11);
+#pragma unroll
+        for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+            for (int q = 0; q < 3; q++) an[mi][q] = wa[mi][3 * tn + q];
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int cp = 0; cp < 11; cp++) {
+            const float* xp = xb + 2 * cp * kNc0Ld + tap;
+            const float b0 = xp[0], b1 = xp[6 * 32];
+#pragma unroll
+            for (int mi = 0; mi < 2; mi++) {
+                const float4 a4 = ac[mi][cp / 4];
+                const float av = cp % 4 == 0 ? a4.x : cp % 4 == 1 ? a4.y : cp % 4 == 2 ? a4.z : a4.w;
+                acc[mi][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(av, b0, acc[mi][0], 0, 0, 0);
+                acc[mi][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(av, b1, acc[mi][1], 0, 0, 0);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+            for (int q = 0; q < 3; q++) ac[mi][q] = an[mi][q];
+    }
+    // D layout: element 4 g + r of tile (mi, ni) is channel 64 wave + 32 mi + 8 g + 4 h + r of
+    // output column t0 + 32 ni + l32
+#pragma unroll
+    for (int ni = 0; ni < 2; ni++) {
+        const int64_t col = t0 + 32 * ni + l32;
+        if (col < l_out) {
+#pragma unroll
+            for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+                for (int g = 0; g < 4; g++)
+                    *(float4*)(y + col * y_ld + wave * 64 + mi * 32 + 8 * g + 4 * h) =
+                        make_float4(acc[mi][ni][4 * g], acc[mi][ni][4 * g + 1], acc[mi][ni][4 * g + 2],
+                                    acc[mi][ni][4 * g + 3]);
+        }
+    }
+}
+
 // ------------------------------------------------------------------ SineGen (kernels/kokoro.cu:188-254)
 __device__ __forceinline__ float remainder1(float a) {
     float m = fmodf(a, 1.0f);
@@ -582,11 +697,18 @@ hipError_t launch_adain_pool(const float* x, int64_t ld, int c, const Coef* coef
 }
 
 hipError_t launch_noise_conv(const float* spec, int64_t spec_ld, int64_t l_in, const int32_t* col_in, const float* wt,
-                             const float* b, int cout, int k, int stride, int pad, float* y, int64_t y_ld,
-                             int64_t l_out, hipStream_t s) {
+                             const float* wp, const float* b, int cout, int k, int stride, int pad, float* y,
+                             int64_t y_ld, int64_t l_out, hipStream_t s) {
     const int win = (kNcRows - 1) * stride + k;
     if (win > kNcMaxWin) return hipErrorInvalidValue;
     const dim3 grid(blocks_for(l_out, kNcRows));
+    if (wp) {
+        // the matrix-core path: noise_convs.0's shape only, weights packed by pack_noise_conv0
+        if (cout != 256 || k != 12 || stride != 6) return hipErrorInvalidValue;
+        hipLaunchKernelGGL(noise_conv0_mfma_kernel, grid, dim3(256), 0, s, spec, spec_ld, l_in, col_in,
+                           (const float4*)wp, b, pad, y, y_ld, l_out);
+        return hipGetLastError();
+    }
     // noise_convs.0 (k 12, stride 6) stages a 390-row window; noise_convs.1 (k 1) 64 rows, small
     // enough for 16 blocks per CU
     if (cout == 256)
