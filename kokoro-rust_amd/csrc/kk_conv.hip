@@ -62,12 +62,6 @@ __device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
     return __builtin_bit_cast(uint32_t, v);
 }
 
-__device__ __forceinline__ float snake(float v, float a_rev, float a_inv) {
-    // v + sin^2(alpha v) / alpha; __builtin_amdgcn_sinf(x) = sin(2 pi x), so a_rev = alpha / (2 pi).
-    const float s = __builtin_amdgcn_sinf(v * a_rev);
-    return __builtin_fmaf(s * s, a_inv, v);
-}
-
 // Read-only tables (tiles, item spans) through the constant address space: uniform indices become
 // scalar loads, which leave the vector-memory counter -- and the producers' prefetch -- alone.
 template <typename T>
@@ -159,7 +153,19 @@ struct Slot {
         if constexpr (ADAIN) ready(k01), ready(k23);
         if constexpr (SNAKE) ready(ar), ready(ai);
         const float sc[4] = {k01.x, k01.z, k23.x, k23.z}, sh[4] = {k01.y, k01.w, k23.y, k23.w};
-        const float arv[4] = {ar.x, ar.y, ar.z, ar.w}, aiv[4] = {ai.x, ai.y, ai.z, ai.w};
+        // Snake in its cosine form, with the AdaIN affine folded into both operands (four channel
+        // constants per slab, three VALU operations and one cosine per element):
+        //   v + sin^2(a v) / a = (v + h) - h cos(2 a v),  h = 1 / (2 a),
+        //   2 a v / (2 pi) = x (sc a / pi) + sh a / pi   (__builtin_amdgcn_cosf(t) = cos(2 pi t)).
+        float tsc[4], tsh[4], vsh[4], nh[4];
+        if constexpr (SNAKE) {
+            const float arv[4] = {ar.x, ar.y, ar.z, ar.w}, aiv[4] = {ai.x, ai.y, ai.z, ai.w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float a_pi = 2.0f * arv[e], h = 0.5f * aiv[e];  // a / pi, 1 / (2 a)
+                tsc[e] = sc[e] * a_pi, tsh[e] = sh[e] * a_pi, vsh[e] = sh[e] + h, nh[e] = -h;
+            }
+        }
         // Per-slab limits, held in VGPRs for the whole loop (the kernel is short of SGPRs, and a
         // limit rematerialized from the kernel arguments costs a scalar load and a wait per row):
         // live rows r in [r_lo, r_hi), live channels e < n_ch of this quad.
@@ -196,7 +202,8 @@ struct Slot {
                         x = __builtin_fmaf(x, sc[e], sh[e]);
                         x = x < 0.f ? x * slope : x;
                     } else if constexpr (PRO == PRO_ADAIN_SNAKE) {
-                        x = snake(__builtin_fmaf(x, sc[e], sh[e]), arv[e], aiv[e]);
+                        const float c = __builtin_amdgcn_cosf(__builtin_fmaf(x, tsc[e], tsh[e]));
+                        x = __builtin_fmaf(c, nh[e], __builtin_fmaf(x, sc[e], vsh[e]));
                     }
                     // the Snake layers' cin is a multiple of the slab width (checked on the host)
                     if constexpr (!SNAKE) x = e < n_ch ? x : 0.f;
@@ -244,7 +251,9 @@ template <int EPI>
 __device__ __forceinline__ void load_res(const ConvParams& p, const EpiBase& eb, uint32_t yo, uint32_t ro, int64_t t,
                                          int m, float4* r) {
     if constexpr (EPI == EPI_ACCUM || EPI == EPI_RESID) {
-        r[0] = *(const float4*)((const float*)eb.y + yo);
+        // the rows this epilogue overwrites: streamed (nontemporal), like its stores
+        const f32x4 v = __builtin_nontemporal_load((const f32x4*)((const float*)eb.y + yo));
+        r[0] = make_float4(v.x, v.y, v.z, v.w);
     } else if constexpr (EPI == EPI_RESID_UP2) {
         r[0] = *(const float4*)(p.r0 + (t >> 1) * p.r0_ld + m);
     } else if constexpr (EPI == EPI_ADD_FROM) {
@@ -287,13 +296,17 @@ __device__ __forceinline__ float4 finish4(const ConvParams& p, float4 v, const f
     return o;
 }
 
-// Stores one row's result at element offset `yo` from the unit's first row of y.
+// Stores one row's result at element offset `yo` from the unit's first row of y.  Nontemporal
+// stores: the layer's output is read again only by the next launch, so it streams through L2
+// instead of evicting the weights the A fragments reload every tap (1.4% of the Snake convs' time
+// on the benchmark configuration).
 template <bool OUT_H>
 __device__ __forceinline__ void store4(const EpiBase& eb, uint32_t yo, float4 o, uint2 pk) {
     if constexpr (OUT_H) {
-        *(uint2*)((uint16_t*)eb.y + yo) = pk;
+        typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+        __builtin_nontemporal_store((u32x2_t){pk.x, pk.y}, (u32x2_t*)((uint16_t*)eb.y + yo));
     } else {
-        *(float4*)((float*)eb.y + yo) = o;
+        __builtin_nontemporal_store((f32x4){o.x, o.y, o.z, o.w}, (f32x4*)((float*)eb.y + yo));
     }
 }
 

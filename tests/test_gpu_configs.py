@@ -3,8 +3,9 @@
 - Config 1 (generator only, one item of 100 decoder frames): against the fp32 oracle.
 - Config 2 (one 256-channel k7 Snake block, 16 ragged items of 500-2000 columns): the whole batch
   on the GPU; the three shortest items against the bf16-emulated oracle (the block's increment,
-  >= 55 dB) and the fp32 oracle (>= 40 dB); the longest item alone is bit-identical to its copy in
-  the batch.
+  >= 50 dB: the emulation's own floor against a copy of itself with one more fp16 rounding point
+  is 54.6-55 dB here) and the fp32 oracle (>= 40 dB); the longest item alone is bit-identical to
+  its copy in the batch.
 - Config 5 (128 items, generator frames log-uniform in [80, 4000], ~27 GiB of plan): size-
   independent properties at full size: every item finite with the right length, two items (the
   shortest and the longest) bit-identical to runs of themselves alone, and the shortest against
@@ -64,7 +65,7 @@ def test_config2_snake_block(gpu_ctx, oracle_model):
         with O.bf16_emulation():
             emu = oracle_model.snake_block(prefix, x, s)
         _print("  T", x.shape[1], "fp32 snr", snr_db(ref - x, y - x), "emu snr", snr_db(emu - x, y - x))
-        assert snr_db(emu - x, y - x) >= 55.0
+        assert snr_db(emu - x, y - x) >= 50.0
         assert snr_db(ref - x, y - x) >= 40.0
     j = int(order[-1])
     with api.Plan.snake(gpu_ctx, prefix, [xs[j]], [styles[j]], gap=40) as plan:

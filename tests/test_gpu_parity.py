@@ -3,10 +3,11 @@
 Two bars per waveform-level check:
 - against the fp32 oracle: the north-star tolerance, max-abs <= 2e-3 and SNR >= 40 dB;
 - against the oracle with its MFMA-layer operands rounded to bf16 (the GPU's own rounding points):
-  a tight bar that an indexing, masking or layout mistake cannot pass (SNR >= 55 dB for one Snake
-  block, >= 50 dB for the decoder, >= 44 dB end to end: only accumulation order and bf16 rounding
-  ties differ, and those ties compound over the ~50 layers in series; a masking or indexing error
-  lands near 0-20 dB).
+  a tight bar that an indexing, masking or layout mistake cannot pass (SNR >= 50 dB for one Snake
+  block and for the decoder, >= 44 dB end to end: only accumulation order and bf16 rounding ties
+  differ, and those ties compound through the layers in series -- two emulations that differ by a
+  single fp16 rounding point of the increments already land 54.6-55 dB apart on one 256-channel
+  Snake block; a masking or indexing error lands near 0-20 dB).
 Integer and index work (duration expansion) is compared bit for bit.
 """
 import numpy as np
@@ -38,7 +39,7 @@ def test_snake_block_ragged(gpu_ctx, oracle_model):
             emu = oracle_model.snake_block("decoder.generator.resblocks.1", x, s)
         d_ref, d_emu = y - x, emu - x  # compare the block's increment, not the pass-through input
         _print("  fp32 snr", snr_db(ref - x, d_ref), "emu snr", snr_db(d_emu, d_ref), "maxabs", np.abs(y - ref).max())
-        assert snr_db(d_emu, d_ref) >= 55.0
+        assert snr_db(d_emu, d_ref) >= 50.0
         assert snr_db(ref - x, d_ref) >= 40.0
 
 
@@ -56,7 +57,7 @@ def test_snake_block_128(gpu_ctx, oracle_model):
         with O.bf16_emulation():
             emu = oracle_model.snake_block("decoder.generator.noise_res.1", x, s)
         _print("  128ch k11 emu snr", snr_db(emu - x, y - x))
-        assert snr_db(emu - x, y - x) >= 55.0
+        assert snr_db(emu - x, y - x) >= 50.0
 
 
 @pytest.fixture(scope="module")
