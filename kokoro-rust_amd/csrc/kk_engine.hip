@@ -460,6 +460,15 @@ struct kk_plan {
     double conv_flop = 0, snake_flop = 0;
     int64_t launches = 0;
     int last_until = 0;
+    // The launch sequence of kk_plan_run(until = graph_until), captured on its second run with that
+    // stage and replayed from then on (every buffer and tile list is fixed at plan creation).
+    hipGraphExec_t graph = nullptr;
+    int graph_until = -1;
+    int eager_until = -1;  // stage of the last eager run
+    void drop_graph() {
+        if (graph) (void)hipGraphExecDestroy(graph);
+        graph = nullptr, graph_until = -1;
+    }
     std::vector<kk::DevBuf*> owned() {
         return {&t_en, &src_row, &f0, &en, &style, &seeds, &kinds, &rand_ini, &fixed_noise, &gb, &xcat, &xin_a,
                 &xin_b, &hdec, &pool, &sc_half, &dec_out, &pp, &spec, &B[0], &B[1], &B[2], &B[3], &B[4], &B[5],
@@ -1070,6 +1079,7 @@ static void prebuild_tiles(kk_plan* p) {
 }
 
 static void release_plan_device(kk_plan* p) {
+    p->drop_graph();
     for (DevBuf* b : p->owned()) b->release();
     for (kk::Dom* d : {&p->dn, &p->d2, &p->d20, &p->d120, &p->ds}) {
         d->col_d.release();
@@ -1225,9 +1235,38 @@ int kk_plan_run(kk_plan* plan, int until, char* err, size_t errlen) {
     return guard(err, errlen, [&] {
         use_device(plan->ctx);
         check(plan->ctx->model.ready, "no model uploaded");
-        Runner r{plan, plan->ctx, plan->ctx->model, plan->ctx->stream};
-        r.run(until);
-        plan->conv_flop = r.flop, plan->snake_flop = r.snake_flop, plan->launches = r.launches;
+        hipStream_t s = plan->ctx->stream;
+        Runner r{plan, plan->ctx, plan->ctx->model, s};
+        // Per-launch profiling records events between the kernels: those runs stay eager.
+        const bool graphs = !plan->ctx->profiling;
+        if (graphs && plan->graph && plan->graph_until == until) {
+            KK_HIP(hipGraphLaunch(plan->graph, s));  // counters stay those of the captured run
+        } else if (graphs && plan->eager_until == until) {
+            // second run of this stage: capture it (the first, eager run has set every kernel
+            // attribute and surfaced any launch error) and replay the graph from now on
+            plan->drop_graph();
+            hipGraph_t g = nullptr;
+            KK_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+            try {
+                r.run(until);
+            } catch (...) {
+                (void)hipStreamEndCapture(s, &g);
+                if (g) (void)hipGraphDestroy(g);
+                throw;
+            }
+            KK_HIP(hipStreamEndCapture(s, &g));
+            hipGraphExec_t e = nullptr;
+            const hipError_t ie = hipGraphInstantiate(&e, g, nullptr, nullptr, 0);
+            (void)hipGraphDestroy(g);
+            KK_HIP(ie);
+            plan->graph = e, plan->graph_until = until;
+            KK_HIP(hipGraphLaunch(e, s));
+            plan->conv_flop = r.flop, plan->snake_flop = r.snake_flop, plan->launches = r.launches;
+        } else {
+            r.run(until);
+            plan->eager_until = until;
+            plan->conv_flop = r.flop, plan->snake_flop = r.snake_flop, plan->launches = r.launches;
+        }
         plan->last_until = until;
     });
 }
@@ -1336,6 +1375,7 @@ void kk_plan_free(kk_plan* plan) {
     if (plan->ctx) {  // an orphan's device memory went with its context (kk_close)
         (void)hipSetDevice(plan->ctx->device);
         (void)hipStreamSynchronize(plan->ctx->stream);
+        plan->drop_graph();
         plan->ctx->plans.erase(plan);
     }
     delete plan;

@@ -97,17 +97,22 @@ def _run(ctx, items):
 
 
 def test_rerun_and_one_shot_bit_identical(gpu_ctx):
+    """Run 1 is eager, run 2 captures the launch sequence into a HIP graph, later runs replay it;
+    another plan's eager run and an eager stage run sit between replays."""
     from kokoro_hip import api, workloads
     items = workloads.small_items(61, [11, 5, 17])
     with api.Plan.decoder(gpu_ctx, items) as plan:
-        plan.run()
-        a = plan.fetch()
-        plan.run()
-        plan.run()
-        b = plan.fetch()
+        runs = []
+        for i in range(4):
+            plan.run()
+            runs.append(plan.fetch())
+            if i == 2:
+                _run(gpu_ctx, workloads.small_items(60, [6, 9]))
+                plan.run(until="gen0")
     c = gpu_ctx.forward_decoder_batch(items)
-    for x, y, z in zip(a, b, c):
-        assert np.array_equal(x, y) and np.array_equal(x, z)
+    for r in runs[1:] + [c]:
+        for x, y in zip(runs[0], r):
+            assert np.array_equal(x, y)
 
 
 def test_item_independent_of_batch(gpu_ctx):
