@@ -271,13 +271,11 @@ __device__ __forceinline__ void load_res(const ConvParams& p, const EpiBase& eb,
 template <int EPI, bool OUT_H>
 __device__ __forceinline__ float4 finish4(const ConvParams& p, float4 v, const float4* r, uint2& pk) {
     if constexpr (OUT_H) {
-        // fp16 storage; the statistics use the f32 values (the fp16 rounding moves the mean and
-        // variance by ~2^-12 relative, far below the next layer's bf16 operand rounding)
+        // fp16 storage; the statistics use the f32 values, as the reference's f32 h does (the fp16
+        // rounding would move the mean and variance by ~2^-12 relative, far below the next
+        // layer's bf16 operand rounding)
         pk = make_uint2(pack_f16x2(v.x, v.y), pack_f16x2(v.z, v.w));
-        return make_float4((float)__builtin_bit_cast(_Float16, (uint16_t)(pk.x & 0xffffu)),
-                           (float)__builtin_bit_cast(_Float16, (uint16_t)(pk.x >> 16)),
-                           (float)__builtin_bit_cast(_Float16, (uint16_t)(pk.y & 0xffffu)),
-                           (float)__builtin_bit_cast(_Float16, (uint16_t)(pk.y >> 16)));
+        return v;
     }
     float4 o = v;
     if constexpr (EPI == EPI_ACCUM || EPI == EPI_ADD_FROM) {
