@@ -152,6 +152,22 @@ typedef struct {
 int kk_plan_get_info(const kk_plan* plan, kk_plan_info* info);
 void kk_plan_free(kk_plan* plan);
 
+/* ------------------------------------------------------------------ output formats (src/wav.rs)
+ * PCM_16 encoding of the last run's audio on the device (wav::encode, src/wav.rs:63-80): per
+ * sample v = round_ties_even(s * 32767) in f32; values outside [-32768, 32767] (NaN and the
+ * infinities included) are clamped and counted, NaN stores 0.  dst[b] receives item b's 600 N_b
+ * samples; clipped (optional) its count.  Half the bytes of kk_plan_fetch over PCIe. */
+int kk_plan_fetch_pcm16(kk_plan* plan, int16_t* const* dst, int64_t* clipped, char* err, size_t errlen);
+/* The same encoding of a host array (uploads, encodes on the device, downloads). */
+int kk_encode_pcm16(kk_ctx* ctx, const float* audio, int64_t n, int16_t* out, int64_t* clipped, char* err,
+                    size_t errlen);
+/* The canonical 44-byte mono RIFF/WAVE header (wav::header, src/wav.rs:43-61): format tag 1
+ * (PCM_16) or 3 (IEEE float32); data_bytes above 2^32 - 1 - 36 is refused (check_riff_size,
+ * src/wav.rs:34-40), never wrapped. */
+#define KK_WAV_PCM16 0
+#define KK_WAV_FLOAT32 1
+int kk_wav_header(int format, uint32_t sample_rate, uint64_t data_bytes, uint8_t* out, char* err, size_t errlen);
+
 /* ------------------------------------------------------------------ measurement
  * With profiling on, kk_plan_run brackets every MFMA conv launch with HIP events on the
  * context's stream; kk_profile_read reports, per kernel class, the summed event time and the

@@ -455,6 +455,7 @@ struct kk_plan {
         return *it->second;
     }
     kk::DevBuf src_item, src_f0, ist_item, ist_s0;
+    kk::DevBuf pcm, pcm_len, pcm_clip;  // PCM_16 output: samples [600 ln], samples per item, clip counts
     int64_t n_src = 0, n_ist = 0;
     int64_t dev_bytes = 0;
     double conv_flop = 0, snake_flop = 0;
@@ -473,7 +474,7 @@ struct kk_plan {
         return {&t_en, &src_row, &f0, &en, &style, &seeds, &kinds, &rand_ini, &fixed_noise, &gb, &xcat, &xin_a,
                 &xin_b, &hdec, &pool, &sc_half, &dec_out, &pp, &spec, &B[0], &B[1], &B[2], &B[3], &B[4], &B[5],
                 &post, &audio, &audio_start, &part, &coef[0], &coef[1], &coef[2], &coef[3], &coef[4], &src_item,
-                &src_f0, &ist_item, &ist_s0};
+                &src_f0, &ist_item, &ist_s0, &pcm, &pcm_len, &pcm_clip};
     }
 };
 
@@ -570,9 +571,12 @@ static void setup_generator(kk_plan* p, const std::vector<const float*>& f0s, co
     }
     p->n_src = (int64_t)si.size(), p->n_ist = (int64_t)ii.size();
     p->src_item.upload(si), p->src_f0.upload(sf), p->ist_item.upload(ii), p->ist_s0.upload(is);
-    std::vector<int64_t> as(nb);
-    for (int b = 0; b < nb; b++) as[b] = 600 * p->a[b];
+    std::vector<int64_t> as(nb), ns(nb);
+    for (int b = 0; b < nb; b++) as[b] = 600 * p->a[b], ns[b] = 600 * p->nfr[b];
     p->audio_start.upload(as);
+    p->pcm_len.upload(ns);
+    p->pcm.alloc((size_t)600 * ln * sizeof(int16_t));
+    p->pcm_clip.alloc((size_t)nb * sizeof(unsigned long long));
 
     p->gb.alloc((size_t)nb * p->ctx->model.style_rows * sizeof(float));
     p->pp.alloc((size_t)kHarmonics * l2 * sizeof(float));
@@ -1313,6 +1317,84 @@ int kk_plan_fetch(kk_plan* plan, kk_output* out, char* err, size_t errlen) {
     });
     if (rc != KK_OK) kk_output_free(out, plan->nb);
     return rc;
+}
+
+int kk_plan_fetch_pcm16(kk_plan* plan, int16_t* const* dst, int64_t* clipped, char* err, size_t errlen) {
+    if (!plan || !dst) return KK_ERR_INVALID;
+    if (!plan->ctx) {
+        set_err(err, errlen, "plan outlived its context");
+        return KK_ERR_STATE;
+    }
+    return guard(err, errlen, [&] {
+        use_device(plan->ctx);
+        check(plan->kind != PLAN_SNAKE, "a snake plan has no audio");
+        check(plan->last_until >= KK_STAGE_ALL, "plan has not run to the end");
+        for (int b = 0; b < plan->nb; b++) check(dst[b] != nullptr, "null destination for item " + std::to_string(b));
+        hipStream_t s = plan->ctx->stream;
+        KK_HIP(launch_zero(plan->pcm_clip.p, (int64_t)plan->nb * 8, s));
+        KK_HIP(launch_pcm16(plan->audio.as<float>(), plan->audio_start.as<int64_t>(), plan->pcm_len.as<int64_t>(),
+                            plan->ist_item.as<int64_t>(), plan->ist_s0.as<int64_t>(), plan->n_ist,
+                            plan->pcm.as<int16_t>(), plan->pcm_clip.as<unsigned long long>(), s));
+        KK_HIP(hipStreamSynchronize(s));
+        for (int b = 0; b < plan->nb; b++)
+            KK_HIP(hipMemcpy(dst[b], plan->pcm.as<int16_t>() + 600 * plan->a[b], sizeof(int16_t) * 600 * plan->nfr[b],
+                             hipMemcpyDeviceToHost));
+        if (clipped) {
+            std::vector<unsigned long long> c(plan->nb);
+            KK_HIP(hipMemcpy(c.data(), plan->pcm_clip.p, sizeof(unsigned long long) * plan->nb, hipMemcpyDeviceToHost));
+            for (int b = 0; b < plan->nb; b++) clipped[b] = (int64_t)c[b];
+        }
+    });
+}
+
+int kk_encode_pcm16(kk_ctx* ctx, const float* audio, int64_t n, int16_t* out, int64_t* clipped, char* err,
+                    size_t errlen) {
+    if (!ctx || n < 0 || (n > 0 && (!audio || !out))) return KK_ERR_INVALID;
+    return guard(err, errlen, [&] {
+        use_device(ctx);
+        DevBuf a, o, len, clip;
+        a.upload(audio, (size_t)n);
+        o.alloc((size_t)n * sizeof(int16_t));
+        const int64_t nn[1] = {n};
+        len.upload(nn, 1);
+        clip.alloc(sizeof(unsigned long long));
+        KK_HIP(launch_zero(clip.p, 8, ctx->stream));
+        KK_HIP(launch_pcm16(a.as<float>(), nullptr, len.as<int64_t>(), nullptr, nullptr, ceil_div(n, kIstftSamples),
+                            o.as<int16_t>(), clip.as<unsigned long long>(), ctx->stream));
+        KK_HIP(hipStreamSynchronize(ctx->stream));
+        if (n) KK_HIP(hipMemcpy(out, o.p, sizeof(int16_t) * n, hipMemcpyDeviceToHost));
+        unsigned long long c = 0;
+        KK_HIP(hipMemcpy(&c, clip.p, sizeof(c), hipMemcpyDeviceToHost));
+        if (clipped) *clipped = (int64_t)c;
+    });
+}
+
+int kk_wav_header(int format, uint32_t sample_rate, uint64_t data_bytes, uint8_t* out, char* err, size_t errlen) {
+    if (!out) return KK_ERR_INVALID;
+    return guard(err, errlen, [&] {
+        check(format == KK_WAV_PCM16 || format == KK_WAV_FLOAT32, "unknown WAV format");
+        // check_riff_size (src/wav.rs:34-40): the RIFF size field is 36 + data in 32 bits
+        check(data_bytes <= (uint64_t)UINT32_MAX - 36,
+              "the audio (" + std::to_string(data_bytes) + " bytes) exceeds the 4 GiB limit of a WAV file");
+        const uint16_t bits = format == KK_WAV_PCM16 ? 16 : 32, tag = format == KK_WAV_PCM16 ? 1 : 3;
+        auto put = [&](int at, const void* v, int n) { std::memcpy(out + at, v, n); };
+        auto u32 = [&](int at, uint32_t v) {
+            for (int i = 0; i < 4; i++) out[at + i] = (uint8_t)(v >> (8 * i));
+        };
+        auto u16 = [&](int at, uint16_t v) { out[at] = (uint8_t)v, out[at + 1] = (uint8_t)(v >> 8); };
+        put(0, "RIFF", 4);
+        u32(4, (uint32_t)(36 + data_bytes));
+        put(8, "WAVEfmt ", 8);
+        u32(16, 16);
+        u16(20, tag);
+        u16(22, 1);
+        u32(24, sample_rate);
+        u32(28, sample_rate * bits / 8);
+        u16(32, bits / 8);
+        u16(34, bits);
+        put(36, "data", 4);
+        u32(40, (uint32_t)data_bytes);
+    });
 }
 
 int kk_plan_tap(kk_plan* plan, const char* name, int item, float* dst, int64_t count, char* err, size_t errlen) {

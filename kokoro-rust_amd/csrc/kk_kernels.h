@@ -155,6 +155,13 @@ struct IstftParams {
     const int64_t* audio_start;
 };
 hipError_t launch_istft(const IstftParams& p, hipStream_t s);
+// PCM_16 encoding of packed audio (src/wav.rs:63-80) over the iSTFT's work list (blocks of
+// kIstftSamples samples of one item; blk_item null: one item of n samples from 0): out[i] =
+// clamp(round-half-even(audio[i] * 32767)), NaN -> 0; clipped[b] += samples outside
+// [-32768, 32767] after rounding (NaN and infinities included).  clipped must start at zero.
+hipError_t launch_pcm16(const float* audio, const int64_t* audio_start, const int64_t* item_len,
+                        const int64_t* blk_item, const int64_t* blk_s0, int64_t n_blocks, int16_t* out,
+                        unsigned long long* clipped, hipStream_t s);
 // Zero a buffer (a kernel, so the sequence stays capturable in a graph).
 hipError_t launch_zero(void* p, int64_t bytes, hipStream_t s);
 

@@ -629,6 +629,38 @@ __global__ __launch_bounds__(256) void istft_kernel(IstftParams p) {
     }
 }
 
+// ------------------------------------------------------------------ PCM_16 (src/wav.rs:63-80)
+// v = (s * 32767).round_ties_even() in f32; !(-32768 <= v <= 32767) counts as clipped (NaN
+// included); the stored value is v clamped, and NaN casts to 0 as Rust's saturating `as i16`.
+__global__ __launch_bounds__(256) void pcm16_kernel(const float* __restrict__ audio,
+                                                    const int64_t* __restrict__ audio_start,
+                                                    const int64_t* __restrict__ item_len,
+                                                    const int64_t* __restrict__ blk_item,
+                                                    const int64_t* __restrict__ blk_s0, int16_t* __restrict__ out,
+                                                    unsigned long long* __restrict__ clipped) {
+    const int64_t blk = blockIdx.x;
+    const int b = blk_item ? (int)blk_item[blk] : 0;
+    const int64_t s0 = blk_item ? blk_s0[blk] : blk * kIstftSamples;
+    const int64_t base = audio_start ? audio_start[b] : 0;
+    const int64_t end = min(s0 + kIstftSamples, item_len[b]);
+    unsigned n_clip = 0;
+    for (int64_t i = s0 + threadIdx.x; i < end; i += blockDim.x) {
+        const float v = rintf(__fmul_rn(audio[base + i], 32767.0f));
+        const bool in = v >= -32768.0f && v <= 32767.0f;
+        n_clip += in ? 0u : 1u;
+        out[base + i] = (int16_t)(v != v ? 0.0f : fminf(fmaxf(v, -32768.0f), 32767.0f));
+    }
+    // block total (integer: the result does not depend on the order), one atomic per block
+    for (int o = 32; o > 0; o >>= 1) n_clip += __shfl_xor(n_clip, o, 64);
+    __shared__ unsigned part[4];
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = n_clip;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const unsigned t = part[0] + part[1] + part[2] + part[3];
+        if (t) atomicAdd(clipped + b, (unsigned long long)t);
+    }
+}
+
 __global__ void zero_kernel(uint32_t* p, int64_t n) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) p[i] = 0u;
@@ -738,6 +770,15 @@ hipError_t launch_source_stft(const SourceParams& p, hipStream_t s) {
 
 hipError_t launch_istft(const IstftParams& p, hipStream_t s) {
     hipLaunchKernelGGL(istft_kernel, dim3((unsigned)p.n_blocks), dim3(256), 0, s, p);
+    return hipGetLastError();
+}
+
+hipError_t launch_pcm16(const float* audio, const int64_t* audio_start, const int64_t* item_len,
+                        const int64_t* blk_item, const int64_t* blk_s0, int64_t n_blocks, int16_t* out,
+                        unsigned long long* clipped, hipStream_t s) {
+    if (n_blocks <= 0) return hipSuccess;
+    hipLaunchKernelGGL(pcm16_kernel, dim3((unsigned)n_blocks), dim3(256), 0, s, audio, audio_start, item_len,
+                       blk_item, blk_s0, out, clipped);
     return hipGetLastError();
 }
 

@@ -22,6 +22,7 @@ EXPORTS = [
     "kk_output_free", "kk_plan_create", "kk_plan_create_generator", "kk_plan_create_snake", "kk_plan_run",
     "kk_plan_sync", "kk_plan_fetch", "kk_plan_tap", "kk_plan_get_info", "kk_plan_free", "kk_set_profiling",
     "kk_profile_read", "kk_durations_from_logits", "kk_layout_frames", "kk_layout_col_item", "kk_layout_src_row",
+    "kk_plan_fetch_pcm16", "kk_encode_pcm16", "kk_wav_header",
 ]
 
 
@@ -89,6 +90,9 @@ def lib():
         L.kk_plan_sync.argtypes = [vp, cp, sz]
         L.kk_plan_fetch.argtypes = [vp, C.POINTER(Output), cp, sz]
         L.kk_plan_tap.argtypes = [vp, cp, i32, vp, i64, cp, sz]
+        L.kk_plan_fetch_pcm16.argtypes = [vp, C.POINTER(vp), vp, cp, sz]
+        L.kk_encode_pcm16.argtypes = [vp, vp, i64, vp, vp, cp, sz]
+        L.kk_wav_header.argtypes = [i32, C.c_uint32, C.c_uint64, vp, cp, sz]
         L.kk_plan_get_info.argtypes = [vp, C.POINTER(PlanInfo)]
         L.kk_plan_free.argtypes = [vp]
         L.kk_plan_free.restype = None
@@ -122,6 +126,17 @@ def _f32(a):
 
 def identity():
     return lib().kk_identity().decode()
+
+
+WAV_PCM16, WAV_FLOAT32 = 0, 1
+
+
+def wav_header(fmt, sample_rate, data_bytes):
+    """wav::header (src/wav.rs:43-61): the canonical 44-byte mono header; KKError beyond 4 GiB."""
+    out = np.zeros(44, np.uint8)
+    err = _err()
+    _check(lib().kk_wav_header(int(fmt), int(sample_rate), int(data_bytes), _p(out), err, len(err)), err)
+    return out.tobytes()
 
 
 # ------------------------------------------------------------------ host rules
@@ -226,6 +241,15 @@ class Context:
     def plan(self, items):
         return Plan.decoder(self, items)
 
+    def encode_pcm16(self, audio):
+        """kk_encode_pcm16: a host f32 array as PCM_16 (encoded on the device) and its clipped count."""
+        a = _f32(audio).ravel()
+        out = np.zeros(a.size, np.int16)
+        clipped = np.zeros(1, np.int64)
+        err = _err()
+        _check(lib().kk_encode_pcm16(self.h, _p(a), a.size, _p(out), _p(clipped), err, len(err)), err)
+        return out, int(clipped[0])
+
 
 def _decoder_items(items):
     keep = []
@@ -247,8 +271,9 @@ def _decoder_items(items):
 
 
 class Plan:
-    def __init__(self, ctx, h, n, kind):
+    def __init__(self, ctx, h, n, kind, n_samples=None):
         self.ctx, self.h, self.n, self.kind = ctx, h, n, kind
+        self.n_samples = n_samples  # audio samples per item (decoder / generator plans)
 
     @classmethod
     def decoder(cls, ctx, items):
@@ -256,7 +281,7 @@ class Plan:
         h = C.c_void_p()
         err = _err()
         _check(lib().kk_plan_create(ctx.h, arr, len(items), C.byref(h), err, len(err)), err)
-        return cls(ctx, h, len(items), "decoder")
+        return cls(ctx, h, len(items), "decoder", [600 * it.n_frames for it in items])
 
     @classmethod
     def generator(cls, ctx, xs, f0s, ref_ss, seeds):
@@ -273,7 +298,7 @@ class Plan:
         h = C.c_void_p()
         err = _err()
         _check(lib().kk_plan_create_generator(ctx.h, arr, len(xs), C.byref(h), err, len(err)), err)
-        return cls(ctx, h, len(xs), "generator")
+        return cls(ctx, h, len(xs), "generator", [600 * (_f32(x).shape[1] // 2) for x in xs])
 
     @classmethod
     def snake(cls, ctx, prefix, xs, ref_ss, gap=40):
@@ -308,6 +333,15 @@ class Plan:
         if self.kind == "snake":
             res = [r.reshape(s) for r, s in zip(res, self.shapes)]
         return res
+
+    def fetch_pcm16(self):
+        """Each item's audio as PCM_16 (encoded on the device) and its clipped-sample count."""
+        outs = [np.zeros(n, np.int16) for n in self.n_samples]
+        ptrs = (C.c_void_p * self.n)(*[o.ctypes.data for o in outs])
+        clipped = np.zeros(self.n, np.int64)
+        err = _err()
+        _check(lib().kk_plan_fetch_pcm16(self.h, ptrs, _p(clipped), err, len(err)), err)
+        return outs, clipped
 
     def tap(self, name, item, shape):
         out = np.zeros(shape, np.float32)

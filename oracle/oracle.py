@@ -7,6 +7,7 @@ from __future__ import annotations
 
 import ctypes as C
 import os
+import struct
 
 import numpy as np
 
@@ -122,6 +123,31 @@ def durations_from_logits(logits, speed):
     out = np.zeros(t, np.int64)
     lib().ko_durations_from_logits(logits.reshape(-1), t, float(speed), out)
     return out
+
+
+# ------------------------------------------------------------------ output formats (src/wav.rs)
+
+
+def encode_pcm16(audio):
+    """wav::encode, PCM_16 (src/wav.rs:63-80): v = (s * 32767).round_ties_even() in f32; a sample
+    counts as clipped when v is outside [-32768, 32767] (NaN included); the stored value is v
+    clamped, and NaN becomes 0 (Rust's saturating `as i16`).  Returns (int16 samples, clipped)."""
+    a = np.asarray(audio, np.float32)
+    with np.errstate(invalid="ignore", over="ignore"):
+        v = np.rint(a * np.float32(32767.0))  # f32 product, round half to even
+        inside = (v >= np.float32(-32768.0)) & (v <= np.float32(32767.0))
+        out = np.where(np.isnan(v), np.float32(0.0), np.clip(v, -32768.0, 32767.0)).astype(np.int16)
+    return out, int(np.count_nonzero(~inside))
+
+
+def wav_header(fmt, sample_rate, data_bytes):
+    """wav::header (src/wav.rs:43-61): canonical 44-byte mono RIFF/WAVE header, format tag 1
+    (fmt 0, PCM_16) or 3 (fmt 1, float32); ValueError past check_riff_size (src/wav.rs:34-40)."""
+    if data_bytes > 0xFFFFFFFF - 36:
+        raise ValueError(f"the audio ({data_bytes} bytes) exceeds the 4 GiB limit of a WAV file")
+    bits, tag = (16, 1) if fmt == 0 else (32, 3)
+    return struct.pack("<4sI8sIHHIIHH4sI", b"RIFF", 36 + data_bytes, b"WAVEfmt ", 16, tag, 1, sample_rate,
+                       sample_rate * bits // 8, bits // 8, bits, b"data", data_bytes)
 
 
 # ------------------------------------------------------------------ primitives
