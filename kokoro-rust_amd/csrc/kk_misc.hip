@@ -13,6 +13,17 @@ __constant__ double c_cos[11][20];
 __constant__ double c_sin[11][20];
 __constant__ float c_win[20];
 
+// The DFT tables in LDS: the (frame, bin) loops index them per lane, which the constant cache
+// serves one address at a time.
+struct DftLds {
+    double cs[11][20], sn[11][20];
+    float win[20];
+};
+__device__ __forceinline__ void stage_dft(DftLds& t) {
+    for (int i = threadIdx.x; i < 220; i += blockDim.x) (&t.cs[0][0])[i] = (&c_cos[0][0])[i], (&t.sn[0][0])[i] = (&c_sin[0][0])[i];
+    if (threadIdx.x < 20) t.win[threadIdx.x] = c_win[threadIdx.x];
+}
+
 namespace {
 
 constexpr float kPiF = 3.14159274101257324f;  // (float)M_PI, kernels/kokoro.cu:9
@@ -547,6 +558,8 @@ __device__ float har_sample(const SourceParams& p, int b, int t) {
 __global__ __launch_bounds__(256) void source_stft_kernel(SourceParams p) {
 #pragma clang fp contract(off)
     __shared__ float har[kSourceFrames * 5 + 15];
+    __shared__ DftLds dft;
+    stage_dft(dft);
     const int64_t blk = blockIdx.x;
     const int b = (int)p.blk_item[blk];
     const int64_t f_begin = p.blk_f0[blk];
@@ -565,9 +578,9 @@ __global__ __launch_bounds__(256) void source_stft_kernel(SourceParams p) {
         const int fl = i / 11, k = i - fl * 11;
         double re = 0.0, im = 0.0;
         for (int n = 0; n < 20; n++) {
-            const double v = (double)(har[fl * 5 + n] * c_win[n]);
-            re += v * c_cos[k][n];
-            im -= v * c_sin[k][n];
+            const double v = (double)(har[fl * 5 + n] * dft.win[n]);
+            re += v * dft.cs[k][n];
+            im -= v * dft.sn[k][n];
         }
         if (k == 0 || k == 10) im = 0.0;
         const float rf = (float)re, imf = (float)im;
@@ -584,6 +597,8 @@ __global__ __launch_bounds__(256) void istft_kernel(IstftParams p) {
     __shared__ double re[kIstftFrames][11];
     __shared__ double im[kIstftFrames][11];
     __shared__ double fr[kIstftFrames][20];
+    __shared__ DftLds dft;
+    stage_dft(dft);
     const int64_t blk = blockIdx.x;
     const int b = (int)p.blk_item[blk];
     const int64_t s0 = p.blk_s0[blk];
@@ -596,20 +611,34 @@ __global__ __launch_bounds__(256) void istft_kernel(IstftParams p) {
     const int64_t f_last = min((s1 - 1 + 10) / 5, nframes - 1);
     const int nfr = (int)(f_last - f_first + 1);
     const float* post = p.post + (p.start120[b] + f_first) * p.post_ld;
-    for (int i = threadIdx.x; i < nfr * 11; i += blockDim.x) {
+    // the block's frames of post, every load in flight before the first use (one memory latency)
+    constexpr int kPer = (kIstftFrames * 11 + 255) / 256;
+    float lm[kPer], lp[kPer];
+#pragma unroll
+    for (int j = 0; j < kPer; j++) {
+        const int i = min((int)threadIdx.x + j * 256, nfr * 11 - 1);
         const int q = i / 11, k = i - q * 11;
-        const float m = expf(post[q * p.post_ld + k]);
-        const float ph = sinf(post[q * p.post_ld + 11 + k]);
-        re[q][k] = (double)(m * cosf(ph));
-        im[q][k] = (double)(m * sinf(ph));
+        lm[j] = post[q * p.post_ld + k];
+        lp[j] = post[q * p.post_ld + 11 + k];
+    }
+#pragma unroll
+    for (int j = 0; j < kPer; j++) {
+        const int i = threadIdx.x + j * 256;
+        if (i < nfr * 11) {
+            const int q = i / 11, k = i - q * 11;
+            const float m = expf(lm[j]);
+            const float ph = sinf(lp[j]);
+            re[q][k] = (double)(m * cosf(ph));
+            im[q][k] = (double)(m * sinf(ph));
+        }
     }
     __syncthreads();
     for (int i = threadIdx.x; i < nfr * 20; i += blockDim.x) {
         const int q = i / 20, n = i - q * 20;
         double v = re[q][0] + re[q][10] * ((n % 2 == 0) ? 1.0 : -1.0);
-        for (int k = 1; k < 10; k++) v += 2.0 * (re[q][k] * c_cos[k][n] - im[q][k] * c_sin[k][n]);
+        for (int k = 1; k < 10; k++) v += 2.0 * (re[q][k] * dft.cs[k][n] - im[q][k] * dft.sn[k][n]);
         v = v / 20.0;
-        fr[q][n] = v * (double)c_win[n];
+        fr[q][n] = v * (double)dft.win[n];
     }
     __syncthreads();
     float* out = p.audio + p.audio_start[b];
@@ -622,7 +651,7 @@ __global__ __launch_bounds__(256) void istft_kernel(IstftParams p) {
         for (int64_t f = f_lo; f <= f_hi; f++) {
             const int n = (int)(j - 5 * f);
             acc += fr[f - f_first][n];
-            const double w = (double)c_win[n];
+            const double w = (double)dft.win[n];
             env += w * w;
         }
         out[i] = (float)(acc / env);
