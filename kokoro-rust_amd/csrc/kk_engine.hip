@@ -586,8 +586,9 @@ static void setup_generator(kk_plan* p, const std::vector<const float*>& f0s, co
     alloc_zero(p, p->post, (size_t)l120 * kPostLd * sizeof(float));
     alloc_zero(p, p->audio, (size_t)600 * ln * sizeof(float));
     for (int i = 0; i < 5; i++) p->coef[i].alloc((size_t)nb * kXinLd * sizeof(Coef));
-    // statistics partials: every partial covers at most 128 columns of one item
-    auto bound = [&](int64_t l, int64_t c) { return (l / 128 + 2 * (int64_t)nb + 2) * c; };
+    // statistics partials: every partial but the last two of each item covers at least 64 columns
+    // of one item (the noise convs' 64-column tiles; the convs' 128-column wave spans)
+    auto bound = [&](int64_t l, int64_t c) { return (l / 64 + 2 * (int64_t)nb + 2) * c; };
     const int64_t np = std::max({bound(ln, 1152), bound(2 * ln, 512), bound(l20, 256), bound(l120, 128)});
     p->part.alloc((size_t)np * sizeof(StatPart));
     p->part_bytes = (int64_t)p->part.bytes;
@@ -895,10 +896,14 @@ struct Runner {
     }
 
     // snake_b (src/gpu_batch.rs:140-154) in place on X.  The statistics of each conv's output are
-    // reduced in its epilogue; only the block input needs a statistics pass.
-    void snake_block(const MSnake& blk, float* X, float* h, const Dom& d) {
+    // reduced in its epilogue; the block input's come from the kernel that produced X (`xin`: its
+    // tiles, one partial per tile and channel) or, when null, from a statistics pass here.
+    void snake_block(const MSnake& blk, float* X, float* h, const Dom& d, const Tiles* xin = nullptr) {
         const int c = blk.c, wn = kShapeWN[blk.c1[0].shape];
-        stats_fin(X, c, c, d, blk.a1[0], cf(0));
+        if (xin)
+            fin(*xin, 1, c, blk.a1[0], cf(0));
+        else
+            stats_fin(X, c, c, d, blk.a1[0], cf(0));
         for (int i = 0; i < 3; i++) {
             const Tiles& t = conv(blk.c1[i], snake_op(blk, d, X, h, EPI_STORE, cf(0), i, false, true));
             fin(t, wn, c, blk.a2[i], cf(1));
@@ -1018,12 +1023,13 @@ struct Runner {
         for (int j = 0; j < 6; j++) B[j] = p->B[j].as<float>();
         // xs = noise_res[i](noise_convs[i](masked spec)) (src/gpu_batch.rs:362-375)
         const MNoiseConv& nc = m.nc[i];
+        const Tiles& tn = p->tl(dout, kNoiseTile);
+        need_part(tn.count * c);
         KK_LAUNCH(launch_noise_conv(p->spec.as<float>(), kSpecLd, p->d120.l, p->d120.col_d.as<int32_t>(),
                                  nc.w.as<float>(), nc.wp.p ? nc.wp.as<float>() : nullptr, nc.b.as<float>(), nc.cout,
-                                 nc.k, nc.stride, nc.pad, B[1], c,
-                                 dout.l, s));
+                                 nc.k, nc.stride, nc.pad, B[1], c, tn.dev(), p->part.as<StatPart>(), s));
         launches++;
-        snake_block(m.noise_res[i], B[1], B[2], dout);
+        snake_block(m.noise_res[i], B[1], B[2], dout, &tn);
         // y = ups[i](leaky_0.1(x) masked) (+ per-item reflect pad on stage 1) + xs
         Op ou;
         ou.pro = PRO_LEAKY, ou.epi = i == 0 ? EPI_CONVT : EPI_CONVT_REFLECT, ou.slope = 0.1f;

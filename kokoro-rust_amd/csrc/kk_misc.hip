@@ -234,19 +234,23 @@ __global__ void adain_pool_kernel(const float* __restrict__ x, int64_t ld, int c
 // output rows x COUT channels; thread = 4 consecutive channels x TT rows, so every weight load is
 // one coalesced float4 across the wave and every input value is a wave-uniform LDS broadcast.
 // Weights are pre-transposed to [k][22][COUT].  Accumulation order per output: bias, then taps
-// ascending, channels ascending within a tap (f32 FMA).
-constexpr int kNcRows = 64;
+// ascending, channels ascending within a tap (f32 FMA).  A block computes one item-aligned tile
+// (<= 64 output rows of one item) and, for the next layer's AdaIN, the tile's statistics partial
+// per channel (sums of v - b over its rows, shift b: the bias is a value of the data's scale).
+constexpr int kNcRows = kNoiseTile;
 constexpr int kNcMaxWin = (kNcRows - 1) * 6 + 12;
 template <int COUT, int TT, int WIN>
 __global__ __launch_bounds__(256) void noise_conv_kernel(const float* __restrict__ spec, int64_t spec_ld, int64_t l_in,
                                                          const int32_t* __restrict__ col_in,
                                                          const float* __restrict__ wt, const float* __restrict__ b,
                                                          int k, int stride, int pad, float* __restrict__ y,
-                                                         int64_t y_ld, int64_t l_out) {
+                                                         int64_t y_ld, TilesDev tl, StatPart* __restrict__ part) {
     constexpr int CQ = COUT / 4, TG = 256 / CQ;
     static_assert(TG * TT == kNcRows, "rows per block");
     __shared__ float xs[WIN][22];  // the input window (its size sets how many blocks share a CU)
-    const int64_t t0 = (int64_t)blockIdx.x * kNcRows;
+    __shared__ float4 red[2][TG][CQ];
+    const int64_t t0 = tl.t0[blockIdx.x];
+    const int nv = tl.n[blockIdx.x];
     const int win = (kNcRows - 1) * stride + k;
     const int64_t in0 = t0 * stride - pad;
     // Stage the input window: every load of a thread is issued before the first is used (rows
@@ -294,10 +298,29 @@ __global__ __launch_bounds__(256) void noise_conv_kernel(const float* __restrict
             }
         }
     }
+    float4 s1 = make_float4(0.f, 0.f, 0.f, 0.f), s2 = s1;
 #pragma unroll
     for (int tt = 0; tt < TT; tt++) {
-        const int64_t row = t0 + tg * TT + tt;
-        if (row < l_out) *(float4*)(y + row * y_ld + cq * 4) = acc[tt];
+        const int r = tg * TT + tt;
+        if (r < nv) {
+            *(float4*)(y + (t0 + r) * y_ld + cq * 4) = acc[tt];
+            const float4 d = make_float4(acc[tt].x - bias.x, acc[tt].y - bias.y, acc[tt].z - bias.z, acc[tt].w - bias.w);
+            s1.x += d.x, s1.y += d.y, s1.z += d.z, s1.w += d.w;
+            s2.x = __builtin_fmaf(d.x, d.x, s2.x), s2.y = __builtin_fmaf(d.y, d.y, s2.y);
+            s2.z = __builtin_fmaf(d.z, d.z, s2.z), s2.w = __builtin_fmaf(d.w, d.w, s2.w);
+        }
+    }
+    red[0][tg][cq] = s1, red[1][tg][cq] = s2;
+    __syncthreads();
+    if (threadIdx.x < COUT) {
+        const int c = threadIdx.x, q = c / 4, e = c % 4;
+        float a1 = 0.f, a2 = 0.f;
+        for (int g = 0; g < TG; g++) {  // row groups in order
+            const float4 u = red[0][g][q], v = red[1][g][q];
+            a1 += e == 0 ? u.x : e == 1 ? u.y : e == 2 ? u.z : u.w;
+            a2 += e == 0 ? v.x : e == 1 ? v.y : e == 2 ? v.z : v.w;
+        }
+        part[(int64_t)blockIdx.x * COUT + c] = StatPart{a1, a2, b[c], (float)nv};
     }
 }
 
@@ -311,14 +334,15 @@ __global__ __launch_bounds__(256) void noise_conv_kernel(const float* __restrict
 // Accumulators start at the bias; the epilogue stores each lane's 4 consecutive channels.
 constexpr int kNc0Win = (kNcRows - 1) * 6 + 12;  // 390 input rows per 64 output columns
 constexpr int kNc0Ld = kNc0Win + 2;               // channel-major window row stride (floats)
-__global__ __launch_bounds__(256) void noise_conv0_mfma_kernel(const float* __restrict__ spec, int64_t spec_ld,
+__global__ __launch_bounds__(256, 4) void noise_conv0_mfma_kernel(const float* __restrict__ spec, int64_t spec_ld,
                                                                int64_t l_in, const int32_t* __restrict__ col_in,
                                                                const float4* __restrict__ wp, const float* __restrict__ b,
                                                                int pad, float* __restrict__ y, int64_t y_ld,
-                                                               int64_t l_out) {
+                                                               TilesDev tl, StatPart* __restrict__ part) {
     typedef float f32x16 __attribute__((ext_vector_type(16)));
     __shared__ float xs[22 * kNc0Ld];
-    const int64_t t0 = (int64_t)blockIdx.x * kNcRows;
+    const int64_t t0 = tl.t0[blockIdx.x];
+    const int nv = tl.n[blockIdx.x];
     const int64_t in0 = t0 * 6 - pad;
     // the window in batches of 12 loads per thread, each batch in flight before its first use (rows
     // clamped, the gap / range mask applied afterwards)
@@ -401,19 +425,46 @@ __global__ __launch_bounds__(256) void noise_conv0_mfma_kernel(const float* __re
     }
     // D layout: element 4 g + r of tile (mi, ni) is channel 64 wave + 32 mi + 8 g + 4 h + r of
     // output column t0 + 32 ni + l32
+    // Stores, and the tile's statistics partial (sums of v - b over its rows, per channel): each
+    // lane sums its two columns and its neighbour's (a DPP lane swap); the 16 lane pairs of a
+    // channel are then added through LDS (the input window's space, once every wave is done with
+    // it), in order.  Each accumulator is read once.
+    const bool ok0 = l32 < nv, ok1 = 32 + l32 < nv;
+    constexpr int kRl = 257;  // [2 statistics][16 lane pairs][256 channels + 1]
+    static_assert(2 * 16 * kRl <= 22 * kNc0Ld, "reduction buffer");
+    auto pair_sum = [](float v) {  // v + v of lane l ^ 1 (quad_perm [1, 0, 3, 2])
+        return v + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));
+    };
+    __syncthreads();
 #pragma unroll
-    for (int ni = 0; ni < 2; ni++) {
-        const int64_t col = t0 + 32 * ni + l32;
-        if (col < l_out) {
+    for (int mi = 0; mi < 2; mi++)
 #pragma unroll
-            for (int mi = 0; mi < 2; mi++)
+        for (int g = 0; g < 4; g++) {
+            const int c0 = wave * 64 + mi * 32 + 8 * g + 4 * h;
+            const float4 v0 = make_float4(acc[mi][0][4 * g], acc[mi][0][4 * g + 1], acc[mi][0][4 * g + 2],
+                                          acc[mi][0][4 * g + 3]);
+            const float4 v1 = make_float4(acc[mi][1][4 * g], acc[mi][1][4 * g + 1], acc[mi][1][4 * g + 2],
+                                          acc[mi][1][4 * g + 3]);
+            if (ok0) *(float4*)(y + (t0 + l32) * y_ld + c0) = v0;
+            if (ok1) *(float4*)(y + (t0 + 32 + l32) * y_ld + c0) = v1;
+            const float4 bv = *(const float4*)(b + c0);
+            const float e0[4] = {v0.x - bv.x, v0.y - bv.y, v0.z - bv.z, v0.w - bv.w};
+            const float e1[4] = {v1.x - bv.x, v1.y - bv.y, v1.z - bv.z, v1.w - bv.w};
 #pragma unroll
-                for (int g = 0; g < 4; g++)
-                    *(float4*)(y + col * y_ld + wave * 64 + mi * 32 + 8 * g + 4 * h) =
-                        make_float4(acc[mi][ni][4 * g], acc[mi][ni][4 * g + 1], acc[mi][ni][4 * g + 2],
-                                    acc[mi][ni][4 * g + 3]);
+            for (int r = 0; r < 4; r++) {
+                const float d0 = ok0 ? e0[r] : 0.f, d1 = ok1 ? e1[r] : 0.f;
+                const float p1 = pair_sum(d0 + d1), p2 = pair_sum(__builtin_fmaf(d1, d1, d0 * d0));
+                if ((l32 & 1) == 0) {
+                    xs[(l32 >> 1) * kRl + c0 + r] = p1;
+                    xs[(16 + (l32 >> 1)) * kRl + c0 + r] = p2;
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);  // one group at a time: registers stay at the main loop's
         }
-    }
+    __syncthreads();
+    float a1 = 0.f, a2 = 0.f;
+    for (int l = 0; l < 16; l++) a1 += xs[l * kRl + threadIdx.x], a2 += xs[(16 + l) * kRl + threadIdx.x];
+    part[(int64_t)blockIdx.x * 256 + threadIdx.x] = StatPart{a1, a2, b[threadIdx.x], (float)nv};
 }
 
 // ------------------------------------------------------------------ SineGen (kernels/kokoro.cu:188-254)
@@ -759,28 +810,29 @@ hipError_t launch_adain_pool(const float* x, int64_t ld, int c, const Coef* coef
 
 hipError_t launch_noise_conv(const float* spec, int64_t spec_ld, int64_t l_in, const int32_t* col_in, const float* wt,
                              const float* wp, const float* b, int cout, int k, int stride, int pad, float* y,
-                             int64_t y_ld, int64_t l_out, hipStream_t s) {
+                             int64_t y_ld, TilesDev t, StatPart* part, hipStream_t s) {
     const int win = (kNcRows - 1) * stride + k;
     if (win > kNcMaxWin) return hipErrorInvalidValue;
-    const dim3 grid(blocks_for(l_out, kNcRows));
+    if (t.count == 0) return hipSuccess;
+    const dim3 grid((unsigned)t.count);
     if (wp) {
         // the matrix-core path: noise_convs.0's shape only, weights packed by pack_noise_conv0
         if (cout != 256 || k != 12 || stride != 6) return hipErrorInvalidValue;
         hipLaunchKernelGGL(noise_conv0_mfma_kernel, grid, dim3(256), 0, s, spec, spec_ld, l_in, col_in,
-                           (const float4*)wp, b, pad, y, y_ld, l_out);
+                           (const float4*)wp, b, pad, y, y_ld, t, part);
         return hipGetLastError();
     }
     // noise_convs.0 (k 12, stride 6) stages a 390-row window; noise_convs.1 (k 1) 64 rows, small
     // enough for 16 blocks per CU
     if (cout == 256)
         hipLaunchKernelGGL((noise_conv_kernel<256, 16, kNcMaxWin>), grid, dim3(256), 0, s, spec, spec_ld, l_in, col_in,
-                           wt, b, k, stride, pad, y, y_ld, l_out);
+                           wt, b, k, stride, pad, y, y_ld, t, part);
     else if (cout == 128 && win <= kNcRows)
         hipLaunchKernelGGL((noise_conv_kernel<128, 8, kNcRows>), grid, dim3(256), 0, s, spec, spec_ld, l_in, col_in, wt,
-                           b, k, stride, pad, y, y_ld, l_out);
+                           b, k, stride, pad, y, y_ld, t, part);
     else if (cout == 128)
         hipLaunchKernelGGL((noise_conv_kernel<128, 8, kNcMaxWin>), grid, dim3(256), 0, s, spec, spec_ld, l_in, col_in,
-                           wt, b, k, stride, pad, y, y_ld, l_out);
+                           wt, b, k, stride, pad, y, y_ld, t, part);
     else
         return hipErrorInvalidValue;
     return hipGetLastError();
