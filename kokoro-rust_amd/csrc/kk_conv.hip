@@ -381,6 +381,7 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
     const uint32_t yo0 = (uint32_t)(wcol0 + cg) * yld + m, ro0 = (uint32_t)(wcol0 + cg) * rld + m;
     const uint32_t yz = u.m0, rz = u.m0;  // clamped operand of an invalid row: row 0 of the unit
     float s1[4] = {0.f, 0.f, 0.f, 0.f}, s2[4] = {0.f, 0.f, 0.f, 0.f}, sft[4] = {0.f, 0.f, 0.f, 0.f};
+    float cnt = 0.f;  // ConvT: rows this lane group wrote (the statistics' count)
 #pragma unroll
     for (int j = 0; j < 4; j++) {
 #pragma unroll
@@ -423,7 +424,7 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
             for (int qq = 0; qq < QB; qq++) {
                 const int q = q0 + qq;
                 const int col = wcol0 + j * 32 + 4 * q + cg;
-                const bool valid = col < u.nv;
+                bool valid = col < u.nv;
                 // the values are computed for every row (they feed the statistics, masked there);
                 // only the store is conditional
                 float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -432,13 +433,17 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
                     const int64_t d = convt_dest(col, ok);
                     const float4 w = make_float4(v[qq].x + cb.x, v[qq].y + cb.y, v[qq].z + cb.z, v[qq].w + cb.w);
                     const float4 r = res[qq][0];
-                    if (ok) *(float4*)(p.y + d * p.y_ld + cg_.co) = make_float4(w.x + r.x, w.y + r.y, w.z + r.z, w.w + r.w);
+                    o = make_float4(w.x + r.x, w.y + r.y, w.z + r.z, w.w + r.w);
+                    valid = ok;
+                    if (ok) *(float4*)(p.y + d * p.y_ld + cg_.co) = o;
                     if (EPI == EPI_CONVT_REFLECT && ok && d == cg_.os + 2) {
                         // o = os + 1 also fills the item's first row (the reflected sample)
+                        // (the statistics leave this row to finalize, which reads it back)
                         const float4 r2 = *(const float4*)(p.r0 + cg_.os * p.r0_ld + cg_.co);
                         *(float4*)(p.y + cg_.os * p.y_ld + cg_.co) =
                             make_float4(w.x + r2.x, w.y + r2.y, w.z + r2.z, w.w + r2.w);
                     }
+                    if constexpr (STATS) cnt += ok ? 1.f : 0.f;
                 } else {
                     uint2 pk;  // v = conv + bias (the accumulators started at the bias)
                     o = finish4<EPI, OUT_H>(p, v[qq], res[qq], pk);
@@ -466,13 +471,20 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
             s1[r] += __shfl_xor(s1[r], 32, 64);
             s2[r] += __shfl_xor(s2[r], 32, 64);
         }
-        // every wave writes its record, an empty one (n = 0) when the tile ends before its columns
+        if constexpr (CONVT) {
+            cnt += __shfl_xor(cnt, 16, 64);
+            cnt += __shfl_xor(cnt, 32, 64);
+        }
+        // every wave writes its record, an empty one (n = 0) when the tile ends before its columns;
+        // ConvT: one record per (tile, phase, wave column), over the rows the wave wrote
         if (cg == 0) {
-            StatPart* dst = p.part + ((int64_t)u.tile * WN + wn) * p.cout;
-            const float nc = (float)max(min(u.nv - wcol0, 128), 0);
+            StatPart* dst = CONVT ? p.part + (((int64_t)u.tile * p.stride_t + cg_.ph) * WN + wn) * p.cout + cg_.co
+                                  : p.part + ((int64_t)u.tile * WN + wn) * p.cout + m;
+            const float nc = CONVT ? cnt : (float)max(min(u.nv - wcol0, 128), 0);
 #pragma unroll
             for (int r = 0; r < 4; r++)
-                if (m + r < p.cout) dst[m + r] = nc > 0.f ? StatPart{s1[r], s2[r], sft[r], nc} : StatPart{0.f, 0.f, 0.f, 0.f};
+                if (mok && (CONVT ? cg_.co : m) + r < p.cout)
+                    dst[r] = nc > 0.f ? StatPart{s1[r], s2[r], sft[r], nc} : StatPart{0.f, 0.f, 0.f, 0.f};
         }
     }
     init_acc<!CONVT>(acc, bias_s, next_m0, wm, lane);  // the next unit starts at its bias
@@ -726,8 +738,8 @@ hipError_t launch_conv(const ConvParams& p, int pro, int epi, int shape, bool st
     KK_CONV(PRO_F32, EPI_STORE, SHAPE_64x256, 1, 2, false, false, false)
     KK_CONV(PRO_BF16, EPI_STORE, SHAPE_256x128, 4, 1, true, false, false)
     // ConvT ups and conv_post
-    KK_CONV(PRO_LEAKY, EPI_CONVT, SHAPE_256x128, 4, 1, false, false, false)
-    KK_CONV(PRO_LEAKY, EPI_CONVT_REFLECT, SHAPE_256x128, 4, 1, false, false, false)
+    KK_CONV(PRO_LEAKY, EPI_CONVT, SHAPE_256x128, 4, 1, true, false, false)
+    KK_CONV(PRO_LEAKY, EPI_CONVT_REFLECT, SHAPE_256x128, 4, 1, true, false, false)
     KK_CONV(PRO_LEAKY, EPI_STORE, SHAPE_64x256, 1, 2, false, false, false)
 #undef KK_CONV
     return hipErrorInvalidValue;

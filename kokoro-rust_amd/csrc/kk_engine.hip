@@ -589,7 +589,10 @@ static void setup_generator(kk_plan* p, const std::vector<const float*>& f0s, co
     // statistics partials: every partial but the last two of each item covers at least 64 columns
     // of one item (the noise convs' 64-column tiles; the convs' 128-column wave spans)
     auto bound = [&](int64_t l, int64_t c) { return (l / 64 + 2 * (int64_t)nb + 2) * c; };
-    const int64_t np = std::max({bound(ln, 1152), bound(2 * ln, 512), bound(l20, 256), bound(l120, 128)});
+    // the ConvTs' partials: per 128-column input tile, phase and output channel
+    auto bound_t = [&](int64_t l_in, int64_t stride, int64_t c) { return (l_in / 128 + 2 * (int64_t)nb + 1) * stride * c; };
+    const int64_t np = std::max({bound(ln, 1152), bound(2 * ln, 512), bound(l20, 256), bound(l120, 128),
+                                 bound_t(l2, 10, 256), bound_t(l20, 6, 128)});
     p->part.alloc((size_t)np * sizeof(StatPart));
     p->part_bytes = (int64_t)p->part.bytes;
 }
@@ -811,10 +814,12 @@ struct Runner {
         launches++;
         return t;
     }
-    // Partials -> coefficients of AdaIN layer a.
-    void fin(const Tiles& t, int wn, int c, const MAdain& a, Coef* coef) {
+    // Partials -> coefficients of AdaIN layer a (`wn` partials per tile; xrow: one more sample per
+    // item, row xrow_at[b] of xrow [.][c]).
+    void fin(const Tiles& t, int wn, int c, const MAdain& a, Coef* coef, const float* xrow = nullptr,
+             const int64_t* xrow_at = nullptr) {
         KK_LAUNCH(launch_finalize(p->part.as<StatPart>(), c, wn, t.dev(), p->nb, p->gb.as<float>(), gb_ld(),
-                               a.gb_off, a.nw.as<float>(), a.nb.as<float>(), coef, s));
+                               a.gb_off, a.nw.as<float>(), a.nb.as<float>(), coef, s, xrow, c, xrow_at));
         launches++;
     }
     void stats_fin(const float* x, int64_t ld, int c, const Dom& d, const MAdain& a, Coef* coef) {
@@ -860,7 +865,7 @@ struct Runner {
         q.stride_t = o.stride, q.pad_t = o.pad_t;
         q.out_start = o.dout->start_d.as<int64_t>(), q.out_len = o.dout->len_d.as<int64_t>();
         if (o.stats) {
-            need_part(t.count * wn * c.cout);
+            need_part(t.count * wn * (o.convt ? o.stride : 1) * c.cout);  // ConvT: per phase too
             q.part = p->part.as<StatPart>();
         }
         // algorithmic FLOP over valid columns; ConvT (K = 2 stride): each input column feeds
@@ -913,11 +918,20 @@ struct Runner {
     }
 
     // x = (rb0(y) + rb1(y) + rb2(y)) / 3 (src/gpu_batch.rs:395-401); result in X[2].
-    void resblock_mean(const MSnake* rbs, const float* y, float* X[3], float* h, const Dom& d) {
+    // yt: the tiles whose partials of y its producer (the ConvT) wrote, `yparts` per tile, with the
+    // reflected first row of each item (xrow_at) outside them when y_refl; null: a statistics pass.
+    void resblock_mean(const MSnake* rbs, const float* y, float* X[3], float* h, const Dom& d,
+                       const Tiles* yt = nullptr, int yparts = 1, bool y_refl = false) {
         const int c = rbs[0].c, wn = kShapeWN[rbs[0].c1[0].shape];
-        // the three blocks' first AdaIN share one statistics pass over y
-        const Tiles& ts = stats(y, c, c, d);
-        for (int j = 0; j < 3; j++) fin(ts, 1, c, rbs[j].a1[0], cf(2 + j));
+        // the three blocks' first AdaIN share one set of statistics of y
+        if (yt) {
+            for (int j = 0; j < 3; j++)
+                fin(*yt, yparts, c, rbs[j].a1[0], cf(2 + j), y_refl ? y : nullptr,
+                    y_refl ? d.start_d.as<int64_t>() : nullptr);
+        } else {
+            const Tiles& ts = stats(y, c, c, d);
+            for (int j = 0; j < 3; j++) fin(ts, 1, c, rbs[j].a1[0], cf(2 + j));
+        }
         for (int j = 0; j < 3; j++) {
             const MSnake& blk = rbs[j];
             for (int i = 0; i < 3; i++) {
@@ -1036,9 +1050,10 @@ struct Runner {
         ou.x = i == 0 ? (const void*)p->dec_out.p : (const void*)B[0], ou.x_ld = i == 0 ? 512 : 256;
         ou.din = &din, ou.dout = &dout, ou.y = B[3], ou.y_ld = c, ou.r0 = B[1], ou.r0_ld = c;
         ou.convt = true, ou.stride = m.ups_stride[i], ou.pad_t = m.ups_pad[i], ou.cls = PC_CONVT;
-        conv(m.ups[i], ou);
+        ou.stats = true;  // partials of y per (tile, phase, wave column) for the resblocks' first AdaIN
+        const Tiles& tu = conv(m.ups[i], ou);
         float* X[3] = {B[4], B[5], B[0]};
-        resblock_mean(&m.rb[3 * i], B[3], X, B[2], dout);
+        resblock_mean(&m.rb[3 * i], B[3], X, B[2], dout, &tu, kShapeWN[m.ups[i].shape] * ou.stride, i == 1);
     }
 
     void post_istft() {

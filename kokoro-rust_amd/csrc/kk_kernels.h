@@ -92,8 +92,11 @@ hipError_t launch_conv(const ConvParams& p, int pro, int epi, int shape, bool st
 hipError_t launch_stats_tiles(const float* x, int64_t ld, int c, TilesDev t, StatPart* part, hipStream_t s);
 // Partials -> per-(item, channel) mean / rstd (chan_stats_seg semantics) -> AdaIN coefficients.
 // `wn` partials per tile (records [tile * wn + w][c]).
+// xrow (optional): one more sample per item outside the partials, row xrow_at[b] of xrow [.][xrow_ld]
+// (the reflected first row of the stage-1 ConvT output).
 hipError_t launch_finalize(const StatPart* part, int c, int wn, TilesDev t, int nb, const float* gb, int64_t gb_ld,
-                           int gb_off, const float* nw, const float* nb_, Coef* coef, hipStream_t s);
+                           int gb_off, const float* nw, const float* nb_, Coef* coef, hipStream_t s,
+                           const float* xrow = nullptr, int64_t xrow_ld = 0, const int64_t* xrow_at = nullptr);
 // gb[b][j] = W[j] . style[b] + bias[j] for every AdaIN layer at once.
 hipError_t launch_style_fc(const float* w, const float* bias, int rows, const float* style, int nb, float* gb,
                            hipStream_t s);

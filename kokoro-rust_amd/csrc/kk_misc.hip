@@ -71,7 +71,8 @@ constexpr int kFinSub = 16;
 __global__ __launch_bounds__(256) void finalize_kernel(const StatPart* __restrict__ part, int c, int wn, TilesDev t,
                                                        const float* __restrict__ gb, int64_t gb_ld, int gb_off,
                                                        const float* __restrict__ nw, const float* __restrict__ nbias,
-                                                       Coef* __restrict__ coef) {
+                                                       Coef* __restrict__ coef, const float* __restrict__ xrow,
+                                                       int64_t xrow_ld, const int64_t* __restrict__ xrow_at) {
     __shared__ double sa[kFinSub][16], sb[kFinSub][16], sn[kFinSub][16];
     const int cl = threadIdx.x & 15, sub = threadIdx.x >> 4;
     const int b = blockIdx.x;
@@ -110,6 +111,10 @@ __global__ __launch_bounds__(256) void finalize_kernel(const StatPart* __restric
     }
     if (sub != 0 || ch >= c) return;
     a1 = sa[0][cl], a2 = sb[0][cl], n = sn[0][cl];
+    if (xrow) {  // one more sample of the item, outside the partials: row xrow_at[b] of xrow
+        const double d = (double)xrow[xrow_at[b] * xrow_ld + ch] - ref;
+        a1 += d, a2 += d * d, n += 1.0;
+    }
     const int64_t i = (int64_t)b * c + ch;
     if (n <= 0.0) {
         coef[i] = Coef{0.f, 0.f};
@@ -766,9 +771,11 @@ hipError_t launch_stats_tiles(const float* x, int64_t ld, int c, TilesDev t, Sta
 }
 
 hipError_t launch_finalize(const StatPart* part, int c, int wn, TilesDev t, int nb, const float* gb, int64_t gb_ld,
-                           int gb_off, const float* nw, const float* nb_, Coef* coef, hipStream_t s) {
+                           int gb_off, const float* nw, const float* nb_, Coef* coef, hipStream_t s, const float* xrow,
+                           int64_t xrow_ld, const int64_t* xrow_at) {
     dim3 grid((unsigned)nb, (unsigned)ceil_div(c, 16));
-    hipLaunchKernelGGL(finalize_kernel, grid, dim3(256), 0, s, part, c, wn, t, gb, gb_ld, gb_off, nw, nb_, coef);
+    hipLaunchKernelGGL(finalize_kernel, grid, dim3(256), 0, s, part, c, wn, t, gb, gb_ld, gb_off, nw, nb_, coef, xrow,
+                       xrow_ld, xrow_at);
     return hipGetLastError();
 }
 
