@@ -243,6 +243,7 @@ constexpr int kNumRes = EPI == EPI_MEAN3 ? 3
 struct EpiBase {
     void* y;
     const float *r0, *r1, *r2;
+    __amdgpu_buffer_rsrc_t ry;  // y from the unit's first row, as a buffer resource (see store4)
 };
 
 // Residual operands of output row t, channels m..m+3 (`yo`, `ro`: element offsets from the unit's
@@ -294,17 +295,29 @@ __device__ __forceinline__ float4 finish4(const ConvParams& p, float4 v, const f
     return o;
 }
 
-// Stores one row's result at element offset `yo` from the unit's first row of y.  Nontemporal
-// stores: the layer's output is read again only by the next launch, so it streams through L2
-// instead of evicting the weights the A fragments reload every tap (1.4% of the Snake convs' time
-// on the benchmark configuration).
+// Stores one row's result at element offset `yo` from the unit's first row of y, if `ok`.
+// Buffer stores: a store of a lane that must not write gets a byte offset past the resource's
+// range and is dropped by the hardware's range check, so no branch surrounds the store.  (Branches
+// around stores make the compiler's vector-memory wait counts assume the store was skipped and
+// wait for it on the other path: a residual load issued after a store would be waited for together
+// with that store.)  Nontemporal: the layer's output is read again only by the next launch, so it
+// streams through L2 instead of evicting the weights the A fragments reload every tap (1.4% of the
+// Snake convs' time on the benchmark configuration).
+constexpr int kBufRecords = 0x7fffffff;         // the resource's range in bytes
+constexpr uint32_t kDropOffset = 0x80000000u;   // past it: the store is dropped
+constexpr int kCpolNT = 2;                      // cache policy: nontemporal
+constexpr int kBufFormat = 0x00020000;          // descriptor word 3: 32-bit data format, no swizzle
 template <bool OUT_H>
-__device__ __forceinline__ void store4(const EpiBase& eb, uint32_t yo, float4 o, uint2 pk) {
+__device__ __forceinline__ void store4(const EpiBase& eb, uint32_t yo, bool ok, float4 o, uint2 pk) {
+    typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+    typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+    const uint32_t off = ok ? yo * (OUT_H ? 2u : 4u) : kDropOffset;
     if constexpr (OUT_H) {
-        typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
-        __builtin_nontemporal_store((u32x2_t){pk.x, pk.y}, (u32x2_t*)((uint16_t*)eb.y + yo));
+        __builtin_amdgcn_raw_buffer_store_b64((u32x2_t){pk.x, pk.y}, eb.ry, (int)off, 0, kCpolNT);
     } else {
-        __builtin_nontemporal_store((f32x4){o.x, o.y, o.z, o.w}, (f32x4*)((float*)eb.y + yo));
+        __builtin_amdgcn_raw_buffer_store_b128(
+            (u32x4_t){__float_as_uint(o.x), __float_as_uint(o.y), __float_as_uint(o.z), __float_as_uint(o.w)}, eb.ry,
+            (int)off, 0, kCpolNT);
     }
 }
 
@@ -344,7 +357,7 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
     constexpr bool CONVT = EPI == EPI_CONVT || EPI == EPI_CONVT_REFLECT;
     constexpr int NR = CONVT ? 1 : kNumRes<EPI>;
     constexpr int NRA = NR > 0 ? NR : 1;
-    constexpr int QB = NR > 1 ? 2 : (CONVT ? 4 : 8);  // column groups per residual batch
+    constexpr int QB = NR > 1 ? 2 : (NR == 1 ? 4 : 8);  // column groups per batch
     const int l32 = lane & 31, lh = lane >> 5;
     const int cq = lane & 15, cg = lane >> 4;
     const int wcol0 = wn * 128;                // this wave's first column within the tile
@@ -374,6 +387,7 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
     EpiBase eb;
     const int64_t n0 = u.n0;
     eb.y = OUT_H ? (void*)((uint16_t*)p.y + n0 * p.y_ld) : (void*)(p.y + n0 * p.y_ld);
+    eb.ry = __builtin_amdgcn_make_buffer_rsrc(eb.y, 0, kBufRecords, kBufFormat);  // raw (stride 0) buffer
     eb.r0 = eb.r1 = eb.r2 = nullptr;
     if constexpr (EPI == EPI_ADD_FROM || EPI == EPI_MEAN3) eb.r0 = p.r0 + n0 * p.r0_ld;
     if constexpr (EPI == EPI_MEAN3) eb.r1 = p.r1 + n0 * p.r0_ld, eb.r2 = p.r2 + n0 * p.r0_ld;
@@ -382,37 +396,48 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
     const uint32_t yz = u.m0, rz = u.m0;  // clamped operand of an invalid row: row 0 of the unit
     float s1[4] = {0.f, 0.f, 0.f, 0.f}, s2[4] = {0.f, 0.f, 0.f, 0.f}, sft[4] = {0.f, 0.f, 0.f, 0.f};
     float cnt = 0.f;  // ConvT: rows this lane group wrote (the statistics' count)
+    // Batches of QB column groups, BPS per 32-column slice.  The residual loads of batch b + LEAD are
+    // issued before batch b's stores: vector-memory counters complete in issue order (stores
+    // included), so a load issued after a store could only be waited for together with that store.
+    constexpr int BPS = 8 / QB, NB = 4 * BPS;
+    constexpr int LEAD = (NR > 0 && !CONVT) ? 1 : 0, RING = LEAD + 1;  // ConvT: no registers to spare
+    float4 res[RING][QB][NRA];
+    // unconditional loads (invalid columns / rows read column 0 / row 0 of the tile)
+    auto issue = [&](int b) {
+        const int j = b / BPS, q0 = (b % BPS) * QB;
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
+        for (int qq = 0; qq < QB; qq++) {
+            const int c = j * 32 + 4 * (q0 + qq);
+            if constexpr (CONVT) {
+                bool ok;
+                const int64_t d = convt_dest(wcol0 + c + cg, ok);
+                res[b % RING][qq][0] = *(const float4*)(p.r0 + d * p.r0_ld + cg_.co);
+            } else {
+                const bool ok = wcol0 + c + cg < u.nv && mok;
+                load_res<EPI>(p, eb, ok ? yo0 + __umul24(c, yld) : yz, ok ? ro0 + __umul24(c, rld) : rz,
+                              ok ? n0 + wcol0 + cg + c : n0, ok ? m : u.m0, res[b % RING][qq]);
+            }
+        }
+    };
+    if constexpr (NR > 0) {
 #pragma unroll
-        for (int i = 0; i < 2; i++)
+        for (int b = 0; b < LEAD; b++) issue(b);
+    }
 #pragma unroll
-            for (int g = 0; g < 4; g++)
-                *(float4*)(scr + l32 * kScrLd + i * 32 + 8 * g + 4 * lh) =
-                    make_float4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]);
-        __builtin_amdgcn_wave_barrier();  // LDS operations of one wave execute in order
+    for (int b = 0; b < NB; b++) {
+        const int j = b / BPS, q0 = (b % BPS) * QB;
+        if (b % BPS == 0) {
 #pragma unroll
-        for (int q0 = 0; q0 < 8; q0 += QB) {
-            float4 res[QB][NRA];
+            for (int i = 0; i < 2; i++)
+#pragma unroll
+                for (int g = 0; g < 4; g++)
+                    *(float4*)(scr + l32 * kScrLd + i * 32 + 8 * g + 4 * lh) = make_float4(
+                        acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]);
+            __builtin_amdgcn_wave_barrier();  // LDS operations of one wave execute in order
+        }
+        {
             if constexpr (NR > 0) {
-                // unconditional loads (invalid columns / rows read column 0 / row 0 of the tile)
-#pragma unroll
-                for (int qq = 0; qq < QB; qq++) {
-                    const int c = j * 32 + 4 * (q0 + qq);
-                    if constexpr (CONVT) {
-                        bool ok;
-                        const int64_t d = convt_dest(wcol0 + c + cg, ok);
-                        res[qq][0] = *(const float4*)(p.r0 + d * p.r0_ld + cg_.co);
-                    } else {
-                        const bool ok = wcol0 + c + cg < u.nv && mok;
-                        load_res<EPI>(p, eb, ok ? yo0 + __umul24(c, yld) : yz, ok ? ro0 + __umul24(c, rld) : rz,
-                                      ok ? n0 + wcol0 + cg + c : n0, ok ? m : u.m0, res[qq]);
-                    }
-                }
-#pragma unroll
-                for (int qq = 0; qq < QB; qq++)
-#pragma unroll
-                    for (int e = 0; e < NRA; e++) ready(res[qq][e]);
+                if (b + LEAD < NB) issue(b + LEAD);
             }
             // all LDS reads of the batch first, one wait, then the arithmetic and the stores
             float4 v[QB];
@@ -420,6 +445,13 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
             for (int qq = 0; qq < QB; qq++) v[qq] = *(const float4*)(scr + (4 * (q0 + qq) + cg) * kScrLd + 4 * cq);
 #pragma unroll
             for (int qq = 0; qq < QB; qq++) ready(v[qq]);
+            float4(&rc)[QB][NRA] = res[b % RING];
+            if constexpr (NR > 0) {
+#pragma unroll
+                for (int qq = 0; qq < QB; qq++)
+#pragma unroll
+                    for (int e = 0; e < NRA; e++) ready(rc[qq][e]);
+            }
 #pragma unroll
             for (int qq = 0; qq < QB; qq++) {
                 const int q = q0 + qq;
@@ -432,7 +464,7 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
                     bool ok;
                     const int64_t d = convt_dest(col, ok);
                     const float4 w = make_float4(v[qq].x + cb.x, v[qq].y + cb.y, v[qq].z + cb.z, v[qq].w + cb.w);
-                    const float4 r = res[qq][0];
+                    const float4 r = rc[qq][0];
                     o = make_float4(w.x + r.x, w.y + r.y, w.z + r.z, w.w + r.w);
                     valid = ok;
                     if (ok) *(float4*)(p.y + d * p.y_ld + cg_.co) = o;
@@ -446,8 +478,8 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
                     if constexpr (STATS) cnt += ok ? 1.f : 0.f;
                 } else {
                     uint2 pk;  // v = conv + bias (the accumulators started at the bias)
-                    o = finish4<EPI, OUT_H>(p, v[qq], res[qq], pk);
-                    if (valid && mok) store4<OUT_H>(eb, yo0 + __umul24(j * 32 + 4 * q, yld), o, pk);
+                    o = finish4<EPI, OUT_H>(p, v[qq], rc[qq], pk);
+                    store4<OUT_H>(eb, yo0 + __umul24(j * 32 + 4 * q, yld), valid && mok, o, pk);
                 }
                 if constexpr (STATS) {
                     const float ov[4] = {o.x, o.y, o.z, o.w};
@@ -461,7 +493,7 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
                 }
             }
         }
-        __builtin_amdgcn_wave_barrier();  // LDS operations of one wave execute in order
+        if (b % BPS == BPS - 1) __builtin_amdgcn_wave_barrier();  // the slice's LDS reads before the next writes
     }
     if constexpr (STATS) {
 #pragma unroll
@@ -689,6 +721,8 @@ hipError_t launch_t(const ConvParams& p, int n_cu, hipStream_t s) {
     if (!CONVT && p.m_pad > kMaxBias) return hipErrorInvalidValue;  // the bias staged in LDS
     if (PRO == PRO_ADAIN_SNAKE && p.cin % kCK != 0) return hipErrorInvalidValue;  // no channel mask there
     if (p.l_in >= (int64_t)1 << 30 || p.tiles.count >= (int64_t)1 << 28) return hipErrorInvalidValue;  // 32-bit rows
+    // epilogue stores: byte offsets within one unit's rows inside the buffer resource's range
+    if (!CONVT && ((int64_t)BN * p.y_ld + p.m_pad) * 4 >= kBufRecords) return hipErrorInvalidValue;
     // producer loads: 32-bit byte offsets within one item's rows
     if (p.in_max_len * p.x_ld * (PRO != PRO_BF16 && !IN_H ? 4 : 2) >= (int64_t)1 << 32) return hipErrorInvalidValue;
     auto kern = conv_mfma_kernel<PRO, EPI, WM, WN, STATS, IN_H, OUT_H>;
