@@ -351,7 +351,8 @@ __device__ __forceinline__ void init_acc(f32x16 (&acc)[2][4], const float* bias_
 // f32): afterwards 16 lanes hold one column's 64 channels (lane group cg = column, cq = channel
 // quad), so every store and residual load covers whole 256-byte column rows, and the statistics
 // accumulate per lane over columns with one cross-group reduction at the end.
-template <int EPI, int WM, int WN, bool STATS, bool OUT_H>
+// FULL: every column of the wave and every row of the unit is valid (no masks).
+template <int EPI, int WM, int WN, bool STATS, bool OUT_H, bool FULL>
 __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32x16 (&acc)[2][4], int wm, int wn,
                                          int lane, float* scr, const float* bias_s, int next_m0) {
     constexpr bool CONVT = EPI == EPI_CONVT || EPI == EPI_CONVT_REFLECT;
@@ -362,7 +363,7 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
     const int cq = lane & 15, cg = lane >> 4;
     const int wcol0 = wn * 128;                // this wave's first column within the tile
     const int m = u.m0 + wm * 64 + 4 * cq;     // this lane's 4 output rows after the transpose
-    const bool mok = m < p.m;
+    const bool mok = FULL || m < p.m;
     // ConvT: the item's output span (uniform, scalar loads), the lane's phase / channel and bias,
     // all once per unit
     ConvTGeo cg_ = {0, 0, 0, 0};
@@ -413,7 +414,7 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
                 const int64_t d = convt_dest(wcol0 + c + cg, ok);
                 res[b % RING][qq][0] = *(const float4*)(p.r0 + d * p.r0_ld + cg_.co);
             } else {
-                const bool ok = wcol0 + c + cg < u.nv && mok;
+                const bool ok = FULL || (wcol0 + c + cg < u.nv && mok);
                 load_res<EPI>(p, eb, ok ? yo0 + __umul24(c, yld) : yz, ok ? ro0 + __umul24(c, rld) : rz,
                               ok ? n0 + wcol0 + cg + c : n0, ok ? m : u.m0, res[b % RING][qq]);
             }
@@ -456,7 +457,7 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
             for (int qq = 0; qq < QB; qq++) {
                 const int q = q0 + qq;
                 const int col = wcol0 + j * 32 + 4 * q + cg;
-                bool valid = col < u.nv;
+                bool valid = FULL || col < u.nv;
                 // the values are computed for every row (they feed the statistics, masked there);
                 // only the store is conditional
                 float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -695,7 +696,16 @@ __global__ __launch_bounds__(64 * WM * WN + kNP) void conv_mfma_kernel(ConvParam
                 load_a(A[kc], n_m0, n_kk, n_c16 + kc);
             }
         }
-        if (last) epilogue<EPI, WM, WN, STATS, OUT_H>(p, cu, acc, wm, wn, lane, scr, bias_s, has_next ? nu.m0 : cu.m0);
+        if (last) {
+            const int next_m0 = has_next ? nu.m0 : cu.m0;
+            // (not for the 256-channel accumulate-with-statistics variant: a second epilogue copy
+            // makes it spill)
+            constexpr bool kFullPath = !CONVT && !(EPI == EPI_ACCUM && WM == 4 && STATS);
+            if (kFullPath && cu.nv >= wn * 128 + 128 && cu.m0 + BM <= p.m)  // uniform: the common case
+                epilogue<EPI, WM, WN, STATS, OUT_H, true>(p, cu, acc, wm, wn, lane, scr, bias_s, next_m0);
+            else
+                epilogue<EPI, WM, WN, STATS, OUT_H, false>(p, cu, acc, wm, wn, lane, scr, bias_s, next_m0);
+        }
         __syncthreads();  // hand the slab buffer back to the producers
         if (last) {
             sl = 0;
