@@ -367,13 +367,19 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
     // ConvT: the item's output span (uniform, scalar loads), the lane's phase / channel and bias,
     // all once per unit
     ConvTGeo cg_ = {0, 0, 0, 0};
-    float4 cb = make_float4(0.f, 0.f, 0.f, 0.f);
+    float4 cb = make_float4(0.f, 0.f, 0.f, 0.f), rfl = cb;
+    int64_t ubase = 0;  // ConvT: the first output row the unit can write (its stores' base)
     if constexpr (CONVT) {
         cg_.os = ld_const(p.out_start, u.item);
         cg_.ol = ld_const(p.out_len, u.item) - (EPI == EPI_CONVT_REFLECT ? 1 : 0);
         const int mm = mok ? m : u.m0;
         cg_.ph = mm / p.cout, cg_.co = mm - cg_.ph * p.cout;
         cb = *(const float4*)(p.bias + cg_.co);
+        // rows o >= stride n0 - pad (o + 1 with the reflection pad), and the item's first row when
+        // the unit writes o = os + 1 (then stride n0 - pad - 1 <= os)
+        ubase = max(cg_.os, (int64_t)p.stride_t * u.n0 - p.pad_t - 1);
+        // the reflected row's residual: r0 at the item's first row
+        if constexpr (EPI == EPI_CONVT_REFLECT) rfl = *(const float4*)(p.r0 + cg_.os * p.r0_ld + cg_.co);
         ready(cb);
     }
     // ConvT output column of tile column col, whether this lane writes it, and the row written
@@ -388,6 +394,7 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
     EpiBase eb;
     const int64_t n0 = u.n0;
     eb.y = OUT_H ? (void*)((uint16_t*)p.y + n0 * p.y_ld) : (void*)(p.y + n0 * p.y_ld);
+    if constexpr (CONVT) eb.y = p.y + ubase * p.y_ld;
     eb.ry = __builtin_amdgcn_make_buffer_rsrc(eb.y, 0, kBufRecords, kBufFormat);  // raw (stride 0) buffer
     eb.r0 = eb.r1 = eb.r2 = nullptr;
     if constexpr (EPI == EPI_ADD_FROM || EPI == EPI_MEAN3) eb.r0 = p.r0 + n0 * p.r0_ld;
@@ -401,7 +408,7 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
     // issued before batch b's stores: vector-memory counters complete in issue order (stores
     // included), so a load issued after a store could only be waited for together with that store.
     constexpr int BPS = 8 / QB, NB = 4 * BPS;
-    constexpr int LEAD = (NR > 0 && !CONVT) ? 1 : 0, RING = LEAD + 1;  // ConvT: no registers to spare
+    constexpr int LEAD = NR > 0 ? 1 : 0, RING = LEAD + 1;
     float4 res[RING][QB][NRA];
     // unconditional loads (invalid columns / rows read column 0 / row 0 of the tile)
     auto issue = [&](int b) {
@@ -468,13 +475,13 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
                     const float4 r = rc[qq][0];
                     o = make_float4(w.x + r.x, w.y + r.y, w.z + r.z, w.w + r.w);
                     valid = ok;
-                    if (ok) *(float4*)(p.y + d * p.y_ld + cg_.co) = o;
-                    if (EPI == EPI_CONVT_REFLECT && ok && d == cg_.os + 2) {
+                    const uint2 nopk = make_uint2(0u, 0u);
+                    store4<false>(eb, (uint32_t)((d - ubase) * p.y_ld) + cg_.co, ok, o, nopk);
+                    if constexpr (EPI == EPI_CONVT_REFLECT) {
                         // o = os + 1 also fills the item's first row (the reflected sample)
                         // (the statistics leave this row to finalize, which reads it back)
-                        const float4 r2 = *(const float4*)(p.r0 + cg_.os * p.r0_ld + cg_.co);
-                        *(float4*)(p.y + cg_.os * p.y_ld + cg_.co) =
-                            make_float4(w.x + r2.x, w.y + r2.y, w.z + r2.z, w.w + r2.w);
+                        store4<false>(eb, (uint32_t)((cg_.os - ubase) * p.y_ld) + cg_.co, ok && d == cg_.os + 2,
+                                      make_float4(w.x + rfl.x, w.y + rfl.y, w.z + rfl.z, w.w + rfl.w), nopk);
                     }
                     if constexpr (STATS) cnt += ok ? 1.f : 0.f;
                 } else {
@@ -733,6 +740,7 @@ hipError_t launch_t(const ConvParams& p, int n_cu, hipStream_t s) {
     if (p.l_in >= (int64_t)1 << 30 || p.tiles.count >= (int64_t)1 << 28) return hipErrorInvalidValue;  // 32-bit rows
     // epilogue stores: byte offsets within one unit's rows inside the buffer resource's range
     if (!CONVT && ((int64_t)BN * p.y_ld + p.m_pad) * 4 >= kBufRecords) return hipErrorInvalidValue;
+    if (CONVT && ((int64_t)p.stride_t * (BN + 1) + p.pad_t + 2) * p.y_ld * 4 >= kBufRecords) return hipErrorInvalidValue;
     // producer loads: 32-bit byte offsets within one item's rows
     if (p.in_max_len * p.x_ld * (PRO != PRO_BF16 && !IN_H ? 4 : 2) >= (int64_t)1 << 32) return hipErrorInvalidValue;
     auto kern = conv_mfma_kernel<PRO, EPI, WM, WN, STATS, IN_H, OUT_H>;
