@@ -158,6 +158,22 @@ void kk_plan_free(kk_plan* plan);
  * infinities included) are clamped and counted, NaN stores 0.  dst[b] receives item b's 600 N_b
  * samples; clipped (optional) its count.  Half the bytes of kk_plan_fetch over PCIe. */
 int kk_plan_fetch_pcm16(kk_plan* plan, int16_t* const* dst, int64_t* clipped, char* err, size_t errlen);
+/* Asynchronous output path, so that the host writes batch n while the GPU computes batch n + 1
+ * (the reference overlaps its WAV writer threads with synthesis, src/cli.rs:553-622).
+ * kk_host_alloc / kk_host_free: pinned host memory (hipHostMalloc).
+ * kk_plan_item_samples: item `item`'s sample offset and count in the plan's sample layout
+ * (offset 600 a_b, a_b = sum_{j<b} (N_j + 2); count 600 N_b).
+ * kk_plan_fetch_pcm16_async: enqueues the PCM_16 encoding of kk_plan_fetch_pcm16 and one copy of
+ * the whole sample layout (600 ln int16, gap samples 0) into `dst`, and of the clip counts into
+ * `clipped` (optional, n_items int64), behind the plan's work on the context's stream, and returns.
+ * Both must be pinned memory from kk_host_alloc.  kk_plan_fetch_wait blocks until they have
+ * landed; a later kk_plan_run of the plan is ordered after the copy (one stream), so it may be
+ * enqueued before the wait.  One fetch per plan may be pending. */
+int kk_host_alloc(kk_ctx* ctx, size_t bytes, void** out, char* err, size_t errlen);
+void kk_host_free(void* p);
+int kk_plan_item_samples(const kk_plan* plan, int item, int64_t* offset, int64_t* count);
+int kk_plan_fetch_pcm16_async(kk_plan* plan, int16_t* dst, int64_t* clipped, char* err, size_t errlen);
+int kk_plan_fetch_wait(kk_plan* plan, char* err, size_t errlen);
 /* The same encoding of a host array (uploads, encodes on the device, downloads). */
 int kk_encode_pcm16(kk_ctx* ctx, const float* audio, int64_t n, int16_t* out, int64_t* clipped, char* err,
                     size_t errlen);

@@ -13,6 +13,7 @@
 #include <map>
 #include <set>
 #include <memory>
+#include <mutex>
 #include <string>
 #include <tuple>
 #include <vector>
@@ -470,6 +471,13 @@ struct kk_plan {
         if (graph) (void)hipGraphExecDestroy(graph);
         graph = nullptr, graph_until = -1;
     }
+    // kk_plan_fetch_pcm16_async: recorded after its copies; pending until kk_plan_fetch_wait
+    hipEvent_t fetch_ev = nullptr;
+    bool fetch_pending = false;
+    void drop_fetch_event() {
+        if (fetch_ev) (void)hipEventDestroy(fetch_ev);
+        fetch_ev = nullptr, fetch_pending = false;
+    }
     std::vector<kk::DevBuf*> owned() {
         return {&t_en, &src_row, &f0, &en, &style, &seeds, &kinds, &rand_ini, &fixed_noise, &gb, &xcat, &xin_a,
                 &xin_b, &hdec, &pool, &sc_half, &dec_out, &pp, &spec, &B[0], &B[1], &B[2], &B[3], &B[4], &B[5],
@@ -575,7 +583,7 @@ static void setup_generator(kk_plan* p, const std::vector<const float*>& f0s, co
     for (int b = 0; b < nb; b++) as[b] = 600 * p->a[b], ns[b] = 600 * p->nfr[b];
     p->audio_start.upload(as);
     p->pcm_len.upload(ns);
-    p->pcm.alloc((size_t)600 * ln * sizeof(int16_t));
+    alloc_zero(p, p->pcm, (size_t)600 * ln * sizeof(int16_t));  // gap samples stay 0
     p->pcm_clip.alloc((size_t)nb * sizeof(unsigned long long));
 
     p->gb.alloc((size_t)nb * p->ctx->model.style_rows * sizeof(float));
@@ -1105,6 +1113,7 @@ static void prebuild_tiles(kk_plan* p) {
 
 static void release_plan_device(kk_plan* p) {
     p->drop_graph();
+    p->drop_fetch_event();
     for (DevBuf* b : p->owned()) b->release();
     for (kk::Dom* d : {&p->dn, &p->d2, &p->d20, &p->d120, &p->ds}) {
         d->col_d.release();
@@ -1368,6 +1377,95 @@ int kk_plan_fetch_pcm16(kk_plan* plan, int16_t* const* dst, int64_t* clipped, ch
     });
 }
 
+// Pinned host allocations made by kk_host_alloc: [base, base + bytes) by base.
+static std::mutex g_pinned_mu;
+static std::map<uintptr_t, size_t> g_pinned;
+
+static bool is_pinned(const void* p, size_t bytes) {
+    std::lock_guard<std::mutex> lock(g_pinned_mu);
+    const uintptr_t a = (uintptr_t)p;
+    auto it = g_pinned.upper_bound(a);
+    if (it == g_pinned.begin()) return false;
+    --it;
+    return a >= it->first && a + bytes <= it->first + it->second;
+}
+
+int kk_host_alloc(kk_ctx* ctx, size_t bytes, void** out, char* err, size_t errlen) {
+    if (!ctx || !out) return KK_ERR_INVALID;
+    *out = nullptr;
+    return guard(err, errlen, [&] {
+        use_device(ctx);
+        check(bytes > 0, "kk_host_alloc of 0 bytes");
+        void* p = nullptr;
+        KK_HIP(hipHostMalloc(&p, bytes, hipHostMallocDefault));
+        std::lock_guard<std::mutex> lock(g_pinned_mu);
+        g_pinned[(uintptr_t)p] = bytes;
+        *out = p;
+    });
+}
+
+void kk_host_free(void* p) {
+    if (!p) return;
+    {
+        std::lock_guard<std::mutex> lock(g_pinned_mu);
+        auto it = g_pinned.find((uintptr_t)p);
+        if (it == g_pinned.end()) return;  // not ours: left alone
+        g_pinned.erase(it);
+    }
+    (void)hipHostFree(p);
+}
+
+int kk_plan_item_samples(const kk_plan* plan, int item, int64_t* offset, int64_t* count) {
+    if (!plan || !offset || !count || item < 0 || item >= plan->nb || plan->kind == PLAN_SNAKE) return KK_ERR_INVALID;
+    *offset = 600 * plan->a[item];
+    *count = 600 * plan->nfr[item];
+    return KK_OK;
+}
+
+int kk_plan_fetch_pcm16_async(kk_plan* plan, int16_t* dst, int64_t* clipped, char* err, size_t errlen) {
+    if (!plan || !dst) return KK_ERR_INVALID;
+    if (!plan->ctx) {
+        set_err(err, errlen, "plan outlived its context");
+        return KK_ERR_STATE;
+    }
+    return guard(err, errlen, [&] {
+        use_device(plan->ctx);
+        check(plan->kind != PLAN_SNAKE, "a snake plan has no audio");
+        check(plan->last_until >= KK_STAGE_ALL, "plan has not run to the end");
+        check(!plan->fetch_pending, "the previous asynchronous fetch has not been waited for");
+        const size_t pcm_bytes = sizeof(int16_t) * 600 * (size_t)plan->ln;
+        check(is_pinned(dst, pcm_bytes), "dst must be " + std::to_string(pcm_bytes) +
+                                             " bytes of pinned memory from kk_host_alloc");
+        check(!clipped || is_pinned(clipped, sizeof(int64_t) * plan->nb),
+              "clipped must be pinned memory from kk_host_alloc");
+        hipStream_t s = plan->ctx->stream;
+        if (!plan->fetch_ev) KK_HIP(hipEventCreateWithFlags(&plan->fetch_ev, hipEventDisableTiming));
+        KK_HIP(launch_zero(plan->pcm_clip.p, (int64_t)plan->nb * 8, s));
+        KK_HIP(launch_pcm16(plan->audio.as<float>(), plan->audio_start.as<int64_t>(), plan->pcm_len.as<int64_t>(),
+                            plan->ist_item.as<int64_t>(), plan->ist_s0.as<int64_t>(), plan->n_ist,
+                            plan->pcm.as<int16_t>(), plan->pcm_clip.as<unsigned long long>(), s));
+        KK_HIP(hipMemcpyAsync(dst, plan->pcm.p, pcm_bytes, hipMemcpyDeviceToHost, s));
+        if (clipped)
+            KK_HIP(hipMemcpyAsync(clipped, plan->pcm_clip.p, sizeof(int64_t) * plan->nb, hipMemcpyDeviceToHost, s));
+        KK_HIP(hipEventRecord(plan->fetch_ev, s));
+        plan->fetch_pending = true;
+    });
+}
+
+int kk_plan_fetch_wait(kk_plan* plan, char* err, size_t errlen) {
+    if (!plan) return KK_ERR_INVALID;
+    if (!plan->ctx) {
+        set_err(err, errlen, "plan outlived its context");
+        return KK_ERR_STATE;
+    }
+    return guard(err, errlen, [&] {
+        if (!plan->fetch_pending) return;
+        use_device(plan->ctx);
+        plan->fetch_pending = false;
+        KK_HIP(hipEventSynchronize(plan->fetch_ev));
+    });
+}
+
 int kk_encode_pcm16(kk_ctx* ctx, const float* audio, int64_t n, int16_t* out, int64_t* clipped, char* err,
                     size_t errlen) {
     if (!ctx || n < 0 || (n > 0 && (!audio || !out))) return KK_ERR_INVALID;
@@ -1479,6 +1577,7 @@ void kk_plan_free(kk_plan* plan) {
         (void)hipSetDevice(plan->ctx->device);
         (void)hipStreamSynchronize(plan->ctx->stream);
         plan->drop_graph();
+        plan->drop_fetch_event();
         plan->ctx->plans.erase(plan);
     }
     delete plan;

@@ -22,7 +22,8 @@ EXPORTS = [
     "kk_output_free", "kk_plan_create", "kk_plan_create_generator", "kk_plan_create_snake", "kk_plan_run",
     "kk_plan_sync", "kk_plan_fetch", "kk_plan_tap", "kk_plan_get_info", "kk_plan_free", "kk_set_profiling",
     "kk_profile_read", "kk_durations_from_logits", "kk_layout_frames", "kk_layout_col_item", "kk_layout_src_row",
-    "kk_plan_fetch_pcm16", "kk_encode_pcm16", "kk_wav_header",
+    "kk_plan_fetch_pcm16", "kk_encode_pcm16", "kk_wav_header", "kk_host_alloc", "kk_host_free",
+    "kk_plan_item_samples", "kk_plan_fetch_pcm16_async", "kk_plan_fetch_wait",
 ]
 
 
@@ -92,6 +93,12 @@ def lib():
         L.kk_plan_tap.argtypes = [vp, cp, i32, vp, i64, cp, sz]
         L.kk_plan_fetch_pcm16.argtypes = [vp, C.POINTER(vp), vp, cp, sz]
         L.kk_encode_pcm16.argtypes = [vp, vp, i64, vp, vp, cp, sz]
+        L.kk_host_alloc.argtypes = [vp, sz, C.POINTER(vp), cp, sz]
+        L.kk_host_free.argtypes = [vp]
+        L.kk_host_free.restype = None
+        L.kk_plan_item_samples.argtypes = [vp, i32, C.POINTER(C.c_int64), C.POINTER(C.c_int64)]
+        L.kk_plan_fetch_pcm16_async.argtypes = [vp, vp, vp, cp, sz]
+        L.kk_plan_fetch_wait.argtypes = [vp, cp, sz]
         L.kk_wav_header.argtypes = [i32, C.c_uint32, C.c_uint64, vp, cp, sz]
         L.kk_plan_get_info.argtypes = [vp, C.POINTER(PlanInfo)]
         L.kk_plan_free.argtypes = [vp]
@@ -241,6 +248,10 @@ class Context:
     def plan(self, items):
         return Plan.decoder(self, items)
 
+    def host_alloc(self, count, dtype):
+        """kk_host_alloc: a pinned host array of `count` elements of `dtype` (freed with .free())."""
+        return PinnedArray(self, count, dtype)
+
     def encode_pcm16(self, audio):
         """kk_encode_pcm16: a host f32 array as PCM_16 (encoded on the device) and its clipped count."""
         a = _f32(audio).ravel()
@@ -249,6 +260,24 @@ class Context:
         err = _err()
         _check(lib().kk_encode_pcm16(self.h, _p(a), a.size, _p(out), _p(clipped), err, len(err)), err)
         return out, int(clipped[0])
+
+
+class PinnedArray:
+    """Pinned host memory from kk_host_alloc, viewed as a numpy array (`.array`)."""
+
+    def __init__(self, ctx, count, dtype):
+        dt = np.dtype(dtype)
+        self.ptr = C.c_void_p()
+        err = _err()
+        _check(lib().kk_host_alloc(ctx.h, max(1, count) * dt.itemsize, C.byref(self.ptr), err, len(err)), err)
+        buf = (C.c_char * (max(1, count) * dt.itemsize)).from_address(self.ptr.value)
+        self.array = np.frombuffer(buf, dt, count)
+
+    def free(self):
+        if self.ptr:
+            self.array = None
+            lib().kk_host_free(self.ptr)
+            self.ptr = C.c_void_p()
 
 
 def _decoder_items(items):
@@ -342,6 +371,22 @@ class Plan:
         err = _err()
         _check(lib().kk_plan_fetch_pcm16(self.h, ptrs, _p(clipped), err, len(err)), err)
         return outs, clipped
+
+    def item_samples(self, item):
+        """kk_plan_item_samples: (offset, count) of item `item` in the plan's sample layout."""
+        off, cnt = C.c_int64(), C.c_int64()
+        _check(lib().kk_plan_item_samples(self.h, item, C.byref(off), C.byref(cnt)), _err())
+        return off.value, cnt.value
+
+    def fetch_pcm16_async(self, dst, clipped=None):
+        """kk_plan_fetch_pcm16_async into PinnedArrays (int16 of 600 ln, int64 of n_items)."""
+        err = _err()
+        _check(lib().kk_plan_fetch_pcm16_async(self.h, dst.ptr, clipped.ptr if clipped else None, err, len(err)),
+               err)
+
+    def fetch_wait(self):
+        err = _err()
+        _check(lib().kk_plan_fetch_wait(self.h, err, len(err)), err)
 
     def tap(self, name, item, shape):
         out = np.zeros(shape, np.float32)

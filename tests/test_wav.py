@@ -112,3 +112,47 @@ def test_plan_fetch_pcm16(gpu_ctx):
     for a, p, c in zip(audio, pcm, clipped):
         want, wclip = O.encode_pcm16(a)
         assert p.shape == a.shape and np.array_equal(p, want) and c == wclip
+
+
+@pytest.mark.gpu
+def test_plan_fetch_pcm16_async(gpu_ctx):
+    """The asynchronous fetch into pinned memory: the same bits as the synchronous fetch, gap samples
+    0, and a run of the next batch enqueued before the wait does not disturb the copy."""
+    from kokoro_hip import api, workloads
+    items = workloads.small_items(73, [5, 11, 2])
+    other = workloads.small_items(74, [12, 4, 9])  # a different batch of the same shape
+    with api.Plan.decoder(gpu_ctx, items) as plan, api.Plan.decoder(gpu_ctx, other) as plan2:
+        plan.run()
+        pcm, clipped = plan.fetch_pcm16()
+        ln = plan.info()["ln"]
+        dst = gpu_ctx.host_alloc(600 * ln, np.int16)
+        clip = gpu_ctx.host_alloc(len(items), np.int64)
+        try:
+            dst.array[:] = 12345
+            plan.fetch_pcm16_async(dst, clip)
+            plan.run()  # the next batch on the same plan, enqueued before the wait
+            plan2.run()
+            plan.fetch_wait()
+            got = dst.array.copy()
+            covered = np.zeros(got.size, bool)
+            for b in range(len(items)):
+                off, cnt = plan.item_samples(b)
+                assert cnt == pcm[b].size
+                assert np.array_equal(got[off:off + cnt], pcm[b]), b
+                covered[off:off + cnt] = True
+            assert not got[~covered].any()  # gap samples
+            assert np.array_equal(clip.array, clipped)
+            # a second fetch without a wait is refused; one into pageable memory too
+            plan.fetch_pcm16_async(dst)
+            with pytest.raises(api.KKError, match="not been waited"):
+                plan.fetch_pcm16_async(dst)
+            plan.fetch_wait()
+            plan.fetch_wait()  # nothing pending: a no-op
+            pageable = api.PinnedArray.__new__(api.PinnedArray)
+            host = np.zeros(600 * ln, np.int16)
+            pageable.ptr = api.C.c_void_p(host.ctypes.data)
+            with pytest.raises(api.KKError, match="pinned"):
+                plan.fetch_pcm16_async(pageable)
+        finally:
+            dst.free()
+            clip.free()
