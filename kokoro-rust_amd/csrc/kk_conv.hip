@@ -44,7 +44,8 @@ namespace {
 constexpr int kCK = 64;       // input channels per LDS slab
 constexpr int kRS = kCK + 8;  // LDS row stride (bf16 elements, 144 bytes)
 constexpr int kNJ = 8;        // 16-column MFMA tiles per wave (wave N = 128)
-constexpr int kMaxHalo = 64;  // largest (k - 1) * dil the staging covers
+constexpr int kMaxHalo = 64;    // largest (k - 1) * dil the staging covers
+constexpr int kSmallHalo = 16;  // layers with (k - 1) * dil up to this run fewer producer passes
 constexpr int kNP = 256;      // producer threads per block
 
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
@@ -94,10 +95,10 @@ __device__ __forceinline__ float vgpr_f(float x) { return __int_as_float(vgpr(__
 // number of loads is fixed and the producers' wait counts are static), convert() applies the
 // prologue and writes bf16 rows into an LDS buffer.  Rows outside the item, and channels >= cin,
 // are staged as 0 (the conv's zero padding of the activated signal).
-template <int PRO, bool IN_H, int BN>
+template <int PRO, bool IN_H, int BN, int MAXH>
 struct Slot {
-    static constexpr int RP = kNP / 16;                       // rows per pass
-    static constexpr int RB = (BN + kMaxHalo + RP - 1) / RP;  // passes
+    static constexpr int RP = kNP / 16;                   // rows per pass
+    static constexpr int RB = (BN + MAXH + RP - 1) / RP;  // passes (MAXH: the largest halo served)
     static constexpr bool WIDE = PRO != PRO_BF16 && !IN_H;    // f32 source: 4 dwords per quad
     static constexpr int NW = WIDE ? 4 : 2;
     static constexpr bool ADAIN = PRO == PRO_ADAIN_LEAKY || PRO == PRO_ADAIN_SNAKE;
@@ -530,7 +531,7 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
     init_acc<!CONVT>(acc, bias_s, next_m0, wm, lane);  // the next unit starts at its bias
 }
 
-template <int PRO, int EPI, int WM, int WN, bool STATS, bool IN_H, bool OUT_H>
+template <int PRO, int EPI, int WM, int WN, bool STATS, bool IN_H, bool OUT_H, int MAXH>
 __global__ __launch_bounds__(64 * WM * WN + kNP) void conv_mfma_kernel(ConvParams p) {
     constexpr int BM = 64 * WM, BN = 16 * kNJ * WN, NC = 64 * WM * WN;
     extern __shared__ __align__(16) uint16_t xs[];
@@ -575,7 +576,7 @@ __global__ __launch_bounds__(64 * WM * WN + kNP) void conv_mfma_kernel(ConvParam
         // last unit), so the number of loads in flight is the same at every wait.
         const int pt = threadIdx.x - NC;
         const int q = (pt & 15) * 4, rr = pt >> 4;
-        Slot<PRO, IN_H, BN> s0, s1;
+        Slot<PRO, IN_H, BN, MAXH> s0, s1;
         // iterators over (unit, slab) steps: load and convert
         int lU = blockIdx.x, ls = 0, cU = blockIdx.x, cs = 0;
         Unit lu, cuv;
@@ -743,21 +744,26 @@ hipError_t launch_t(const ConvParams& p, int n_cu, hipStream_t s) {
     if (CONVT && ((int64_t)p.stride_t * (BN + 1) + p.pad_t + 2) * p.y_ld * 4 >= kBufRecords) return hipErrorInvalidValue;
     // producer loads: 32-bit byte offsets within one item's rows
     if (p.in_max_len * p.x_ld * (PRO != PRO_BF16 && !IN_H ? 4 : 2) >= (int64_t)1 << 32) return hipErrorInvalidValue;
-    auto kern = conv_mfma_kernel<PRO, EPI, WM, WN, STATS, IN_H, OUT_H>;
-    static bool attr = false;
-    if (!attr) {
-        const hipError_t e =
-            hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem_max);
-        if (e != hipSuccess) return e;
-        attr = true;
-    }
     // one persistent block per CU; the grid is a multiple of 8 * mblocks
     const int64_t grp = 8 * (int64_t)(p.m_pad / BM);
     const int64_t units = ceil_div(p.tiles.count, 8) * grp;  // padded unit count
     const int64_t fit = std::max<int64_t>(1, n_cu / grp) * grp;
     const int64_t grid = std::min(units, fit);
-    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(NT), smem, s, p);
-    return hipGetLastError();
+    auto go = [&](auto kern, bool& attr) -> hipError_t {
+        if (!attr) {
+            const hipError_t e =
+                hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem_max);
+            if (e != hipSuccess) return e;
+            attr = true;
+        }
+        hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(NT), smem, s, p);
+        return hipGetLastError();
+    };
+    // small halos (every k3 layer, k7 at dilation 1, the ConvTs, 1x1 convs): the producers stage
+    // BN + 16 rows instead of BN + 64 (3 of 20 row passes fewer at BN 256, 3 of 12 at BN 128)
+    static bool attr_small = false, attr_max = false;
+    if (halo <= kSmallHalo) return go(conv_mfma_kernel<PRO, EPI, WM, WN, STATS, IN_H, OUT_H, kSmallHalo>, attr_small);
+    return go(conv_mfma_kernel<PRO, EPI, WM, WN, STATS, IN_H, OUT_H, kMaxHalo>, attr_max);
 }
 
 }  // namespace
