@@ -165,6 +165,8 @@ struct kk_ctx {
     int n_cu = 1;
     std::set<kk_plan*> plans;  // live plans: released (and orphaned) by kk_close
     hipStream_t stream = nullptr;
+    // two more streams (default priority) for the generator's independent resblock chains
+    hipStream_t side[2] = {nullptr, nullptr};
     std::string name;
     kk::Model model;
     bool profiling = false;
@@ -441,7 +443,9 @@ struct kk_plan {
     int64_t t_rows = 0;
     // intermediates
     kk::DevBuf gb, xcat, xin_a, xin_b, hdec, pool, sc_half, dec_out, pp, spec, B[6], post, audio, audio_start;
-    kk::DevBuf part, coef[5];
+    // coef[0..1]: the Snake steps' AdaIN pair; [2..4]: the resblocks' first AdaIN; [5..8]: the pair
+    // of resblock chains 0 and 1 (run on the context's side streams)
+    kk::DevBuf part, coef[9];
     int64_t part_bytes = 0;
     std::map<std::tuple<const kk::Dom*, int, int>, std::unique_ptr<kk::Tiles>> tiles;
     // item-aligned tiles of domain d, width w (built on first use, at plan creation)
@@ -462,26 +466,21 @@ struct kk_plan {
     double conv_flop = 0, snake_flop = 0;
     int64_t launches = 0;
     int last_until = 0;
-    // The launch sequence of kk_plan_run(until = graph_until), captured on its second run with that
-    // stage and replayed from then on (every buffer and tile list is fixed at plan creation).
-    hipGraphExec_t graph = nullptr;
-    int graph_until = -1;
-    int eager_until = -1;  // stage of the last eager run
-    void drop_graph() {
-        if (graph) (void)hipGraphExecDestroy(graph);
-        graph = nullptr, graph_until = -1;
-    }
     // kk_plan_fetch_pcm16_async: recorded after its copies; pending until kk_plan_fetch_wait
     hipEvent_t fetch_ev = nullptr;
     bool fetch_pending = false;
     void drop_fetch_event() {
         if (fetch_ev) (void)hipEventDestroy(fetch_ev);
         fetch_ev = nullptr, fetch_pending = false;
+        for (auto& e : chain_ev)
+            if (e) (void)hipEventDestroy(e), e = nullptr;
     }
+    // fork / join of the resblock chains (created on first use)
+    hipEvent_t chain_ev[3] = {nullptr, nullptr, nullptr};
     std::vector<kk::DevBuf*> owned() {
         return {&t_en, &src_row, &f0, &en, &style, &seeds, &kinds, &rand_ini, &fixed_noise, &gb, &xcat, &xin_a,
                 &xin_b, &hdec, &pool, &sc_half, &dec_out, &pp, &spec, &B[0], &B[1], &B[2], &B[3], &B[4], &B[5],
-                &post, &audio, &audio_start, &part, &coef[0], &coef[1], &coef[2], &coef[3], &coef[4], &src_item,
+                &post, &audio, &audio_start, &part, &coef[0], &coef[1], &coef[2], &coef[3], &coef[4], &coef[5], &coef[6], &coef[7], &coef[8], &src_item,
                 &src_f0, &ist_item, &ist_s0, &pcm, &pcm_len, &pcm_clip};
     }
 };
@@ -593,7 +592,7 @@ static void setup_generator(kk_plan* p, const std::vector<const float*>& f0s, co
     for (int i = 0; i < 6; i++) alloc_zero(p, p->B[i], big);
     alloc_zero(p, p->post, (size_t)l120 * kPostLd * sizeof(float));
     alloc_zero(p, p->audio, (size_t)600 * ln * sizeof(float));
-    for (int i = 0; i < 5; i++) p->coef[i].alloc((size_t)nb * kXinLd * sizeof(Coef));
+    for (int i = 0; i < 9; i++) p->coef[i].alloc((size_t)nb * kXinLd * sizeof(Coef));
     // statistics partials: every partial but the last two of each item covers at least 64 columns
     // of one item (the noise convs' 64-column tiles; the convs' 128-column wave spans)
     auto bound = [&](int64_t l, int64_t c) { return (l / 64 + 2 * (int64_t)nb + 2) * c; };
@@ -601,8 +600,9 @@ static void setup_generator(kk_plan* p, const std::vector<const float*>& f0s, co
     auto bound_t = [&](int64_t l_in, int64_t stride, int64_t c) { return (l_in / 128 + 2 * (int64_t)nb + 1) * stride * c; };
     const int64_t np = std::max({bound(ln, 1152), bound(2 * ln, 512), bound(l20, 256), bound(l120, 128),
                                  bound_t(l2, 10, 256), bound_t(l20, 6, 128)});
-    p->part.alloc((size_t)np * sizeof(StatPart));
-    p->part_bytes = (int64_t)p->part.bytes;
+    // three regions, one per concurrent resblock chain; part_bytes is one region
+    p->part.alloc((size_t)3 * np * sizeof(StatPart));
+    p->part_bytes = (int64_t)np * (int64_t)sizeof(StatPart);
 }
 
 struct Runner;
@@ -798,6 +798,8 @@ struct Runner {
     int64_t launches = 0;
     int64_t gb_ld() const { return m.style_rows; }
     Coef* cf(int i) const { return p->coef[i].as<Coef>(); }
+    int region = 0;  // statistics partials region of the current chain
+    StatPart* part() const { return p->part.as<StatPart>() + (size_t)region * (size_t)(p->part_bytes / sizeof(StatPart)); }
 
     hipEvent_t ev() {
         if (!ctx->event_pool.empty()) {
@@ -818,7 +820,7 @@ struct Runner {
     const Tiles& stats(const float* x, int64_t ld, int c, const Dom& d) {
         const Tiles& t = p->tl(d, kStatTile);
         need_part(t.count * c);
-        KK_LAUNCH(launch_stats_tiles(x, ld, c, t.dev(), p->part.as<StatPart>(), s));
+        KK_LAUNCH(launch_stats_tiles(x, ld, c, t.dev(), part(), s));
         launches++;
         return t;
     }
@@ -826,7 +828,7 @@ struct Runner {
     // item, row xrow_at[b] of xrow [.][c]).
     void fin(const Tiles& t, int wn, int c, const MAdain& a, Coef* coef, const float* xrow = nullptr,
              const int64_t* xrow_at = nullptr) {
-        KK_LAUNCH(launch_finalize(p->part.as<StatPart>(), c, wn, t.dev(), p->nb, p->gb.as<float>(), gb_ld(),
+        KK_LAUNCH(launch_finalize(part(), c, wn, t.dev(), p->nb, p->gb.as<float>(), gb_ld(),
                                a.gb_off, a.nw.as<float>(), a.nb.as<float>(), coef, s, xrow, c, xrow_at));
         launches++;
     }
@@ -874,7 +876,7 @@ struct Runner {
         q.out_start = o.dout->start_d.as<int64_t>(), q.out_len = o.dout->len_d.as<int64_t>();
         if (o.stats) {
             need_part(t.count * wn * (o.convt ? o.stride : 1) * c.cout);  // ConvT: per phase too
-            q.part = p->part.as<StatPart>();
+            q.part = part();
         }
         // algorithmic FLOP over valid columns; ConvT (K = 2 stride): each input column feeds
         // K x cout outputs = 2 m MACs per input channel
@@ -928,7 +930,8 @@ struct Runner {
     // x = (rb0(y) + rb1(y) + rb2(y)) / 3 (src/gpu_batch.rs:395-401); result in X[2].
     // yt: the tiles whose partials of y its producer (the ConvT) wrote, `yparts` per tile, with the
     // reflected first row of each item (xrow_at) outside them when y_refl; null: a statistics pass.
-    void resblock_mean(const MSnake* rbs, const float* y, float* X[3], float* h, const Dom& d,
+    // hs: the fp16 h buffer of each block (distinct when the blocks run concurrently).
+    void resblock_mean(const MSnake* rbs, const float* y, float* X[3], float* const hs[3], const Dom& d,
                        const Tiles* yt = nullptr, int yparts = 1, bool y_refl = false) {
         const int c = rbs[0].c, wn = kShapeWN[rbs[0].c1[0].shape];
         // the three blocks' first AdaIN share one set of statistics of y
@@ -940,20 +943,47 @@ struct Runner {
             const Tiles& ts = stats(y, c, c, d);
             for (int j = 0; j < 3; j++) fin(ts, 1, c, rbs[j].a1[0], cf(2 + j));
         }
+        // The three blocks are independent until the mean: blocks 0 and 1 run on the context's
+        // side streams and block 2 on the main stream, each with its own h, statistics region and
+        // AdaIN coefficients, and the mean (block 2's last conv) waits for the other two.  One
+        // chain's kernels fill the CUs that another's tail leaves idle.  The kernels and their
+        // arithmetic are those of the serial order (kept for per-launch profiling).
+        const bool conc = !ctx->profiling && !dry;
+        hipStream_t main_s = s;
+        if (conc) {
+            for (auto& e : p->chain_ev)
+                if (!e) KK_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+            KK_HIP(hipEventRecord(p->chain_ev[2], main_s));
+            for (int q = 0; q < 2; q++) KK_HIP(hipStreamWaitEvent(ctx->side[q], p->chain_ev[2], 0));
+        }
         for (int j = 0; j < 3; j++) {
             const MSnake& blk = rbs[j];
+            const bool side = conc && j < 2;
+            s = side ? ctx->side[j] : main_s;
+            region = conc ? j : 0;
+            Coef* ca = side ? cf(5 + 2 * j) : cf(0);  // the steps' AdaIN pair
+            Coef* cb = side ? cf(6 + 2 * j) : cf(1);
+            float* h = conc ? hs[j] : hs[0];
             for (int i = 0; i < 3; i++) {
                 const float* in = i == 0 ? y : X[j];
                 const Tiles& t =
-                    conv(blk.c1[i], snake_op(blk, d, in, h, EPI_STORE, i == 0 ? cf(2 + j) : cf(0), i, false, true));
-                fin(t, wn, c, blk.a2[i], cf(1));
-                Op o2 = snake_op(blk, d, h, X[j], EPI_ACCUM, cf(1), i, true, i < 2);
+                    conv(blk.c1[i], snake_op(blk, d, in, h, EPI_STORE, i == 0 ? cf(2 + j) : ca, i, false, true));
+                fin(t, wn, c, blk.a2[i], cb);
+                Op o2 = snake_op(blk, d, h, X[j], EPI_ACCUM, cb, i, true, i < 2);
                 if (i == 0) o2.epi = EPI_ADD_FROM, o2.r0 = y, o2.r0_ld = c;
-                if (j == 2 && i == 2) o2.epi = EPI_MEAN3, o2.r0 = X[0], o2.r1 = X[1], o2.r2 = X[2], o2.r0_ld = c;
+                if (j == 2 && i == 2) {
+                    o2.epi = EPI_MEAN3, o2.r0 = X[0], o2.r1 = X[1], o2.r2 = X[2], o2.r0_ld = c;
+                    if (conc)
+                        for (int q = 0; q < 2; q++) {
+                            KK_HIP(hipEventRecord(p->chain_ev[q], ctx->side[q]));
+                            KK_HIP(hipStreamWaitEvent(main_s, p->chain_ev[q], 0));
+                        }
+                }
                 conv(blk.c2[i], o2);
-                if (i < 2) fin(t, wn, c, blk.a1[i + 1], cf(0));
+                if (i < 2) fin(t, wn, c, blk.a1[i + 1], ca);
             }
         }
+        s = main_s, region = 0;
     }
 
     // AdainResBlk1d (src/gpu_batch.rs:104-135) without upsampling: in [ln][in_ld] -> out[:, 0:dout].
@@ -1049,7 +1079,7 @@ struct Runner {
         need_part(tn.count * c);
         KK_LAUNCH(launch_noise_conv(p->spec.as<float>(), kSpecLd, p->d120.l, p->d120.col_d.as<int32_t>(),
                                  nc.w.as<float>(), nc.wp.p ? nc.wp.as<float>() : nullptr, nc.b.as<float>(), nc.cout,
-                                 nc.k, nc.stride, nc.pad, B[1], c, tn.dev(), p->part.as<StatPart>(), s));
+                                 nc.k, nc.stride, nc.pad, B[1], c, tn.dev(), part(), s));
         launches++;
         snake_block(m.noise_res[i], B[1], B[2], dout, &tn);
         // y = ups[i](leaky_0.1(x) masked) (+ per-item reflect pad on stage 1) + xs
@@ -1061,7 +1091,10 @@ struct Runner {
         ou.stats = true;  // partials of y per (tile, phase, wave column) for the resblocks' first AdaIN
         const Tiles& tu = conv(m.ups[i], ou);
         float* X[3] = {B[4], B[5], B[0]};
-        resblock_mean(&m.rb[3 * i], B[3], X, B[2], dout, &tu, kShapeWN[m.ups[i].shape] * ou.stride, i == 1);
+        // h of the three blocks: the two halves of B[2] (an fp16 [rows][c] fits in half of a buffer
+        // sized for f32 [rows][128] at d120 and [rows][256] at d20) and B[1] (xs, consumed above)
+        float* const hs[3] = {B[2], B[2] + p->B[2].bytes / 2 / sizeof(float), B[1]};
+        resblock_mean(&m.rb[3 * i], B[3], X, hs, dout, &tu, kShapeWN[m.ups[i].shape] * ou.stride, i == 1);
     }
 
     void post_istft() {
@@ -1112,7 +1145,6 @@ static void prebuild_tiles(kk_plan* p) {
 }
 
 static void release_plan_device(kk_plan* p) {
-    p->drop_graph();
     p->drop_fetch_event();
     for (DevBuf* b : p->owned()) b->release();
     for (kk::Dom* d : {&p->dn, &p->d2, &p->d20, &p->d120, &p->ds}) {
@@ -1184,6 +1216,7 @@ int kk_open(int ordinal, kk_ctx** out, char* err, size_t errlen) {
         ctx->n_cu = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 1;
         KK_HIP(hipSetDevice(ordinal));
         KK_HIP(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking));
+        for (auto& ss : ctx->side) KK_HIP(hipStreamCreateWithFlags(&ss, hipStreamNonBlocking));
         // twiddles and periodic Hann window in f64 (src/gpu.rs:93-101)
         double cs[220], sn[220];
         float win[20];
@@ -1203,6 +1236,8 @@ void kk_close(kk_ctx* ctx) {
     if (!ctx) return;
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
+    for (auto ss : ctx->side)
+        if (ss) (void)hipStreamSynchronize(ss);
     // plans still alive lose their device memory now and become orphans: kk_plan_free later only
     // releases the host object, and every other entry on them reports KK_ERR_STATE
     for (kk_plan* p : ctx->plans) release_plan_device(p);
@@ -1213,6 +1248,8 @@ void kk_close(kk_ctx* ctx) {
     }
     for (auto e : ctx->event_pool) (void)hipEventDestroy(e);
     ctx->model = Model();
+    for (auto ss : ctx->side)
+        if (ss) (void)hipStreamSynchronize(ss), (void)hipStreamDestroy(ss);
     (void)hipStreamDestroy(ctx->stream);
     delete ctx;
 }
@@ -1271,36 +1308,11 @@ int kk_plan_run(kk_plan* plan, int until, char* err, size_t errlen) {
         check(plan->ctx->model.ready, "no model uploaded");
         hipStream_t s = plan->ctx->stream;
         Runner r{plan, plan->ctx, plan->ctx->model, s};
-        // Per-launch profiling records events between the kernels: those runs stay eager.
-        const bool graphs = !plan->ctx->profiling;
-        if (graphs && plan->graph && plan->graph_until == until) {
-            KK_HIP(hipGraphLaunch(plan->graph, s));  // counters stay those of the captured run
-        } else if (graphs && plan->eager_until == until) {
-            // second run of this stage: capture it (the first, eager run has set every kernel
-            // attribute and surfaced any launch error) and replay the graph from now on
-            plan->drop_graph();
-            hipGraph_t g = nullptr;
-            KK_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
-            try {
-                r.run(until);
-            } catch (...) {
-                (void)hipStreamEndCapture(s, &g);
-                if (g) (void)hipGraphDestroy(g);
-                throw;
-            }
-            KK_HIP(hipStreamEndCapture(s, &g));
-            hipGraphExec_t e = nullptr;
-            const hipError_t ie = hipGraphInstantiate(&e, g, nullptr, nullptr, 0);
-            (void)hipGraphDestroy(g);
-            KK_HIP(ie);
-            plan->graph = e, plan->graph_until = until;
-            KK_HIP(hipGraphLaunch(e, s));
-            plan->conv_flop = r.flop, plan->snake_flop = r.snake_flop, plan->launches = r.launches;
-        } else {
-            r.run(until);
-            plan->eager_until = until;
-            plan->conv_flop = r.flop, plan->snake_flop = r.snake_flop, plan->launches = r.launches;
-        }
+        // Eager launches: the generator's three resblock chains run on three streams at once, which
+        // a captured HIP graph executes one node at a time on this runtime (measured: the graph
+        // replay of the same sequence is 1.7% slower per step).
+        r.run(until);
+        plan->conv_flop = r.flop, plan->snake_flop = r.snake_flop, plan->launches = r.launches;
         plan->last_until = until;
     });
 }
@@ -1576,7 +1588,8 @@ void kk_plan_free(kk_plan* plan) {
     if (plan->ctx) {  // an orphan's device memory went with its context (kk_close)
         (void)hipSetDevice(plan->ctx->device);
         (void)hipStreamSynchronize(plan->ctx->stream);
-        plan->drop_graph();
+        // a run that failed between a fork and its join may leave work on the side streams
+        for (auto ss : plan->ctx->side) (void)hipStreamSynchronize(ss);
         plan->drop_fetch_event();
         plan->ctx->plans.erase(plan);
     }

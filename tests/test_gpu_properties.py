@@ -97,8 +97,7 @@ def _run(ctx, items):
 
 
 def test_rerun_and_one_shot_bit_identical(gpu_ctx):
-    """Run 1 is eager, run 2 captures the launch sequence into a HIP graph, later runs replay it;
-    another plan's eager run and an eager stage run sit between replays."""
+    """Runs of one plan repeat bit for bit, with another plan's run and a stage run between them."""
     from kokoro_hip import api, workloads
     items = workloads.small_items(61, [11, 5, 17])
     with api.Plan.decoder(gpu_ctx, items) as plan:
@@ -112,6 +111,29 @@ def test_rerun_and_one_shot_bit_identical(gpu_ctx):
     c = gpu_ctx.forward_decoder_batch(items)
     for r in runs[1:] + [c]:
         for x, y in zip(runs[0], r):
+            assert np.array_equal(x, y)
+
+
+def test_concurrent_chains_match_serial(gpu_ctx):
+    """The resblock chains on three streams (the default) and in one stream (per-launch profiling
+    runs them serially) give the same bits: stage 0's output and the audio."""
+    from kokoro_hip import api, workloads
+    items = workloads.small_items(65, [14, 3, 22, 8])
+    outs = []
+    for prof in (False, True, False):
+        gpu_ctx.set_profiling(prof)
+        try:
+            with api.Plan.decoder(gpu_ctx, items) as plan:
+                plan.run(until="gen0")  # stage 0's chains
+                taps = [plan.tap("gen0", b, (256, 20 * it.n_frames)) for b, it in enumerate(items)]
+                plan.run()
+                outs.append((taps, plan.fetch()))
+        finally:
+            gpu_ctx.set_profiling(False)
+    for taps, audio in outs[1:]:
+        for x, y in zip(outs[0][0], taps):
+            assert np.array_equal(x, y)
+        for x, y in zip(outs[0][1], audio):
             assert np.array_equal(x, y)
 
 
