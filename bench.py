@@ -7,8 +7,8 @@ iSTFT), with every input already resident in HBM.  `value` = audio seconds synth
 second, timed without per-launch instrumentation.  The roofline block reports the dominant kernel
 (the Snake-block MFMA convolutions): algorithmic FLOP / summed HIP-event time of those launches over
 a second timed pass of the same K steps with an event pair around every conv launch on the
-library's stream, against the bf16
-dense MFMA peak; its `traffic` is the HBM bytes per launch measured by the FETCH_SIZE / WRITE_SIZE
+library's stream (with per-launch profiling on, the library runs the generator's three resblock
+chains in that one stream instead of three), against the bf16 dense MFMA peak; its `traffic` is the HBM bytes per launch measured by the FETCH_SIZE / WRITE_SIZE
 counters (profiles/conv_mfma_snake_config3_traffic.json, made with --calibrate-copy-mib and
 kokoro_hip/profsum.py).  The CPU baseline is the oracle (a CPU restatement of the same path) on a bounded
 sample of the same batch.
@@ -120,7 +120,8 @@ def main():
     ms = (t1 - t0) * 1e3 / args.steps
     value = audio_s / (ms / 1e3)
     # per-kernel durations: the same K steps again, launched one by one with a HIP event pair
-    # around every conv launch on the library's stream
+    # around every conv launch on the library's stream (the resblock chains serial, so that each
+    # kernel has the GPU to itself)
     prof = {}
     if not args.no_events:
         ctx.set_profiling(True)
