@@ -165,8 +165,9 @@ struct kk_ctx {
     int n_cu = 1;
     std::set<kk_plan*> plans;  // live plans: released (and orphaned) by kk_close
     hipStream_t stream = nullptr;
-    // two more streams (default priority) for the generator's independent resblock chains
-    hipStream_t side[2] = {nullptr, nullptr};
+    // three more streams (default priority): the generator's independent resblock chains (0, 1) and
+    // the source + noise branches (2)
+    hipStream_t side[3] = {nullptr, nullptr, nullptr};
     std::string name;
     kk::Model model;
     bool profiling = false;
@@ -443,9 +444,10 @@ struct kk_plan {
     int64_t t_rows = 0;
     // intermediates
     kk::DevBuf gb, xcat, xin_a, xin_b, hdec, pool, sc_half, dec_out, pp, spec, B[6], post, audio, audio_start;
+    kk::DevBuf xs[2], hn;  // the noise branches' outputs (d20 x 256, d120 x 128 f32) and their fp16 h
     // coef[0..1]: the Snake steps' AdaIN pair; [2..4]: the resblocks' first AdaIN; [5..8]: the pair
-    // of resblock chains 0 and 1 (run on the context's side streams)
-    kk::DevBuf part, coef[9];
+    // of resblock chains 0 and 1 (run on the context's side streams); [9..10]: the noise branches'
+    kk::DevBuf part, coef[11];
     int64_t part_bytes = 0;
     std::map<std::tuple<const kk::Dom*, int, int>, std::unique_ptr<kk::Tiles>> tiles;
     // item-aligned tiles of domain d, width w (built on first use, at plan creation)
@@ -474,13 +476,16 @@ struct kk_plan {
         fetch_ev = nullptr, fetch_pending = false;
         for (auto& e : chain_ev)
             if (e) (void)hipEventDestroy(e), e = nullptr;
+        for (auto& e : noise_ev)
+            if (e) (void)hipEventDestroy(e), e = nullptr;
     }
-    // fork / join of the resblock chains (created on first use)
+    // fork / join of the resblock chains, and of the noise branches (created on first use)
     hipEvent_t chain_ev[3] = {nullptr, nullptr, nullptr};
+    hipEvent_t noise_ev[3] = {nullptr, nullptr, nullptr};
     std::vector<kk::DevBuf*> owned() {
         return {&t_en, &src_row, &f0, &en, &style, &seeds, &kinds, &rand_ini, &fixed_noise, &gb, &xcat, &xin_a,
                 &xin_b, &hdec, &pool, &sc_half, &dec_out, &pp, &spec, &B[0], &B[1], &B[2], &B[3], &B[4], &B[5],
-                &post, &audio, &audio_start, &part, &coef[0], &coef[1], &coef[2], &coef[3], &coef[4], &coef[5], &coef[6], &coef[7], &coef[8], &src_item,
+                &post, &audio, &audio_start, &part, &coef[0], &coef[1], &coef[2], &coef[3], &coef[4], &coef[5], &coef[6], &coef[7], &coef[8], &coef[9], &coef[10], &xs[0], &xs[1], &hn, &src_item,
                 &src_f0, &ist_item, &ist_s0, &pcm, &pcm_len, &pcm_clip};
     }
 };
@@ -592,7 +597,10 @@ static void setup_generator(kk_plan* p, const std::vector<const float*>& f0s, co
     for (int i = 0; i < 6; i++) alloc_zero(p, p->B[i], big);
     alloc_zero(p, p->post, (size_t)l120 * kPostLd * sizeof(float));
     alloc_zero(p, p->audio, (size_t)600 * ln * sizeof(float));
-    for (int i = 0; i < 9; i++) p->coef[i].alloc((size_t)nb * kXinLd * sizeof(Coef));
+    for (int i = 0; i < 11; i++) p->coef[i].alloc((size_t)nb * kXinLd * sizeof(Coef));
+    alloc_zero(p, p->xs[0], (size_t)l20 * 256 * sizeof(float));
+    alloc_zero(p, p->xs[1], (size_t)l120 * 128 * sizeof(float));
+    alloc_zero(p, p->hn, (size_t)std::max(l20 * 256, l120 * 128) * sizeof(uint16_t));
     // statistics partials: every partial but the last two of each item covers at least 64 columns
     // of one item (the noise convs' 64-column tiles; the convs' 128-column wave spans)
     auto bound = [&](int64_t l, int64_t c) { return (l / 64 + 2 * (int64_t)nb + 2) * c; };
@@ -600,8 +608,9 @@ static void setup_generator(kk_plan* p, const std::vector<const float*>& f0s, co
     auto bound_t = [&](int64_t l_in, int64_t stride, int64_t c) { return (l_in / 128 + 2 * (int64_t)nb + 1) * stride * c; };
     const int64_t np = std::max({bound(ln, 1152), bound(2 * ln, 512), bound(l20, 256), bound(l120, 128),
                                  bound_t(l2, 10, 256), bound_t(l20, 6, 128)});
-    // three regions, one per concurrent resblock chain; part_bytes is one region
-    p->part.alloc((size_t)3 * np * sizeof(StatPart));
+    // four regions: one per concurrent resblock chain and one for the noise branches; part_bytes
+    // is one region
+    p->part.alloc((size_t)4 * np * sizeof(StatPart));
     p->part_bytes = (int64_t)np * (int64_t)sizeof(StatPart);
 }
 
@@ -913,17 +922,20 @@ struct Runner {
     // snake_b (src/gpu_batch.rs:140-154) in place on X.  The statistics of each conv's output are
     // reduced in its epilogue; the block input's come from the kernel that produced X (`xin`: its
     // tiles, one partial per tile and channel) or, when null, from a statistics pass here.
-    void snake_block(const MSnake& blk, float* X, float* h, const Dom& d, const Tiles* xin = nullptr) {
+    // ca / cb: the coefficient pair of the block's two AdaIN per step (default cf(0), cf(1)).
+    void snake_block(const MSnake& blk, float* X, float* h, const Dom& d, const Tiles* xin = nullptr,
+                     Coef* ca = nullptr, Coef* cb = nullptr) {
         const int c = blk.c, wn = kShapeWN[blk.c1[0].shape];
+        if (!ca) ca = cf(0), cb = cf(1);
         if (xin)
-            fin(*xin, 1, c, blk.a1[0], cf(0));
+            fin(*xin, 1, c, blk.a1[0], ca);
         else
-            stats_fin(X, c, c, d, blk.a1[0], cf(0));
+            stats_fin(X, c, c, d, blk.a1[0], ca);
         for (int i = 0; i < 3; i++) {
-            const Tiles& t = conv(blk.c1[i], snake_op(blk, d, X, h, EPI_STORE, cf(0), i, false, true));
-            fin(t, wn, c, blk.a2[i], cf(1));
-            conv(blk.c2[i], snake_op(blk, d, h, X, EPI_ACCUM, cf(1), i, true, i < 2));
-            if (i < 2) fin(t, wn, c, blk.a1[i + 1], cf(0));
+            const Tiles& t = conv(blk.c1[i], snake_op(blk, d, X, h, EPI_STORE, ca, i, false, true));
+            fin(t, wn, c, blk.a2[i], cb);
+            conv(blk.c2[i], snake_op(blk, d, h, X, EPI_ACCUM, cb, i, true, i < 2));
+            if (i < 2) fin(t, wn, c, blk.a1[i + 1], ca);
         }
     }
 
@@ -1067,32 +1079,43 @@ struct Runner {
         launches += 2;
     }
 
+    // xs_i = noise_res[i](noise_convs[i](masked spec)) (src/gpu_batch.rs:362-375) into p->xs[i],
+    // with its own h, statistics region (3) and coefficient pair, so that it can run beside the
+    // decoder and the previous stage.
+    void noise_branch(int i) {
+        const Dom& dout = i == 0 ? p->d20 : p->d120;
+        const int c = m.ups[i].cout;
+        float* xs = p->xs[i].as<float>();
+        const int reg = region;
+        region = 3;
+        const MNoiseConv& nc = m.nc[i];
+        const Tiles& tn = p->tl(dout, kNoiseTile);
+        need_part(tn.count * c);
+        KK_LAUNCH(launch_noise_conv(p->spec.as<float>(), kSpecLd, p->d120.l, p->d120.col_d.as<int32_t>(),
+                                 nc.w.as<float>(), nc.wp.p ? nc.wp.as<float>() : nullptr, nc.b.as<float>(), nc.cout,
+                                 nc.k, nc.stride, nc.pad, xs, c, tn.dev(), part(), s));
+        launches++;
+        snake_block(m.noise_res[i], xs, p->hn.as<float>(), dout, &tn, cf(9), cf(10));
+        region = reg;
+    }
+
     void gen_stage(int i) {
         const Dom& din = i == 0 ? p->d2 : p->d20;
         const Dom& dout = i == 0 ? p->d20 : p->d120;
         const int c = m.ups[i].cout;
         float* B[6];
         for (int j = 0; j < 6; j++) B[j] = p->B[j].as<float>();
-        // xs = noise_res[i](noise_convs[i](masked spec)) (src/gpu_batch.rs:362-375)
-        const MNoiseConv& nc = m.nc[i];
-        const Tiles& tn = p->tl(dout, kNoiseTile);
-        need_part(tn.count * c);
-        KK_LAUNCH(launch_noise_conv(p->spec.as<float>(), kSpecLd, p->d120.l, p->d120.col_d.as<int32_t>(),
-                                 nc.w.as<float>(), nc.wp.p ? nc.wp.as<float>() : nullptr, nc.b.as<float>(), nc.cout,
-                                 nc.k, nc.stride, nc.pad, B[1], c, tn.dev(), part(), s));
-        launches++;
-        snake_block(m.noise_res[i], B[1], B[2], dout, &tn);
-        // y = ups[i](leaky_0.1(x) masked) (+ per-item reflect pad on stage 1) + xs
+        // y = ups[i](leaky_0.1(x) masked) (+ per-item reflect pad on stage 1) + xs (noise branch i)
         Op ou;
         ou.pro = PRO_LEAKY, ou.epi = i == 0 ? EPI_CONVT : EPI_CONVT_REFLECT, ou.slope = 0.1f;
         ou.x = i == 0 ? (const void*)p->dec_out.p : (const void*)B[0], ou.x_ld = i == 0 ? 512 : 256;
-        ou.din = &din, ou.dout = &dout, ou.y = B[3], ou.y_ld = c, ou.r0 = B[1], ou.r0_ld = c;
+        ou.din = &din, ou.dout = &dout, ou.y = B[3], ou.y_ld = c, ou.r0 = p->xs[i].as<float>(), ou.r0_ld = c;
         ou.convt = true, ou.stride = m.ups_stride[i], ou.pad_t = m.ups_pad[i], ou.cls = PC_CONVT;
         ou.stats = true;  // partials of y per (tile, phase, wave column) for the resblocks' first AdaIN
         const Tiles& tu = conv(m.ups[i], ou);
         float* X[3] = {B[4], B[5], B[0]};
         // h of the three blocks: the two halves of B[2] (an fp16 [rows][c] fits in half of a buffer
-        // sized for f32 [rows][128] at d120 and [rows][256] at d20) and B[1] (xs, consumed above)
+        // sized for f32 [rows][128] at d120 and [rows][256] at d20) and B[1]
         float* const hs[3] = {B[2], B[2] + p->B[2].bytes / 2 / sizeof(float), B[1]};
         resblock_mean(&m.rb[3 * i], B[3], X, hs, dout, &tu, kShapeWN[m.ups[i].shape] * ou.stride, i == 1);
     }
@@ -1123,12 +1146,40 @@ struct Runner {
             snake_block(*p->sblk, p->B[0].as<float>(), p->B[1].as<float>(), p->ds);
             return;
         }
+        // The harmonic source and both stages' noise branches depend only on the inputs and the style:
+        // they run on a third side stream beside the decoder and stage 0 (per-launch profiling and
+        // runs that stop at the source keep them in order on the main stream).
+        const bool conc = !ctx->profiling && !dry && until > KK_STAGE_SOURCE;
+        hipStream_t main_s = s;
+        if (conc) {
+            for (auto& e : p->noise_ev)
+                if (!e) KK_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+            KK_HIP(hipEventRecord(p->noise_ev[0], main_s));  // after style_fc
+            KK_HIP(hipStreamWaitEvent(ctx->side[2], p->noise_ev[0], 0));
+            s = ctx->side[2];
+            source();
+            noise_branch(0);
+            KK_HIP(hipEventRecord(p->noise_ev[1], s));
+            if (until > KK_STAGE_GEN0) {
+                noise_branch(1);
+                KK_HIP(hipEventRecord(p->noise_ev[2], s));
+            }
+            s = main_s;
+        }
         if (p->kind == PLAN_DECODER) decoder();
         if (until <= KK_STAGE_DECODER) return;
-        source();
+        if (!conc) source();
         if (until <= KK_STAGE_SOURCE) return;
+        if (conc)
+            KK_HIP(hipStreamWaitEvent(main_s, p->noise_ev[1], 0));
+        else
+            noise_branch(0);
         gen_stage(0);
         if (until <= KK_STAGE_GEN0) return;
+        if (conc)
+            KK_HIP(hipStreamWaitEvent(main_s, p->noise_ev[2], 0));
+        else
+            noise_branch(1);
         gen_stage(1);
         if (until <= KK_STAGE_GEN1) return;
         post_istft();
