@@ -968,7 +968,12 @@ struct Runner {
             KK_HIP(hipEventRecord(p->chain_ev[2], main_s));
             for (int q = 0; q < 2; q++) KK_HIP(hipStreamWaitEvent(ctx->side[q], p->chain_ev[2], 0));
         }
-        for (int j = 0; j < 3; j++) {
+        // Concurrent: the longest chain (block 2, k = 11) is enqueued first and its last conv (the
+        // mean) after the other two chains and the join.
+        Op mean_op;
+        bool mean_pending = false;
+        for (int jj = 0; jj < 3; jj++) {
+            const int j = conc ? 2 - jj : jj;
             const MSnake& blk = rbs[j];
             const bool side = conc && j < 2;
             s = side ? ctx->side[j] : main_s;
@@ -985,15 +990,22 @@ struct Runner {
                 if (i == 0) o2.epi = EPI_ADD_FROM, o2.r0 = y, o2.r0_ld = c;
                 if (j == 2 && i == 2) {
                     o2.epi = EPI_MEAN3, o2.r0 = X[0], o2.r1 = X[1], o2.r2 = X[2], o2.r0_ld = c;
-                    if (conc)
-                        for (int q = 0; q < 2; q++) {
-                            KK_HIP(hipEventRecord(p->chain_ev[q], ctx->side[q]));
-                            KK_HIP(hipStreamWaitEvent(main_s, p->chain_ev[q], 0));
-                        }
+                    if (conc) {
+                        mean_op = o2, mean_pending = true;
+                        continue;
+                    }
                 }
                 conv(blk.c2[i], o2);
                 if (i < 2) fin(t, wn, c, blk.a1[i + 1], ca);
             }
+        }
+        if (mean_pending) {
+            s = main_s;
+            for (int q = 0; q < 2; q++) {
+                KK_HIP(hipEventRecord(p->chain_ev[q], ctx->side[q]));
+                KK_HIP(hipStreamWaitEvent(main_s, p->chain_ev[q], 0));
+            }
+            conv(rbs[2].c2[2], mean_op);
         }
         s = main_s, region = 0;
     }
