@@ -99,8 +99,11 @@ void kk_output_free(kk_output* out, int n);
 /* ------------------------------------------------------------------ plans (device-resident runs)
  * kk_forward_decoder_batch = kk_plan_create + kk_plan_run + kk_plan_fetch + kk_plan_free.
  * A plan builds the layout, uploads the inputs and allocates every device buffer once; kk_plan_run
- * only enqueues kernels on the context's stream (no allocation, no host synchronization), so it
- * can be timed with inputs already resident in HBM and run repeatedly. */
+ * only enqueues kernels (no allocation, no host synchronization), so it can be timed with inputs
+ * already resident in HBM and run repeatedly.  It enqueues on the context's stream and on three
+ * side streams of the context (the generator's independent resblock chains, the harmonic source
+ * and noise branches), forked from and joined back into the context's stream within the run:
+ * work enqueued on the context's stream after kk_plan_run sees all of it. */
 int kk_plan_create(kk_ctx* ctx, const kk_decoder_item* items, int n, kk_plan** out, char* err, size_t errlen);
 /* Generator-only plan: per item the decoder output x [512][2N] channel-major,
  * F0 [2N], ref_s [256], noise. */
@@ -185,8 +188,8 @@ int kk_encode_pcm16(kk_ctx* ctx, const float* audio, int64_t n, int16_t* out, in
 int kk_wav_header(int format, uint32_t sample_rate, uint64_t data_bytes, uint8_t* out, char* err, size_t errlen);
 
 /* ------------------------------------------------------------------ measurement
- * With profiling on, kk_plan_run brackets every MFMA conv launch with HIP events on the
- * context's stream; kk_profile_read reports, per kernel class, the summed event time and the
+ * With profiling on, kk_plan_run runs every kernel on the context's stream (no side streams) and
+ * brackets every MFMA conv launch with HIP events there; kk_profile_read reports, per kernel class, the summed event time and the
  * algorithmic FLOP of those launches (classes: "snake_conv", "decoder_conv", "convt", "post_conv"). */
 int kk_set_profiling(kk_ctx* ctx, int on);
 typedef struct {
