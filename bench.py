@@ -1,23 +1,33 @@
 """Benchmark: batched ragged Kokoro-82M decoder + iSTFTNet generator on one MI355X.
 
 Workload (the metric's config): 32 ragged items, N ~ U[100, 800] decoder
-frames each, seeded synthetic inputs and random-init weights.  One step = one pass of the hot path
-over the batch (kk_plan_run: duration expansion -> decoder -> harmonic source + STFT -> generator ->
-iSTFT), with every input already resident in HBM.  `value` = audio seconds synthesized per wall
-second, timed without per-launch instrumentation.  The roofline block reports the dominant kernel
-(the Snake-block MFMA convolutions): algorithmic FLOP / summed HIP-event time of those launches over
-a second timed pass of the same K steps with an event pair around every conv launch on the
-library's stream (with per-launch profiling on, the library runs the generator's three resblock
-chains in that one stream instead of three), against the bf16 dense MFMA peak; its `traffic` is the HBM bytes per launch measured by the FETCH_SIZE / WRITE_SIZE
-counters (profiles/conv_mfma_snake_config3_traffic.json, made with --calibrate-copy-mib and
-kokoro_hip/profsum.py).  The CPU baseline is the oracle (a CPU restatement of the same path) on a bounded
-sample of the same batch.
+frames each, seeded synthetic inputs and random-init weights of the real architecture.
+
+- `value` (the protocol of BASELINE.md section 5): one step = one C-ABI call of
+  kk_forward_decoder_batch, from host inputs to host audio (layout, upload, duration expansion ->
+  decoder -> harmonic source + STFT -> generator -> iSTFT -> audio copied back).  W warm calls, then
+  K timed calls, each timed on its own; `value` = audio seconds / the median call.
+- `kernel_only`: the same batch as a plan whose inputs are resident in HBM, K runs of kk_plan_run
+  timed together (device time per step, no host transfers).
+- `roofline`: the dominant kernel, the Snake-block MFMA convolutions.  A profiling pass of the same
+  K steps runs every kernel alone on the library's stream with a HIP event pair around each launch;
+  achieved = algorithmic FLOP per launch / average launch time, against the bf16 dense MFMA peak.
+  `traffic` is the HBM bytes per launch from the FETCH_SIZE / WRITE_SIZE counters
+  (profiles/conv_mfma_snake_config3_traffic.json, made with --calibrate-copy-mib and
+  kokoro_hip/profsum.py).
+- `hbm`: every bandwidth kernel of the same pass: algorithmic bytes (valid rows read and written
+  once) per launch / its time, against 8 TB/s.
+- `parity`: item 0 of the timed calls' audio against the fp32 CPU oracle.
+- `cpu_baseline`: the oracle (a C restatement of the same path, OpenMP) on a bounded sample of the
+  same batch, and on config 1; beside it the torch-CPU functional restatement (oracle/torch_ref.py,
+  float32) on the same sample.  A reported baseline, not the target.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--config 3|5]
 """
 import argparse
 import json
 import os
+import statistics
 import sys
 import time
 
@@ -27,14 +37,32 @@ sys.path.insert(0, ROOT)
 
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0
+BANDWIDTH_KERNELS = ["stats_tiles", "finalize", "style_fc", "expand", "f0n_conv", "copy_cols", "adain_pool",
+                     "noise_conv0", "noise_conv1", "phase_pre", "source_stft", "istft"]
 
 
-def cpu_baseline(weights, items, budget_s=12.0):
-    """Oracle (fp32 C restatement of the path) on the first items of the batch, OpenMP threads =
-    the host cores available to this process (at most 16), until `budget_s` of CPU wall time."""
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(weights, items, budget_s=12.0, torch_budget_s=8.0):
+    """The oracle (fp32 C restatement of the path) on the first items of the batch until `budget_s` of
+    wall time, with OpenMP threads = the box's CPU share (OMP_NUM_THREADS, else nproc); config 1 with
+    the same threads; and the torch-CPU float32 functional restatement on the first items until
+    `torch_budget_s`."""
+    import numpy as np
+    from kokoro_hip import workloads
     from oracle import oracle as O
-    cores = min(16, len(os.sched_getaffinity(0)))
-    O.set_threads(cores)
+    nproc = len(os.sched_getaffinity(0))
+    threads = int(os.environ.get("OMP_NUM_THREADS") or nproc)
+    O.set_threads(threads)
     m = O.Model(weights)
     done_s, done_audio, n_items = 0.0, 0.0, 0
     for it in items:
@@ -45,9 +73,44 @@ def cpu_baseline(weights, items, budget_s=12.0):
         n_items += 1
         if done_s >= budget_s:
             break
-    return {"value": round(done_audio / done_s, 4), "unit": "audio-s/s", "cores": cores, "kind": "port",
-            "sample": f"oracle (oracle/kk_oracle.c, fp32, OpenMP {cores} threads) on the first {n_items} items "
-                      f"of the same batch: {done_audio:.1f} audio-s in {done_s:.1f} s"}
+    res = {"value": round(done_audio / done_s, 4), "unit": "audio-s/s", "cores": threads, "kind": "port",
+           "sample": f"oracle (oracle/kk_oracle.c, fp32, OpenMP {threads} threads) on the first {n_items} items "
+                     f"of the same batch: {done_audio:.1f} audio-s in {done_s:.1f} s",
+           "nproc": nproc, "cpu_model": _cpu_model()}
+    # config 1: generator only, one item of 100 decoder frames (2.5 s of audio), median of 3
+    x, f0, style, seed = workloads.config1_generator_input()
+    ri, nz = O.rand_ini(seed), O.gen_noise(seed, 600 * (x.shape[1] // 2) * 9)
+    ts = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        m.generator(x, f0, style, ri, nz)
+        ts.append(time.perf_counter() - t0)
+    c1_audio = 600 * (x.shape[1] // 2) / 24000.0
+    res["config1"] = {"value": round(c1_audio / statistics.median(ts), 4), "unit": "audio-s/s",
+                      "sample": f"oracle, config 1 generator ({c1_audio:.1f} audio-s), median of 3"}
+    # torch-CPU functional leg (float32, torch.set_num_threads = the same threads)
+    import torch
+    from oracle import torch_ref as R
+    R.set_dtype(torch.float32)
+    torch.set_num_threads(threads)
+    done_s, done_audio, n_items = 0.0, 0.0, 0
+    with torch.no_grad():
+        for it in items:
+            t0 = time.perf_counter()
+            asr = O.expand_tokens(it.t_en, it.dur)
+            xd = R.decoder(weights, asr, it.f0, it.energy, it.ref_s)
+            ri, nz = O.item_noise(it)
+            R.generator(weights, xd, it.f0, it.ref_s, ri, nz)
+            done_s += time.perf_counter() - t0
+            done_audio += it.n_samples / 24000.0
+            n_items += 1
+            if done_s >= torch_budget_s:
+                break
+    res["torch_cpu"] = {"value": round(done_audio / done_s, 4), "unit": "audio-s/s", "threads": threads,
+                        "sample": f"oracle/torch_ref.py in float32 on the first {n_items} items: "
+                                  f"{done_audio:.1f} audio-s in {done_s:.1f} s"}
+    R.set_dtype(torch.float64)
+    return res, m
 
 
 def _traffic(config):
@@ -63,12 +126,11 @@ def _traffic(config):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=10)
-    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--no-pcie", action="store_true", help="skip the host-buffer (PCIe-inclusive) rate")
-    ap.add_argument("--no-events", action="store_true", help="time without the per-launch HIP events")
+    ap.add_argument("--no-events", action="store_true", help="skip the per-launch profiling pass")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="first run one plain copy kernel over this many MiB (reference for PMC byte counters)")
     args = ap.parse_args()
@@ -102,12 +164,35 @@ def main():
         wl = "config3: decoder+generator, batch 32 ragged, N ~ U[100, 800] frames"
     ctx = api.Context(0)
     ctx.upload_model(weights)
+    samples = sum(it.n_samples for it in items)
+    audio_s = samples / 24000.0
+
+    # ---- the headline: host inputs in, host audio out, one C-ABI call per step
+    pb = ctx.prepare(items)
+    for _ in range(args.warmup):
+        ctx.forward_prepared(pb)
+        pb.release()
+    times = []
+    t_region0 = time.perf_counter()
+    for k in range(args.steps):
+        t0 = time.perf_counter()
+        ctx.forward_prepared(pb)
+        times.append(time.perf_counter() - t0)
+        if k + 1 < args.steps:
+            pb.release()
+    t_region = time.perf_counter() - t_region0
+    audio0 = pb.audio(0)
+    finite = all(np.isfinite(pb.audio(b)).all() for b in range(len(items)))
+    pb.release()
+    assert finite, "non-finite audio"
+    ms = statistics.median(times) * 1e3
+    value = audio_s / (ms / 1e3)
+
+    # ---- device-resident steps (kernel_only) and the per-launch profiling pass
     plan = api.Plan.decoder(ctx, items)
     info = plan.info()
-    audio_s = info["samples"] / 24000.0
     print(f"# device {ctx.device_name()}  items {len(items)}  frames {info['frames']}  audio {audio_s:.1f} s  "
-          f"plan {info['device_bytes'] / 2**30:.2f} GiB", file=sys.stderr, flush=True)
-
+          f"plan {info['device_bytes'] / 2**30:.2f} GiB  one-shot median {ms:.2f} ms", file=sys.stderr, flush=True)
     for _ in range(args.warmup):
         plan.run()
     plan.sync()
@@ -115,13 +200,8 @@ def main():
     for _ in range(args.steps):
         plan.run()
     plan.sync()
-    t1 = time.perf_counter()
+    k_ms = (time.perf_counter() - t0) * 1e3 / args.steps
     info = plan.info()
-    ms = (t1 - t0) * 1e3 / args.steps
-    value = audio_s / (ms / 1e3)
-    # per-kernel durations: the same K steps again, launched one by one with a HIP event pair
-    # around every conv launch on the library's stream (the resblock chains serial, so that each
-    # kernel has the GPU to itself)
     prof = {}
     if not args.no_events:
         ctx.set_profiling(True)
@@ -131,14 +211,9 @@ def main():
         plan.sync()
         prof = ctx.profile_read()
         ctx.set_profiling(False)
+    plan.free()
 
-    # parity spot check of the measured batch's first item is done by the test suite; here only a
-    # sanity check that the output is finite
-    out = plan.fetch()
-    assert all(np.isfinite(a).all() for a in out[:2])
-
-    roof = None
-    util = None
+    roof, util, hbm = None, None, None
     if prof:
         sn = prof["snake_conv"]
         achieved = sn["flop"] / (sn["ms"] / 1e3) / 1e12
@@ -146,21 +221,29 @@ def main():
                 "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": _traffic(args.config),
                 "kernel": "conv_mfma_kernel<PRO_ADAIN_SNAKE> (48 Snake-block convs per step)",
                 "avg_launch_ms": round(sn["ms"] / max(sn["launches"], 1), 4),
-                "flop_per_launch": sn["flop"] / max(sn["launches"], 1)}
-        if args.config == 3:
-            # the same launches against HBM: algorithmic bytes (activations in and out) per launch
-            from kokoro_hip import profsum
-            layers, _ = profsum.snake_layers()
-            alg = sum(l["bytes"] for l in layers) / len(layers)
-            gbs = alg / (roof["avg_launch_ms"] / 1e3) / 1e9
-            roof.update({"hbm_bytes_per_launch": alg, "hbm_achieved_gbs": round(gbs, 1),
-                         "hbm_frac": round(gbs / PEAK_HBM_GBS, 4)})
-        conv_ms = sum(v["ms"] for v in prof.values())
-        conv_flop = sum(v["flop"] for v in prof.values())
-        util = {k: {"launches": v["launches"], "ms_per_step": round(v["ms"] / args.steps, 3),
-                    "tflops": round(v["flop"] / max(v["ms"], 1e-9) / 1e9, 1)} for k, v in prof.items()}
+                "flop_per_launch": sn["flop"] / max(sn["launches"], 1),
+                "hbm_bytes_per_launch": sn["bytes"] / max(sn["launches"], 1)}
+        gbs = sn["bytes"] / (sn["ms"] / 1e3) / 1e9
+        roof.update({"hbm_achieved_gbs": round(gbs, 1), "hbm_frac": round(gbs / PEAK_HBM_GBS, 4)})
+        convs = {k: v for k, v in prof.items() if k in ("snake_conv", "decoder_conv", "convt", "post_conv")}
+        conv_ms = sum(v["ms"] for v in convs.values())
+        conv_flop = sum(v["flop"] for v in convs.values())
+        util = {k: {"launches_per_step": v["launches"] // args.steps, "ms_per_step": round(v["ms"] / args.steps, 3),
+                    "tflops": round(v["flop"] / max(v["ms"], 1e-9) / 1e9, 1),
+                    "gbs": round(v["bytes"] / max(v["ms"], 1e-9) / 1e6, 1)} for k, v in convs.items()}
         util["all_convs_mfma_util_pct"] = round(100 * conv_flop / (conv_ms / 1e3) / 1e12 / PEAK_BF16_TFLOPS, 2)
-        util["conv_share_of_step_pct"] = round(100 * conv_ms / args.steps / ms, 1)
+        all_ms = sum(v["ms"] for v in prof.values())
+        util["conv_share_of_kernel_time_pct"] = round(100 * conv_ms / all_ms, 1)
+        hbm = {}
+        for k in BANDWIDTH_KERNELS:
+            if k not in prof:
+                continue
+            v = prof[k]
+            g = v["bytes"] / max(v["ms"], 1e-9) / 1e6
+            hbm[k] = {"launches_per_step": v["launches"] // args.steps, "ms_per_step": round(v["ms"] / args.steps, 4),
+                      "bytes_per_launch": round(v["bytes"] / max(v["launches"], 1)), "gbs": round(g, 1),
+                      "frac": round(g / PEAK_HBM_GBS, 4)}
+        hbm["serial_kernel_ms_per_step"] = round(all_ms / args.steps, 3)
 
     res = {
         "metric": "audio-sec synthesized per wall-sec at batch 32 ragged; conv MFMA util %",
@@ -177,24 +260,26 @@ def main():
         "data": "synthetic (seeded inputs, random-init weights)",
         "config": {"workload": wl, "items": len(items), "frames": info["frames"], "samples": info["samples"],
                    "audio_s": round(audio_s, 2), "conv_tflop_per_step": round(info["conv_flop"] / 1e12, 3),
-                   "launches_per_step": info["launches"]},
+                   "launches_per_step": info["launches"],
+                   "step": "kk_forward_decoder_batch, host inputs -> host audio (median of K calls)",
+                   "timed_region_s": round(t_region, 3)},
+        "kernel_only": {"value": round(audio_s / (k_ms / 1e3), 2), "unit": "audio-s/s", "ms_per_step": round(k_ms, 3),
+                        "step": "kk_plan_run with inputs resident in HBM (mean of K)"},
         "roofline": roof,
         "conv_mfma": util,
+        "hbm": hbm,
     }
-    plan.free()
-    if not args.no_pcie:
-        # the one-shot entry with host buffers (upload, plan build, run, audio back): reported
-        # beside the device-resident rate, never as `value`
-        ctx.forward_decoder_batch(items)
-        t0 = time.perf_counter()
-        reps = 3
-        for _ in range(reps):
-            ctx.forward_decoder_batch(items)
-        dt = (time.perf_counter() - t0) / reps
-        res["pcie_inclusive"] = {"value": round(audio_s / dt, 2), "unit": "audio-s/s", "ms_per_call": round(dt * 1e3, 2),
-                                 "entry": "kk_forward_decoder_batch (host inputs in, host audio out)"}
-    if not args.no_cpu:
-        res["cpu_baseline"] = cpu_baseline(weights, items)
+    # parity of the measured batch: item 0 of the timed calls against the fp32 oracle
+    from oracle import oracle as O
+    if args.no_cpu:
+        model = O.Model(weights)
+    else:
+        res["cpu_baseline"], model = cpu_baseline(weights, items)
+    ref = O.synth_item(model, items[0])
+    err = (audio0.astype(np.float64) - ref) ** 2
+    res["parity"] = {"item": 0, "n_frames": items[0].n_frames, "maxabs": float(np.abs(audio0 - ref).max()),
+                     "snr_db": round(float(10 * np.log10((ref.astype(np.float64) ** 2).sum() / max(err.sum(), 1e-300))), 2),
+                     "vs": "oracle/kk_oracle.c fp32"}
     ctx.close()
     print(json.dumps(res), flush=True)
 

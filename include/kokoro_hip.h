@@ -82,8 +82,10 @@ typedef struct {
     int64_t sine_len;
 } kk_decoder_item;
 
-/* Output (src/model.rs:101-104): the item's audio, 600 N samples at 24 kHz, malloc'ed by the
- * library and released by kk_output_free. */
+/* Output (src/model.rs:101-104): the item's audio, 600 N samples at 24 kHz, owned by the caller
+ * until released by kk_output_free.  The audio of one call lands with a single DMA copy in a block
+ * of pinned host memory that the library keeps for reuse; each item's pointer lies in that block,
+ * which is free again once kk_output_free has released all of its items. */
 typedef struct {
     float* audio;
     int64_t n_samples;
@@ -91,16 +93,27 @@ typedef struct {
 
 /* The decoder + generator part of GpuKokoro::forward_batch (src/gpu_batch.rs:250-420): ragged
  * layout, duration expansion, decoder, harmonic source + STFT, generator, iSTFT, per-item audio in
- * input order.  `out` is a caller array of n entries. */
+ * input order.  `out` is a caller array of n entries.  The context keeps this entry's device
+ * buffers between calls and reuses them for the next batch that fits (growing them when it does
+ * not); every table and input of a call reaches the device in one copy.  Any failure releases the
+ * kept buffers, so that a caller who splits the batch on KK_ERR_OOM (src/engine.rs:229-234) has the
+ * whole device for the halves.
+ * Test hooks, read from the environment at each call and plan creation:
+ *   KOKORO_BATCH_NEGCTL_NOMASK (set: convolutions read neighbours and gaps as an item's own rows;
+ *   the reference's negative control, src/gpu_batch.rs:62-66), KOKORO_HIP_TEST_OOM_ABOVE=k (a batch
+ *   of more than k items fails with KK_ERR_OOM before allocating), KOKORO_HIP_TEST_POISON=1 (device
+ *   buffers are filled with NaN bytes instead of being reused as they are). */
 int kk_forward_decoder_batch(kk_ctx* ctx, const kk_decoder_item* items, int n, kk_output* out, char* err,
                              size_t errlen);
 void kk_output_free(kk_output* out, int n);
 
 /* ------------------------------------------------------------------ plans (device-resident runs)
  * kk_forward_decoder_batch = kk_plan_create + kk_plan_run + kk_plan_fetch + kk_plan_free.
- * A plan builds the layout, uploads the inputs and allocates every device buffer once; kk_plan_run
- * only enqueues kernels (no allocation, no host synchronization), so it can be timed with inputs
- * already resident in HBM and run repeatedly.  It enqueues on the context's stream and on three
+ * A plan builds the layout, uploads the inputs (one copy of all tables) and allocates every device
+ * buffer once, and validates every launch's parameters (KK_ERR_INVALID at creation, never half-way
+ * through a run); kk_plan_run only enqueues kernels (no allocation, no host synchronization), so it
+ * can be timed with inputs already resident in HBM and run repeatedly.  A run that fails after
+ * forking joins the side streams back into the context's stream before it returns.  It enqueues on the context's stream and on three
  * side streams of the context (the generator's independent resblock chains, the harmonic source
  * and noise branches), forked from and joined back into the context's stream within the run:
  * work enqueued on the context's stream after kk_plan_run sees all of it. */
@@ -188,15 +201,20 @@ int kk_encode_pcm16(kk_ctx* ctx, const float* audio, int64_t n, int16_t* out, in
 int kk_wav_header(int format, uint32_t sample_rate, uint64_t data_bytes, uint8_t* out, char* err, size_t errlen);
 
 /* ------------------------------------------------------------------ measurement
- * With profiling on, kk_plan_run runs every kernel on the context's stream (no side streams) and
- * brackets every MFMA conv launch with HIP events there; kk_profile_read reports, per kernel class, the summed event time and the
- * algorithmic FLOP of those launches (classes: "snake_conv", "decoder_conv", "convt", "post_conv"). */
+ * With profiling on, kk_plan_run runs every kernel on the context's stream (no side streams, so
+ * each kernel has the GPU to itself) and brackets every launch with HIP events there;
+ * kk_profile_read reports, per kernel class with at least one launch since the last read, the summed
+ * event time and the algorithmic FLOP and bytes of those launches (valid rows only; bytes = the
+ * data the step must read and write once).  Classes: the MFMA convolutions "snake_conv",
+ * "decoder_conv", "convt", "post_conv"; "stats_tiles", "finalize", "style_fc", "expand", "f0n_conv",
+ * "copy_cols", "adain_pool", "noise_conv0", "noise_conv1", "phase_pre", "source_stft", "istft". */
 int kk_set_profiling(kk_ctx* ctx, int on);
 typedef struct {
     char name[32];
     int64_t launches;
     double ms;
     double flop;
+    double bytes;
 } kk_profile_entry;
 int kk_profile_read(kk_ctx* ctx, kk_profile_entry* out, int max, int* n_out, char* err, size_t errlen);
 

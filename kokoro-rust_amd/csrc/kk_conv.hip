@@ -36,6 +36,7 @@
 #include "kk_kernels.h"
 
 #include <algorithm>
+#include <atomic>
 
 namespace kk {
 
@@ -69,6 +70,15 @@ template <typename T>
 __device__ __forceinline__ T ld_const(const T* p, int64_t i) {
     return ((const __attribute__((address_space(4))) T*)p)[i];
 }
+
+// Per-device flags (device ordinals below 64), safe to set from several host threads.
+struct DeviceFlags {
+    std::atomic<uint64_t> bits{0};
+    bool test(int dev) const { return dev >= 0 && dev < 64 && ((bits.load() >> dev) & 1u); }
+    void set(int dev) {
+        if (dev >= 0 && dev < 64) bits.fetch_or(1ull << dev);
+    }
+};
 
 // One (tile, M-block) unit of work.  Rows fit in 32 bits (checked on the host).
 struct Unit {
@@ -727,7 +737,7 @@ __global__ __launch_bounds__(64 * WM * WN + kNP) void conv_mfma_kernel(ConvParam
 }
 
 template <int PRO, int EPI, int WM, int WN, bool STATS, bool IN_H, bool OUT_H>
-hipError_t launch_t(const ConvParams& p, int n_cu, hipStream_t s) {
+hipError_t launch_t(const ConvParams& p, int n_cu, hipStream_t s, bool validate_only) {
     constexpr int BM = 64 * WM, BN = 16 * kNJ * WN, NT = 64 * WM * WN + kNP;
     const int halo = (p.k - 1) * p.dil;
     constexpr size_t scr_bytes = (size_t)WM * WN * 32 * kScrLd * sizeof(float) + kMaxBias * sizeof(float);
@@ -742,26 +752,34 @@ hipError_t launch_t(const ConvParams& p, int n_cu, hipStream_t s) {
     // epilogue stores: byte offsets within one unit's rows inside the buffer resource's range
     if (!CONVT && ((int64_t)BN * p.y_ld + p.m_pad) * 4 >= kBufRecords) return hipErrorInvalidValue;
     if (CONVT && ((int64_t)p.stride_t * (BN + 1) + p.pad_t + 2) * p.y_ld * 4 >= kBufRecords) return hipErrorInvalidValue;
-    // producer loads: 32-bit byte offsets within one item's rows
+    // producer loads: 32-bit byte offsets within one item's rows, rows and channels within the
+    // 24-bit multiplier
     if (p.in_max_len * p.x_ld * (PRO != PRO_BF16 && !IN_H ? 4 : 2) >= (int64_t)1 << 32) return hipErrorInvalidValue;
+    if (p.in_max_len >= (int64_t)1 << 24 || p.x_ld >= (int64_t)1 << 24 || p.y_ld >= (int64_t)1 << 24 ||
+        p.r0_ld >= (int64_t)1 << 24)
+        return hipErrorInvalidValue;
+    if (validate_only) return hipSuccess;
     // one persistent block per CU; the grid is a multiple of 8 * mblocks
     const int64_t grp = 8 * (int64_t)(p.m_pad / BM);
     const int64_t units = ceil_div(p.tiles.count, 8) * grp;  // padded unit count
     const int64_t fit = std::max<int64_t>(1, n_cu / grp) * grp;
     const int64_t grid = std::min(units, fit);
-    auto go = [&](auto kern, bool& attr) -> hipError_t {
-        if (!attr) {
-            const hipError_t e =
-                hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem_max);
+    // the dynamic LDS limit is a per-device attribute of each kernel: set once per device
+    auto go = [&](auto kern, DeviceFlags& attr) -> hipError_t {
+        int dev = 0;
+        hipError_t e = hipGetDevice(&dev);
+        if (e != hipSuccess) return e;
+        if (!attr.test(dev)) {
+            e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem_max);
             if (e != hipSuccess) return e;
-            attr = true;
+            attr.set(dev);
         }
         hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(NT), smem, s, p);
         return hipGetLastError();
     };
     // small halos (every k3 layer, k7 at dilation 1, the ConvTs, 1x1 convs): the producers stage
     // BN + 16 rows instead of BN + 64 (3 of 20 row passes fewer at BN 256, 3 of 12 at BN 128)
-    static bool attr_small = false, attr_max = false;
+    static DeviceFlags attr_small, attr_max;
     if (halo <= kSmallHalo) return go(conv_mfma_kernel<PRO, EPI, WM, WN, STATS, IN_H, OUT_H, kSmallHalo>, attr_small);
     return go(conv_mfma_kernel<PRO, EPI, WM, WN, STATS, IN_H, OUT_H, kMaxHalo>, attr_max);
 }
@@ -771,11 +789,11 @@ hipError_t launch_t(const ConvParams& p, int n_cu, hipStream_t s) {
 // The (prologue, epilogue, block shape, statistics, fp16 in/out) combinations the engine uses;
 // anything else is refused.
 hipError_t launch_conv(const ConvParams& p, int pro, int epi, int shape, bool stats, bool in_h, bool out_h, int n_cu,
-                       hipStream_t s) {
+                       hipStream_t s, bool validate_only) {
     if (p.tiles.count == 0) return hipSuccess;
 #define KK_CONV(P, E, SH, WM, WN, ST, IH, OH)                                              \
     if (pro == P && epi == E && shape == SH && stats == ST && in_h == IH && out_h == OH) \
-        return launch_t<P, E, WM, WN, ST, IH, OH>(p, n_cu, s);
+        return launch_t<P, E, WM, WN, ST, IH, OH>(p, n_cu, s, validate_only);
     // Snake blocks, 256 ch (stage 0) and 128 ch (stage 1): conv1 X (f32) -> h (fp16) with statistics;
     // conv2 h -> X (ACCUM / ADD_FROM with statistics, last step without; MEAN3)
     KK_CONV(PRO_ADAIN_SNAKE, EPI_STORE, SHAPE_256x128, 4, 1, true, false, true)

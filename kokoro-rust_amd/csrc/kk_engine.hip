@@ -42,27 +42,36 @@ static void check(bool ok, const std::string& m) {
     } while (0)
 
 // ------------------------------------------------------------------ device buffers
+// A device allocation (cap > 0) or a view of part of another one (cap == 0: not freed here).
+// alloc() keeps an owned allocation that is large enough (grow-only reuse: the one-shot entry's
+// cached plan runs batch after batch in the same memory).
 struct DevBuf {
     void* p = nullptr;
-    size_t bytes = 0;
+    size_t bytes = 0;  // in use
+    size_t cap = 0;    // owned capacity
     DevBuf() = default;
     DevBuf(const DevBuf&) = delete;
     DevBuf& operator=(const DevBuf&) = delete;
-    DevBuf(DevBuf&& o) noexcept : p(o.p), bytes(o.bytes) { o.p = nullptr, o.bytes = 0; }
+    DevBuf(DevBuf&& o) noexcept : p(o.p), bytes(o.bytes), cap(o.cap) { o.p = nullptr, o.bytes = 0, o.cap = 0; }
     DevBuf& operator=(DevBuf&& o) noexcept {
         release();
-        p = o.p, bytes = o.bytes;
-        o.p = nullptr, o.bytes = 0;
+        p = o.p, bytes = o.bytes, cap = o.cap;
+        o.p = nullptr, o.bytes = 0, o.cap = 0;
         return *this;
     }
     ~DevBuf() { release(); }
     void release() {
-        if (p) (void)hipFree(p);
-        p = nullptr, bytes = 0;
+        if (p && cap) (void)hipFree(p);
+        p = nullptr, bytes = 0, cap = 0;
     }
-    void alloc(size_t n) {
-        release();
+    // Returns true when the memory is new (its contents undefined until written).
+    bool alloc(size_t n) {
         if (n == 0) n = 16;
+        if (p && cap >= n) {
+            bytes = n;
+            return false;
+        }
+        release();
         hipError_t e = hipMalloc(&p, n);
         if (e != hipSuccess) {
             p = nullptr;
@@ -70,10 +79,16 @@ struct DevBuf {
             fail(e == hipErrorOutOfMemory ? KK_ERR_OOM : KK_ERR_HIP,
                  "hipMalloc(" + std::to_string(n) + " bytes): " + hipGetErrorString(e));
         }
-        bytes = n;
+        bytes = cap = n;
+        return true;
+    }
+    void view(void* base, size_t n) {
+        release();
+        p = base, bytes = n;
     }
     template <class T>
     void upload(const T* h, size_t count) {
+        release();
         alloc(count * sizeof(T));
         if (count) KK_HIP(hipMemcpy(p, h, count * sizeof(T), hipMemcpyHostToDevice));
     }
@@ -151,11 +166,37 @@ struct Model {
 
 struct ProfRec {
     int cls;
-    double flop;
+    double flop, bytes;
     hipEvent_t e0, e1;
 };
-static const char* kProfNames[4] = {"snake_conv", "decoder_conv", "convt", "post_conv"};
-enum { PC_SNAKE = 0, PC_DECODER = 1, PC_CONVT = 2, PC_POST = 3 };
+// Kernel classes of the per-launch profile: the MFMA convolutions (by role), then the bandwidth
+// and glue kernels.
+enum {
+    PC_SNAKE = 0, PC_DECODER, PC_CONVT, PC_POST, PC_STATS, PC_FINALIZE, PC_STYLE, PC_EXPAND, PC_F0N, PC_COPY,
+    PC_POOL, PC_NOISE0, PC_NOISE1, PC_PHASE, PC_SOURCE, PC_ISTFT, PC_COUNT
+};
+static const char* kProfNames[PC_COUNT] = {"snake_conv", "decoder_conv", "convt",      "post_conv",
+                                           "stats_tiles", "finalize",    "style_fc",   "expand",
+                                           "f0n_conv",    "copy_cols",   "adain_pool", "noise_conv0",
+                                           "noise_conv1", "phase_pre",   "source_stft", "istft"};
+
+// Host staging of a plan's tables and inputs.  Everything a plan uploads (layout tables, tile lists,
+// work lists, the items' inputs) is written into one pinned host buffer of the context and reaches
+// the device in one copy into the plan's table buffer; every staged DevBuf then becomes a view of
+// its range there.
+struct Staging {
+    char* host = nullptr;  // pinned (hipHostMalloc), grow-only; or `heap` (pageable)
+    size_t cap = 0, used = 0;
+    bool pageable = false;  // host heap instead of pinned memory (the no-allocation entry point)
+    std::vector<char> heap;
+    hipEvent_t done = nullptr;  // recorded after the last copy out of `host`
+    bool pending = false;
+    struct Ref {
+        DevBuf* buf;
+        size_t off, bytes;
+    };
+    std::vector<Ref> refs;
+};
 
 }  // namespace kk
 
@@ -168,11 +209,16 @@ struct kk_ctx {
     // three more streams (default priority): the generator's independent resblock chains (0, 1) and
     // the source + noise branches (2)
     hipStream_t side[3] = {nullptr, nullptr, nullptr};
+    hipEvent_t join_ev[3] = {nullptr, nullptr, nullptr};  // error path: side streams joined back
     std::string name;
     kk::Model model;
     bool profiling = false;
     std::vector<kk::ProfRec> prof;
     std::vector<hipEvent_t> event_pool;
+    kk::Staging stage;
+    // kk_forward_decoder_batch's plan, kept between calls: its device buffers are reused whenever
+    // the next batch fits (released on any failure, so that a split batch can use the memory)
+    kk_plan* oneshot = nullptr;
 };
 
 namespace kk {
@@ -367,32 +413,100 @@ static void load_model(kk_ctx* ctx, const kk_tensor* tensors, int n) {
 }
 
 // ------------------------------------------------------------------ plans
+static void stage_begin(kk_ctx* ctx) {
+    Staging& s = ctx->stage;
+    if (s.pending) {
+        KK_HIP(hipEventSynchronize(s.done));  // the previous plan's copy has left the buffer
+        s.pending = false;
+    }
+    s.used = 0;
+    s.refs.clear();
+}
+
+// Reserves `count` elements for `b` in the staging buffer and returns where to write them (valid
+// until the next stage call, which may move the buffer).
+template <class T>
+static T* stage(kk_ctx* ctx, DevBuf& b, size_t count) {
+    Staging& s = ctx->stage;
+    const size_t bytes = std::max<size_t>(count * sizeof(T), 16);
+    const size_t off = (s.used + 255) / 256 * 256;
+    if (off + bytes > s.cap) {
+        const size_t ncap = std::max<size_t>(off + bytes + (off + bytes) / 2, (size_t)4 << 20);
+        if (s.pageable) {
+            s.heap.resize(ncap);
+            s.host = s.heap.data();
+        } else {
+            void* nh = nullptr;
+            KK_HIP(hipHostMalloc(&nh, ncap, hipHostMallocDefault));
+            if (s.used) std::memcpy(nh, s.host, s.used);
+            if (s.host) (void)hipHostFree(s.host);
+            s.host = (char*)nh;
+        }
+        s.cap = ncap;
+    }
+    s.used = off + bytes;
+    s.refs.push_back(Staging::Ref{&b, off, bytes});
+    return (T*)(s.host + off);
+}
+template <class T>
+static void stage_copy(kk_ctx* ctx, DevBuf& b, const T* h, size_t count) {
+    T* d = stage<T>(ctx, b, count);
+    if (count) std::memcpy(d, h, count * sizeof(T));
+}
+template <class T>
+static void stage_vec(kk_ctx* ctx, DevBuf& b, const std::vector<T>& v) {
+    stage_copy(ctx, b, v.data(), v.size());
+}
+// Everything staged since stage_begin goes to the device in one copy into `table` (grow-only), on
+// stream st; the staged buffers become views of it.
+static void stage_flush(kk_ctx* ctx, DevBuf& table, hipStream_t st) {
+    Staging& s = ctx->stage;
+    table.alloc(s.used);
+    if (s.used) KK_HIP(hipMemcpyAsync(table.p, s.host, s.used, hipMemcpyHostToDevice, st));
+    KK_HIP(hipEventRecord(s.done, st));
+    s.pending = true;
+    for (const auto& r : s.refs) r.buf->view((char*)table.p + r.off, r.bytes);
+    s.refs.clear();
+}
+
 struct Dom {
     int64_t l = 0;
     std::vector<int64_t> start, len;
-    std::vector<int32_t> col;
     DevBuf col_d, start_d, len_d;
+    // every item's span widened to the whole domain: what the convolutions read as an item's rows
+    // when gap masking is switched off (the negative-control hook)
+    DevBuf wstart_d, wlen_d;
     int64_t valid() const {
         int64_t s = 0;
         for (auto v : len) s += v;
         return s;
     }
-    // Dom::new (src/gpu_batch.rs:42-54): col_item per column, overflow / overlap are errors.
-    void build(int64_t l_, std::vector<int64_t> st, std::vector<int64_t> ln) {
+    // Dom::new (src/gpu_batch.rs:42-54), through kk_layout_col_item: col_item per column (-1 in
+    // gaps, built only for the domains a kernel masks with it), overflow and overlap are errors.
+    void build(kk_ctx* ctx, int64_t l_, std::vector<int64_t> st, std::vector<int64_t> ln, bool with_col, bool whole) {
         l = l_, start = std::move(st), len = std::move(ln);
-        col.assign(l, -1);
-        for (size_t b = 0; b < start.size(); b++) {
-            check(start[b] >= 0 && len[b] >= 0 && start[b] + len[b] <= l, "layout overflow");
-            for (int64_t t = start[b]; t < start[b] + len[b]; t++) {
-                check(col[t] < 0, "overlapping item spans");
-                col[t] = (int32_t)b;
-            }
+        const int n = (int)start.size();
+        for (int b = 0; b < n; b++) check(start[b] >= 0 && len[b] >= 0 && start[b] + len[b] <= l, "layout overflow");
+        stage_vec(ctx, start_d, start);
+        stage_vec(ctx, len_d, len);
+        if (with_col) {
+            int32_t* col = stage<int32_t>(ctx, col_d, (size_t)l);
+            check(kk_layout_col_item(l, start.data(), len.data(), n, col) == KK_OK, "overlapping item spans");
+        } else {
+            col_d.release();
         }
-        col_d.upload(col);
-        start_d.upload(start);
-        len_d.upload(len);
+        if (whole) {
+            int64_t* ws = stage<int64_t>(ctx, wstart_d, n);
+            for (int b = 0; b < n; b++) ws[b] = 0;
+            int64_t* wl = stage<int64_t>(ctx, wlen_d, n);
+            for (int b = 0; b < n; b++) wl[b] = l;
+        } else {
+            wstart_d.release(), wlen_d.release();
+        }
     }
-    DomDev dev() const { return DomDev{l, col_d.as<int32_t>(), start_d.as<int64_t>(), len_d.as<int64_t>(), (int)start.size()}; }
+    void release() {
+        for (DevBuf* b : {&col_d, &start_d, &len_d, &wstart_d, &wlen_d}) b->release();
+    }
 };
 
 // Item-aligned GEMM-column tiles of a domain (see TilesDev in kk_kernels.h).
@@ -406,21 +520,23 @@ struct Tiles {
     }
     // tiles of width `w` over [start_b, start_b + len_b + extra) for every item (extra = 1: the
     // ConvT GEMM column one past the item's last input)
-    void build(const Dom& d, int w, int extra) {
-        std::vector<int32_t> it, nn, lo(d.start.size()), hi(d.start.size());
+    void build(kk_ctx* ctx, const Dom& d, int w, int extra) {
+        const int nb = (int)d.start.size();
+        std::vector<int32_t> it, nn, lo_(nb), hi_(nb);
         std::vector<int64_t> t;
-        for (size_t b = 0; b < d.start.size(); b++) {
-            lo[b] = (int32_t)it.size();
+        for (int b = 0; b < nb; b++) {
+            lo_[b] = (int32_t)it.size();
             const int64_t len = d.len[b] + extra;
             for (int64_t j = 0; j < len; j += w) {
                 it.push_back((int32_t)b);
                 t.push_back(d.start[b] + j);
                 nn.push_back((int32_t)std::min<int64_t>(w, len - j));
             }
-            hi[b] = (int32_t)it.size();
+            hi_[b] = (int32_t)it.size();
         }
         count = (int64_t)it.size(), width = w;
-        item.upload(it), t0.upload(t), n.upload(nn), this->lo.upload(lo), this->hi.upload(hi);
+        stage_vec(ctx, item, it), stage_vec(ctx, t0, t), stage_vec(ctx, n, nn);
+        stage_vec(ctx, lo, lo_), stage_vec(ctx, hi, hi_);
     }
 };
 
@@ -436,9 +552,13 @@ struct kk_plan {
     std::vector<int64_t> a;    // frame layout starts
     int64_t ln = 0;
     kk::Dom dn, d2, d20, d120, ds;
+    // test hooks read at plan creation (see apply_test_hooks)
+    bool nomask = false, poison = false;
     // snake plans
     const kk::MSnake* sblk = nullptr;
     int sc = 0;
+    // every staged table and input of the plan, one device buffer (see Staging)
+    kk::DevBuf tables;
     // inputs
     kk::DevBuf t_en, src_row, f0, en, style, seeds, kinds, rand_ini, fixed_noise;
     int64_t t_rows = 0;
@@ -450,17 +570,19 @@ struct kk_plan {
     kk::DevBuf part, coef[11];
     int64_t part_bytes = 0;
     std::map<std::tuple<const kk::Dom*, int, int>, std::unique_ptr<kk::Tiles>> tiles;
-    // item-aligned tiles of domain d, width w (built on first use, at plan creation)
+    // item-aligned tiles of domain d, width w (built on first use: by the dry run at plan creation)
     const kk::Tiles& tl(const kk::Dom& d, int w, int extra = 0) {
         auto key = std::make_tuple(&d, w, extra);
         auto it = tiles.find(key);
         if (it == tiles.end()) {
+            kk::check(!frozen, "internal: tile list requested after plan creation");
             auto t = std::make_unique<kk::Tiles>();
-            t->build(d, w, extra);
+            t->build(ctx, d, w, extra);
             it = tiles.emplace(key, std::move(t)).first;
         }
         return *it->second;
     }
+    bool frozen = false;  // tables uploaded: no more staging
     kk::DevBuf src_item, src_f0, ist_item, ist_s0;
     kk::DevBuf pcm, pcm_len, pcm_clip;  // PCM_16 output: samples [600 ln], samples per item, clip counts
     int64_t n_src = 0, n_ist = 0;
@@ -471,7 +593,7 @@ struct kk_plan {
     // kk_plan_fetch_pcm16_async: recorded after its copies; pending until kk_plan_fetch_wait
     hipEvent_t fetch_ev = nullptr;
     bool fetch_pending = false;
-    void drop_fetch_event() {
+    void drop_events() {
         if (fetch_ev) (void)hipEventDestroy(fetch_ev);
         fetch_ev = nullptr, fetch_pending = false;
         for (auto& e : chain_ev)
@@ -479,14 +601,15 @@ struct kk_plan {
         for (auto& e : noise_ev)
             if (e) (void)hipEventDestroy(e), e = nullptr;
     }
-    // fork / join of the resblock chains, and of the noise branches (created on first use)
+    // fork / join of the resblock chains, and of the noise branches (created with the plan)
     hipEvent_t chain_ev[3] = {nullptr, nullptr, nullptr};
     hipEvent_t noise_ev[3] = {nullptr, nullptr, nullptr};
     std::vector<kk::DevBuf*> owned() {
-        return {&t_en, &src_row, &f0, &en, &style, &seeds, &kinds, &rand_ini, &fixed_noise, &gb, &xcat, &xin_a,
-                &xin_b, &hdec, &pool, &sc_half, &dec_out, &pp, &spec, &B[0], &B[1], &B[2], &B[3], &B[4], &B[5],
-                &post, &audio, &audio_start, &part, &coef[0], &coef[1], &coef[2], &coef[3], &coef[4], &coef[5], &coef[6], &coef[7], &coef[8], &coef[9], &coef[10], &xs[0], &xs[1], &hn, &src_item,
-                &src_f0, &ist_item, &ist_s0, &pcm, &pcm_len, &pcm_clip};
+        return {&tables, &t_en, &src_row, &f0, &en, &style, &seeds, &kinds, &rand_ini, &fixed_noise, &gb, &xcat,
+                &xin_a, &xin_b, &hdec, &pool, &sc_half, &dec_out, &pp, &spec, &B[0], &B[1], &B[2], &B[3], &B[4], &B[5],
+                &post, &audio, &audio_start, &part, &coef[0], &coef[1], &coef[2], &coef[3], &coef[4], &coef[5],
+                &coef[6], &coef[7], &coef[8], &coef[9], &coef[10], &xs[0], &xs[1], &hn, &src_item, &src_f0,
+                &ist_item, &ist_s0, &pcm, &pcm_len, &pcm_clip};
     }
 };
 
@@ -496,20 +619,59 @@ constexpr int kGapN = 2;  // GAP_N (src/gpu_batch.rs:27)
 constexpr int kGapT = 2;  // GAP_T (src/gpu_batch.rs:29)
 constexpr int64_t kXcatLd = 576, kXinLd = 1152, kSpecLd = 32, kPostLd = 32;
 
-static void alloc_zero(kk_plan* p, DevBuf& b, size_t bytes) {
-    b.alloc(bytes);
-    KK_HIP(launch_zero(b.p, (int64_t)((bytes + 3) / 4 * 4), p->ctx->stream));
+// A plan buffer.  Every element a run reads was written earlier in the same run (convolutions and
+// statistics read only the rows of their tiles' items, the masks of the reference are row-range
+// tests), so reused memory is not cleared; new memory is zeroed once.  With the poison hook every
+// buffer is filled with 0xff bytes (NaN in f32, fp16 and bf16) at every plan creation instead.
+static void alloc_buf(kk_plan* p, DevBuf& b, size_t bytes) {
+    const bool fresh = b.alloc((bytes + 255) / 256 * 256);
+    if (p->poison)
+        KK_HIP(launch_fill(b.p, (int64_t)b.bytes, 0xffffffffu, p->ctx->stream));
+    else if (fresh)
+        KK_HIP(launch_zero(b.p, (int64_t)b.bytes, p->ctx->stream));
 }
 
-// Layout shared by decoder and generator plans (src/gpu_batch.rs:250-263).
+static int64_t env_i64(const char* name, int64_t dflt) {
+    const char* v = std::getenv(name);
+    return v && *v ? std::strtoll(v, nullptr, 10) : dflt;
+}
+
+// Test hooks, read from the environment at plan creation:
+// - KOKORO_BATCH_NEGCTL_NOMASK (any value): the convolutions read every item's neighbours and gaps
+//   as if they were the item's own rows -- the reference's negative-control hook that turns gap
+//   masking off (src/gpu_batch.rs:62-66), so that tests can show they detect leakage;
+// - KOKORO_HIP_TEST_OOM_ABOVE=k: a batch of more than k items fails with KK_ERR_OOM before any
+//   allocation, as a device allocation failure would (the Err that Engine::synth_batch splits on,
+//   src/engine.rs:229-234);
+// - KOKORO_HIP_TEST_POISON=1: plan buffers are filled with NaN bytes instead of reused or zeroed.
+static void apply_test_hooks(kk_plan* p, int n) {
+    const int64_t lim = env_i64("KOKORO_HIP_TEST_OOM_ABOVE", -1);
+    if (lim >= 0 && n > lim)
+        fail(KK_ERR_OOM, "batch of " + std::to_string(n) + " items refused by KOKORO_HIP_TEST_OOM_ABOVE=" +
+                             std::to_string(lim) + " (simulated device allocation failure)");
+    p->nomask = std::getenv("KOKORO_BATCH_NEGCTL_NOMASK") != nullptr;
+    p->poison = env_i64("KOKORO_HIP_TEST_POISON", 0) != 0;
+}
+
+// Resets a plan's host state for a new batch (a fresh plan, or the one-shot plan being reused).
+static void reset_plan(kk_plan* p, int kind, int n) {
+    p->kind = kind, p->nb = n;
+    p->nfr.clear(), p->a.clear();
+    p->tiles.clear();
+    p->frozen = false;
+    p->sblk = nullptr, p->sc = 0;
+    p->ln = 0, p->t_rows = 0, p->n_src = p->n_ist = 0;
+    p->conv_flop = p->snake_flop = 0, p->launches = 0, p->last_until = 0;
+    p->fetch_pending = false;
+    apply_test_hooks(p, n);
+}
+
+// Layout shared by decoder and generator plans (src/gpu_batch.rs:250-263), through kk_layout_frames.
 static void build_frame_layout(kk_plan* p) {
+    kk_ctx* ctx = p->ctx;
     p->a.resize(p->nb);
-    int64_t ln = 0;
-    for (int b = 0; b < p->nb; b++) {
-        p->a[b] = ln;
-        ln += p->nfr[b] + kGapN;
-    }
-    p->ln = ln;
+    p->ln = kk_layout_frames(p->nfr.data(), p->nb, p->a.data());
+    check(p->ln >= 0, "frame layout: negative frame count");
     auto scale = [&](int64_t f) {
         std::vector<int64_t> v(p->nb);
         for (int b = 0; b < p->nb; b++) v[b] = p->a[b] * f;
@@ -520,10 +682,12 @@ static void build_frame_layout(kk_plan* p) {
         for (int b = 0; b < p->nb; b++) v[b] = p->nfr[b] * f + add;
         return v;
     };
-    p->dn.build(ln, scale(1), lens(1, 0));
-    p->d2.build(2 * ln, scale(2), lens(2, 0));
-    p->d20.build(20 * ln, scale(20), lens(20, 0));
-    p->d120.build(120 * ln + 1, scale(120), lens(120, 1));
+    const int64_t ln = p->ln;
+    const bool w = p->nomask;
+    p->dn.build(ctx, ln, scale(1), lens(1, 0), true, w);
+    p->d2.build(ctx, 2 * ln, scale(2), lens(2, 0), true, w);
+    p->d20.build(ctx, 20 * ln, scale(20), lens(20, 0), false, w);
+    p->d120.build(ctx, 120 * ln + 1, scale(120), lens(120, 1), true, w);
 }
 
 struct NoiseIn {
@@ -537,15 +701,19 @@ struct NoiseIn {
 // Generator inputs: F0 at d2, styles, noise (src/gpu_batch.rs:319-341) and all generator buffers.
 static void setup_generator(kk_plan* p, const std::vector<const float*>& f0s, const std::vector<const float*>& ref_s,
                             const std::vector<NoiseIn>& noise) {
+    kk_ctx* ctx = p->ctx;
     const int nb = p->nb;
     const int64_t ln = p->ln, l2 = 2 * ln, l20 = 20 * ln, l120 = 120 * ln + 1;
-    hipStream_t s = p->ctx->stream;
-    std::vector<float> f0h(l2, 0.f);
-    for (int b = 0; b < nb; b++) std::memcpy(&f0h[2 * p->a[b]], f0s[b], sizeof(float) * 2 * p->nfr[b]);
-    p->f0.upload(f0h);
-    std::vector<float> st((size_t)nb * kStyleDim);
-    for (int b = 0; b < nb; b++) std::memcpy(&st[(size_t)b * kStyleDim], ref_s[b], sizeof(float) * kStyleDim);
-    p->style.upload(st);
+    {
+        // F0 in the d2 layout, 0 in the gaps (F0_conv reads one gap sample at each item edge)
+        float* f0h = stage<float>(ctx, p->f0, (size_t)l2);
+        std::memset(f0h, 0, sizeof(float) * l2);
+        for (int b = 0; b < nb; b++) std::memcpy(&f0h[2 * p->a[b]], f0s[b], sizeof(float) * 2 * p->nfr[b]);
+    }
+    {
+        float* st = stage<float>(ctx, p->style, (size_t)nb * kStyleDim);
+        for (int b = 0; b < nb; b++) std::memcpy(&st[(size_t)b * kStyleDim], ref_s[b], sizeof(float) * kStyleDim);
+    }
     std::vector<uint64_t> seeds(nb);
     std::vector<int32_t> kinds(nb);
     std::vector<float> ri((size_t)nb * kHarmonics);
@@ -563,16 +731,19 @@ static void setup_generator(kk_plan* p, const std::vector<const float*>& f0s, co
             std::memcpy(&ri[(size_t)b * kHarmonics], noise[b].rand_ini, sizeof(float) * kHarmonics);
         }
     }
-    p->seeds.upload(seeds);
-    p->kinds.upload(kinds);
-    p->rand_ini.upload(ri);
+    stage_vec(ctx, p->seeds, seeds);
+    stage_vec(ctx, p->kinds, kinds);
+    stage_vec(ctx, p->rand_ini, ri);
     if (any_fixed) {
+        // caller-provided noise (rare, and 216 B per sample): its own buffer and copy
         std::vector<float> fx((size_t)600 * ln * kHarmonics, 0.f);
         for (int b = 0; b < nb; b++)
             if (noise[b].kind == KK_NOISE_FIXED)
                 std::memcpy(&fx[(size_t)600 * p->a[b] * kHarmonics], noise[b].sine,
                             sizeof(float) * 600 * p->nfr[b] * kHarmonics);
         p->fixed_noise.upload(fx);
+    } else {
+        p->fixed_noise.release();
     }
     // work lists of the one-launch source+STFT and iSTFT kernels
     std::vector<int64_t> si, sf, ii, is;
@@ -582,25 +753,28 @@ static void setup_generator(kk_plan* p, const std::vector<const float*>& f0s, co
         for (int64_t q = 0; q < samples; q += kIstftSamples) ii.push_back(b), is.push_back(q);
     }
     p->n_src = (int64_t)si.size(), p->n_ist = (int64_t)ii.size();
-    p->src_item.upload(si), p->src_f0.upload(sf), p->ist_item.upload(ii), p->ist_s0.upload(is);
+    stage_vec(ctx, p->src_item, si), stage_vec(ctx, p->src_f0, sf);
+    stage_vec(ctx, p->ist_item, ii), stage_vec(ctx, p->ist_s0, is);
     std::vector<int64_t> as(nb), ns(nb);
     for (int b = 0; b < nb; b++) as[b] = 600 * p->a[b], ns[b] = 600 * p->nfr[b];
-    p->audio_start.upload(as);
-    p->pcm_len.upload(ns);
-    alloc_zero(p, p->pcm, (size_t)600 * ln * sizeof(int16_t));  // gap samples stay 0
-    p->pcm_clip.alloc((size_t)nb * sizeof(unsigned long long));
+    stage_vec(ctx, p->audio_start, as);
+    stage_vec(ctx, p->pcm_len, ns);
+    // the PCM_16 layout's gap samples are 0 (kk_plan_fetch_pcm16_async copies the whole layout)
+    p->pcm.alloc((size_t)600 * ln * sizeof(int16_t));
+    KK_HIP(launch_zero(p->pcm.p, (int64_t)p->pcm.bytes, ctx->stream));
+    alloc_buf(p, p->pcm_clip, (size_t)nb * sizeof(unsigned long long));
 
-    p->gb.alloc((size_t)nb * p->ctx->model.style_rows * sizeof(float));
-    p->pp.alloc((size_t)kHarmonics * l2 * sizeof(float));
-    alloc_zero(p, p->spec, (size_t)l120 * kSpecLd * sizeof(float));
+    alloc_buf(p, p->gb, (size_t)nb * ctx->model.style_rows * sizeof(float));
+    alloc_buf(p, p->pp, (size_t)kHarmonics * l2 * sizeof(float));
+    alloc_buf(p, p->spec, (size_t)l120 * kSpecLd * sizeof(float));
     const size_t big = (size_t)std::max(l20 * 256, l120 * 128) * sizeof(float);
-    for (int i = 0; i < 6; i++) alloc_zero(p, p->B[i], big);
-    alloc_zero(p, p->post, (size_t)l120 * kPostLd * sizeof(float));
-    alloc_zero(p, p->audio, (size_t)600 * ln * sizeof(float));
-    for (int i = 0; i < 11; i++) p->coef[i].alloc((size_t)nb * kXinLd * sizeof(Coef));
-    alloc_zero(p, p->xs[0], (size_t)l20 * 256 * sizeof(float));
-    alloc_zero(p, p->xs[1], (size_t)l120 * 128 * sizeof(float));
-    alloc_zero(p, p->hn, (size_t)std::max(l20 * 256, l120 * 128) * sizeof(uint16_t));
+    for (int i = 0; i < 6; i++) alloc_buf(p, p->B[i], big);
+    alloc_buf(p, p->post, (size_t)l120 * kPostLd * sizeof(float));
+    alloc_buf(p, p->audio, (size_t)600 * ln * sizeof(float));
+    for (int i = 0; i < 11; i++) alloc_buf(p, p->coef[i], (size_t)nb * kXinLd * sizeof(Coef));
+    alloc_buf(p, p->xs[0], (size_t)l20 * 256 * sizeof(float));
+    alloc_buf(p, p->xs[1], (size_t)l120 * 128 * sizeof(float));
+    alloc_buf(p, p->hn, (size_t)std::max(l20 * 256, l120 * 128) * sizeof(uint16_t));
     // statistics partials: every partial but the last two of each item covers at least 64 columns
     // of one item (the noise convs' 64-column tiles; the convs' 128-column wave spans)
     auto bound = [&](int64_t l, int64_t c) { return (l / 64 + 2 * (int64_t)nb + 2) * c; };
@@ -610,24 +784,26 @@ static void setup_generator(kk_plan* p, const std::vector<const float*>& f0s, co
                                  bound_t(l2, 10, 256), bound_t(l20, 6, 128)});
     // four regions: one per concurrent resblock chain and one for the noise branches; part_bytes
     // is one region
-    p->part.alloc((size_t)4 * np * sizeof(StatPart));
+    alloc_buf(p, p->part, (size_t)4 * np * sizeof(StatPart));
     p->part_bytes = (int64_t)np * (int64_t)sizeof(StatPart);
 }
 
 struct Runner;
 static void prebuild_tiles(kk_plan* p);
 
+// Completes a plan: the dry run builds every tile list and validates every launch, the staged
+// tables go to the device in one copy, the fork / join events are made.  The copy is ordered before
+// any run on the context's stream; kk_plan_create waits for it besides.
 static void finish_plan(kk_plan* p) {
     prebuild_tiles(p);
-    KK_HIP(hipStreamSynchronize(p->ctx->stream));
+    stage_flush(p->ctx, p->tables, p->ctx->stream);
+    p->frozen = true;
+    for (auto& e : p->chain_ev)
+        if (!e) KK_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+    for (auto& e : p->noise_ev)
+        if (!e) KK_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
     p->dev_bytes = 0;
-    for (DevBuf* b : p->owned()) p->dev_bytes += (int64_t)b->bytes;
-    for (kk::Dom* d : {&p->dn, &p->d2, &p->d20, &p->d120, &p->ds})
-        p->dev_bytes += (int64_t)(d->col_d.bytes + d->start_d.bytes + d->len_d.bytes);
-    for (auto& kv : p->tiles) {
-        const kk::Tiles& t = *kv.second;
-        p->dev_bytes += (int64_t)(t.item.bytes + t.t0.bytes + t.n.bytes + t.lo.bytes + t.hi.bytes);
-    }
+    for (DevBuf* b : p->owned()) p->dev_bytes += (int64_t)b->cap;
 }
 
 static void check_noise(const NoiseIn& nz, int64_t n_frames, int b) {
@@ -640,12 +816,15 @@ static void check_noise(const NoiseIn& nz, int64_t n_frames, int b) {
     }
 }
 
-static kk_plan* create_decoder_plan(kk_ctx* ctx, const kk_decoder_item* items, int n) {
+// Fills plan p (new, or the one-shot plan whose device buffers are reused) for a decoder batch.
+static void init_decoder_plan(kk_plan* p, const kk_decoder_item* items, int n) {
+    kk_ctx* ctx = p->ctx;
     check(ctx->model.ready, "no model uploaded");
     check(items != nullptr && n > 0, "empty batch");
-    auto p = std::make_unique<kk_plan>();
-    p->ctx = ctx, p->kind = PLAN_DECODER, p->nb = n;
+    reset_plan(p, PLAN_DECODER, n);
     std::vector<int64_t> tstart(n);
+    std::vector<const int64_t*> durs(n);
+    std::vector<int32_t> ntok(n);
     int64_t rows = 0;
     for (int b = 0; b < n; b++) {
         const kk_decoder_item& it = items[b];
@@ -662,33 +841,32 @@ static kk_plan* create_decoder_plan(kk_ctx* ctx, const kk_decoder_item* items, i
         p->nfr.push_back(nf);
         tstart[b] = rows;  // token layout (src/gpu_batch.rs:188-197)
         rows += it.n_tok + kGapT;
+        durs[b] = it.dur, ntok[b] = it.n_tok;
     }
-    build_frame_layout(p.get());
+    stage_begin(ctx);
+    build_frame_layout(p);
     const int64_t ln = p->ln;
     // t_en in the token layout, channel-major [512][rows] (text_encoder_b output convention)
     p->t_rows = rows;
     {
-        std::vector<float> te((size_t)512 * rows, 0.f);
-        for (int b = 0; b < n; b++)
-            for (int c = 0; c < 512; c++)
-                std::memcpy(&te[(size_t)c * rows + tstart[b]], items[b].t_en + (size_t)c * items[b].n_tok,
-                            sizeof(float) * items[b].n_tok);
-        p->t_en.upload(te);
+        float* te = stage<float>(ctx, p->t_en, (size_t)512 * rows);
+        for (int c = 0; c < 512; c++)
+            for (int b = 0; b < n; b++) {
+                float* dst = te + (size_t)c * rows + tstart[b];
+                std::memcpy(dst, items[b].t_en + (size_t)c * items[b].n_tok, sizeof(float) * items[b].n_tok);
+                dst[items[b].n_tok] = dst[items[b].n_tok + 1] = 0.f;
+            }
     }
-    // frame -> token row table (src/gpu_batch.rs:265-276)
+    // frame -> token row table (src/gpu_batch.rs:265-276), through kk_layout_src_row
     {
-        std::vector<int32_t> sr(ln, -1);
-        for (int b = 0; b < n; b++) {
-            int64_t f = p->a[b];
-            for (int tok = 0; tok < items[b].n_tok; tok++)
-                for (int64_t r = 0; r < items[b].dur[tok]; r++) sr[f++] = (int32_t)(tstart[b] + tok);
-        }
-        p->src_row.upload(sr);
+        int32_t* sr = stage<int32_t>(ctx, p->src_row, (size_t)ln);
+        check(kk_layout_src_row(durs.data(), ntok.data(), n, tstart.data(), p->a.data(), ln, sr) == KK_OK,
+              "duration expansion overflows the frame layout");
     }
     {
-        std::vector<float> eh(2 * ln, 0.f);
+        float* eh = stage<float>(ctx, p->en, (size_t)2 * ln);
+        std::memset(eh, 0, sizeof(float) * 2 * ln);
         for (int b = 0; b < n; b++) std::memcpy(&eh[2 * p->a[b]], items[b].energy, sizeof(float) * 2 * p->nfr[b]);
-        p->en.upload(eh);
     }
     std::vector<const float*> f0s(n), refs(n);
     std::vector<NoiseIn> nz(n);
@@ -696,24 +874,37 @@ static kk_plan* create_decoder_plan(kk_ctx* ctx, const kk_decoder_item* items, i
         f0s[b] = items[b].f0, refs[b] = items[b].ref_s;
         nz[b] = NoiseIn{items[b].noise_kind, items[b].seed, items[b].rand_ini, items[b].sine, items[b].sine_len};
     }
-    setup_generator(p.get(), f0s, refs, nz);
-    alloc_zero(p.get(), p->xcat, (size_t)ln * kXcatLd * sizeof(float));
-    alloc_zero(p.get(), p->xin_a, (size_t)ln * kXinLd * sizeof(float));
-    alloc_zero(p.get(), p->xin_b, (size_t)ln * kXinLd * sizeof(float));
-    alloc_zero(p.get(), p->hdec, (size_t)ln * 1024 * sizeof(float));
-    alloc_zero(p.get(), p->pool, (size_t)2 * ln * kXinLd * sizeof(uint16_t));
-    alloc_zero(p.get(), p->sc_half, (size_t)ln * 512 * sizeof(float));
-    alloc_zero(p.get(), p->dec_out, (size_t)2 * ln * 512 * sizeof(float));
-    finish_plan(p.get());
+    setup_generator(p, f0s, refs, nz);
+    alloc_buf(p, p->xcat, (size_t)ln * kXcatLd * sizeof(float));
+    alloc_buf(p, p->xin_a, (size_t)ln * kXinLd * sizeof(float));
+    alloc_buf(p, p->xin_b, (size_t)ln * kXinLd * sizeof(float));
+    alloc_buf(p, p->hdec, (size_t)ln * 1024 * sizeof(float));
+    alloc_buf(p, p->pool, (size_t)2 * ln * kXinLd * sizeof(uint16_t));
+    alloc_buf(p, p->sc_half, (size_t)ln * 512 * sizeof(float));
+    alloc_buf(p, p->dec_out, (size_t)2 * ln * 512 * sizeof(float));
+    finish_plan(p);
+}
+
+// A user plan is complete (its inputs on the device) when kk_plan_create returns.
+static kk_plan* register_plan(kk_ctx* ctx, std::unique_ptr<kk_plan> p) {
+    KK_HIP(hipStreamSynchronize(ctx->stream));
     ctx->plans.insert(p.get());
     return p.release();
+}
+
+static kk_plan* create_decoder_plan(kk_ctx* ctx, const kk_decoder_item* items, int n) {
+    auto p = std::make_unique<kk_plan>();
+    p->ctx = ctx;
+    init_decoder_plan(p.get(), items, n);
+    return register_plan(ctx, std::move(p));
 }
 
 static kk_plan* create_generator_plan(kk_ctx* ctx, const kk_generator_item* items, int n) {
     check(ctx->model.ready, "no model uploaded");
     check(items != nullptr && n > 0, "empty batch");
     auto p = std::make_unique<kk_plan>();
-    p->ctx = ctx, p->kind = PLAN_GENERATOR, p->nb = n;
+    p->ctx = ctx;
+    reset_plan(p.get(), PLAN_GENERATOR, n);
     for (int b = 0; b < n; b++) {
         const std::string sb = std::to_string(b);
         check(items[b].x && items[b].f0 && items[b].ref_s, "item " + sb + ": null input");
@@ -722,6 +913,7 @@ static kk_plan* create_generator_plan(kk_ctx* ctx, const kk_generator_item* item
                     items[b].n_frames, b);
         p->nfr.push_back(items[b].n_frames);
     }
+    stage_begin(ctx);
     build_frame_layout(p.get());
     std::vector<const float*> f0s(n), refs(n);
     std::vector<NoiseIn> nz(n);
@@ -730,18 +922,17 @@ static kk_plan* create_generator_plan(kk_ctx* ctx, const kk_generator_item* item
         nz[b] = NoiseIn{items[b].noise_kind, items[b].seed, items[b].rand_ini, items[b].sine, items[b].sine_len};
     }
     setup_generator(p.get(), f0s, refs, nz);
-    // decoder output x [512][2N] per item -> time-major d2 rows
+    // decoder output x [512][2N] per item -> time-major d2 rows, 0 in the gaps
     const int64_t l2 = 2 * p->ln;
-    std::vector<float> xh((size_t)l2 * 512, 0.f);
+    float* xh = stage<float>(ctx, p->dec_out, (size_t)l2 * 512);
+    std::memset(xh, 0, sizeof(float) * l2 * 512);
     for (int b = 0; b < n; b++) {
         const int64_t t2 = 2 * p->nfr[b];
         for (int c = 0; c < 512; c++)
             for (int64_t t = 0; t < t2; t++) xh[(size_t)(2 * p->a[b] + t) * 512 + c] = items[b].x[(size_t)c * t2 + t];
     }
-    p->dec_out.upload(xh);
     finish_plan(p.get());
-    ctx->plans.insert(p.get());
-    return p.release();
+    return register_plan(ctx, std::move(p));
 }
 
 static const MSnake* find_snake(const Model& m, const std::string& prefix) {
@@ -759,7 +950,9 @@ static kk_plan* create_snake_plan(kk_ctx* ctx, const char* prefix, const float* 
     const MSnake* blk = find_snake(ctx->model, prefix);
     check(blk != nullptr, std::string("no Snake block named ") + prefix);
     auto p = std::make_unique<kk_plan>();
-    p->ctx = ctx, p->kind = PLAN_SNAKE, p->nb = n, p->sblk = blk, p->sc = blk->c;
+    p->ctx = ctx;
+    reset_plan(p.get(), PLAN_SNAKE, n);
+    p->sblk = blk, p->sc = blk->c;
     // receptive field of one dilation step: (k - 1) * 5 / 2 + (k - 1) / 2 columns
     const int k = blk->c1[0].k;
     check(gap >= (k - 1) * 5 / 2, "gap narrower than the block's conv reach");
@@ -771,31 +964,30 @@ static kk_plan* create_snake_plan(kk_ctx* ctx, const char* prefix, const float* 
         p->nfr.push_back(t[b]);
         l += t[b] + gap;
     }
-    p->ds.build(l, st, ln);
+    stage_begin(ctx);
+    p->ds.build(ctx, l, st, ln, false, p->nomask);
     const int c = blk->c;
-    std::vector<float> xh((size_t)l * c, 0.f);
-    for (int b = 0; b < n; b++)
-        for (int ch = 0; ch < c; ch++)
-            for (int64_t i = 0; i < t[b]; i++) xh[(size_t)(st[b] + i) * c + ch] = x[b][(size_t)ch * t[b] + i];
-    p->B[0].upload(xh);
-    std::vector<float> sth((size_t)n * kStyleDim);
-    for (int b = 0; b < n; b++) std::memcpy(&sth[(size_t)b * kStyleDim], ref_s[b], sizeof(float) * kStyleDim);
-    p->style.upload(sth);
-    p->gb.alloc((size_t)n * ctx->model.style_rows * sizeof(float));
-    alloc_zero(p.get(), p->B[1], (size_t)l * c * sizeof(float));
-    for (int i = 0; i < 2; i++) p->coef[i].alloc((size_t)n * c * sizeof(Coef));
-    p->part.alloc((size_t)(l / 128 + 2 * (int64_t)n + 2) * c * sizeof(StatPart));
+    {
+        float* xh = stage<float>(ctx, p->B[0], (size_t)l * c);
+        std::memset(xh, 0, sizeof(float) * l * c);
+        for (int b = 0; b < n; b++)
+            for (int ch = 0; ch < c; ch++)
+                for (int64_t i = 0; i < t[b]; i++) xh[(size_t)(st[b] + i) * c + ch] = x[b][(size_t)ch * t[b] + i];
+    }
+    {
+        float* sth = stage<float>(ctx, p->style, (size_t)n * kStyleDim);
+        for (int b = 0; b < n; b++) std::memcpy(&sth[(size_t)b * kStyleDim], ref_s[b], sizeof(float) * kStyleDim);
+    }
+    alloc_buf(p.get(), p->gb, (size_t)n * ctx->model.style_rows * sizeof(float));
+    alloc_buf(p.get(), p->B[1], (size_t)l * c * sizeof(float));
+    for (int i = 0; i < 2; i++) alloc_buf(p.get(), p->coef[i], (size_t)n * c * sizeof(Coef));
+    alloc_buf(p.get(), p->part, (size_t)(l / 128 + 2 * (int64_t)n + 2) * c * sizeof(StatPart));
     p->part_bytes = (int64_t)p->part.bytes;
     finish_plan(p.get());
-    ctx->plans.insert(p.get());
-    return p.release();
+    return register_plan(ctx, std::move(p));
 }
 
 // ------------------------------------------------------------------ the launch sequence
-#define KK_LAUNCH(x)                  \
-    do {                              \
-        if (!dry) KK_HIP(x);          \
-    } while (0)
 
 struct Runner {
     kk_plan* p;
@@ -821,6 +1013,26 @@ struct Runner {
         return e;
     }
 
+    // One kernel launch (nothing in the dry run): counted and, with profiling on, bracketed by an
+    // event pair on the launch stream and recorded under class `cls` with its algorithmic FLOP and
+    // bytes (valid rows only: the data the step must read and write once).
+    template <class F>
+    void launch(int cls, double f, double bytes, F&& fn) {
+        launches++;
+        if (dry) return;
+        hipEvent_t e0 = nullptr, e1 = nullptr;
+        if (ctx->profiling) {
+            e0 = ev(), e1 = ev();
+            KK_HIP(hipEventRecord(e0, s));
+        }
+        KK_HIP(fn());
+        if (ctx->profiling) {
+            KK_HIP(hipEventRecord(e1, s));
+            ctx->prof.push_back(ProfRec{cls, f, bytes, e0, e1});
+        }
+    }
+    int64_t frames() const { return p->dn.valid(); }
+
     void need_part(int64_t n) {
         check(n * (int64_t)sizeof(StatPart) <= p->part_bytes, "statistics partials buffer too small");
     }
@@ -829,17 +1041,19 @@ struct Runner {
     const Tiles& stats(const float* x, int64_t ld, int c, const Dom& d) {
         const Tiles& t = p->tl(d, kStatTile);
         need_part(t.count * c);
-        KK_LAUNCH(launch_stats_tiles(x, ld, c, t.dev(), part(), s));
-        launches++;
+        const double bytes = (double)d.valid() * c * 4 + (double)t.count * c * sizeof(StatPart);
+        launch(PC_STATS, 0, bytes, [&] { return launch_stats_tiles(x, ld, c, t.dev(), part(), s); });
         return t;
     }
     // Partials -> coefficients of AdaIN layer a (`wn` partials per tile; xrow: one more sample per
     // item, row xrow_at[b] of xrow [.][c]).
     void fin(const Tiles& t, int wn, int c, const MAdain& a, Coef* coef, const float* xrow = nullptr,
              const int64_t* xrow_at = nullptr) {
-        KK_LAUNCH(launch_finalize(part(), c, wn, t.dev(), p->nb, p->gb.as<float>(), gb_ld(),
-                               a.gb_off, a.nw.as<float>(), a.nb.as<float>(), coef, s, xrow, c, xrow_at));
-        launches++;
+        const double bytes = (double)t.count * wn * c * sizeof(StatPart) + (double)p->nb * c * (sizeof(Coef) + 8);
+        launch(PC_FINALIZE, 0, bytes, [&] {
+            return launch_finalize(part(), c, wn, t.dev(), p->nb, p->gb.as<float>(), gb_ld(), a.gb_off,
+                                   a.nw.as<float>(), a.nb.as<float>(), coef, s, xrow, c, xrow_at);
+        });
     }
     void stats_fin(const float* x, int64_t ld, int c, const Dom& d, const MAdain& a, Coef* coef) {
         fin(stats(x, ld, c, d), 1, c, a, coef);
@@ -874,6 +1088,10 @@ struct Runner {
         q.x = o.x, q.x_ld = o.x_ld, q.l_in = o.din->l, q.cin = c.cin, q.cin_pad = c.cin_pad;
         q.in_max_len = o.din->len.empty() ? 0 : *std::max_element(o.din->len.begin(), o.din->len.end());
         q.in_start = o.din->start_d.as<int64_t>(), q.in_len = o.din->len_d.as<int64_t>();
+        if (p->nomask) {  // negative-control hook: every item reads the whole domain as its rows
+            q.in_max_len = o.din->l;
+            q.in_start = o.din->wstart_d.as<int64_t>(), q.in_len = o.din->wlen_d.as<int64_t>();
+        }
         q.tiles = t.dev();
         q.coef = o.coef, q.alpha_rev = o.ar ? o.ar->as<float>() : nullptr;
         q.alpha_inv = o.ai ? o.ai->as<float>() : nullptr, q.slope = o.slope;
@@ -893,17 +1111,22 @@ struct Runner {
         const double f = 2.0 * (double)c.cin * valid * (o.convt ? 2.0 * c.m : (double)c.cout * c.k);
         flop += f;
         if (o.cls == PC_SNAKE) snake_flop += f;
-        hipEvent_t e0 = nullptr, e1 = nullptr;
-        if (ctx->profiling && !dry) {
-            e0 = ev(), e1 = ev();
-            KK_HIP(hipEventRecord(e0, s));
+        // algorithmic bytes: the input read once, the output written once, residual operands read
+        const double v_in = (double)o.din->valid(), v_out = (double)o.dout->valid();
+        const double es_in = (o.in_h || o.pro == PRO_BF16) ? 2 : 4, es_out = o.out_h ? 2 : 4;
+        const int nres = o.convt ? 1
+                         : o.epi == EPI_MEAN3 ? 3
+                         : (o.epi == EPI_ACCUM || o.epi == EPI_RESID || o.epi == EPI_ADD_FROM) ? 1
+                                                                                                 : 0;
+        double bytes = v_in * c.cin * es_in + v_out * c.cout * (es_out + 4.0 * nres);
+        if (o.epi == EPI_RESID_UP2) bytes += v_out / 2 * c.cout * 4;
+        // the dry run (plan creation) validates the launch parameters without launching
+        if (dry) {
+            if (launch_conv(q, o.pro, o.epi, c.shape, o.stats, o.in_h, o.out_h, ctx->n_cu, s, true) != hipSuccess)
+                fail(KK_ERR_INVALID, "convolution parameters out of the kernel's range (batch too large?)");
         }
-        KK_LAUNCH(launch_conv(q, o.pro, o.epi, c.shape, o.stats, o.in_h, o.out_h, ctx->n_cu, s));
-        launches++;
-        if (ctx->profiling && !dry) {
-            KK_HIP(hipEventRecord(e1, s));
-            ctx->prof.push_back(ProfRec{o.cls, f, e0, e1});
-        }
+        launch(o.cls, f, bytes,
+               [&] { return launch_conv(q, o.pro, o.epi, c.shape, o.stats, o.in_h, o.out_h, ctx->n_cu, s); });
         return t;
     }
 
@@ -963,8 +1186,6 @@ struct Runner {
         const bool conc = !ctx->profiling && !dry;
         hipStream_t main_s = s;
         if (conc) {
-            for (auto& e : p->chain_ev)
-                if (!e) KK_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
             KK_HIP(hipEventRecord(p->chain_ev[2], main_s));
             for (int q = 0; q < 2; q++) KK_HIP(hipStreamWaitEvent(ctx->side[q], p->chain_ev[2], 0));
         }
@@ -1038,27 +1259,31 @@ struct Runner {
         float* xa = p->xin_a.as<float>();
         float* xb = p->xin_b.as<float>();
         // asr = t_en expanded by the durations; F0 / N convs (src/gpu_batch.rs:295-302)
-        KK_LAUNCH(launch_expand(p->t_en.as<float>(), p->t_rows, p->src_row.as<int32_t>(), ln, xcat, kXcatLd, s));
-        KK_LAUNCH(launch_f0n_conv(p->f0.as<float>(), p->en.as<float>(), 2 * ln, m.f0w.as<float>(), m.f0b.as<float>(),
-                               m.nw_.as<float>(), m.nb_.as<float>(), xcat, kXcatLd, 512, 513, col, ln, s));
-        launches += 2;
+        const double nf = (double)frames();
+        launch(PC_EXPAND, 0, nf * 512 * 8, [&] {
+            return launch_expand(p->t_en.as<float>(), p->t_rows, p->src_row.as<int32_t>(), ln, xcat, kXcatLd, s);
+        });
+        launch(PC_F0N, 0, nf * 24, [&] {
+            return launch_f0n_conv(p->f0.as<float>(), p->en.as<float>(), 2 * ln, m.f0w.as<float>(), m.f0b.as<float>(),
+                                   m.nw_.as<float>(), m.nb_.as<float>(), xcat, kXcatLd, 512, 513, col, ln, s);
+        });
         resblk(m.encode, xcat, kXcatLd, xa, kXinLd);
         // asr_res (512 -> 64, k1) into channels [1024, 1088); F0n, Nn into 1088, 1089
         Op oa;
         oa.x = xcat, oa.x_ld = kXcatLd, oa.din = oa.dout = &dn, oa.y = xa + 1024, oa.y_ld = kXinLd;
         conv(m.asr_res, oa);
-        KK_LAUNCH(launch_copy_cols(xcat + 512, kXcatLd, 2, xa, kXinLd, 1088, col, ln, s));
-        KK_LAUNCH(launch_copy_cols(xa + 1024, kXinLd, 66, xb, kXinLd, 1024, col, ln, s));
-        launches += 2;
+        launch(PC_COPY, 0, nf * 2 * 8, [&] { return launch_copy_cols(xcat + 512, kXcatLd, 2, xa, kXinLd, 1088, col, ln, s); });
+        launch(PC_COPY, 0, nf * 66 * 8, [&] { return launch_copy_cols(xa + 1024, kXinLd, 66, xb, kXinLd, 1024, col, ln, s); });
         resblk(m.decode[0], xa, kXinLd, xb, kXinLd);
         resblk(m.decode[1], xb, kXinLd, xa, kXinLd);
         resblk(m.decode[2], xa, kXinLd, xb, kXinLd);
         // decode.3: upsample block to 2N (src/gpu_batch.rs:106-133)
         const MResblk& r = m.decode[3];
         stats_fin(xb, kXinLd, r.din, dn, r.n1, cf(0));
-        KK_LAUNCH(launch_adain_pool(xb, kXinLd, r.din, cf(0), col, ln, r.pool_w.as<float>(), r.pool_b.as<float>(),
-                                 d2.col_d.as<int32_t>(), p->pool.as<uint16_t>(), kXinLd, s));
-        launches++;
+        launch(PC_POOL, 0, nf * r.din * 4 + 2 * nf * kXinLd * 2, [&] {
+            return launch_adain_pool(xb, kXinLd, r.din, cf(0), col, ln, r.pool_w.as<float>(), r.pool_b.as<float>(),
+                                     d2.col_d.as<int32_t>(), p->pool.as<uint16_t>(), kXinLd, s);
+        });
         float* h = p->hdec.as<float>();
         Op o1;
         o1.pro = PRO_BF16, o1.x = p->pool.p, o1.x_ld = kXinLd, o1.din = o1.dout = &d2, o1.y = h, o1.y_ld = 512;
@@ -1077,8 +1302,11 @@ struct Runner {
     }
 
     void source() {
-        KK_LAUNCH(launch_phase_pre(p->f0.as<float>(), p->d2.start_d.as<int64_t>(), p->d2.len_d.as<int64_t>(), p->nb,
-                                p->rand_ini.as<float>(), p->pp.as<float>(), 2 * p->ln, s));
+        const double n2 = (double)p->d2.valid(), nfr120 = (double)p->d120.valid();
+        launch(PC_PHASE, 0, n2 * 4 * (1 + kHarmonics), [&] {
+            return launch_phase_pre(p->f0.as<float>(), p->d2.start_d.as<int64_t>(), p->d2.len_d.as<int64_t>(), p->nb,
+                                    p->rand_ini.as<float>(), p->pp.as<float>(), 2 * p->ln, s);
+        });
         SourceParams q{};
         q.f0 = p->f0.as<float>(), q.start2 = p->d2.start_d.as<int64_t>(), q.len2 = p->d2.len_d.as<int64_t>();
         q.pp = p->pp.as<float>(), q.pp_ld = 2 * p->ln, q.seeds = p->seeds.as<uint64_t>();
@@ -1087,8 +1315,8 @@ struct Runner {
         q.start120 = p->d120.start_d.as<int64_t>(), q.f_len = p->d120.len_d.as<int64_t>();
         q.blk_item = p->src_item.as<int64_t>(), q.blk_f0 = p->src_f0.as<int64_t>(), q.n_blocks = p->n_src;
         q.spec = p->spec.as<float>(), q.spec_ld = kSpecLd;
-        KK_LAUNCH(launch_source_stft(q, s));
-        launches += 2;
+        // reads F0 and the phases (d2), writes 22 f32 per STFT frame
+        launch(PC_SOURCE, 0, n2 * 4 * (1 + kHarmonics) + nfr120 * 88, [&] { return launch_source_stft(q, s); });
     }
 
     // xs_i = noise_res[i](noise_convs[i](masked spec)) (src/gpu_batch.rs:362-375) into p->xs[i],
@@ -1103,10 +1331,13 @@ struct Runner {
         const MNoiseConv& nc = m.nc[i];
         const Tiles& tn = p->tl(dout, kNoiseTile);
         need_part(tn.count * c);
-        KK_LAUNCH(launch_noise_conv(p->spec.as<float>(), kSpecLd, p->d120.l, p->d120.col_d.as<int32_t>(),
-                                 nc.w.as<float>(), nc.wp.p ? nc.wp.as<float>() : nullptr, nc.b.as<float>(), nc.cout,
-                                 nc.k, nc.stride, nc.pad, xs, c, tn.dev(), part(), s));
-        launches++;
+        // reads the spectrum's valid rows once (22 f32), writes cout f32 per output row
+        const double bytes = (double)p->d120.valid() * 88 + (double)dout.valid() * c * 4;
+        launch(i == 0 ? PC_NOISE0 : PC_NOISE1, 2.0 * 22 * nc.k * c * (double)dout.valid(), bytes, [&] {
+            return launch_noise_conv(p->spec.as<float>(), kSpecLd, p->d120.l, p->d120.col_d.as<int32_t>(),
+                                     nc.w.as<float>(), nc.wp.p ? nc.wp.as<float>() : nullptr, nc.b.as<float>(), nc.cout,
+                                     nc.k, nc.stride, nc.pad, xs, c, tn.dev(), part(), s);
+        });
         snake_block(m.noise_res[i], xs, p->hn.as<float>(), dout, &tn, cf(9), cf(10));
         region = reg;
     }
@@ -1146,14 +1377,16 @@ struct Runner {
         q.start120 = p->d120.start_d.as<int64_t>(), q.f_len = p->d120.len_d.as<int64_t>();
         q.blk_item = p->ist_item.as<int64_t>(), q.blk_s0 = p->ist_s0.as<int64_t>(), q.n_blocks = p->n_ist;
         q.audio = p->audio.as<float>(), q.audio_start = p->audio_start.as<int64_t>();
-        KK_LAUNCH(launch_istft(q, s));
-        launches++;
+        // 22 f32 read per frame, one f32 written per sample (21.6 B per sample)
+        launch(PC_ISTFT, 0, (double)p->d120.valid() * 88 + (double)frames() * 600 * 4,
+               [&] { return launch_istft(q, s); });
     }
 
     void run(int until) {
-        KK_LAUNCH(launch_style_fc(m.style_wt.as<float>(), m.style_b.as<float>(), m.style_rows, p->style.as<float>(),
-                               p->nb, p->gb.as<float>(), s));
-        launches++;
+        launch(PC_STYLE, 0, (double)m.style_rows * (kStyleDim + 1 + p->nb) * 4, [&] {
+            return launch_style_fc(m.style_wt.as<float>(), m.style_b.as<float>(), m.style_rows, p->style.as<float>(),
+                                   p->nb, p->gb.as<float>(), s);
+        });
         if (p->kind == PLAN_SNAKE) {
             snake_block(*p->sblk, p->B[0].as<float>(), p->B[1].as<float>(), p->ds);
             return;
@@ -1164,8 +1397,6 @@ struct Runner {
         const bool conc = !ctx->profiling && !dry && until > KK_STAGE_SOURCE;
         hipStream_t main_s = s;
         if (conc) {
-            for (auto& e : p->noise_ev)
-                if (!e) KK_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
             KK_HIP(hipEventRecord(p->noise_ev[0], main_s));  // after style_fc
             KK_HIP(hipStreamWaitEvent(ctx->side[2], p->noise_ev[0], 0));
             s = ctx->side[2];
@@ -1208,15 +1439,79 @@ static void prebuild_tiles(kk_plan* p) {
 }
 
 static void release_plan_device(kk_plan* p) {
-    p->drop_fetch_event();
-    for (DevBuf* b : p->owned()) b->release();
-    for (kk::Dom* d : {&p->dn, &p->d2, &p->d20, &p->d120, &p->ds}) {
-        d->col_d.release();
-        d->start_d.release();
-        d->len_d.release();
-    }
+    p->drop_events();
     p->tiles.clear();
+    for (kk::Dom* d : {&p->dn, &p->d2, &p->d20, &p->d120, &p->ds}) d->release();
+    for (DevBuf* b : p->owned()) b->release();
     p->ctx = nullptr;
+}
+
+// After a failed run: work the run left on the side streams (between a fork and its join) is
+// joined back into the context's stream, so that later work there -- a retried run, a fetch, a
+// free -- is ordered after it.
+static void join_side_streams(kk_ctx* ctx) {
+    for (int q = 0; q < 3; q++) {
+        if (!ctx->side[q] || !ctx->join_ev[q]) continue;
+        if (hipEventRecord(ctx->join_ev[q], ctx->side[q]) == hipSuccess)
+            (void)hipStreamWaitEvent(ctx->stream, ctx->join_ev[q], 0);
+    }
+}
+
+// Drops the one-shot plan and its device memory (after a failure, or at kk_close).
+static void drop_oneshot(kk_ctx* ctx) {
+    if (!ctx->oneshot) return;
+    (void)hipStreamSynchronize(ctx->stream);
+    for (auto ss : ctx->side)
+        if (ss) (void)hipStreamSynchronize(ss);
+    release_plan_device(ctx->oneshot);
+    delete ctx->oneshot;
+    ctx->oneshot = nullptr;
+}
+
+// ------------------------------------------------------------------ host output memory
+// The audio of kk_plan_fetch / kk_forward_decoder_batch lands in pinned host blocks that the
+// library keeps for reuse: one block per fetch holds the whole packed sample layout (one DMA copy,
+// no host-side copy), and each item's kk_output points into it.  kk_output_free returns the
+// item's reference; the block is free again when all its items are.  Blocks are process-wide (an
+// output may outlive its context) and never shrink below the largest batch fetched.
+struct OutBlock {
+    char* base;
+    size_t bytes;
+    int refs;  // live items pointing into the block
+};
+static std::mutex g_out_mu;
+static std::vector<OutBlock> g_out;
+
+static char* out_block_take(size_t bytes, int refs) {
+    std::lock_guard<std::mutex> lock(g_out_mu);
+    int best = -1;
+    for (int i = 0; i < (int)g_out.size(); i++)
+        if (g_out[i].refs == 0 && g_out[i].bytes >= bytes && (best < 0 || g_out[i].bytes < g_out[best].bytes)) best = i;
+    if (best < 0) {
+        // free blocks too small for this size would only grow the pool: release them
+        for (int i = (int)g_out.size() - 1; i >= 0; i--)
+            if (g_out[i].refs == 0) {
+                (void)hipHostFree(g_out[i].base);
+                g_out.erase(g_out.begin() + i);
+            }
+        void* p = nullptr;
+        KK_HIP(hipHostMalloc(&p, bytes, hipHostMallocDefault));
+        g_out.push_back(OutBlock{(char*)p, bytes, 0});
+        best = (int)g_out.size() - 1;
+    }
+    g_out[best].refs = refs;
+    return g_out[best].base;
+}
+
+// Releases one item reference; false when `p` is not inside a block of the pool.
+static bool out_block_release(const void* p) {
+    std::lock_guard<std::mutex> lock(g_out_mu);
+    for (auto& b : g_out)
+        if ((const char*)p >= b.base && (const char*)p < b.base + b.bytes && b.refs > 0) {
+            b.refs--;
+            return true;
+        }
+    return false;
 }
 
 static void set_err(char* err, size_t errlen, const std::string& m) {
@@ -1256,6 +1551,30 @@ static void tap_rows(const void* dev, int64_t ld, int64_t r0, int64_t rows, int 
 
 using namespace kk;
 
+namespace kk {
+static void run_plan(kk_plan* plan, int until) {
+    use_device(plan->ctx);
+    check(plan->ctx->model.ready, "no model uploaded");
+    check(until >= KK_STAGE_DECODER && until <= KK_STAGE_ALL, "unknown stage");
+    hipStream_t s = plan->ctx->stream;
+    Runner r{plan, plan->ctx, plan->ctx->model, s};
+    plan->last_until = 0;
+    try {
+        // Eager launches: the generator's three resblock chains run on three streams at once, which
+        // a captured HIP graph executes one node at a time on this runtime (measured: the graph
+        // replay of the same sequence is 1.7% slower per step).
+        r.run(until);
+    } catch (...) {
+        join_side_streams(plan->ctx);
+        throw;
+    }
+    plan->conv_flop = r.flop, plan->snake_flop = r.snake_flop, plan->launches = r.launches;
+    plan->last_until = until;
+}
+
+
+}  // namespace kk
+
 extern "C" {
 
 const char* kk_identity(void) { return "hip-gfx950 bf16-mfma f32-acc"; }
@@ -1280,6 +1599,8 @@ int kk_open(int ordinal, kk_ctx** out, char* err, size_t errlen) {
         KK_HIP(hipSetDevice(ordinal));
         KK_HIP(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking));
         for (auto& ss : ctx->side) KK_HIP(hipStreamCreateWithFlags(&ss, hipStreamNonBlocking));
+        for (auto& e : ctx->join_ev) KK_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+        KK_HIP(hipEventCreateWithFlags(&ctx->stage.done, hipEventDisableTiming));
         // twiddles and periodic Hann window in f64 (src/gpu.rs:93-101)
         double cs[220], sn[220];
         float win[20];
@@ -1305,6 +1626,11 @@ void kk_close(kk_ctx* ctx) {
     // releases the host object, and every other entry on them reports KK_ERR_STATE
     for (kk_plan* p : ctx->plans) release_plan_device(p);
     ctx->plans.clear();
+    drop_oneshot(ctx);
+    if (ctx->stage.host) (void)hipHostFree(ctx->stage.host);
+    if (ctx->stage.done) (void)hipEventDestroy(ctx->stage.done);
+    for (auto e : ctx->join_ev)
+        if (e) (void)hipEventDestroy(e);
     for (auto& r : ctx->prof) {
         (void)hipEventDestroy(r.e0);
         (void)hipEventDestroy(r.e1);
@@ -1366,18 +1692,7 @@ int kk_plan_run(kk_plan* plan, int until, char* err, size_t errlen) {
         set_err(err, errlen, "plan outlived its context");
         return KK_ERR_STATE;
     }
-    return guard(err, errlen, [&] {
-        use_device(plan->ctx);
-        check(plan->ctx->model.ready, "no model uploaded");
-        hipStream_t s = plan->ctx->stream;
-        Runner r{plan, plan->ctx, plan->ctx->model, s};
-        // Eager launches: the generator's three resblock chains run on three streams at once, which
-        // a captured HIP graph executes one node at a time on this runtime (measured: the graph
-        // replay of the same sequence is 1.7% slower per step).
-        r.run(until);
-        plan->conv_flop = r.flop, plan->snake_flop = r.snake_flop, plan->launches = r.launches;
-        plan->last_until = until;
-    });
+    return guard(err, errlen, [&] { run_plan(plan, until); });
 }
 
 int kk_plan_sync(kk_plan* plan, char* err, size_t errlen) {
@@ -1392,6 +1707,30 @@ int kk_plan_sync(kk_plan* plan, char* err, size_t errlen) {
     });
 }
 
+// Each item's result into `out` (see kk_plan_fetch).  Audio: one copy of the whole packed sample
+// layout into a pinned block of the output pool; the items point into it.
+static void fetch_plan(kk_plan* plan, kk_output* out) {
+    use_device(plan->ctx);
+    check(plan->last_until >= KK_STAGE_ALL || plan->kind == PLAN_SNAKE, "plan has not run to the end");
+    hipStream_t s = plan->ctx->stream;
+    if (plan->kind == PLAN_SNAKE) {
+        KK_HIP(hipStreamSynchronize(s));
+        for (int b = 0; b < plan->nb; b++) {
+            const int64_t t = plan->ds.len[b];
+            out[b].n_samples = t * plan->sc;
+            out[b].audio = (float*)std::malloc(sizeof(float) * out[b].n_samples);
+            if (!out[b].audio) throw std::bad_alloc();
+            tap_rows(plan->B[0].p, plan->sc, plan->ds.start[b], t, plan->sc, out[b].audio);
+        }
+        return;
+    }
+    const size_t bytes = sizeof(float) * 600 * (size_t)plan->ln;
+    float* blk = (float*)out_block_take(bytes, plan->nb);
+    for (int b = 0; b < plan->nb; b++) out[b] = kk_output{blk + 600 * plan->a[b], 600 * plan->nfr[b]};
+    KK_HIP(hipMemcpyAsync(blk, plan->audio.p, bytes, hipMemcpyDeviceToHost, s));
+    KK_HIP(hipStreamSynchronize(s));
+}
+
 int kk_plan_fetch(kk_plan* plan, kk_output* out, char* err, size_t errlen) {
     if (!plan || !out) return KK_ERR_INVALID;
     if (!plan->ctx) {
@@ -1399,27 +1738,7 @@ int kk_plan_fetch(kk_plan* plan, kk_output* out, char* err, size_t errlen) {
         return KK_ERR_STATE;
     }
     for (int b = 0; b < plan->nb; b++) out[b] = kk_output{nullptr, 0};
-    int rc = guard(err, errlen, [&] {
-        use_device(plan->ctx);
-        check(plan->last_until >= KK_STAGE_ALL || plan->kind == PLAN_SNAKE, "plan has not run to the end");
-        KK_HIP(hipStreamSynchronize(plan->ctx->stream));
-        for (int b = 0; b < plan->nb; b++) {
-            if (plan->kind == PLAN_SNAKE) {
-                const int64_t t = plan->ds.len[b];
-                out[b].n_samples = t * plan->sc;
-                out[b].audio = (float*)std::malloc(sizeof(float) * out[b].n_samples);
-                if (!out[b].audio) throw std::bad_alloc();
-                tap_rows(plan->B[0].p, plan->sc, plan->ds.start[b], t, plan->sc, out[b].audio);
-            } else {
-                const int64_t ns = 600 * plan->nfr[b];
-                out[b].n_samples = ns;
-                out[b].audio = (float*)std::malloc(sizeof(float) * ns);
-                if (!out[b].audio) throw std::bad_alloc();
-                KK_HIP(hipMemcpy(out[b].audio, plan->audio.as<float>() + 600 * plan->a[b], sizeof(float) * ns,
-                                 hipMemcpyDeviceToHost));
-            }
-        }
-    });
+    int rc = guard(err, errlen, [&] { fetch_plan(plan, out); });
     if (rc != KK_OK) kk_output_free(out, plan->nb);
     return rc;
 }
@@ -1653,7 +1972,7 @@ void kk_plan_free(kk_plan* plan) {
         (void)hipStreamSynchronize(plan->ctx->stream);
         // a run that failed between a fork and its join may leave work on the side streams
         for (auto ss : plan->ctx->side) (void)hipStreamSynchronize(ss);
-        plan->drop_fetch_event();
+        plan->drop_events();
         plan->ctx->plans.erase(plan);
     }
     delete plan;
@@ -1661,20 +1980,34 @@ void kk_plan_free(kk_plan* plan) {
 
 int kk_forward_decoder_batch(kk_ctx* ctx, const kk_decoder_item* items, int n, kk_output* out, char* err,
                              size_t errlen) {
-    if (!ctx || !out) return KK_ERR_INVALID;
-    kk_plan* plan = nullptr;
-    int rc = kk_plan_create(ctx, items, n, &plan, err, errlen);
-    if (rc != KK_OK) return rc;
-    rc = kk_plan_run(plan, KK_STAGE_ALL, err, errlen);
-    if (rc == KK_OK) rc = kk_plan_fetch(plan, out, err, errlen);
-    kk_plan_free(plan);
+    if (!ctx || !out || n < 0) return KK_ERR_INVALID;
+    for (int b = 0; b < n; b++) out[b] = kk_output{nullptr, 0};
+    int rc = guard(err, errlen, [&] {
+        use_device(ctx);
+        // the one-shot plan is kept: its device buffers serve the next batch that fits
+        if (!ctx->oneshot) {
+            ctx->oneshot = new kk_plan();
+            ctx->oneshot->ctx = ctx;
+        }
+        try {
+            init_decoder_plan(ctx->oneshot, items, n);
+            run_plan(ctx->oneshot, KK_STAGE_ALL);
+            fetch_plan(ctx->oneshot, out);
+        } catch (...) {
+            // a failure (device memory exhausted above all) releases the cached buffers, so that a
+            // caller splitting the batch (src/engine.rs:229-234) has the whole device again
+            drop_oneshot(ctx);
+            throw;
+        }
+    });
+    if (rc != KK_OK) kk_output_free(out, n);
     return rc;
 }
 
 void kk_output_free(kk_output* out, int n) {
     if (!out) return;
     for (int b = 0; b < n; b++) {
-        std::free(out[b].audio);
+        if (out[b].audio && !out_block_release(out[b].audio)) std::free(out[b].audio);
         out[b].audio = nullptr;
         out[b].n_samples = 0;
     }
@@ -1691,8 +2024,8 @@ int kk_profile_read(kk_ctx* ctx, kk_profile_entry* out, int max, int* n_out, cha
     return guard(err, errlen, [&] {
         use_device(ctx);
         KK_HIP(hipStreamSynchronize(ctx->stream));
-        kk_profile_entry acc[4];
-        for (int i = 0; i < 4; i++) {
+        kk_profile_entry acc[PC_COUNT];
+        for (int i = 0; i < PC_COUNT; i++) {
             std::memset(&acc[i], 0, sizeof(acc[i]));
             std::snprintf(acc[i].name, sizeof(acc[i].name), "%s", kProfNames[i]);
         }
@@ -1702,12 +2035,14 @@ int kk_profile_read(kk_ctx* ctx, kk_profile_entry* out, int max, int* n_out, cha
             acc[r.cls].launches++;
             acc[r.cls].ms += ms;
             acc[r.cls].flop += r.flop;
+            acc[r.cls].bytes += r.bytes;
             ctx->event_pool.push_back(r.e0);
             ctx->event_pool.push_back(r.e1);
         }
         ctx->prof.clear();
         int k = 0;
-        for (int i = 0; i < 4 && k < max; i++) out[k++] = acc[i];
+        for (int i = 0; i < PC_COUNT && k < max; i++)
+            if (acc[i].launches > 0) out[k++] = acc[i];
         *n_out = k;
     });
 }

@@ -83,9 +83,10 @@ struct ConvParams {
 };
 
 // in_h / out_h: fp16 input (conv2 of a Snake step) / fp16 output (conv1 of a Snake step).
-// n_cu: compute units of the device (persistent grid size).
+// n_cu: compute units of the device (persistent grid size).  validate_only: check the parameters
+// against the kernel's limits (hipErrorInvalidValue when out of range) and launch nothing.
 hipError_t launch_conv(const ConvParams& p, int pro, int epi, int shape, bool stats, bool in_h, bool out_h, int n_cu,
-                       hipStream_t s);
+                       hipStream_t s, bool validate_only = false);
 
 // ---------------------------------------------------------------- bandwidth kernels (kk_misc.hip)
 // Statistics partials of x [l][ld] over tiles (one partial per tile and channel).
@@ -167,8 +168,10 @@ hipError_t launch_istft(const IstftParams& p, hipStream_t s);
 hipError_t launch_pcm16(const float* audio, const int64_t* audio_start, const int64_t* item_len,
                         const int64_t* blk_item, const int64_t* blk_s0, int64_t n_blocks, int16_t* out,
                         unsigned long long* clipped, hipStream_t s);
-// Zero a buffer (a kernel, so the sequence stays capturable in a graph).
+// Zero a buffer / fill it with a 32-bit pattern (kernels, so the sequence stays capturable in a
+// graph); bytes is a multiple of 4.
 hipError_t launch_zero(void* p, int64_t bytes, hipStream_t s);
+hipError_t launch_fill(void* p, int64_t bytes, uint32_t value, hipStream_t s);
 
 constexpr int kSourceFrames = 128;  // STFT frames per source block
 constexpr int kIstftSamples = 512;  // output samples per iSTFT block

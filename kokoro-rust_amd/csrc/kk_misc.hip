@@ -746,9 +746,9 @@ __global__ __launch_bounds__(256) void pcm16_kernel(const float* __restrict__ au
     }
 }
 
-__global__ void zero_kernel(uint32_t* p, int64_t n) {
+__global__ void fill_kernel(uint32_t* p, int64_t n, uint32_t v) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) p[i] = 0u;
+    if (i < n) p[i] = v;
 }
 
 unsigned blocks_for(int64_t n, int per) { return (unsigned)ceil_div(n, per); }
@@ -870,10 +870,13 @@ hipError_t launch_pcm16(const float* audio, const int64_t* audio_start, const in
     return hipGetLastError();
 }
 
-hipError_t launch_zero(void* p, int64_t bytes, hipStream_t s) {
+hipError_t launch_fill(void* p, int64_t bytes, uint32_t value, hipStream_t s) {
     const int64_t n = bytes / 4;
-    hipLaunchKernelGGL(zero_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, s, (uint32_t*)p, n);
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(fill_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, s, (uint32_t*)p, n, value);
     return hipGetLastError();
 }
+
+hipError_t launch_zero(void* p, int64_t bytes, hipStream_t s) { return launch_fill(p, bytes, 0u, s); }
 
 }  // namespace kk

@@ -60,7 +60,8 @@ class PlanInfo(C.Structure):
 
 
 class ProfileEntry(C.Structure):
-    _fields_ = [("name", C.c_char * 32), ("launches", C.c_int64), ("ms", C.c_double), ("flop", C.c_double)]
+    _fields_ = [("name", C.c_char * 32), ("launches", C.c_int64), ("ms", C.c_double), ("flop", C.c_double),
+                ("bytes", C.c_double)]
 
 
 _lib = None
@@ -227,11 +228,12 @@ class Context:
         lib().kk_set_profiling(self.h, int(bool(on)))
 
     def profile_read(self):
-        ents = (ProfileEntry * 8)()
+        ents = (ProfileEntry * 32)()
         n = C.c_int()
         err = _err()
-        _check(lib().kk_profile_read(self.h, ents, 8, C.byref(n), err, len(err)), err)
-        return {e.name.decode(): {"launches": e.launches, "ms": e.ms, "flop": e.flop} for e in ents[: n.value]}
+        _check(lib().kk_profile_read(self.h, ents, 32, C.byref(n), err, len(err)), err)
+        return {e.name.decode(): {"launches": e.launches, "ms": e.ms, "flop": e.flop, "bytes": e.bytes}
+                for e in ents[: n.value]}
 
     # -------------------------------------------------------------- batch entry points
     def forward_decoder_batch(self, items):
@@ -248,6 +250,17 @@ class Context:
     def plan(self, items):
         return Plan.decoder(self, items)
 
+    def prepare(self, items):
+        """The items marshalled once into the ABI's structs, for repeated calls (timing)."""
+        return PreparedBatch(items)
+
+    def forward_prepared(self, pb):
+        """kk_forward_decoder_batch on a PreparedBatch; the outputs stay in pb.outs (release with
+        pb.release()).  Raises KKError on failure."""
+        err = _err()
+        _check(lib().kk_forward_decoder_batch(self.h, pb.arr, pb.n, pb.outs, err, len(err)), err)
+
+
     def host_alloc(self, count, dtype):
         """kk_host_alloc: a pinned host array of `count` elements of `dtype` (freed with .free())."""
         return PinnedArray(self, count, dtype)
@@ -260,6 +273,20 @@ class Context:
         err = _err()
         _check(lib().kk_encode_pcm16(self.h, _p(a), a.size, _p(out), _p(clipped), err, len(err)), err)
         return out, int(clipped[0])
+
+
+class PreparedBatch:
+    def __init__(self, items):
+        self.arr, self._keep = _decoder_items(items)
+        self.n = len(items)
+        self.outs = (Output * self.n)()
+
+    def audio(self, b):
+        o = self.outs[b]
+        return np.ctypeslib.as_array(o.audio, shape=(o.n_samples,)).copy()
+
+    def release(self):
+        lib().kk_output_free(self.outs, self.n)
 
 
 class PinnedArray:

@@ -5,6 +5,8 @@ Test infrastructure: it pins the C oracle (oracle/kk_oracle.c) from a second, st
 implementation that follows the upstream model definition the reference restates (StyleTTS2
 AdainResBlk1d / iSTFTNet AdaINResBlock1, SineGen, TorchSTFT; docs/truth-pack/OQ_INDEX.md OQ-8,
 OQ-9), so a wrong padding, dilation, weight orientation or op order in the oracle shows up here.
+In float32 (set_dtype) it is also the torch-CPU functional baseline that bench.py times beside the
+GPU: the op sequence upstream kokoro runs on a CPU, one item at a time.
 """
 import math
 
@@ -13,6 +15,12 @@ import torch
 import torch.nn.functional as F
 
 DT = torch.float64
+
+
+def set_dtype(dt):
+    """Arithmetic type of every op below (float64 to pin the oracle, float32 for the CPU baseline)."""
+    global DT
+    DT = dt
 
 
 def T(a):

@@ -1,5 +1,5 @@
 """Write tests/golden/golden_v1.npz: small input/output vectors from the float64 torch restatement
-(tests/torch_ref.py, library routines only) that pin the CPU oracle independently of the torch
+(oracle/torch_ref.py, library routines only) that pin the CPU oracle independently of the torch
 version installed later.  Weights are model_spec.random_weights(seed=0); their sha256 is stored.
 
 Run: python tests/golden/make_golden.py
@@ -13,9 +13,9 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(os.path.dirname(HERE))
-sys.path.insert(0, os.path.join(ROOT, "tests"))
+sys.path.insert(0, ROOT)
 sys.path.insert(0, os.path.join(ROOT, "kokoro-rust_amd"))
-import torch_ref as R  # noqa: E402
+from oracle import torch_ref as R  # noqa: E402
 from kokoro_hip import model_spec, workloads  # noqa: E402
 
 

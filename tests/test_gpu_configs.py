@@ -92,3 +92,50 @@ def test_config5_full_size(gpu_ctx, oracle_model):
         plan.run()
         (alone,) = plan.fetch()
     assert np.array_equal(alone, outs[hi]), f"item {hi} (N {ns[hi]})"
+
+
+def test_config3_full_size(gpu_ctx, oracle_model):
+    """The benchmark's own batch (32 ragged items, N ~ U[100, 800]) at full size.
+
+    - every item finite with 600 N samples;
+    - the shortest, the median and the longest item against the fp32 oracle at the north-star bar
+      (max-abs <= 2e-3, SNR >= 40 dB) and against the bf16-emulated oracle (>= 44 dB); an item whose
+      spectrum has a bin on atan2's branch cut is compared through the oracle's generator run from
+      the GPU's own spectrum (see test_gpu_properties._check_vs_oracle);
+    - the shortest and the longest item bit-identical to runs of themselves alone."""
+    from kokoro_hip import api, workloads
+    from oracle import oracle as O
+    items = workloads.config3_items()
+    ns = [it.n_frames for it in items]
+    _print("  config 3:", len(items), "items, frames", sum(ns))
+    order = list(np.argsort(ns, kind="stable"))
+    picks = [int(order[0]), int(order[len(order) // 2]), int(order[-1])]
+    with api.Plan.decoder(gpu_ctx, items) as plan:
+        plan.run()
+        outs = plan.fetch()
+        specs = {b: plan.tap("spec", b, (22, 120 * ns[b] + 1)) for b in picks}
+    for it, a in zip(items, outs):
+        assert a.shape == (600 * it.n_frames,) and np.isfinite(a).all()
+    for b in picks:
+        it, a, g = items[b], outs[b], specs[b]
+        ref, spec, _ = O.synth_item(oracle_model, it, taps=True)
+        with O.bf16_emulation():
+            emu, _, _ = O.synth_item(oracle_model, it, taps=True)
+        flips = int((np.abs(g[11:] - spec[11:]) > np.pi).sum())
+        if flips:
+            asr = O.expand_tokens(it.t_en, it.dur)
+            x = oracle_model.decoder(asr, it.f0, it.energy, it.ref_s)
+            ref, _ = oracle_model.generator_from_spec(x, g, it.ref_s)
+            with O.bf16_emulation():
+                xe = oracle_model.decoder(asr, it.f0, it.energy, it.ref_s)
+                emu, _ = oracle_model.generator_from_spec(xe, g, it.ref_s)
+        _print(f"  item {b} N {ns[b]}: branch-cut bins {flips} fp32 snr {snr_db(ref, a):.2f} "
+               f"maxabs {np.abs(a - ref).max():.3g} emu snr {snr_db(emu, a):.2f}")
+        assert np.abs(a - ref).max() <= 2e-3
+        assert snr_db(ref, a) >= 40.0
+        assert snr_db(emu, a) >= 44.0
+    for b in (picks[0], picks[-1]):
+        with api.Plan.decoder(gpu_ctx, [items[b]]) as plan:
+            plan.run()
+            (alone,) = plan.fetch()
+        assert np.array_equal(alone, outs[b]), f"item {b} (N {ns[b]})"

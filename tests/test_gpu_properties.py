@@ -173,3 +173,53 @@ def test_long_item_vs_oracle(gpu_ctx, oracle_model):
     """One 600-frame item (15 s of audio) between two short ones."""
     from kokoro_hip import workloads
     _check_vs_oracle(gpu_ctx, oracle_model, workloads.small_items(67, [7, 600, 3]), "long")
+
+
+def test_one_shot_reuses_memory(gpu_ctx, monkeypatch):
+    """kk_forward_decoder_batch keeps its device buffers between calls and does not clear them: every
+    value a run reads must have been written earlier in the same run.  With the poison hook every
+    buffer is filled with NaN bytes before each call, so a read of anything stale or unwritten
+    (a gap row, a pad channel, a previous batch's data) would reach the audio.  Batches of growing
+    and shrinking layouts, one after another, must equal fresh plans bit for bit."""
+    from kokoro_hip import workloads
+    batches = [workloads.small_items(71, [30, 7, 44]), workloads.small_items(72, [5, 61]),
+               workloads.small_items(73, [12, 3, 25, 9, 1]), workloads.small_items(74, [2])]
+    fresh = [_run(gpu_ctx, b) for b in batches]
+    for poison in ("1", None):
+        if poison:
+            monkeypatch.setenv("KOKORO_HIP_TEST_POISON", poison)
+        else:
+            monkeypatch.delenv("KOKORO_HIP_TEST_POISON", raising=False)
+        for i, (b, f) in enumerate(zip(batches, fresh)):
+            out = gpu_ctx.forward_decoder_batch(b)
+            for j, (x, y) in enumerate(zip(f, out)):
+                assert np.isfinite(y).all() and np.array_equal(x, y), f"poison {poison} batch {i} item {j}"
+    _print("  one-shot reuse: 4 batches x 2 passes bit-identical to fresh plans")
+
+
+def test_gap_mask_negative_control(gpu_ctx, oracle_model, monkeypatch):
+    """The reference proves its batch tests detect padding contamination by switching gap masking
+    off (KOKORO_BATCH_NEGCTL_NOMASK, src/gpu_batch.rs:62-66; tests/bf16x_regression.rs:47-55).  The
+    same hook here makes every convolution read an item's neighbours and gaps as its own rows; the
+    checks this suite relies on must then fail: the batch's audio changes, an item in the batch no
+    longer equals its run alone (with masking), and items fall below the oracle bar."""
+    from kokoro_hip import workloads
+    from oracle import oracle as O
+    items = workloads.small_items(75, [9, 14, 6])
+    masked = _run(gpu_ctx, items)
+    alone = _run(gpu_ctx, [items[1]])[0]
+    assert np.array_equal(alone, masked[1])
+    monkeypatch.setenv("KOKORO_BATCH_NEGCTL_NOMASK", "1")
+    unmasked = _run(gpu_ctx, items)
+    monkeypatch.delenv("KOKORO_BATCH_NEGCTL_NOMASK")
+    assert all(np.isfinite(u).all() for u in unmasked)
+    assert not np.array_equal(alone, unmasked[1])
+    failing = 0
+    for it, a, u in zip(items, masked, unmasked):
+        ref = O.synth_item(oracle_model, it)
+        ok_m = np.abs(a - ref).max() <= 2e-3 and snr_db(ref, a) >= 40.0
+        ok_u = np.abs(u - ref).max() <= 2e-3 and snr_db(ref, u) >= 40.0
+        _print(f"  N {it.n_frames}: masked snr {snr_db(ref, a):.1f} maxabs {np.abs(a - ref).max():.3g} | "
+               f"unmasked snr {snr_db(ref, u):.1f} maxabs {np.abs(u - ref).max():.3g}")
+        failing += not ok_u
+    assert failing >= 1

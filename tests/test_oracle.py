@@ -3,7 +3,7 @@
 Every oracle function is checked against something that does not share its code: published
 known-answer values (splitmix64), closed forms (durations, layout tables, Box-Muller, Snake),
 library routines (torch.nn.functional conv / instance_norm / interpolate, torch.stft / istft), and
-an independent float64 torch restatement of the whole decoder and generator (tests/torch_ref.py).
+an independent float64 torch restatement of the whole decoder and generator (oracle/torch_ref.py).
 Negative controls plant a mistake on the CPU and check that the comparison catches it.
 """
 import numpy as np
@@ -11,7 +11,7 @@ import pytest
 import torch
 import torch.nn.functional as F
 
-import torch_ref as R
+from oracle import torch_ref as R
 from conftest import snr_db
 from oracle import oracle as O
 
