@@ -138,6 +138,21 @@ int kk_plan_create_generator(kk_ctx* ctx, const kk_generator_item* items, int n,
  * columns (snake_b, src/gpu_batch.rs:140-154). */
 int kk_plan_create_snake(kk_ctx* ctx, const char* prefix, const float* const* x, const int64_t* t,
                          const float* const* ref_s, int n, int gap, kk_plan** out, char* err, size_t errlen);
+/* The Snake block of kk_plan_create_snake + kk_plan_run on caller device memory, allocating nothing.
+ * No counterpart in the reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  x: device pointer,
+ * time-major f32 [rows][C] (C = the block's channels), item b at rows [start[b], start[b] + len[b])
+ * (spans disjoint, any rows between them), updated in place; ref_s: n host pointers to 128+ style
+ * values.  Intermediates live in a fixed device scratch array of KK_NOALLOC_SCRATCH_BYTES per device
+ * (held from the library's first use on that device until the process ends); calls beyond
+ * KK_NOALLOC_MAX_ROWS rows or KK_NOALLOC_MAX_ITEMS items are refused with KK_ERR_INVALID.  Every
+ * call on one device shares that device's array: calls that overlap on one device race.  The call
+ * returns when x holds the result. */
+#define KK_NOALLOC_MAX_ROWS 65536
+#define KK_NOALLOC_MAX_ITEMS 64
+#define KK_NOALLOC_SCRATCH_BYTES (48u << 20)
+int kk_snake_block_noalloc(kk_ctx* ctx, const char* prefix, float* x, int64_t rows, const int64_t* start,
+                           const int64_t* len, int n, const float* const* ref_s, char* err, size_t errlen);
 /* Enqueue the plan's kernels; `until` = KK_STAGE_ALL or an earlier stage (for stage taps). */
 #define KK_STAGE_DECODER 1
 #define KK_STAGE_SOURCE 2

@@ -219,6 +219,8 @@ struct kk_ctx {
     // kk_forward_decoder_batch's plan, kept between calls: its device buffers are reused whenever
     // the next batch fits (released on any failure, so that a split batch can use the memory)
     kk_plan* oneshot = nullptr;
+    // device address of this device's copy of the no-allocation entry point's scratch array
+    unsigned char* scratch = nullptr;
 };
 
 namespace kk {
@@ -1551,6 +1553,32 @@ static void tap_rows(const void* dev, int64_t ld, int64_t r0, int64_t rows, int 
 
 using namespace kk;
 
+// ------------------------------------------------------------------ no-allocation entry point
+// kk_snake_block_noalloc's device scratch: one array per device, held from the first use of the
+// library on that device until the process ends.  Regions (bytes, 256-aligned):
+//   h        fp16 [rows][C]                          (the Snake steps' conv1 output)
+//   part     statistics partials                     (rows / 128 + 2 items + 2) x C records
+//   coef     two AdaIN coefficient sets              [items][C] each
+//   gb       style projections of every AdaIN        [items][style rows]
+//   tables   the call's layout, tile lists, styles   (one copy from the host)
+// Nothing in it must start at zero: every region is written by the call before it is read.
+namespace {
+constexpr size_t kNaRows = KK_NOALLOC_MAX_ROWS, kNaItems = KK_NOALLOC_MAX_ITEMS, kNaMaxC = 256;
+constexpr size_t na_align(size_t v) { return (v + 255) / 256 * 256; }
+constexpr size_t kNaH = 0;
+constexpr size_t kNaPart = kNaH + na_align(kNaRows * kNaMaxC * 2);
+constexpr size_t kNaPartBytes = na_align((kNaRows / 128 + 2 * kNaItems + 2) * kNaMaxC * sizeof(StatPart));
+constexpr size_t kNaCoef = kNaPart + kNaPartBytes;
+constexpr size_t kNaCoefBytes = na_align(kNaItems * kNaMaxC * sizeof(Coef));
+constexpr size_t kNaGb = kNaCoef + 2 * kNaCoefBytes;
+constexpr size_t kNaGbBytes = (size_t)12 << 20;  // items x style rows x 4 (37,396 rows for Kokoro-82M)
+constexpr size_t kNaTables = kNaGb + kNaGbBytes;
+constexpr size_t kNaTablesBytes = (size_t)1 << 20;
+constexpr size_t kNaTotal = kNaTables + kNaTablesBytes;
+static_assert(kNaTotal <= KK_NOALLOC_SCRATCH_BYTES, "scratch regions exceed the array");
+}  // namespace
+static __device__ __align__(256) unsigned char scratch[KK_NOALLOC_SCRATCH_BYTES];
+
 namespace kk {
 static void run_plan(kk_plan* plan, int until) {
     use_device(plan->ctx);
@@ -1573,6 +1601,76 @@ static void run_plan(kk_plan* plan, int until) {
 }
 
 
+// The Snake block on caller memory: a plan whose buffers are views of x and of the scratch regions;
+// its tables are staged in host heap memory and copied into the tables region (a pageable copy:
+// no pinned allocation).
+static void snake_block_noalloc(kk_ctx* ctx, const char* prefix, float* x, int64_t rows, const int64_t* start,
+                                const int64_t* len, int n, const float* const* ref_s) {
+    use_device(ctx);
+    check(ctx->model.ready, "no model uploaded");
+    check(ctx->scratch != nullptr, "context without scratch");
+    check(prefix && x && start && len && ref_s, "null argument");
+    const MSnake* blk = find_snake(ctx->model, prefix);
+    check(blk != nullptr, std::string("no Snake block named ") + prefix);
+    check(n >= 1 && n <= (int)kNaItems, "kk_snake_block_noalloc takes 1 to " + std::to_string(kNaItems) +
+                                            " items (" + std::to_string(n) + " given)");
+    check(rows >= 1 && rows <= (int64_t)kNaRows, "kk_snake_block_noalloc takes at most " +
+                                                     std::to_string(kNaRows) + " rows (" + std::to_string(rows) +
+                                                     " given)");
+    const int c = blk->c;
+    check((size_t)c <= kNaMaxC, "block wider than the scratch");
+    check((size_t)n * ctx->model.style_rows * sizeof(float) <= kNaGbBytes, "too many items for the style scratch");
+    // item spans: inside [0, rows), pairwise disjoint
+    std::vector<std::pair<int64_t, int64_t>> sp(n);
+    for (int b = 0; b < n; b++) {
+        check(ref_s[b] != nullptr, "item " + std::to_string(b) + ": null style");
+        check(start[b] >= 0 && len[b] >= 1 && start[b] + len[b] <= rows,
+              "item " + std::to_string(b) + ": span outside [0, rows)");
+        sp[b] = {start[b], len[b]};
+    }
+    std::sort(sp.begin(), sp.end());
+    for (int b = 1; b < n; b++) check(sp[b - 1].first + sp[b - 1].second <= sp[b].first, "overlapping item spans");
+
+    kk_plan p;
+    p.ctx = ctx;
+    reset_plan(&p, PLAN_SNAKE, n);
+    p.sblk = blk, p.sc = c;
+    for (int b = 0; b < n; b++) p.nfr.push_back(len[b]);
+    // host staging of the tables in heap memory, in place of the context's pinned buffer
+    Staging local;
+    local.pageable = true;
+    std::swap(local, ctx->stage);
+    struct Restore {
+        kk_ctx* ctx;
+        Staging* saved;
+        ~Restore() { std::swap(*saved, ctx->stage); }
+    } restore{ctx, &local};
+    stage_begin(ctx);
+    p.ds.build(ctx, rows, std::vector<int64_t>(start, start + n), std::vector<int64_t>(len, len + n), false,
+               p.nomask);
+    {
+        float* sth = stage<float>(ctx, p.style, (size_t)n * kStyleDim);
+        for (int b = 0; b < n; b++) std::memcpy(&sth[(size_t)b * kStyleDim], ref_s[b], sizeof(float) * kStyleDim);
+    }
+    unsigned char* base = ctx->scratch;
+    p.B[0].view(x, (size_t)rows * c * sizeof(float));
+    p.B[1].view(base + kNaH, (size_t)rows * c * 2);
+    p.part.view(base + kNaPart, kNaPartBytes);
+    p.part_bytes = (int64_t)kNaPartBytes;
+    for (int i = 0; i < 2; i++) p.coef[i].view(base + kNaCoef + i * kNaCoefBytes, (size_t)n * c * sizeof(Coef));
+    p.gb.view(base + kNaGb, (size_t)n * ctx->model.style_rows * sizeof(float));
+    prebuild_tiles(&p);  // tile lists staged, launches validated (partials bound included)
+    Staging& st = ctx->stage;
+    check(st.used <= kNaTablesBytes, "layout tables exceed the scratch");
+    hipStream_t s = ctx->stream;
+    KK_HIP(hipMemcpyAsync(base + kNaTables, st.host, st.used, hipMemcpyHostToDevice, s));
+    for (const auto& r : st.refs) r.buf->view(base + kNaTables + r.off, r.bytes);
+    st.refs.clear();
+    p.frozen = true;
+    run_plan(&p, KK_STAGE_ALL);
+    // x holds the result when the call returns (and the host tables outlive their copy)
+    KK_HIP(hipStreamSynchronize(s));
+}
 }  // namespace kk
 
 extern "C" {
@@ -1612,6 +1710,13 @@ int kk_open(int ordinal, kk_ctx** out, char* err, size_t errlen) {
             }
         for (int j = 0; j < 20; j++) win[j] = (float)(0.5 - 0.5 * std::cos(2.0 * M_PI * (double)j / 20.0));
         KK_HIP(upload_stft_tables(cs, sn, win));
+        // this device's copy of kk_snake_block_noalloc's scratch array: its device address, taken
+        // once per context with the device current (in host code the array's name is only a
+        // stand-in, not a device address)
+        void* sp = nullptr;
+        KK_HIP(hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch)));
+        check(sp != nullptr, "no device address for the scratch array");
+        ctx->scratch = (unsigned char*)sp;
         *out = ctx.release();
     });
 }
@@ -1674,6 +1779,12 @@ int kk_plan_create_generator(kk_ctx* ctx, const kk_generator_item* items, int n,
         use_device(ctx);
         *out = create_generator_plan(ctx, items, n);
     });
+}
+
+int kk_snake_block_noalloc(kk_ctx* ctx, const char* prefix, float* x, int64_t rows, const int64_t* start,
+                           const int64_t* len, int n, const float* const* ref_s, char* err, size_t errlen) {
+    if (!ctx) return KK_ERR_INVALID;
+    return guard(err, errlen, [&] { snake_block_noalloc(ctx, prefix, x, rows, start, len, n, ref_s); });
 }
 
 int kk_plan_create_snake(kk_ctx* ctx, const char* prefix, const float* const* x, const int64_t* t,

@@ -23,8 +23,10 @@ EXPORTS = [
     "kk_plan_sync", "kk_plan_fetch", "kk_plan_tap", "kk_plan_get_info", "kk_plan_free", "kk_set_profiling",
     "kk_profile_read", "kk_durations_from_logits", "kk_layout_frames", "kk_layout_col_item", "kk_layout_src_row",
     "kk_plan_fetch_pcm16", "kk_encode_pcm16", "kk_wav_header", "kk_host_alloc", "kk_host_free",
-    "kk_plan_item_samples", "kk_plan_fetch_pcm16_async", "kk_plan_fetch_wait",
+    "kk_plan_item_samples", "kk_plan_fetch_pcm16_async", "kk_plan_fetch_wait", "kk_snake_block_noalloc",
 ]
+NOALLOC_MAX_ROWS = 65536
+NOALLOC_MAX_ITEMS = 64
 
 
 class KKError(RuntimeError):
@@ -101,6 +103,7 @@ def lib():
         L.kk_plan_fetch_pcm16_async.argtypes = [vp, vp, vp, cp, sz]
         L.kk_plan_fetch_wait.argtypes = [vp, cp, sz]
         L.kk_wav_header.argtypes = [i32, C.c_uint32, C.c_uint64, vp, cp, sz]
+        L.kk_snake_block_noalloc.argtypes = [vp, cp, vp, i64, vp, vp, i32, C.POINTER(vp), cp, sz]
         L.kk_plan_get_info.argtypes = [vp, C.POINTER(PlanInfo)]
         L.kk_plan_free.argtypes = [vp]
         L.kk_plan_free.restype = None
@@ -249,6 +252,17 @@ class Context:
 
     def plan(self, items):
         return Plan.decoder(self, items)
+
+    def snake_block_noalloc(self, prefix, x_ptr, rows, starts, lens, ref_ss):
+        """kk_snake_block_noalloc: the Snake block in place on device memory at x_ptr (time-major f32
+        [rows][C]), items at rows [starts[b], starts[b] + lens[b]); allocates nothing."""
+        starts = np.ascontiguousarray(starts, np.int64)
+        lens = np.ascontiguousarray(lens, np.int64)
+        rss = [_f32(np.pad(np.asarray(r, np.float32), (0, max(0, 256 - len(r))))) for r in ref_ss]
+        rp = (C.c_void_p * len(rss))(*[r.ctypes.data for r in rss])
+        err = _err()
+        _check(lib().kk_snake_block_noalloc(self.h, prefix.encode(), C.c_void_p(x_ptr), int(rows), _p(starts),
+                                            _p(lens), len(lens), rp, err, len(err)), err)
 
     def prepare(self, items):
         """The items marshalled once into the ABI's structs, for repeated calls (timing)."""
