@@ -156,6 +156,7 @@ def main():
     ap.add_argument("--config", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-events", action="store_true", help="skip the per-launch profiling pass")
+    ap.add_argument("--layers", default="", help="write the profiling pass's per-launch table (JSON) here")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="first run one plain copy kernel over this many MiB (reference for PMC byte counters)")
     args = ap.parse_args()
@@ -234,6 +235,16 @@ def main():
         for _ in range(args.steps):
             plan.run()
         plan.sync()
+        if args.layers:
+            per = {}
+            for name, cls, lms, fl, by in ctx.profile_launches():
+                e = per.setdefault(name, {"cls": cls, "launches": 0, "ms": 0.0, "flop": 0.0, "bytes": 0.0})
+                e["launches"] += 1
+                e["ms"] += lms
+                e["flop"] += fl
+                e["bytes"] += by
+            with open(args.layers, "w") as f:
+                json.dump({"steps": args.steps, "workload": wl, "layers": per}, f, indent=1)
         prof = ctx.profile_read()
         ctx.set_profiling(False)
     spec0 = plan.tap("spec", 0, (22, 120 * items[0].n_frames + 1))

@@ -232,6 +232,17 @@ typedef struct {
     double bytes;
 } kk_profile_entry;
 int kk_profile_read(kk_ctx* ctx, kk_profile_entry* out, int max, int* n_out, char* err, size_t errlen);
+/* The launches recorded since the last kk_profile_read, one record each in launch order (the first
+ * `max`; *n_out = how many were recorded), without clearing them: the layer's state-dict prefix and
+ * step (e.g. "resblocks.3.d1.conv1"), or the kernel class for the other kernels. */
+typedef struct {
+    char name[48];
+    char cls[32];
+    double ms;
+    double flop;
+    double bytes;
+} kk_launch_record;
+int kk_profile_launches(kk_ctx* ctx, kk_launch_record* out, int max, int* n_out, char* err, size_t errlen);
 
 /* ------------------------------------------------------------------ host rules (bit-exact)
  * durations_from_logits (src/model.rs:90-99): d_i = max(1, round_half_even(sum_j sigmoid(l_ij) /

@@ -131,12 +131,14 @@ struct MAdain {
     int c = 0, gb_off = 0;
 };
 struct MSnake {
+    std::string name;  // state-dict prefix after "decoder.generator."
     MConv c1[3], c2[3];
     MAdain a1[3], a2[3];
     DevBuf ar1[3], ai1[3], ar2[3], ai2[3];
     int c = 0;
 };
 struct MResblk {
+    std::string name;  // state-dict prefix after "decoder."
     MConv conv1, conv2, conv1x1;
     bool has1x1 = false, up = false;
     MAdain n1, n2;
@@ -168,6 +170,7 @@ struct ProfRec {
     int cls;
     double flop, bytes;
     hipEvent_t e0, e1;
+    std::string label;  // the layer (state-dict prefix and step) or the kernel class
 };
 // Kernel classes of the per-launch profile: the MFMA convolutions (by role), then the bandwidth
 // and glue kernels.
@@ -310,6 +313,7 @@ static void load_adain(MAdain& a, const Table& t, const std::string& p, int c, S
 static void load_snake(MSnake& s, const Table& t, const std::string& p, int c, int k, StyleRows& sr) {
     static const int dil[3] = {1, 3, 5};
     s.c = c;
+    s.name = p.substr(p.find("generator.") == std::string::npos ? 0 : p.find("generator.") + 10);
     const int shape = c >= 256 ? SHAPE_256x128 : SHAPE_128x256;
     for (int i = 0; i < 3; i++) {
         const std::string si = std::to_string(i);
@@ -335,6 +339,7 @@ static void load_snake(MSnake& s, const Table& t, const std::string& p, int c, i
 static void load_resblk(MResblk& r, const Table& t, const std::string& p, int din, int dout, bool up,
                         StyleRows& sr) {
     r.din = din, r.dout = dout, r.up = up;
+    r.name = p.substr(p.find("decoder.") == std::string::npos ? 0 : 8);
     load_conv(r.conv1, t, p + ".conv1", din, dout, 3, 1, 1, true, SHAPE_256x128);
     load_conv(r.conv2, t, p + ".conv2", dout, dout, 3, 1, 1, true, SHAPE_256x128);
     load_adain(r.n1, t, p + ".norm1", din, sr);
@@ -1018,9 +1023,12 @@ struct Runner {
     // One kernel launch (nothing in the dry run): counted and, with profiling on, bracketed by an
     // event pair on the launch stream and recorded under class `cls` with its algorithmic FLOP and
     // bytes (valid rows only: the data the step must read and write once).
+    std::string label;  // the next launch's profile label (default: its class)
     template <class F>
     void launch(int cls, double f, double bytes, F&& fn) {
         launches++;
+        std::string lb = label.empty() ? std::string(kProfNames[cls]) : label;
+        label.clear();
         if (dry) return;
         hipEvent_t e0 = nullptr, e1 = nullptr;
         if (ctx->profiling) {
@@ -1030,7 +1038,7 @@ struct Runner {
         KK_HIP(fn());
         if (ctx->profiling) {
             KK_HIP(hipEventRecord(e1, s));
-            ctx->prof.push_back(ProfRec{cls, f, bytes, e0, e1});
+            ctx->prof.push_back(ProfRec{cls, f, bytes, e0, e1, std::move(lb)});
         }
     }
     int64_t frames() const { return p->dn.valid(); }
@@ -1079,6 +1087,7 @@ struct Runner {
         float scale = 1.f;
         bool stats = false;
         int cls = PC_DECODER;
+        std::string label;  // profile label
         bool convt = false;
         int stride = 1, pad_t = 0;
         bool in_h = false, out_h = false;  // fp16 input / output (the Snake steps' h)
@@ -1127,6 +1136,7 @@ struct Runner {
             if (launch_conv(q, o.pro, o.epi, c.shape, o.stats, o.in_h, o.out_h, ctx->n_cu, s, true) != hipSuccess)
                 fail(KK_ERR_INVALID, "convolution parameters out of the kernel's range (batch too large?)");
         }
+        label = o.label;
         launch(o.cls, f, bytes,
                [&] { return launch_conv(q, o.pro, o.epi, c.shape, o.stats, o.in_h, o.out_h, ctx->n_cu, s); });
         return t;
@@ -1137,6 +1147,7 @@ struct Runner {
         Op o;
         o.pro = PRO_ADAIN_SNAKE, o.epi = epi, o.x = x, o.x_ld = blk.c, o.din = o.dout = &d, o.y = y;
         o.y_ld = blk.c, o.coef = coef, o.stats = stats, o.cls = PC_SNAKE;
+        o.label = blk.name + ".d" + std::to_string(2 * i + 1) + (second ? ".conv2" : ".conv1");
         o.ar = second ? &blk.ar2[i] : &blk.ar1[i];
         o.ai = second ? &blk.ai2[i] : &blk.ai1[i];
         // conv1 writes h in fp16, conv2 reads it
@@ -1241,14 +1252,17 @@ struct Runner {
         Op o1;
         o1.pro = PRO_ADAIN_LEAKY, o1.x = in, o1.x_ld = in_ld, o1.din = o1.dout = &d, o1.y = h, o1.y_ld = r.dout;
         o1.coef = cf(0), o1.slope = 0.2f, o1.stats = true;
+        o1.label = r.name + ".conv1";
         const Tiles& t = conv(r.conv1, o1);
         fin(t, kShapeWN[r.conv1.shape], r.dout, r.n2, cf(1));
         Op os;
         os.x = in, os.x_ld = in_ld, os.din = os.dout = &d, os.y = out, os.y_ld = out_ld;
+        os.label = r.name + ".conv1x1";
         conv(r.conv1x1, os);
         Op o2;
         o2.pro = PRO_ADAIN_LEAKY, o2.epi = EPI_RESID, o2.x = h, o2.x_ld = r.dout, o2.din = o2.dout = &d;
         o2.y = out, o2.y_ld = out_ld, o2.coef = cf(1), o2.slope = 0.2f, o2.scale = 1.0f / sqrtf(2.0f);
+        o2.label = r.name + ".conv2";
         conv(r.conv2, o2);
     }
 
@@ -1273,6 +1287,7 @@ struct Runner {
         // asr_res (512 -> 64, k1) into channels [1024, 1088); F0n, Nn into 1088, 1089
         Op oa;
         oa.x = xcat, oa.x_ld = kXcatLd, oa.din = oa.dout = &dn, oa.y = xa + 1024, oa.y_ld = kXinLd;
+        oa.label = "asr_res";
         conv(m.asr_res, oa);
         launch(PC_COPY, 0, nf * 2 * 8, [&] { return launch_copy_cols(xcat + 512, kXcatLd, 2, xa, kXinLd, 1088, col, ln, s); });
         launch(PC_COPY, 0, nf * 66 * 8, [&] { return launch_copy_cols(xa + 1024, kXinLd, 66, xb, kXinLd, 1024, col, ln, s); });
@@ -1290,16 +1305,19 @@ struct Runner {
         Op o1;
         o1.pro = PRO_BF16, o1.x = p->pool.p, o1.x_ld = kXinLd, o1.din = o1.dout = &d2, o1.y = h, o1.y_ld = 512;
         o1.stats = true;
+        o1.label = r.name + ".conv1";
         const Tiles& t = conv(r.conv1, o1);
         fin(t, kShapeWN[r.conv1.shape], 512, r.n2, cf(1));
         // shortcut conv1x1(nearest x2 (x)) = nearest x2 (conv1x1(x)) for a 1x1 conv: computed at N
         Op os;
         os.x = xb, os.x_ld = kXinLd, os.din = os.dout = &dn, os.y = p->sc_half.as<float>(), os.y_ld = 512;
+        os.label = r.name + ".conv1x1";
         conv(r.conv1x1, os);
         Op o2;
         o2.pro = PRO_ADAIN_LEAKY, o2.epi = EPI_RESID_UP2, o2.x = h, o2.x_ld = 512, o2.din = o2.dout = &d2;
         o2.y = p->dec_out.as<float>(), o2.y_ld = 512, o2.coef = cf(1), o2.slope = 0.2f;
         o2.r0 = p->sc_half.as<float>(), o2.r0_ld = 512, o2.scale = 1.0f / sqrtf(2.0f);
+        o2.label = r.name + ".conv2";
         conv(r.conv2, o2);
     }
 
@@ -1357,6 +1375,7 @@ struct Runner {
         ou.din = &din, ou.dout = &dout, ou.y = B[3], ou.y_ld = c, ou.r0 = p->xs[i].as<float>(), ou.r0_ld = c;
         ou.convt = true, ou.stride = m.ups_stride[i], ou.pad_t = m.ups_pad[i], ou.cls = PC_CONVT;
         ou.stats = true;  // partials of y per (tile, phase, wave column) for the resblocks' first AdaIN
+        ou.label = "ups." + std::to_string(i);
         const Tiles& tu = conv(m.ups[i], ou);
         float* X[3] = {B[4], B[5], B[0]};
         // h of the three blocks: the two halves of B[2] (an fp16 [rows][c] fits in half of a buffer
@@ -1370,6 +1389,7 @@ struct Runner {
         Op o;
         o.pro = PRO_LEAKY, o.slope = 0.01f, o.x = p->B[0].p, o.x_ld = 128, o.din = o.dout = &d;
         o.y = p->post.as<float>(), o.y_ld = kPostLd, o.cls = PC_POST;
+        o.label = "conv_post";
         conv(m.post, o);
     }
 
@@ -2154,6 +2174,28 @@ int kk_profile_read(kk_ctx* ctx, kk_profile_entry* out, int max, int* n_out, cha
         int k = 0;
         for (int i = 0; i < PC_COUNT && k < max; i++)
             if (acc[i].launches > 0) out[k++] = acc[i];
+        *n_out = k;
+    });
+}
+
+int kk_profile_launches(kk_ctx* ctx, kk_launch_record* out, int max, int* n_out, char* err, size_t errlen) {
+    if (!ctx || (!out && max > 0) || !n_out) return KK_ERR_INVALID;
+    return guard(err, errlen, [&] {
+        use_device(ctx);
+        KK_HIP(hipStreamSynchronize(ctx->stream));
+        int k = 0;
+        for (auto& r : ctx->prof) {
+            if (k < max) {
+                kk_launch_record& o = out[k];
+                std::memset(&o, 0, sizeof(o));
+                std::snprintf(o.name, sizeof(o.name), "%s", r.label.c_str());
+                std::snprintf(o.cls, sizeof(o.cls), "%s", kProfNames[r.cls]);
+                float ms = 0.f;
+                KK_HIP(hipEventElapsedTime(&ms, r.e0, r.e1));
+                o.ms = ms, o.flop = r.flop, o.bytes = r.bytes;
+            }
+            k++;
+        }
         *n_out = k;
     });
 }

@@ -23,7 +23,7 @@ EXPORTS = [
     "kk_plan_sync", "kk_plan_fetch", "kk_plan_tap", "kk_plan_get_info", "kk_plan_free", "kk_set_profiling",
     "kk_profile_read", "kk_durations_from_logits", "kk_layout_frames", "kk_layout_col_item", "kk_layout_src_row",
     "kk_plan_fetch_pcm16", "kk_encode_pcm16", "kk_wav_header", "kk_host_alloc", "kk_host_free",
-    "kk_plan_item_samples", "kk_plan_fetch_pcm16_async", "kk_plan_fetch_wait", "kk_snake_block_noalloc",
+    "kk_plan_item_samples", "kk_plan_fetch_pcm16_async", "kk_plan_fetch_wait", "kk_snake_block_noalloc", "kk_profile_launches",
 ]
 NOALLOC_MAX_ROWS = 65536
 NOALLOC_MAX_ITEMS = 64
@@ -59,6 +59,11 @@ class PlanInfo(C.Structure):
     _fields_ = [("n_items", C.c_int64), ("ln", C.c_int64), ("frames", C.c_int64), ("samples", C.c_int64),
                 ("conv_flop", C.c_double), ("snake_flop", C.c_double), ("device_bytes", C.c_int64),
                 ("launches", C.c_int64)]
+
+
+class LaunchRecord(C.Structure):
+    _fields_ = [("name", C.c_char * 48), ("cls", C.c_char * 32), ("ms", C.c_double), ("flop", C.c_double),
+                ("bytes", C.c_double)]
 
 
 class ProfileEntry(C.Structure):
@@ -109,6 +114,7 @@ def lib():
         L.kk_plan_free.restype = None
         L.kk_set_profiling.argtypes = [vp, i32]
         L.kk_profile_read.argtypes = [vp, C.POINTER(ProfileEntry), i32, C.POINTER(C.c_int), cp, sz]
+        L.kk_profile_launches.argtypes = [vp, C.POINTER(LaunchRecord), i32, C.POINTER(C.c_int), cp, sz]
         L.kk_durations_from_logits.argtypes = [vp, i32, C.c_float, vp]
         L.kk_layout_frames.argtypes = [vp, i32, vp]
         L.kk_layout_frames.restype = i64
@@ -229,6 +235,15 @@ class Context:
 
     def set_profiling(self, on):
         lib().kk_set_profiling(self.h, int(bool(on)))
+
+    def profile_launches(self):
+        """Per-launch records since the last profile_read: [(name, class, ms, flop, bytes)]."""
+        n = C.c_int()
+        err = _err()
+        _check(lib().kk_profile_launches(self.h, None, 0, C.byref(n), err, len(err)), err)
+        recs = (LaunchRecord * max(1, n.value))()
+        _check(lib().kk_profile_launches(self.h, recs, n.value, C.byref(n), err, len(err)), err)
+        return [(r.name.decode(), r.cls.decode(), r.ms, r.flop, r.bytes) for r in recs[: n.value]]
 
     def profile_read(self):
         ents = (ProfileEntry * 32)()

@@ -1,8 +1,12 @@
 """Summaries of rocprofv3 output for bench.py runs of the config-3 workload.
 
-    python -m kokoro_hip.profsum stats <trace_dir>
-        per-kernel table from a `rocprofv3 --kernel-trace` CSV run, plus the per-layer breakdown of
-        the 48 Snake-block convolutions of one step (algorithmic TFLOP/s and GB/s per layer)
+    python -m kokoro_hip.profsum stats <trace_dir> <steps>
+        per-kernel table from a `rocprofv3 --kernel-trace` CSV run of bench.py, plus the average
+        Snake-block conv duration of its profiling pass (the last <steps> steps)
+    python -m kokoro_hip.profsum layers <layers.json>
+        per-layer table of bench.py's profiling pass (`--layers`): every kernel alone on the stream,
+        HIP events around each launch; time per launch, algorithmic TFLOP/s and GB/s, and the
+        fraction of the launch's roofline floor max(FLOP / 2.5 PFLOP/s, bytes / 8 TB/s)
     python -m kokoro_hip.profsum traffic <fetch_dir> <write_dir> <M>
         HBM bytes per Snake-conv launch from a `--pmc FETCH_SIZE` and a `--pmc WRITE_SIZE` run of
         `bench.py --calibrate-copy-mib M`, each scaled by what the same counter reads for the plain
@@ -56,7 +60,9 @@ def _short(name):
     return m.group(1) if m else name[:48]
 
 
-def stats(trace_dir):
+def stats(trace_dir, steps):
+    """Per-kernel table of the whole trace, and the Snake-block convs of bench.py's profiling pass (its
+    last `steps` steps, where every kernel runs alone on the stream): average duration per launch."""
     rows = _rows(os.path.join(trace_dir, "run_kernel_trace.csv"))
     rows.sort(key=lambda r: int(r["Start_Timestamp"]))
     dur = lambda r: (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
@@ -69,19 +75,46 @@ def stats(trace_dir):
         lines.append(f"| `{k}` | {len(v)} | {sum(v) / 1e3:.2f} | {sum(v) / len(v):.1f} | {100 * sum(v) / total:.2f} |")
     layers, frames = snake_layers()
     sn = [r for r in rows if SNAKE.search(r["Kernel_Name"])]
-    n_steps = len(sn) // len(layers)
-    lines += ["", f"Snake-block convs, per layer (config 3: {frames} frames; average over {n_steps} steps):", "",
-              "| layer | avg us | TFLOP/s | GB/s (algorithmic) |", "|---|---:|---:|---:|"]
-    acc = [[] for _ in layers]
-    for i, r in enumerate(sn[: n_steps * len(layers)]):
-        acc[i % len(layers)].append(dur(r))
-    tot = 0.0
-    for lay, v in zip(layers, acc):
-        us = sum(v) / len(v)
-        tot += us
-        lines.append(f"| {lay['name']} | {us:.1f} | {lay['flop'] / us / 1e6:.1f} | {lay['bytes'] / us / 1e3:.1f} |")
-    fl = sum(l["flop"] for l in layers)
-    lines.append(f"| **all 48** | {tot:.1f} | {fl / tot / 1e6:.1f} | |")
+    last = sn[-steps * len(layers):]
+    avg = sum(dur(r) for r in last) / len(last)
+    fl = sum(l["flop"] for l in layers) / len(layers)
+    lines += ["", f"Snake-block convs of the profiling pass (the trace's last {steps} steps, {len(last)} dispatches, "
+                  f"each alone on the stream): **{avg:.1f} us** per launch on average, "
+                  f"{fl / avg / 1e6:.1f} TFLOP/s algorithmic ({100 * fl / avg / 1e6 / 2500:.1f}% of 2.5 PFLOP/s); "
+                  f"all {len(sn)} Snake dispatches of the trace (the timed steps overlap three chains) "
+                  f"average {sum(dur(r) for r in sn) / len(sn):.1f} us."]
+    return "\n".join(lines)
+
+
+PEAK_FLOPS, PEAK_BYTES = 2.5e15, 8e12
+
+
+def layers_table(path):
+    with open(path) as f:
+        d = json.load(f)
+    k = d["steps"]
+    lines = [f"Per-launch profile, {d['workload']} ({k} steps; each kernel alone on the stream):", "",
+             "| layer | class | launches/step | us per launch | TFLOP/s | GB/s | floor us | frac of floor |",
+             "|---|---|---:|---:|---:|---:|---:|---:|"]
+    tot = {}
+    for name, e in d["layers"].items():
+        n = e["launches"]
+        us = e["ms"] * 1e3 / n
+        fl, by = e["flop"] / n, e["bytes"] / n
+        floor = max(fl / PEAK_FLOPS, by / PEAK_BYTES) * 1e6
+        t = tot.setdefault(e["cls"], [0.0, 0.0, 0.0, 0.0])
+        t[0] += e["ms"] / k
+        t[1] += e["flop"] / k
+        t[2] += e["bytes"] / k
+        t[3] += floor * n / k / 1e3
+        lines.append(f"| {name} | {e['cls']} | {n // k} | {us:.1f} | {fl / max(us, 1e-9) / 1e6:.1f} | "
+                     f"{by / max(us, 1e-9) / 1e3:.1f} | {floor:.1f} | {floor / max(us, 1e-9):.3f} |")
+    lines += ["", "| class | ms per step | TFLOP/s | GB/s | floor ms | frac of floor |", "|---|---:|---:|---:|---:|---:|"]
+    for c, (ms, fl, by, floor) in sorted(tot.items(), key=lambda kv: -kv[1][0]):
+        lines.append(f"| {c} | {ms:.3f} | {fl / ms / 1e9:.1f} | {by / ms / 1e6:.1f} | {floor:.3f} | "
+                     f"{floor / ms:.3f} |")
+    all_ms = sum(v[0] for v in tot.values())
+    lines.append(f"| **all** | {all_ms:.3f} | | | {sum(v[3] for v in tot.values()):.3f} | |")
     return "\n".join(lines)
 
 
@@ -116,7 +149,9 @@ def traffic(fetch_dir, write_dir, mib):
 if __name__ == "__main__":
     sys.path.insert(0, os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
     if sys.argv[1] == "stats":
-        print(stats(sys.argv[2]))
+        print(stats(sys.argv[2], int(sys.argv[3])))
+    elif sys.argv[1] == "layers":
+        print(layers_table(sys.argv[2]))
     elif sys.argv[1] == "traffic":
         print(json.dumps(traffic(sys.argv[2], sys.argv[3], float(sys.argv[4])), indent=1))
     else:
