@@ -6,6 +6,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <chrono>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -694,7 +695,7 @@ static void build_frame_layout(kk_plan* p) {
     p->dn.build(ctx, ln, scale(1), lens(1, 0), true, w);
     p->d2.build(ctx, 2 * ln, scale(2), lens(2, 0), true, w);
     p->d20.build(ctx, 20 * ln, scale(20), lens(20, 0), false, w);
-    p->d120.build(ctx, 120 * ln + 1, scale(120), lens(120, 1), true, w);
+    p->d120.build(ctx, 120 * ln + 1, scale(120), lens(120, 1), false, w);
 }
 
 struct NoiseIn {
@@ -1354,7 +1355,8 @@ struct Runner {
         // reads the spectrum's valid rows once (22 f32), writes cout f32 per output row
         const double bytes = (double)p->d120.valid() * 88 + (double)dout.valid() * c * 4;
         launch(i == 0 ? PC_NOISE0 : PC_NOISE1, 2.0 * 22 * nc.k * c * (double)dout.valid(), bytes, [&] {
-            return launch_noise_conv(p->spec.as<float>(), kSpecLd, p->d120.l, p->d120.col_d.as<int32_t>(),
+            return launch_noise_conv(p->spec.as<float>(), kSpecLd, p->d120.l, p->d120.start_d.as<int64_t>(),
+                                     p->d120.len_d.as<int64_t>(),
                                      nc.w.as<float>(), nc.wp.p ? nc.wp.as<float>() : nullptr, nc.b.as<float>(), nc.cout,
                                      nc.k, nc.stride, nc.pad, xs, c, tn.dev(), part(), s);
         });
@@ -2121,9 +2123,23 @@ int kk_forward_decoder_batch(kk_ctx* ctx, const kk_decoder_item* items, int n, k
             ctx->oneshot->ctx = ctx;
         }
         try {
+            // KOKORO_HIP_TIMING=1: host-side phase times of this call on stderr (diagnostics)
+            static const bool timing = env_i64("KOKORO_HIP_TIMING", 0) != 0;
+            const auto t0 = std::chrono::steady_clock::now();
             init_decoder_plan(ctx->oneshot, items, n);
+            const auto t1 = std::chrono::steady_clock::now();
             run_plan(ctx->oneshot, KK_STAGE_ALL);
+            const auto t2 = std::chrono::steady_clock::now();
+            if (timing) KK_HIP(hipStreamSynchronize(ctx->stream));
+            const auto t3 = std::chrono::steady_clock::now();
             fetch_plan(ctx->oneshot, out);
+            const auto t4 = std::chrono::steady_clock::now();
+            if (timing) {
+                auto ms = [](auto a, auto b) { return std::chrono::duration<double, std::milli>(b - a).count(); };
+                std::fprintf(stderr, "kk_forward_decoder_batch: plan %.3f ms (staged %.2f MB), enqueue %.3f ms, "
+                             "device %.3f ms, fetch %.3f ms\n", ms(t0, t1), ctx->stage.used / 1e6, ms(t1, t2),
+                             ms(t2, t3), ms(t3, t4));
+            }
         } catch (...) {
             // a failure (device memory exhausted above all) releases the cached buffers, so that a
             // caller splitting the batch (src/engine.rs:229-234) has the whole device again

@@ -115,13 +115,15 @@ hipError_t launch_copy_cols(const float* src, int64_t src_ld, int c, float* dst,
 hipError_t launch_adain_pool(const float* x, int64_t ld, int c, const Coef* coef, const int32_t* col_n,
                              int64_t ln, const float* pw, const float* pb, const int32_t* col_2, uint16_t* out,
                              int64_t out_ld, hipStream_t s);
-// Strided f32 conv 22 -> cout (noise_convs.0: k12 s6 p3; noise_convs.1: k1) on the masked spectrum,
+// Strided f32 conv 22 -> cout (noise_convs.0: k12 s6 p3; noise_convs.1: k1) on the spectrum, rows
+// outside the tile's item span [in_start, in_start + in_len) read as 0 (the reference's gap mask),
 // over item-aligned tiles t (<= kNoiseTile output rows each; rows outside the tiles are not
 // written), with the statistics partial of each tile ([tile][cout], shift = bias) for the next
 // layer's AdaIN.  wt: [k][22][cout] f32 (VALU kernel); wp: the noise_convs.0 weights packed for
 // the f32 matrix cores ([32-row tile][2][32][12 taps][12] f32), or null.
 constexpr int kNoiseTile = 64;
-hipError_t launch_noise_conv(const float* spec, int64_t spec_ld, int64_t l_in, const int32_t* col_in,
+hipError_t launch_noise_conv(const float* spec, int64_t spec_ld, int64_t l_in, const int64_t* in_start,
+                             const int64_t* in_len,
                              const float* wt, const float* wp, const float* b, int cout, int k, int stride, int pad,
                              float* y, int64_t y_ld, TilesDev t, StatPart* part, hipStream_t s);
 // SineGen phase_pre: per item and harmonic, f64 cumulative sum of the 1/300-downsampled rad values.

@@ -246,7 +246,8 @@ constexpr int kNcRows = kNoiseTile;
 constexpr int kNcMaxWin = (kNcRows - 1) * 6 + 12;
 template <int COUT, int TT, int WIN>
 __global__ __launch_bounds__(256) void noise_conv_kernel(const float* __restrict__ spec, int64_t spec_ld, int64_t l_in,
-                                                         const int32_t* __restrict__ col_in,
+                                                         const int64_t* __restrict__ in_start,
+                                                         const int64_t* __restrict__ in_len,
                                                          const float* __restrict__ wt, const float* __restrict__ b,
                                                          int k, int stride, int pad, float* __restrict__ y,
                                                          int64_t y_ld, TilesDev tl, StatPart* __restrict__ part) {
@@ -258,20 +259,21 @@ __global__ __launch_bounds__(256) void noise_conv_kernel(const float* __restrict
     const int nv = tl.n[blockIdx.x];
     const int win = (kNcRows - 1) * stride + k;
     const int64_t in0 = t0 * stride - pad;
+    // the tile's item: input rows outside its span are the zero padding (gap masking)
+    const int item = tl.item[blockIdx.x];
+    const int64_t i_lo = in_start[item], i_hi = i_lo + in_len[item];
     // Stage the input window: every load of a thread is issued before the first is used (rows
     // clamped into the buffer, the gap / range mask applied afterwards), so the window costs one
     // memory latency rather than one per element.
     constexpr int kPer = (WIN * 22 + 255) / 256;
     {
         float sv[kPer];
-        int cv[kPer];
 #pragma unroll
         for (int kk = 0; kk < kPer; kk++) {
             if (kk * 256 >= win * 22) break;  // uniform
             const int i = threadIdx.x + kk * 256;
             const int r = i / 22, ci = i - r * 22;
-            const int64_t row = min(max(in0 + r, (int64_t)0), l_in - 1);
-            cv[kk] = col_in[row];
+            const int64_t row = min(max(in0 + r, i_lo), i_hi - 1);
             sv[kk] = spec[row * spec_ld + ci];
         }
 #pragma unroll
@@ -280,7 +282,7 @@ __global__ __launch_bounds__(256) void noise_conv_kernel(const float* __restrict
             const int i = threadIdx.x + kk * 256;
             const int r = i / 22, ci = i - r * 22;
             const int64_t row = in0 + r;
-            if (i < win * 22) xs[r][ci] = (row >= 0 && row < l_in && cv[kk] >= 0) ? sv[kk] : 0.f;
+            if (i < win * 22) xs[r][ci] = (row >= i_lo && row < i_hi) ? sv[kk] : 0.f;
         }
     }
     __syncthreads();
@@ -340,7 +342,8 @@ __global__ __launch_bounds__(256) void noise_conv_kernel(const float* __restrict
 constexpr int kNc0Win = (kNcRows - 1) * 6 + 12;  // 390 input rows per 64 output columns
 constexpr int kNc0Ld = kNc0Win + 2;               // channel-major window row stride (floats)
 __global__ __launch_bounds__(256, 4) void noise_conv0_mfma_kernel(const float* __restrict__ spec, int64_t spec_ld,
-                                                               int64_t l_in, const int32_t* __restrict__ col_in,
+                                                               int64_t l_in, const int64_t* __restrict__ in_start,
+                                                               const int64_t* __restrict__ in_len,
                                                                const float4* __restrict__ wp, const float* __restrict__ b,
                                                                int pad, float* __restrict__ y, int64_t y_ld,
                                                                TilesDev tl, StatPart* __restrict__ part) {
@@ -349,19 +352,20 @@ __global__ __launch_bounds__(256, 4) void noise_conv0_mfma_kernel(const float* _
     const int64_t t0 = tl.t0[blockIdx.x];
     const int nv = tl.n[blockIdx.x];
     const int64_t in0 = t0 * 6 - pad;
+    // the tile's item: input rows outside its span are the zero padding (gap masking)
+    const int item = tl.item[blockIdx.x];
+    const int64_t i_lo = in_start[item], i_hi = i_lo + in_len[item];
     // the window in batches of 12 loads per thread, each batch in flight before its first use (rows
     // clamped, the gap / range mask applied afterwards)
     constexpr int kPer = (kNc0Win * 22 + 255) / 256, kBatch = 12;
 #pragma unroll 1
     for (int k0 = 0; k0 < kPer; k0 += kBatch) {
         float sv[kBatch];
-        int cv[kBatch];
 #pragma unroll
         for (int kk = 0; kk < kBatch; kk++) {
             const int i = min((int)threadIdx.x + (k0 + kk) * 256, kNc0Win * 22 - 1);
             const int r = i / 22, ci = i - r * 22;
-            const int64_t row = min(max(in0 + r, (int64_t)0), l_in - 1);
-            cv[kk] = col_in[row];
+            const int64_t row = min(max(in0 + r, i_lo), i_hi - 1);
             sv[kk] = spec[row * spec_ld + ci];
         }
 #pragma unroll
@@ -370,7 +374,7 @@ __global__ __launch_bounds__(256, 4) void noise_conv0_mfma_kernel(const float* _
             if (i < kNc0Win * 22) {
                 const int r = i / 22, ci = i - r * 22;
                 const int64_t row = in0 + r;
-                xs[ci * kNc0Ld + r] = (row >= 0 && row < l_in && cv[kk] >= 0) ? sv[kk] : 0.f;
+                xs[ci * kNc0Ld + r] = (row >= i_lo && row < i_hi) ? sv[kk] : 0.f;
             }
         }
     }
@@ -815,7 +819,8 @@ hipError_t launch_adain_pool(const float* x, int64_t ld, int c, const Coef* coef
     return hipGetLastError();
 }
 
-hipError_t launch_noise_conv(const float* spec, int64_t spec_ld, int64_t l_in, const int32_t* col_in, const float* wt,
+hipError_t launch_noise_conv(const float* spec, int64_t spec_ld, int64_t l_in, const int64_t* in_start,
+                             const int64_t* in_len, const float* wt,
                              const float* wp, const float* b, int cout, int k, int stride, int pad, float* y,
                              int64_t y_ld, TilesDev t, StatPart* part, hipStream_t s) {
     const int win = (kNcRows - 1) * stride + k;
@@ -825,20 +830,20 @@ hipError_t launch_noise_conv(const float* spec, int64_t spec_ld, int64_t l_in, c
     if (wp) {
         // the matrix-core path: noise_convs.0's shape only, weights packed by pack_noise_conv0
         if (cout != 256 || k != 12 || stride != 6) return hipErrorInvalidValue;
-        hipLaunchKernelGGL(noise_conv0_mfma_kernel, grid, dim3(256), 0, s, spec, spec_ld, l_in, col_in,
+        hipLaunchKernelGGL(noise_conv0_mfma_kernel, grid, dim3(256), 0, s, spec, spec_ld, l_in, in_start, in_len,
                            (const float4*)wp, b, pad, y, y_ld, t, part);
         return hipGetLastError();
     }
     // noise_convs.0 (k 12, stride 6) stages a 390-row window; noise_convs.1 (k 1) 64 rows, small
     // enough for 16 blocks per CU
     if (cout == 256)
-        hipLaunchKernelGGL((noise_conv_kernel<256, 16, kNcMaxWin>), grid, dim3(256), 0, s, spec, spec_ld, l_in, col_in,
+        hipLaunchKernelGGL((noise_conv_kernel<256, 16, kNcMaxWin>), grid, dim3(256), 0, s, spec, spec_ld, l_in, in_start, in_len,
                            wt, b, k, stride, pad, y, y_ld, t, part);
     else if (cout == 128 && win <= kNcRows)
-        hipLaunchKernelGGL((noise_conv_kernel<128, 8, kNcRows>), grid, dim3(256), 0, s, spec, spec_ld, l_in, col_in, wt,
+        hipLaunchKernelGGL((noise_conv_kernel<128, 8, kNcRows>), grid, dim3(256), 0, s, spec, spec_ld, l_in, in_start, in_len, wt,
                            b, k, stride, pad, y, y_ld, t, part);
     else if (cout == 128)
-        hipLaunchKernelGGL((noise_conv_kernel<128, 8, kNcMaxWin>), grid, dim3(256), 0, s, spec, spec_ld, l_in, col_in,
+        hipLaunchKernelGGL((noise_conv_kernel<128, 8, kNcMaxWin>), grid, dim3(256), 0, s, spec, spec_ld, l_in, in_start, in_len,
                            wt, b, k, stride, pad, y, y_ld, t, part);
     else
         return hipErrorInvalidValue;

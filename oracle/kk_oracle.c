@@ -24,9 +24,17 @@
 
 static int g_bf16 = 0;      /* operand format: 0 off, 1 bf16, 2 fp16 */
 static int g_groups = 0xff; /* layer groups the emulation applies to (KO_GROUP_*) */
-void ko_set_bf16_emulation(int on) { g_bf16 = on ? 1 : 0; g_groups = 0xff; }
+static int g_fp16 = 0;      /* of those, the groups whose operands round to fp16 instead */
+void ko_set_bf16_emulation(int on) { g_bf16 = on ? 1 : 0; g_groups = 0xff; g_fp16 = 0; }
 int ko_get_bf16_emulation(void) { return g_bf16; }
-void ko_set_operand_emulation(int fmt, int groups) { g_bf16 = fmt; g_groups = groups; }
+void ko_set_operand_emulation(int fmt, int groups) { g_bf16 = fmt; g_groups = groups; g_fp16 = fmt == 2 ? groups : 0; }
+/* Mixed operand formats: the groups in fp16_groups round to fp16, the other groups in `groups` to
+ * bf16 (the HIP path's decoder convolutions run on fp16 operands). */
+void ko_set_operand_formats(int groups, int fp16_groups) {
+    g_bf16 = groups ? 1 : 0;
+    g_groups = groups;
+    g_fp16 = fp16_groups & groups;
+}
 void ko_set_threads(int n) {
     if (n > 0) omp_set_num_threads(n);
 }
@@ -62,9 +70,9 @@ float ko_fp16_round(float x) {
     return r;
 }
 
-static float* round_copy(const float* x, size_t n) {
+static float* round_copy(const float* x, size_t n, int group) {
     float* r = (float*)malloc(n * sizeof(float));
-    if (g_bf16 == 2)
+    if (g_bf16 == 2 || (g_fp16 & group))
         for (size_t i = 0; i < n; i++) r[i] = ko_fp16_round(x[i]);
     else
         for (size_t i = 0; i < n; i++) r[i] = ko_bf16_round(x[i]);
@@ -695,8 +703,8 @@ int ko_model_create(int n, const char* const* names, const float* const* data, c
 /* A conv layer with the bf16 operand emulation applied to the layers the HIP path runs on MFMA. */
 static void conv_layer(const conv_t* c, const float* x, int t, float* y, int tout) {
     if (g_bf16 && (c->mfma & g_groups)) {
-        float* xr = round_copy(x, (size_t)c->cin * t);
-        float* wr = round_copy(c->w, (size_t)c->cout * c->cin * c->k);
+        float* xr = round_copy(x, (size_t)c->cin * t, c->mfma);
+        float* wr = round_copy(c->w, (size_t)c->cout * c->cin * c->k, c->mfma);
         conv1d_raw(xr, c->cin, t, wr, c->b, c->cout, c->k, c->stride, c->pad, c->dil, y, tout);
         free(xr);
         free(wr);
@@ -707,8 +715,8 @@ static void conv_layer(const conv_t* c, const float* x, int t, float* y, int tou
 
 static void convt_layer(const convt_t* c, const float* x, int t, float* y, int tout) {
     if (g_bf16 && (g_groups & KO_GROUP_UPS)) {
-        float* xr = round_copy(x, (size_t)c->cin * t);
-        float* wr = round_copy(c->w, (size_t)c->cin * c->cout * c->k);
+        float* xr = round_copy(x, (size_t)c->cin * t, KO_GROUP_UPS);
+        float* wr = round_copy(c->w, (size_t)c->cin * c->cout * c->k, KO_GROUP_UPS);
         ko_conv_transpose1d(xr, c->cin, t, wr, c->b, c->cout, c->k, c->stride, c->pad, y, tout);
         free(xr);
         free(wr);

@@ -36,6 +36,7 @@ int ko_get_bf16_emulation(void);
 #define KO_GROUP_POST 4
 #define KO_GROUP_UPS 8
 #define KO_GROUP_H16 16 /* fp16 storage of each Snake step's conv1 output */
+void ko_set_operand_formats(int groups, int fp16_groups);
 void ko_set_operand_emulation(int fmt, int groups);
 float ko_fp16_round(float x);
 void ko_set_threads(int n);

@@ -27,6 +27,7 @@ def lib():
             raise RuntimeError(f"oracle library missing: {LIB_PATH} (run oracle/build_oracle.py)")
         L = C.CDLL(LIB_PATH)
         L.ko_set_bf16_emulation.argtypes = [C.c_int]
+        L.ko_set_operand_formats.argtypes = [C.c_int, C.c_int]
         L.ko_set_threads.argtypes = [C.c_int]
         L.ko_bf16_round.argtypes = [C.c_float]
         L.ko_bf16_round.restype = C.c_float
@@ -69,6 +70,23 @@ def _f32(a):
 def _chk(rc, what):
     if rc != 0:
         raise ValueError(f"oracle {what} failed (rc={rc})")
+
+
+GROUP_DECODER, GROUP_SNAKE, GROUP_POST, GROUP_UPS, GROUP_H16 = 1, 2, 4, 8, 16
+
+
+class operand_formats:
+    """Context manager: round the operands of the layer groups in `groups` (GROUP_*) to bf16, those
+    also in `fp16_groups` to fp16 instead (error-budget analysis)."""
+
+    def __init__(self, groups, fp16_groups=0):
+        self.groups, self.fp16 = groups, fp16_groups
+
+    def __enter__(self):
+        lib().ko_set_operand_formats(self.groups, self.fp16)
+
+    def __exit__(self, *a):
+        lib().ko_set_bf16_emulation(0)
 
 
 class bf16_emulation:

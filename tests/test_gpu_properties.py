@@ -25,12 +25,15 @@ def _print(*a):
     print(*a, flush=True)
 
 
-# Below this many decoder frames the decoder's InstanceNorm runs over so few columns (two values
-# normalize to +-1 whatever their difference) that bf16 operand rounding moves its output by tens of
-# percent: the bf16-emulated oracle itself lands 15-20 dB from the fp32 one at N = 2.  Such items
-# are checked stage by stage (the decoder against the emulation's own deviation, the generator from
-# the GPU's decoder output at the full bar).
-SHORT_N = 6
+# Items of exactly two decoder frames: the decoder's InstanceNorm then runs over two columns, which
+# normalize to +-d / sqrt(d^2 + 4 eps) whatever their difference d, so a channel whose two values lie
+# within ~sqrt(eps) of each other turns operand rounding into an O(1) change.  Measured on the
+# oracle (tests use the same seeds): with bf16 operands the decoder lands 14-16 dB and the audio
+# 29-30 dB from fp32; fp16 operands do not fix it (15-18 and 30-32 dB).  One- and three-frame and
+# longer items meet the full bar end to end (audio 43-44 dB).  Two-frame items are checked stage by
+# stage: the decoder against the emulation's own deviation, the generator from the GPU's decoder
+# output at the full bar.
+ILL_CONDITIONED_N = (2,)
 
 
 def _check_vs_oracle(ctx, oracle_model, items, label):
@@ -44,7 +47,7 @@ def _check_vs_oracle(ctx, oracle_model, items, label):
       last frame of every item are symmetric under the reflect padding, so all their bins are real)
       reads +pi on one side and -pi on the other from ulp-level differences of sin/tanh; the
       generator sees that 2 pi jump, in the reference against upstream torch as here.
-    - Items shorter than SHORT_N frames: the decoder output within 6 dB of the bf16-emulated
+    - Two-frame items (ILL_CONDITIONED_N): the decoder output within 6 dB of the bf16-emulated
       oracle's own distance from fp32, and the audio against the oracle's generator run from the
       GPU's decoder output and spectrum.
     Returns the number of items compared end to end and the audio."""
@@ -68,7 +71,7 @@ def _check_vs_oracle(ctx, oracle_model, items, label):
         flips = int((np.abs(g[11:] - spec[11:]) > np.pi).sum())
         assert mag_err < 1e-4 and np.abs(dphi[energetic]).max() < 1e-3
         note = ""
-        if it.n_frames < SHORT_N:
+        if it.n_frames in ILL_CONDITIONED_N:
             x = oracle_model.decoder(asr, it.f0, it.energy, it.ref_s)
             with O.bf16_emulation():
                 xe = oracle_model.decoder(asr, it.f0, it.energy, it.ref_s)
@@ -163,7 +166,7 @@ def test_fixed_noise_vs_oracle(gpu_ctx, oracle_model):
     assert np.array_equal(again[0], outs[0])
 
 
-@pytest.mark.parametrize("ns", [[1], [2, 1], [1, 3, 2]])
+@pytest.mark.parametrize("ns", [[1], [2, 1], [1, 3, 2], [5, 4]])
 def test_tiny_items_vs_oracle(gpu_ctx, oracle_model, ns):
     from kokoro_hip import workloads
     _check_vs_oracle(gpu_ctx, oracle_model, workloads.small_items(64 + len(ns), ns), "tiny")
