@@ -58,6 +58,38 @@ typedef struct {
  * The tensors are copied; the caller keeps ownership. */
 int kk_upload_model(kk_ctx* ctx, const kk_tensor* tensors, int n, char* err, size_t errlen);
 
+/* ------------------------------------------------------------------ checkpoints and voices (host)
+ * The released model file and voice packs are PyTorch zip archives (torch.save).  They are read
+ * on the host, never executed: STORED zip entries, and a pickle interpreter that accepts only
+ * float32 tensors in (ordered) dicts (globals collections.OrderedDict,
+ * torch._utils._rebuild_tensor_v2, torch.FloatStorage); anything else is KK_ERR_INVALID. */
+typedef struct kk_checkpoint kk_checkpoint;
+/* load_kmodel_checkpoint (src/torchpt.rs:311-327): {submodule: state_dict} flattened to
+ * "submodule.param" (a leading "module." of a parameter stripped), tensors as contiguous f32. */
+int kk_checkpoint_open(const char* path, kk_checkpoint** out, char* err, size_t errlen);
+int kk_checkpoint_count(const kk_checkpoint* ck);
+/* Entry i (names sorted): its name, shape [ndim] and data [numel], valid until kk_checkpoint_free. */
+int kk_checkpoint_entry(const kk_checkpoint* ck, int i, const char** name, const int64_t** shape, int* ndim,
+                        const float** data, int64_t* numel);
+void kk_checkpoint_free(kk_checkpoint* ck);
+/* Weights::load_pth + GpuKokoro::with_gpu for the decoder + generator (src/weights.rs:19-26,
+ * src/gpu.rs:685-724): the "decoder.*" tensors of the checkpoint, each conv weight resolved from
+ * weight_g / weight_v when "X.weight" is absent (Weights::conv_weight, src/weights.rs:62-73), the
+ * AdaIN InstanceNorm affine parameters defaulting to 1 / 0 when absent
+ * (Weights::get_instance_norm_affine, src/weights.rs:76-84), then as kk_upload_model. */
+int kk_upload_checkpoint(kk_ctx* ctx, const kk_checkpoint* ck, char* err, size_t errlen);
+/* weight_norm (src/ops.rs:9-23): w = v * (g[r] / ||v_r||) per row r of `per_row` values, the norm
+ * summed in f64. */
+int kk_weight_norm(const float* v, const float* g, int64_t rows, int64_t per_row, float* w);
+/* load_voice_pack (src/torchpt.rs:329-335) and Engine::voice (src/engine.rs:114-137): the packs at
+ * paths[0..n) ([rows, 1, 256] each), element-wise mean when n > 1 (summed in order in f32), as a
+ * malloc'ed [rows][256] array released by kk_voice_free. */
+int kk_voice_load(const char* const* paths, int n, float** pack, int64_t* rows, char* err, size_t errlen);
+void kk_voice_free(float* pack);
+/* Voice::ref_s (src/engine.rs:54-59): the style of an utterance of n phoneme characters is row
+ * n - 1 (256 values); n outside [1, rows] is KK_ERR_INVALID. */
+int kk_voice_ref_s(const float* pack, int64_t rows, int64_t n_phoneme_chars, const float** ref_s);
+
 /* ------------------------------------------------------------------ batch items */
 
 #define KK_NOISE_COUNTER 0 /* ItemNoise::Counter(seed) (src/gpu_batch.rs:15) */

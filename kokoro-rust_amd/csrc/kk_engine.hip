@@ -19,6 +19,7 @@
 #include <tuple>
 #include <vector>
 
+#include "kk_ckpt.h"
 #include "kk_common.h"
 #include "kk_kernels.h"
 #include "kokoro_hip.h"
@@ -234,8 +235,24 @@ static int round_up(int v, int m) { return (v + m - 1) / m * m; }
 // Weight table lookup (names as the checkpoint's state dict).
 struct Table {
     std::map<std::string, const kk_tensor*> byname;
+    // Weights::get_instance_norm_affine (src/weights.rs:76-84): the AdaIN InstanceNorm affine
+    // parameters are absent from the released checkpoint and take torch's initial values (weight 1,
+    // bias 0); only names ending in ".norm.weight" / ".norm.bias" may default, and only when this
+    // is set (checkpoint uploads).
+    bool norm_defaults = false;
+    mutable std::vector<std::unique_ptr<std::vector<float>>> defaults;
     const float* get(const std::string& name, int64_t numel) const {
         auto it = byname.find(name);
+        if (it == byname.end() && norm_defaults) {
+            auto ends = [&](const char* suf) {
+                const size_t k = std::strlen(suf);
+                return name.size() >= k && name.compare(name.size() - k, k, suf) == 0;
+            };
+            if (ends(".norm.weight") || ends(".norm.bias")) {
+                defaults.push_back(std::make_unique<std::vector<float>>((size_t)numel, ends(".norm.weight") ? 1.f : 0.f));
+                return defaults.back()->data();
+            }
+        }
         check(it != byname.end(), "missing tensor " + name);
         check(it->second->numel == numel, "tensor " + name + " has " + std::to_string(it->second->numel) +
                                               " values, expected " + std::to_string(numel));
@@ -353,8 +370,9 @@ static void load_resblk(MResblk& r, const Table& t, const std::string& p, int di
     }
 }
 
-static void load_model(kk_ctx* ctx, const kk_tensor* tensors, int n) {
+static void load_model(kk_ctx* ctx, const kk_tensor* tensors, int n, bool norm_defaults = false) {
     Table t;
+    t.norm_defaults = norm_defaults;
     for (int i = 0; i < n; i++) {
         check(tensors[i].name != nullptr, "tensor without a name");
         t.byname[tensors[i].name] = &tensors[i];
@@ -1575,6 +1593,46 @@ static void tap_rows(const void* dev, int64_t ld, int64_t r0, int64_t rows, int 
 
 using namespace kk;
 
+// A model checkpoint read on the host: flattened "submodule.param" names (sorted) to tensors.
+struct kk_checkpoint {
+    std::map<std::string, kk::HostTensor> t;
+    std::vector<const std::string*> names;  // index -> name
+};
+
+namespace kk {
+// The decoder's tensors of a checkpoint as the weight table kk_upload_model takes, with weight_norm
+// resolved: a conv whose "X.weight" is absent is built from "X.weight_g" / "X.weight_v"
+// (Weights::conv_weight, src/weights.rs:62-73).
+static void upload_checkpoint(kk_ctx* ctx, const kk_checkpoint* ck) {
+    std::vector<kk_tensor> tab;
+    std::vector<std::unique_ptr<std::vector<float>>> resolved;
+    std::vector<std::unique_ptr<std::string>> names;
+    for (const auto& kv : ck->t) {
+        const std::string& nm = kv.first;
+        if (nm.compare(0, 8, "decoder.") != 0) continue;
+        tab.push_back(kk_tensor{nm.c_str(), kv.second.data.data(), (int64_t)kv.second.data.size()});
+        const std::string suf = ".weight_v";
+        if (nm.size() > suf.size() && nm.compare(nm.size() - suf.size(), suf.size(), suf) == 0) {
+            const std::string base = nm.substr(0, nm.size() - suf.size());
+            if (ck->t.count(base + ".weight")) continue;
+            auto g = ck->t.find(base + ".weight_g");
+            check(g != ck->t.end(), "checkpoint: " + nm + " without " + base + ".weight_g");
+            const HostTensor& v = kv.second;
+            check(!v.shape.empty() && v.shape[0] > 0, "checkpoint: " + nm + " has no rows");
+            const int64_t rows = v.shape[0], per = (int64_t)v.data.size() / rows;
+            check(g->second.data.size() == (size_t)rows, "checkpoint: " + base + ".weight_g holds " +
+                                                             std::to_string(g->second.data.size()) + " values for " +
+                                                             std::to_string(rows) + " rows");
+            resolved.push_back(std::make_unique<std::vector<float>>(v.data.size()));
+            weight_norm(v.data.data(), g->second.data.data(), rows, per, resolved.back()->data());
+            names.push_back(std::make_unique<std::string>(base + ".weight"));
+            tab.push_back(kk_tensor{names.back()->c_str(), resolved.back()->data(), (int64_t)v.data.size()});
+        }
+    }
+    load_model(ctx, tab.data(), (int)tab.size(), true);
+}
+}  // namespace kk
+
 // ------------------------------------------------------------------ no-allocation entry point
 // kk_snake_block_noalloc's device scratch: one array per device, held from the first use of the
 // library on that device until the process ends.  Regions (bytes, 256-aligned):
@@ -1773,6 +1831,94 @@ void kk_close(kk_ctx* ctx) {
 int kk_device_name(const kk_ctx* ctx, char* buf, size_t len) {
     if (!ctx || !buf || !len) return KK_ERR_INVALID;
     std::snprintf(buf, len, "%s", ctx->name.c_str());
+    return KK_OK;
+}
+
+int kk_checkpoint_open(const char* path, kk_checkpoint** out, char* err, size_t errlen) {
+    if (!path || !out) return KK_ERR_INVALID;
+    *out = nullptr;
+    return guard(err, errlen, [&] {
+        auto ck = std::make_unique<kk_checkpoint>();
+        try {
+            ck->t = read_model_checkpoint(path);
+        } catch (const std::runtime_error& e) {
+            fail(KK_ERR_INVALID, e.what());
+        }
+        for (const auto& kv : ck->t) ck->names.push_back(&kv.first);
+        *out = ck.release();
+    });
+}
+
+int kk_checkpoint_count(const kk_checkpoint* ck) { return ck ? (int)ck->names.size() : KK_ERR_INVALID; }
+
+int kk_checkpoint_entry(const kk_checkpoint* ck, int i, const char** name, const int64_t** shape, int* ndim,
+                        const float** data, int64_t* numel) {
+    if (!ck || i < 0 || i >= (int)ck->names.size()) return KK_ERR_INVALID;
+    const std::string& nm = *ck->names[i];
+    const HostTensor& t = ck->t.at(nm);
+    if (name) *name = nm.c_str();
+    if (shape) *shape = t.shape.data();
+    if (ndim) *ndim = (int)t.shape.size();
+    if (data) *data = t.data.data();
+    if (numel) *numel = (int64_t)t.data.size();
+    return KK_OK;
+}
+
+void kk_checkpoint_free(kk_checkpoint* ck) { delete ck; }
+
+int kk_upload_checkpoint(kk_ctx* ctx, const kk_checkpoint* ck, char* err, size_t errlen) {
+    if (!ctx || !ck) return KK_ERR_INVALID;
+    return guard(err, errlen, [&] {
+        use_device(ctx);
+        upload_checkpoint(ctx, ck);
+    });
+}
+
+int kk_weight_norm(const float* v, const float* g, int64_t rows, int64_t per_row, float* w) {
+    if (!v || !g || !w || rows < 0 || per_row < 0) return KK_ERR_INVALID;
+    weight_norm(v, g, rows, per_row, w);
+    return KK_OK;
+}
+
+int kk_voice_load(const char* const* paths, int n, float** pack, int64_t* rows, char* err, size_t errlen) {
+    if (!paths || n <= 0 || !pack || !rows) return KK_ERR_INVALID;
+    *pack = nullptr, *rows = 0;
+    return guard(err, errlen, [&] {
+        std::vector<HostTensor> packs;
+        for (int i = 0; i < n; i++) {
+            check(paths[i] != nullptr, "null voice path");
+            try {
+                packs.push_back(read_voice_pack(paths[i]));
+            } catch (const std::runtime_error& e) {
+                fail(KK_ERR_INVALID, e.what());
+            }
+            check(packs.back().shape == packs[0].shape, "voice packs have different shapes");
+        }
+        const size_t m = packs[0].data.size();
+        float* out = (float*)std::malloc(sizeof(float) * std::max<size_t>(m, 1));
+        if (!out) throw std::bad_alloc();
+        if (n == 1) {
+            std::memcpy(out, packs[0].data.data(), sizeof(float) * m);
+        } else {
+            // the element-wise mean of the packs, summed in order in f32 (src/engine.rs:127-130)
+            const float fn = (float)n;
+            for (size_t i = 0; i < m; i++) {
+                float s = 0.f;
+                for (int p = 0; p < n; p++) s += packs[p].data[i];
+                out[i] = s / fn;
+            }
+        }
+        *pack = out;
+        *rows = packs[0].shape[0];
+    });
+}
+
+void kk_voice_free(float* pack) { std::free(pack); }
+
+int kk_voice_ref_s(const float* pack, int64_t rows, int64_t n_phoneme_chars, const float** ref_s) {
+    // Voice::ref_s (src/engine.rs:54-59): row n - 1 of the pack, 256 values
+    if (!pack || !ref_s || n_phoneme_chars < 1 || n_phoneme_chars > rows) return KK_ERR_INVALID;
+    *ref_s = pack + (n_phoneme_chars - 1) * 256;
     return KK_OK;
 }
 

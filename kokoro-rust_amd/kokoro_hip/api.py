@@ -23,7 +23,9 @@ EXPORTS = [
     "kk_plan_sync", "kk_plan_fetch", "kk_plan_tap", "kk_plan_get_info", "kk_plan_free", "kk_set_profiling",
     "kk_profile_read", "kk_durations_from_logits", "kk_layout_frames", "kk_layout_col_item", "kk_layout_src_row",
     "kk_plan_fetch_pcm16", "kk_encode_pcm16", "kk_wav_header", "kk_host_alloc", "kk_host_free",
-    "kk_plan_item_samples", "kk_plan_fetch_pcm16_async", "kk_plan_fetch_wait", "kk_snake_block_noalloc", "kk_profile_launches",
+    "kk_plan_item_samples", "kk_plan_fetch_pcm16_async", "kk_plan_fetch_wait", "kk_snake_block_noalloc", "kk_profile_launches", "kk_checkpoint_open", "kk_checkpoint_count",
+    "kk_checkpoint_entry", "kk_checkpoint_free", "kk_upload_checkpoint", "kk_weight_norm", "kk_voice_load",
+    "kk_voice_free", "kk_voice_ref_s",
 ]
 NOALLOC_MAX_ROWS = 65536
 NOALLOC_MAX_ITEMS = 64
@@ -108,6 +110,18 @@ def lib():
         L.kk_plan_fetch_pcm16_async.argtypes = [vp, vp, vp, cp, sz]
         L.kk_plan_fetch_wait.argtypes = [vp, cp, sz]
         L.kk_wav_header.argtypes = [i32, C.c_uint32, C.c_uint64, vp, cp, sz]
+        L.kk_checkpoint_open.argtypes = [cp, C.POINTER(vp), cp, sz]
+        L.kk_checkpoint_count.argtypes = [vp]
+        L.kk_checkpoint_entry.argtypes = [vp, i32, C.POINTER(C.c_char_p), C.POINTER(C.POINTER(C.c_int64)),
+                                          C.POINTER(C.c_int), C.POINTER(C.POINTER(C.c_float)), C.POINTER(C.c_int64)]
+        L.kk_checkpoint_free.argtypes = [vp]
+        L.kk_checkpoint_free.restype = None
+        L.kk_upload_checkpoint.argtypes = [vp, vp, cp, sz]
+        L.kk_weight_norm.argtypes = [vp, vp, i64, i64, vp]
+        L.kk_voice_load.argtypes = [C.POINTER(cp), i32, C.POINTER(C.POINTER(C.c_float)), C.POINTER(C.c_int64), cp, sz]
+        L.kk_voice_free.argtypes = [C.POINTER(C.c_float)]
+        L.kk_voice_free.restype = None
+        L.kk_voice_ref_s.argtypes = [C.POINTER(C.c_float), i64, i64, C.POINTER(C.POINTER(C.c_float))]
         L.kk_snake_block_noalloc.argtypes = [vp, cp, vp, i64, vp, vp, i32, C.POINTER(vp), cp, sz]
         L.kk_plan_get_info.argtypes = [vp, C.POINTER(PlanInfo)]
         L.kk_plan_free.argtypes = [vp]
@@ -154,6 +168,74 @@ def wav_header(fmt, sample_rate, data_bytes):
     err = _err()
     _check(lib().kk_wav_header(int(fmt), int(sample_rate), int(data_bytes), _p(out), err, len(err)), err)
     return out.tobytes()
+
+
+# ------------------------------------------------------------------ checkpoints and voices
+
+
+class Checkpoint:
+    """kk_checkpoint_open: a torch.save model file read by the library (host only)."""
+
+    def __init__(self, path):
+        h = C.c_void_p()
+        err = _err()
+        _check(lib().kk_checkpoint_open(str(path).encode(), C.byref(h), err, len(err)), err)
+        self.h = h
+
+    def tensors(self):
+        """{name: float32 array of its shape} (copies)."""
+        out = {}
+        for i in range(lib().kk_checkpoint_count(self.h)):
+            nm, shp, nd, data, n = C.c_char_p(), C.POINTER(C.c_int64)(), C.c_int(), C.POINTER(C.c_float)(), C.c_int64()
+            _check(lib().kk_checkpoint_entry(self.h, i, C.byref(nm), C.byref(shp), C.byref(nd), C.byref(data),
+                                             C.byref(n)), _err())
+            shape = tuple(shp[k] for k in range(nd.value))
+            arr = np.ctypeslib.as_array(data, shape=(n.value,)).copy() if n.value else np.zeros(0, np.float32)
+            out[nm.value.decode()] = arr.reshape(shape)
+        return out
+
+    def free(self):
+        if getattr(self, "h", None):
+            lib().kk_checkpoint_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.free()
+
+
+def weight_norm(v, g):
+    """kk_weight_norm over the first dimension of v."""
+    v = _f32(v)
+    g = _f32(g).reshape(-1)
+    w = np.empty_like(v)
+    rc = lib().kk_weight_norm(_p(v), _p(g), v.shape[0], v.size // max(v.shape[0], 1), _p(w))
+    if rc != KK_OK:
+        raise KKError(rc, "weight_norm")
+    return w
+
+
+def voice_load(paths):
+    """kk_voice_load: the (mean) voice pack as float32 [rows, 256]."""
+    enc = [str(p).encode() for p in paths]
+    arr = (C.c_char_p * len(enc))(*enc)
+    pack, rows = C.POINTER(C.c_float)(), C.c_int64()
+    err = _err()
+    _check(lib().kk_voice_load(arr, len(enc), C.byref(pack), C.byref(rows), err, len(err)), err)
+    out = np.ctypeslib.as_array(pack, shape=(rows.value * 256,)).copy().reshape(rows.value, 256)
+    lib().kk_voice_free(pack)
+    return out
+
+
+def voice_ref_s(pack, n_phoneme_chars):
+    """kk_voice_ref_s on a [rows, 256] pack: its row n - 1."""
+    pk = _f32(pack)
+    ptr = pk.ctypes.data_as(C.POINTER(C.c_float))
+    out = C.POINTER(C.c_float)()
+    rc = lib().kk_voice_ref_s(ptr, pk.shape[0], int(n_phoneme_chars), C.byref(out))
+    if rc != KK_OK:
+        raise KKError(rc, "voice_ref_s")
+    off = (C.addressof(out.contents) - pk.ctypes.data) // 4
+    return pk.reshape(-1)[off:off + 256].copy()
 
 
 # ------------------------------------------------------------------ host rules
@@ -232,6 +314,11 @@ class Context:
         tab = (Tensor * len(names))(*[Tensor(e, a.ctypes.data, a.size) for e, a in zip(enc, arrs)])
         err = _err()
         _check(lib().kk_upload_model(self.h, tab, len(names), err, len(err)), err)
+
+    def upload_checkpoint(self, ck):
+        """kk_upload_checkpoint from a Checkpoint."""
+        err = _err()
+        _check(lib().kk_upload_checkpoint(self.h, ck.h, err, len(err)), err)
 
     def set_profiling(self, on):
         lib().kk_set_profiling(self.h, int(bool(on)))

@@ -79,6 +79,20 @@ static float* round_copy(const float* x, size_t n, int group) {
     return r;
 }
 
+/* ================================================================ hydration */
+
+/* weight_norm (src/ops.rs:9-23): per row r, norm = sqrt(sum of v^2 in f64) rounded to f32,
+ * scale = g[r] / norm in f32, w = v * scale in f32. */
+void ko_weight_norm(const float* v, const float* g, int64_t rows, int64_t per_row, float* w) {
+    for (int64_t r = 0; r < rows; r++) {
+        double ss = 0.0;
+        for (int64_t j = 0; j < per_row; j++) ss += (double)v[r * per_row + j] * (double)v[r * per_row + j];
+        const float nrm = (float)sqrt(ss);
+        const float scale = g[r] / nrm;
+        for (int64_t j = 0; j < per_row; j++) w[r * per_row + j] = v[r * per_row + j] * scale;
+    }
+}
+
 /* ================================================================ layout (a1-a3) */
 
 /* src/gpu_batch.rs:250-258: a[b] = running sum of (N_j + GAP_N). */

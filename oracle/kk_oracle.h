@@ -40,6 +40,7 @@ void ko_set_operand_formats(int groups, int fp16_groups);
 void ko_set_operand_emulation(int fmt, int groups);
 float ko_fp16_round(float x);
 void ko_set_threads(int n);
+void ko_weight_norm(const float* v, const float* g, int64_t rows, int64_t per_row, float* w);
 float ko_bf16_round(float x);
 
 /* ---------------------------------------------------------------- ragged layout (a1-a3) */

@@ -28,6 +28,8 @@ def lib():
         L = C.CDLL(LIB_PATH)
         L.ko_set_bf16_emulation.argtypes = [C.c_int]
         L.ko_set_operand_formats.argtypes = [C.c_int, C.c_int]
+        L.ko_weight_norm.argtypes = [C.c_void_p, C.c_void_p, C.c_int64, C.c_int64, C.c_void_p]
+        L.ko_weight_norm.restype = None
         L.ko_set_threads.argtypes = [C.c_int]
         L.ko_bf16_round.argtypes = [C.c_float]
         L.ko_bf16_round.restype = C.c_float
@@ -100,6 +102,15 @@ class bf16_emulation:
 
     def __exit__(self, *a):
         lib().ko_set_bf16_emulation(0)
+
+
+def weight_norm(v, g):
+    """weight_norm (src/ops.rs:9-23) over the first dimension of v."""
+    v = _f32(v)
+    g = _f32(g).reshape(-1)
+    w = np.empty_like(v)
+    lib().ko_weight_norm(v.ctypes.data, g.ctypes.data, v.shape[0], v.size // max(v.shape[0], 1), w.ctypes.data)
+    return w
 
 
 def set_threads(n):
