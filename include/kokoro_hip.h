@@ -139,6 +139,46 @@ int kk_forward_decoder_batch(kk_ctx* ctx, const kk_decoder_item* items, int n, k
                              size_t errlen);
 void kk_output_free(kk_output* out, int n);
 
+/* ------------------------------------------------------------------ the whole forward (ids -> audio)
+ * kk_upload_model / kk_upload_checkpoint load the stages before the decoder as well when the table
+ * holds them ("bert.*", "bert_encoder.*", "text_encoder.*", "predictor.*"): ALBERT, the text encoder
+ * and the prosody predictor (Albert::load src/albert.rs:36-67, TextEncoder::load / Predictor::load
+ * src/model.rs:29-88, Kokoro::from_weights src/model.rs:122-141). */
+
+/* BatchItem (src/gpu_batch.rs:19-24): one utterance's input_ids (with the two boundary tokens),
+ * style ref_s (256 values: [0,128) the decoder's, [128,256) the prosody predictor's), speed and
+ * noise source.  A fixed noise source must hold 600 N * 9 values for the N frames the predicted
+ * durations give (src/gpu_batch.rs:338); anything else is KK_ERR_INVALID. */
+typedef struct {
+    const int64_t* ids;   /* [n_ids], each in [0, 178) */
+    int32_t n_ids;        /* 2..512 (src/gpu_batch.rs:184) */
+    const float* ref_s;   /* [256] */
+    float speed;          /* > 0, finite */
+    int32_t noise_kind;   /* KK_NOISE_* */
+    uint64_t seed;
+    const float* rand_ini;/* [9]        (KK_NOISE_FIXED) */
+    const float* sine;    /* [600N * 9] (KK_NOISE_FIXED) */
+    int64_t sine_len;
+} kk_item;
+
+/* Output (src/model.rs:101-104): the audio (600 N samples, in the pinned output pool as kk_output)
+ * and the predicted durations pred_dur [n_tok] (malloc'ed); both released by kk_result_free. */
+typedef struct {
+    float* audio;
+    int64_t n_samples;
+    int64_t* pred_dur;
+    int32_t n_tok;
+} kk_result;
+
+/* GpuKokoro::forward_batch (src/gpu_batch.rs:179-420): the token phase (ALBERT, bert_encoder, the
+ * duration encoder, the duration LSTM and projection; the text encoder beside them), the durations
+ * from the logits on the host (durations_from_logits, src/model.rs:90-100: one copy of the logits
+ * back), then the frame layout, the shared LSTM, the F0 / N stacks, the decoder, the generator and
+ * the iSTFT.  Results in input order.  Kept buffers, failure release and test hooks as
+ * kk_forward_decoder_batch. */
+int kk_forward_batch(kk_ctx* ctx, const kk_item* items, int n, kk_result* out, char* err, size_t errlen);
+void kk_result_free(kk_result* out, int n);
+
 /* ------------------------------------------------------------------ plans (device-resident runs)
  * kk_forward_decoder_batch = kk_plan_create + kk_plan_run + kk_plan_fetch + kk_plan_free.
  * A plan builds the layout, uploads the inputs (one copy of all tables) and allocates every device
@@ -185,7 +225,15 @@ int kk_plan_create_snake(kk_ctx* ctx, const char* prefix, const float* const* x,
 #define KK_NOALLOC_SCRATCH_BYTES (48u << 20)
 int kk_snake_block_noalloc(kk_ctx* ctx, const char* prefix, float* x, int64_t rows, const int64_t* start,
                            const int64_t* len, int n, const float* const* ref_s, char* err, size_t errlen);
-/* Enqueue the plan's kernels; `until` = KK_STAGE_ALL or an earlier stage (for stage taps). */
+/* Ids-level plan (kk_forward_batch = kk_plan_create_full + run + fetch): creation runs the token
+ * phase once and fixes the frame layout from its durations; kk_plan_run then runs the whole
+ * forward, token phase included, on the same durations (the recomputed logits are identical). */
+int kk_plan_create_full(kk_ctx* ctx, const kk_item* items, int n, kk_plan** out, char* err, size_t errlen);
+/* The predicted durations of item `item` of an ids-level plan (valid while the plan lives). */
+int kk_plan_durations(const kk_plan* plan, int item, const int64_t** dur, int32_t* n_tok);
+/* Enqueue the plan's kernels; `until` = KK_STAGE_ALL or an earlier stage (for stage taps).
+ * KK_STAGE_PROSODY (ids-level plans only): through the F0 / N curves and the text encoder. */
+#define KK_STAGE_PROSODY 0
 #define KK_STAGE_DECODER 1
 #define KK_STAGE_SOURCE 2
 #define KK_STAGE_GEN0 3
@@ -199,8 +247,10 @@ int kk_plan_sync(kk_plan* plan, char* err, size_t errlen);
 int kk_plan_fetch(kk_plan* plan, kk_output* out, char* err, size_t errlen);
 /* Copy a named device buffer of the last run to the host, per item and channel-major like the
  * reference's host tensors: "asr" [512][N], "decoder" [512][2N], "spec" [22][120N+1],
- * "gen0" [256][20N], "post" [22][120N+1], "audio" [600N].  `dst` receives item `item` only;
- * `count` is its element count. */
+ * "gen0" [256][20N], "post" [22][120N+1], "audio" [600N]; of ids-level plans also "bert"
+ * [768][T], "d" [640][T] (the duration encoder's output), "logits" [50][T], "t_en" [512][T],
+ * "shared" [512][N], "f0" [2N], "n" [2N] (T = n_ids).  `dst` receives item `item` only; `count`
+ * is its element count. */
 int kk_plan_tap(kk_plan* plan, const char* name, int item, float* dst, int64_t count, char* err, size_t errlen);
 typedef struct {
     int64_t n_items;

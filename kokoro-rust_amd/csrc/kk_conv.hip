@@ -215,6 +215,9 @@ struct Slot {
                     } else if constexpr (PRO == PRO_ADAIN_SNAKE) {
                         const float c = __builtin_amdgcn_cosf(__builtin_fmaf(x, tsc[e], tsh[e]));
                         x = __builtin_fmaf(c, nh[e], __builtin_fmaf(x, sc[e], vsh[e]));
+                    } else if constexpr (PRO == PRO_GELU) {
+                        // gelu_new, sqrt(2 / pi) rounded to f32
+                        x = 0.5f * x * (1.0f + tanhf(0.797884560802865355f * (x + 0.044715f * x * x * x)));
                     }
                     // the Snake layers' cin is a multiple of the slab width (checked on the host)
                     if constexpr (!SNAKE) x = e < n_ch ? x : 0.f;
@@ -813,6 +816,10 @@ hipError_t launch_conv(const ConvParams& p, int pro, int epi, int shape, bool st
     KK_CONV(PRO_F32, EPI_STORE, SHAPE_256x128, 4, 1, false, false, false)
     KK_CONV(PRO_F32, EPI_STORE, SHAPE_64x256, 1, 2, false, false, false)
     KK_CONV(PRO_BF16, EPI_STORE, SHAPE_256x128, 4, 1, true, false, false)
+    // stages before the decoder: residual linears (ALBERT attention output, FFN output with gelu_new
+    // applied to its input)
+    KK_CONV(PRO_F32, EPI_RESID, SHAPE_256x128, 4, 1, false, false, false)
+    KK_CONV(PRO_GELU, EPI_RESID, SHAPE_256x128, 4, 1, false, false, false)
     // ConvT ups and conv_post
     KK_CONV(PRO_LEAKY, EPI_CONVT, SHAPE_256x128, 4, 1, true, false, false)
     KK_CONV(PRO_LEAKY, EPI_CONVT_REFLECT, SHAPE_256x128, 4, 1, true, false, false)

@@ -151,7 +151,39 @@ struct MNoiseConv {
     DevBuf w, b, wp;  // wp: f32 matrix-core packing (noise_convs.0)
     int cout = 0, k = 0, stride = 1, pad = 0;
 };
+// A Linear [dout][din] on the MFMA conv kernel (k = 1), in pieces of at most 1024 output rows (the
+// kernel stages the bias of one piece in LDS); piece i writes output columns [col0[i], ...).
+struct MLinear {
+    std::vector<MConv> piece;
+    std::vector<int> col0;
+    int din = 0, dout = 0;
+};
+// BiLstm (src/nn.rs:168-190) as the reference's GLstm (src/gpu.rs:600-613): W_ih of both directions
+// as one linear (gx [rows][2048], forward | reverse, bias b_ih), W_hh f32 k-major [2][256][1024],
+// b_hh [2][1024].
+struct MLstm {
+    MLinear wih;
+    DevBuf whh_t, bhh;
+};
+// The stages before the decoder (src/albert.rs:36-67, src/model.rs:21-88, 122-141).
+struct MUp {
+    DevBuf word, pos, tok0, emb_g, emb_b;  // ALBERT embeddings
+    MLinear map_in, qkv, dense, ffn, ffn_out, bert_enc;
+    DevBuf attn_g, attn_b, full_g, full_b;
+    DevBuf te_emb;  // text encoder
+    MConv te_cnn[3];
+    DevBuf te_g[3], te_b[3];
+    MLstm te_lstm, dur_lstm[3], pred_lstm, shared;
+    int dur_gb_off[3] = {0, 0, 0};  // AdaLayerNorm projections in the prosody style table
+    MLinear dur_proj;
+    MResblk f0[3], nn[3];
+    DevBuf f0p_w, f0p_b, np_w, np_b;  // F0_proj / N_proj (256 -> 1)
+    DevBuf style_wt, style_b;         // every prosody-style projection, transposed [128][rows]
+    int style_rows = 0;
+    bool ready = false;
+};
 struct Model {
+    MUp up;
     MResblk encode, decode[4];
     DevBuf f0w, f0b, nw_, nb_;
     MConv asr_res;
@@ -178,12 +210,15 @@ struct ProfRec {
 // and glue kernels.
 enum {
     PC_SNAKE = 0, PC_DECODER, PC_CONVT, PC_POST, PC_STATS, PC_FINALIZE, PC_STYLE, PC_EXPAND, PC_F0N, PC_COPY,
-    PC_POOL, PC_NOISE0, PC_NOISE1, PC_PHASE, PC_SOURCE, PC_ISTFT, PC_COUNT
+    PC_POOL, PC_NOISE0, PC_NOISE1, PC_PHASE, PC_SOURCE, PC_ISTFT, PC_LINEAR, PC_ATTN, PC_LSTM, PC_PCONV, PC_ROWS,
+    PC_COUNT
 };
 static const char* kProfNames[PC_COUNT] = {"snake_conv", "decoder_conv", "convt",      "post_conv",
                                            "stats_tiles", "finalize",    "style_fc",   "expand",
                                            "f0n_conv",    "copy_cols",   "adain_pool", "noise_conv0",
-                                           "noise_conv1", "phase_pre",   "source_stft", "istft"};
+                                           "noise_conv1", "phase_pre",   "source_stft", "istft",
+                                           "linear",      "attention",   "lstm",       "prosody_conv",
+                                           "rows"};
 
 // Host staging of a plan's tables and inputs.  Everything a plan uploads (layout tables, tile lists,
 // work lists, the items' inputs) is written into one pinned host buffer of the context and reaches
@@ -263,13 +298,12 @@ struct Table {
 
 // A stride-1 conv, w [cout][cin][k] -> packed [k][cin_pad/16][m_pad][16] bf16 (one MFMA A fragment,
 // 32 rows x 16 channels, is a contiguous 1 KB).
-static void load_conv(MConv& c, const Table& t, const std::string& p, int cin, int cout, int k, int pad, int dil,
-                      bool bias, int shape) {
-    c.cin = cin, c.cout = cout, c.k = k, c.pad = pad, c.dil = dil, c.shape = shape, c.bias = bias;
+static void load_conv_raw(MConv& c, const float* w, const float* bias_v, int cin, int cout, int k, int pad, int dil,
+                          int shape) {
+    c.cin = cin, c.cout = cout, c.k = k, c.pad = pad, c.dil = dil, c.shape = shape, c.bias = bias_v != nullptr;
     c.cin_pad = round_up(cin, 64);
     c.m = cout;
     c.m_pad = round_up(cout, kShapeM[shape]);
-    const float* w = t.get(p + ".weight", (int64_t)cout * cin * k);
     const int n16 = c.cin_pad / 16;
     std::vector<uint16_t> pk((size_t)k * n16 * c.m_pad * 16, 0);
     for (int co = 0; co < cout; co++)
@@ -280,8 +314,13 @@ static void load_conv(MConv& c, const Table& t, const std::string& p, int cin, i
     c.w.upload(pk);
     // a layer without a bias gets a zero vector: the conv epilogue always reads one
     std::vector<float> b(round_up(cout, 4), 0.f);
-    if (bias) std::memcpy(b.data(), t.get(p + ".bias", cout), sizeof(float) * cout);
+    if (bias_v) std::memcpy(b.data(), bias_v, sizeof(float) * cout);
     c.b.upload(b);
+}
+static void load_conv(MConv& c, const Table& t, const std::string& p, int cin, int cout, int k, int pad, int dil,
+                      bool bias, int shape) {
+    load_conv_raw(c, t.get(p + ".weight", (int64_t)cout * cin * k), bias ? t.get(p + ".bias", cout) : nullptr, cin,
+                  cout, k, pad, dil, shape);
 }
 
 // ConvTranspose1d with K = 2 * stride as a 2-tap conv over input rows (i - 1, i) whose GEMM row
@@ -370,6 +409,116 @@ static void load_resblk(MResblk& r, const Table& t, const std::string& p, int di
     }
 }
 
+// ------------------------------------------------------------------ the stages before the decoder
+// One piece of a linear: rows [r0, r0 + rows) of w [.][din] (and of its bias) -> output columns
+// col0 + [0, rows).
+static void add_piece(MLinear& L, const float* w, const float* b, int din, int r0, int rows, int col0, int shape) {
+    L.piece.emplace_back();
+    load_conv_raw(L.piece.back(), w + (size_t)r0 * din, b ? b + r0 : nullptr, din, rows, 1, 0, 1, shape);
+    L.col0.push_back(col0);
+    L.din = din;
+    L.dout = std::max(L.dout, col0 + rows);
+}
+// Linear::load (src/nn.rs:14-22) of `prefix`, in pieces of at most 1024 rows.
+static void load_linear(MLinear& L, const Table& t, const std::string& prefix, int din, int dout, int col0 = 0,
+                        int shape = SHAPE_256x128) {
+    const float* w = t.get(prefix + ".weight", (int64_t)dout * din);
+    const float* b = t.get(prefix + ".bias", dout);
+    for (int r0 = 0; r0 < dout; r0 += 1024) add_piece(L, w, b, din, r0, std::min(1024, dout - r0), col0 + r0, shape);
+}
+// BiLstm::load (src/nn.rs:178-189): torch.nn.LSTM names, H = 256.
+static void load_lstm(MLstm& l, const Table& t, const std::string& p, int din) {
+    constexpr int H = 256;
+    std::vector<float> whh_t((size_t)2 * H * 4 * H), bhh((size_t)2 * 4 * H);
+    for (int d = 0; d < 2; d++) {
+        const std::string sfx = d ? "_reverse" : "";
+        const float* wih = t.get(p + ".weight_ih_l0" + sfx, (int64_t)4 * H * din);
+        const float* bih = t.get(p + ".bias_ih_l0" + sfx, 4 * H);
+        add_piece(l.wih, wih, bih, din, 0, 4 * H, d * 4 * H, SHAPE_256x128);
+        const float* whh = t.get(p + ".weight_hh_l0" + sfx, (int64_t)4 * H * H);
+        for (int r = 0; r < 4 * H; r++)
+            for (int k = 0; k < H; k++) whh_t[((size_t)d * H + k) * 4 * H + r] = whh[(size_t)r * H + k];
+        std::memcpy(&bhh[(size_t)d * 4 * H], t.get(p + ".bias_hh_l0" + sfx, 4 * H), sizeof(float) * 4 * H);
+    }
+    l.whh_t.upload(whh_t);
+    l.bhh.upload(bhh);
+}
+static void upload_style_table(DevBuf& wt_d, DevBuf& b_d, int& rows, const StyleRows& sr) {
+    std::vector<float> wt((size_t)kStyleDim * sr.rows);
+    for (int r = 0; r < sr.rows; r++)
+        for (int k = 0; k < kStyleDim; k++) wt[(size_t)k * sr.rows + r] = sr.wt_rows[(size_t)r * kStyleDim + k];
+    wt_d.upload(wt);
+    b_d.upload(sr.bias);
+    rows = sr.rows;
+}
+
+// ALBERT, bert_encoder, the text encoder and the prosody predictor (Albert::load src/albert.rs:36-67,
+// TextEncoder::load / Predictor::load src/model.rs:29-88, Kokoro::from_weights src/model.rs:122-141).
+static void load_upstream(MUp& u, const Table& t) {
+    constexpr int NT = 178, EMB = 128, HID = 768, FFN = 2048, POS = 512, HIDDEN = 512;
+    u.ready = false;
+    u.word.upload(t.get("bert.embeddings.word_embeddings.weight", NT * EMB), (size_t)NT * EMB);
+    u.pos.upload(t.get("bert.embeddings.position_embeddings.weight", POS * EMB), (size_t)POS * EMB);
+    u.tok0.upload(t.get("bert.embeddings.token_type_embeddings.weight", 2 * EMB), EMB);  // token type 0
+    u.emb_g.upload(t.get("bert.embeddings.LayerNorm.weight", EMB), EMB);
+    u.emb_b.upload(t.get("bert.embeddings.LayerNorm.bias", EMB), EMB);
+    const std::string L = "bert.encoder.albert_layer_groups.0.albert_layers.0";
+    u.map_in = MLinear{}, u.qkv = MLinear{}, u.dense = MLinear{}, u.ffn = MLinear{}, u.ffn_out = MLinear{};
+    u.bert_enc = MLinear{}, u.dur_proj = MLinear{};
+    load_linear(u.map_in, t, "bert.encoder.embedding_hidden_mapping_in", EMB, HID);
+    load_linear(u.qkv, t, L + ".attention.query", HID, HID, 0);
+    load_linear(u.qkv, t, L + ".attention.key", HID, HID, HID);
+    load_linear(u.qkv, t, L + ".attention.value", HID, HID, 2 * HID);
+    load_linear(u.dense, t, L + ".attention.dense", HID, HID);
+    u.attn_g.upload(t.get(L + ".attention.LayerNorm.weight", HID), HID);
+    u.attn_b.upload(t.get(L + ".attention.LayerNorm.bias", HID), HID);
+    load_linear(u.ffn, t, L + ".ffn", HID, FFN);
+    load_linear(u.ffn_out, t, L + ".ffn_output", FFN, HID);
+    u.full_g.upload(t.get(L + ".full_layer_layer_norm.weight", HID), HID);
+    u.full_b.upload(t.get(L + ".full_layer_layer_norm.bias", HID), HID);
+    load_linear(u.bert_enc, t, "bert_encoder", HID, HIDDEN);
+    // text encoder: Conv1d 512 -> 512 k5 p2, LayerNorm(gamma, beta), BiLSTM
+    u.te_emb.upload(t.get("text_encoder.embedding.weight", NT * HIDDEN), (size_t)NT * HIDDEN);
+    for (int i = 0; i < 3; i++) {
+        const std::string c = "text_encoder.cnn." + std::to_string(i);
+        load_conv(u.te_cnn[i], t, c + ".0", HIDDEN, HIDDEN, 5, 2, 1, true, SHAPE_256x128);
+        u.te_g[i].upload(t.get(c + ".1.gamma", HIDDEN), HIDDEN);
+        u.te_b[i].upload(t.get(c + ".1.beta", HIDDEN), HIDDEN);
+    }
+    u.te_lstm = MLstm{}, u.pred_lstm = MLstm{}, u.shared = MLstm{};
+    load_lstm(u.te_lstm, t, "text_encoder.lstm", HIDDEN);
+    // prosody predictor: its style is ref_s[128:256] (src/gpu_batch.rs:206-210)
+    StyleRows sr;
+    const int cin = HIDDEN + kStyleDim;
+    for (int i = 0; i < 3; i++) {
+        u.dur_lstm[i] = MLstm{};
+        load_lstm(u.dur_lstm[i], t, "predictor.text_encoder.lstms." + std::to_string(2 * i), cin);
+        const std::string fc = "predictor.text_encoder.lstms." + std::to_string(2 * i + 1) + ".fc";
+        const float* fw = t.get(fc + ".weight", (int64_t)2 * HIDDEN * kStyleDim);
+        const float* fb = t.get(fc + ".bias", 2 * HIDDEN);
+        u.dur_gb_off[i] = sr.rows;
+        sr.wt_rows.insert(sr.wt_rows.end(), fw, fw + (size_t)2 * HIDDEN * kStyleDim);
+        sr.bias.insert(sr.bias.end(), fb, fb + 2 * HIDDEN);
+        sr.rows += 2 * HIDDEN;
+    }
+    load_lstm(u.pred_lstm, t, "predictor.lstm", cin);
+    load_linear(u.dur_proj, t, "predictor.duration_proj.linear_layer", HIDDEN, 50, 0, SHAPE_64x256);
+    load_lstm(u.shared, t, "predictor.shared", cin);
+    for (int s = 0; s < 2; s++) {
+        MResblk* blk = s == 0 ? u.f0 : u.nn;
+        const std::string nm = std::string("predictor.") + (s == 0 ? "F0" : "N");
+        load_resblk(blk[0], t, nm + ".0", HIDDEN, HIDDEN, false, sr);
+        load_resblk(blk[1], t, nm + ".1", HIDDEN, HIDDEN / 2, true, sr);
+        load_resblk(blk[2], t, nm + ".2", HIDDEN / 2, HIDDEN / 2, false, sr);
+    }
+    u.f0p_w.upload(t.get("predictor.F0_proj.weight", HIDDEN / 2), HIDDEN / 2);
+    u.f0p_b.upload(t.get("predictor.F0_proj.bias", 1), 1);
+    u.np_w.upload(t.get("predictor.N_proj.weight", HIDDEN / 2), HIDDEN / 2);
+    u.np_b.upload(t.get("predictor.N_proj.bias", 1), 1);
+    upload_style_table(u.style_wt, u.style_b, u.style_rows, sr);
+    u.ready = true;
+}
+
 static void load_model(kk_ctx* ctx, const kk_tensor* tensors, int n, bool norm_defaults = false) {
     Table t;
     t.norm_defaults = norm_defaults;
@@ -428,12 +577,10 @@ static void load_model(kk_ctx* ctx, const kk_tensor* tensors, int n, bool norm_d
         load_snake(m.rb[i], t, g + ".resblocks." + std::to_string(i), i < 3 ? 256 : 128, ks[i % 3], sr);
     load_conv(m.post, t, g + ".conv_post", 128, 22, 7, 3, 1, true, SHAPE_64x256);
     // style projections of every AdaIN, transposed [128][rows]
-    std::vector<float> wt((size_t)kStyleDim * sr.rows);
-    for (int r = 0; r < sr.rows; r++)
-        for (int k = 0; k < kStyleDim; k++) wt[(size_t)k * sr.rows + r] = sr.wt_rows[(size_t)r * kStyleDim + k];
-    m.style_wt.upload(wt);
-    m.style_b.upload(sr.bias);
-    m.style_rows = sr.rows;
+    upload_style_table(m.style_wt, m.style_b, m.style_rows, sr);
+    // the stages before the decoder, when the table holds them (kk_forward_batch needs them)
+    m.up.ready = false;
+    if (t.byname.count("bert.embeddings.word_embeddings.weight")) load_upstream(m.up, t);
     KK_HIP(hipDeviceSynchronize());
     m.ready = true;
 }
@@ -566,7 +713,7 @@ struct Tiles {
     }
 };
 
-enum PlanKind { PLAN_DECODER = 0, PLAN_GENERATOR = 1, PLAN_SNAKE = 2 };
+enum PlanKind { PLAN_DECODER = 0, PLAN_GENERATOR = 1, PLAN_SNAKE = 2, PLAN_FULL = 3 };
 
 }  // namespace kk
 
@@ -610,12 +757,27 @@ struct kk_plan {
     }
     bool frozen = false;  // tables uploaded: no more staging
     kk::DevBuf src_item, src_f0, ist_item, ist_s0;
+    // ids-level plans (PLAN_FULL): the stages before the decoder.  dt: the token rows by item (the
+    // text encoder's convolutions, the attention, the recurrences); dtf: every token row as one span
+    // (the linear layers: a row's output depends on that row only, so gap rows may be computed and
+    // are never read)
+    kk::Dom dt, dtf;
+    std::vector<int64_t> tstart, ntok;          // token layout
+    std::vector<std::vector<int64_t>> pred;     // predicted durations per item
+    kk::DevBuf tables_tok;                      // the token phase's staged tables
+    kk::DevBuf ids, row_item, att_item, att_head, att_q0, style_pro, gbp;
+    kk::DevBuf u_emb, u_h, u_qkv, u_ctx, u_ffn, u_x, u_gx, u_xl, u_logits, u_te, u_te2, u_gxt, u_gxs, u_sh;
+    kk::DevBuf u_fx[2], u_fpool[2], u_fh[2], u_fsc[2], u_fy[2];  // the F0 and N stacks
+    int64_t n_att = 0;
+    float* logits_host = nullptr;  // pinned, grow-only (the duration logits come back through it)
+    size_t logits_cap = 0;
+    hipEvent_t te_ev[2] = {nullptr, nullptr};  // fork / join of the text encoder and of the N stack
     kk::DevBuf pcm, pcm_len, pcm_clip;  // PCM_16 output: samples [600 ln], samples per item, clip counts
     int64_t n_src = 0, n_ist = 0;
     int64_t dev_bytes = 0;
     double conv_flop = 0, snake_flop = 0;
     int64_t launches = 0;
-    int last_until = 0;
+    int last_until = -1;  // the last run's stage (-1: none)
     // kk_plan_fetch_pcm16_async: recorded after its copies; pending until kk_plan_fetch_wait
     hipEvent_t fetch_ev = nullptr;
     bool fetch_pending = false;
@@ -626,6 +788,10 @@ struct kk_plan {
             if (e) (void)hipEventDestroy(e), e = nullptr;
         for (auto& e : noise_ev)
             if (e) (void)hipEventDestroy(e), e = nullptr;
+        for (auto& e : te_ev)
+            if (e) (void)hipEventDestroy(e), e = nullptr;
+        if (logits_host) (void)hipHostFree(logits_host);
+        logits_host = nullptr, logits_cap = 0;
     }
     // fork / join of the resblock chains, and of the noise branches (created with the plan)
     hipEvent_t chain_ev[3] = {nullptr, nullptr, nullptr};
@@ -635,7 +801,10 @@ struct kk_plan {
                 &xin_a, &xin_b, &hdec, &pool, &sc_half, &dec_out, &pp, &spec, &B[0], &B[1], &B[2], &B[3], &B[4], &B[5],
                 &post, &audio, &audio_start, &part, &coef[0], &coef[1], &coef[2], &coef[3], &coef[4], &coef[5],
                 &coef[6], &coef[7], &coef[8], &coef[9], &coef[10], &xs[0], &xs[1], &hn, &src_item, &src_f0,
-                &ist_item, &ist_s0, &pcm, &pcm_len, &pcm_clip};
+                &ist_item, &ist_s0, &pcm, &pcm_len, &pcm_clip, &tables_tok, &ids, &row_item, &att_item,
+                &att_head, &att_q0, &style_pro, &gbp, &u_emb, &u_h, &u_qkv, &u_ctx, &u_ffn, &u_x, &u_gx, &u_xl,
+                &u_logits, &u_te, &u_te2, &u_gxt, &u_gxs, &u_sh, &u_fx[0], &u_fx[1], &u_fpool[0], &u_fpool[1],
+                &u_fh[0], &u_fh[1], &u_fsc[0], &u_fsc[1], &u_fy[0], &u_fy[1]};
     }
 };
 
@@ -683,11 +852,12 @@ static void apply_test_hooks(kk_plan* p, int n) {
 static void reset_plan(kk_plan* p, int kind, int n) {
     p->kind = kind, p->nb = n;
     p->nfr.clear(), p->a.clear();
+    p->tstart.clear(), p->ntok.clear(), p->pred.clear(), p->n_att = 0;
     p->tiles.clear();
     p->frozen = false;
     p->sblk = nullptr, p->sc = 0;
     p->ln = 0, p->t_rows = 0, p->n_src = p->n_ist = 0;
-    p->conv_flop = p->snake_flop = 0, p->launches = 0, p->last_until = 0;
+    p->conv_flop = p->snake_flop = 0, p->launches = 0, p->last_until = -1;
     p->fetch_pending = false;
     apply_test_hooks(p, n);
 }
@@ -730,7 +900,10 @@ static void setup_generator(kk_plan* p, const std::vector<const float*>& f0s, co
     kk_ctx* ctx = p->ctx;
     const int nb = p->nb;
     const int64_t ln = p->ln, l2 = 2 * ln, l20 = 20 * ln, l120 = 120 * ln + 1;
-    {
+    if (f0s.empty()) {
+        // ids-level plans compute F0 on the device (F0_proj writes every row, 0 in the gaps)
+        alloc_buf(p, p->f0, (size_t)l2 * sizeof(float));
+    } else {
         // F0 in the d2 layout, 0 in the gaps (F0_conv reads one gap sample at each item edge)
         float* f0h = stage<float>(ctx, p->f0, (size_t)l2);
         std::memset(f0h, 0, sizeof(float) * l2);
@@ -872,16 +1045,17 @@ static void init_decoder_plan(kk_plan* p, const kk_decoder_item* items, int n) {
     stage_begin(ctx);
     build_frame_layout(p);
     const int64_t ln = p->ln;
-    // t_en in the token layout, channel-major [512][rows] (text_encoder_b output convention)
+    // t_en in the token layout, time-major [rows][512] (the items hand it over channel-major)
     p->t_rows = rows;
     {
         float* te = stage<float>(ctx, p->t_en, (size_t)512 * rows);
-        for (int c = 0; c < 512; c++)
-            for (int b = 0; b < n; b++) {
-                float* dst = te + (size_t)c * rows + tstart[b];
-                std::memcpy(dst, items[b].t_en + (size_t)c * items[b].n_tok, sizeof(float) * items[b].n_tok);
-                dst[items[b].n_tok] = dst[items[b].n_tok + 1] = 0.f;
-            }
+        for (int b = 0; b < n; b++) {
+            const int nt = items[b].n_tok;
+            float* dst = te + (size_t)tstart[b] * 512;
+            for (int i = 0; i < nt; i++)
+                for (int c = 0; c < 512; c++) dst[(size_t)i * 512 + c] = items[b].t_en[(size_t)c * nt + i];
+            std::memset(dst + (size_t)nt * 512, 0, sizeof(float) * 512 * kGapT);
+        }
     }
     // frame -> token row table (src/gpu_batch.rs:265-276), through kk_layout_src_row
     {
@@ -1023,7 +1197,12 @@ struct Runner {
     bool dry = false;  // build the plan's tile lists only, launch nothing
     double flop = 0, snake_flop = 0;
     int64_t launches = 0;
-    int64_t gb_ld() const { return m.style_rows; }
+    // AdaIN projections: the decoder + generator table (ref_s[0:128]) or, while pro_style is set,
+    // the prosody predictor's (ref_s[128:256])
+    bool pro_style = false;
+    const float* gbuf() const { return pro_style ? p->gbp.as<float>() : p->gb.as<float>(); }
+    int64_t gb_ld() const { return pro_style ? m.up.style_rows : m.style_rows; }
+    bool skip_tokens = false;  // the token phase ran at plan creation (kk_forward_batch)
     Coef* cf(int i) const { return p->coef[i].as<Coef>(); }
     int region = 0;  // statistics partials region of the current chain
     StatPart* part() const { return p->part.as<StatPart>() + (size_t)region * (size_t)(p->part_bytes / sizeof(StatPart)); }
@@ -1080,7 +1259,7 @@ struct Runner {
              const int64_t* xrow_at = nullptr) {
         const double bytes = (double)t.count * wn * c * sizeof(StatPart) + (double)p->nb * c * (sizeof(Coef) + 8);
         launch(PC_FINALIZE, 0, bytes, [&] {
-            return launch_finalize(part(), c, wn, t.dev(), p->nb, p->gb.as<float>(), gb_ld(), a.gb_off,
+            return launch_finalize(part(), c, wn, t.dev(), p->nb, gbuf(), gb_ld(), a.gb_off,
                                    a.nw.as<float>(), a.nb.as<float>(), coef, s, xrow, c, xrow_at);
         });
     }
@@ -1424,7 +1603,235 @@ struct Runner {
                [&] { return launch_istft(q, s); });
     }
 
+    // ------------------------------------------------------------ the stages before the decoder
+    // Linear L over the rows of domain d: x [rows][x_ld] -> y [rows][y_ld] (piece i at its columns).
+    void linear(const MLinear& L, const void* x, int64_t x_ld, const Dom& d, float* y, int64_t y_ld,
+                const std::string& name, int pro = PRO_F32, int epi = EPI_STORE) {
+        for (size_t i = 0; i < L.piece.size(); i++) {
+            Op o;
+            o.pro = pro, o.epi = epi, o.x = x, o.x_ld = x_ld, o.din = o.dout = &d, o.y = y + L.col0[i];
+            o.y_ld = y_ld, o.cls = PC_LINEAR, o.label = name;
+            conv(L.piece[i], o);
+        }
+    }
+    // BiLSTM recurrence over the item spans of d (gx rows through gx_row, or the spans' own rows);
+    // h into out[row][0:512].  Algorithmic traffic: gx read and h written once per row, W_hh once.
+    void recur(const MLstm& l, const float* gx, const int32_t* gx_row, const Dom& d, float* out, int64_t out_ld,
+               const std::string& name) {
+        const double v = (double)d.valid();
+        label = name;
+        launch(PC_LSTM, v * 2 * 1024 * 256 * 2, v * (2048 + 512) * 4 + 2.0 * 1024 * 257 * 4, [&] {
+            return launch_lstm(gx, 2048, gx_row, d.start_d.as<int64_t>(), d.len_d.as<int64_t>(), p->nb,
+                               l.whh_t.as<float>(), l.bhh.as<float>(), out, out_ld, s);
+        });
+    }
+    void layernorm(float* x, int64_t ld, int d, const float* g, const float* b, int gb_off, float eps, bool leaky,
+                   const std::string& name) {
+        const double v = (double)p->dt.valid();
+        label = name;
+        launch(PC_ROWS, 0, v * d * 8, [&] {
+            return launch_layernorm(x, ld, d, p->dtf.l, p->row_item.as<int32_t>(), g, b,
+                                    g ? nullptr : p->gbp.as<float>(), m.up.style_rows, gb_off, eps, leaky, 0.2f, s);
+        });
+    }
+    // text_encoder_b (src/gpu_batch.rs:457-481): embedding, 3 x (conv k5, LayerNorm, leaky 0.2),
+    // BiLSTM into t_en [rows][512].
+    void text_encoder() {
+        const MUp& u = m.up;
+        const Dom& dt = p->dt;
+        const int64_t R = p->dtf.l;
+        float* in = p->u_te.as<float>();
+        float* out = p->u_te2.as<float>();
+        label = "text_encoder.embedding";
+        launch(PC_ROWS, 0, (double)dt.valid() * 512 * 8, [&] {
+            return launch_text_embed(p->ids.as<int32_t>(), p->row_item.as<int32_t>(), R, u.te_emb.as<float>(), in, s);
+        });
+        for (int i = 0; i < 3; i++) {
+            const std::string nm = "text_encoder.cnn." + std::to_string(i);
+            Op o;
+            o.x = in, o.x_ld = 512, o.din = o.dout = &dt, o.y = out, o.y_ld = 512, o.cls = PC_PCONV, o.label = nm + ".0";
+            conv(u.te_cnn[i], o);
+            layernorm(out, 512, 512, u.te_g[i].as<float>(), u.te_b[i].as<float>(), 0, 1e-5f, true, nm + ".1");
+            std::swap(in, out);
+        }
+        linear(u.te_lstm.wih, in, 512, p->dtf, p->u_gxt.as<float>(), 2048, "text_encoder.lstm.ih");
+        recur(u.te_lstm, p->u_gxt.as<float>(), nullptr, dt, p->t_en.as<float>(), 512, "text_encoder.lstm");
+    }
+    // The token phase (src/gpu_batch.rs:198-248): ALBERT, bert_encoder, the duration encoder, the
+    // duration LSTM and projection (logits [rows][kLogitsLd]), the shared LSTM's gate
+    // pre-activations on the token rows; the text encoder beside them on side stream 0.
+    static constexpr int64_t kLogitsLd = 52;  // 50 logits, the row padded to the epilogue's 4 channels
+    void tokens() {
+        const MUp& u = m.up;
+        const Dom& dt = p->dt;
+        const Dom& dtf = p->dtf;
+        const int64_t R = dtf.l;
+        const double v = (double)dt.valid();
+        const bool conc = !ctx->profiling && !dry;
+        hipStream_t main_s = s;
+        if (conc) {
+            KK_HIP(hipEventRecord(p->te_ev[0], main_s));
+            KK_HIP(hipStreamWaitEvent(ctx->side[0], p->te_ev[0], 0));
+            s = ctx->side[0];
+        }
+        text_encoder();
+        if (conc) {
+            KK_HIP(hipEventRecord(p->te_ev[1], s));
+            s = main_s;
+        }
+        // prosody styles: every AdaLayerNorm / AdaIN projection of the predictor
+        label = "predictor.style_fc";
+        launch(PC_STYLE, 0, (double)u.style_rows * (kStyleDim + 1 + p->nb) * 4, [&] {
+            return launch_style_fc(u.style_wt.as<float>(), u.style_b.as<float>(), u.style_rows,
+                                   p->style_pro.as<float>(), p->nb, p->gbp.as<float>(), s);
+        });
+        // ALBERT (albert_b, src/gpu_batch.rs:423-455)
+        float* H = p->u_h.as<float>();
+        float* QKV = p->u_qkv.as<float>();
+        float* CTX = p->u_ctx.as<float>();
+        float* FF = p->u_ffn.as<float>();
+        label = "bert.embeddings";
+        launch(PC_ROWS, 0, v * 128 * 12, [&] {
+            return launch_albert_embed(p->ids.as<int32_t>(), p->row_item.as<int32_t>(), dt.start_d.as<int64_t>(), R,
+                                       u.word.as<float>(), u.pos.as<float>(), u.tok0.as<float>(), u.emb_g.as<float>(),
+                                       u.emb_b.as<float>(), p->u_emb.as<float>(), s);
+        });
+        linear(u.map_in, p->u_emb.p, 128, dtf, H, 768, "bert.embedding_hidden_mapping_in");
+        double att_flop = 0;
+        for (int64_t t : dt.len) att_flop += 12.0 * 4 * 64 * (double)t * (double)t;
+        for (int l = 0; l < 12; l++) {
+            const std::string nm = "bert.layer" + std::to_string(l);
+            linear(u.qkv, H, 768, dtf, QKV, 2304, nm + ".qkv");
+            label = nm + ".attention";
+            launch(PC_ATTN, att_flop, v * (2304 + 768) * 4, [&] {
+                return launch_attention(QKV, dt.start_d.as<int64_t>(), dt.len_d.as<int64_t>(),
+                                        p->att_item.as<int32_t>(), p->att_head.as<int32_t>(), p->att_q0.as<int32_t>(),
+                                        p->n_att, CTX, s);
+            });
+            linear(u.dense, CTX, 768, dtf, H, 768, nm + ".dense", PRO_F32, EPI_RESID);
+            layernorm(H, 768, 768, u.attn_g.as<float>(), u.attn_b.as<float>(), 0, 1e-12f, false, nm + ".attention_ln");
+            linear(u.ffn, H, 768, dtf, FF, 2048, nm + ".ffn");
+            linear(u.ffn_out, FF, 2048, dtf, H, 768, nm + ".ffn_output", PRO_GELU, EPI_RESID);
+            layernorm(H, 768, 768, u.full_g.as<float>(), u.full_b.as<float>(), 0, 1e-12f, false, nm + ".full_ln");
+        }
+        // duration encoder on x = [h | s] (640 wide): bert_encoder and each LSTM write h in place,
+        // the style half is written once (src/gpu_batch.rs:212-233)
+        float* X = p->u_x.as<float>();
+        float* GX = p->u_gx.as<float>();
+        linear(u.bert_enc, H, 768, dtf, X, 640, "bert_encoder");
+        label = "predictor.cat_style";
+        launch(PC_ROWS, 0, v * 128 * 4, [&] {
+            return launch_style_cols(X, 640, 512, R, p->row_item.as<int32_t>(), p->style_pro.as<float>(), s);
+        });
+        for (int i = 0; i < 3; i++) {
+            const std::string nm = "predictor.text_encoder.lstms." + std::to_string(2 * i);
+            linear(u.dur_lstm[i].wih, X, 640, dtf, GX, 2048, nm + ".ih");
+            recur(u.dur_lstm[i], GX, nullptr, dt, X, 640, nm);
+            layernorm(X, 640, 512, nullptr, nullptr, u.dur_gb_off[i], 1e-5f, false,
+                      "predictor.text_encoder.lstms." + std::to_string(2 * i + 1));
+        }
+        linear(u.pred_lstm.wih, X, 640, dtf, GX, 2048, "predictor.lstm.ih");
+        recur(u.pred_lstm, GX, nullptr, dt, p->u_xl.as<float>(), 512, "predictor.lstm");
+        linear(u.dur_proj, p->u_xl.p, 512, dtf, p->u_logits.as<float>(), kLogitsLd, "predictor.duration_proj");
+        // the shared LSTM's gate pre-activations on the token rows: a frame's are its token's
+        linear(u.shared.wih, X, 640, dtf, p->u_gxs.as<float>(), 2048, "predictor.shared.ih");
+        if (conc) KK_HIP(hipStreamWaitEvent(main_s, p->te_ev[1], 0));
+    }
+    // AdainResBlk1d with an identity shortcut (din = dout), in place on X [rows][ld] of domain d.
+    void resblk_same(const MResblk& r, float* X, int64_t ld, const Dom& d, float* h, Coef* ca, Coef* cb) {
+        stats_fin(X, ld, r.din, d, r.n1, ca);
+        Op o1;
+        o1.pro = PRO_ADAIN_LEAKY, o1.x = X, o1.x_ld = ld, o1.din = o1.dout = &d, o1.y = h, o1.y_ld = r.dout;
+        o1.coef = ca, o1.slope = 0.2f, o1.stats = true, o1.cls = PC_PCONV, o1.label = r.name + ".conv1";
+        const Tiles& t = conv(r.conv1, o1);
+        fin(t, kShapeWN[r.conv1.shape], r.dout, r.n2, cb);
+        Op o2;
+        o2.pro = PRO_ADAIN_LEAKY, o2.epi = EPI_RESID, o2.x = h, o2.x_ld = r.dout, o2.din = o2.dout = &d, o2.y = X;
+        o2.y_ld = ld, o2.coef = cb, o2.slope = 0.2f, o2.scale = 1.0f / sqrtf(2.0f), o2.cls = PC_PCONV;
+        o2.label = r.name + ".conv2";
+        conv(r.conv2, o2);
+    }
+    // The upsampling AdainResBlk1d (src/gpu_batch.rs:104-135): X [ln][xld] at dn -> Y [2 ln][yld] at d2.
+    void resblk_up(const MResblk& r, const float* X, int64_t xld, float* Y, int64_t yld, uint16_t* pool, float* h,
+                   float* sc, Coef* ca, Coef* cb) {
+        const Dom& dn = p->dn;
+        const Dom& d2 = p->d2;
+        const double nf = (double)frames();
+        stats_fin(X, xld, r.din, dn, r.n1, ca);
+        label = r.name + ".pool";
+        launch(PC_POOL, 0, nf * r.din * 4 + 2 * nf * r.din * 2, [&] {
+            return launch_adain_pool(X, xld, r.din, ca, dn.col_d.as<int32_t>(), p->ln, r.pool_w.as<float>(),
+                                     r.pool_b.as<float>(), d2.col_d.as<int32_t>(), pool, r.din, s);
+        });
+        Op o1;
+        o1.pro = PRO_BF16, o1.x = pool, o1.x_ld = r.din, o1.din = o1.dout = &d2, o1.y = h, o1.y_ld = r.dout;
+        o1.stats = true, o1.cls = PC_PCONV, o1.label = r.name + ".conv1";
+        const Tiles& t = conv(r.conv1, o1);
+        fin(t, kShapeWN[r.conv1.shape], r.dout, r.n2, cb);
+        // shortcut conv1x1(nearest x2 (x)) = nearest x2 (conv1x1(x)) for a 1x1 conv: computed at N
+        Op os;
+        os.x = X, os.x_ld = xld, os.din = os.dout = &dn, os.y = sc, os.y_ld = r.dout, os.cls = PC_PCONV;
+        os.label = r.name + ".conv1x1";
+        conv(r.conv1x1, os);
+        Op o2;
+        o2.pro = PRO_ADAIN_LEAKY, o2.epi = EPI_RESID_UP2, o2.x = h, o2.x_ld = r.dout, o2.din = o2.dout = &d2;
+        o2.y = Y, o2.y_ld = yld, o2.coef = cb, o2.slope = 0.2f, o2.r0 = sc, o2.r0_ld = r.dout;
+        o2.scale = 1.0f / sqrtf(2.0f), o2.cls = PC_PCONV, o2.label = r.name + ".conv2";
+        conv(r.conv2, o2);
+    }
+    // F0 (k = 0) or N (k = 1) from the shared LSTM's output (src/gpu_batch.rs:282-292) into p->f0 /
+    // p->en at d2, 0 in the gaps.
+    void f0n_stack(int k, Coef* ca, Coef* cb) {
+        const MUp& u = m.up;
+        const MResblk* blk = k == 0 ? u.f0 : u.nn;
+        float* fx = p->u_fx[k].as<float>();
+        float* fh = p->u_fh[k].as<float>();
+        float* fy = p->u_fy[k].as<float>();
+        const double nf = (double)frames();
+        launch(PC_COPY, 0, nf * 512 * 8, [&] {
+            return launch_copy_cols(p->u_sh.as<float>(), 512, 512, fx, 512, 0, p->dn.col_d.as<int32_t>(), p->ln, s);
+        });
+        resblk_same(blk[0], fx, 512, p->dn, fh, ca, cb);
+        resblk_up(blk[1], fx, 512, fy, 256, p->u_fpool[k].as<uint16_t>(), fh, p->u_fsc[k].as<float>(), ca, cb);
+        resblk_same(blk[2], fy, 256, p->d2, fh, ca, cb);
+        label = k == 0 ? "predictor.F0_proj" : "predictor.N_proj";
+        launch(PC_ROWS, 2.0 * 2 * nf * 256, 2 * nf * 256 * 4 + 2 * (double)p->ln * 4, [&] {
+            return launch_proj1(fy, 256, 256, (k == 0 ? u.f0p_w : u.np_w).as<float>(),
+                                (k == 0 ? u.f0p_b : u.np_b).as<float>(), p->d2.col_d.as<int32_t>(), 2 * p->ln,
+                                (k == 0 ? p->f0 : p->en).as<float>(), s);
+        });
+    }
+    // The frame phase before the decoder: the shared BiLSTM over the frames (a frame's gate
+    // pre-activations are its token row's, through src_row), then the F0 and N stacks, N on side
+    // stream 0 beside F0 (each with its own statistics region and AdaIN coefficients).
+    void prosody() {
+        recur(m.up.shared, p->u_gxs.as<float>(), p->src_row.as<int32_t>(), p->dn, p->u_sh.as<float>(), 512,
+              "predictor.shared");
+        pro_style = true;
+        const bool conc = !ctx->profiling && !dry;
+        hipStream_t main_s = s;
+        if (conc) {
+            KK_HIP(hipEventRecord(p->te_ev[0], main_s));
+            KK_HIP(hipStreamWaitEvent(ctx->side[0], p->te_ev[0], 0));
+            s = ctx->side[0], region = 1;
+            f0n_stack(1, cf(5), cf(6));
+            KK_HIP(hipEventRecord(p->te_ev[1], s));
+            s = main_s, region = 0;
+            f0n_stack(0, cf(0), cf(1));
+            KK_HIP(hipStreamWaitEvent(main_s, p->te_ev[1], 0));
+        } else {
+            f0n_stack(0, cf(0), cf(1));
+            f0n_stack(1, cf(0), cf(1));
+        }
+        pro_style = false;
+    }
+
     void run(int until) {
+        if (p->kind == PLAN_FULL) {
+            if (!skip_tokens) tokens();
+            prosody();
+            if (until <= KK_STAGE_PROSODY) return;
+        }
         launch(PC_STYLE, 0, (double)m.style_rows * (kStyleDim + 1 + p->nb) * 4, [&] {
             return launch_style_fc(m.style_wt.as<float>(), m.style_b.as<float>(), m.style_rows, p->style.as<float>(),
                                    p->nb, p->gb.as<float>(), s);
@@ -1451,7 +1858,7 @@ struct Runner {
             }
             s = main_s;
         }
-        if (p->kind == PLAN_DECODER) decoder();
+        if (p->kind == PLAN_DECODER || p->kind == PLAN_FULL) decoder();
         if (until <= KK_STAGE_DECODER) return;
         if (!conc) source();
         if (until <= KK_STAGE_SOURCE) return;
@@ -1480,10 +1887,160 @@ static void prebuild_tiles(kk_plan* p) {
     r.run(KK_STAGE_ALL);
 }
 
+// Fills plan p (new, or the one-shot plan whose device buffers are reused) for an ids-level batch
+// (GpuKokoro::forward_batch, src/gpu_batch.rs:179-297).  Phase A, at once: the token layout
+// (src/gpu_batch.rs:188-197), the token phase on the device, its logits back to the host and the
+// durations (src/gpu_batch.rs:234-248).  Phase B: the frame layout and everything after, as a
+// decoder plan whose t_en, F0 and N the plan computes itself.
+static void init_full_plan(kk_plan* p, const kk_item* items, int n) {
+    kk_ctx* ctx = p->ctx;
+    const Model& m = ctx->model;
+    check(m.ready && m.up.ready, "no model with the stages before the decoder uploaded");
+    check(items != nullptr && n > 0, "empty batch");
+    reset_plan(p, PLAN_FULL, n);
+    int64_t rows = 0;
+    p->tstart.assign(n, 0), p->ntok.assign(n, 0);
+    for (int b = 0; b < n; b++) {
+        const kk_item& it = items[b];
+        const std::string sb = std::to_string(b);
+        // src/gpu_batch.rs:182-187
+        check(it.ids != nullptr && it.ref_s != nullptr, "item " + sb + ": null input");
+        check(it.n_ids >= 2 && it.n_ids <= 512, "item " + sb + ": input_ids length outside [2, 512]");
+        check(std::isfinite(it.speed) && it.speed > 0.f, "item " + sb + ": speed must be positive and finite");
+        for (int i = 0; i < it.n_ids; i++)
+            check(it.ids[i] >= 0 && it.ids[i] < 178, "item " + sb + ": token id " + std::to_string(it.ids[i]) +
+                                                          " out of range");
+        check(it.noise_kind == KK_NOISE_COUNTER || it.noise_kind == KK_NOISE_FIXED, "item " + sb + ": unknown noise kind");
+        p->tstart[b] = rows, p->ntok[b] = it.n_ids;
+        rows += it.n_ids + kGapT;
+    }
+    // ---- phase A: the token phase
+    stage_begin(ctx);
+    p->dt.build(ctx, rows, p->tstart, p->ntok, false, p->nomask);
+    p->dtf.build(ctx, rows, {0}, {rows}, false, p->nomask);
+    {
+        int32_t* idh = stage<int32_t>(ctx, p->ids, (size_t)rows);
+        for (int64_t r = 0; r < rows; r++) idh[r] = 0;
+        for (int b = 0; b < n; b++)
+            for (int i = 0; i < items[b].n_ids; i++) idh[p->tstart[b] + i] = (int32_t)items[b].ids[i];
+    }
+    {
+        int32_t* ri = stage<int32_t>(ctx, p->row_item, (size_t)rows);
+        for (int64_t r = 0; r < rows; r++) ri[r] = -1;
+        for (int b = 0; b < n; b++)
+            for (int i = 0; i < items[b].n_ids; i++) ri[p->tstart[b] + i] = b;
+    }
+    {
+        float* sp = stage<float>(ctx, p->style_pro, (size_t)n * kStyleDim);
+        for (int b = 0; b < n; b++) std::memcpy(&sp[(size_t)b * kStyleDim], items[b].ref_s + kStyleDim, sizeof(float) * kStyleDim);
+    }
+    {
+        // attention work list: (item, head, first query) per 16 queries
+        std::vector<int32_t> wi, wh, wq;
+        for (int b = 0; b < n; b++)
+            for (int h = 0; h < 12; h++)
+                for (int q = 0; q < items[b].n_ids; q += 16) wi.push_back(b), wh.push_back(h), wq.push_back(q);
+        p->n_att = (int64_t)wi.size();
+        stage_vec(ctx, p->att_item, wi), stage_vec(ctx, p->att_head, wh), stage_vec(ctx, p->att_q0, wq);
+    }
+    const size_t R = (size_t)rows;
+    alloc_buf(p, p->gbp, (size_t)n * m.up.style_rows * sizeof(float));
+    alloc_buf(p, p->u_emb, R * 128 * sizeof(float));
+    alloc_buf(p, p->u_h, R * 768 * sizeof(float));
+    alloc_buf(p, p->u_qkv, R * 2304 * sizeof(float));
+    alloc_buf(p, p->u_ctx, R * 768 * sizeof(float));
+    alloc_buf(p, p->u_ffn, R * 2048 * sizeof(float));
+    alloc_buf(p, p->u_x, R * 640 * sizeof(float));
+    alloc_buf(p, p->u_gx, R * 2048 * sizeof(float));
+    alloc_buf(p, p->u_xl, R * 512 * sizeof(float));
+    alloc_buf(p, p->u_logits, R * Runner::kLogitsLd * sizeof(float));
+    alloc_buf(p, p->u_te, R * 512 * sizeof(float));
+    alloc_buf(p, p->u_te2, R * 512 * sizeof(float));
+    alloc_buf(p, p->u_gxt, R * 2048 * sizeof(float));
+    alloc_buf(p, p->u_gxs, R * 2048 * sizeof(float));
+    alloc_buf(p, p->t_en, R * 512 * sizeof(float));
+    p->t_rows = rows;
+    for (auto& e : p->te_ev)
+        if (!e) KK_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+    {
+        Runner r{p, ctx, m, ctx->stream};
+        r.dry = true;  // builds (stages) the token phase's tile lists and validates its launches
+        r.tokens();
+    }
+    stage_flush(ctx, p->tables_tok, ctx->stream);
+    {
+        Runner r{p, ctx, m, ctx->stream};
+        r.tokens();
+    }
+    const size_t lg_bytes = R * Runner::kLogitsLd * sizeof(float);
+    if (p->logits_cap < lg_bytes) {
+        if (p->logits_host) (void)hipHostFree(p->logits_host);
+        p->logits_host = nullptr, p->logits_cap = 0;
+        KK_HIP(hipHostMalloc((void**)&p->logits_host, lg_bytes, hipHostMallocDefault));
+        p->logits_cap = lg_bytes;
+    }
+    KK_HIP(hipMemcpyAsync(p->logits_host, p->u_logits.p, lg_bytes, hipMemcpyDeviceToHost, ctx->stream));
+    KK_HIP(hipStreamSynchronize(ctx->stream));
+    // durations_from_logits (src/model.rs:90-100) per item
+    p->pred.assign(n, {});
+    std::vector<float> lg;
+    for (int b = 0; b < n; b++) {
+        const int t = items[b].n_ids;
+        lg.resize((size_t)t * 50);
+        for (int i = 0; i < t; i++)
+            std::memcpy(&lg[(size_t)i * 50], p->logits_host + (size_t)(p->tstart[b] + i) * Runner::kLogitsLd,
+                        sizeof(float) * 50);
+        p->pred[b].assign(t, 0);
+        check(kk_durations_from_logits(lg.data(), t, items[b].speed, p->pred[b].data()) == KK_OK, "durations");
+        int64_t nf = 0;
+        for (int64_t d : p->pred[b]) nf += d;
+        check(nf <= (int64_t)1 << 22, "item " + std::to_string(b) + ": too many frames");
+        check_noise(NoiseIn{items[b].noise_kind, items[b].seed, items[b].rand_ini, items[b].sine, items[b].sine_len},
+                    nf, b);
+        p->nfr.push_back(nf);
+    }
+    // ---- phase B: the frame layout and the decoder + generator inputs
+    stage_begin(ctx);
+    build_frame_layout(p);
+    const int64_t ln = p->ln;
+    {
+        std::vector<const int64_t*> durs(n);
+        std::vector<int32_t> nt(n);
+        for (int b = 0; b < n; b++) durs[b] = p->pred[b].data(), nt[b] = (int32_t)p->ntok[b];
+        int32_t* sr = stage<int32_t>(ctx, p->src_row, (size_t)ln);
+        check(kk_layout_src_row(durs.data(), nt.data(), n, p->tstart.data(), p->a.data(), ln, sr) == KK_OK,
+              "duration expansion overflows the frame layout");
+    }
+    std::vector<const float*> refs(n);
+    std::vector<NoiseIn> nz(n);
+    for (int b = 0; b < n; b++) {
+        refs[b] = items[b].ref_s;
+        nz[b] = NoiseIn{items[b].noise_kind, items[b].seed, items[b].rand_ini, items[b].sine, items[b].sine_len};
+    }
+    setup_generator(p, {}, refs, nz);
+    alloc_buf(p, p->en, (size_t)2 * ln * sizeof(float));
+    alloc_buf(p, p->u_sh, (size_t)ln * 512 * sizeof(float));
+    for (int k = 0; k < 2; k++) {
+        alloc_buf(p, p->u_fx[k], (size_t)ln * 512 * sizeof(float));
+        alloc_buf(p, p->u_fpool[k], (size_t)2 * ln * 512 * sizeof(uint16_t));
+        alloc_buf(p, p->u_fh[k], (size_t)2 * ln * 256 * sizeof(float));
+        alloc_buf(p, p->u_fsc[k], (size_t)ln * 256 * sizeof(float));
+        alloc_buf(p, p->u_fy[k], (size_t)2 * ln * 256 * sizeof(float));
+    }
+    alloc_buf(p, p->xcat, (size_t)ln * kXcatLd * sizeof(float));
+    alloc_buf(p, p->xin_a, (size_t)ln * kXinLd * sizeof(float));
+    alloc_buf(p, p->xin_b, (size_t)ln * kXinLd * sizeof(float));
+    alloc_buf(p, p->hdec, (size_t)ln * 1024 * sizeof(float));
+    alloc_buf(p, p->pool, (size_t)2 * ln * kXinLd * sizeof(uint16_t));
+    alloc_buf(p, p->sc_half, (size_t)ln * 512 * sizeof(float));
+    alloc_buf(p, p->dec_out, (size_t)2 * ln * 512 * sizeof(float));
+    finish_plan(p);
+}
+
 static void release_plan_device(kk_plan* p) {
     p->drop_events();
     p->tiles.clear();
-    for (kk::Dom* d : {&p->dn, &p->d2, &p->d20, &p->d120, &p->ds}) d->release();
+    for (kk::Dom* d : {&p->dn, &p->d2, &p->d20, &p->d120, &p->ds, &p->dt, &p->dtf}) d->release();
     for (DevBuf* b : p->owned()) b->release();
     p->ctx = nullptr;
 }
@@ -1600,7 +2157,7 @@ struct kk_checkpoint {
 };
 
 namespace kk {
-// The decoder's tensors of a checkpoint as the weight table kk_upload_model takes, with weight_norm
+// The model's tensors of a checkpoint as the weight table kk_upload_model takes, with weight_norm
 // resolved: a conv whose "X.weight" is absent is built from "X.weight_g" / "X.weight_v"
 // (Weights::conv_weight, src/weights.rs:62-73).
 static void upload_checkpoint(kk_ctx* ctx, const kk_checkpoint* ck) {
@@ -1609,7 +2166,10 @@ static void upload_checkpoint(kk_ctx* ctx, const kk_checkpoint* ck) {
     std::vector<std::unique_ptr<std::string>> names;
     for (const auto& kv : ck->t) {
         const std::string& nm = kv.first;
-        if (nm.compare(0, 8, "decoder.") != 0) continue;
+        static const char* const kPrefixes[] = {"decoder.", "bert.", "bert_encoder.", "predictor.", "text_encoder."};
+        bool keep = false;
+        for (const char* pre : kPrefixes) keep = keep || nm.compare(0, std::strlen(pre), pre) == 0;
+        if (!keep) continue;
         tab.push_back(kk_tensor{nm.c_str(), kv.second.data.data(), (int64_t)kv.second.data.size()});
         const std::string suf = ".weight_v";
         if (nm.size() > suf.size() && nm.compare(nm.size() - suf.size(), suf.size(), suf) == 0) {
@@ -1660,13 +2220,16 @@ static_assert(kNaTotal <= KK_NOALLOC_SCRATCH_BYTES, "scratch regions exceed the 
 static __device__ __align__(256) unsigned char scratch[KK_NOALLOC_SCRATCH_BYTES];
 
 namespace kk {
-static void run_plan(kk_plan* plan, int until) {
+static void run_plan(kk_plan* plan, int until, bool skip_tokens = false) {
     use_device(plan->ctx);
     check(plan->ctx->model.ready, "no model uploaded");
-    check(until >= KK_STAGE_DECODER && until <= KK_STAGE_ALL, "unknown stage");
+    check(plan->kind != PLAN_FULL || plan->ctx->model.up.ready, "no model with the stages before the decoder uploaded");
+    check(until >= (plan->kind == PLAN_FULL ? KK_STAGE_PROSODY : KK_STAGE_DECODER) && until <= KK_STAGE_ALL,
+          "unknown stage");
     hipStream_t s = plan->ctx->stream;
     Runner r{plan, plan->ctx, plan->ctx->model, s};
-    plan->last_until = 0;
+    r.skip_tokens = skip_tokens;
+    plan->last_until = -1;
     try {
         // Eager launches: the generator's three resblock chains run on three streams at once, which
         // a captured HIP graph executes one node at a time on this runtime (measured: the graph
@@ -1939,6 +2502,25 @@ int kk_plan_create(kk_ctx* ctx, const kk_decoder_item* items, int n, kk_plan** o
     });
 }
 
+int kk_plan_create_full(kk_ctx* ctx, const kk_item* items, int n, kk_plan** out, char* err, size_t errlen) {
+    if (!ctx || !out) return KK_ERR_INVALID;
+    *out = nullptr;
+    return guard(err, errlen, [&] {
+        use_device(ctx);
+        auto p = std::make_unique<kk_plan>();
+        p->ctx = ctx;
+        init_full_plan(p.get(), items, n);
+        *out = register_plan(ctx, std::move(p));
+    });
+}
+
+int kk_plan_durations(const kk_plan* plan, int item, const int64_t** dur, int32_t* n_tok) {
+    if (!plan || !dur || !n_tok || plan->kind != PLAN_FULL || item < 0 || item >= plan->nb) return KK_ERR_INVALID;
+    *dur = plan->pred[item].data();
+    *n_tok = (int32_t)plan->pred[item].size();
+    return KK_OK;
+}
+
 int kk_plan_create_generator(kk_ctx* ctx, const kk_generator_item* items, int n, kk_plan** out, char* err,
                              size_t errlen) {
     if (!ctx || !out) return KK_ERR_INVALID;
@@ -2203,8 +2785,30 @@ int kk_plan_tap(kk_plan* plan, const char* name, int item, float* dst, int64_t c
         const std::string n(name);
         const int64_t N = plan->nfr[item], a = plan->a[item];
         auto need = [&](int64_t c) { check(count == c, "tap " + n + " holds " + std::to_string(c) + " values"); };
-        if (n == "asr") {
-            check(plan->kind == PLAN_DECODER, "asr exists in decoder plans only");
+        const bool full = plan->kind == PLAN_FULL;
+        auto full_only = [&] { check(full, n + " exists in ids-level plans only"); };
+        const int64_t T = full ? plan->ntok[item] : 0, ts = full ? plan->tstart[item] : 0;
+        if (n == "bert") {
+            full_only(), need(768 * T);
+            tap_rows(plan->u_h.p, 768, ts, T, 768, dst);
+        } else if (n == "d") {
+            full_only(), need(640 * T);
+            tap_rows(plan->u_x.p, 640, ts, T, 640, dst);
+        } else if (n == "logits") {
+            full_only(), need(50 * T);
+            tap_rows(plan->u_logits.p, Runner::kLogitsLd, ts, T, 50, dst);
+        } else if (n == "t_en") {
+            full_only(), need(512 * T);
+            tap_rows(plan->t_en.p, 512, ts, T, 512, dst);
+        } else if (n == "shared") {
+            full_only(), need(512 * N);
+            tap_rows(plan->u_sh.p, 512, a, N, 512, dst);
+        } else if (n == "f0" || n == "n") {
+            full_only(), need(2 * N);
+            KK_HIP(hipMemcpy(dst, (n == "f0" ? plan->f0 : plan->en).as<float>() + 2 * a, sizeof(float) * 2 * N,
+                             hipMemcpyDeviceToHost));
+        } else if (n == "asr") {
+            check(plan->kind == PLAN_DECODER || full, "asr exists in decoder and ids-level plans only");
             need(512 * N);
             tap_rows(plan->xcat.p, kXcatLd, a, N, 512, dst);
         } else if (n == "decoder") {
@@ -2295,6 +2899,64 @@ int kk_forward_decoder_batch(kk_ctx* ctx, const kk_decoder_item* items, int n, k
     });
     if (rc != KK_OK) kk_output_free(out, n);
     return rc;
+}
+
+int kk_forward_batch(kk_ctx* ctx, const kk_item* items, int n, kk_result* out, char* err, size_t errlen) {
+    if (!ctx || !out || n < 0) return KK_ERR_INVALID;
+    for (int b = 0; b < n; b++) out[b] = kk_result{nullptr, 0, nullptr, 0};
+    std::vector<kk_output> audio(std::max(n, 0), kk_output{nullptr, 0});
+    int rc = guard(err, errlen, [&] {
+        use_device(ctx);
+        if (!ctx->oneshot) {
+            ctx->oneshot = new kk_plan();
+            ctx->oneshot->ctx = ctx;
+        }
+        try {
+            static const bool timing = env_i64("KOKORO_HIP_TIMING", 0) != 0;
+            const auto t0 = std::chrono::steady_clock::now();
+            init_full_plan(ctx->oneshot, items, n);  // the token phase runs here
+            const auto t1 = std::chrono::steady_clock::now();
+            run_plan(ctx->oneshot, KK_STAGE_ALL, true);
+            if (timing) KK_HIP(hipStreamSynchronize(ctx->stream));
+            const auto t2 = std::chrono::steady_clock::now();
+            fetch_plan(ctx->oneshot, audio.data());
+            for (int b = 0; b < n; b++) {
+                const auto& d = ctx->oneshot->pred[b];
+                out[b].pred_dur = (int64_t*)std::malloc(sizeof(int64_t) * d.size());
+                if (!out[b].pred_dur) throw std::bad_alloc();
+                std::memcpy(out[b].pred_dur, d.data(), sizeof(int64_t) * d.size());
+                out[b].n_tok = (int32_t)d.size();
+            }
+            for (int b = 0; b < n; b++) out[b].audio = audio[b].audio, out[b].n_samples = audio[b].n_samples;
+            const auto t3 = std::chrono::steady_clock::now();
+            if (timing) {
+                auto ms = [](auto a, auto b) { return std::chrono::duration<double, std::milli>(b - a).count(); };
+                std::fprintf(stderr, "kk_forward_batch: tokens + durations %.3f ms, frames %.3f ms, fetch %.3f ms\n",
+                             ms(t0, t1), ms(t1, t2), ms(t2, t3));
+            }
+        } catch (...) {
+            drop_oneshot(ctx);
+            throw;
+        }
+    });
+    if (rc != KK_OK) {
+        kk_output_free(audio.data(), n);
+        for (int b = 0; b < n; b++) {
+            std::free(out[b].pred_dur);
+            out[b] = kk_result{nullptr, 0, nullptr, 0};
+        }
+    }
+    return rc;
+}
+
+void kk_result_free(kk_result* out, int n) {
+    if (!out) return;
+    for (int b = 0; b < n; b++) {
+        kk_output o{out[b].audio, out[b].n_samples};
+        kk_output_free(&o, 1);
+        std::free(out[b].pred_dur);
+        out[b] = kk_result{nullptr, 0, nullptr, 0};
+    }
 }
 
 void kk_output_free(kk_output* out, int n) {

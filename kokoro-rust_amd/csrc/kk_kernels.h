@@ -31,6 +31,7 @@ enum Prologue {
     PRO_LEAKY = 2,        // leaky ReLU(slope)
     PRO_ADAIN_LEAKY = 3,  // AdaIN (per item, per channel affine) + leaky ReLU(slope)
     PRO_ADAIN_SNAKE = 4,  // AdaIN + Snake x + sin^2(a x)/a
+    PRO_GELU = 5,         // gelu_new (kernels/kokoro.cu:84-90)
 };
 enum Epilogue {
     EPI_STORE = 0,          // y = conv + b
@@ -101,7 +102,8 @@ hipError_t launch_finalize(const StatPart* part, int c, int wn, TilesDev t, int 
 // gb[b][j] = W[j] . style[b] + bias[j] for every AdaIN layer at once.
 hipError_t launch_style_fc(const float* w, const float* bias, int rows, const float* style, int nb, float* gb,
                            hipStream_t s);
-// asr[t][c] = t_en[c][src_row[t]] (0 in gaps), time-major [l][ld] with channels [0, 512).
+// asr[t][c] = t_en[src_row[t]][c] (0 in gaps): t_en token rows [t_rows][512] -> frame rows [l][ld],
+// channels [0, 512).
 hipError_t launch_expand(const float* t_en, int64_t t_rows, const int32_t* src_row, int64_t l, float* asr,
                          int64_t ld, hipStream_t s);
 // F0_conv / N_conv: 1 -> 1 channel, k3 s2 p1 on d2 -> dn; out at columns col_f0 / col_n of [ln][ld].
@@ -174,6 +176,39 @@ hipError_t launch_pcm16(const float* audio, const int64_t* audio_start, const in
 // graph); bytes is a multiple of 4.
 hipError_t launch_zero(void* p, int64_t bytes, hipStream_t s);
 hipError_t launch_fill(void* p, int64_t bytes, uint32_t value, hipStream_t s);
+
+// ---------------------------------------------------------------- stages before the decoder (kk_upstream.hip)
+// Row tables: row_item [rows] (owning item, -1 in gaps), ids [rows] (token id), start [nb] (first
+// row of each item).  Gap rows are neither read nor written.
+// ALBERT embeddings + LayerNorm 1e-12 -> out [rows][128].
+hipError_t launch_albert_embed(const int32_t* ids, const int32_t* row_item, const int64_t* start, int64_t rows,
+                               const float* word, const float* pos, const float* tok0, const float* g, const float* b,
+                               float* out, hipStream_t s);
+// text encoder embedding -> out [rows][512].
+hipError_t launch_text_embed(const int32_t* ids, const int32_t* row_item, int64_t rows, const float* emb, float* out,
+                             hipStream_t s);
+// LayerNorm of channels [0, d) (d = 512 or 768) of x [rows][ld] in place: affine g, b, or
+// AdaLayerNorm with gb (gamma at gb[item][gb_off + c], beta at gb[item][gb_off + d + c]) when gb is
+// not null; then leaky ReLU(slope) when leaky.
+hipError_t launch_layernorm(float* x, int64_t ld, int d, int64_t rows, const int32_t* row_item, const float* g,
+                            const float* b, const float* gb, int64_t gb_ld, int gb_off, float eps, bool leaky,
+                            float slope, hipStream_t s);
+// ALBERT attention, 12 heads of 64, scale 1/8: qkv [rows][2304] -> out [rows][768]; work list of
+// (item, head, first query) blocks of 16 queries; items of at most 512 tokens.
+hipError_t launch_attention(const float* qkv, const int64_t* start, const int64_t* len, const int32_t* w_item,
+                            const int32_t* w_head, const int32_t* w_q0, int64_t n_blocks, float* out, hipStream_t s);
+// BiLSTM recurrence, H = 256, over the item spans [start, start + len): gx [*][gx_ld] gate
+// pre-activations (W_ih x + b_ih, forward at columns [0, 1024), reverse at [1024, 2048)) at row
+// gx_row[r] (or r when gx_row is null); whh_t [2][256][1024] (k-major), bhh [2][1024];
+// h -> out[r][dir 256 + j].
+hipError_t launch_lstm(const float* gx, int64_t gx_ld, const int32_t* gx_row, const int64_t* start, const int64_t* len,
+                       int nb, const float* whh_t, const float* bhh, float* out, int64_t out_ld, hipStream_t s);
+// F0_proj / N_proj: y[r] = b + w . x[r][0:c] (c = 256) on the rows with col[r] >= 0, 0 elsewhere.
+hipError_t launch_proj1(const float* x, int64_t ld, int c, const float* w, const float* b, const int32_t* col,
+                        int64_t rows, float* y, hipStream_t s);
+// x[r][col0 .. col0 + 128) = styles[row_item[r]] for the item rows.
+hipError_t launch_style_cols(float* x, int64_t ld, int col0, int64_t rows, const int32_t* row_item,
+                             const float* styles, hipStream_t s);
 
 constexpr int kSourceFrames = 128;  // STFT frames per source block
 constexpr int kIstftSamples = 512;  // output samples per iSTFT block

@@ -167,7 +167,7 @@ __global__ void expand_kernel(const float* __restrict__ t_en, int64_t t_rows, co
     const int64_t t = i >> 9;
     const int ch = (int)(i & 511);
     const int32_t r = src_row[t];
-    asr[t * ld + ch] = r < 0 ? 0.0f : t_en[(int64_t)ch * t_rows + r];
+    asr[t * ld + ch] = r < 0 ? 0.0f : t_en[(int64_t)r * 512 + ch];
 }
 
 // F0_conv / N_conv (src/vocoder.rs:106-107): Conv1d 1->1 k3 s2 p1, d2 -> dn, f32; gap rows -> 0.

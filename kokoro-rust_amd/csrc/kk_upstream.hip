@@ -1,0 +1,347 @@
+// kk_upstream.hip -- gfx950 kernels of the stages before the decoder (src/gpu_batch.rs:179-297):
+// the ALBERT and text-encoder embeddings, LayerNorm / AdaLayerNorm over rows, ALBERT's per-item
+// attention and the BiLSTM recurrence.  The linear layers and the text encoder's convolutions run
+// on the MFMA conv kernel (kk_conv.hip) with bf16 operands and f32 accumulation, as the reference's
+// GLinear / fused BF16 conv do (src/gpu.rs:280-301); everything here is f32.
+//
+// Token rows use the packed time-major layout of the decoder: items along the rows with gap rows
+// between them, row_item[r] = owning item or -1.  Gap rows are never read by a consumer (the
+// convolutions mask by item span, the attention and the recurrence read their item's rows only), so
+// these kernels do not write them.
+#include "kk_kernels.h"
+
+namespace kk {
+namespace {
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+__device__ __forceinline__ float sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+// Albert::embeddings (src/albert.rs:70-81): (word[id] + token_type[0]) + position[t], LayerNorm
+// (eps 1e-12) over the 128 channels; one wave per row, two channels per lane.
+__global__ void __launch_bounds__(256) albert_embed_kernel(const int32_t* ids, const int32_t* row_item,
+                                                           const int64_t* start, int64_t rows, const float* word,
+                                                           const float* pos, const float* tok0, const float* g,
+                                                           const float* b, float* out) {
+    const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (r >= rows) return;
+    const int it = row_item[r];
+    if (it < 0) return;
+    const int64_t id = ids[r], t = r - start[it];
+    float v[2];
+#pragma unroll
+    for (int e = 0; e < 2; e++) {
+        const int c = 2 * lane + e;
+        v[e] = (word[id * 128 + c] + tok0[c]) + pos[t * 128 + c];
+    }
+    const float mean = wave_sum(v[0] + v[1]) * (1.0f / 128.0f);
+    const float d0 = v[0] - mean, d1 = v[1] - mean;
+    const float var = wave_sum(d0 * d0 + d1 * d1) * (1.0f / 128.0f);
+    const float inv = 1.0f / sqrtf(var + 1e-12f);
+#pragma unroll
+    for (int e = 0; e < 2; e++) {
+        const int c = 2 * lane + e;
+        out[r * 128 + c] = (v[e] - mean) * inv * g[c] + b[c];
+    }
+}
+
+// text_encoder_b's embedding (src/gpu_batch.rs:461-469): out[r][0:512] = embedding[id]; one wave
+// per row, two float4 per lane.
+__global__ void __launch_bounds__(256) text_embed_kernel(const int32_t* ids, const int32_t* row_item, int64_t rows,
+                                                         const float* emb, float* out) {
+    const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (r >= rows || row_item[r] < 0) return;
+    const float4* src = (const float4*)(emb + (int64_t)ids[r] * 512);
+    float4* dst = (float4*)(out + r * 512);
+    dst[lane] = src[lane];
+    dst[lane + 64] = src[lane + 64];
+}
+
+// LayerNorm over the first D channels of each item row of x [rows][ld], in place
+// (layer_norm_rows / adaln_rows_seg, kernels/kokoro.cu:44-82, 337-373): mean, then the mean of
+// squared deviations, inv = 1 / sqrt(var + eps); then either the affine g, b, or AdaLayerNorm's
+// (1 + gamma[c]) o + beta[c] with gamma, beta = gb[item][gb_off + c], gb[item][gb_off + D + c];
+// optionally leaky ReLU.  One wave per row, D / 256 float4 per lane.
+template <int D>
+__global__ void __launch_bounds__(256) layernorm_kernel(float* x, int64_t ld, int64_t rows, const int32_t* row_item,
+                                                        const float* g, const float* b, const float* gb, int64_t gb_ld,
+                                                        int gb_off, float eps, int leaky, float slope) {
+    constexpr int NV = D / 256;  // float4 per lane
+    const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (r >= rows) return;
+    const int it = row_item[r];
+    if (it < 0) return;
+    float4* row = (float4*)(x + r * ld);
+    float4 v[NV];
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        v[i] = row[lane + 64 * i];
+        s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
+    }
+    const float mean = wave_sum(s) * (1.0f / D);
+    float q = 0.f;
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        const float a = v[i].x - mean, bb = v[i].y - mean, c = v[i].z - mean, d = v[i].w - mean;
+        q += (a * a + bb * bb) + (c * c + d * d);
+    }
+    const float inv = 1.0f / sqrtf(wave_sum(q) * (1.0f / D) + eps);
+    const float* gam = gb ? gb + (int64_t)it * gb_ld + gb_off : nullptr;
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        const int c0 = 4 * (lane + 64 * i);
+        float o[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            float y = (o[e] - mean) * inv;
+            if (gam)
+                y = (1.0f + gam[c0 + e]) * y + gam[D + c0 + e];
+            else
+                y = y * g[c0 + e] + b[c0 + e];
+            if (leaky) y = y < 0.f ? y * slope : y;
+            o[e] = y;
+        }
+        row[lane + 64 * i] = make_float4(o[0], o[1], o[2], o[3]);
+    }
+}
+
+// Per-item multi-head attention of ALBERT (src/gpu_batch.rs:433-441; softmax_rows
+// kernels/kokoro.cu:92-125): for queries [q0, q0 + 16) of one (item, head),
+// s = (q . k) * scale over the item's keys, p = exp(s - max) / sum, ctx = p v.  qkv [rows][2304]
+// (q | k | v, head h at columns 64 h), out [rows][768].  f32 throughout; the scores of the 16
+// queries stay in LDS (items are at most 512 tokens).
+constexpr int kAttQ = 16, kAttMaxT = 512, kAttLd = 65;
+__global__ void __launch_bounds__(256) attention_kernel(const float* qkv, const int64_t* start, const int64_t* len,
+                                                        const int32_t* w_item, const int32_t* w_head,
+                                                        const int32_t* w_q0, float* out, float scale) {
+    __shared__ float Qs[kAttQ][kAttLd];
+    __shared__ float KV[64][kAttLd];
+    __shared__ float S[kAttQ][kAttMaxT + 1];
+    const int tid = threadIdx.x;
+    const int item = w_item[blockIdx.x], head = w_head[blockIdx.x], q0 = w_q0[blockIdx.x];
+    const int64_t s0 = start[item];
+    const int t = (int)len[item];
+    const int nq = min(kAttQ, t - q0);
+    constexpr int64_t LD = 3 * 768;
+    // queries
+    for (int i = tid; i < kAttQ * 16; i += 256) {
+        const int q = i >> 4, d4 = (i & 15) * 4;
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (q < nq) v = *(const float4*)(qkv + (s0 + q0 + q) * LD + head * 64 + d4);
+        Qs[q][d4] = v.x, Qs[q][d4 + 1] = v.y, Qs[q][d4 + 2] = v.z, Qs[q][d4 + 3] = v.w;
+    }
+    const int qi = tid >> 4, kg = tid & 15;  // query of this thread; key / dim group
+    // scores
+    for (int k0 = 0; k0 < t; k0 += 64) {
+        const int nk = min(64, t - k0);
+        __syncthreads();
+        for (int i = tid; i < 64 * 16; i += 256) {
+            const int k = i >> 4, d4 = (i & 15) * 4;
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (k < nk) v = *(const float4*)(qkv + (s0 + k0 + k) * LD + 768 + head * 64 + d4);
+            KV[k][d4] = v.x, KV[k][d4 + 1] = v.y, KV[k][d4 + 2] = v.z, KV[k][d4 + 3] = v.w;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int k = kg + 16 * j;
+            float acc = 0.f;
+#pragma unroll 16
+            for (int d = 0; d < 64; d++) acc = fmaf(Qs[qi][d], KV[k][d], acc);
+            if (k < nk) S[qi][k0 + k] = acc * scale;
+        }
+    }
+    __syncthreads();
+    // softmax over the keys, 16 lanes per query
+    float mx = -INFINITY;
+    for (int k = kg; k < t; k += 16) mx = fmaxf(mx, S[qi][k]);
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    float sum = 0.f;
+    for (int k = kg; k < t; k += 16) {
+        const float e = expf(S[qi][k] - mx);
+        S[qi][k] = e;
+        sum += e;
+    }
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) sum += __shfl_xor(sum, o);
+    const float inv = 1.0f / sum;
+    // ctx = p v: this thread's 4 dims of its query
+    const int d0 = kg * 4;
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int k0 = 0; k0 < t; k0 += 64) {
+        const int nk = min(64, t - k0);
+        __syncthreads();
+        for (int i = tid; i < 64 * 16; i += 256) {
+            const int k = i >> 4, d4 = (i & 15) * 4;
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (k < nk) v = *(const float4*)(qkv + (s0 + k0 + k) * LD + 1536 + head * 64 + d4);
+            KV[k][d4] = v.x, KV[k][d4 + 1] = v.y, KV[k][d4 + 2] = v.z, KV[k][d4 + 3] = v.w;
+        }
+        __syncthreads();
+        for (int k = 0; k < nk; k++) {
+            const float p = S[qi][k0 + k] * inv;
+#pragma unroll
+            for (int e = 0; e < 4; e++) acc[e] = fmaf(p, KV[k][d0 + e], acc[e]);
+        }
+    }
+    if (qi < nq) *(float4*)(out + (s0 + q0 + qi) * 768 + head * 64 + d0) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+}
+
+// BiLSTM recurrence (lstm_seq_batched semantics, kernels/kokoro.cu:400-455): one block per
+// (item, direction), thread r = gate row r of 4H = 1024 (gates i, f, g, o).  Per step:
+// gate_r = gx[row][dir 4H + r] + (W_hh[r] . h + b_hh[r]); threads j < H then update
+// c_j = f c_j + i g, h_j = o tanh(c_j), written to out[row][dir H + j].  The forward direction walks
+// the item's rows in order, the reverse one backwards.  gx rows come through gx_row (the frame ->
+// token table: the gate pre-activations of a repeated token row are the same) or are the item's
+// own rows.  W_hh is k-major [dir][H][4H] f32: each k is one coalesced 4 KB row read from L2.
+// No block waits for another: every block ends after its item's steps.
+constexpr int kH = 256;
+__global__ void __launch_bounds__(1024) lstm_kernel(const float* gx, int64_t gx_ld, const int32_t* gx_row,
+                                                    const int64_t* start, const int64_t* len, const float* whh_t,
+                                                    const float* bhh, float* out, int64_t out_ld) {
+    __shared__ __align__(16) float hs[kH];
+    __shared__ float gs[4 * kH];
+    const int item = blockIdx.x >> 1, dir = blockIdx.x & 1;
+    const int r = threadIdx.x;
+    const int64_t s0 = start[item], n = len[item];
+    const float* w = whh_t + (int64_t)dir * kH * 4 * kH + r;
+    const float bh = bhh[dir * 4 * kH + r];
+    float c = 0.f;
+    if (r < kH) hs[r] = 0.f;
+    __syncthreads();
+    for (int64_t step = 0; step < n; step++) {
+        const int64_t row = s0 + (dir == 0 ? step : n - 1 - step);
+        const int64_t grow = gx_row ? (int64_t)gx_row[row] : row;
+        const float gxv = gx[grow * gx_ld + dir * 4 * kH + r];
+        float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+#pragma unroll 8
+        for (int k = 0; k < kH; k += 4) {
+            const float4 h4 = *(const float4*)&hs[k];
+            a0 = fmaf(w[(int64_t)(k + 0) * 4 * kH], h4.x, a0);
+            a1 = fmaf(w[(int64_t)(k + 1) * 4 * kH], h4.y, a1);
+            a2 = fmaf(w[(int64_t)(k + 2) * 4 * kH], h4.z, a2);
+            a3 = fmaf(w[(int64_t)(k + 3) * 4 * kH], h4.w, a3);
+        }
+        gs[r] = gxv + (((a0 + a1) + (a2 + a3)) + bh);
+        __syncthreads();
+        if (r < kH) {
+            const float ig = sigmoid(gs[r]), fg = sigmoid(gs[kH + r]), gg = tanhf(gs[2 * kH + r]),
+                        og = sigmoid(gs[3 * kH + r]);
+            c = fg * c + ig * gg;
+            const float h = og * tanhf(c);
+            hs[r] = h;
+            out[row * out_ld + dir * kH + r] = h;
+        }
+        __syncthreads();
+    }
+}
+
+// out[r][col0 + c] = styles[row_item[r]][c] for the item rows (cat_style_rows_seg's style half,
+// kernels/kokoro.cu:375-384; the other half is written in place by its producer).
+__global__ void __launch_bounds__(256) style_cols_kernel(float* x, int64_t ld, int col0, int64_t rows,
+                                                         const int32_t* row_item, const float* styles) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= rows * 32) return;
+    const int64_t r = i >> 5;
+    const int c4 = (int)(i & 31) * 4;
+    const int it = row_item[r];
+    if (it < 0) return;
+    *(float4*)(x + r * ld + col0 + c4) = *(const float4*)(styles + (int64_t)it * 128 + c4);
+}
+
+// F0_proj / N_proj, Conv1d k1 256 -> 1, over every row of the domain: y[r] = b + w . x[r] on item
+// rows, 0 in the gaps (the reference masks F0 and N after the projection, src/gpu_batch.rs:291-292).
+// One wave per row, four channels per lane.
+__global__ void __launch_bounds__(256) proj1_kernel(const float* x, int64_t ld, const float* w, const float* b,
+                                                    const int32_t* col, int64_t rows, float* y) {
+    const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (r >= rows) return;
+    if (col[r] < 0) {
+        if (lane == 0) y[r] = 0.f;
+        return;
+    }
+    const float4 v = *(const float4*)(x + r * ld + 4 * lane), ww = *(const float4*)(w + 4 * lane);
+    const float d = wave_sum((v.x * ww.x + v.y * ww.y) + (v.z * ww.z + v.w * ww.w));
+    if (lane == 0) y[r] = b[0] + d;
+}
+
+}  // namespace
+
+hipError_t launch_proj1(const float* x, int64_t ld, int c, const float* w, const float* b, const int32_t* col,
+                        int64_t rows, float* y, hipStream_t s) {
+    if (rows <= 0) return hipSuccess;
+    if (c != 256 || ld % 4 != 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(proj1_kernel, dim3((unsigned)ceil_div(rows, 4)), dim3(256), 0, s, x, ld, w, b, col, rows, y);
+    return hipGetLastError();
+}
+
+hipError_t launch_albert_embed(const int32_t* ids, const int32_t* row_item, const int64_t* start, int64_t rows,
+                               const float* word, const float* pos, const float* tok0, const float* g, const float* b,
+                               float* out, hipStream_t s) {
+    if (rows <= 0) return hipSuccess;
+    hipLaunchKernelGGL(albert_embed_kernel, dim3((unsigned)ceil_div(rows, 4)), dim3(256), 0, s, ids, row_item, start,
+                       rows, word, pos, tok0, g, b, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_text_embed(const int32_t* ids, const int32_t* row_item, int64_t rows, const float* emb, float* out,
+                             hipStream_t s) {
+    if (rows <= 0) return hipSuccess;
+    hipLaunchKernelGGL(text_embed_kernel, dim3((unsigned)ceil_div(rows, 4)), dim3(256), 0, s, ids, row_item, rows, emb,
+                       out);
+    return hipGetLastError();
+}
+
+hipError_t launch_layernorm(float* x, int64_t ld, int d, int64_t rows, const int32_t* row_item, const float* g,
+                            const float* b, const float* gb, int64_t gb_ld, int gb_off, float eps, bool leaky,
+                            float slope, hipStream_t s) {
+    if (rows <= 0) return hipSuccess;
+    if (ld % 4 != 0 || (gb == nullptr && (g == nullptr || b == nullptr))) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)ceil_div(rows, 4));
+    if (d == 768)
+        hipLaunchKernelGGL(layernorm_kernel<768>, grid, dim3(256), 0, s, x, ld, rows, row_item, g, b, gb, gb_ld, gb_off,
+                           eps, (int)leaky, slope);
+    else if (d == 512)
+        hipLaunchKernelGGL(layernorm_kernel<512>, grid, dim3(256), 0, s, x, ld, rows, row_item, g, b, gb, gb_ld, gb_off,
+                           eps, (int)leaky, slope);
+    else
+        return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+hipError_t launch_attention(const float* qkv, const int64_t* start, const int64_t* len, const int32_t* w_item,
+                            const int32_t* w_head, const int32_t* w_q0, int64_t n_blocks, float* out, hipStream_t s) {
+    if (n_blocks <= 0) return hipSuccess;
+    hipLaunchKernelGGL(attention_kernel, dim3((unsigned)n_blocks), dim3(256), 0, s, qkv, start, len, w_item, w_head,
+                       w_q0, out, 0.125f);
+    return hipGetLastError();
+}
+
+hipError_t launch_lstm(const float* gx, int64_t gx_ld, const int32_t* gx_row, const int64_t* start, const int64_t* len,
+                       int nb, const float* whh_t, const float* bhh, float* out, int64_t out_ld, hipStream_t s) {
+    if (nb <= 0) return hipSuccess;
+    hipLaunchKernelGGL(lstm_kernel, dim3((unsigned)(2 * nb)), dim3(4 * kH), 0, s, gx, gx_ld, gx_row, start, len, whh_t,
+                       bhh, out, out_ld);
+    return hipGetLastError();
+}
+
+hipError_t launch_style_cols(float* x, int64_t ld, int col0, int64_t rows, const int32_t* row_item,
+                             const float* styles, hipStream_t s) {
+    if (rows <= 0) return hipSuccess;
+    if ((ld | col0) % 4 != 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(style_cols_kernel, dim3((unsigned)ceil_div(rows * 32, 256)), dim3(256), 0, s, x, ld, col0, rows,
+                       row_item, styles);
+    return hipGetLastError();
+}
+
+}  // namespace kk

@@ -16,7 +16,7 @@ LIB_PATH = os.path.join(os.path.dirname(HERE), "lib", "libkokoro_hip.so")
 KK_OK = 0
 KK_NOISE_COUNTER = 0
 KK_NOISE_FIXED = 1
-STAGES = {"decoder": 1, "source": 2, "gen0": 3, "gen1": 4, "post": 5, "all": 6}
+STAGES = {"prosody": 0, "decoder": 1, "source": 2, "gen0": 3, "gen1": 4, "post": 5, "all": 6}
 EXPORTS = [
     "kk_open", "kk_close", "kk_device_name", "kk_identity", "kk_upload_model", "kk_forward_decoder_batch",
     "kk_output_free", "kk_plan_create", "kk_plan_create_generator", "kk_plan_create_snake", "kk_plan_run",
@@ -25,7 +25,8 @@ EXPORTS = [
     "kk_plan_fetch_pcm16", "kk_encode_pcm16", "kk_wav_header", "kk_host_alloc", "kk_host_free",
     "kk_plan_item_samples", "kk_plan_fetch_pcm16_async", "kk_plan_fetch_wait", "kk_snake_block_noalloc", "kk_profile_launches", "kk_checkpoint_open", "kk_checkpoint_count",
     "kk_checkpoint_entry", "kk_checkpoint_free", "kk_upload_checkpoint", "kk_weight_norm", "kk_voice_load",
-    "kk_voice_free", "kk_voice_ref_s",
+    "kk_voice_free", "kk_voice_ref_s", "kk_forward_batch", "kk_result_free", "kk_plan_create_full",
+    "kk_plan_durations",
 ]
 NOALLOC_MAX_ROWS = 65536
 NOALLOC_MAX_ITEMS = 64
@@ -55,6 +56,18 @@ class GeneratorItem(C.Structure):
 
 class Output(C.Structure):
     _fields_ = [("audio", C.POINTER(C.c_float)), ("n_samples", C.c_int64)]
+
+
+class Item(C.Structure):
+    """kk_item: BatchItem (src/gpu_batch.rs:19-24)."""
+    _fields_ = [("ids", C.c_void_p), ("n_ids", C.c_int32), ("ref_s", C.c_void_p), ("speed", C.c_float),
+                ("noise_kind", C.c_int32), ("seed", C.c_uint64), ("rand_ini", C.c_void_p), ("sine", C.c_void_p),
+                ("sine_len", C.c_int64)]
+
+
+class Result(C.Structure):
+    _fields_ = [("audio", C.POINTER(C.c_float)), ("n_samples", C.c_int64), ("pred_dur", C.POINTER(C.c_int64)),
+                ("n_tok", C.c_int32)]
 
 
 class PlanInfo(C.Structure):
@@ -123,6 +136,11 @@ def lib():
         L.kk_voice_free.restype = None
         L.kk_voice_ref_s.argtypes = [C.POINTER(C.c_float), i64, i64, C.POINTER(C.POINTER(C.c_float))]
         L.kk_snake_block_noalloc.argtypes = [vp, cp, vp, i64, vp, vp, i32, C.POINTER(vp), cp, sz]
+        L.kk_forward_batch.argtypes = [vp, C.POINTER(Item), i32, C.POINTER(Result), cp, sz]
+        L.kk_result_free.argtypes = [C.POINTER(Result), i32]
+        L.kk_result_free.restype = None
+        L.kk_plan_create_full.argtypes = [vp, C.POINTER(Item), i32, C.POINTER(vp), cp, sz]
+        L.kk_plan_durations.argtypes = [vp, i32, C.POINTER(C.POINTER(C.c_int64)), C.POINTER(C.c_int32)]
         L.kk_plan_get_info.argtypes = [vp, C.POINTER(PlanInfo)]
         L.kk_plan_free.argtypes = [vp]
         L.kk_plan_free.restype = None
@@ -352,6 +370,18 @@ class Context:
         del keep
         return res
 
+    def forward_batch(self, items):
+        """kk_forward_batch: list of workloads.IdsItem -> list of (audio, pred_dur)."""
+        arr, keep = _items(items)
+        outs = (Result * len(items))()
+        err = _err()
+        _check(lib().kk_forward_batch(self.h, arr, len(items), outs, err, len(err)), err)
+        res = [(np.ctypeslib.as_array(o.audio, shape=(o.n_samples,)).copy(),
+                np.ctypeslib.as_array(o.pred_dur, shape=(o.n_tok,)).copy()) for o in outs]
+        lib().kk_result_free(outs, len(items))
+        del keep
+        return res
+
     def plan(self, items):
         return Plan.decoder(self, items)
 
@@ -442,6 +472,24 @@ def _decoder_items(items):
     return arr, keep
 
 
+def _items(items):
+    keep = []
+    arr = (Item * len(items))()
+    for i, it in enumerate(items):
+        ids = np.ascontiguousarray(it.ids, np.int64)
+        rs = _f32(it.ref_s)
+        keep += [ids, rs]
+        d = arr[i]
+        d.ids, d.n_ids, d.ref_s, d.speed = ids.ctypes.data, len(ids), rs.ctypes.data, float(it.speed)
+        if getattr(it, "sine", None) is not None:
+            ri, sn = _f32(it.rand_ini), _f32(it.sine)
+            keep += [ri, sn]
+            d.noise_kind, d.rand_ini, d.sine, d.sine_len = KK_NOISE_FIXED, ri.ctypes.data, sn.ctypes.data, sn.size
+        else:
+            d.noise_kind, d.seed = KK_NOISE_COUNTER, int(it.seed) & 0xFFFFFFFFFFFFFFFF
+    return arr, keep
+
+
 class Plan:
     def __init__(self, ctx, h, n, kind, n_samples=None):
         self.ctx, self.h, self.n, self.kind = ctx, h, n, kind
@@ -454,6 +502,23 @@ class Plan:
         err = _err()
         _check(lib().kk_plan_create(ctx.h, arr, len(items), C.byref(h), err, len(err)), err)
         return cls(ctx, h, len(items), "decoder", [600 * it.n_frames for it in items])
+
+    @classmethod
+    def full(cls, ctx, items):
+        """Ids-level plan (kk_plan_create_full): the token phase runs at creation."""
+        arr, keep = _items(items)
+        h = C.c_void_p()
+        err = _err()
+        _check(lib().kk_plan_create_full(ctx.h, arr, len(items), C.byref(h), err, len(err)), err)
+        p = cls(ctx, h, len(items), "full")
+        p.durations = [p.item_durations(b) for b in range(len(items))]
+        p.n_samples = [600 * int(d.sum()) for d in p.durations]
+        return p
+
+    def item_durations(self, item):
+        d, n = C.POINTER(C.c_int64)(), C.c_int32()
+        _check(lib().kk_plan_durations(self.h, item, C.byref(d), C.byref(n)), _err())
+        return np.ctypeslib.as_array(d, shape=(n.value,)).copy()
 
     @classmethod
     def generator(cls, ctx, xs, f0s, ref_ss, seeds):

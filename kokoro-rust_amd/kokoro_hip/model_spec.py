@@ -90,6 +90,86 @@ def tensor_spec():
     return spec
 
 
+# ------------------------------------------------------------------ upstream stages
+N_TOKEN = 178
+ALBERT_EMB, ALBERT_HID, ALBERT_FFN, ALBERT_POS = 128, 768, 2048, 512
+ALBERT_LAYER = "bert.encoder.albert_layer_groups.0.albert_layers.0"
+LSTM_H = 256
+MAX_DUR = 50
+
+
+def _linear(spec, prefix, din, dout, bias=True, kind="conv"):
+    spec.append((f"{prefix}.weight", (dout, din), kind, din))
+    if bias:
+        spec.append((f"{prefix}.bias", (dout,), kind, din))
+
+
+def _lstm(spec, prefix, din, h=LSTM_H):
+    """BiLstm::load (src/nn.rs:178-189): torch.nn.LSTM names, gate order i, f, g, o."""
+    for sfx in ("", "_reverse"):
+        spec.append((f"{prefix}.weight_ih_l0{sfx}", (4 * h, din), "lstm", h))
+        spec.append((f"{prefix}.weight_hh_l0{sfx}", (4 * h, h), "lstm", h))
+        spec.append((f"{prefix}.bias_ih_l0{sfx}", (4 * h,), "lstm", h))
+        spec.append((f"{prefix}.bias_hh_l0{sfx}", (4 * h,), "lstm", h))
+
+
+def upstream_spec():
+    """[(name, shape, init kind, fan_in)] for ALBERT, bert_encoder, the text encoder and the prosody
+    predictor (src/albert.rs:36-67, src/model.rs:21-88, src/model.rs:122-141)."""
+    spec = []
+    spec.append(("bert.embeddings.word_embeddings.weight", (N_TOKEN, ALBERT_EMB), "emb", 0))
+    spec.append(("bert.embeddings.position_embeddings.weight", (ALBERT_POS, ALBERT_EMB), "emb", 0))
+    spec.append(("bert.embeddings.token_type_embeddings.weight", (2, ALBERT_EMB), "emb", 0))
+    spec.append(("bert.embeddings.LayerNorm.weight", (ALBERT_EMB,), "norm_w", 0))
+    spec.append(("bert.embeddings.LayerNorm.bias", (ALBERT_EMB,), "norm_b", 0))
+    _linear(spec, "bert.encoder.embedding_hidden_mapping_in", ALBERT_EMB, ALBERT_HID)
+    for nm in ("query", "key", "value", "dense"):
+        _linear(spec, f"{ALBERT_LAYER}.attention.{nm}", ALBERT_HID, ALBERT_HID)
+    spec.append((f"{ALBERT_LAYER}.attention.LayerNorm.weight", (ALBERT_HID,), "norm_w", 0))
+    spec.append((f"{ALBERT_LAYER}.attention.LayerNorm.bias", (ALBERT_HID,), "norm_b", 0))
+    _linear(spec, f"{ALBERT_LAYER}.ffn", ALBERT_HID, ALBERT_FFN)
+    _linear(spec, f"{ALBERT_LAYER}.ffn_output", ALBERT_FFN, ALBERT_HID)
+    spec.append((f"{ALBERT_LAYER}.full_layer_layer_norm.weight", (ALBERT_HID,), "norm_w", 0))
+    spec.append((f"{ALBERT_LAYER}.full_layer_layer_norm.bias", (ALBERT_HID,), "norm_b", 0))
+    _linear(spec, "bert_encoder", ALBERT_HID, HIDDEN)
+    # text encoder (src/model.rs:29-44)
+    spec.append(("text_encoder.embedding.weight", (N_TOKEN, HIDDEN), "emb", 0))
+    for i in range(3):
+        _conv(spec, f"text_encoder.cnn.{i}.0", HIDDEN, HIDDEN, 5)
+        spec.append((f"text_encoder.cnn.{i}.1.gamma", (HIDDEN,), "norm_w", 0))
+        spec.append((f"text_encoder.cnn.{i}.1.beta", (HIDDEN,), "norm_b", 0))
+    _lstm(spec, "text_encoder.lstm", HIDDEN)
+    # prosody predictor (src/model.rs:60-88)
+    cin = HIDDEN + STYLE_DIM
+    for i in range(3):
+        _lstm(spec, f"predictor.text_encoder.lstms.{2 * i}", cin)
+        _linear(spec, f"predictor.text_encoder.lstms.{2 * i + 1}.fc", STYLE_DIM, 2 * HIDDEN)
+    _lstm(spec, "predictor.lstm", cin)
+    spec.append(("predictor.duration_proj.linear_layer.weight", (MAX_DUR, HIDDEN), "dur_w", HIDDEN))
+    spec.append(("predictor.duration_proj.linear_layer.bias", (MAX_DUR,), "dur_bias", 0))
+    _lstm(spec, "predictor.shared", cin)
+    for name in ("F0", "N"):
+        _resblk(spec, f"predictor.{name}.0", HIDDEN, HIDDEN, False)
+        _resblk(spec, f"predictor.{name}.1", HIDDEN, HIDDEN // 2, True)
+        _resblk(spec, f"predictor.{name}.2", HIDDEN // 2, HIDDEN // 2, False)
+    spec.append(("predictor.F0_proj.weight", (1, HIDDEN // 2, 1), "conv", HIDDEN // 2))
+    spec.append(("predictor.F0_proj.bias", (1,), "f0_bias", 0))
+    _conv(spec, "predictor.N_proj", HIDDEN // 2, 1, 1)
+    return spec
+
+
+def random_upstream_weights(seed=0):
+    """{name: float32 array} for the upstream stages (same init rule as random_weights)."""
+    return {name: init_tensor(name, shape, kind, fan_in, seed) for name, shape, kind, fan_in in upstream_spec()}
+
+
+def random_model_weights(seed=0):
+    """Decoder + generator and the upstream stages: the whole Kokoro-82M model."""
+    w = random_weights(seed)
+    w.update(random_upstream_weights(seed))
+    return w
+
+
 def fnv1a64(s: str) -> int:
     h = 0xCBF29CE484222325
     for byte in s.encode():
@@ -121,6 +201,26 @@ def init_tensor(name, shape, kind, fan_in, seed):
         v = rng.uniform(-0.1, 0.1, n)
     elif kind == "alpha":
         v = rng.uniform(0.5, 1.5, n)
+    elif kind == "lstm":
+        # torch.nn.LSTM's default: U(-1/sqrt(H), 1/sqrt(H))
+        bound = 1.0 / np.sqrt(fan_in)
+        v = rng.uniform(-bound, bound, n)
+    elif kind == "emb":
+        v = rng.standard_normal(n)
+    elif kind == "dur_w":
+        # a row shared by the 50 outputs (3x the Linear default) plus the default per row: the 50
+        # logits of a token move together, so that the durations vary from token to token (about
+        # 2 to 12 frames) instead of averaging out in the sum of 50 sigmoids
+        bound = 1.0 / np.sqrt(fan_in)
+        common = rng.uniform(-3 * bound, 3 * bound, shape[1])
+        v = (common[None, :] + rng.uniform(-bound, bound, shape)).reshape(-1)
+    elif kind == "f0_bias":
+        # a voiced F0 curve (Hz) around which the stack's output varies
+        v = rng.uniform(120.0, 200.0, n)
+    elif kind == "dur_bias":
+        # about 5 frames per token on average over N(0, 1) styles (sigmoid(-2.2) * 50 = 5.0 before the
+        # shared row of the weight moves it)
+        v = -2.2 + rng.uniform(-0.1, 0.1, n)
     else:
         raise ValueError(kind)
     return v.astype(np.float32).reshape(shape)

@@ -115,3 +115,32 @@ def config5_items(seed=5, batch=128, g_lo=80, g_hi=4000):
     gs = np.exp(rng.uniform(np.log(g_lo), np.log(g_hi), batch))
     ns = np.maximum(1, (gs / 2).astype(np.int64))
     return [make_item(rng, int(n), seed=int(rng.integers(0, 2**63))) for n in ns]
+
+
+# ------------------------------------------------------------------ ids-level items (the whole forward)
+@dataclass
+class IdsItem:
+    """BatchItem (src/gpu_batch.rs:19-24): input_ids with the two boundary tokens, ref_s, speed, noise."""
+    ids: np.ndarray          # int64 [n_ids], each in [0, 178)
+    ref_s: np.ndarray        # float32 [256]
+    seed: int
+    speed: float = 1.0
+    rand_ini: np.ndarray | None = None
+    sine: np.ndarray | None = None
+
+
+def make_ids_item(rng, n_phonemes, seed, speed=1.0):
+    """n_phonemes ids uniform over the vocabulary, wrapped in the boundary token 0; ref_s ~ N(0, 1)."""
+    ids = np.concatenate([[0], rng.integers(0, 178, n_phonemes), [0]]).astype(np.int64)
+    return IdsItem(ids=ids, ref_s=rng.standard_normal(256).astype(np.float32), seed=int(seed), speed=speed)
+
+
+def config4_items(seed=4, batch=64, lo=20, hi=510):
+    """batch 64, phoneme ids uniform over vocab 178, lengths uniform 20-510."""
+    rng = np.random.default_rng(seed)
+    return [make_ids_item(rng, int(rng.integers(lo, hi + 1)), 4000 + b) for b in range(batch)]
+
+
+def small_ids_items(seed, ns, speed=1.0):
+    rng = np.random.default_rng(seed)
+    return [make_ids_item(rng, n, 7000 + b, speed) for b, n in enumerate(ns)]

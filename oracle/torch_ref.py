@@ -27,9 +27,29 @@ def T(a):
     return torch.as_tensor(np.asarray(a), dtype=DT)
 
 
+ROUND_OPERANDS = False
+
+
+class bf16_operands:
+    """Within: conv() and linear() round their input and weight to bf16 first (the GPU's MFMA
+    operands, and the reference's GLinear / BF16 convs, src/gpu.rs:280-301), accumulating in DT."""
+
+    def __enter__(self):
+        global ROUND_OPERANDS
+        ROUND_OPERANDS = True
+
+    def __exit__(self, *a):
+        global ROUND_OPERANDS
+        ROUND_OPERANDS = False
+
+
+def _rb(t):
+    return t.to(torch.float32).to(torch.bfloat16).to(DT) if ROUND_OPERANDS else t
+
+
 def conv(w, prefix, x, stride=1, pad=0, dil=1, bias=True):
     b = T(w[prefix + ".bias"]) if bias else None
-    return F.conv1d(x[None], T(w[prefix + ".weight"]), b, stride=stride, padding=pad, dilation=dil)[0]
+    return F.conv1d(_rb(x)[None], _rb(T(w[prefix + ".weight"])), b, stride=stride, padding=pad, dilation=dil)[0]
 
 
 def adain(w, prefix, x, s):
@@ -164,3 +184,154 @@ def generator(w, x, f0, s, rand_ini, noise, taps=None, spec=None):
     if taps is not None:
         taps["post"] = post
     return istft(post)
+
+
+# ------------------------------------------------------------------ upstream stages (ids -> F0, N, t_en)
+# The reference runs these on its GPU engine (src/gpu_batch.rs:179-297); the host-side pieces are the
+# ALBERT embedding lookup (src/albert.rs:70-81) and the duration rounding (src/model.rs:90-100).
+
+HEADS, HEAD_DIM = 12, 64
+
+
+def linear(w, prefix, x):
+    """Linear on row-major x [t, din] (src/nn.rs:7-23; GLinear::fwd src/gpu.rs:280-301)."""
+    b = T(w[prefix + ".bias"]) if prefix + ".bias" in w else None
+    return F.linear(_rb(x), _rb(T(w[prefix + ".weight"])), b)
+
+
+def gelu_new(x):
+    """kernels/kokoro.cu:84-90: 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3)))."""
+    return 0.5 * x * (1 + torch.tanh(math.sqrt(2 / math.pi) * (x + 0.044715 * x ** 3)))
+
+
+def albert_embeddings(w, ids):
+    """Albert::embeddings (src/albert.rs:70-81): (word + token_type[0]) + position, LayerNorm 1e-12."""
+    ids = torch.as_tensor(np.asarray(ids, np.int64))
+    e = (T(w["bert.embeddings.word_embeddings.weight"])[ids] + T(w["bert.embeddings.token_type_embeddings.weight"])[0])
+    e = e + T(w["bert.embeddings.position_embeddings.weight"])[: len(ids)]
+    return F.layer_norm(e, (e.shape[1],), T(w["bert.embeddings.LayerNorm.weight"]),
+                        T(w["bert.embeddings.LayerNorm.bias"]), eps=1e-12)
+
+
+def albert(w, ids):
+    """albert_b (src/gpu_batch.rs:423-455): one shared post-LN layer applied 12 times; per head
+    softmax(q k^T / 8) v over the item's own tokens (src/gpu_batch.rs:433-441)."""
+    L = "bert.encoder.albert_layer_groups.0.albert_layers.0"
+    h = linear(w, "bert.encoder.embedding_hidden_mapping_in", albert_embeddings(w, ids))
+    t = h.shape[0]
+    for _ in range(12):
+        q, k, v = (linear(w, f"{L}.attention.{n}", h).reshape(t, HEADS, HEAD_DIM).transpose(0, 1)
+                   for n in ("query", "key", "value"))
+        p = torch.softmax(q @ k.transpose(1, 2) * HEAD_DIM ** -0.5, dim=-1)   # [heads, t, t]
+        ctx = (p @ v).transpose(0, 1).reshape(t, HEADS * HEAD_DIM)
+        a = F.layer_norm(linear(w, f"{L}.attention.dense", ctx) + h, (h.shape[1],),
+                         T(w[f"{L}.attention.LayerNorm.weight"]), T(w[f"{L}.attention.LayerNorm.bias"]), eps=1e-12)
+        f = gelu_new(linear(w, f"{L}.ffn", a))
+        h = F.layer_norm(linear(w, f"{L}.ffn_output", f) + a, (h.shape[1],),
+                         T(w[f"{L}.full_layer_layer_norm.weight"]), T(w[f"{L}.full_layer_layer_norm.bias"]), eps=1e-12)
+    return h
+
+
+def lstm_dir(w, prefix, sfx, x, reverse):
+    """One direction of torch.nn.LSTM (gates i, f, g, o; lstm_seq_batched kernels/kokoro.cu:404-455:
+    gate = (W_ih x + b_ih) + (W_hh h + b_hh), c = f c + i g, h = o tanh(c))."""
+    wih, whh = T(w[f"{prefix}.weight_ih_l0{sfx}"]), T(w[f"{prefix}.weight_hh_l0{sfx}"])
+    bih, bhh = T(w[f"{prefix}.bias_ih_l0{sfx}"]), T(w[f"{prefix}.bias_hh_l0{sfx}"])
+    hd = whh.shape[1]
+    gx = F.linear(_rb(x), _rb(wih), bih)  # W_ih on the GLinear route (bf16 operands on the GPU)
+    h = torch.zeros(hd, dtype=DT)
+    c = torch.zeros(hd, dtype=DT)
+    out = torch.zeros(x.shape[0], hd, dtype=DT)
+    order = range(x.shape[0] - 1, -1, -1) if reverse else range(x.shape[0])
+    for t in order:
+        g = gx[t] + (whh @ h + bhh)
+        i, f, gg, o = torch.sigmoid(g[:hd]), torch.sigmoid(g[hd:2 * hd]), torch.tanh(g[2 * hd:3 * hd]), torch.sigmoid(g[3 * hd:])
+        c = f * c + i * gg
+        h = o * torch.tanh(c)
+        out[t] = h
+    return out
+
+
+def bilstm(w, prefix, x):
+    """BiLstm (src/nn.rs:168-190): [t, din] -> [t, 2H], forward then reverse direction."""
+    return torch.cat([lstm_dir(w, prefix, "", x, False), lstm_dir(w, prefix, "_reverse", x, True)], dim=1)
+
+
+def text_encoder(w, ids):
+    """text_encoder_b (src/gpu_batch.rs:457-481): embedding, 3 x (Conv1d k5 p2, LayerNorm over the
+    channels with gamma / beta eps 1e-5, leaky ReLU 0.2), BiLSTM.  Returns t_en [t, 512]."""
+    ids = torch.as_tensor(np.asarray(ids, np.int64))
+    x = T(w["text_encoder.embedding.weight"])[ids].T  # [512, t]
+    for i in range(3):
+        y = conv(w, f"text_encoder.cnn.{i}.0", x, pad=2).T  # [t, 512]
+        y = F.layer_norm(y, (y.shape[1],), T(w[f"text_encoder.cnn.{i}.1.gamma"]), T(w[f"text_encoder.cnn.{i}.1.beta"]),
+                         eps=1e-5)
+        x = F.leaky_relu(y, 0.2).T
+    return bilstm(w, "text_encoder.lstm", x.T)
+
+
+def ada_layer_norm(w, prefix, h, s):
+    """adaln_rows_seg (kernels/kokoro.cu:337-373): (1 + gamma) LayerNorm(h) + beta, eps 1e-5, no
+    affine; gamma, beta = fc(s) (src/gpu_batch.rs:225-231)."""
+    gb = F.linear(T(s), T(w[prefix + ".weight"]), T(w[prefix + ".bias"]))
+    d = h.shape[1]
+    return (1 + gb[:d]) * F.layer_norm(h, (d,), eps=1e-5) + gb[d:]
+
+
+def duration_encoder(w, d_en, s_pro):
+    """src/gpu_batch.rs:216-233: x = [d_en | s]; 3 x (BiLSTM, AdaLayerNorm, [h | s]).  [t, 640]."""
+    s = T(s_pro)
+    srow = s[None].expand(d_en.shape[0], -1)
+    x = torch.cat([d_en, srow], dim=1)
+    for i in range(3):
+        h = bilstm(w, f"predictor.text_encoder.lstms.{2 * i}", x)
+        h = ada_layer_norm(w, f"predictor.text_encoder.lstms.{2 * i + 1}.fc", h, s)
+        x = torch.cat([h, srow], dim=1)
+    return x
+
+
+def durations(logits, speed):
+    """durations_from_logits (src/model.rs:90-100): round-half-even(sum sigmoid / speed), >= 1."""
+    s = torch.sigmoid(torch.as_tensor(logits, dtype=DT)).sum(dim=1) / speed
+    return np.maximum(np.round(s.numpy()).astype(np.int64), 1)
+
+
+def f0n(w, d, dur, s_pro, taps=None):
+    """src/gpu_batch.rs:265-294: en = d's rows repeated by the durations, shared BiLSTM, then the F0
+    and N stacks (AdainResBlk1d 512->512, 512->256 upsampled, 256->256; Conv1d k1 -> 1) at 2N."""
+    src = np.repeat(np.arange(len(dur)), dur)
+    en = d[torch.as_tensor(src)]
+    sh = bilstm(w, "predictor.shared", en)
+    if taps is not None:
+        taps["shared"] = sh
+    return f0n_stacks(w, sh, s_pro)
+
+
+def f0n_stacks(w, sh, s_pro):
+    """The F0 and N stacks on the shared LSTM's output sh [N, 512] (src/gpu_batch.rs:282-292)."""
+    sh = torch.as_tensor(sh, dtype=DT).T  # [512, N]
+    out = []
+    for name in ("F0", "N"):
+        h = resblk(w, f"predictor.{name}.0", sh, s_pro)
+        h = resblk(w, f"predictor.{name}.1", h, s_pro, upsample=True)
+        h = resblk(w, f"predictor.{name}.2", h, s_pro)
+        out.append(conv(w, f"predictor.{name}_proj", h)[0])
+    return out[0], out[1]
+
+
+def upstream(w, ids, ref_s, speed=1.0, taps=None, dur=None):
+    """forward_batch up to the decoder for one item (src/gpu_batch.rs:179-297): returns
+    (durations, t_en [512, t], F0 [2N], N [2N]); `dur` overrides the predicted durations."""
+    ref_s = np.asarray(ref_s)
+    s_pro = ref_s[128:]
+    bert = albert(w, ids)
+    d_en = linear(w, "bert_encoder", bert)
+    d = duration_encoder(w, d_en, s_pro)
+    xl = bilstm(w, "predictor.lstm", d)
+    logits = linear(w, "predictor.duration_proj.linear_layer", xl)
+    pred = durations(logits, speed) if dur is None else np.asarray(dur, np.int64)
+    f0, n = f0n(w, d, pred, s_pro, taps)
+    t_en = text_encoder(w, ids)
+    if taps is not None:
+        taps.update(bert=bert, d_en=d_en, d=d, xl=xl, logits=logits, t_en=t_en, f0=f0, n=n)
+    return pred, t_en.T, f0, n

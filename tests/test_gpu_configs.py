@@ -15,7 +15,7 @@ import numpy as np
 import pytest
 
 from conftest import snr_db
-from test_gpu_properties import _check_vs_oracle
+from gpu_checks import check_vs_oracle
 
 pytestmark = pytest.mark.gpu
 
@@ -26,7 +26,7 @@ def _print(*a):
 
 def test_config1_generator(gpu_ctx, oracle_model):
     """End to end against the oracle, or from the GPU's own spectrum when a bin sits on atan2's
-    branch cut (see test_gpu_properties._check_vs_oracle)."""
+    branch cut (see gpu_checks.check_vs_oracle)."""
     from kokoro_hip import api, workloads
     from oracle import oracle as O
     x, f0, style, seed = workloads.config1_generator_input()
@@ -86,7 +86,7 @@ def test_config5_full_size(gpu_ctx, oracle_model):
         assert a.shape == (600 * it.n_frames,) and np.isfinite(a).all()
     lo, hi = int(np.argmin(ns)), int(np.argmax(ns))
     # the shortest item alone, against the oracle (spectrum and audio, as in the property tests)
-    _, (alone,) = _check_vs_oracle(gpu_ctx, oracle_model, [items[lo]], "config 5 shortest")
+    _, (alone,) = check_vs_oracle(gpu_ctx, oracle_model, [items[lo]], "config 5 shortest")
     assert np.array_equal(alone, outs[lo])
     with api.Plan.decoder(gpu_ctx, [items[hi]]) as plan:
         plan.run()
@@ -101,7 +101,7 @@ def test_config3_full_size(gpu_ctx, oracle_model):
     - the shortest, the median and the longest item against the fp32 oracle at the north-star bar
       (max-abs <= 2e-3, SNR >= 40 dB) and against the bf16-emulated oracle (>= 44 dB); an item whose
       spectrum has a bin on atan2's branch cut is compared through the oracle's generator run from
-      the GPU's own spectrum (see test_gpu_properties._check_vs_oracle);
+      the GPU's own spectrum (see gpu_checks.check_vs_oracle);
     - the shortest and the longest item bit-identical to runs of themselves alone."""
     from kokoro_hip import api, workloads
     from oracle import oracle as O
