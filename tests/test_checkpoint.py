@@ -134,23 +134,24 @@ def test_voice_packs(tmp_path):
 
 
 def kokoro_like_checkpoint(weights, path, seed=5):
-    """The random-init decoder written the way the released model file holds it: per-submodule state
-    dicts under "module.", every decoder conv except the noise convs as a weight_g / weight_v pair
-    (v a rescaled copy of the weight, g within 25% of its row norms: the resolved weight is
-    weight_norm(v, g), not the original), and
-    the AdaIN InstanceNorm affine parameters left out.  Returns the table the checkpoint resolves
-    to, built with the oracle's weight_norm and the defaults 1 / 0."""
+    """A random-init model written the way the released model file holds it: per-submodule state
+    dicts ("bert", "bert_encoder", "predictor", "text_encoder", "decoder") whose keys carry a
+    "module." prefix; every conv weight except the noise convs and the F0 / N projections as a
+    weight_g / weight_v pair (v a rescaled copy of the weight, g within 25% of its row norms: the
+    resolved weight is weight_norm(v, g), not the original); the AdaIN InstanceNorm affine
+    parameters left out.  Returns the table the checkpoint resolves to, built with the oracle's
+    weight_norm and the defaults 1 / 0."""
     rng = np.random.default_rng(seed)
-    dec = collections.OrderedDict()
+    subs = collections.OrderedDict()
     resolved = {}
     for name, arr in weights.items():
-        assert name.startswith("decoder.")
-        key = name[len("decoder."):]
+        sub, key = name.split(".", 1)
+        dec = subs.setdefault(sub, collections.OrderedDict())
         if name.endswith(".norm.weight") or name.endswith(".norm.bias"):
             if ".adain" in name or ".norm1." in name or ".norm2." in name:
                 resolved[name] = np.ones_like(arr) if name.endswith("weight") else np.zeros_like(arr)
                 continue
-        if name.endswith(".weight") and arr.ndim == 3 and "noise_convs" not in name:
+        if (name.endswith(".weight") and arr.ndim == 3 and "noise_convs" not in name and "_proj" not in name):
             v = (arr * rng.uniform(0.5, 2.0, (arr.shape[0],) + (1,) * (arr.ndim - 1))).astype(np.float32)
             # g near the original row norms, so that activations keep their scale
             norms = np.sqrt((arr.astype(np.float64) ** 2).reshape(arr.shape[0], -1).sum(1)).reshape(-1, 1, 1)
@@ -161,8 +162,8 @@ def kokoro_like_checkpoint(weights, path, seed=5):
             continue
         dec["module." + key] = torch.from_numpy(np.ascontiguousarray(arr, np.float32))
         resolved[name] = arr
-    top = {"bert": collections.OrderedDict(dummy=torch.zeros(4)), "decoder": dec}
-    torch.save(top, path)
+    subs.setdefault("bert", collections.OrderedDict(dummy=torch.zeros(4)))
+    torch.save(dict(subs), path)
     return resolved
 
 
@@ -187,3 +188,28 @@ def test_upload_checkpoint_matches_resolved_table(weights, tmp_path):
         b.close()
     for x, y in zip(out_a, out_b):
         assert np.isfinite(x).all() and np.array_equal(x, y)
+
+
+@pytest.mark.gpu
+def test_upload_checkpoint_whole_model(tmp_path):
+    """The whole model from a checkpoint (ALBERT, the text encoder and the predictor included, their
+    weight-normed convs resolved in the library) gives the same durations and audio, bit for bit,
+    through kk_forward_batch as kk_upload_model of the table resolved on the CPU."""
+    from kokoro_hip import api, model_spec, workloads
+    w = model_spec.random_model_weights(seed=0)
+    path = tmp_path / "kokoro-like-full.pth"
+    resolved = kokoro_like_checkpoint(w, path, seed=6)
+    items = workloads.small_ids_items(84, [21, 9, 40])
+    a = api.Context(0)
+    b = api.Context(0)
+    try:
+        ck = api.Checkpoint(path)
+        a.upload_checkpoint(ck)
+        ck.free()
+        b.upload_model(resolved)
+        out_a, out_b = a.forward_batch(items), b.forward_batch(items)
+    finally:
+        a.close()
+        b.close()
+    for (x, dx), (y, dy) in zip(out_a, out_b):
+        assert np.array_equal(dx, dy) and np.isfinite(x).all() and np.array_equal(x, y)

@@ -260,3 +260,53 @@ def test_refusals(full_ctx, gpu_ctx):
     with pytest.raises(api.KKError) as e:
         gpu_ctx.forward_batch([it])
     assert "stages before the decoder" in str(e.value)
+
+
+def test_config4_full_size(full_ctx, full_weights, oracle_model):
+    """BASELINE config 4 at full size: 64 items of 20-510 phoneme ids uniform over the vocabulary.
+
+    - every item: 600 x sum(pred_dur) finite samples, durations >= 1;
+    - all 64 items' audio bit-identical to the decoder entry's on the plan's own durations, t_en, F0
+      and N (the decoder entry is pinned against the oracle elsewhere);
+    - the shortest and the longest item: the token-phase taps and the shared LSTM against the
+      bf16-operand oracle, F0 / N against the oracle's stacks on the GPU's shared output;
+    - the shortest and the median item's audio against the oracle (check_vs_oracle's protocol);
+    - the shortest and the longest item bit-identical when run alone."""
+    from gpu_checks import check_vs_oracle
+    from kokoro_hip import api, workloads
+    from oracle import torch_ref as R
+    items = workloads.config4_items()
+    lens = [len(it.ids) for it in items]
+    order = list(np.argsort(lens, kind="stable"))
+    lo, mid, hi = int(order[0]), int(order[len(order) // 2]), int(order[-1])
+    with api.Plan.full(full_ctx, items) as plan:
+        plan.run()
+        audio = plan.fetch()
+        durs = plan.durations
+        _print(f"  config 4: {len(items)} items, {sum(lens)} ids, {sum(int(d.sum()) for d in durs)} frames")
+        small = {b: (plan.tap("t_en", b, (512, lens[b])), plan.tap("f0", b, (2 * int(durs[b].sum()),)),
+                     plan.tap("n", b, (2 * int(durs[b].sum()),))) for b in range(len(items))}
+        big = {b: _taps(plan, b, lens[b], int(durs[b].sum())) for b in (lo, hi)}
+    for it, a, d in zip(items, audio, durs):
+        assert d.min() >= 1 and a.shape == (600 * int(d.sum()),) and np.isfinite(a).all()
+    dec = [workloads.DecoderItem(dur=d, t_en=small[b][0], f0=small[b][1], energy=small[b][2], ref_s=it.ref_s,
+                                 seed=it.seed) for b, (it, d) in enumerate(zip(items, durs))]
+    ref = full_ctx.forward_decoder_batch(dec)
+    for a, r in zip(audio, ref):
+        assert np.array_equal(a, r)
+    b_f0 = float(full_weights["predictor.F0_proj.bias"][0])
+    for b in (lo, hi):
+        it, tp, d = items[b], big[b], durs[b]
+        e = {}
+        with R.bf16_operands():
+            R.upstream(full_weights, it.ids, it.ref_s, taps=e, dur=d)
+            f0_g, n_g = R.f0n_stacks(full_weights, tp["shared"].T, it.ref_s[128:])
+        s = {name: snr_db(e[name].numpy().T, tp[name]) for name in ("bert", "d", "logits", "t_en", "shared")}
+        s["F0"] = snr_db(f0_g.numpy() - b_f0, tp["f0"] - b_f0)
+        s["N"] = snr_db(n_g.numpy(), tp["n"])
+        _print(f"  item {b} ({lens[b]} ids, {int(d.sum())} frames): " + ", ".join(f"{k} {v:.1f}" for k, v in s.items()))
+        assert min(s.values()) >= 40.0
+    check_vs_oracle(full_ctx, oracle_model, [dec[lo], dec[mid]], "config 4")
+    for b in (lo, hi):
+        ((alone, d_alone),) = full_ctx.forward_batch([items[b]])
+        assert np.array_equal(d_alone, durs[b]) and np.array_equal(alone, audio[b])
