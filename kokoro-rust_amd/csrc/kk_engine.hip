@@ -1935,11 +1935,11 @@ static void init_full_plan(kk_plan* p, const kk_item* items, int n) {
         for (int b = 0; b < n; b++) std::memcpy(&sp[(size_t)b * kStyleDim], items[b].ref_s + kStyleDim, sizeof(float) * kStyleDim);
     }
     {
-        // attention work list: (item, head, first query) per 16 queries
+        // attention work list: (item, head, first query) per 64 queries
         std::vector<int32_t> wi, wh, wq;
         for (int b = 0; b < n; b++)
             for (int h = 0; h < 12; h++)
-                for (int q = 0; q < items[b].n_ids; q += 16) wi.push_back(b), wh.push_back(h), wq.push_back(q);
+                for (int q = 0; q < items[b].n_ids; q += 64) wi.push_back(b), wh.push_back(h), wq.push_back(q);
         p->n_att = (int64_t)wi.size();
         stage_vec(ctx, p->att_item, wi), stage_vec(ctx, p->att_head, wh), stage_vec(ctx, p->att_q0, wq);
     }

@@ -116,86 +116,115 @@ __global__ void __launch_bounds__(256) layernorm_kernel(float* x, int64_t ld, in
 }
 
 // Per-item multi-head attention of ALBERT (src/gpu_batch.rs:433-441; softmax_rows
-// kernels/kokoro.cu:92-125): for queries [q0, q0 + 16) of one (item, head),
-// s = (q . k) * scale over the item's keys, p = exp(s - max) / sum, ctx = p v.  qkv [rows][2304]
-// (q | k | v, head h at columns 64 h), out [rows][768].  f32 throughout; the scores of the 16
-// queries stay in LDS (items are at most 512 tokens).
-constexpr int kAttQ = 16, kAttMaxT = 512, kAttLd = 65;
+// kernels/kokoro.cu:92-125): softmax over the item's keys of (q . k) / 8, times v, f32 throughout.
+// qkv [rows][2304] (q | k | v, head h at columns 64 h), out [rows][768].  One block per (item, head,
+// 64 queries); keys in chunks of 64 with the softmax carried across chunks (running row maximum and
+// sum; the same exponentials as the reference's max-then-exp up to f32 rounding).  Thread (ty, tx)
+// holds the scores of queries 4 ty..4 ty+3 x keys 4 tx..4 tx+3 and the output of those queries x
+// dims 4 tx..4 tx+3: every LDS float4 read feeds 16 FMAs.
+constexpr int kAttQ = 64, kAttLd = 68;  // queries per block; LDS row stride (floats)
 __global__ void __launch_bounds__(256) attention_kernel(const float* qkv, const int64_t* start, const int64_t* len,
                                                         const int32_t* w_item, const int32_t* w_head,
                                                         const int32_t* w_q0, float* out, float scale) {
-    __shared__ float Qs[kAttQ][kAttLd];
-    __shared__ float KV[64][kAttLd];
-    __shared__ float S[kAttQ][kAttMaxT + 1];
-    const int tid = threadIdx.x;
+    __shared__ __align__(16) float Qt[64][kAttLd];  // [dim][query]
+    __shared__ __align__(16) float Kt[64][kAttLd];  // [dim][key]
+    __shared__ __align__(16) float Vs[64][kAttLd];  // [key][dim]
+    __shared__ __align__(16) float Pt[64][kAttLd];  // [key][query]
+    const int tid = threadIdx.x, ty = tid >> 4, tx = tid & 15;
     const int item = w_item[blockIdx.x], head = w_head[blockIdx.x], q0 = w_q0[blockIdx.x];
     const int64_t s0 = start[item];
     const int t = (int)len[item];
     const int nq = min(kAttQ, t - q0);
     constexpr int64_t LD = 3 * 768;
-    // queries
+    // the query tile, transposed into LDS (rows past the item's queries as 0)
     for (int i = tid; i < kAttQ * 16; i += 256) {
         const int q = i >> 4, d4 = (i & 15) * 4;
         float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
         if (q < nq) v = *(const float4*)(qkv + (s0 + q0 + q) * LD + head * 64 + d4);
-        Qs[q][d4] = v.x, Qs[q][d4 + 1] = v.y, Qs[q][d4 + 2] = v.z, Qs[q][d4 + 3] = v.w;
+        Qt[d4][q] = v.x, Qt[d4 + 1][q] = v.y, Qt[d4 + 2][q] = v.z, Qt[d4 + 3][q] = v.w;
     }
-    const int qi = tid >> 4, kg = tid & 15;  // query of this thread; key / dim group
-    // scores
+    float m[4], l[4], o[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        m[i] = -INFINITY, l[i] = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; j++) o[i][j] = 0.f;
+    }
     for (int k0 = 0; k0 < t; k0 += 64) {
         const int nk = min(64, t - k0);
-        __syncthreads();
+        __syncthreads();  // the previous chunk's Kt / Vs / Pt are consumed
         for (int i = tid; i < 64 * 16; i += 256) {
             const int k = i >> 4, d4 = (i & 15) * 4;
-            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (k < nk) v = *(const float4*)(qkv + (s0 + k0 + k) * LD + 768 + head * 64 + d4);
-            KV[k][d4] = v.x, KV[k][d4 + 1] = v.y, KV[k][d4 + 2] = v.z, KV[k][d4 + 3] = v.w;
+            float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
+            if (k < nk) {
+                const float* r = qkv + (s0 + k0 + k) * LD + head * 64 + d4;
+                kv = *(const float4*)(r + 768), vv = *(const float4*)(r + 1536);
+            }
+            Kt[d4][k] = kv.x, Kt[d4 + 1][k] = kv.y, Kt[d4 + 2][k] = kv.z, Kt[d4 + 3][k] = kv.w;
+            *(float4*)&Vs[k][d4] = vv;
         }
         __syncthreads();
+        float sc[4][4];
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int k = kg + 16 * j;
-            float acc = 0.f;
-#pragma unroll 16
-            for (int d = 0; d < 64; d++) acc = fmaf(Qs[qi][d], KV[k][d], acc);
-            if (k < nk) S[qi][k0 + k] = acc * scale;
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) sc[i][j] = 0.f;
+#pragma unroll 8
+        for (int d = 0; d < 64; d++) {
+            const float4 a = *(const float4*)&Qt[d][4 * ty], b = *(const float4*)&Kt[d][4 * tx];
+            const float av[4] = {a.x, a.y, a.z, a.w}, bv[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) sc[i][j] = fmaf(av[i], bv[j], sc[i][j]);
         }
-    }
-    __syncthreads();
-    // softmax over the keys, 16 lanes per query
-    float mx = -INFINITY;
-    for (int k = kg; k < t; k += 16) mx = fmaxf(mx, S[qi][k]);
+        // scale, mask the keys past the item, carry the row maximum and sum (16 lanes per row)
 #pragma unroll
-    for (int o = 8; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-    float sum = 0.f;
-    for (int k = kg; k < t; k += 16) {
-        const float e = expf(S[qi][k] - mx);
-        S[qi][k] = e;
-        sum += e;
-    }
+        for (int i = 0; i < 4; i++) {
+            float mx = -INFINITY;
 #pragma unroll
-    for (int o = 8; o > 0; o >>= 1) sum += __shfl_xor(sum, o);
-    const float inv = 1.0f / sum;
-    // ctx = p v: this thread's 4 dims of its query
-    const int d0 = kg * 4;
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
-    for (int k0 = 0; k0 < t; k0 += 64) {
-        const int nk = min(64, t - k0);
+            for (int j = 0; j < 4; j++) {
+                sc[i][j] = 4 * tx + j < nk ? sc[i][j] * scale : -INFINITY;
+                mx = fmaxf(mx, sc[i][j]);
+            }
+#pragma unroll
+            for (int off = 8; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+            const float mn = fmaxf(m[i], mx);
+            const float corr = expf(m[i] - mn);  // 0 on the first chunk
+            float sum = 0.f;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const float e = expf(sc[i][j] - mn);
+                Pt[4 * tx + j][4 * ty + i] = e;
+                sum += e;
+            }
+#pragma unroll
+            for (int off = 8; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+            l[i] = l[i] * corr + sum;
+            m[i] = mn;
+#pragma unroll
+            for (int j = 0; j < 4; j++) o[i][j] *= corr;
+        }
         __syncthreads();
-        for (int i = tid; i < 64 * 16; i += 256) {
-            const int k = i >> 4, d4 = (i & 15) * 4;
-            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (k < nk) v = *(const float4*)(qkv + (s0 + k0 + k) * LD + 1536 + head * 64 + d4);
-            KV[k][d4] = v.x, KV[k][d4 + 1] = v.y, KV[k][d4 + 2] = v.z, KV[k][d4 + 3] = v.w;
-        }
-        __syncthreads();
-        for (int k = 0; k < nk; k++) {
-            const float p = S[qi][k0 + k] * inv;
+#pragma unroll 8
+        for (int k = 0; k < 64; k++) {
+            const float4 p4 = *(const float4*)&Pt[k][4 * ty], v4 = *(const float4*)&Vs[k][4 * tx];
+            const float pv[4] = {p4.x, p4.y, p4.z, p4.w}, vv[4] = {v4.x, v4.y, v4.z, v4.w};
 #pragma unroll
-            for (int e = 0; e < 4; e++) acc[e] = fmaf(p, KV[k][d0 + e], acc[e]);
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) o[i][j] = fmaf(pv[i], vv[j], o[i][j]);
         }
     }
-    if (qi < nq) *(float4*)(out + (s0 + q0 + qi) * 768 + head * 64 + d0) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int q = 4 * ty + i;
+        if (q < nq) {
+            const float inv = 1.0f / l[i];
+            *(float4*)(out + (s0 + q0 + q) * 768 + head * 64 + 4 * tx) =
+                make_float4(o[i][0] * inv, o[i][1] * inv, o[i][2] * inv, o[i][3] * inv);
+        }
+    }
 }
 
 // BiLSTM recurrence (lstm_seq_batched semantics, kernels/kokoro.cu:400-455): one block per

@@ -19,17 +19,27 @@ def _print(*a):
 ILL_CONDITIONED_N = (2,)
 
 
+def unstable_phase_bins(spec_gpu, spec_ref):
+    """Spectral bins whose phase input to the generator differs between two spectra by more than
+    1e-2 rad (raw, not wrapped: the generator reads the phase values themselves).  Two kinds occur,
+    both set by rounding, in the reference against upstream torch as here: atan2's branch cut (a bin
+    with a ~0 imaginary part and a negative real part reads +pi on one side and -pi on the other),
+    and the real DC / Nyquist bins of a frame whose sum cancels to ~1e-8, which read 0 or pi by
+    that sum's sign."""
+    return int((np.abs(np.asarray(spec_gpu[11:], np.float64) - spec_ref[11:]) > 1e-2).sum())
+
+
 def check_vs_oracle(ctx, oracle_model, items, label):
     """Runs the items and compares each with the oracle.
 
     - Duration expansion: bit-exact.
     - Source spectrum: magnitudes to f32 rounding, phases on the circle where a bin carries energy.
     - Audio with the north-star bar (max-abs <= 2e-3, SNR >= 40 dB): end to end against the oracle,
-      or against the oracle's generator run from the GPU's own spectrum when a spectral bin sits on
-      atan2's branch cut.  A bin whose imaginary part is ~0 with a negative real part (the first and
-      last frame of every item are symmetric under the reflect padding, so all their bins are real)
-      reads +pi on one side and -pi on the other from ulp-level differences of sin/tanh; the
-      generator sees that 2 pi jump, in the reference against upstream torch as here.
+      or against the oracle's generator run from the GPU's own spectrum when a bin's phase is set by
+      rounding (unstable_phase_bins: atan2's branch cut -- the first and last frame of every item are
+      symmetric under the reflect padding, so all their bins are real -- and real DC / Nyquist bins
+      whose sum cancels); the generator sees such a phase jump as an input change, in the reference
+      against upstream torch as here.
     - Two-frame items (ILL_CONDITIONED_N): the decoder output within 6 dB of the bf16-emulated
       oracle's own distance from fp32, and the audio against the oracle's generator run from the
       GPU's decoder output and spectrum.
@@ -51,7 +61,7 @@ def check_vs_oracle(ctx, oracle_model, items, label):
         mag_err = np.abs(g[:11] - spec[:11]).max() / max(np.abs(spec[:11]).max(), 1e-6)
         dphi = np.angle(np.exp(1j * (g[11:].astype(np.float64) - spec[11:])))
         energetic = spec[:11] > 1e-4 * spec[:11].max()
-        flips = int((np.abs(g[11:] - spec[11:]) > np.pi).sum())
+        flips = unstable_phase_bins(g, spec)
         assert mag_err < 1e-4 and np.abs(dphi[energetic]).max() < 1e-3
         note = ""
         if it.n_frames in ILL_CONDITIONED_N:
@@ -69,7 +79,7 @@ def check_vs_oracle(ctx, oracle_model, items, label):
         else:
             end_to_end += 1
         _print(f"  {label} N {it.n_frames}: mag err {mag_err:.3g} phase err {np.abs(dphi[energetic]).max():.3g} "
-               f"branch-cut bins {flips} audio snr {snr_db(ref, a):.2f} maxabs {np.abs(a - ref).max():.3g}{note}")
+               f"phase-unstable bins {flips} audio snr {snr_db(ref, a):.2f} maxabs {np.abs(a - ref).max():.3g}{note}")
         assert np.abs(a - ref).max() <= 2e-3
         assert snr_db(ref, a) >= 40.0
     return end_to_end, outs

@@ -7,8 +7,9 @@ The argument has three parts:
    in tests/test_upstream_oracle.py), twice: as is, and with the operands of its linear layers and
    convolutions rounded to bf16 where the GPU's MFMA layers (and the reference's GLinear / BF16
    convs) round them -- the tight bar;
-2. the durations bit for bit, except tokens whose sigmoid sum lies within 0.02 of a rounding tie
-   (there the f32 logits of any implementation may round either way);
+2. the durations: bit for bit the host rule on the device's logits, and equal to the oracle's
+   except tokens whose sigmoid sum lies within 0.05 of a rounding tie (there the f32 logits of any
+   implementation may round either way);
 3. the audio of the ids-level call bit for bit equal to the decoder entry's audio on the ids-level
    call's own durations, t_en, F0 and N -- and the decoder entry is pinned against the oracle by
    tests/test_gpu_parity.py.
@@ -24,7 +25,7 @@ from conftest import snr_db
 
 pytestmark = pytest.mark.gpu
 
-TIE = 0.02
+TIE = 0.05
 
 
 def _print(*a):
@@ -99,16 +100,24 @@ def test_token_phase_vs_oracle(full_run, oracle_runs):
 
 
 def test_durations_vs_oracle(full_run, oracle_runs):
+    """Integer parity of the rule: the durations are durations_from_logits (src/model.rs:90-100) of
+    the device's own logits, bit for bit.  Against the oracle: the sigmoid sums within TIE of the
+    bf16-operand oracle's, and the durations equal wherever the oracle's sum lies further than TIE
+    from a rounding tie (a sum of 50 sigmoids carries the logits' correlated rounding noise)."""
     import torch
+    from kokoro_hip import api
     from oracle import torch_ref as R
-    items, _, durs, _ = full_run
+    items, _, durs, taps = full_run
     _, emu = oracle_runs
-    for it, d, e in zip(items, durs, emu):
+    for it, d, tp, e in zip(items, durs, taps, emu):
+        assert np.array_equal(d, api.durations_from_logits(np.ascontiguousarray(tp["logits"].T), it.speed))
         s = torch.sigmoid(e["logits"]).sum(1).numpy() / it.speed
+        s_gpu = torch.sigmoid(torch.from_numpy(tp["logits"].T.astype(np.float64))).sum(1).numpy() / it.speed
         want = R.durations(e["logits"], it.speed)
         tie = np.abs(s - np.floor(s) - 0.5) < TIE
-        _print(f"  durations: {len(d)} tokens, {int(tie.sum())} within {TIE} of a tie, "
-               f"{int((d != want).sum())} differ")
+        _print(f"  durations: {len(d)} tokens, max |sum sigmoid - oracle| {np.abs(s_gpu - s).max():.4f}, "
+               f"{int(tie.sum())} within {TIE} of a tie, {int((d != want).sum())} differ")
+        assert np.abs(s_gpu - s).max() < TIE
         assert np.array_equal(d[~tie], want[~tie])
         assert d.min() >= 1
 
@@ -163,7 +172,7 @@ def test_end_to_end_vs_oracle(full_ctx, full_run, full_weights, oracle_model):
     from oracle import torch_ref as R
     items, audio, durs, taps = full_run
     # (a) the decoder entry on the ids-level call's prosody is its audio bit for bit (tested above);
-    # against the oracle with the decoder tests' protocol (atan2 branch-cut bins handled there)
+    # against the oracle with the decoder tests' protocol (phases set by rounding handled there)
     dec = [workloads.DecoderItem(dur=d, t_en=tp["t_en"], f0=tp["f0"], energy=tp["n"], ref_s=it.ref_s, seed=it.seed)
            for it, d, tp in zip(items, durs, taps)]
     _, outs_a = check_vs_oracle(full_ctx, oracle_model, dec, "ids-level prosody")
