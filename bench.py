@@ -21,8 +21,11 @@ frames each, seeded synthetic inputs and random-init weights of the real archite
 - `cpu_baseline`: the oracle (a C restatement of the same path, OpenMP) on a bounded sample of the
   same batch, and on config 1; beside it the torch-CPU functional restatement (oracle/torch_ref.py,
   float32) on the same sample.  A reported baseline, not the target.
+- `e2e`: BASELINE.json configs[3], the whole forward from phoneme ids (kk_forward_batch) on its own
+  batch (64 ragged items, 20-510 ids), with its device-resident time, a serial per-class kernel
+  breakdown and its own torch-CPU baseline (see e2e_leg).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--config 3|5]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-e2e] [--config 3|5]
 """
 import argparse
 import json
@@ -141,6 +144,94 @@ def parity(model, it, audio, spec_gpu):
     return out
 
 
+def e2e_cpu_baseline(w, items, budget_s=15.0):
+    """The torch-CPU float32 restatement of every stage (oracle/torch_ref.py) on the shortest items
+    of the batch until `budget_s` of wall time, torch threads = the box's CPU share."""
+    import torch
+    from oracle import oracle as O
+    from oracle import torch_ref as R
+    threads = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    R.set_dtype(torch.float32)
+    order = sorted(range(len(items)), key=lambda b: len(items[b].ids))
+    done_s, t0, n_items = 0.0, time.perf_counter(), 0
+    try:
+        for b in order:
+            it = items[b]
+            with torch.no_grad():
+                pred, t_en, f0, n = R.upstream(w, it.ids, it.ref_s)
+                x = R.decoder(w, O.expand_tokens(t_en.numpy(), pred), f0, n, it.ref_s)
+                R.generator(w, x, f0, it.ref_s, O.rand_ini(it.seed), O.gen_noise(it.seed, 600 * int(pred.sum()) * 9))
+            done_s += 600 * int(pred.sum()) / 24000.0
+            n_items += 1
+            if time.perf_counter() - t0 > budget_s:
+                break
+    finally:
+        R.set_dtype(torch.float64)
+    el = time.perf_counter() - t0
+    return {"value": round(done_s / el, 3), "unit": "audio-s/s", "cores": threads, "kind": "port",
+            "sample": f"the {n_items} shortest items of the batch ({done_s:.1f} s of audio), torch-CPU float32 "
+                      "restatement of every stage (oracle/torch_ref.py)", "cpu_model": _cpu_model()}
+
+
+def e2e_leg(steps, warmup, with_cpu):
+    """BASELINE config 4, the whole forward from phoneme ids (kk_forward_batch): 64 ragged items,
+    20-510 ids uniform over the vocabulary, random-init weights of every stage.  One step = one
+    C-ABI call from host ids to host audio (token phase, the durations on the host from one copy of
+    the logits, frame layout, prosody, decoder, generator, iSTFT, audio back).  Beside it: the same
+    batch as a device-resident plan (token phase included), a per-launch profiling pass by kernel
+    class, and the torch-CPU float32 restatement (oracle/torch_ref.py) on a bounded sample."""
+    import numpy as np
+    from kokoro_hip import api, model_spec, workloads
+    w = model_spec.random_model_weights(seed=0)
+    items = workloads.config4_items()
+    ctx = api.Context(0)
+    ctx.upload_model(w)
+    for _ in range(warmup):
+        res = ctx.forward_batch(items)
+    times = []
+    for _ in range(steps):
+        t0 = time.perf_counter()
+        res = ctx.forward_batch(items)
+        times.append(time.perf_counter() - t0)
+    frames = sum(int(d.sum()) for _, d in res)
+    assert all(np.isfinite(a).all() for a, _ in res), "non-finite audio"
+    audio_s = 600 * frames / 24000.0
+    ms = statistics.median(times) * 1e3
+    plan = api.Plan.full(ctx, items)
+    for until, key in (("prosody", "to_prosody_ms"), ("all", "kernel_only_ms")):
+        plan.run(until)
+        plan.sync()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            plan.run(until)
+        plan.sync()
+        if key == "kernel_only_ms":
+            k_ms = (time.perf_counter() - t0) * 1e3 / steps
+        else:
+            p_ms = (time.perf_counter() - t0) * 1e3 / steps
+    ctx.set_profiling(True)
+    ctx.profile_read()
+    plan.run()
+    plan.sync()
+    prof = ctx.profile_read()
+    ctx.set_profiling(False)
+    plan.free()
+    ctx.close()
+    out = {"workload": "config4: phoneme ids -> audio, batch 64 ragged, 20-510 ids uniform over vocab 178",
+           "value": round(audio_s / (ms / 1e3), 2), "unit": "audio-s/s", "ms_per_step": round(ms, 3),
+           "step": "kk_forward_batch, host ids -> host audio (median of K calls)", "items": len(items),
+           "ids": sum(len(it.ids) for it in items), "frames": frames, "audio_s": round(audio_s, 2),
+           "frames_per_token": round(frames / sum(len(it.ids) for it in items), 3),
+           "kernel_only": {"value": round(audio_s / (k_ms / 1e3), 2), "ms_per_step": round(k_ms, 3),
+                           "through_prosody_ms": round(p_ms, 3),
+                           "step": "kk_plan_run of an ids-level plan, token phase included (mean of K)"},
+           "serial_ms_by_class": {k: round(v["ms"], 3) for k, v in sorted(prof.items(), key=lambda kv: -kv[1]["ms"])}}
+    if with_cpu:
+        out["cpu_baseline"] = e2e_cpu_baseline(w, items)
+    return out
+
+
 def _traffic(config):
     """HBM bytes per Snake-conv launch (FETCH_SIZE + WRITE_SIZE, copy-calibrated) from the committed
     PMC summary of the config-3 workload; None for other workloads or when it is absent."""
@@ -159,6 +250,8 @@ def main():
     ap.add_argument("--config", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-events", action="store_true", help="skip the per-launch profiling pass")
+    ap.add_argument("--no-e2e", action="store_true", help="skip the ids-level (config 4) leg")
+    ap.add_argument("--e2e-steps", type=int, default=5)
     ap.add_argument("--layers", default="", help="write the profiling pass's per-launch table (JSON) here")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="first run one plain copy kernel over this many MiB (reference for PMC byte counters)")
@@ -317,6 +410,8 @@ def main():
         res["cpu_baseline"], model = cpu_baseline(weights, items)
     res["parity"] = parity(model, items[0], audio0, spec0)
     ctx.close()
+    if not args.no_e2e:
+        res["e2e"] = e2e_leg(args.e2e_steps, 1, not args.no_cpu)
     print(json.dumps(res), flush=True)
 
 
