@@ -15,9 +15,10 @@ pytestmark = pytest.mark.gpu
 KK_ERR_OOM = -3
 
 
-def synth_batch(ctx, items, max_batch):
-    """Engine::synth_batch's retry loop (src/engine.rs:213-239) over forward_decoder_batch: returns
-    per-item audio or the KKError of a single item, and the sizes of the calls made."""
+def synth_batch(ctx, items, max_batch, call=None):
+    """Engine::synth_batch's retry loop (src/engine.rs:213-239) over forward_decoder_batch (or
+    `call`): returns per-item results or the KKError of a single item, and the sizes of the calls
+    made."""
     from kokoro_hip import api
     results = [None] * len(items)
     # plan_batches (src/engine.rs:165-183) with a fixed cap: consecutive chunks of max_batch
@@ -28,7 +29,7 @@ def synth_batch(ctx, items, max_batch):
         batch = stack.pop()
         calls.append(len(batch))
         try:
-            outs = ctx.forward_decoder_batch([items[k] for k in batch])
+            outs = (call or ctx.forward_decoder_batch)([items[k] for k in batch])
         except api.KKError as e:
             if len(batch) > 1:
                 mid = len(batch) // 2
@@ -71,3 +72,27 @@ def test_single_item_oom_is_that_items_error(gpu_ctx, monkeypatch):
         ref = plan.fetch()
     for a, b in zip(ref, again):
         assert np.array_equal(a, b)
+
+
+def test_ids_level_halving_on_oom(monkeypatch):
+    """The same loop over the ids-level entry (kk_forward_batch, the call Engine::synth_batch makes
+    on the reference): every item's audio and durations bit-identical to the unsplit batch, in
+    input order; a single item's OOM is that item's error."""
+    from kokoro_hip import api, model_spec, workloads
+    ctx = api.Context(0)
+    try:
+        ctx.upload_model(model_spec.random_model_weights(seed=0))
+        items = workloads.small_ids_items(85, [14, 3, 30, 8, 22])
+        full = ctx.forward_batch(items)
+        monkeypatch.setenv("KOKORO_HIP_TEST_OOM_ABOVE", "2")
+        res, calls = synth_batch(ctx, items, max_batch=8, call=ctx.forward_batch)
+        print("  calls:", calls, flush=True)
+        # 5 fails -> [0, 1] ok; [2, 3, 4] fails -> [2] ok, [3, 4] ok
+        assert calls == [5, 2, 3, 1, 2]
+        for k, ((a, d), r) in enumerate(zip(full, res)):
+            assert isinstance(r, tuple) and np.array_equal(a, r[0]) and np.array_equal(d, r[1]), f"item {k}"
+        monkeypatch.setenv("KOKORO_HIP_TEST_OOM_ABOVE", "0")
+        res, calls = synth_batch(ctx, items[:2], max_batch=8, call=ctx.forward_batch)
+        assert calls == [2, 1, 1] and all(isinstance(r, api.KKError) and r.code == KK_ERR_OOM for r in res)
+    finally:
+        ctx.close()
