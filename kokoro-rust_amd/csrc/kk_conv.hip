@@ -34,6 +34,7 @@
 //   traffic of f32, 8x the precision of the bf16 operands; the residual stream stays f32.
 #include "kk_common.h"
 #include "kk_kernels.h"
+#include "kk_walk.h"
 
 #include <algorithm>
 #include <atomic>
@@ -556,13 +557,8 @@ __global__ __launch_bounds__(64 * WM * WN + kNP) void conv_mfma_kernel(ConvParam
     // Units: U = g * 8 * mblocks + w * 8 + x is M-block w of tile g * 8 + x.  Block b runs units
     // b, b + G, b + 2G, ... (G = gridDim.x, a multiple of 8 * mblocks, so b keeps its w and x).
     // Workgroup slots go to the 8 XCDs round-robin: block b stays on XCD x.
-    const int grp_units = 8 * mblocks;
     auto unit_at = [&](int U, Unit& u) -> bool {
-        const int g = U / grp_units;
-        const int within = U - g * grp_units;
-        u.tile = g * 8 + (within & 7);
-        if (u.tile >= p.tiles.count) return false;
-        u.m0 = (within >> 3) * BM;
+        if (!walk_unit(U, mblocks, BM, p.tiles.count, u.tile, u.m0)) return false;
         u.item = ld_const(p.tiles.item, u.tile);
         u.n0 = (int)ld_const(p.tiles.t0, u.tile);
         u.nv = ld_const(p.tiles.n, u.tile);
@@ -572,13 +568,7 @@ __global__ __launch_bounds__(64 * WM * WN + kNP) void conv_mfma_kernel(ConvParam
         return true;
     };
     // slabs this block runs: units b + i G with tile g_i * 8 + x < count, g_i = g_0 + i * (G / grp)
-    int n_units = 0;
-    {
-        const int b = blockIdx.x;
-        const int g0 = b / grp_units, x = (b - g0 * grp_units) & 7;
-        const int gmax = ((int)p.tiles.count - 1 - x) >> 3;  // last group whose tile g*8+x exists
-        if (p.tiles.count > x && gmax >= g0) n_units = (gmax - g0) / ((int)gridDim.x / grp_units) + 1;
-    }
+    const int n_units = walk_n_units(blockIdx.x, gridDim.x, mblocks, p.tiles.count);
     const int G = n_units * nsl;
     if (G == 0) return;
 
@@ -682,7 +672,7 @@ __global__ __launch_bounds__(64 * WM * WN + kNP) void conv_mfma_kernel(ConvParam
 
 
     int U = blockIdx.x, sl = 0;
-    Unit cu, nu;
+    Unit cu{}, nu{};
     unit_at(U, cu);
     bool has_next = unit_at(U + gridDim.x, nu);
     // A of the current tap, one register set per 16-channel step; each set is refilled with the
@@ -699,12 +689,8 @@ __global__ __launch_bounds__(64 * WM * WN + kNP) void conv_mfma_kernel(ConvParam
         for (int kk = 0; kk < p.k; kk++) {
             // the tap after this one: same slab, first tap of the next slab, or of the next unit
             // (the very last tap reloads tap 0 of this slab: a harmless load keeps the count static)
-            int n_m0 = cu.m0, n_kk = kk + 1, n_c16 = 4 * sl;
-            if (kk + 1 == p.k) {
-                n_kk = 0;
-                if (!last) n_c16 = 4 * sl + 4;
-                else if (has_next) n_m0 = nu.m0, n_c16 = 0;
-            }
+            int n_m0, n_kk, n_c16;
+            walk_next_a(kk, p.k, sl, nsl, has_next, cu.m0, nu.m0, n_m0, n_kk, n_c16);
 #pragma unroll
             for (int kc = 0; kc < 4; kc++) {
                 bf16x8(&bc)[4] = (kc & 1) ? B1 : B0;
@@ -763,10 +749,7 @@ hipError_t launch_t(const ConvParams& p, int n_cu, hipStream_t s, bool validate_
         return hipErrorInvalidValue;
     if (validate_only) return hipSuccess;
     // one persistent block per CU; the grid is a multiple of 8 * mblocks
-    const int64_t grp = 8 * (int64_t)(p.m_pad / BM);
-    const int64_t units = ceil_div(p.tiles.count, 8) * grp;  // padded unit count
-    const int64_t fit = std::max<int64_t>(1, n_cu / grp) * grp;
-    const int64_t grid = std::min(units, fit);
+    const int64_t grid = walk_grid(p.tiles.count, p.m_pad / BM, n_cu);
     // the dynamic LDS limit is a per-device attribute of each kernel: set once per device
     auto go = [&](auto kern, DeviceFlags& attr) -> hipError_t {
         int dev = 0;
