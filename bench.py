@@ -25,7 +25,7 @@ frames each, seeded synthetic inputs and random-init weights of the real archite
   batch (64 ragged items, 20-510 ids), with its device-resident time, a serial per-class kernel
   breakdown and its own torch-CPU baseline (see e2e_leg).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-e2e] [--config 3|5]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-e2e | --only-e2e] [--config 3|5]
 """
 import argparse
 import json
@@ -40,6 +40,7 @@ sys.path.insert(0, ROOT)
 
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0
+PEAK_F32_VALU_TFLOPS = 78.6  # 256 CUs x 64 FMA / clk x 2.4 GHz (the attention runs on the VALU)
 BANDWIDTH_KERNELS = ["stats_tiles", "finalize", "style_fc", "expand", "f0n_conv", "copy_cols", "adain_pool",
                      "noise_conv0", "noise_conv1", "phase_pre", "source_stft", "istft"]
 
@@ -218,6 +219,18 @@ def e2e_leg(steps, warmup, with_cpu):
     ctx.set_profiling(False)
     plan.free()
     ctx.close()
+    # the recurrences are sequential in time: their cost is the longest item's steps
+    lens = [len(it.ids) for it in items]
+    frames_max = max(int(d.sum()) for _, d in res)
+    lstm_steps = 5 * max(lens) + frames_max
+    cls = {k: v for k, v in prof.items()}
+    def rate(k, peak):
+        v = cls.get(k)
+        if not v or v["ms"] <= 0:
+            return None
+        t = v["flop"] / (v["ms"] / 1e3) / 1e12
+        return {"serial_ms": round(v["ms"], 3), "launches": v["launches"], "tflops": round(t, 1),
+                "peak_tflops": peak, "frac": round(t / peak, 4)}
     out = {"workload": "config4: phoneme ids -> audio, batch 64 ragged, 20-510 ids uniform over vocab 178",
            "value": round(audio_s / (ms / 1e3), 2), "unit": "audio-s/s", "ms_per_step": round(ms, 3),
            "step": "kk_forward_batch, host ids -> host audio (median of K calls)", "items": len(items),
@@ -226,7 +239,16 @@ def e2e_leg(steps, warmup, with_cpu):
            "kernel_only": {"value": round(audio_s / (k_ms / 1e3), 2), "ms_per_step": round(k_ms, 3),
                            "through_prosody_ms": round(p_ms, 3),
                            "step": "kk_plan_run of an ids-level plan, token phase included (mean of K)"},
-           "serial_ms_by_class": {k: round(v["ms"], 3) for k, v in sorted(prof.items(), key=lambda kv: -kv[1]["ms"])}}
+           "serial_ms_by_class": {k: round(v["ms"], 3) for k, v in sorted(prof.items(), key=lambda kv: -kv[1]["ms"])},
+           "kernels": {
+               "lstm": {"serial_ms": round(cls["lstm"]["ms"], 3), "critical_steps": lstm_steps,
+                        "us_per_step": round(1e3 * cls["lstm"]["ms"] / lstm_steps, 2),
+                        "note": "5 token-level BiLSTMs (longest item's ids) + the shared BiLSTM (longest item's "
+                                "frames); per step bound by streaming 496 KB of W_hh per CU"},
+               "attention": rate("attention", PEAK_F32_VALU_TFLOPS),
+               "linear": rate("linear", PEAK_BF16_TFLOPS),
+               "prosody_conv": rate("prosody_conv", PEAK_BF16_TFLOPS),
+               "snake_conv": rate("snake_conv", PEAK_BF16_TFLOPS)}}
     if with_cpu:
         out["cpu_baseline"] = e2e_cpu_baseline(w, items)
     return out
@@ -252,6 +274,7 @@ def main():
     ap.add_argument("--no-events", action="store_true", help="skip the per-launch profiling pass")
     ap.add_argument("--no-e2e", action="store_true", help="skip the ids-level (config 4) leg")
     ap.add_argument("--e2e-steps", type=int, default=5)
+    ap.add_argument("--only-e2e", action="store_true", help="run only the ids-level (config 4) leg")
     ap.add_argument("--layers", default="", help="write the profiling pass's per-launch table (JSON) here")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="first run one plain copy kernel over this many MiB (reference for PMC byte counters)")
@@ -265,6 +288,9 @@ def main():
     import numpy as np
     from kokoro_hip import api, model_spec, workloads
 
+    if args.only_e2e:
+        print(json.dumps({"e2e": e2e_leg(args.e2e_steps, 1, not args.no_cpu)}), flush=True)
+        return
     if args.calibrate_copy_mib:
         # one elementwise kernel that reads and writes exactly M MiB: the FETCH_SIZE / WRITE_SIZE
         # counters of this dispatch scale those of the conv kernels to bytes

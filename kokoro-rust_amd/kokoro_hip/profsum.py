@@ -3,6 +3,8 @@
     python -m kokoro_hip.profsum stats <trace_dir> <steps>
         per-kernel table from a `rocprofv3 --kernel-trace` CSV run of bench.py, plus the average
         Snake-block conv duration of its profiling pass (the last <steps> steps)
+    python -m kokoro_hip.profsum kernels <trace_dir>
+        per-kernel table (calls, total, average, share) of any `rocprofv3 --kernel-trace --stats` run
     python -m kokoro_hip.profsum layers <layers.json>
         per-layer table of bench.py's profiling pass (`--layers`): every kernel alone on the stream,
         HIP events around each launch; time per launch, algorithmic TFLOP/s and GB/s, and the
@@ -89,6 +91,24 @@ def stats(trace_dir, steps):
 PEAK_FLOPS, PEAK_BYTES = 2.5e15, 8e12
 
 
+def kernels_table(trace_dir, top=40):
+    """Every kernel of a `rocprofv3 --kernel-trace --stats` CSV run: calls, total, average, share."""
+    rows = []
+    for root, _, files in os.walk(trace_dir):
+        for f in files:
+            if f.endswith("kernel_stats.csv"):
+                rows += _rows(os.path.join(root, f))
+    tot = sum(float(r["TotalDurationNs"]) for r in rows) or 1.0
+    rows.sort(key=lambda r: -float(r["TotalDurationNs"]))
+    out = ["| kernel | calls | total ms | avg us | % |", "|---|---:|---:|---:|---:|"]
+    for r in rows[:top]:
+        t = float(r["TotalDurationNs"])
+        out.append(f"| `{_short(r['Name'])}` | {r['Calls']} | {t / 1e6:.2f} | {float(r['AverageNs']) / 1e3:.1f} | "
+                   f"{100 * t / tot:.2f} |")
+    out.append(f"\nAll kernels: {tot / 1e6:.2f} ms over {sum(int(r['Calls']) for r in rows)} dispatches.")
+    return "\n".join(out)
+
+
 def layers_table(path):
     with open(path) as f:
         d = json.load(f)
@@ -150,6 +170,8 @@ if __name__ == "__main__":
     sys.path.insert(0, os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
     if sys.argv[1] == "stats":
         print(stats(sys.argv[2], int(sys.argv[3])))
+    elif sys.argv[1] == "kernels":
+        print(kernels_table(sys.argv[2]))
     elif sys.argv[1] == "layers":
         print(layers_table(sys.argv[2]))
     elif sys.argv[1] == "traffic":
