@@ -132,29 +132,44 @@ __global__ __launch_bounds__(256) void finalize_kernel(const StatPart* __restric
 }
 
 // ------------------------------------------------------------------ style projections
-// GLinear of every AdaIN (src/gpu_batch.rs:84): gb[b][j] = bias[j] + sum_k W[j][k] style[b][k].
-// W is stored transposed [128][rows] so consecutive threads read consecutive rows.
+// GLinear of every AdaIN (src/gpu_batch.rs:84): gb[b][j] = bias[j] + sum_k W[j][k] style[b][k], summed
+// in f64.  W is stored transposed [128][rows] so consecutive threads read consecutive rows.  A block
+// covers 64 rows; its four waves take one quarter of k each (the loads of a quarter issued
+// together), and the quarters' sums meet in LDS, 16 items per pass.
 __global__ __launch_bounds__(256) void style_fc_kernel(const float* __restrict__ wt, const float* __restrict__ bias,
                                                        int rows, const float* __restrict__ style, int nb,
                                                        float* __restrict__ gb) {
     __shared__ float st[16][kStyleDim];
-    const int j = blockIdx.x * 256 + threadIdx.x;
+    __shared__ double part[3][16][64];
+    const int r = threadIdx.x & 63, q = threadIdx.x >> 6;
+    const int j = blockIdx.x * 64 + r;
+    const int jc = j < rows ? j : rows - 1;
+    float w[32];
+#pragma unroll
+    for (int i = 0; i < 32; i++) w[i] = wt[(int64_t)(32 * q + i) * rows + jc];
     for (int b0 = 0; b0 < nb; b0 += 16) {
         const int cnt = min(16, nb - b0);
         __syncthreads();
-        for (int i = threadIdx.x; i < cnt * kStyleDim; i += 256) st[i / kStyleDim][i % kStyleDim] = style[(int64_t)b0 * kStyleDim + i];
+        for (int i = threadIdx.x; i < 16 * kStyleDim; i += 256)
+            st[i / kStyleDim][i % kStyleDim] = i / kStyleDim < cnt ? style[(int64_t)b0 * kStyleDim + i] : 0.f;
         __syncthreads();
-        if (j < rows) {
-            double acc[16];
+        double acc[16];
 #pragma unroll
-            for (int e = 0; e < 16; e++) acc[e] = 0.0;
-            for (int k = 0; k < kStyleDim; k++) {
-                const double w = wt[(int64_t)k * rows + j];
+        for (int e = 0; e < 16; e++) acc[e] = 0.0;
 #pragma unroll
-                for (int e = 0; e < 16; e++) acc[e] += w * (double)st[e][k];
-            }
-            for (int e = 0; e < cnt; e++) gb[(int64_t)(b0 + e) * rows + j] = (float)(acc[e] + (double)bias[j]);
+        for (int i = 0; i < 32; i++) {
+            const double wv = w[i];
+#pragma unroll
+            for (int e = 0; e < 16; e++) acc[e] += wv * (double)st[e][32 * q + i];
         }
+        if (q > 0)
+#pragma unroll
+            for (int e = 0; e < 16; e++) part[q - 1][e][r] = acc[e];
+        __syncthreads();
+        if (q == 0 && j < rows)
+            for (int e = 0; e < cnt; e++)
+                gb[(int64_t)(b0 + e) * rows + j] =
+                    (float)(((acc[e] + part[0][e][r]) + (part[1][e][r] + part[2][e][r])) + (double)bias[j]);
     }
 }
 
@@ -190,46 +205,55 @@ __global__ void f0n_kernel(const float* __restrict__ f0, const float* __restrict
     out[t * ld + col_n] = gap ? 0.f : b;
 }
 
-__global__ void copy_cols_kernel(const float* __restrict__ src, int64_t src_ld, int c, float* __restrict__ dst,
-                                 int64_t dst_ld, int dst_c0, const int32_t* __restrict__ col, int64_t l) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= l * c) return;
-    const int64_t t = i / c;
-    const int ch = (int)(i - t * c);
-    dst[t * dst_ld + dst_c0 + ch] = col[t] < 0 ? 0.f : src[t * src_ld + ch];
+__global__ __launch_bounds__(256) void copy_cols_kernel(const float* __restrict__ src, int64_t src_ld, int c,
+                                                        float* __restrict__ dst, int64_t dst_ld, int dst_c0,
+                                                        const int32_t* __restrict__ col, int64_t l) {
+    const int64_t t = blockIdx.x;  // one row per block, threads over its channels
+    const bool live = col[t] >= 0;
+    for (int ch = threadIdx.x; ch < c; ch += 256) dst[t * dst_ld + dst_c0 + ch] = live ? src[t * src_ld + ch] : 0.f;
 }
 
 // Decoder upsample block (src/gpu_batch.rs:106-117): AdaIN + leaky 0.2 (adain_apply_seg, gaps -> 0)
 // followed by the depthwise ConvTranspose1d k3 s2 p1 op1 (dw_convT_k3s2, kernels/kokoro.cu:150-166:
 // bias, then ascending contributing inputs), masked on d2 and rounded to bf16 for conv1.
-__global__ void adain_pool_kernel(const float* __restrict__ x, int64_t ld, int c, const Coef* __restrict__ coef,
-                                  const int32_t* __restrict__ col_n, int64_t ln, const float* __restrict__ pw,
-                                  const float* __restrict__ pb, const int32_t* __restrict__ col_2,
-                                  uint16_t* __restrict__ out, int64_t out_ld) {
+// One block per output row o of d2, threads over channel pairs: the row's item and contributing
+// inputs are uniform, every load and store is coalesced across the row.
+__global__ __launch_bounds__(256) void adain_pool_kernel(const float* __restrict__ x, int64_t ld, int c,
+                                                         const Coef* __restrict__ coef,
+                                                         const int32_t* __restrict__ col_n, int64_t ln,
+                                                         const float* __restrict__ pw, const float* __restrict__ pb,
+                                                         const int32_t* __restrict__ col_2, uint16_t* __restrict__ out,
+                                                         int64_t out_ld) {
 #pragma clang fp contract(off)
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= 2 * ln * out_ld) return;
-    const int64_t o = i / out_ld;
-    const int ch = (int)(i - o * out_ld);
-    float v = 0.f;
-    if (ch < c && col_2[o] >= 0) {
-        float acc = pb[ch];
-        for (int64_t t = (o - 1) / 2 - 1; t <= (o + 1) / 2; t++) {
-            if (t < 0 || t >= ln) continue;
-            const int64_t k = o + 1 - 2 * t;
-            if (k < 0 || k >= 3) continue;
-            const int b = col_n[t];
-            float a = 0.f;
-            if (b >= 0) {
-                const Coef cf = coef[(int64_t)b * c + ch];
-                a = __builtin_fmaf(x[t * ld + ch], cf.sc, cf.sh);
-                a = a < 0.f ? a * 0.2f : a;
-            }
-            acc = acc + pw[ch * 3 + k] * a;
-        }
-        v = acc;
+    const int64_t o = blockIdx.x;
+    const bool live = col_2[o] >= 0;
+    // contributing inputs t (ascending) and their taps k = o + 1 - 2 t in [0, 3), at most two
+    int64_t tt[2];
+    int kk[2], bb[2], nt = 0;
+    for (int64_t t = (o - 1) / 2 - 1; t <= (o + 1) / 2; t++) {
+        if (t < 0 || t >= ln) continue;
+        const int64_t k = o + 1 - 2 * t;
+        if (k < 0 || k >= 3 || nt == 2) continue;
+        tt[nt] = t, kk[nt] = (int)k, bb[nt] = col_n[t], nt++;
     }
-    out[o * out_ld + ch] = f32_to_bf16_bits(v);
+    for (int ch = 2 * threadIdx.x; ch < out_ld; ch += 512) {
+        float v[2] = {0.f, 0.f};
+        if (live && ch < c) {
+            for (int e = 0; e < 2; e++) v[e] = pb[ch + e];
+            for (int q = 0; q < nt; q++) {
+                float a[2] = {0.f, 0.f};
+                if (bb[q] >= 0) {
+                    const float2 xv = *(const float2*)(x + tt[q] * ld + ch);
+                    const float4 cf = *(const float4*)(coef + (int64_t)bb[q] * c + ch);  // (sc, sh) x 2
+                    a[0] = __builtin_fmaf(xv.x, cf.x, cf.y);
+                    a[1] = __builtin_fmaf(xv.y, cf.z, cf.w);
+                    for (int e = 0; e < 2; e++) a[e] = a[e] < 0.f ? a[e] * 0.2f : a[e];
+                }
+                for (int e = 0; e < 2; e++) v[e] = v[e] + pw[(ch + e) * 3 + kk[q]] * a[e];
+            }
+        }
+        *(uint32_t*)(out + o * out_ld + ch) = (uint32_t)f32_to_bf16_bits(v[0]) | ((uint32_t)f32_to_bf16_bits(v[1]) << 16);
+    }
 }
 
 // ------------------------------------------------------------------ noise convolutions (f32)
@@ -701,20 +725,23 @@ __global__ __launch_bounds__(256) void istft_kernel(IstftParams p) {
         fr[q][n] = v * (double)dft.win[n];
     }
     __syncthreads();
+    // overlap-add in block-local coordinates: jr = j - 5 f_first lies in [10, 531) (f_first is the
+    // first frame touching j = s0 + 10), so frame indices and taps are small 32-bit numbers
     float* out = p.audio + p.audio_start[b];
-    for (int64_t i = s0 + threadIdx.x; i < s1; i += blockDim.x) {
-        const int64_t j = i + 10;
-        const int64_t f_lo = j - 19 > 0 ? (j - 19 + 4) / 5 : 0;
-        int64_t f_hi = j / 5;
-        if (f_hi > nframes - 1) f_hi = nframes - 1;
+    const int jr0 = (int)(s0 + 10 - 5 * f_first);
+    const int fmax = (int)(nframes - 1 - f_first);
+    for (int ii = threadIdx.x; ii < (int)(s1 - s0); ii += blockDim.x) {
+        const int jr = jr0 + ii;
+        const int f_lo = f_first > 0 || jr > 19 ? (jr - 15) / 5 : 0;  // first frame with j - 5 f <= 19
+        const int f_hi = min(jr / 5, fmax);
         double acc = 0.0, env = 0.0;
-        for (int64_t f = f_lo; f <= f_hi; f++) {
-            const int n = (int)(j - 5 * f);
-            acc += fr[f - f_first][n];
+        for (int f = f_lo; f <= f_hi; f++) {
+            const int n = jr - 5 * f;
+            acc += fr[f][n];
             const double w = (double)dft.win[n];
             env += w * w;
         }
-        out[i] = (float)(acc / env);
+        out[s0 + ii] = (float)(acc / env);
     }
 }
 
@@ -785,7 +812,8 @@ hipError_t launch_finalize(const StatPart* part, int c, int wn, TilesDev t, int 
 
 hipError_t launch_style_fc(const float* w, const float* bias, int rows, const float* style, int nb, float* gb,
                            hipStream_t s) {
-    hipLaunchKernelGGL(style_fc_kernel, dim3(blocks_for(rows, 256)), dim3(256), 0, s, w, bias, rows, style, nb, gb);
+    if (rows <= 0 || nb <= 0) return hipSuccess;
+    hipLaunchKernelGGL(style_fc_kernel, dim3(blocks_for(rows, 64)), dim3(256), 0, s, w, bias, rows, style, nb, gb);
     return hipGetLastError();
 }
 
@@ -806,16 +834,19 @@ hipError_t launch_f0n_conv(const float* f0, const float* en, int64_t l2, const f
 
 hipError_t launch_copy_cols(const float* src, int64_t src_ld, int c, float* dst, int64_t dst_ld, int dst_c0,
                             const int32_t* col, int64_t l, hipStream_t s) {
-    hipLaunchKernelGGL(copy_cols_kernel, dim3(blocks_for(l * c, 256)), dim3(256), 0, s, src, src_ld, c, dst, dst_ld,
-                       dst_c0, col, l);
+    if (l <= 0 || c <= 0) return hipSuccess;
+    hipLaunchKernelGGL(copy_cols_kernel, dim3((unsigned)l), dim3(256), 0, s, src, src_ld, c, dst, dst_ld, dst_c0, col, l);
     return hipGetLastError();
 }
 
 hipError_t launch_adain_pool(const float* x, int64_t ld, int c, const Coef* coef, const int32_t* col_n, int64_t ln,
                              const float* pw, const float* pb, const int32_t* col_2, uint16_t* out, int64_t out_ld,
                              hipStream_t s) {
-    hipLaunchKernelGGL(adain_pool_kernel, dim3(blocks_for(2 * ln * out_ld, 256)), dim3(256), 0, s, x, ld, c, coef,
-                       col_n, ln, pw, pb, col_2, out, out_ld);
+    if (ln <= 0) return hipSuccess;
+    // channel pairs: float2 / two-Coef / bf16x2 accesses need even widths and leading dimensions
+    if ((c | ld | out_ld) & 1 || c > out_ld) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(adain_pool_kernel, dim3((unsigned)(2 * ln)), dim3(256), 0, s, x, ld, c, coef, col_n, ln, pw, pb,
+                       col_2, out, out_ld);
     return hipGetLastError();
 }
 
