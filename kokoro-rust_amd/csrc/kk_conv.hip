@@ -216,9 +216,6 @@ struct Slot {
                     } else if constexpr (PRO == PRO_ADAIN_SNAKE) {
                         const float c = __builtin_amdgcn_cosf(__builtin_fmaf(x, tsc[e], tsh[e]));
                         x = __builtin_fmaf(c, nh[e], __builtin_fmaf(x, sc[e], vsh[e]));
-                    } else if constexpr (PRO == PRO_GELU) {
-                        // gelu_new, sqrt(2 / pi) rounded to f32
-                        x = 0.5f * x * (1.0f + tanhf(0.797884560802865355f * (x + 0.044715f * x * x * x)));
                     }
                     // the Snake layers' cin is a multiple of the slab width (checked on the host)
                     if constexpr (!SNAKE) x = e < n_ch ? x : 0.f;
@@ -286,7 +283,23 @@ __device__ __forceinline__ void load_res(const ConvParams& p, const EpiBase& eb,
 // the fp16 bits.
 template <int EPI, bool OUT_H>
 __device__ __forceinline__ float4 finish4(const ConvParams& p, float4 v, const float4* r, uint2& pk) {
-    if constexpr (OUT_H) {
+    if constexpr (EPI == EPI_GELU_BF16) {
+        // gelu_new x (1 + tanh u) / 2, u = sqrt(2 / pi) (x + 0.044715 x^3), once per element, as
+        // x sigmoid(2 u) = x / (1 + 2^(-2 u log2 e)): one exp2 and one reciprocal (~1 ulp each, far
+        // below the bf16 rounding that follows), no cancellation for negative x, and the limits
+        // come out exact (2^(+inf) = inf -> -0, 2^(-inf) = 0 -> x).  Stored as the bf16 operand
+        // the next linear's MFMA reads (round to nearest even, as its f32 prologue would do).
+        constexpr float k2ul = 2.0f * 0.797884560802865355f * 1.44269504088896341f;
+        float g[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const float x = g[e];
+            const float t = __builtin_amdgcn_exp2f(-k2ul * __builtin_fmaf(0.044715f * x, x * x, x));
+            g[e] = x * __builtin_amdgcn_rcpf(1.0f + t);
+        }
+        pk = make_uint2(pack_bf16x2(g[0], g[1]), pack_bf16x2(g[2], g[3]));
+        return v;
+    } else if constexpr (OUT_H) {
         // fp16 storage; the statistics use the f32 values, as the reference's f32 h does (the fp16
         // rounding would move the mean and variance by ~2^-12 relative, far below the next
         // layer's bf16 operand rounding)
@@ -799,10 +812,11 @@ hipError_t launch_conv(const ConvParams& p, int pro, int epi, int shape, bool st
     KK_CONV(PRO_F32, EPI_STORE, SHAPE_256x128, 4, 1, false, false, false)
     KK_CONV(PRO_F32, EPI_STORE, SHAPE_64x256, 1, 2, false, false, false)
     KK_CONV(PRO_BF16, EPI_STORE, SHAPE_256x128, 4, 1, true, false, false)
-    // stages before the decoder: residual linears (ALBERT attention output, FFN output with gelu_new
-    // applied to its input)
+    // stages before the decoder: residual linears (ALBERT attention output; FFN output from the
+    // FFN's bf16 gelu_new output) and the FFN itself
     KK_CONV(PRO_F32, EPI_RESID, SHAPE_256x128, 4, 1, false, false, false)
-    KK_CONV(PRO_GELU, EPI_RESID, SHAPE_256x128, 4, 1, false, false, false)
+    KK_CONV(PRO_BF16, EPI_RESID, SHAPE_256x128, 4, 1, false, false, false)
+    KK_CONV(PRO_F32, EPI_GELU_BF16, SHAPE_256x128, 4, 1, false, false, true)
     // ConvT ups and conv_post
     KK_CONV(PRO_LEAKY, EPI_CONVT, SHAPE_256x128, 4, 1, true, false, false)
     KK_CONV(PRO_LEAKY, EPI_CONVT_REFLECT, SHAPE_256x128, 4, 1, true, false, false)

@@ -16,6 +16,7 @@
 #include <memory>
 #include <mutex>
 #include <string>
+#include <thread>
 #include <tuple>
 #include <vector>
 
@@ -686,6 +687,7 @@ struct Dom {
 struct Tiles {
     DevBuf item, t0, n, lo, hi;
     int64_t count = 0;
+    int64_t max_tiles = 0;  // the most tiles of any item
     int width = 0;
     TilesDev dev() const {
         return TilesDev{item.as<int32_t>(), t0.as<int64_t>(), n.as<int32_t>(), lo.as<int32_t>(), hi.as<int32_t>(),
@@ -697,6 +699,7 @@ struct Tiles {
         const int nb = (int)d.start.size();
         std::vector<int32_t> it, nn, lo_(nb), hi_(nb);
         std::vector<int64_t> t;
+        max_tiles = 0;
         for (int b = 0; b < nb; b++) {
             lo_[b] = (int32_t)it.size();
             const int64_t len = d.len[b] + extra;
@@ -706,6 +709,7 @@ struct Tiles {
                 nn.push_back((int32_t)std::min<int64_t>(w, len - j));
             }
             hi_[b] = (int32_t)it.size();
+            max_tiles = std::max<int64_t>(max_tiles, hi_[b] - lo_[b]);
         }
         count = (int64_t)it.size(), width = w;
         stage_vec(ctx, item, it), stage_vec(ctx, t0, t), stage_vec(ctx, n, nn);
@@ -1259,7 +1263,7 @@ struct Runner {
              const int64_t* xrow_at = nullptr) {
         const double bytes = (double)t.count * wn * c * sizeof(StatPart) + (double)p->nb * c * (sizeof(Coef) + 8);
         launch(PC_FINALIZE, 0, bytes, [&] {
-            return launch_finalize(part(), c, wn, t.dev(), p->nb, gbuf(), gb_ld(), a.gb_off,
+            return launch_finalize(part(), c, wn, t.dev(), p->nb, t.max_tiles * wn, gbuf(), gb_ld(), a.gb_off,
                                    a.nw.as<float>(), a.nb.as<float>(), coef, s, xrow, c, xrow_at);
         });
     }
@@ -1604,12 +1608,15 @@ struct Runner {
     }
 
     // ------------------------------------------------------------ the stages before the decoder
-    // Linear L over the rows of domain d: x [rows][x_ld] -> y [rows][y_ld] (piece i at its columns).
-    void linear(const MLinear& L, const void* x, int64_t x_ld, const Dom& d, float* y, int64_t y_ld,
+    // Linear L over the rows of domain d: x [rows][x_ld] -> y [rows][y_ld] (piece i at its columns;
+    // y_ld and the columns in elements of y: f32, or bf16 for EPI_GELU_BF16).
+    void linear(const MLinear& L, const void* x, int64_t x_ld, const Dom& d, void* y, int64_t y_ld,
                 const std::string& name, int pro = PRO_F32, int epi = EPI_STORE) {
+        const bool out_h = epi == EPI_GELU_BF16;
         for (size_t i = 0; i < L.piece.size(); i++) {
             Op o;
-            o.pro = pro, o.epi = epi, o.x = x, o.x_ld = x_ld, o.din = o.dout = &d, o.y = y + L.col0[i];
+            o.pro = pro, o.epi = epi, o.x = x, o.x_ld = x_ld, o.din = o.dout = &d, o.out_h = out_h;
+            o.y = (float*)((char*)y + L.col0[i] * (out_h ? 2 : 4));
             o.y_ld = y_ld, o.cls = PC_LINEAR, o.label = name;
             conv(L.piece[i], o);
         }
@@ -1689,7 +1696,7 @@ struct Runner {
         float* H = p->u_h.as<float>();
         float* QKV = p->u_qkv.as<float>();
         float* CTX = p->u_ctx.as<float>();
-        float* FF = p->u_ffn.as<float>();
+        uint16_t* FF = p->u_ffn.as<uint16_t>();
         label = "bert.embeddings";
         launch(PC_ROWS, 0, v * 128 * 12, [&] {
             return launch_albert_embed(p->ids.as<int32_t>(), p->row_item.as<int32_t>(), dt.start_d.as<int64_t>(), R,
@@ -1710,8 +1717,8 @@ struct Runner {
             });
             linear(u.dense, CTX, 768, dtf, H, 768, nm + ".dense", PRO_F32, EPI_RESID);
             layernorm(H, 768, 768, u.attn_g.as<float>(), u.attn_b.as<float>(), 0, 1e-12f, false, nm + ".attention_ln");
-            linear(u.ffn, H, 768, dtf, FF, 2048, nm + ".ffn");
-            linear(u.ffn_out, FF, 2048, dtf, H, 768, nm + ".ffn_output", PRO_GELU, EPI_RESID);
+            linear(u.ffn, H, 768, dtf, FF, 2048, nm + ".ffn", PRO_F32, EPI_GELU_BF16);  // bf16 gelu_new(ffn)
+            linear(u.ffn_out, FF, 2048, dtf, H, 768, nm + ".ffn_output", PRO_BF16, EPI_RESID);
             layernorm(H, 768, 768, u.full_g.as<float>(), u.full_b.as<float>(), 0, 1e-12f, false, nm + ".full_ln");
         }
         // duration encoder on x = [h | s] (640 wide): bert_encoder and each LSTM write h in place,
@@ -1892,11 +1899,30 @@ static void prebuild_tiles(kk_plan* p) {
 // (src/gpu_batch.rs:188-197), the token phase on the device, its logits back to the host and the
 // durations (src/gpu_batch.rs:234-248).  Phase B: the frame layout and everything after, as a
 // decoder plan whose t_en, F0 and N the plan computes itself.
+// KOKORO_HIP_TIMING=1: host-side times between the marks of one call on stderr (diagnostics).
+struct PhaseMarks {
+    bool on = env_i64("KOKORO_HIP_TIMING", 0) != 0;
+    std::chrono::steady_clock::time_point t = std::chrono::steady_clock::now();
+    std::string line;
+    void mark(const char* what) {
+        if (!on) return;
+        const auto now = std::chrono::steady_clock::now();
+        char buf[96];
+        std::snprintf(buf, sizeof buf, " %s %.3f ms,", what, std::chrono::duration<double, std::milli>(now - t).count());
+        line += buf;
+        t = now;
+    }
+    void print(const char* who) {
+        if (on) std::fprintf(stderr, "%s:%s\n", who, line.c_str());
+    }
+};
+
 static void init_full_plan(kk_plan* p, const kk_item* items, int n) {
     kk_ctx* ctx = p->ctx;
     const Model& m = ctx->model;
     check(m.ready && m.up.ready, "no model with the stages before the decoder uploaded");
     check(items != nullptr && n > 0, "empty batch");
+    PhaseMarks pm;
     reset_plan(p, PLAN_FULL, n);
     int64_t rows = 0;
     p->tstart.assign(n, 0), p->ntok.assign(n, 0);
@@ -1949,7 +1975,7 @@ static void init_full_plan(kk_plan* p, const kk_item* items, int n) {
     alloc_buf(p, p->u_h, R * 768 * sizeof(float));
     alloc_buf(p, p->u_qkv, R * 2304 * sizeof(float));
     alloc_buf(p, p->u_ctx, R * 768 * sizeof(float));
-    alloc_buf(p, p->u_ffn, R * 2048 * sizeof(float));
+    alloc_buf(p, p->u_ffn, R * 2048 * sizeof(uint16_t));
     alloc_buf(p, p->u_x, R * 640 * sizeof(float));
     alloc_buf(p, p->u_gx, R * 2048 * sizeof(float));
     alloc_buf(p, p->u_xl, R * 512 * sizeof(float));
@@ -1968,10 +1994,12 @@ static void init_full_plan(kk_plan* p, const kk_item* items, int n) {
         r.tokens();
     }
     stage_flush(ctx, p->tables_tok, ctx->stream);
+    pm.mark("token plan");
     {
         Runner r{p, ctx, m, ctx->stream};
         r.tokens();
     }
+    pm.mark("token enqueue");
     const size_t lg_bytes = R * Runner::kLogitsLd * sizeof(float);
     if (p->logits_cap < lg_bytes) {
         if (p->logits_host) (void)hipHostFree(p->logits_host);
@@ -1981,17 +2009,32 @@ static void init_full_plan(kk_plan* p, const kk_item* items, int n) {
     }
     KK_HIP(hipMemcpyAsync(p->logits_host, p->u_logits.p, lg_bytes, hipMemcpyDeviceToHost, ctx->stream));
     KK_HIP(hipStreamSynchronize(ctx->stream));
-    // durations_from_logits (src/model.rs:90-100) per item
+    pm.mark("token device");
+    // durations_from_logits (src/model.rs:90-100) per item, the items spread over a few host
+    // threads (each item's arithmetic is the rule's own, in its own order)
     p->pred.assign(n, {});
-    std::vector<float> lg;
+    for (int b = 0; b < n; b++) p->pred[b].assign(items[b].n_ids, 0);
+    std::vector<int> drc(n, KK_OK);
+    auto durations_of = [&](int b0, int stride) {
+        std::vector<float> lg;
+        for (int b = b0; b < n; b += stride) {
+            const int t = items[b].n_ids;
+            lg.resize((size_t)t * 50);
+            for (int i = 0; i < t; i++)
+                std::memcpy(&lg[(size_t)i * 50], p->logits_host + (size_t)(p->tstart[b] + i) * Runner::kLogitsLd,
+                            sizeof(float) * 50);
+            drc[b] = kk_durations_from_logits(lg.data(), t, items[b].speed, p->pred[b].data());
+        }
+    };
+    {
+        const int nt = std::max(1, std::min({n, 8, (int)std::thread::hardware_concurrency()}));
+        std::vector<std::thread> th;
+        for (int k = 1; k < nt; k++) th.emplace_back(durations_of, k, nt);
+        durations_of(0, nt);
+        for (auto& x : th) x.join();
+    }
     for (int b = 0; b < n; b++) {
-        const int t = items[b].n_ids;
-        lg.resize((size_t)t * 50);
-        for (int i = 0; i < t; i++)
-            std::memcpy(&lg[(size_t)i * 50], p->logits_host + (size_t)(p->tstart[b] + i) * Runner::kLogitsLd,
-                        sizeof(float) * 50);
-        p->pred[b].assign(t, 0);
-        check(kk_durations_from_logits(lg.data(), t, items[b].speed, p->pred[b].data()) == KK_OK, "durations");
+        check(drc[b] == KK_OK, "durations");
         int64_t nf = 0;
         for (int64_t d : p->pred[b]) nf += d;
         check(nf <= (int64_t)1 << 22, "item " + std::to_string(b) + ": too many frames");
@@ -1999,6 +2042,7 @@ static void init_full_plan(kk_plan* p, const kk_item* items, int n) {
                     nf, b);
         p->nfr.push_back(nf);
     }
+    pm.mark("durations");
     // ---- phase B: the frame layout and the decoder + generator inputs
     stage_begin(ctx);
     build_frame_layout(p);
@@ -2017,7 +2061,9 @@ static void init_full_plan(kk_plan* p, const kk_item* items, int n) {
         refs[b] = items[b].ref_s;
         nz[b] = NoiseIn{items[b].noise_kind, items[b].seed, items[b].rand_ini, items[b].sine, items[b].sine_len};
     }
+    pm.mark("frame layout");
     setup_generator(p, {}, refs, nz);
+    pm.mark("generator setup");
     alloc_buf(p, p->en, (size_t)2 * ln * sizeof(float));
     alloc_buf(p, p->u_sh, (size_t)ln * 512 * sizeof(float));
     for (int k = 0; k < 2; k++) {
@@ -2034,7 +2080,10 @@ static void init_full_plan(kk_plan* p, const kk_item* items, int n) {
     alloc_buf(p, p->pool, (size_t)2 * ln * kXinLd * sizeof(uint16_t));
     alloc_buf(p, p->sc_half, (size_t)ln * 512 * sizeof(float));
     alloc_buf(p, p->dec_out, (size_t)2 * ln * 512 * sizeof(float));
+    pm.mark("frame buffers");
     finish_plan(p);
+    pm.mark("frame plan");
+    pm.print("init_full_plan");
 }
 
 static void release_plan_device(kk_plan* p) {

@@ -31,7 +31,6 @@ enum Prologue {
     PRO_LEAKY = 2,        // leaky ReLU(slope)
     PRO_ADAIN_LEAKY = 3,  // AdaIN (per item, per channel affine) + leaky ReLU(slope)
     PRO_ADAIN_SNAKE = 4,  // AdaIN + Snake x + sin^2(a x)/a
-    PRO_GELU = 5,         // gelu_new (kernels/kokoro.cu:84-90)
 };
 enum Epilogue {
     EPI_STORE = 0,          // y = conv + b
@@ -42,6 +41,7 @@ enum Epilogue {
     EPI_MEAN3 = 5,          // y = ((r0 + r1) + (r2 + conv + b)) / 3
     EPI_CONVT = 6,          // polyphase ConvT scatter, y[o] = conv + b + r0[o]
     EPI_CONVT_REFLECT = 7,  // ConvT scatter with per-item ReflectionPad1d((1,0)), + r0
+    EPI_GELU_BF16 = 8,      // y (bf16) = gelu_new(conv + b) (kernels/kokoro.cu:84-90), 2-byte output
 };
 enum BlockShape {
     SHAPE_256x128 = 0,  // 4 waves (4 x 1), wave tile 64 x 128
@@ -93,12 +93,14 @@ hipError_t launch_conv(const ConvParams& p, int pro, int epi, int shape, bool st
 // Statistics partials of x [l][ld] over tiles (one partial per tile and channel).
 hipError_t launch_stats_tiles(const float* x, int64_t ld, int c, TilesDev t, StatPart* part, hipStream_t s);
 // Partials -> per-(item, channel) mean / rstd (chan_stats_seg semantics) -> AdaIN coefficients.
-// `wn` partials per tile (records [tile * wn + w][c]).
+// `wn` partials per tile (records [tile * wn + w][c]); max_parts: the most partials of any item
+// (tiles x wn), which sizes the reduction.
 // xrow (optional): one more sample per item outside the partials, row xrow_at[b] of xrow [.][xrow_ld]
 // (the reflected first row of the stage-1 ConvT output).
-hipError_t launch_finalize(const StatPart* part, int c, int wn, TilesDev t, int nb, const float* gb, int64_t gb_ld,
-                           int gb_off, const float* nw, const float* nb_, Coef* coef, hipStream_t s,
-                           const float* xrow = nullptr, int64_t xrow_ld = 0, const int64_t* xrow_at = nullptr);
+hipError_t launch_finalize(const StatPart* part, int c, int wn, TilesDev t, int nb, int64_t max_parts,
+                           const float* gb, int64_t gb_ld, int gb_off, const float* nw, const float* nb_, Coef* coef,
+                           hipStream_t s, const float* xrow = nullptr, int64_t xrow_ld = 0,
+                           const int64_t* xrow_at = nullptr);
 // gb[b][j] = W[j] . style[b] + bias[j] for every AdaIN layer at once.
 hipError_t launch_style_fc(const float* w, const float* bias, int rows, const float* style, int nb, float* gb,
                            hipStream_t s);

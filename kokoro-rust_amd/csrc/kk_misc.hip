@@ -65,14 +65,18 @@ __global__ __launch_bounds__(256) void stats_tiles_kernel(const float* __restric
 // AdaIN affine of adain_apply_seg (kernels/kokoro.cu:318-334) folded into v = x * sc + sh.
 // Every partial is re-centred on one reference per (item, channel) -- the item's first partial's
 // shift, a value of the data -- so the f64 sums need no division per partial and the final
-// E[d^2] - E[d]^2 cancels only over a few standard deviations.  16 threads per (item, channel)
-// reduce in a fixed tree: deterministic, no atomics.
-constexpr int kFinSub = 16;
-__global__ __launch_bounds__(256) void finalize_kernel(const StatPart* __restrict__ part, int c, int wn, TilesDev t,
-                                                       const float* __restrict__ gb, int64_t gb_ld, int gb_off,
-                                                       const float* __restrict__ nw, const float* __restrict__ nbias,
-                                                       Coef* __restrict__ coef, const float* __restrict__ xrow,
-                                                       int64_t xrow_ld, const int64_t* __restrict__ xrow_at) {
+// E[d^2] - E[d]^2 cancels only over a few standard deviations.  SUB threads per (item, channel)
+// reduce in a fixed tree: deterministic, no atomics.  Each thread issues the loads of up to LOADS
+// partials before it adds any, and the launcher picks the smallest SUB (16, 32 or 64) and LOADS
+// (1, 4 or 8) that cover the largest item's partials in one such round: one memory latency per
+// launch for most layers, and no idle threads for the decoder's few partials per item.
+template <int SUB, int LOADS>
+__global__ __launch_bounds__(16 * SUB) void finalize_kernel(const StatPart* __restrict__ part, int c, int wn, TilesDev t,
+                                                            const float* __restrict__ gb, int64_t gb_ld, int gb_off,
+                                                            const float* __restrict__ nw, const float* __restrict__ nbias,
+                                                            Coef* __restrict__ coef, const float* __restrict__ xrow,
+                                                            int64_t xrow_ld, const int64_t* __restrict__ xrow_at) {
+    constexpr int kFinSub = SUB;
     __shared__ double sa[kFinSub][16], sb[kFinSub][16], sn[kFinSub][16];
     const int cl = threadIdx.x & 15, sub = threadIdx.x >> 4;
     const int b = blockIdx.x;
@@ -90,14 +94,17 @@ __global__ __launch_bounds__(256) void finalize_kernel(const StatPart* __restric
     };
     if (ch < c && lo < hi) {
         ref = (double)part[lo * c + ch].shift;
-        // partials lo + sub, lo + sub + 16, ... in increasing order, four loads in flight
-        int64_t pi = lo + sub;
-        for (; pi + 3 * kFinSub < hi; pi += 4 * kFinSub) {
-            const StatPart q0 = part[pi * c + ch], q1 = part[(pi + kFinSub) * c + ch];
-            const StatPart q2 = part[(pi + 2 * kFinSub) * c + ch], q3 = part[(pi + 3 * kFinSub) * c + ch];
-            add(q0), add(q1), add(q2), add(q3);
+        // partials lo + sub, lo + sub + SUB, ... in increasing order; past hi a record with n = 0
+        for (int64_t base = lo + sub; base < hi; base += LOADS * kFinSub) {
+            StatPart q[LOADS];
+#pragma unroll
+            for (int j = 0; j < LOADS; j++) {
+                const int64_t pi = base + j * kFinSub;
+                q[j] = pi < hi ? part[pi * c + ch] : StatPart{0.f, 0.f, 0.f, 0.f};
+            }
+#pragma unroll
+            for (int j = 0; j < LOADS; j++) add(q[j]);
         }
-        for (; pi < hi; pi += kFinSub) add(part[pi * c + ch]);
     }
     sa[sub][cl] = a1, sb[sub][cl] = a2, sn[sub][cl] = n;
     __syncthreads();
@@ -801,13 +808,20 @@ hipError_t launch_stats_tiles(const float* x, int64_t ld, int c, TilesDev t, Sta
     return hipGetLastError();
 }
 
-hipError_t launch_finalize(const StatPart* part, int c, int wn, TilesDev t, int nb, const float* gb, int64_t gb_ld,
-                           int gb_off, const float* nw, const float* nb_, Coef* coef, hipStream_t s, const float* xrow,
-                           int64_t xrow_ld, const int64_t* xrow_at) {
+hipError_t launch_finalize(const StatPart* part, int c, int wn, TilesDev t, int nb, int64_t max_parts,
+                           const float* gb, int64_t gb_ld, int gb_off, const float* nw, const float* nb_, Coef* coef,
+                           hipStream_t s, const float* xrow, int64_t xrow_ld, const int64_t* xrow_at) {
     dim3 grid((unsigned)nb, (unsigned)ceil_div(c, 16));
-    hipLaunchKernelGGL(finalize_kernel, grid, dim3(256), 0, s, part, c, wn, t, gb, gb_ld, gb_off, nw, nb_, coef, xrow,
-                       xrow_ld, xrow_at);
-    return hipGetLastError();
+    auto go = [&](auto kern, int sub) {
+        hipLaunchKernelGGL(kern, grid, dim3(16 * sub), 0, s, part, c, wn, t, gb, gb_ld, gb_off, nw, nb_, coef, xrow,
+                           xrow_ld, xrow_at);
+        return hipGetLastError();
+    };
+    if (max_parts <= 16) return go(finalize_kernel<16, 1>, 16);
+    if (max_parts <= 64) return go(finalize_kernel<16, 4>, 16);
+    if (max_parts <= 128) return go(finalize_kernel<16, 8>, 16);
+    if (max_parts <= 256) return go(finalize_kernel<32, 8>, 32);
+    return go(finalize_kernel<64, 8>, 64);
 }
 
 hipError_t launch_style_fc(const float* w, const float* bias, int rows, const float* style, int nb, float* gb,

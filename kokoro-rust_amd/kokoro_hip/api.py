@@ -407,6 +407,16 @@ class Context:
         _check(lib().kk_forward_decoder_batch(self.h, pb.arr, pb.n, pb.outs, err, len(err)), err)
 
 
+    def forward_ids_prepared(self, pb):
+        """kk_forward_batch on a PreparedIdsBatch; the results stay in pb.outs (release with
+        pb.release()).  Raises KKError on failure."""
+        err = _err()
+        _check(lib().kk_forward_batch(self.h, pb.arr, pb.n, pb.outs, err, len(err)), err)
+
+    def prepare_ids(self, items):
+        """The ids-level items marshalled once into the ABI's structs, for repeated calls (timing)."""
+        return PreparedIdsBatch(items)
+
     def host_alloc(self, count, dtype):
         """kk_host_alloc: a pinned host array of `count` elements of `dtype` (freed with .free())."""
         return PinnedArray(self, count, dtype)
@@ -433,6 +443,24 @@ class PreparedBatch:
 
     def release(self):
         lib().kk_output_free(self.outs, self.n)
+
+
+class PreparedIdsBatch:
+    def __init__(self, items):
+        self.arr, self._keep = _items(items)
+        self.n = len(items)
+        self.outs = (Result * self.n)()
+
+    def audio(self, b):
+        o = self.outs[b]
+        return np.ctypeslib.as_array(o.audio, shape=(o.n_samples,)).copy()
+
+    def pred_dur(self, b):
+        o = self.outs[b]
+        return np.ctypeslib.as_array(o.pred_dur, shape=(o.n_tok,)).copy()
+
+    def release(self):
+        lib().kk_result_free(self.outs, self.n)
 
 
 class PinnedArray:

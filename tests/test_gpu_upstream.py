@@ -8,8 +8,10 @@ The argument has three parts:
    convolutions rounded to bf16 where the GPU's MFMA layers (and the reference's GLinear / BF16
    convs) round them -- the tight bar;
 2. the durations: bit for bit the host rule on the device's logits, and equal to the oracle's
-   except tokens whose sigmoid sum lies within 0.05 of a rounding tie (there the f32 logits of any
-   implementation may round either way);
+   except tokens whose sigmoid sum lies near a rounding tie -- "near" measured by the oracle itself:
+   its float32 run differs from its float64 run by up to ~0.04 in these sums (a sum of 50 sigmoids
+   carries the logits' correlated rounding noise), so any f32 implementation may round such a
+   token either way;
 3. the audio of the ids-level call bit for bit equal to the decoder entry's audio on the ids-level
    call's own durations, t_en, F0 and N -- and the decoder entry is pinned against the oracle by
    tests/test_gpu_parity.py.
@@ -25,7 +27,12 @@ from conftest import snr_db
 
 pytestmark = pytest.mark.gpu
 
-TIE = 0.05
+# The device's duration sigmoid sums against the oracle's own float32-vs-float64 spread: the largest
+# deviation within MAX_FACTOR x the spread's largest (a maximum over ~120 tokens of noise of the
+# same scale varies by ~2x from one draw to the next: 1.8x between the device and the oracle's f32
+# run, measured), the mean deviation within MEAN_FACTOR x the spread's mean.
+MAX_FACTOR = 3.0
+MEAN_FACTOR = 2.0
 
 
 def _print(*a):
@@ -69,6 +76,26 @@ def full_run(full_ctx):
 
 
 @pytest.fixture(scope="module")
+def oracle_f32_sums(full_run, full_weights):
+    """The bf16-operand oracle run in float32: its duration logits' sigmoid sums, the spread that
+    float32 rounding alone puts between two correct implementations."""
+    import torch
+    from oracle import torch_ref as R
+    items = full_run[0]
+    out = []
+    R.set_dtype(torch.float32)
+    try:
+        for it in items:
+            t = {}
+            with R.bf16_operands():
+                R.upstream(full_weights, it.ids, it.ref_s, taps=t)
+            out.append(torch.sigmoid(t["logits"].to(torch.float64)).sum(1).numpy() / it.speed)
+    finally:
+        R.set_dtype(torch.float64)
+    return out
+
+
+@pytest.fixture(scope="module")
 def oracle_runs(full_run, full_weights):
     from oracle import torch_ref as R
     items, _, durs, _ = full_run
@@ -99,27 +126,34 @@ def test_token_phase_vs_oracle(full_run, oracle_runs):
             assert s_plain >= 25.0, name
 
 
-def test_durations_vs_oracle(full_run, oracle_runs):
+def test_durations_vs_oracle(full_run, oracle_runs, oracle_f32_sums):
     """Integer parity of the rule: the durations are durations_from_logits (src/model.rs:90-100) of
-    the device's own logits, bit for bit.  Against the oracle: the sigmoid sums within TIE of the
-    bf16-operand oracle's, and the durations equal wherever the oracle's sum lies further than TIE
-    from a rounding tie (a sum of 50 sigmoids carries the logits' correlated rounding noise)."""
+    the device's own logits, bit for bit.  Against the bf16-operand oracle (float64): the sigmoid
+    sums within MAX_FACTOR x the oracle's own float32-vs-float64 spread (the largest over the
+    batch, at least 0.02) at every token, and within MEAN_FACTOR x its mean spread on average;
+    the durations equal wherever the oracle's sum lies further than that bar from a rounding tie."""
     import torch
     from kokoro_hip import api
     from oracle import torch_ref as R
     items, _, durs, taps = full_run
     _, emu = oracle_runs
-    for it, d, tp, e in zip(items, durs, taps, emu):
+    sums = [torch.sigmoid(e["logits"]).sum(1).numpy() / it.speed for it, e in zip(items, emu)]
+    spread = np.concatenate([np.abs(a - b) for a, b in zip(sums, oracle_f32_sums)])
+    bar = MAX_FACTOR * max(float(spread.max()), 0.02)
+    dev = []
+    for it, d, tp, e, s in zip(items, durs, taps, emu, sums):
         assert np.array_equal(d, api.durations_from_logits(np.ascontiguousarray(tp["logits"].T), it.speed))
-        s = torch.sigmoid(e["logits"]).sum(1).numpy() / it.speed
         s_gpu = torch.sigmoid(torch.from_numpy(tp["logits"].T.astype(np.float64))).sum(1).numpy() / it.speed
         want = R.durations(e["logits"], it.speed)
-        tie = np.abs(s - np.floor(s) - 0.5) < TIE
-        _print(f"  durations: {len(d)} tokens, max |sum sigmoid - oracle| {np.abs(s_gpu - s).max():.4f}, "
-               f"{int(tie.sum())} within {TIE} of a tie, {int((d != want).sum())} differ")
-        assert np.abs(s_gpu - s).max() < TIE
+        tie = np.abs(s - np.floor(s) - 0.5) < bar
+        dev.append(np.abs(s_gpu - s))
+        _print(f"  durations: {len(d)} tokens, max |sum sigmoid - oracle| {dev[-1].max():.4f} "
+               f"(oracle f32 spread {spread.max():.4f}, bar {bar:.4f}), {int(tie.sum())} within the bar of a tie, "
+               f"{int((d != want).sum())} differ")
+        assert dev[-1].max() < bar
         assert np.array_equal(d[~tie], want[~tie])
         assert d.min() >= 1
+    assert np.concatenate(dev).mean() <= MEAN_FACTOR * spread.mean()
 
 
 def test_prosody_vs_oracle(full_run, oracle_runs, full_weights):
