@@ -175,7 +175,11 @@ typedef struct {
  * from the logits on the host (durations_from_logits, src/model.rs:90-100: one copy of the logits
  * back), then the frame layout, the shared LSTM, the F0 / N stacks, the decoder, the generator and
  * the iSTFT.  Results in input order.  Kept buffers, failure release and test hooks as
- * kk_forward_decoder_batch. */
+ * kk_forward_decoder_batch.  Every BiLSTM recurrence runs each (item, direction) on a pair of CUs
+ * that trade their halves of h each step; a block that waits more than 2 s for its partner ends
+ * its launch and the call fails with KK_ERR_HIP (KOKORO_HIP_LSTM_SINGLE=1, read once per process,
+ * selects the one-CU kernel instead; test hook KOKORO_HIP_TEST_LSTM_SILENT=1, read at each launch,
+ * forces that failure with a 10 us wait). */
 int kk_forward_batch(kk_ctx* ctx, const kk_item* items, int n, kk_result* out, char* err, size_t errlen);
 void kk_result_free(kk_result* out, int n);
 

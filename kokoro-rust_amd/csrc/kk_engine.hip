@@ -772,9 +772,14 @@ struct kk_plan {
     kk::DevBuf ids, row_item, att_item, att_head, att_q0, style_pro, gbp;
     kk::DevBuf u_emb, u_h, u_qkv, u_ctx, u_ffn, u_x, u_gx, u_xl, u_logits, u_te, u_te2, u_gxt, u_gxs, u_sh;
     kk::DevBuf u_fx[2], u_fpool[2], u_fh[2], u_fsc[2], u_fy[2];  // the F0 and N stacks
+    // the two-CU recurrences' exchange words: word 0 the run's abort flag, then one region per
+    // stream that runs recurrences (the main stream, and side stream 0 for the text encoder)
+    kk::DevBuf u_lstmx;
+    static constexpr int64_t kLstmXHead = 64;
     int64_t n_att = 0;
     float* logits_host = nullptr;  // pinned, grow-only (the duration logits come back through it)
     size_t logits_cap = 0;
+    uint64_t* abort_host = nullptr;  // pinned: the recurrences' abort flag comes back through it
     hipEvent_t te_ev[2] = {nullptr, nullptr};  // fork / join of the text encoder and of the N stack
     kk::DevBuf pcm, pcm_len, pcm_clip;  // PCM_16 output: samples [600 ln], samples per item, clip counts
     int64_t n_src = 0, n_ist = 0;
@@ -796,6 +801,8 @@ struct kk_plan {
             if (e) (void)hipEventDestroy(e), e = nullptr;
         if (logits_host) (void)hipHostFree(logits_host);
         logits_host = nullptr, logits_cap = 0;
+        if (abort_host) (void)hipHostFree(abort_host);
+        abort_host = nullptr;
     }
     // fork / join of the resblock chains, and of the noise branches (created with the plan)
     hipEvent_t chain_ev[3] = {nullptr, nullptr, nullptr};
@@ -808,7 +815,7 @@ struct kk_plan {
                 &ist_item, &ist_s0, &pcm, &pcm_len, &pcm_clip, &tables_tok, &ids, &row_item, &att_item,
                 &att_head, &att_q0, &style_pro, &gbp, &u_emb, &u_h, &u_qkv, &u_ctx, &u_ffn, &u_x, &u_gx, &u_xl,
                 &u_logits, &u_te, &u_te2, &u_gxt, &u_gxs, &u_sh, &u_fx[0], &u_fx[1], &u_fpool[0], &u_fpool[1],
-                &u_fh[0], &u_fh[1], &u_fsc[0], &u_fsc[1], &u_fy[0], &u_fy[1]};
+                &u_fh[0], &u_fh[1], &u_fsc[0], &u_fsc[1], &u_fy[0], &u_fy[1], &u_lstmx};
     }
 };
 
@@ -1623,13 +1630,26 @@ struct Runner {
     }
     // BiLSTM recurrence over the item spans of d (gx rows through gx_row, or the spans' own rows);
     // h into out[row][0:512].  Algorithmic traffic: gx read and h written once per row, W_hh once.
+    // Each sequence runs on two CUs (launch_lstm_pair) with its exchange words in `region` (one per
+    // stream that runs recurrences at the same time); KOKORO_HIP_LSTM_SINGLE=1 selects the one-CU
+    // kernel (W_hh partly streamed from L2 each step).  Test hook, read at each launch:
+    // KOKORO_HIP_TEST_LSTM_SILENT=1 keeps the second half of every pair from publishing and cuts the
+    // wait to 10 us, so that the run ends with the pair kernel's abort.
     void recur(const MLstm& l, const float* gx, const int32_t* gx_row, const Dom& d, float* out, int64_t out_ld,
-               const std::string& name) {
+               const std::string& name, int region = 0) {
+        static const bool single = env_i64("KOKORO_HIP_LSTM_SINGLE", 0) != 0;
+        const bool silent = env_i64("KOKORO_HIP_TEST_LSTM_SILENT", 0) != 0;
         const double v = (double)d.valid();
         label = name;
         launch(PC_LSTM, v * 2 * 1024 * 256 * 2, v * (2048 + 512) * 4 + 2.0 * 1024 * 257 * 4, [&] {
-            return launch_lstm(gx, 2048, gx_row, d.start_d.as<int64_t>(), d.len_d.as<int64_t>(), p->nb,
-                               l.whh_t.as<float>(), l.bhh.as<float>(), out, out_ld, s);
+            if (single)
+                return launch_lstm(gx, 2048, gx_row, d.start_d.as<int64_t>(), d.len_d.as<int64_t>(), p->nb,
+                                   l.whh_t.as<float>(), l.bhh.as<float>(), out, out_ld, s);
+            uint64_t* x = p->u_lstmx.as<uint64_t>();
+            return launch_lstm_pair(gx, 2048, gx_row, d.start_d.as<int64_t>(), d.len_d.as<int64_t>(), p->nb,
+                                    l.whh_t.as<float>(), l.bhh.as<float>(), out, out_ld,
+                                    x + kk_plan::kLstmXHead + (int64_t)region * 2 * p->nb * 512, (int*)x, s,
+                                    silent ? 1000 : kLstmPairWaitTicks, silent ? 1 : -1);
         });
     }
     void layernorm(float* x, int64_t ld, int d, const float* g, const float* b, int gb_off, float eps, bool leaky,
@@ -1662,7 +1682,7 @@ struct Runner {
             std::swap(in, out);
         }
         linear(u.te_lstm.wih, in, 512, p->dtf, p->u_gxt.as<float>(), 2048, "text_encoder.lstm.ih");
-        recur(u.te_lstm, p->u_gxt.as<float>(), nullptr, dt, p->t_en.as<float>(), 512, "text_encoder.lstm");
+        recur(u.te_lstm, p->u_gxt.as<float>(), nullptr, dt, p->t_en.as<float>(), 512, "text_encoder.lstm", 1);
     }
     // The token phase (src/gpu_batch.rs:198-248): ALBERT, bert_encoder, the duration encoder, the
     // duration LSTM and projection (logits [rows][kLogitsLd]), the shared LSTM's gate
@@ -1676,6 +1696,7 @@ struct Runner {
         const double v = (double)dt.valid();
         const bool conc = !ctx->profiling && !dry;
         hipStream_t main_s = s;
+        if (!dry) KK_HIP(launch_clear_u64(p->u_lstmx.as<uint64_t>(), 1, s));  // the run's abort flag
         if (conc) {
             KK_HIP(hipEventRecord(p->te_ev[0], main_s));
             KK_HIP(hipStreamWaitEvent(ctx->side[0], p->te_ev[0], 0));
@@ -1899,6 +1920,14 @@ static void prebuild_tiles(kk_plan* p) {
 // (src/gpu_batch.rs:188-197), the token phase on the device, its logits back to the host and the
 // durations (src/gpu_batch.rs:234-248).  Phase B: the frame layout and everything after, as a
 // decoder plan whose t_en, F0 and N the plan computes itself.
+// A two-CU recurrence whose block waited more than 2 s for its partner ends every block of its
+// launch and leaves the run's abort flag set (read back into abort_host with the run's last copy).
+static void check_lstm_abort(kk_plan* p) {
+    if (p->abort_host && *p->abort_host != 0)
+        fail(KK_ERR_HIP, "BiLSTM recurrence: a block of a two-CU pair waited more than 2 s for its partner "
+                          "(set KOKORO_HIP_LSTM_SINGLE=1 for the one-CU kernel)");
+}
+
 // KOKORO_HIP_TIMING=1: host-side times between the marks of one call on stderr (diagnostics).
 struct PhaseMarks {
     bool on = env_i64("KOKORO_HIP_TIMING", 0) != 0;
@@ -1985,6 +2014,8 @@ static void init_full_plan(kk_plan* p, const kk_item* items, int n) {
     alloc_buf(p, p->u_gxt, R * 2048 * sizeof(float));
     alloc_buf(p, p->u_gxs, R * 2048 * sizeof(float));
     alloc_buf(p, p->t_en, R * 512 * sizeof(float));
+    alloc_buf(p, p->u_lstmx, (size_t)(kk_plan::kLstmXHead + 2 * 2 * (int64_t)n * 512) * sizeof(uint64_t));
+    if (!p->abort_host) KK_HIP(hipHostMalloc((void**)&p->abort_host, sizeof(uint64_t), hipHostMallocDefault));
     p->t_rows = rows;
     for (auto& e : p->te_ev)
         if (!e) KK_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
@@ -2008,7 +2039,9 @@ static void init_full_plan(kk_plan* p, const kk_item* items, int n) {
         p->logits_cap = lg_bytes;
     }
     KK_HIP(hipMemcpyAsync(p->logits_host, p->u_logits.p, lg_bytes, hipMemcpyDeviceToHost, ctx->stream));
+    KK_HIP(hipMemcpyAsync(p->abort_host, p->u_lstmx.p, sizeof(uint64_t), hipMemcpyDeviceToHost, ctx->stream));
     KK_HIP(hipStreamSynchronize(ctx->stream));
+    check_lstm_abort(p);
     pm.mark("token device");
     // durations_from_logits (src/model.rs:90-100) per item, the items spread over a few host
     // threads (each item's arithmetic is the rule's own, in its own order)
@@ -2638,7 +2671,10 @@ static void fetch_plan(kk_plan* plan, kk_output* out) {
     float* blk = (float*)out_block_take(bytes, plan->nb);
     for (int b = 0; b < plan->nb; b++) out[b] = kk_output{blk + 600 * plan->a[b], 600 * plan->nfr[b]};
     KK_HIP(hipMemcpyAsync(blk, plan->audio.p, bytes, hipMemcpyDeviceToHost, s));
+    if (plan->kind == PLAN_FULL)
+        KK_HIP(hipMemcpyAsync(plan->abort_host, plan->u_lstmx.p, sizeof(uint64_t), hipMemcpyDeviceToHost, s));
     KK_HIP(hipStreamSynchronize(s));
+    if (plan->kind == PLAN_FULL) check_lstm_abort(plan);
 }
 
 int kk_plan_fetch(kk_plan* plan, kk_output* out, char* err, size_t errlen) {

@@ -205,6 +205,17 @@ hipError_t launch_attention(const float* qkv, const int64_t* start, const int64_
 // h -> out[r][dir 256 + j].
 hipError_t launch_lstm(const float* gx, int64_t gx_ld, const int32_t* gx_row, const int64_t* start, const int64_t* len,
                        int nb, const float* whh_t, const float* bhh, float* out, int64_t out_ld, hipStream_t s);
+// The same recurrence with each (item, direction) split over two CUs that trade their halves of h
+// every step (the whole of W_hh on chip).  xbuf: 2 nb x 512 exchange words (cleared by the launch);
+// *abort is set, and every block ends, if a block waits more than wait_ticks (100 MHz clock) for
+// its partner.  silent_half >= 0 (a test hook) keeps that half of every pair from publishing.
+constexpr uint64_t kLstmPairWaitTicks = 200000000ull;  // 2 s
+hipError_t launch_lstm_pair(const float* gx, int64_t gx_ld, const int32_t* gx_row, const int64_t* start,
+                            const int64_t* len, int nb, const float* whh_t, const float* bhh, float* out, int64_t out_ld,
+                            uint64_t* xbuf, int* abort, hipStream_t s, uint64_t wait_ticks = kLstmPairWaitTicks,
+                            int silent_half = -1);
+// Zeroes n 64-bit words.
+hipError_t launch_clear_u64(uint64_t* x, int64_t n, hipStream_t s);
 // F0_proj / N_proj: y[r] = b + w . x[r][0:c] (c = 256) on the rows with col[r] >= 0, 0 elsewhere.
 hipError_t launch_proj1(const float* x, int64_t ld, int c, const float* w, const float* b, const int32_t* col,
                         int64_t rows, float* y, hipStream_t s);

@@ -330,6 +330,136 @@ __global__ void __launch_bounds__(kLstmThreads) lstm_kernel(const float* gx, int
     }
 }
 
+// The same recurrence with each (item, direction) sequence split over a pair of blocks on two CUs:
+// block half hf owns hidden units [128 hf, 128 hf + 128), i.e. the 512 gate rows g 256 + 128 hf + u,
+// and all 512 KB of their W_hh stay on its CU (thread t: rows 4c..4c+3 of the half, c = t mod 128,
+// over the k-quarter [64 q, 64 q + 64), q = t / 128; 48 of its k in registers, 16 in LDS).  Each
+// step a block computes its 128 units of h and trades them with its partner through the exchange
+// buffer: one 64-bit word per unit, (step + 1) << 32 | bits(h), written and polled with relaxed
+// device-scope atomics -- a word carries its own step, so no fence orders data and flag.  Two
+// parities of words per half: a block overwrites the words of step s at step s + 2 only after its
+// partner has used them (the partner's step s + 1 needed them).  The buffer starts at zero each
+// launch (lstm_exchange_clear_kernel), the first valid tag is 1.
+// Pairing: block B = 16 grp + 8 hf + x is half hf of sequence 8 grp + x, so the two halves sit 8
+// apart (the same XCD under round-robin dispatch, and consecutive on it).  Every wait is bounded:
+// past wait_ticks of the 100 MHz clock (or once another block gave up) the block sets *abort and
+// ends, and the host reports the run as failed.  silent_half (a test hook; -1 otherwise): the
+// blocks of that half publish nothing, so that their partners' waits run out.
+constexpr int kLpKR = 48, kLpKL = 16;  // per thread: k in registers, k in LDS (of 64)
+constexpr size_t kLpLds = ((size_t)4 * kLpKL * 512 + 4 * 512 + kH) * sizeof(float);
+__global__ void __launch_bounds__(kLstmThreads) lstm_pair_kernel(const float* gx, int64_t gx_ld, const int32_t* gx_row,
+                                                                 const int64_t* start, const int64_t* len, int nseq,
+                                                                 const float* whh_t, const float* bhh, float* out,
+                                                                 int64_t out_ld, uint64_t* xbuf, int* abort,
+                                                                 uint64_t wait_ticks, int silent_half) {
+    extern __shared__ __align__(16) float lsm[];
+    float* Wl = lsm;                       // [4 quarters][kLpKL][512 rows]
+    float* part = Wl + 4 * kLpKL * 512;    // [4][512] partial dot products
+    float* hs = part + 4 * 512;            // [256] h of the previous step
+    __shared__ int gave_up;
+    const int B = blockIdx.x, grp = B >> 4, hf = (B >> 3) & 1;
+    const int seq = grp * 8 + (B & 7);
+    if (seq >= nseq) return;  // the pair's other half returns too
+    const int item = seq >> 1, dir = seq & 1;
+    const int t = threadIdx.x, q = t >> 7, c = t & 127;
+    const int64_t s0 = start[item], n = len[item];
+    // this thread's four gate rows (one gate g = c / 32, units 4 (c mod 32) .. + 3 of the half)
+    const int g0 = (c >> 5) * kH + 128 * hf + 4 * (c & 31);
+    const float* W = whh_t + (int64_t)dir * kH * 4 * kH;
+    float4 wr[kLpKR];
+#pragma unroll
+    for (int i = 0; i < kLpKR; i++) wr[i] = *(const float4*)(W + (int64_t)(64 * q + i) * 4 * kH + g0);
+    for (int i = t; i < 4 * kLpKL * 128; i += kLstmThreads) {
+        const int row = i >> 7, qq = row / kLpKL, ii = row - qq * kLpKL, cc = i & 127;
+        const int gg = (cc >> 5) * kH + 128 * hf + 4 * (cc & 31);
+        *(float4*)(Wl + (int64_t)row * 512 + 4 * cc) = *(const float4*)(W + (int64_t)(64 * qq + kLpKR + ii) * 4 * kH + gg);
+    }
+    float cst = 0.f, bh[4];
+    if (t < 128) {
+#pragma unroll
+        for (int g = 0; g < 4; g++) bh[g] = bhh[dir * 4 * kH + g * kH + 128 * hf + t];
+    }
+    if (t < kH) hs[t] = 0.f;
+    if (t == 0) gave_up = 0;
+    __syncthreads();
+    const float* Wlq = Wl + (int64_t)(q * kLpKL) * 512 + 4 * c;
+    const float* hq = hs + 64 * q;
+    uint64_t* xw = xbuf + (int64_t)seq * 512 + hf * 256;        // [parity][128] this half's words
+    const uint64_t* xr = xbuf + (int64_t)seq * 512 + (1 - hf) * 256;  // the partner's
+    for (int64_t step = 0; step < n; step++) {
+        const int64_t row = s0 + (dir == 0 ? step : n - 1 - step);
+        float gxv[4];
+        if (t < 128) {
+            const int64_t grow = gx_row ? (int64_t)gx_row[row] : row;
+#pragma unroll
+            for (int g = 0; g < 4; g++) gxv[g] = gx[grow * gx_ld + dir * 4 * kH + g * kH + 128 * hf + t];
+        }
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int i = 0; i < kLpKR; i += 4) {
+            const float4 h4 = *(const float4*)(hq + i);
+            const float hv[4] = {h4.x, h4.y, h4.z, h4.w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float4 w = wr[i + e];
+                acc.x = fmaf(w.x, hv[e], acc.x), acc.y = fmaf(w.y, hv[e], acc.y);
+                acc.z = fmaf(w.z, hv[e], acc.z), acc.w = fmaf(w.w, hv[e], acc.w);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < kLpKL; i++) {
+            const float hv = hq[kLpKR + i];
+            const float4 w = *(const float4*)(Wlq + (int64_t)i * 512);
+            acc.x = fmaf(w.x, hv, acc.x), acc.y = fmaf(w.y, hv, acc.y);
+            acc.z = fmaf(w.z, hv, acc.z), acc.w = fmaf(w.w, hv, acc.w);
+        }
+        *(float4*)(part + q * 512 + 4 * c) = acc;
+        __syncthreads();
+        if (t < 128) {
+            float gate[4];
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                const int r = g * 128 + t;
+                gate[g] = gxv[g] + (((part[r] + part[512 + r]) + (part[1024 + r] + part[1536 + r])) + bh[g]);
+            }
+            const float ig = sigmoid(gate[0]), fg = sigmoid(gate[1]), gg = tanhf(gate[2]), og = sigmoid(gate[3]);
+            cst = fg * cst + ig * gg;
+            const float h = og * tanhf(cst);
+            const uint64_t tag = (uint64_t)(step + 1) << 32;
+            if (hf != silent_half)
+                __hip_atomic_store(xw + (step & 1) * 128 + t, tag | __float_as_uint(h), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+            hs[128 * hf + t] = h;
+            out[row * out_ld + dir * kH + 128 * hf + t] = h;
+            // the partner's unit t of this step
+            const uint64_t* src = xr + (step & 1) * 128 + t;
+            const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+            uint64_t w;
+            for (uint32_t spin = 1;; spin++) {
+                w = __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if ((w & 0xffffffff00000000ull) == tag) break;
+                if ((spin & 255) == 0 && (__hip_atomic_load(abort, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0 ||
+                                          __builtin_amdgcn_s_memrealtime() - t0 > wait_ticks)) {
+                    gave_up = 1;
+                    break;
+                }
+            }
+            hs[128 * (1 - hf) + t] = __uint_as_float((uint32_t)w);
+        }
+        __syncthreads();
+        if (gave_up) {
+            if (t == 0) __hip_atomic_store(abort, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            return;
+        }
+    }
+}
+
+// Zeroes the pair recurrence's exchange words (n 64-bit words) before a launch.
+__global__ void __launch_bounds__(256) lstm_exchange_clear_kernel(uint64_t* x, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) x[i] = 0;
+}
+
 // out[r][col0 + c] = styles[row_item[r]][c] for the item rows (cat_style_rows_seg's style half,
 // kernels/kokoro.cu:375-384; the other half is written in place by its producer).
 __global__ void __launch_bounds__(256) style_cols_kernel(float* x, int64_t ld, int col0, int64_t rows,
@@ -428,6 +558,37 @@ hipError_t launch_lstm(const float* gx, int64_t gx_ld, const int32_t* gx_row, co
     }
     hipLaunchKernelGGL(lstm_kernel, dim3((unsigned)(2 * nb)), dim3(kLstmThreads), kLstmLds, s, gx, gx_ld, gx_row, start,
                        len, whh_t, bhh, out, out_ld);
+    return hipGetLastError();
+}
+
+hipError_t launch_lstm_pair(const float* gx, int64_t gx_ld, const int32_t* gx_row, const int64_t* start,
+                            const int64_t* len, int nb, const float* whh_t, const float* bhh, float* out, int64_t out_ld,
+                            uint64_t* xbuf, int* abort, hipStream_t s, uint64_t wait_ticks, int silent_half) {
+    if (nb <= 0) return hipSuccess;
+    if (!xbuf || !abort || wait_ticks == 0) return hipErrorInvalidValue;
+    static std::atomic<uint64_t> attr_set{0};
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+    if (!((attr_set.load() >> dev) & 1u)) {
+        e = hipFuncSetAttribute((const void*)lstm_pair_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLpLds);
+        if (e != hipSuccess) return e;
+        attr_set.fetch_or(1ull << dev);
+    }
+    const int nseq = 2 * nb;
+    const int64_t words = (int64_t)nseq * 512;
+    hipLaunchKernelGGL(lstm_exchange_clear_kernel, dim3((unsigned)ceil_div(words, 256)), dim3(256), 0, s, xbuf, words);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(lstm_pair_kernel, dim3((unsigned)(ceil_div(nseq, 8) * 16)), dim3(kLstmThreads), kLpLds, s, gx,
+                       gx_ld, gx_row, start, len, nseq, whh_t, bhh, out, out_ld, xbuf, abort, wait_ticks, silent_half);
+    return hipGetLastError();
+}
+
+hipError_t launch_clear_u64(uint64_t* x, int64_t n, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(lstm_exchange_clear_kernel, dim3((unsigned)ceil_div(n, 256)), dim3(256), 0, s, x, n);
     return hipGetLastError();
 }
 

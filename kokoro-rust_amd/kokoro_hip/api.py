@@ -14,6 +14,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(os.path.dirname(HERE), "lib", "libkokoro_hip.so")
 
 KK_OK = 0
+KK_ERR_INVALID, KK_ERR_HIP, KK_ERR_OOM, KK_ERR_STATE = -1, -2, -3, -4
 KK_NOISE_COUNTER = 0
 KK_NOISE_FIXED = 1
 STAGES = {"prosody": 0, "decoder": 1, "source": 2, "gen0": 3, "gen1": 4, "post": 5, "all": 6}

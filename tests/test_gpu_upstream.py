@@ -239,6 +239,68 @@ def test_forward_batch_equals_plan(full_ctx, full_run):
         assert np.array_equal(d, d2) and np.array_equal(a, a2)
 
 
+def test_lstm_pair_wait_ends_in_an_error(full_ctx, full_run):
+    """The two-CU recurrence's bounded wait, forced from the host: with KOKORO_HIP_TEST_LSTM_SILENT=1
+    the second half of every pair publishes nothing and the wait limit is 10 us, so every pair's
+    first half gives up, the launch ends, and the call fails with KK_ERR_HIP and a message; the next
+    call runs normally and gives the same audio as before."""
+    from kokoro_hip import api
+    items, audio, durs, _ = full_run
+    os.environ["KOKORO_HIP_TEST_LSTM_SILENT"] = "1"
+    try:
+        with pytest.raises(api.KKError) as e:
+            full_ctx.forward_batch(items)
+    finally:
+        del os.environ["KOKORO_HIP_TEST_LSTM_SILENT"]
+    assert e.value.code == api.KK_ERR_HIP and "partner" in str(e.value)
+    res = full_ctx.forward_batch(items)
+    for (a, d), a2, d2 in zip(res, audio, durs):
+        assert np.array_equal(d, d2) and np.array_equal(a, a2)
+
+
+_SINGLE_LSTM_SCRIPT = """
+import sys, numpy as np
+sys.path.insert(0, sys.argv[1])
+from kokoro_hip import api, model_spec, workloads
+w = model_spec.random_model_weights(seed=0)
+items = workloads.small_ids_items(41, [30, 75, 12])
+ctx = api.Context(0)
+ctx.upload_model(w)
+out = {}
+with api.Plan.full(ctx, items) as plan:
+    plan.run()
+    for b, it in enumerate(items):
+        T, N = len(it.ids), int(plan.durations[b].sum())
+        out[f"dur{b}"] = plan.durations[b]
+        for name, shape in (("d", (640, T)), ("logits", (50, T)), ("t_en", (512, T)), ("shared", (512, N))):
+            out[f"{name}{b}"] = plan.tap(name, b, shape)
+ctx.close()
+np.savez(sys.argv[2], **out)
+"""
+
+
+def test_lstm_pair_matches_one_cu_kernel(full_run, tmp_path):
+    """The two-CU recurrence against the one-CU kernel (KOKORO_HIP_LSTM_SINGLE=1, in a child
+    process: the switch is read once per process) on the same batch: the same arithmetic in another
+    summation order, so every recurrence's output agrees to >= 90 dB (f32 rounding), and the
+    durations are equal."""
+    import subprocess
+    import sys
+    items, _, durs, taps = full_run
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    f = tmp_path / "single.npz"
+    env = dict(os.environ, KOKORO_HIP_LSTM_SINGLE="1")
+    subprocess.run([sys.executable, "-c", _SINGLE_LSTM_SCRIPT, os.path.join(root, "kokoro-rust_amd"), str(f)],
+                   env=env, check=True, timeout=240)
+    one = np.load(f)
+    for b in range(len(items)):
+        assert np.array_equal(one[f"dur{b}"], durs[b])
+        for name in ("d", "logits", "t_en", "shared"):
+            s = snr_db(one[f"{name}{b}"], taps[b][name])
+            _print(f"  item {b} {name}: pair vs one-CU kernel {s:.1f} dB")
+            assert s >= 90.0, (b, name)
+
+
 def test_item_independent_of_batch(full_ctx):
     from kokoro_hip import workloads
     items = workloads.small_ids_items(43, [40, 9, 120, 3])
