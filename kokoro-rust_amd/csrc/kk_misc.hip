@@ -682,14 +682,37 @@ __global__ __launch_bounds__(256) void source_stft_kernel(SourceParams p) {
 }
 
 // ------------------------------------------------------------------ iSTFT (kernels/kokoro.cu:264-280, 492-508)
+// One block per kIstftSamples output samples of one item.  The block's frames' spectra
+// (m cos(sin p), m sin(sin p), computed in f32) are staged in LDS, widened to f64 once, and each
+// output sample sums the inverse DFTs of its (up to four) frames at its own tap, in the reference's
+// order -- no per-frame buffer, so a CU keeps more blocks (and their loads) in flight.  The f64
+// arithmetic is the reference's, rounding for rounding, with three exact rewrites: the tables hold
+// 2 cos / 2 sin (scaling by 2 is exact, so RN(re 2c - im 2s) = 2 RN(re c - im s)), the (-1)^n
+// term is a sign flip, and v / 20 is q = RN(v r), q + RN((v - 20 q) r) with r = RN(1 / 20) -- the
+// correctly rounded quotient (v / 5 of a double is never a binary tie, and the one FMA correction
+// brings q within half an ulp; checked against IEEE division on 4e8 values over 200 binades).
+// FP contraction is off: every other product and sum rounds as written.
 constexpr int kIstftFrames = kIstftSamples / 5 + 5;
+struct IdftLds {
+    double cs2[20][10], sn2[20][10];  // row n: 2 cos / 2 sin(2 pi k n / 20), k = 1..9, one pad
+    float win[20];
+};
+__device__ __forceinline__ double div20(double v) {
+    constexpr double r = 1.0 / 20.0;
+    const double q = v * r;
+    return __builtin_fma(__builtin_fma(-q, 20.0, v), r, q);
+}
 __global__ __launch_bounds__(256) void istft_kernel(IstftParams p) {
 #pragma clang fp contract(off)
-    __shared__ double re[kIstftFrames][11];
-    __shared__ double im[kIstftFrames][11];
-    __shared__ double fr[kIstftFrames][20];
-    __shared__ DftLds dft;
-    stage_dft(dft);
+    __shared__ __align__(16) double re[kIstftFrames][12];
+    __shared__ __align__(16) double im[kIstftFrames][12];
+    __shared__ __align__(16) IdftLds dft;
+    for (int i = threadIdx.x; i < 200; i += blockDim.x) {
+        const int n = i / 10, k = i - n * 10 + 1;
+        (&dft.cs2[0][0])[i] = k < 10 ? 2.0 * c_cos[k][n] : 0.0;
+        (&dft.sn2[0][0])[i] = k < 10 ? 2.0 * c_sin[k][n] : 0.0;
+    }
+    if (threadIdx.x < 20) dft.win[threadIdx.x] = c_win[threadIdx.x];
     const int64_t blk = blockIdx.x;
     const int b = (int)p.blk_item[blk];
     const int64_t s0 = p.blk_s0[blk];
@@ -719,21 +742,16 @@ __global__ __launch_bounds__(256) void istft_kernel(IstftParams p) {
             const int q = i / 11, k = i - q * 11;
             const float m = expf(lm[j]);
             const float ph = sinf(lp[j]);
-            re[q][k] = (double)(m * cosf(ph));
-            im[q][k] = (double)(m * sinf(ph));
+            float sn, cs;
+            sincosf(ph, &sn, &cs);
+            re[q][k] = (double)(m * cs);
+            im[q][k] = (double)(m * sn);
         }
     }
     __syncthreads();
-    for (int i = threadIdx.x; i < nfr * 20; i += blockDim.x) {
-        const int q = i / 20, n = i - q * 20;
-        double v = re[q][0] + re[q][10] * ((n % 2 == 0) ? 1.0 : -1.0);
-        for (int k = 1; k < 10; k++) v += 2.0 * (re[q][k] * dft.cs[k][n] - im[q][k] * dft.sn[k][n]);
-        v = v / 20.0;
-        fr[q][n] = v * (double)dft.win[n];
-    }
-    __syncthreads();
     // overlap-add in block-local coordinates: jr = j - 5 f_first lies in [10, 531) (f_first is the
-    // first frame touching j = s0 + 10), so frame indices and taps are small 32-bit numbers
+    // first frame touching j = s0 + 10), so frame indices and taps are small 32-bit numbers.  Frame
+    // f's sample at tap n: (re0 + (-1)^n re10 + sum_k 2 (re_k cos - im_k sin)) / 20 x window[n].
     float* out = p.audio + p.audio_start[b];
     const int jr0 = (int)(s0 + 10 - 5 * f_first);
     const int fmax = (int)(nframes - 1 - f_first);
@@ -744,8 +762,23 @@ __global__ __launch_bounds__(256) void istft_kernel(IstftParams p) {
         double acc = 0.0, env = 0.0;
         for (int f = f_lo; f <= f_hi; f++) {
             const int n = jr - 5 * f;
-            acc += fr[f][n];
+            double rv[12], iv[12], cv[10], sv[10];
+#pragma unroll
+            for (int e = 0; e < 6; e++) {
+                const double2 r2 = *(const double2*)&re[f][2 * e], i2 = *(const double2*)&im[f][2 * e];
+                rv[2 * e] = r2.x, rv[2 * e + 1] = r2.y, iv[2 * e] = i2.x, iv[2 * e + 1] = i2.y;
+            }
+#pragma unroll
+            for (int e = 0; e < 5; e++) {
+                const double2 c2 = *(const double2*)&dft.cs2[n][2 * e], s2 = *(const double2*)&dft.sn2[n][2 * e];
+                cv[2 * e] = c2.x, cv[2 * e + 1] = c2.y, sv[2 * e] = s2.x, sv[2 * e + 1] = s2.y;
+            }
+            double v = rv[0] + ((n & 1) ? -rv[10] : rv[10]);
+#pragma unroll
+            for (int k = 1; k < 10; k++) v += rv[k] * cv[k - 1] - iv[k] * sv[k - 1];
+            v = div20(v);
             const double w = (double)dft.win[n];
+            acc += v * w;
             env += w * w;
         }
         out[s0 + ii] = (float)(acc / env);
