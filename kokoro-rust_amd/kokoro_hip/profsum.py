@@ -62,19 +62,36 @@ def _short(name):
     return m.group(1) if m else name[:48]
 
 
-def stats(trace_dir, steps):
-    """Per-kernel table of the whole trace, and the Snake-block convs of bench.py's profiling pass (its
-    last `steps` steps, where every kernel runs alone on the stream): average duration per launch."""
-    rows = _rows(os.path.join(trace_dir, "run_kernel_trace.csv"))
-    rows.sort(key=lambda r: int(r["Start_Timestamp"]))
-    dur = lambda r: (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+def _table(rows, dur, per_step=0):
     per = {}
     for r in rows:
         per.setdefault(_short(r["Kernel_Name"]), []).append(dur(r))
     total = sum(sum(v) for v in per.values())
-    lines = ["| kernel | calls | total ms | avg us | % |", "|---|---:|---:|---:|---:|"]
+    head = "| kernel | calls | total ms | avg us | % |" + (" ms per step |" if per_step else "")
+    lines = [head, "|---|---:|---:|---:|---:|" + ("---:|" if per_step else "")]
     for k, v in sorted(per.items(), key=lambda kv: -sum(kv[1])):
-        lines.append(f"| `{k}` | {len(v)} | {sum(v) / 1e3:.2f} | {sum(v) / len(v):.1f} | {100 * sum(v) / total:.2f} |")
+        line = f"| `{k}` | {len(v)} | {sum(v) / 1e3:.2f} | {sum(v) / len(v):.1f} | {100 * sum(v) / total:.2f} |"
+        lines.append(line + (f" {sum(v) / 1e3 / per_step:.3f} |" if per_step else ""))
+    return lines, total
+
+
+def stats(trace_dir, steps):
+    """Per-kernel table of the whole trace; the same table over bench.py's profiling pass alone (its
+    last `steps` runs, every kernel alone on one stream: no span includes another stream's work);
+    and the Snake-block convs' average duration per launch in that pass."""
+    rows = _rows(os.path.join(trace_dir, "run_kernel_trace.csv"))
+    rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+    dur = lambda r: (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+    lines, _ = _table(rows, dur)
+    # the profiling pass: every dispatch after the end of the run before its first (each run ends
+    # with the iSTFT)
+    ist = [r for r in rows if "istft_kernel" in r["Kernel_Name"]]
+    if len(ist) > steps:
+        t0 = int(ist[-steps - 1]["End_Timestamp"])
+        ser = [r for r in rows if int(r["Start_Timestamp"]) > t0]
+        st, tot = _table(ser, dur, steps)
+        lines += ["", f"The profiling pass alone ({len(ser)} dispatches of the last {steps} runs, each kernel alone on "
+                      f"one stream; {tot / 1e3 / steps:.3f} ms of kernels per run):", ""] + st
     layers, frames = snake_layers()
     sn = [r for r in rows if SNAKE.search(r["Kernel_Name"])]
     last = sn[-steps * len(layers):]
