@@ -1026,11 +1026,30 @@ static void check_noise(const NoiseIn& nz, int64_t n_frames, int b) {
     }
 }
 
+// KOKORO_HIP_TIMING=1: host-side times between the marks of one call on stderr (diagnostics).
+struct PhaseMarks {
+    bool on = env_i64("KOKORO_HIP_TIMING", 0) != 0;
+    std::chrono::steady_clock::time_point t = std::chrono::steady_clock::now();
+    std::string line;
+    void mark(const char* what) {
+        if (!on) return;
+        const auto now = std::chrono::steady_clock::now();
+        char buf[96];
+        std::snprintf(buf, sizeof buf, " %s %.3f ms,", what, std::chrono::duration<double, std::milli>(now - t).count());
+        line += buf;
+        t = now;
+    }
+    void print(const char* who) {
+        if (on) std::fprintf(stderr, "%s:%s\n", who, line.c_str());
+    }
+};
+
 // Fills plan p (new, or the one-shot plan whose device buffers are reused) for a decoder batch.
 static void init_decoder_plan(kk_plan* p, const kk_decoder_item* items, int n) {
     kk_ctx* ctx = p->ctx;
     check(ctx->model.ready, "no model uploaded");
     check(items != nullptr && n > 0, "empty batch");
+    PhaseMarks pm;
     reset_plan(p, PLAN_DECODER, n);
     std::vector<int64_t> tstart(n);
     std::vector<const int64_t*> durs(n);
@@ -1053,9 +1072,11 @@ static void init_decoder_plan(kk_plan* p, const kk_decoder_item* items, int n) {
         rows += it.n_tok + kGapT;
         durs[b] = it.dur, ntok[b] = it.n_tok;
     }
+    pm.mark("checks");
     stage_begin(ctx);
     build_frame_layout(p);
     const int64_t ln = p->ln;
+    pm.mark("layout");
     // t_en in the token layout, time-major [rows][512] (the items hand it over channel-major)
     p->t_rows = rows;
     {
@@ -1068,6 +1089,7 @@ static void init_decoder_plan(kk_plan* p, const kk_decoder_item* items, int n) {
             std::memset(dst + (size_t)nt * 512, 0, sizeof(float) * 512 * kGapT);
         }
     }
+    pm.mark("t_en");
     // frame -> token row table (src/gpu_batch.rs:265-276), through kk_layout_src_row
     {
         int32_t* sr = stage<int32_t>(ctx, p->src_row, (size_t)ln);
@@ -1085,7 +1107,9 @@ static void init_decoder_plan(kk_plan* p, const kk_decoder_item* items, int n) {
         f0s[b] = items[b].f0, refs[b] = items[b].ref_s;
         nz[b] = NoiseIn{items[b].noise_kind, items[b].seed, items[b].rand_ini, items[b].sine, items[b].sine_len};
     }
+    pm.mark("src_row, energy");
     setup_generator(p, f0s, refs, nz);
+    pm.mark("generator setup");
     alloc_buf(p, p->xcat, (size_t)ln * kXcatLd * sizeof(float));
     alloc_buf(p, p->xin_a, (size_t)ln * kXinLd * sizeof(float));
     alloc_buf(p, p->xin_b, (size_t)ln * kXinLd * sizeof(float));
@@ -1093,7 +1117,10 @@ static void init_decoder_plan(kk_plan* p, const kk_decoder_item* items, int n) {
     alloc_buf(p, p->pool, (size_t)2 * ln * kXinLd * sizeof(uint16_t));
     alloc_buf(p, p->sc_half, (size_t)ln * 512 * sizeof(float));
     alloc_buf(p, p->dec_out, (size_t)2 * ln * 512 * sizeof(float));
+    pm.mark("buffers");
     finish_plan(p);
+    pm.mark("tiles, dry run, upload");
+    pm.print("init_decoder_plan");
 }
 
 // A user plan is complete (its inputs on the device) when kk_plan_create returns.
@@ -1928,23 +1955,6 @@ static void check_lstm_abort(kk_plan* p) {
                           "(set KOKORO_HIP_LSTM_SINGLE=1 for the one-CU kernel)");
 }
 
-// KOKORO_HIP_TIMING=1: host-side times between the marks of one call on stderr (diagnostics).
-struct PhaseMarks {
-    bool on = env_i64("KOKORO_HIP_TIMING", 0) != 0;
-    std::chrono::steady_clock::time_point t = std::chrono::steady_clock::now();
-    std::string line;
-    void mark(const char* what) {
-        if (!on) return;
-        const auto now = std::chrono::steady_clock::now();
-        char buf[96];
-        std::snprintf(buf, sizeof buf, " %s %.3f ms,", what, std::chrono::duration<double, std::milli>(now - t).count());
-        line += buf;
-        t = now;
-    }
-    void print(const char* who) {
-        if (on) std::fprintf(stderr, "%s:%s\n", who, line.c_str());
-    }
-};
 
 static void init_full_plan(kk_plan* p, const kk_item* items, int n) {
     kk_ctx* ctx = p->ctx;
