@@ -115,9 +115,10 @@ typedef struct {
 } kk_decoder_item;
 
 /* Output (src/model.rs:101-104): the item's audio, 600 N samples at 24 kHz, owned by the caller
- * until released by kk_output_free.  The audio of one call lands with a single DMA copy in a block
- * of pinned host memory that the library keeps for reuse; each item's pointer lies in that block,
- * which is free again once kk_output_free has released all of its items. */
+ * until released by kk_output_free.  The audio of one call lands in a block of pinned host memory
+ * that the library keeps for reuse (the one-shot entries copy each group of items there as soon as
+ * it is done); each item's pointer lies in that block, which is free again once kk_output_free has
+ * released all of its items. */
 typedef struct {
     float* audio;
     int64_t n_samples;

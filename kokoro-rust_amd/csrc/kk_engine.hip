@@ -686,6 +686,7 @@ struct Dom {
 // Item-aligned GEMM-column tiles of a domain (see TilesDev in kk_kernels.h).
 struct Tiles {
     DevBuf item, t0, n, lo, hi;
+    std::vector<int32_t> lo_h, hi_h;  // per item: its tiles are [lo_h, hi_h)
     int64_t count = 0;
     int64_t max_tiles = 0;  // the most tiles of any item
     int width = 0;
@@ -714,6 +715,7 @@ struct Tiles {
         count = (int64_t)it.size(), width = w;
         stage_vec(ctx, item, it), stage_vec(ctx, t0, t), stage_vec(ctx, n, nn);
         stage_vec(ctx, lo, lo_), stage_vec(ctx, hi, hi_);
+        lo_h = std::move(lo_), hi_h = std::move(hi_);
     }
 };
 
@@ -797,6 +799,8 @@ struct kk_plan {
             if (e) (void)hipEventDestroy(e), e = nullptr;
         for (auto& e : noise_ev)
             if (e) (void)hipEventDestroy(e), e = nullptr;
+        for (auto& e : out_ev)
+            if (e) (void)hipEventDestroy(e), e = nullptr;
         for (auto& e : te_ev)
             if (e) (void)hipEventDestroy(e), e = nullptr;
         if (logits_host) (void)hipHostFree(logits_host);
@@ -807,6 +811,14 @@ struct kk_plan {
     // fork / join of the resblock chains, and of the noise branches (created with the plan)
     hipEvent_t chain_ev[3] = {nullptr, nullptr, nullptr};
     hipEvent_t noise_ev[3] = {nullptr, nullptr, nullptr};
+    // the one-shot entries' audio: the run copies each item group's samples into early_out (a
+    // pinned block) on side stream 0 as soon as the group's iSTFT is done; out_ev[g] after the
+    // group's iSTFT, out_ev[kOutGroups] after the last copy
+    static constexpr int kOutGroups = 4;
+    hipEvent_t out_ev[kOutGroups + 1] = {nullptr, nullptr, nullptr, nullptr, nullptr};
+    float* early_out = nullptr;
+    bool early_issued = false;
+    std::vector<int64_t> ist_first;  // per item: its first iSTFT block (and the total at nb)
     std::vector<kk::DevBuf*> owned() {
         return {&tables, &t_en, &src_row, &f0, &en, &style, &seeds, &kinds, &rand_ini, &fixed_noise, &gb, &xcat,
                 &xin_a, &xin_b, &hdec, &pool, &sc_half, &dec_out, &pp, &spec, &B[0], &B[1], &B[2], &B[3], &B[4], &B[5],
@@ -957,11 +969,14 @@ static void setup_generator(kk_plan* p, const std::vector<const float*>& f0s, co
     }
     // work lists of the one-launch source+STFT and iSTFT kernels
     std::vector<int64_t> si, sf, ii, is;
+    p->ist_first.assign(nb + 1, 0);
     for (int b = 0; b < nb; b++) {
         const int64_t frames = 120 * p->nfr[b] + 1, samples = 600 * p->nfr[b];
         for (int64_t f = 0; f < frames; f += kSourceFrames) si.push_back(b), sf.push_back(f);
+        p->ist_first[b] = (int64_t)ii.size();
         for (int64_t q = 0; q < samples; q += kIstftSamples) ii.push_back(b), is.push_back(q);
     }
+    p->ist_first[nb] = (int64_t)ii.size();
     p->n_src = (int64_t)si.size(), p->n_ist = (int64_t)ii.size();
     stage_vec(ctx, p->src_item, si), stage_vec(ctx, p->src_f0, sf);
     stage_vec(ctx, p->ist_item, ii), stage_vec(ctx, p->ist_s0, is);
@@ -1011,6 +1026,8 @@ static void finish_plan(kk_plan* p) {
     for (auto& e : p->chain_ev)
         if (!e) KK_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
     for (auto& e : p->noise_ev)
+        if (!e) KK_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+    for (auto& e : p->out_ev)
         if (!e) KK_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
     p->dev_bytes = 0;
     for (DevBuf* b : p->owned()) p->dev_bytes += (int64_t)b->cap;
@@ -1307,6 +1324,7 @@ struct Runner {
 
     // One MFMA conv launch.
     struct Op {
+        int64_t t_lo = 0, t_hi = -1;  // a range of the output domain's tiles (t_hi < 0: all)
         int pro = PRO_F32, epi = EPI_STORE;
         const void* x = nullptr;
         int64_t x_ld = 0;
@@ -1340,6 +1358,10 @@ struct Runner {
             q.in_start = o.din->wstart_d.as<int64_t>(), q.in_len = o.din->wlen_d.as<int64_t>();
         }
         q.tiles = t.dev();
+        if (o.t_hi >= 0) {  // a range of the tiles (they are in item order): a group of items
+            q.tiles.item += o.t_lo, q.tiles.t0 += o.t_lo, q.tiles.n += o.t_lo;
+            q.tiles.count = o.t_hi - o.t_lo;
+        }
         q.coef = o.coef, q.alpha_rev = o.ar ? o.ar->as<float>() : nullptr;
         q.alpha_inv = o.ai ? o.ai->as<float>() : nullptr, q.slope = o.slope;
         q.w = c.w.as<uint16_t>(), q.bias = c.b.as<float>();
@@ -1354,12 +1376,14 @@ struct Runner {
         }
         // algorithmic FLOP over valid columns; ConvT (K = 2 stride): each input column feeds
         // K x cout outputs = 2 m MACs per input channel
-        const double valid = (double)(o.convt ? o.din->valid() : o.dout->valid());
+        // (a tile range counts its share of the domain)
+        const double share = o.t_hi >= 0 && t.count > 0 ? (double)(o.t_hi - o.t_lo) / (double)t.count : 1.0;
+        const double valid = share * (double)(o.convt ? o.din->valid() : o.dout->valid());
         const double f = 2.0 * (double)c.cin * valid * (o.convt ? 2.0 * c.m : (double)c.cout * c.k);
         flop += f;
         if (o.cls == PC_SNAKE) snake_flop += f;
         // algorithmic bytes: the input read once, the output written once, residual operands read
-        const double v_in = (double)o.din->valid(), v_out = (double)o.dout->valid();
+        const double v_in = share * (double)o.din->valid(), v_out = share * (double)o.dout->valid();
         const double es_in = (o.in_h || o.pro == PRO_BF16) ? 2 : 4, es_out = o.out_h ? 2 : 4;
         const int nres = o.convt ? 1
                          : o.epi == EPI_MEAN3 ? 3
@@ -1621,24 +1645,67 @@ struct Runner {
         resblock_mean(&m.rb[3 * i], B[3], X, hs, dout, &tu, kShapeWN[m.ups[i].shape] * ou.stride, i == 1);
     }
 
-    void post_istft() {
+    // conv_post over the items [b0, b1) (all: b1 < 0)
+    void post_istft(int b0 = 0, int b1 = -1) {
         const Dom& d = p->d120;
         Op o;
         o.pro = PRO_LEAKY, o.slope = 0.01f, o.x = p->B[0].p, o.x_ld = 128, o.din = o.dout = &d;
         o.y = p->post.as<float>(), o.y_ld = kPostLd, o.cls = PC_POST;
         o.label = "conv_post";
+        if (b1 >= 0) {
+            const Tiles& t = p->tl(d, kShapeN[m.post.shape]);
+            o.t_lo = t.lo_h[b0], o.t_hi = t.hi_h[b1 - 1];
+        }
         conv(m.post, o);
     }
 
-    void istft() {
+    // the iSTFT of the items [b0, b1) (all: b1 < 0)
+    void istft(int b0 = 0, int b1 = -1) {
         IstftParams q{};
         q.post = p->post.as<float>(), q.post_ld = kPostLd;
         q.start120 = p->d120.start_d.as<int64_t>(), q.f_len = p->d120.len_d.as<int64_t>();
         q.blk_item = p->ist_item.as<int64_t>(), q.blk_s0 = p->ist_s0.as<int64_t>(), q.n_blocks = p->n_ist;
         q.audio = p->audio.as<float>(), q.audio_start = p->audio_start.as<int64_t>();
+        double share = 1.0;
+        if (b1 >= 0) {
+            const int64_t k0 = p->ist_first[b0], k1 = p->ist_first[b1];
+            q.blk_item += k0, q.blk_s0 += k0, q.n_blocks = k1 - k0;
+            share = p->n_ist > 0 ? (double)(k1 - k0) / (double)p->n_ist : 0.0;
+        }
         // 22 f32 read per frame, one f32 written per sample (21.6 B per sample)
-        launch(PC_ISTFT, 0, (double)p->d120.valid() * 88 + (double)frames() * 600 * 4,
+        launch(PC_ISTFT, 0, share * ((double)p->d120.valid() * 88 + (double)frames() * 600 * 4),
                [&] { return launch_istft(q, s); });
+    }
+
+    // conv_post and the iSTFT in up to kOutGroups groups of items (about equal frames each); after
+    // each group's iSTFT its samples go to p->early_out on side stream 0, while the next groups
+    // compute.  out_ev[kOutGroups] is recorded after the last copy.
+    void post_istft_copy() {
+        const int nb = p->nb, ng = std::min(nb, (int)kk_plan::kOutGroups);
+        int64_t total = 0;
+        for (int b = 0; b < nb; b++) total += p->nfr[b];
+        int b0 = 0;
+        int64_t acc = 0;
+        for (int g = 0; g < ng; g++) {
+            // the group ends where the running frame count passes (g + 1) / ng of the total,
+            // leaving at least one item to each later group
+            int b1 = b0 + 1;
+            acc += p->nfr[b0];
+            while (b1 < nb - (ng - 1 - g) && acc + p->nfr[b1] <= total * (g + 1) / ng) acc += p->nfr[b1++];
+            if (g == ng - 1) {
+                while (b1 < nb) acc += p->nfr[b1++];
+            }
+            post_istft(b0, b1);
+            istft(b0, b1);
+            KK_HIP(hipEventRecord(p->out_ev[g], s));
+            KK_HIP(hipStreamWaitEvent(ctx->side[0], p->out_ev[g], 0));
+            const int64_t a0 = 600 * p->a[b0], a1 = 600 * (p->a[b1 - 1] + p->nfr[b1 - 1]);
+            KK_HIP(hipMemcpyAsync(p->early_out + a0, p->audio.as<float>() + a0, sizeof(float) * (a1 - a0),
+                                  hipMemcpyDeviceToHost, ctx->side[0]));
+            b0 = b1;
+        }
+        KK_HIP(hipEventRecord(p->out_ev[kk_plan::kOutGroups], ctx->side[0]));
+        p->early_issued = true;
     }
 
     // ------------------------------------------------------------ the stages before the decoder
@@ -1929,6 +1996,10 @@ struct Runner {
             noise_branch(1);
         gen_stage(1);
         if (until <= KK_STAGE_GEN1) return;
+        if (p->early_out && until >= KK_STAGE_ALL && !dry && !ctx->profiling && p->nb > 1) {
+            post_istft_copy();
+            return;
+        }
         post_istft();
         if (until <= KK_STAGE_POST) return;
         istft();
@@ -2662,7 +2733,9 @@ int kk_plan_sync(kk_plan* plan, char* err, size_t errlen) {
 
 // Each item's result into `out` (see kk_plan_fetch).  Audio: one copy of the whole packed sample
 // layout into a pinned block of the output pool; the items point into it.
-static void fetch_plan(kk_plan* plan, kk_output* out) {
+// blk: a pinned block already taken for the plan's samples with out[] pointing into it (the
+// one-shot entries: the run may have issued the copies itself, early_issued), or null.
+static void fetch_plan(kk_plan* plan, kk_output* out, float* blk = nullptr) {
     use_device(plan->ctx);
     check(plan->last_until >= KK_STAGE_ALL || plan->kind == PLAN_SNAKE, "plan has not run to the end");
     hipStream_t s = plan->ctx->stream;
@@ -2678,13 +2751,30 @@ static void fetch_plan(kk_plan* plan, kk_output* out) {
         return;
     }
     const size_t bytes = sizeof(float) * 600 * (size_t)plan->ln;
-    float* blk = (float*)out_block_take(bytes, plan->nb);
-    for (int b = 0; b < plan->nb; b++) out[b] = kk_output{blk + 600 * plan->a[b], 600 * plan->nfr[b]};
-    KK_HIP(hipMemcpyAsync(blk, plan->audio.p, bytes, hipMemcpyDeviceToHost, s));
+    if (!blk) {
+        blk = (float*)out_block_take(bytes, plan->nb);
+        for (int b = 0; b < plan->nb; b++) out[b] = kk_output{blk + 600 * plan->a[b], 600 * plan->nfr[b]};
+    }
+    if (!plan->early_issued) KK_HIP(hipMemcpyAsync(blk, plan->audio.p, bytes, hipMemcpyDeviceToHost, s));
     if (plan->kind == PLAN_FULL)
         KK_HIP(hipMemcpyAsync(plan->abort_host, plan->u_lstmx.p, sizeof(uint64_t), hipMemcpyDeviceToHost, s));
     KK_HIP(hipStreamSynchronize(s));
+    if (plan->early_issued) {
+        KK_HIP(hipEventSynchronize(plan->out_ev[kk_plan::kOutGroups]));
+        plan->early_issued = false;
+    }
     if (plan->kind == PLAN_FULL) check_lstm_abort(plan);
+}
+
+// The one-shot entries take the output block before the run, so that the run can copy each group
+// of items' samples into it as soon as they are done (out[] points into it from here on: a failure
+// releases it through kk_output_free after the streams are drained).
+static float* take_early_block(kk_plan* p, kk_output* out) {
+    float* blk = (float*)out_block_take(sizeof(float) * 600 * (size_t)p->ln, p->nb);
+    for (int b = 0; b < p->nb; b++) out[b] = kk_output{blk + 600 * p->a[b], 600 * p->nfr[b]};
+    p->early_out = blk;
+    p->early_issued = false;
+    return blk;
 }
 
 int kk_plan_fetch(kk_plan* plan, kk_output* out, char* err, size_t errlen) {
@@ -2972,12 +3062,14 @@ int kk_forward_decoder_batch(kk_ctx* ctx, const kk_decoder_item* items, int n, k
             static const bool timing = env_i64("KOKORO_HIP_TIMING", 0) != 0;
             const auto t0 = std::chrono::steady_clock::now();
             init_decoder_plan(ctx->oneshot, items, n);
+            float* blk = take_early_block(ctx->oneshot, out);
             const auto t1 = std::chrono::steady_clock::now();
             run_plan(ctx->oneshot, KK_STAGE_ALL);
             const auto t2 = std::chrono::steady_clock::now();
             if (timing) KK_HIP(hipStreamSynchronize(ctx->stream));
             const auto t3 = std::chrono::steady_clock::now();
-            fetch_plan(ctx->oneshot, out);
+            fetch_plan(ctx->oneshot, out, blk);
+            ctx->oneshot->early_out = nullptr;
             const auto t4 = std::chrono::steady_clock::now();
             if (timing) {
                 auto ms = [](auto a, auto b) { return std::chrono::duration<double, std::milli>(b - a).count(); };
@@ -3010,11 +3102,13 @@ int kk_forward_batch(kk_ctx* ctx, const kk_item* items, int n, kk_result* out, c
             static const bool timing = env_i64("KOKORO_HIP_TIMING", 0) != 0;
             const auto t0 = std::chrono::steady_clock::now();
             init_full_plan(ctx->oneshot, items, n);  // the token phase runs here
+            float* blk = take_early_block(ctx->oneshot, audio.data());
             const auto t1 = std::chrono::steady_clock::now();
             run_plan(ctx->oneshot, KK_STAGE_ALL, true);
             if (timing) KK_HIP(hipStreamSynchronize(ctx->stream));
             const auto t2 = std::chrono::steady_clock::now();
-            fetch_plan(ctx->oneshot, audio.data());
+            fetch_plan(ctx->oneshot, audio.data(), blk);
+            ctx->oneshot->early_out = nullptr;
             for (int b = 0; b < n; b++) {
                 const auto& d = ctx->oneshot->pred[b];
                 out[b].pred_dur = (int64_t*)std::malloc(sizeof(int64_t) * d.size());
