@@ -257,6 +257,7 @@ struct kk_ctx {
     std::vector<kk::ProfRec> prof;
     std::vector<hipEvent_t> event_pool;
     kk::Staging stage;
+    kk::Staging stage_late;  // the one-shot decoder entry's t_en, staged while its first kernels run
     // kk_forward_decoder_batch's plan, kept between calls: its device buffers are reused whenever
     // the next batch fits (released on any failure, so that a split batch can use the memory)
     kk_plan* oneshot = nullptr;
@@ -818,6 +819,11 @@ struct kk_plan {
     hipEvent_t out_ev[kOutGroups + 1] = {nullptr, nullptr, nullptr, nullptr, nullptr};
     float* early_out = nullptr;
     bool early_issued = false;
+    // the one-shot decoder entry stages t_en during its run, after the harmonic source and the noise
+    // branch are launched (late_items: the call's items until then; tables_late: its upload)
+    const kk_decoder_item* late_items = nullptr;
+    std::vector<int64_t> late_tstart;
+    kk::DevBuf tables_late;
     std::vector<int64_t> ist_first;  // per item: its first iSTFT block (and the total at nb)
     std::vector<kk::DevBuf*> owned() {
         return {&tables, &t_en, &src_row, &f0, &en, &style, &seeds, &kinds, &rand_ini, &fixed_noise, &gb, &xcat,
@@ -827,7 +833,7 @@ struct kk_plan {
                 &ist_item, &ist_s0, &pcm, &pcm_len, &pcm_clip, &tables_tok, &ids, &row_item, &att_item,
                 &att_head, &att_q0, &style_pro, &gbp, &u_emb, &u_h, &u_qkv, &u_ctx, &u_ffn, &u_x, &u_gx, &u_xl,
                 &u_logits, &u_te, &u_te2, &u_gxt, &u_gxs, &u_sh, &u_fx[0], &u_fx[1], &u_fpool[0], &u_fpool[1],
-                &u_fh[0], &u_fh[1], &u_fsc[0], &u_fsc[1], &u_fy[0], &u_fy[1], &u_lstmx};
+                &u_fh[0], &u_fh[1], &u_fsc[0], &u_fsc[1], &u_fy[0], &u_fy[1], &u_lstmx, &tables_late};
     }
 };
 
@@ -1062,7 +1068,20 @@ struct PhaseMarks {
 };
 
 // Fills plan p (new, or the one-shot plan whose device buffers are reused) for a decoder batch.
-static void init_decoder_plan(kk_plan* p, const kk_decoder_item* items, int n) {
+// t_en in the token layout, time-major [rows][512] (the items hand it over channel-major).
+static void stage_t_en(kk_ctx* ctx, kk_plan* p, const kk_decoder_item* items, const std::vector<int64_t>& tstart) {
+    float* te = stage<float>(ctx, p->t_en, (size_t)512 * p->t_rows);
+    for (int b = 0; b < p->nb; b++) {
+        const int nt = items[b].n_tok;
+        float* dst = te + (size_t)tstart[b] * 512;
+        for (int i = 0; i < nt; i++)
+            for (int c = 0; c < 512; c++) dst[(size_t)i * 512 + c] = items[b].t_en[(size_t)c * nt + i];
+        std::memset(dst + (size_t)nt * 512, 0, sizeof(float) * 512 * kGapT);
+    }
+}
+
+// late_ten: t_en is staged by the run itself (stage_late_ten), after its first launches.
+static void init_decoder_plan(kk_plan* p, const kk_decoder_item* items, int n, bool late_ten = false) {
     kk_ctx* ctx = p->ctx;
     check(ctx->model.ready, "no model uploaded");
     check(items != nullptr && n > 0, "empty batch");
@@ -1096,15 +1115,11 @@ static void init_decoder_plan(kk_plan* p, const kk_decoder_item* items, int n) {
     pm.mark("layout");
     // t_en in the token layout, time-major [rows][512] (the items hand it over channel-major)
     p->t_rows = rows;
-    {
-        float* te = stage<float>(ctx, p->t_en, (size_t)512 * rows);
-        for (int b = 0; b < n; b++) {
-            const int nt = items[b].n_tok;
-            float* dst = te + (size_t)tstart[b] * 512;
-            for (int i = 0; i < nt; i++)
-                for (int c = 0; c < 512; c++) dst[(size_t)i * 512 + c] = items[b].t_en[(size_t)c * nt + i];
-            std::memset(dst + (size_t)nt * 512, 0, sizeof(float) * 512 * kGapT);
-        }
+    p->late_items = nullptr;
+    if (late_ten) {
+        p->late_items = items, p->late_tstart = tstart;
+    } else {
+        stage_t_en(ctx, p, items, tstart);
     }
     pm.mark("t_en");
     // frame -> token row table (src/gpu_batch.rs:265-276), through kk_layout_src_row
@@ -1524,6 +1539,21 @@ struct Runner {
         o2.y = out, o2.y_ld = out_ld, o2.coef = cf(1), o2.slope = 0.2f, o2.scale = 1.0f / sqrtf(2.0f);
         o2.label = r.name + ".conv2";
         conv(r.conv2, o2);
+    }
+
+    // The one-shot decoder entry's t_en: staged in the context's second staging buffer and uploaded
+    // on the run's stream now, while the harmonic source and the noise branch (launched before,
+    // on a side stream) already run; the decoder's launches follow it on the same stream.
+    void stage_late_ten() {
+        std::swap(ctx->stage, ctx->stage_late);
+        struct Restore {
+            kk_ctx* ctx;
+            ~Restore() { std::swap(ctx->stage, ctx->stage_late); }
+        } restore{ctx};
+        stage_begin(ctx);
+        stage_t_en(ctx, p, p->late_items, p->late_tstart);
+        stage_flush(ctx, p->tables_late, s);
+        p->late_items = nullptr;
     }
 
     void decoder() {
@@ -1980,6 +2010,7 @@ struct Runner {
             }
             s = main_s;
         }
+        if (p->late_items && !dry) stage_late_ten();
         if (p->kind == PLAN_DECODER || p->kind == PLAN_FULL) decoder();
         if (until <= KK_STAGE_DECODER) return;
         if (!conc) source();
@@ -2505,6 +2536,7 @@ int kk_open(int ordinal, kk_ctx** out, char* err, size_t errlen) {
         for (auto& ss : ctx->side) KK_HIP(hipStreamCreateWithFlags(&ss, hipStreamNonBlocking));
         for (auto& e : ctx->join_ev) KK_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
         KK_HIP(hipEventCreateWithFlags(&ctx->stage.done, hipEventDisableTiming));
+        KK_HIP(hipEventCreateWithFlags(&ctx->stage_late.done, hipEventDisableTiming));
         // twiddles and periodic Hann window in f64 (src/gpu.rs:93-101)
         double cs[220], sn[220];
         float win[20];
@@ -2540,6 +2572,8 @@ void kk_close(kk_ctx* ctx) {
     drop_oneshot(ctx);
     if (ctx->stage.host) (void)hipHostFree(ctx->stage.host);
     if (ctx->stage.done) (void)hipEventDestroy(ctx->stage.done);
+    if (ctx->stage_late.host) (void)hipHostFree(ctx->stage_late.host);
+    if (ctx->stage_late.done) (void)hipEventDestroy(ctx->stage_late.done);
     for (auto e : ctx->join_ev)
         if (e) (void)hipEventDestroy(e);
     for (auto& r : ctx->prof) {
@@ -3061,7 +3095,7 @@ int kk_forward_decoder_batch(kk_ctx* ctx, const kk_decoder_item* items, int n, k
             // KOKORO_HIP_TIMING=1: host-side phase times of this call on stderr (diagnostics)
             static const bool timing = env_i64("KOKORO_HIP_TIMING", 0) != 0;
             const auto t0 = std::chrono::steady_clock::now();
-            init_decoder_plan(ctx->oneshot, items, n);
+            init_decoder_plan(ctx->oneshot, items, n, true);
             float* blk = take_early_block(ctx->oneshot, out);
             const auto t1 = std::chrono::steady_clock::now();
             run_plan(ctx->oneshot, KK_STAGE_ALL);
