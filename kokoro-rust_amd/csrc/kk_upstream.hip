@@ -69,7 +69,9 @@ __global__ void __launch_bounds__(256) text_embed_kernel(const int32_t* ids, con
 // (layer_norm_rows / adaln_rows_seg, kernels/kokoro.cu:44-82, 337-373): mean, then the mean of
 // squared deviations, inv = 1 / sqrt(var + eps); then either the affine g, b, or AdaLayerNorm's
 // (1 + gamma[c]) o + beta[c] with gamma, beta = gb[item][gb_off + c], gb[item][gb_off + D + c];
-// optionally leaky ReLU.  One wave per row, D / 256 float4 per lane.
+// optionally leaky ReLU.  One wave per row, D / 256 float4 per lane.  The row is loaded together
+// with its item index (a gap row is read and left alone), and the affine parameters as float4
+// before the reductions: one or two memory latencies per row instead of three.
 template <int D>
 __global__ void __launch_bounds__(256) layernorm_kernel(float* x, int64_t ld, int64_t rows, const int32_t* row_item,
                                                         const float* g, const float* b, const float* gb, int64_t gb_ld,
@@ -79,15 +81,23 @@ __global__ void __launch_bounds__(256) layernorm_kernel(float* x, int64_t ld, in
     const int lane = threadIdx.x & 63;
     if (r >= rows) return;
     const int it = row_item[r];
-    if (it < 0) return;
     float4* row = (float4*)(x + r * ld);
     float4 v[NV];
+#pragma unroll
+    for (int i = 0; i < NV; i++) v[i] = row[lane + 64 * i];
+    if (it < 0) return;
+    float4 ga[NV], be[NV];  // the affine scale and shift of this lane's channels
+    if (gb) {
+        const float4* gam = (const float4*)(gb + (int64_t)it * gb_ld + gb_off);
+#pragma unroll
+        for (int i = 0; i < NV; i++) ga[i] = gam[lane + 64 * i], be[i] = gam[D / 4 + lane + 64 * i];
+    } else {
+#pragma unroll
+        for (int i = 0; i < NV; i++) ga[i] = ((const float4*)g)[lane + 64 * i], be[i] = ((const float4*)b)[lane + 64 * i];
+    }
     float s = 0.f;
 #pragma unroll
-    for (int i = 0; i < NV; i++) {
-        v[i] = row[lane + 64 * i];
-        s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
-    }
+    for (int i = 0; i < NV; i++) s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
     const float mean = wave_sum(s) * (1.0f / D);
     float q = 0.f;
 #pragma unroll
@@ -96,22 +106,19 @@ __global__ void __launch_bounds__(256) layernorm_kernel(float* x, int64_t ld, in
         q += (a * a + bb * bb) + (c * c + d * d);
     }
     const float inv = 1.0f / sqrtf(wave_sum(q) * (1.0f / D) + eps);
-    const float* gam = gb ? gb + (int64_t)it * gb_ld + gb_off : nullptr;
 #pragma unroll
     for (int i = 0; i < NV; i++) {
-        const int c0 = 4 * (lane + 64 * i);
-        float o[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+        const float o[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+        const float gv[4] = {ga[i].x, ga[i].y, ga[i].z, ga[i].w}, bv[4] = {be[i].x, be[i].y, be[i].z, be[i].w};
+        float y4[4];
 #pragma unroll
         for (int e = 0; e < 4; e++) {
             float y = (o[e] - mean) * inv;
-            if (gam)
-                y = (1.0f + gam[c0 + e]) * y + gam[D + c0 + e];
-            else
-                y = y * g[c0 + e] + b[c0 + e];
+            y = gb ? (1.0f + gv[e]) * y + bv[e] : y * gv[e] + bv[e];
             if (leaky) y = y < 0.f ? y * slope : y;
-            o[e] = y;
+            y4[e] = y;
         }
-        row[lane + 64 * i] = make_float4(o[0], o[1], o[2], o[3]);
+        row[lane + 64 * i] = make_float4(y4[0], y4[1], y4[2], y4[3]);
     }
 }
 
@@ -522,6 +529,7 @@ hipError_t launch_layernorm(float* x, int64_t ld, int d, int64_t rows, const int
                             float slope, hipStream_t s) {
     if (rows <= 0) return hipSuccess;
     if (ld % 4 != 0 || (gb == nullptr && (g == nullptr || b == nullptr))) return hipErrorInvalidValue;
+    if (gb && (gb_ld % 4 != 0 || gb_off % 4 != 0)) return hipErrorInvalidValue;  // float4 parameter loads
     const dim3 grid((unsigned)ceil_div(rows, 4));
     if (d == 768)
         hipLaunchKernelGGL(layernorm_kernel<768>, grid, dim3(256), 0, s, x, ld, rows, row_item, g, b, gb, gb_ld, gb_off,
