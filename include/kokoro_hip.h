@@ -180,7 +180,8 @@ typedef struct {
  * that trade their halves of h each step; a block that waits more than 2 s for its partner ends
  * its launch and the call fails with KK_ERR_HIP (KOKORO_HIP_LSTM_SINGLE=1, read once per process,
  * selects the one-CU kernel instead; test hook KOKORO_HIP_TEST_LSTM_SILENT=1, read at each launch,
- * forces that failure with a 10 us wait). */
+ * forces that failure with a 10 us wait).  ALBERT's attention runs on the f32 matrix cores;
+ * KOKORO_HIP_ATTENTION_VALU=1 (read once per process) selects the f32 VALU kernel instead. */
 int kk_forward_batch(kk_ctx* ctx, const kk_item* items, int n, kk_result* out, char* err, size_t errlen);
 void kk_result_free(kk_result* out, int n);
 

@@ -1856,9 +1856,11 @@ struct Runner {
             linear(u.qkv, H, 768, dtf, QKV, 2304, nm + ".qkv");
             label = nm + ".attention";
             launch(PC_ATTN, att_flop, v * (2304 + 768) * 4, [&] {
+                // KOKORO_HIP_ATTENTION_VALU=1: the f32 VALU kernel instead of the f32 matrix cores
+                static const bool valu = env_i64("KOKORO_HIP_ATTENTION_VALU", 0) != 0;
                 return launch_attention(QKV, dt.start_d.as<int64_t>(), dt.len_d.as<int64_t>(),
                                         p->att_item.as<int32_t>(), p->att_head.as<int32_t>(), p->att_q0.as<int32_t>(),
-                                        p->n_att, CTX, s);
+                                        p->n_att, CTX, s, valu);
             });
             linear(u.dense, CTX, 768, dtf, H, 768, nm + ".dense", PRO_F32, EPI_RESID);
             layernorm(H, 768, 768, u.attn_g.as<float>(), u.attn_b.as<float>(), 0, 1e-12f, false, nm + ".attention_ln");

@@ -196,9 +196,10 @@ hipError_t launch_layernorm(float* x, int64_t ld, int d, int64_t rows, const int
                             const float* b, const float* gb, int64_t gb_ld, int gb_off, float eps, bool leaky,
                             float slope, hipStream_t s);
 // ALBERT attention, 12 heads of 64, scale 1/8: qkv [rows][2304] -> out [rows][768]; work list of
-// (item, head, first query) blocks of 64 queries.
+// (item, head, first query) blocks of 64 queries.  On the f32 matrix cores, or (valu) on the VALU.
 hipError_t launch_attention(const float* qkv, const int64_t* start, const int64_t* len, const int32_t* w_item,
-                            const int32_t* w_head, const int32_t* w_q0, int64_t n_blocks, float* out, hipStream_t s);
+                            const int32_t* w_head, const int32_t* w_q0, int64_t n_blocks, float* out, hipStream_t s,
+                            bool valu = false);
 // BiLSTM recurrence, H = 256, over the item spans [start, start + len): gx [*][gx_ld] gate
 // pre-activations (W_ih x + b_ih, forward at columns [0, 1024), reverse at [1024, 2048)) at row
 // gx_row[r] (or r when gx_row is null); whh_t [2][256][1024] (k-major), bhh [2][1024];

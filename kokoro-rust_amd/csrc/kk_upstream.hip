@@ -234,6 +234,128 @@ __global__ void __launch_bounds__(256) attention_kernel(const float* qkv, const 
     }
 }
 
+// The same attention on the f32 matrix cores (v_mfma_f32_32x32x2_f32: f32 products, f32 sums, in
+// another order than the VALU kernel above).  One block per (item, head, 64 queries), two waves of
+// 32 queries each, keys in chunks of 64 staged in LDS ([key][dim]).  Everything is transposed so
+// that a query stays in one lane pair: lane (l32, lh) owns query q0 + 32 w + l32, and
+//  - S^T (keys x queries) = K Q^T: A = K[key][d], B = Q[query][d] with d = 32 lh + s at step s (the
+//    lane's 32 dims of Q, pre-scaled by 1/8 -- exact, a power of two -- stay in registers), so the
+//    lane ends with its query's scores for keys 8 (r / 4) + 4 lh + r % 4 (r < 16) of each 32-key
+//    tile: the softmax's maximum and sum are lane-local plus one exchange with lane ^ 32;
+//  - O^T (dims x queries) += V^T P^T: B = the lane's own P values (step s = r above), A =
+//    V[key][dim] for the same keys, so P never leaves registers and the rescale by exp(m - m') is
+//    per lane.
+constexpr int kAmLd = 68;  // LDS row stride (floats) of the K and V chunks
+__global__ void __launch_bounds__(128) attention_mfma_kernel(const float* qkv, const int64_t* start, const int64_t* len,
+                                                             const int32_t* w_item, const int32_t* w_head,
+                                                             const int32_t* w_q0, float* out) {
+    typedef float f32x16 __attribute__((ext_vector_type(16)));
+    __shared__ __align__(16) float Ks[64][kAmLd];
+    __shared__ __align__(16) float Vs[64][kAmLd];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, lh = lane >> 5;
+    const int item = w_item[blockIdx.x], head = w_head[blockIdx.x], q0 = w_q0[blockIdx.x];
+    const int64_t s0 = start[item];
+    const int t = (int)len[item];
+    constexpr int64_t LD = 3 * 768;
+    const int q = q0 + 32 * wave + l32;  // this lane's query (rows past the item compute, unstored)
+    float qr[32];
+    {
+        const float* qp = qkv + (s0 + (q < t ? q : 0)) * LD + head * 64 + 32 * lh;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const float4 v = *(const float4*)(qp + 4 * j);
+            const bool ok = q < t;
+            qr[4 * j] = ok ? v.x * 0.125f : 0.f, qr[4 * j + 1] = ok ? v.y * 0.125f : 0.f;
+            qr[4 * j + 2] = ok ? v.z * 0.125f : 0.f, qr[4 * j + 3] = ok ? v.w * 0.125f : 0.f;
+        }
+    }
+    f32x16 o[2];
+#pragma unroll
+    for (int d = 0; d < 2; d++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) o[d][r] = 0.f;
+    float m = -INFINITY, l = 0.f;
+    for (int k0 = 0; k0 < t; k0 += 64) {
+        const int nk = min(64, t - k0);
+        __syncthreads();  // the previous chunk's K / V are consumed
+        for (int i = tid; i < 64 * 16; i += 128) {
+            const int k = i >> 4, d4 = (i & 15) * 4;
+            float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
+            if (k < nk) {
+                const float* r = qkv + (s0 + k0 + k) * LD + head * 64 + d4;
+                kv = *(const float4*)(r + 768), vv = *(const float4*)(r + 1536);
+            }
+            *(float4*)&Ks[k][d4] = kv;
+            *(float4*)&Vs[k][d4] = vv;
+        }
+        __syncthreads();
+        // S^T for the chunk's two 32-key tiles
+        f32x16 sc[2];
+#pragma unroll
+        for (int kt = 0; kt < 2; kt++) {
+#pragma unroll
+            for (int r = 0; r < 16; r++) sc[kt][r] = 0.f;
+            float kr[32];
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const float4 v = *(const float4*)&Ks[32 * kt + l32][32 * lh + 4 * j];
+                kr[4 * j] = v.x, kr[4 * j + 1] = v.y, kr[4 * j + 2] = v.z, kr[4 * j + 3] = v.w;
+            }
+#pragma unroll
+            for (int st = 0; st < 32; st++) sc[kt] = __builtin_amdgcn_mfma_f32_32x32x2f32(kr[st], qr[st], sc[kt], 0, 0, 0);
+        }
+        // mask the keys past the item; the running maximum and sum of this lane's query
+        float mx = -INFINITY;
+#pragma unroll
+        for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int key = 32 * kt + 8 * (r >> 2) + 4 * lh + (r & 3);
+                sc[kt][r] = key < nk ? sc[kt][r] : -INFINITY;
+                mx = fmaxf(mx, sc[kt][r]);
+            }
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float mn = fmaxf(m, mx);
+        const float corr = expf(m - mn);  // 0 on the first chunk
+        float sum = 0.f;
+#pragma unroll
+        for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                sc[kt][r] = expf(sc[kt][r] - mn);
+                sum += sc[kt][r];
+            }
+        sum += __shfl_xor(sum, 32);
+        l = l * corr + sum;
+        m = mn;
+#pragma unroll
+        for (int d = 0; d < 2; d++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) o[d][r] *= corr;
+        // O^T += V^T P^T: step st of tile kt pairs the keys 32 kt + 8 (st / 4) + 4 lh + st % 4
+#pragma unroll
+        for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+            for (int st = 0; st < 16; st++) {
+                const int key = 32 * kt + 8 * (st >> 2) + 4 * lh + (st & 3);
+#pragma unroll
+                for (int d = 0; d < 2; d++)
+                    o[d] = __builtin_amdgcn_mfma_f32_32x32x2f32(Vs[key][32 * d + l32], sc[kt][st], o[d], 0, 0, 0);
+            }
+    }
+    // lane (l32, lh) holds dims 32 d + 8 (r / 4) + 4 lh + r % 4 of query q: four float4 per tile
+    if (q < t) {
+        const float inv = 1.0f / l;
+        float* op = out + (s0 + q) * 768 + head * 64;
+#pragma unroll
+        for (int d = 0; d < 2; d++)
+#pragma unroll
+            for (int g = 0; g < 4; g++)
+                *(float4*)(op + 32 * d + 8 * g + 4 * lh) =
+                    make_float4(o[d][4 * g] * inv, o[d][4 * g + 1] * inv, o[d][4 * g + 2] * inv, o[d][4 * g + 3] * inv);
+    }
+}
+
 // BiLSTM recurrence (lstm_seq_batched semantics, kernels/kokoro.cu:400-455): one block per
 // (item, direction), 512 threads.  Per step: gate_r = gx[row][dir 4H + r] + (W_hh[r] . h + b_hh[r])
 // for the 4H = 1024 gate rows (gates i, f, g, o), then unit j: c_j = f c_j + i g, h_j = o tanh(c_j),
@@ -543,10 +665,15 @@ hipError_t launch_layernorm(float* x, int64_t ld, int d, int64_t rows, const int
 }
 
 hipError_t launch_attention(const float* qkv, const int64_t* start, const int64_t* len, const int32_t* w_item,
-                            const int32_t* w_head, const int32_t* w_q0, int64_t n_blocks, float* out, hipStream_t s) {
+                            const int32_t* w_head, const int32_t* w_q0, int64_t n_blocks, float* out, hipStream_t s,
+                            bool valu) {
     if (n_blocks <= 0) return hipSuccess;
-    hipLaunchKernelGGL(attention_kernel, dim3((unsigned)n_blocks), dim3(256), 0, s, qkv, start, len, w_item, w_head,
-                       w_q0, out, 0.125f);
+    if (valu)
+        hipLaunchKernelGGL(attention_kernel, dim3((unsigned)n_blocks), dim3(256), 0, s, qkv, start, len, w_item,
+                           w_head, w_q0, out, 0.125f);
+    else
+        hipLaunchKernelGGL(attention_mfma_kernel, dim3((unsigned)n_blocks), dim3(128), 0, s, qkv, start, len, w_item,
+                           w_head, w_q0, out);
     return hipGetLastError();
 }
 

@@ -282,10 +282,17 @@ np.savez(sys.argv[2], **out)
 def test_lstm_pair_matches_one_cu_kernel(full_run, tmp_path):
     """The two-CU recurrence against the one-CU kernel (KOKORO_HIP_LSTM_SINGLE=1, in a child
     process: the switch is read once per process) on the same batch: the same arithmetic in another
-    summation order, so every recurrence's output agrees to >= 90 dB (f32 rounding), and the
-    durations are equal."""
+    summation order.
+    - t_en: the text encoder's recurrence on identical inputs (its conv stack does not depend on the
+      switch), so the outputs differ by f32 rounding only: >= 120 dB;
+    - d, logits, shared: chains of recurrences joined by linear layers with bf16-rounded operands,
+      where an f32-level difference can move an operand across a bf16 rounding boundary (one ulp,
+      2^-8 relative): >= 60 dB;
+    - the durations equal, except tokens whose sigmoid sum lies within 0.05 of a rounding tie."""
     import subprocess
     import sys
+
+    import torch
     items, _, durs, taps = full_run
     root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
     f = tmp_path / "single.npz"
@@ -293,12 +300,56 @@ def test_lstm_pair_matches_one_cu_kernel(full_run, tmp_path):
     subprocess.run([sys.executable, "-c", _SINGLE_LSTM_SCRIPT, os.path.join(root, "kokoro-rust_amd"), str(f)],
                    env=env, check=True, timeout=240)
     one = np.load(f)
+    for b, it in enumerate(items):
+        same = np.array_equal(one[f"dur{b}"], durs[b])
+        if not same:
+            lg = torch.from_numpy(taps[b]["logits"].T.astype(np.float64))
+            s = torch.sigmoid(lg).sum(1).numpy() / it.speed
+            near = np.abs(s - np.floor(s) - 0.5) < 0.05
+            assert np.array_equal(one[f"dur{b}"][~near], durs[b][~near]), b
+        for name, bar in (("t_en", 120.0), ("d", 60.0), ("logits", 60.0), ("shared", 60.0)):
+            if name == "shared" and not same:
+                continue  # another frame count
+            snr = snr_db(one[f"{name}{b}"], taps[b][name])
+            _print(f"  item {b} {name}: pair vs one-CU kernel {snr:.1f} dB")
+            assert snr >= bar, (b, name)
+
+
+_VALU_ATTENTION_SCRIPT = """
+import sys, numpy as np
+sys.path.insert(0, sys.argv[1])
+from kokoro_hip import api, model_spec, workloads
+w = model_spec.random_model_weights(seed=0)
+items = workloads.small_ids_items(41, [30, 75, 12])
+ctx = api.Context(0)
+ctx.upload_model(w)
+with api.Plan.full(ctx, items) as plan:
+    plan.run()
+    out = {f"bert{b}": plan.tap("bert", b, (768, len(it.ids))) for b, it in enumerate(items)}
+ctx.close()
+np.savez(sys.argv[2], **out)
+"""
+
+
+def test_valu_attention_vs_oracle(full_run, oracle_runs, tmp_path):
+    """The f32 VALU attention kernel (KOKORO_HIP_ATTENTION_VALU=1, in a child process), the fallback
+    of the matrix-core one: ALBERT's output against the bf16-operand oracle at the bar the default
+    path meets (>= 40 dB), and within 50 dB of the matrix-core path (the two differ by f32 ordering,
+    amplified where it moves a bf16 operand of a later linear layer across a rounding boundary)."""
+    import subprocess
+    import sys
+    items, _, _, taps = full_run
+    _, emu = oracle_runs
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    f = tmp_path / "valu.npz"
+    env = dict(os.environ, KOKORO_HIP_ATTENTION_VALU="1")
+    subprocess.run([sys.executable, "-c", _VALU_ATTENTION_SCRIPT, os.path.join(root, "kokoro-rust_amd"), str(f)],
+                   env=env, check=True, timeout=240)
+    valu = np.load(f)
     for b in range(len(items)):
-        assert np.array_equal(one[f"dur{b}"], durs[b])
-        for name in ("d", "logits", "t_en", "shared"):
-            s = snr_db(one[f"{name}{b}"], taps[b][name])
-            _print(f"  item {b} {name}: pair vs one-CU kernel {s:.1f} dB")
-            assert s >= 90.0, (b, name)
+        s_emu, s_mfma = snr_db(_cm(emu[b]["bert"]), valu[f"bert{b}"]), snr_db(taps[b]["bert"], valu[f"bert{b}"])
+        _print(f"  item {b}: VALU attention vs oracle {s_emu:.1f} dB, vs the matrix-core path {s_mfma:.1f} dB")
+        assert s_emu >= 40.0 and s_mfma >= 50.0, b
 
 
 def test_item_independent_of_batch(full_ctx):
