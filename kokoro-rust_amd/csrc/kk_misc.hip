@@ -13,17 +13,6 @@ __constant__ double c_cos[11][20];
 __constant__ double c_sin[11][20];
 __constant__ float c_win[20];
 
-// The DFT tables in LDS: the (frame, bin) loops index them per lane, which the constant cache
-// serves one address at a time.
-struct DftLds {
-    double cs[11][20], sn[11][20];
-    float win[20];
-};
-__device__ __forceinline__ void stage_dft(DftLds& t) {
-    for (int i = threadIdx.x; i < 220; i += blockDim.x) (&t.cs[0][0])[i] = (&c_cos[0][0])[i], (&t.sn[0][0])[i] = (&c_sin[0][0])[i];
-    if (threadIdx.x < 20) t.win[threadIdx.x] = c_win[threadIdx.x];
-}
-
 namespace {
 
 constexpr float kPiF = 3.14159274101257324f;  // (float)M_PI, kernels/kokoro.cu:9
@@ -644,13 +633,19 @@ __device__ float har_sample(const SourceParams& p, int b, int t) {
 }
 
 // Harmonic source + STFT (stft20_ld, kernels/kokoro.cu:470-490) over a run of frames of one item:
-// the frames' reflect-padded samples are synthesized into LDS, then each (frame, bin) computes
-// its f64 DFT.  One launch covers every item (work list blk_item / blk_f0).
+// the frames' reflect-padded samples are synthesized into LDS, then each wave takes 64 frames (one
+// per lane) and one half of the 11 bins, so that every twiddle and window value a step reads is
+// the same for the whole wave (a scalar load from constant memory) and the lane's 20 windowed
+// samples stay in registers across its bins.  Each (frame, bin) is the reference's f64 DFT, term
+// by term in the same order.  The magnitudes and phases go through an LDS tile so that the block
+// writes its rows of the spectrum as contiguous runs.  One launch covers every item (work list
+// blk_item / blk_f0).
+constexpr int kSrcOutLd = 23;  // LDS row stride (floats) of the output tile: conflict-free per bin
 __global__ __launch_bounds__(256) void source_stft_kernel(SourceParams p) {
 #pragma clang fp contract(off)
+    static_assert(kSourceFrames == 128, "two frame groups of 64 lanes, two bin halves each");
     __shared__ float har[kSourceFrames * 5 + 15];
-    __shared__ DftLds dft;
-    stage_dft(dft);
+    __shared__ float out[kSourceFrames * kSrcOutLd];
     const int64_t blk = blockIdx.x;
     const int b = (int)p.blk_item[blk];
     const int64_t f_begin = p.blk_f0[blk];
@@ -665,19 +660,38 @@ __global__ __launch_bounds__(256) void source_stft_kernel(SourceParams p) {
         har[i] = har_sample(p, b, src);
     }
     __syncthreads();
-    for (int i = threadIdx.x; i < nf * 11; i += blockDim.x) {
-        const int fl = i / 11, k = i - fl * 11;
-        double re = 0.0, im = 0.0;
-        for (int n = 0; n < 20; n++) {
-            const double v = (double)(har[fl * 5 + n] * dft.win[n]);
-            re += v * dft.cs[k][n];
-            im -= v * dft.sn[k][n];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int fl = (wave >> 1) * 64 + lane;  // this lane's frame within the block
+    const int half = __builtin_amdgcn_readfirstlane(wave & 1);
+    if (fl < nf) {
+        double v[20];
+#pragma unroll
+        for (int n = 0; n < 20; n++) v[n] = (double)(har[fl * 5 + n] * c_win[n]);
+        auto bin = [&](int k) {
+            double re = 0.0, im = 0.0;
+#pragma unroll
+            for (int n = 0; n < 20; n++) {
+                re += v[n] * c_cos[k][n];
+                im -= v[n] * c_sin[k][n];
+            }
+            if (k == 0 || k == 10) im = 0.0;
+            const float rf = (float)re, imf = (float)im;
+            out[fl * kSrcOutLd + k] = hypotf(rf, imf);
+            out[fl * kSrcOutLd + 11 + k] = atan2f(imf, rf);
+        };
+        if (half == 0) {
+#pragma unroll
+            for (int k = 0; k < 6; k++) bin(k);
+        } else {
+#pragma unroll
+            for (int k = 6; k < 11; k++) bin(k);
         }
-        if (k == 0 || k == 10) im = 0.0;
-        const float rf = (float)re, imf = (float)im;
-        float* dst = p.spec + (p.start120[b] + f_begin + fl) * p.spec_ld;
-        dst[k] = hypotf(rf, imf);
-        dst[11 + k] = atan2f(imf, rf);
+    }
+    __syncthreads();
+    float* dst = p.spec + (p.start120[b] + f_begin) * p.spec_ld;
+    for (int i = threadIdx.x; i < nf * 22; i += blockDim.x) {
+        const int f = i / 22, c = i - f * 22;
+        dst[f * p.spec_ld + c] = out[f * kSrcOutLd + c];
     }
 }
 
