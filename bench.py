@@ -3,7 +3,7 @@
 Workload (the metric's config): 32 ragged items, N ~ U[100, 800] decoder
 frames each, seeded synthetic inputs and random-init weights of the real architecture.
 
-- `value` (the protocol of BASELINE.md section 5): one step = one C-ABI call of
+- `value` (the benchmark protocol: the whole call, host to host): one step = one C-ABI call of
   kk_forward_decoder_batch, from host inputs to host audio (layout, upload, duration expansion ->
   decoder -> harmonic source + STFT -> generator -> iSTFT -> audio copied back).  W warm calls, then
   K timed calls, each timed on its own; `value` = audio seconds / the median call.
@@ -289,7 +289,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only: the path is data-parallel over independent items and this "
-              f"build measures one GPU's share (requested --gpus {args.gpus}); see DESIGN.md for sharding.",
+              f"build measures one GPU's share (requested --gpus {args.gpus}); more GPUs would each take "
+              f"their own batches of items, with no traffic between them.",
               file=sys.stderr)
         sys.exit(2)
 
