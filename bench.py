@@ -40,7 +40,7 @@ sys.path.insert(0, ROOT)
 
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0
-PEAK_F32_VALU_TFLOPS = 78.6  # 256 CUs x 64 FMA / clk x 2.4 GHz (the attention runs on the VALU)
+PEAK_F32_MFMA_TFLOPS = 157.3  # dense f32 matrix-core peak (the attention runs on v_mfma_f32_32x32x2f32)
 BANDWIDTH_KERNELS = ["stats_tiles", "finalize", "style_fc", "expand", "f0n_conv", "copy_cols", "adain_pool",
                      "noise_conv0", "noise_conv1", "phase_pre", "source_stft", "istft"]
 
@@ -253,7 +253,7 @@ def e2e_leg(steps, warmup, with_cpu):
                         "note": "5 token-level BiLSTMs (longest item's ids) + the shared BiLSTM (longest item's "
                                 "frames); each (item, direction) on two CUs with all of W_hh on chip: per step "
                                 "~0.9 us of f32 FMA and the exchange of h through L2"},
-               "attention": rate("attention", PEAK_F32_VALU_TFLOPS),
+               "attention": rate("attention", PEAK_F32_MFMA_TFLOPS),
                "linear": rate("linear", PEAK_BF16_TFLOPS),
                "prosody_conv": rate("prosody_conv", PEAK_BF16_TFLOPS),
                "snake_conv": rate("snake_conv", PEAK_BF16_TFLOPS)}}
