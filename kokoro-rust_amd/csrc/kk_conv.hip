@@ -355,14 +355,14 @@ constexpr int kMaxBias = 1152;  // bias vector staged in LDS (output rows, M_pad
 // Starts a unit's accumulators at its bias (stride-1 layers): element 4 g + r of MFMA tile (i, j)
 // is output row i 32 + 8 g + 4 lh + r of the wave's 64 rows, for every column.  ConvT layers
 // (bias per output channel of a phase, added in their scatter) start from zero.
-template <bool BIAS>
-__device__ __forceinline__ void init_acc(f32x16 (&acc)[2][4], const float* bias_s, int m0, int wm, int lane) {
+template <bool BIAS, int MI = 2>
+__device__ __forceinline__ void init_acc(f32x16 (&acc)[MI][4], const float* bias_s, int m0, int wm, int lane) {
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int i = 0; i < MI; i++)
 #pragma unroll
         for (int g = 0; g < 4; g++) {
             float4 bv = make_float4(0.f, 0.f, 0.f, 0.f);
-            if constexpr (BIAS) bv = *(const float4*)(bias_s + m0 + wm * 64 + i * 32 + 8 * g + 4 * (lane >> 5));
+            if constexpr (BIAS) bv = *(const float4*)(bias_s + m0 + wm * 32 * MI + i * 32 + 8 * g + 4 * (lane >> 5));
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 acc[i][j][4 * g] = bv.x, acc[i][j][4 * g + 1] = bv.y;
@@ -558,9 +558,54 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
     init_acc<!CONVT>(acc, bias_s, next_m0, wm, lane);  // the next unit starts at its bias
 }
 
-template <int PRO, int EPI, int WM, int WN, bool STATS, bool IN_H, bool OUT_H, int MAXH>
+// Epilogue of a wave with one 32-row MFMA tile per column tile (layers of at most 32 output rows:
+// conv_post): plain stores of conv + bias.  Each 32-column slice goes through the wave's LDS scratch
+// ([32 columns][kScrLd32] f32), after which 8 lanes hold one column's 32 rows (lane group cg = lane /
+// 8 of 8 columns, cq = lane % 8 a quad of rows), so a store covers 8 columns' 128-byte row pieces.
+constexpr int kScrLd32 = 32 + 4;
+template <int WN>
+__device__ __forceinline__ void epilogue_m32(const ConvParams& p, const Unit& u, f32x16 (&acc)[1][4], int wm, int wn,
+                                             int lane, float* scr, const float* bias_s, int next_m0) {
+    const int l32 = lane & 31, lh = lane >> 5;
+    const int cq = lane & 7, cg = lane >> 3;
+    const int wcol0 = wn * 128;
+    const int m = u.m0 + wm * 32 + 4 * cq;  // this lane's 4 output rows after the transpose
+    const bool mok = m < p.m;
+    EpiBase eb;
+    eb.y = p.y + (int64_t)u.n0 * p.y_ld;
+    eb.ry = __builtin_amdgcn_make_buffer_rsrc(eb.y, 0, kBufRecords, kBufFormat);
+    eb.r0 = eb.r1 = eb.r2 = nullptr;
+    const uint32_t yld = (uint32_t)vgpr((int)p.y_ld);
+    const uint32_t yo0 = (uint32_t)(wcol0 + cg) * yld + m;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+#pragma unroll
+        for (int g = 0; g < 4; g++)
+            *(float4*)(scr + l32 * kScrLd32 + 8 * g + 4 * lh) =
+                make_float4(acc[0][j][4 * g], acc[0][j][4 * g + 1], acc[0][j][4 * g + 2], acc[0][j][4 * g + 3]);
+        __builtin_amdgcn_wave_barrier();  // LDS operations of one wave execute in order
+        float4 v[4];
+#pragma unroll
+        for (int q = 0; q < 4; q++) v[q] = *(const float4*)(scr + (8 * q + cg) * kScrLd32 + 4 * cq);
+#pragma unroll
+        for (int q = 0; q < 4; q++) ready(v[q]);
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int c = j * 32 + 8 * q;  // column of lane group 0 within the wave
+            const uint2 nopk = make_uint2(0u, 0u);
+            store4<false>(eb, yo0 + __umul24(c, yld), wcol0 + c + cg < u.nv && mok, v[q], nopk);
+        }
+        __builtin_amdgcn_wave_barrier();  // the slice's LDS reads before the next writes
+    }
+    init_acc<true, 1>(acc, bias_s, next_m0, wm, lane);  // the next unit starts at its bias
+}
+
+// MI: 32-row MFMA tiles per wave (2: 64 x 128 outputs per wave; 1: 32 x 128, layers of at most 32
+// output rows, plain stores).
+template <int PRO, int EPI, int WM, int WN, bool STATS, bool IN_H, bool OUT_H, int MAXH, int MI = 2>
 __global__ __launch_bounds__(64 * WM * WN + kNP) void conv_mfma_kernel(ConvParams p) {
-    constexpr int BM = 64 * WM, BN = 16 * kNJ * WN, NC = 64 * WM * WN;
+    constexpr int BM = 32 * MI * WM, BN = 16 * kNJ * WN, NC = 64 * WM * WN;
+    static_assert(MI == 2 || (EPI == EPI_STORE && !STATS && !OUT_H), "32-row waves: plain f32 stores only");
     extern __shared__ __align__(16) uint16_t xs[];
     const int mblocks = p.m_pad / BM;
     const int tw = BN + (p.k - 1) * p.dil;
@@ -655,12 +700,12 @@ __global__ __launch_bounds__(64 * WM * WN + kNP) void conv_mfma_kernel(ConvParam
     float* scr = (float*)(xs + 2 * slab_elems) + wave * 32 * kScrLd;
     const int n16 = p.cin_pad / 16;               // 16-channel groups
     const int64_t a_step = (int64_t)p.m_pad * 2;  // one 16-channel group of A, in bf16x8
-    const bf16x8* w_lane = (const bf16x8*)p.w + (int64_t)(wm * 64 + l32) * 2 + lh;
-    // A fragments of tap kk, 16-channel group c16: rows m0 + wm*64 + i*32 + l32 (i < 2)
-    auto load_a = [&](bf16x8 (&dst)[2], int m0, int kk, int c16) {
+    const bf16x8* w_lane = (const bf16x8*)p.w + (int64_t)(wm * 32 * MI + l32) * 2 + lh;
+    // A fragments of tap kk, 16-channel group c16: rows m0 + wm*32*MI + i*32 + l32 (i < MI)
+    auto load_a = [&](bf16x8 (&dst)[MI], int m0, int kk, int c16) {
         const bf16x8* ap = w_lane + (int64_t)m0 * 2 + ((int64_t)kk * n16 + c16) * a_step;
-        dst[0] = ap[0];
-        dst[1] = ap[64];
+#pragma unroll
+        for (int i = 0; i < MI; i++) dst[i] = ap[64 * i];
     };
     // B fragments of tap kk, 16-channel step kc of the slab: columns wn*128 + j*32 + l32 (j < 4)
     auto read_b = [&](bf16x8 (&dst)[4], const uint16_t* buf, int kk, int kc) {
@@ -674,12 +719,12 @@ __global__ __launch_bounds__(64 * WM * WN + kNP) void conv_mfma_kernel(ConvParam
     if constexpr (!CONVT) {
         for (int i = threadIdx.x; i < p.m_pad; i += NC) bias_s[i] = i < p.m ? p.bias[i] : 0.f;
     }
-    f32x16 acc[2][4];
-    auto mfma_step = [&](const bf16x8 (&a)[2], const bf16x8 (&b)[4]) {
+    f32x16 acc[MI][4];
+    auto mfma_step = [&](const bf16x8 (&a)[MI], const bf16x8 (&b)[4]) {
 #pragma unroll
         for (int j = 0; j < 4; j++)
 #pragma unroll
-            for (int i = 0; i < 2; i++)
+            for (int i = 0; i < MI; i++)
                 acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
     };
 
@@ -690,11 +735,11 @@ __global__ __launch_bounds__(64 * WM * WN + kNP) void conv_mfma_kernel(ConvParam
     bool has_next = unit_at(U + gridDim.x, nu);
     // A of the current tap, one register set per 16-channel step; each set is refilled with the
     // next tap's fragments right after its MFMAs issue (a full tap of lead time for the L2 loads).
-    bf16x8 A[4][2], B0[4], B1[4];
+    bf16x8 A[4][MI], B0[4], B1[4];
 #pragma unroll
     for (int kc = 0; kc < 4; kc++) load_a(A[kc], cu.m0, 0, kc);
     __syncthreads();  // slab 0 and the bias staged
-    init_acc<!CONVT>(acc, bias_s, cu.m0, wm, lane);
+    init_acc<!CONVT, MI>(acc, bias_s, cu.m0, wm, lane);
     for (int g = 0; g < G; g++) {
         const uint16_t* buf = xs + (g & 1) * slab_elems;
         const bool last = sl + 1 == nsl;
@@ -721,7 +766,9 @@ __global__ __launch_bounds__(64 * WM * WN + kNP) void conv_mfma_kernel(ConvParam
             // (not for the 256-channel accumulate-with-statistics variant: a second epilogue copy
             // makes it spill)
             constexpr bool kFullPath = !CONVT && !(EPI == EPI_ACCUM && WM == 4 && STATS);
-            if (kFullPath && cu.nv >= wn * 128 + 128 && cu.m0 + BM <= p.m)  // uniform: the common case
+            if constexpr (MI == 1)
+                epilogue_m32<WN>(p, cu, acc, wm, wn, lane, scr, bias_s, next_m0);
+            else if (kFullPath && cu.nv >= wn * 128 + 128 && cu.m0 + BM <= p.m)  // uniform: the common case
                 epilogue<EPI, WM, WN, STATS, OUT_H, true>(p, cu, acc, wm, wn, lane, scr, bias_s, next_m0);
             else
                 epilogue<EPI, WM, WN, STATS, OUT_H, false>(p, cu, acc, wm, wn, lane, scr, bias_s, next_m0);
@@ -738,9 +785,9 @@ __global__ __launch_bounds__(64 * WM * WN + kNP) void conv_mfma_kernel(ConvParam
     }
 }
 
-template <int PRO, int EPI, int WM, int WN, bool STATS, bool IN_H, bool OUT_H>
+template <int PRO, int EPI, int WM, int WN, bool STATS, bool IN_H, bool OUT_H, int MI = 2>
 hipError_t launch_t(const ConvParams& p, int n_cu, hipStream_t s, bool validate_only) {
-    constexpr int BM = 64 * WM, BN = 16 * kNJ * WN, NT = 64 * WM * WN + kNP;
+    constexpr int BM = 32 * MI * WM, BN = 16 * kNJ * WN, NT = 64 * WM * WN + kNP;
     const int halo = (p.k - 1) * p.dil;
     constexpr size_t scr_bytes = (size_t)WM * WN * 32 * kScrLd * sizeof(float) + kMaxBias * sizeof(float);
     const size_t smem = 2 * (size_t)(BN + halo) * kRS * sizeof(uint16_t) + scr_bytes;
@@ -779,8 +826,9 @@ hipError_t launch_t(const ConvParams& p, int n_cu, hipStream_t s, bool validate_
     // small halos (every k3 layer, k7 at dilation 1, the ConvTs, 1x1 convs): the producers stage
     // BN + 16 rows instead of BN + 64 (3 of 20 row passes fewer at BN 256, 3 of 12 at BN 128)
     static DeviceFlags attr_small, attr_max;
-    if (halo <= kSmallHalo) return go(conv_mfma_kernel<PRO, EPI, WM, WN, STATS, IN_H, OUT_H, kSmallHalo>, attr_small);
-    return go(conv_mfma_kernel<PRO, EPI, WM, WN, STATS, IN_H, OUT_H, kMaxHalo>, attr_max);
+    if (halo <= kSmallHalo)
+        return go(conv_mfma_kernel<PRO, EPI, WM, WN, STATS, IN_H, OUT_H, kSmallHalo, MI>, attr_small);
+    return go(conv_mfma_kernel<PRO, EPI, WM, WN, STATS, IN_H, OUT_H, kMaxHalo, MI>, attr_max);
 }
 
 }  // namespace
@@ -821,6 +869,9 @@ hipError_t launch_conv(const ConvParams& p, int pro, int epi, int shape, bool st
     KK_CONV(PRO_LEAKY, EPI_CONVT, SHAPE_256x128, 4, 1, true, false, false)
     KK_CONV(PRO_LEAKY, EPI_CONVT_REFLECT, SHAPE_256x128, 4, 1, true, false, false)
     KK_CONV(PRO_LEAKY, EPI_STORE, SHAPE_64x256, 1, 2, false, false, false)
+    // conv_post (22 output rows) on 32-row waves
+    if (pro == PRO_LEAKY && epi == EPI_STORE && shape == SHAPE_32x256 && !stats && !in_h && !out_h)
+        return launch_t<PRO_LEAKY, EPI_STORE, 1, 2, false, false, false, 1>(p, n_cu, s, validate_only);
 #undef KK_CONV
     return hipErrorInvalidValue;
 }

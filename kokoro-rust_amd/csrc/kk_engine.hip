@@ -577,7 +577,7 @@ static void load_model(kk_ctx* ctx, const kk_tensor* tensors, int n, bool norm_d
     static const int ks[3] = {3, 7, 11};
     for (int i = 0; i < 6; i++)
         load_snake(m.rb[i], t, g + ".resblocks." + std::to_string(i), i < 3 ? 256 : 128, ks[i % 3], sr);
-    load_conv(m.post, t, g + ".conv_post", 128, 22, 7, 3, 1, true, SHAPE_64x256);
+    load_conv(m.post, t, g + ".conv_post", 128, 22, 7, 3, 1, true, SHAPE_32x256);
     // style projections of every AdaIN, transposed [128][rows]
     upload_style_table(m.style_wt, m.style_b, m.style_rows, sr);
     // the stages before the decoder, when the table holds them (kk_forward_batch needs them)

@@ -47,10 +47,11 @@ enum BlockShape {
     SHAPE_256x128 = 0,  // 4 waves (4 x 1), wave tile 64 x 128
     SHAPE_128x256 = 1,  // 4 waves (2 x 2)
     SHAPE_64x256 = 2,   // 2 waves (1 x 2)
+    SHAPE_32x256 = 3,   // 2 waves (1 x 2), wave tile 32 x 128 (layers of at most 32 output rows)
 };
-constexpr int kShapeM[3] = {256, 128, 64};
-constexpr int kShapeN[3] = {128, 256, 256};
-constexpr int kShapeWN[3] = {1, 2, 2};
+constexpr int kShapeM[4] = {256, 128, 64, 32};
+constexpr int kShapeN[4] = {128, 256, 256, 256};
+constexpr int kShapeWN[4] = {1, 2, 2, 2};
 
 struct ConvParams {
     const void* x;           // input [l_in][x_ld] (f32, fp16 or bf16)
