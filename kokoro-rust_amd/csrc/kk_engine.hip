@@ -1097,8 +1097,8 @@ static void init_decoder_plan(kk_plan* p, const kk_decoder_item* items, int n, b
         check(it.dur && it.t_en && it.f0 && it.energy && it.ref_s, "item " + sb + ": null input");
         check(it.n_tok >= 1, "item " + sb + ": no tokens");
         int64_t nf = 0;
-        for (int i = 0; i < it.n_tok; i++) {
-            check(it.dur[i] >= 1, "item " + sb + ": durations must be >= 1");
+        for (int i = 0; i < it.n_tok; i++) {  // the message is built only for a failing duration
+            if (it.dur[i] < 1) check(false, "item " + sb + ": durations must be >= 1");
             nf += it.dur[i];
         }
         check(nf <= (int64_t)1 << 22, "item " + sb + ": too many frames");
@@ -2076,9 +2076,9 @@ static void init_full_plan(kk_plan* p, const kk_item* items, int n) {
         check(it.ids != nullptr && it.ref_s != nullptr, "item " + sb + ": null input");
         check(it.n_ids >= 2 && it.n_ids <= 512, "item " + sb + ": input_ids length outside [2, 512]");
         check(std::isfinite(it.speed) && it.speed > 0.f, "item " + sb + ": speed must be positive and finite");
-        for (int i = 0; i < it.n_ids; i++)
-            check(it.ids[i] >= 0 && it.ids[i] < 178, "item " + sb + ": token id " + std::to_string(it.ids[i]) +
-                                                          " out of range");
+        for (int i = 0; i < it.n_ids; i++)  // the message is built only for a failing id
+            if (it.ids[i] < 0 || it.ids[i] >= 178)
+                check(false, "item " + sb + ": token id " + std::to_string(it.ids[i]) + " out of range");
         check(it.noise_kind == KK_NOISE_COUNTER || it.noise_kind == KK_NOISE_FIXED, "item " + sb + ": unknown noise kind");
         p->tstart[b] = rows, p->ntok[b] = it.n_ids;
         rows += it.n_ids + kGapT;
