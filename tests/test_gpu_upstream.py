@@ -320,7 +320,7 @@ import sys, numpy as np
 sys.path.insert(0, sys.argv[1])
 from kokoro_hip import api, model_spec, workloads
 w = model_spec.random_model_weights(seed=0)
-items = workloads.small_ids_items(41, [30, 75, 12])
+items = workloads.small_ids_items(int(sys.argv[3]), [int(n) for n in sys.argv[4].split(",")])
 ctx = api.Context(0)
 ctx.upload_model(w)
 with api.Plan.full(ctx, items) as plan:
@@ -343,13 +343,41 @@ def test_valu_attention_vs_oracle(full_run, oracle_runs, tmp_path):
     root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
     f = tmp_path / "valu.npz"
     env = dict(os.environ, KOKORO_HIP_ATTENTION_VALU="1")
-    subprocess.run([sys.executable, "-c", _VALU_ATTENTION_SCRIPT, os.path.join(root, "kokoro-rust_amd"), str(f)],
-                   env=env, check=True, timeout=240)
+    subprocess.run([sys.executable, "-c", _VALU_ATTENTION_SCRIPT, os.path.join(root, "kokoro-rust_amd"), str(f),
+                    "41", ",".join(str(len(it.ids) - 2) for it in items)], env=env, check=True, timeout=240)
     valu = np.load(f)
     for b in range(len(items)):
         s_emu, s_mfma = snr_db(_cm(emu[b]["bert"]), valu[f"bert{b}"]), snr_db(taps[b]["bert"], valu[f"bert{b}"])
         _print(f"  item {b}: VALU attention vs oracle {s_emu:.1f} dB, vs the matrix-core path {s_mfma:.1f} dB")
         assert s_emu >= 40.0 and s_mfma >= 50.0, b
+
+
+def test_attention_tile_edges_vs_oracle(full_ctx, full_weights, tmp_path):
+    """ALBERT at lengths on either side of the attention kernels' tiles (32 queries per wave, 64
+    queries per block, 64 keys per chunk; 2 and 512 ids are the input's limits), both kernels --
+    the matrix-core default and the VALU fallback (KOKORO_HIP_ATTENTION_VALU=1, a child process) --
+    against the bf16-operand oracle (>= 40 dB, the token-phase bar)."""
+    import subprocess
+    import sys
+    from kokoro_hip import api, workloads
+    from oracle import torch_ref as R
+    ns = [2, 31, 32, 33, 64, 65, 127, 512]  # ids per item, the two boundary tokens included
+    items = workloads.small_ids_items(43, [n - 2 for n in ns])
+    with api.Plan.full(full_ctx, items) as plan:
+        plan.run()
+        mfma = [plan.tap("bert", b, (768, n)) for b, n in enumerate(ns)]
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    f = tmp_path / "valu.npz"
+    env = dict(os.environ, KOKORO_HIP_ATTENTION_VALU="1")
+    subprocess.run([sys.executable, "-c", _VALU_ATTENTION_SCRIPT, os.path.join(root, "kokoro-rust_amd"), str(f),
+                    "43", ",".join(str(n - 2) for n in ns)], env=env, check=True, timeout=240)
+    valu = np.load(f)
+    for b, (it, n) in enumerate(zip(items, ns)):
+        with R.bf16_operands():
+            ref = _cm(R.albert(full_weights, it.ids))
+        s_m, s_v = snr_db(ref, mfma[b]), snr_db(ref, valu[f"bert{b}"])
+        _print(f"  {n} ids: matrix-core attention {s_m:.1f} dB, VALU attention {s_v:.1f} dB vs the oracle")
+        assert s_m >= 40.0 and s_v >= 40.0, n
 
 
 def test_item_independent_of_batch(full_ctx):
