@@ -246,7 +246,7 @@ struct ConvTGeo {
 
 // Residual operands a stride-1 epilogue reads per 4 output rows.
 template <int EPI>
-constexpr int kNumRes = EPI == EPI_MEAN3 ? 3
+constexpr int kNumRes = (EPI == EPI_MEAN3 || EPI == EPI_MEAN3_LEAKY_BF16) ? 3
                         : (EPI == EPI_ACCUM || EPI == EPI_RESID || EPI == EPI_RESID_UP2 || EPI == EPI_ADD_FROM) ? 1
                                                                                                                  : 0;
 
@@ -271,7 +271,7 @@ __device__ __forceinline__ void load_res(const ConvParams& p, const EpiBase& eb,
         r[0] = *(const float4*)(p.r0 + (t >> 1) * p.r0_ld + m);
     } else if constexpr (EPI == EPI_ADD_FROM) {
         r[0] = *(const float4*)(eb.r0 + ro);
-    } else if constexpr (EPI == EPI_MEAN3) {
+    } else if constexpr (EPI == EPI_MEAN3 || EPI == EPI_MEAN3_LEAKY_BF16) {
         r[0] = *(const float4*)(eb.r0 + ro);
         r[1] = *(const float4*)(eb.r1 + ro);
         r[2] = *(const float4*)(eb.r2 + ro);
@@ -299,6 +299,18 @@ __device__ __forceinline__ float4 finish4(const ConvParams& p, float4 v, const f
         }
         pk = make_uint2(pack_bf16x2(g[0], g[1]), pack_bf16x2(g[2], g[3]));
         return v;
+    } else if constexpr (EPI == EPI_MEAN3_LEAKY_BF16) {
+        // the mean of three blocks as EPI_MEAN3, then the next layer's prologue (leaky ReLU, round to
+        // nearest even bf16): the same operand bits that layer's PRO_LEAKY staging would produce
+        const float4 a = r[0], b1 = r[1], c = r[2];
+        const float o[4] = {((a.x + b1.x) + (c.x + v.x)) / 3.0f, ((a.y + b1.y) + (c.y + v.y)) / 3.0f,
+                            ((a.z + b1.z) + (c.z + v.z)) / 3.0f, ((a.w + b1.w) + (c.w + v.w)) / 3.0f};
+        const float slope = p.slope;
+        float w[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) w[e] = o[e] < 0.f ? o[e] * slope : o[e];
+        pk = make_uint2(pack_bf16x2(w[0], w[1]), pack_bf16x2(w[2], w[3]));
+        return make_float4(o[0], o[1], o[2], o[3]);
     } else if constexpr (OUT_H) {
         // fp16 storage; the statistics use the f32 values, as the reference's f32 h does (the fp16
         // rounding would move the mean and variance by ~2^-12 relative, far below the next
@@ -425,8 +437,9 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
     if constexpr (CONVT) eb.y = p.y + ubase * p.y_ld;
     eb.ry = __builtin_amdgcn_make_buffer_rsrc(eb.y, 0, kBufRecords, kBufFormat);  // raw (stride 0) buffer
     eb.r0 = eb.r1 = eb.r2 = nullptr;
-    if constexpr (EPI == EPI_ADD_FROM || EPI == EPI_MEAN3) eb.r0 = p.r0 + n0 * p.r0_ld;
-    if constexpr (EPI == EPI_MEAN3) eb.r1 = p.r1 + n0 * p.r0_ld, eb.r2 = p.r2 + n0 * p.r0_ld;
+    constexpr bool MEAN = EPI == EPI_MEAN3 || EPI == EPI_MEAN3_LEAKY_BF16;
+    if constexpr (EPI == EPI_ADD_FROM || MEAN) eb.r0 = p.r0 + n0 * p.r0_ld;
+    if constexpr (MEAN) eb.r1 = p.r1 + n0 * p.r0_ld, eb.r2 = p.r2 + n0 * p.r0_ld;
     const uint32_t yld = (uint32_t)vgpr((int)p.y_ld), rld = (uint32_t)vgpr((int)p.r0_ld);
     const uint32_t yo0 = (uint32_t)(wcol0 + cg) * yld + m, ro0 = (uint32_t)(wcol0 + cg) * rld + m;
     const uint32_t yz = u.m0, rz = u.m0;  // clamped operand of an invalid row: row 0 of the unit
@@ -853,6 +866,8 @@ hipError_t launch_conv(const ConvParams& p, int pro, int epi, int shape, bool st
     KK_CONV(PRO_ADAIN_SNAKE, EPI_ACCUM, SHAPE_128x256, 2, 2, false, true, false)
     KK_CONV(PRO_ADAIN_SNAKE, EPI_ADD_FROM, SHAPE_128x256, 2, 2, true, true, false)
     KK_CONV(PRO_ADAIN_SNAKE, EPI_MEAN3, SHAPE_128x256, 2, 2, false, true, false)
+    // stage 1's mean, stored as conv_post's bf16 operand
+    KK_CONV(PRO_ADAIN_SNAKE, EPI_MEAN3_LEAKY_BF16, SHAPE_128x256, 2, 2, false, true, true)
     // decoder
     KK_CONV(PRO_ADAIN_LEAKY, EPI_STORE, SHAPE_256x128, 4, 1, true, false, false)
     KK_CONV(PRO_ADAIN_LEAKY, EPI_RESID, SHAPE_256x128, 4, 1, false, false, false)
@@ -869,7 +884,9 @@ hipError_t launch_conv(const ConvParams& p, int pro, int epi, int shape, bool st
     KK_CONV(PRO_LEAKY, EPI_CONVT, SHAPE_256x128, 4, 1, true, false, false)
     KK_CONV(PRO_LEAKY, EPI_CONVT_REFLECT, SHAPE_256x128, 4, 1, true, false, false)
     KK_CONV(PRO_LEAKY, EPI_STORE, SHAPE_64x256, 1, 2, false, false, false)
-    // conv_post (22 output rows) on 32-row waves
+    // conv_post (22 output rows) on 32-row waves, from its bf16 operand (or f32 through leaky ReLU)
+    if (pro == PRO_BF16 && epi == EPI_STORE && shape == SHAPE_32x256 && !stats && !in_h && !out_h)
+        return launch_t<PRO_BF16, EPI_STORE, 1, 2, false, false, false, 1>(p, n_cu, s, validate_only);
     if (pro == PRO_LEAKY && epi == EPI_STORE && shape == SHAPE_32x256 && !stats && !in_h && !out_h)
         return launch_t<PRO_LEAKY, EPI_STORE, 1, 2, false, false, false, 1>(p, n_cu, s, validate_only);
 #undef KK_CONV

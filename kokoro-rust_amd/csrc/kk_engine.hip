@@ -1401,7 +1401,7 @@ struct Runner {
         const double v_in = share * (double)o.din->valid(), v_out = share * (double)o.dout->valid();
         const double es_in = (o.in_h || o.pro == PRO_BF16) ? 2 : 4, es_out = o.out_h ? 2 : 4;
         const int nres = o.convt ? 1
-                         : o.epi == EPI_MEAN3 ? 3
+                         : (o.epi == EPI_MEAN3 || o.epi == EPI_MEAN3_LEAKY_BF16) ? 3
                          : (o.epi == EPI_ACCUM || o.epi == EPI_RESID || o.epi == EPI_ADD_FROM) ? 1
                                                                                                  : 0;
         double bytes = v_in * c.cin * es_in + v_out * c.cout * (es_out + 4.0 * nres);
@@ -1454,8 +1454,10 @@ struct Runner {
     // yt: the tiles whose partials of y its producer (the ConvT) wrote, `yparts` per tile, with the
     // reflected first row of each item (xrow_at) outside them when y_refl; null: a statistics pass.
     // hs: the fp16 h buffer of each block (distinct when the blocks run concurrently).
+    // post_out: the mean is stored there as conv_post's bf16 operand (leaky ReLU 0.01 applied)
+    // instead of as f32 in X[2] (the generator's last stage: nothing else reads its output)
     void resblock_mean(const MSnake* rbs, const float* y, float* X[3], float* const hs[3], const Dom& d,
-                       const Tiles* yt = nullptr, int yparts = 1, bool y_refl = false) {
+                       const Tiles* yt = nullptr, int yparts = 1, bool y_refl = false, void* post_out = nullptr) {
         const int c = rbs[0].c, wn = kShapeWN[rbs[0].c1[0].shape];
         // the three blocks' first AdaIN share one set of statistics of y
         if (yt) {
@@ -1499,6 +1501,10 @@ struct Runner {
                 if (i == 0) o2.epi = EPI_ADD_FROM, o2.r0 = y, o2.r0_ld = c;
                 if (j == 2 && i == 2) {
                     o2.epi = EPI_MEAN3, o2.r0 = X[0], o2.r1 = X[1], o2.r2 = X[2], o2.r0_ld = c;
+                    if (post_out) {
+                        // y (the stage input) is free once every block's first step has run
+                        o2.epi = EPI_MEAN3_LEAKY_BF16, o2.slope = 0.01f, o2.y = (float*)post_out, o2.out_h = true;
+                    }
                     if (conc) {
                         mean_op = o2, mean_pending = true;
                         continue;
@@ -1672,14 +1678,17 @@ struct Runner {
         // h of the three blocks: the two halves of B[2] (an fp16 [rows][c] fits in half of a buffer
         // sized for f32 [rows][128] at d120 and [rows][256] at d20) and B[1]
         float* const hs[3] = {B[2], B[2] + p->B[2].bytes / 2 / sizeof(float), B[1]};
-        resblock_mean(&m.rb[3 * i], B[3], X, hs, dout, &tu, kShapeWN[m.ups[i].shape] * ou.stride, i == 1);
+        // stage 1's mean goes to B[3] (its own input) as conv_post's bf16 operand
+        resblock_mean(&m.rb[3 * i], B[3], X, hs, dout, &tu, kShapeWN[m.ups[i].shape] * ou.stride, i == 1,
+                      i == 1 ? (void*)B[3] : nullptr);
     }
 
     // conv_post over the items [b0, b1) (all: b1 < 0)
     void post_istft(int b0 = 0, int b1 = -1) {
         const Dom& d = p->d120;
         Op o;
-        o.pro = PRO_LEAKY, o.slope = 0.01f, o.x = p->B[0].p, o.x_ld = 128, o.din = o.dout = &d;
+        // the input: stage 1's output as the bf16 operand its last conv stored (leaky ReLU 0.01 applied)
+        o.pro = PRO_BF16, o.x = p->B[3].p, o.x_ld = 128, o.din = o.dout = &d;
         o.y = p->post.as<float>(), o.y_ld = kPostLd, o.cls = PC_POST;
         o.label = "conv_post";
         if (b1 >= 0) {

@@ -42,6 +42,9 @@ enum Epilogue {
     EPI_CONVT = 6,          // polyphase ConvT scatter, y[o] = conv + b + r0[o]
     EPI_CONVT_REFLECT = 7,  // ConvT scatter with per-item ReflectionPad1d((1,0)), + r0
     EPI_GELU_BF16 = 8,      // y (bf16) = gelu_new(conv + b) (kernels/kokoro.cu:84-90), 2-byte output
+    EPI_MEAN3_LEAKY_BF16 = 9,  // y (bf16) = leaky(EPI_MEAN3's value, slope): the generator's last
+                               // Snake conv storing conv_post's input operand (2-byte output; the
+                               // slope in ConvParams.slope, which the Snake prologue does not use)
 };
 enum BlockShape {
     SHAPE_256x128 = 0,  // 4 waves (4 x 1), wave tile 64 x 128

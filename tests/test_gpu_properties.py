@@ -139,7 +139,10 @@ def test_gap_mask_negative_control(gpu_ctx, oracle_model, monkeypatch):
     off (KOKORO_BATCH_NEGCTL_NOMASK, src/gpu_batch.rs:62-66; tests/bf16x_regression.rs:47-55).  The
     same hook here makes every convolution read an item's neighbours and gaps as its own rows; the
     checks this suite relies on must then fail: the batch's audio changes, an item in the batch no
-    longer equals its run alone (with masking), and items fall below the oracle bar."""
+    longer equals its run alone (with masking), and items fall below the oracle bar.  Unmasked,
+    convolutions also read rows no kernel of the run wrote (gaps, and conv_post's bf16 operand rows
+    over stale f32 words), so that audio may hold non-finite values: they count as different, and
+    as failing the bar."""
     from kokoro_hip import workloads
     from oracle import oracle as O
     items = workloads.small_items(75, [9, 14, 6])
@@ -149,7 +152,7 @@ def test_gap_mask_negative_control(gpu_ctx, oracle_model, monkeypatch):
     monkeypatch.setenv("KOKORO_BATCH_NEGCTL_NOMASK", "1")
     unmasked = _run(gpu_ctx, items)
     monkeypatch.delenv("KOKORO_BATCH_NEGCTL_NOMASK")
-    assert all(np.isfinite(u).all() for u in unmasked)
+    assert all(np.isfinite(a).all() for a in masked)
     assert not np.array_equal(alone, unmasked[1])
     failing = 0
     for it, a, u in zip(items, masked, unmasked):
