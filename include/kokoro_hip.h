@@ -253,7 +253,9 @@ int kk_plan_sync(kk_plan* plan, char* err, size_t errlen);
 int kk_plan_fetch(kk_plan* plan, kk_output* out, char* err, size_t errlen);
 /* Copy a named device buffer of the last run to the host, per item and channel-major like the
  * reference's host tensors: "asr" [512][N], "decoder" [512][2N], "spec" [22][120N+1],
- * "gen0" [256][20N], "post" [22][120N+1], "audio" [600N]; of ids-level plans also "bert"
+ * "gen0" [256][20N] (after a run until KK_STAGE_GEN0: generator stage 0's output as the next
+ * layer's bf16 operand, leaky ReLU 0.1 applied, widened to f32), "post" [22][120N+1], "audio"
+ * [600N]; of ids-level plans also "bert"
  * [768][T], "d" [640][T] (the duration encoder's output), "logits" [50][T], "t_en" [512][T],
  * "shared" [512][N], "f0" [2N], "n" [2N] (T = n_ids).  `dst` receives item `item` only; `count`
  * is its element count. */

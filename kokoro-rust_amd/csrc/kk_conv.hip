@@ -866,7 +866,8 @@ hipError_t launch_conv(const ConvParams& p, int pro, int epi, int shape, bool st
     KK_CONV(PRO_ADAIN_SNAKE, EPI_ACCUM, SHAPE_128x256, 2, 2, false, true, false)
     KK_CONV(PRO_ADAIN_SNAKE, EPI_ADD_FROM, SHAPE_128x256, 2, 2, true, true, false)
     KK_CONV(PRO_ADAIN_SNAKE, EPI_MEAN3, SHAPE_128x256, 2, 2, false, true, false)
-    // stage 1's mean, stored as conv_post's bf16 operand
+    // each stage's mean, stored as the next layer's bf16 operand (ups.1, conv_post)
+    KK_CONV(PRO_ADAIN_SNAKE, EPI_MEAN3_LEAKY_BF16, SHAPE_256x128, 4, 1, false, true, true)
     KK_CONV(PRO_ADAIN_SNAKE, EPI_MEAN3_LEAKY_BF16, SHAPE_128x256, 2, 2, false, true, true)
     // decoder
     KK_CONV(PRO_ADAIN_LEAKY, EPI_STORE, SHAPE_256x128, 4, 1, true, false, false)
@@ -883,6 +884,7 @@ hipError_t launch_conv(const ConvParams& p, int pro, int epi, int shape, bool st
     // ConvT ups and conv_post
     KK_CONV(PRO_LEAKY, EPI_CONVT, SHAPE_256x128, 4, 1, true, false, false)
     KK_CONV(PRO_LEAKY, EPI_CONVT_REFLECT, SHAPE_256x128, 4, 1, true, false, false)
+    KK_CONV(PRO_BF16, EPI_CONVT_REFLECT, SHAPE_256x128, 4, 1, true, false, false)
     KK_CONV(PRO_LEAKY, EPI_STORE, SHAPE_64x256, 1, 2, false, false, false)
     // conv_post (22 output rows) on 32-row waves, from its bf16 operand (or f32 through leaky ReLU)
     if (pro == PRO_BF16 && epi == EPI_STORE && shape == SHAPE_32x256 && !stats && !in_h && !out_h)

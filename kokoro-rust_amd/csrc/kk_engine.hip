@@ -1454,10 +1454,12 @@ struct Runner {
     // yt: the tiles whose partials of y its producer (the ConvT) wrote, `yparts` per tile, with the
     // reflected first row of each item (xrow_at) outside them when y_refl; null: a statistics pass.
     // hs: the fp16 h buffer of each block (distinct when the blocks run concurrently).
-    // post_out: the mean is stored there as conv_post's bf16 operand (leaky ReLU 0.01 applied)
-    // instead of as f32 in X[2] (the generator's last stage: nothing else reads its output)
+    // post_out: the mean is stored there as the next layer's bf16 operand (leaky ReLU with
+    // post_slope applied) instead of as f32 in X[2] (nothing else reads a stage's output); it must not
+    // be a buffer the mean reads (X, the block 2's h)
     void resblock_mean(const MSnake* rbs, const float* y, float* X[3], float* const hs[3], const Dom& d,
-                       const Tiles* yt = nullptr, int yparts = 1, bool y_refl = false, void* post_out = nullptr) {
+                       const Tiles* yt = nullptr, int yparts = 1, bool y_refl = false, void* post_out = nullptr,
+                       float post_slope = 0.f) {
         const int c = rbs[0].c, wn = kShapeWN[rbs[0].c1[0].shape];
         // the three blocks' first AdaIN share one set of statistics of y
         if (yt) {
@@ -1491,7 +1493,7 @@ struct Runner {
             region = conc ? j : 0;
             Coef* ca = side ? cf(5 + 2 * j) : cf(0);  // the steps' AdaIN pair
             Coef* cb = side ? cf(6 + 2 * j) : cf(1);
-            float* h = conc ? hs[j] : hs[0];
+            float* h = hs[j];  // each block its own h in both orders (the mean's output may use hs[0..1])
             for (int i = 0; i < 3; i++) {
                 const float* in = i == 0 ? y : X[j];
                 const Tiles& t =
@@ -1502,8 +1504,8 @@ struct Runner {
                 if (j == 2 && i == 2) {
                     o2.epi = EPI_MEAN3, o2.r0 = X[0], o2.r1 = X[1], o2.r2 = X[2], o2.r0_ld = c;
                     if (post_out) {
-                        // y (the stage input) is free once every block's first step has run
-                        o2.epi = EPI_MEAN3_LEAKY_BF16, o2.slope = 0.01f, o2.y = (float*)post_out, o2.out_h = true;
+                        o2.epi = EPI_MEAN3_LEAKY_BF16, o2.slope = post_slope, o2.y = (float*)post_out;
+                        o2.out_h = true;
                     }
                     if (conc) {
                         mean_op = o2, mean_pending = true;
@@ -1667,8 +1669,9 @@ struct Runner {
         for (int j = 0; j < 6; j++) B[j] = p->B[j].as<float>();
         // y = ups[i](leaky_0.1(x) masked) (+ per-item reflect pad on stage 1) + xs (noise branch i)
         Op ou;
-        ou.pro = PRO_LEAKY, ou.epi = i == 0 ? EPI_CONVT : EPI_CONVT_REFLECT, ou.slope = 0.1f;
-        ou.x = i == 0 ? (const void*)p->dec_out.p : (const void*)B[0], ou.x_ld = i == 0 ? 512 : 256;
+        // ups.1 reads stage 0's output as the bf16 operand stage 0's mean stored (leaky 0.1 applied)
+        ou.pro = i == 0 ? PRO_LEAKY : PRO_BF16, ou.epi = i == 0 ? EPI_CONVT : EPI_CONVT_REFLECT, ou.slope = 0.1f;
+        ou.x = i == 0 ? (const void*)p->dec_out.p : (const void*)B[2], ou.x_ld = i == 0 ? 512 : 256;
         ou.din = &din, ou.dout = &dout, ou.y = B[3], ou.y_ld = c, ou.r0 = p->xs[i].as<float>(), ou.r0_ld = c;
         ou.convt = true, ou.stride = m.ups_stride[i], ou.pad_t = m.ups_pad[i], ou.cls = PC_CONVT;
         ou.stats = true;  // partials of y per (tile, phase, wave column) for the resblocks' first AdaIN
@@ -1678,9 +1681,11 @@ struct Runner {
         // h of the three blocks: the two halves of B[2] (an fp16 [rows][c] fits in half of a buffer
         // sized for f32 [rows][128] at d120 and [rows][256] at d20) and B[1]
         float* const hs[3] = {B[2], B[2] + p->B[2].bytes / 2 / sizeof(float), B[1]};
-        // stage 1's mean goes to B[3] (its own input) as conv_post's bf16 operand
+        // the stage's mean as the next layer's bf16 operand: stage 0's (ups.1: leaky 0.1) in B[2],
+        // blocks 0 and 1's h, free after the join (not B[3]: ups.1 writes there); stage 1's
+        // (conv_post: leaky 0.01) in B[3], the stage's input, free once every block's first step ran
         resblock_mean(&m.rb[3 * i], B[3], X, hs, dout, &tu, kShapeWN[m.ups[i].shape] * ou.stride, i == 1,
-                      i == 1 ? (void*)B[3] : nullptr);
+                      i == 0 ? (void*)B[2] : (void*)B[3], i == 0 ? 0.1f : 0.01f);
     }
 
     // conv_post over the items [b0, b1) (all: b1 < 0)
@@ -2349,6 +2354,19 @@ static void tap_rows(const void* dev, int64_t ld, int64_t r0, int64_t rows, int 
     KK_HIP(hipMemcpy(h.data(), (const float*)dev + r0 * ld, sizeof(float) * rows * ld, hipMemcpyDeviceToHost));
     for (int ch = 0; ch < c; ch++)
         for (int64_t t = 0; t < rows; t++) dst[(size_t)ch * rows + t] = h[(size_t)t * ld + ch];
+}
+// The same for a bf16 [rows][ld] tensor (each value widened exactly).
+static void tap_rows_bf16(const void* dev, int64_t ld, int64_t r0, int64_t rows, int c, float* dst) {
+    std::vector<uint16_t> h((size_t)rows * ld);
+    KK_HIP(hipMemcpy(h.data(), (const uint16_t*)dev + r0 * ld, sizeof(uint16_t) * rows * ld,
+                     hipMemcpyDeviceToHost));
+    for (int ch = 0; ch < c; ch++)
+        for (int64_t t = 0; t < rows; t++) {
+            const uint32_t bits = (uint32_t)h[(size_t)t * ld + ch] << 16;
+            float v;
+            std::memcpy(&v, &bits, sizeof v);
+            dst[(size_t)ch * rows + t] = v;
+        }
 }
 
 }  // namespace kk
@@ -3048,9 +3066,10 @@ int kk_plan_tap(kk_plan* plan, const char* name, int item, float* dst, int64_t c
             need(22 * (120 * N + 1));
             tap_rows(plan->spec.p, kSpecLd, 120 * a, 120 * N + 1, 22, dst);
         } else if (n == "gen0") {
+            // stage 0's output as ups.1's bf16 operand (leaky ReLU 0.1 applied), widened to f32
             check(plan->last_until == KK_STAGE_GEN0, "gen0 is valid after a run until KK_STAGE_GEN0");
             need(256 * 20 * N);
-            tap_rows(plan->B[0].p, 256, 20 * a, 20 * N, 256, dst);
+            tap_rows_bf16(plan->B[2].p, 256, 20 * a, 20 * N, 256, dst);
         } else if (n == "post") {
             need(22 * (120 * N + 1));
             tap_rows(plan->post.p, kPostLd, 120 * a, 120 * N + 1, 22, dst);
