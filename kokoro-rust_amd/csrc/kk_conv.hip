@@ -23,7 +23,8 @@
 //   their own weight loads (L2 hits), and the producers' VALU work co-issues with the MFMAs.
 // * The consumers issue v_mfma_f32_32x32x16_bf16: one wave per SIMD sustains the matrix core's
 //   rate with the 32x32 shape (the 16x16x32 shape needs two).  Each consumer wave owns a 64 x 128
-//   output tile (2 x 4 MFMA tiles, 128 accumulator registers).
+//   output tile (2 x 4 MFMA tiles, 128 accumulator registers); layers of at most 32 output rows
+//   (conv_post) use 32 x 128 tiles (1 x 4).
 // * A (weights) is pre-packed as [tap][cin/16][M_pad][16] bf16: one A fragment (32 rows x 16
 //   channels) is a contiguous 1 KB, loaded into registers a full tap ahead of its use; B fragments
 //   are read from LDS one 16-channel step ahead.
@@ -365,7 +366,7 @@ constexpr int kScrLd = 64 + 4;  // epilogue LDS scratch row stride (f32): one ti
 constexpr int kMaxBias = 1152;  // bias vector staged in LDS (output rows, M_pad)
 
 // Starts a unit's accumulators at its bias (stride-1 layers): element 4 g + r of MFMA tile (i, j)
-// is output row i 32 + 8 g + 4 lh + r of the wave's 64 rows, for every column.  ConvT layers
+// is output row i 32 + 8 g + 4 lh + r of the wave's 32 MI rows, for every column.  ConvT layers
 // (bias per output channel of a phase, added in their scatter) start from zero.
 template <bool BIAS, int MI = 2>
 __device__ __forceinline__ void init_acc(f32x16 (&acc)[MI][4], const float* bias_s, int m0, int wm, int lane) {
