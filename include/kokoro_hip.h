@@ -135,7 +135,9 @@ typedef struct {
  *   KOKORO_BATCH_NEGCTL_NOMASK (set: convolutions read neighbours and gaps as an item's own rows;
  *   the reference's negative control, src/gpu_batch.rs:62-66), KOKORO_HIP_TEST_OOM_ABOVE=k (a batch
  *   of more than k items fails with KK_ERR_OOM before allocating), KOKORO_HIP_TEST_POISON=1 (device
- *   buffers are filled with NaN bytes instead of being reused as they are). */
+ *   buffers are filled with NaN bytes instead of being reused as they are).  Diagnostics, read once
+ *   per process: KOKORO_HIP_TIMING=1 prints each call's host phase times to stderr (plan building,
+ *   launches, the wait for the device, the output copy). */
 int kk_forward_decoder_batch(kk_ctx* ctx, const kk_decoder_item* items, int n, kk_output* out, char* err,
                              size_t errlen);
 void kk_output_free(kk_output* out, int n);
