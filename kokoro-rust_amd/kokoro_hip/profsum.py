@@ -41,8 +41,9 @@ def snake_layers():
                 for cv in (1, 2):
                     # conv1 reads the f32 stream and writes fp16; conv2 reads fp16 and the f32
                     # residual, writes f32; the last conv of the three resblocks also reads the
-                    # other two blocks' streams and writes their mean
-                    per_col = 6 if cv == 1 else (18 if (blk, k, d) == ("resblock", 11, 5) else 10)
+                    # other two blocks' streams and writes their mean as the next layer's bf16
+                    # operand (2 + 3 x 4 + 2 bytes)
+                    per_col = 6 if cv == 1 else (16 if (blk, k, d) == ("resblock", 11, 5) else 10)
                     by = c * cols * per_col
                     out.append({"name": f"stage{st} {blk} k{k} d{d} conv{cv}", "flop": 2.0 * c * c * k * cols,
                                 "bytes": by})
