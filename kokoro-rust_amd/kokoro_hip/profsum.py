@@ -184,6 +184,44 @@ def traffic(fetch_dir, write_dir, mib):
     return res
 
 
+def counters(run_dir):
+    """MFMA utilisation of the conv kernels from one `rocprofv3 --pmc` pass (SQ_VALU_MFMA_BUSY_CYCLES,
+    SQ_INSTS_MFMA, GRBM_GUI_ACTIVE, ...; the counters summed over the device per dispatch).  The
+    matrix cores' busy cycles (SQ_VALU_MFMA_BUSY_CYCLES: each v_mfma_f32_32x32x16_bf16 counts its
+    32 pipeline cycles) against the cycles every SIMD had while the dispatch ran (GRBM_GUI_ACTIVE,
+    summed over the XCDs, / XCDs x SIMDs); the sustained clock is GRBM_GUI_ACTIVE / XCDs / duration.
+    Returns the markdown table and the totals."""
+    gpu = [r for r in _rows(os.path.join(run_dir, "run_agent_info.csv")) if "GPU" in r["Agent_Type"]][0]
+    simds, xcc = int(gpu["Simd_Count"]), int(gpu["Num_Xcc"])
+    disp = {}
+    for r in _rows(os.path.join(run_dir, "run_counter_collection.csv")):
+        d = disp.setdefault(int(r["Dispatch_Id"]), {"name": _short(r["Kernel_Name"]),
+                                                    "ns": int(r["End_Timestamp"]) - int(r["Start_Timestamp"])})
+        d[r["Counter_Name"]] = d.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+    groups = {}
+    for d in disp.values():
+        if not d["name"].startswith("conv_mfma_kernel"):
+            continue
+        cls = "Snake-block convs" if SNAKE.search(d["name"]) else "other convs (decoder, ConvT, conv_post)"
+        for key in (cls, "all convs"):
+            g = groups.setdefault(key, {"n": 0, "ns": 0.0, "busy": 0.0, "insts": 0.0, "gui": 0.0})
+            g["n"] += 1
+            g["ns"] += d["ns"]
+            g["busy"] += d.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0)
+            g["insts"] += d.get("SQ_INSTS_MFMA", 0.0)
+            g["gui"] += d.get("GRBM_GUI_ACTIVE", 0.0)
+    lines = ["| kernels | dispatches | ms | MFMA instructions | busy cycles per MFMA | sustained clock (GHz) | "
+             "MFMA busy (of every SIMD's cycles) |", "|---|---:|---:|---:|---:|---:|---:|"]
+    out = {}
+    for key, g in groups.items():
+        util = g["busy"] / max(g["gui"] / xcc * simds, 1.0)
+        clock = g["gui"] / xcc / max(g["ns"], 1.0)
+        out[key] = {"util": util, "clock_ghz": clock, "mfma_insts": g["insts"], "ms": g["ns"] / 1e6}
+        lines.append(f"| {key} | {g['n']} | {g['ns'] / 1e6:.2f} | {g['insts']:.4g} | "
+                     f"{g['busy'] / max(g['insts'], 1.0):.1f} | {clock:.2f} | {100 * util:.1f}% |")
+    return "\n".join(lines), out
+
+
 if __name__ == "__main__":
     sys.path.insert(0, os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
     if sys.argv[1] == "stats":
@@ -194,5 +232,7 @@ if __name__ == "__main__":
         print(layers_table(sys.argv[2]))
     elif sys.argv[1] == "traffic":
         print(json.dumps(traffic(sys.argv[2], sys.argv[3], float(sys.argv[4])), indent=1))
+    elif sys.argv[1] == "counters":
+        print(counters(sys.argv[2])[0])
     else:
         sys.exit(__doc__)

@@ -45,3 +45,35 @@ def test_traffic_scales_by_the_copy_kernel(tmp_path):
     assert abs(r["fetch"]["scale"] - 2.0) < 1e-9 and abs(r["write"]["scale"] - 1.0) < 1e-9
     assert abs(r["fetch"]["bytes_per_launch"] - mean_kib * 1024 * 2) < 1e-6
     assert abs(r["traffic_bytes_per_launch"] - (mean_kib * 2 + 500.0) * 1024) < 1e-6
+
+
+def test_counters_mfma_utilisation(tmp_path):
+    """MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / XCDs x SIMDs), the clock
+    GRBM_GUI_ACTIVE / XCDs / duration; counters split over several rows of a dispatch are summed."""
+    d = tmp_path / "pmc"
+    os.makedirs(d)
+    with open(d / "run_agent_info.csv", "w", newline="") as f:
+        w = csv.writer(f)
+        w.writerow(["Agent_Type", "Simd_Count", "Num_Xcc"])
+        w.writerow(["CPU", "0", "0"])
+        w.writerow(["GPU", "1024", "8"])
+    other = "void kk::(anonymous namespace)::conv_mfma_kernel<2, 0, 1, 2, false, false, false, 16, 1>(kk::ConvParams)"
+    rows = []
+    # a Snake conv of 1 ms at 2 GHz (2e6 cycles per SIMD): half its SIMD cycles busy with MFMAs
+    gui = 2e6 * 8
+    busy = 0.5 * 2e6 * 1024
+    for name, k in ((SNAKE, 1), (other, 2)):
+        rows += [(k, name, "GRBM_GUI_ACTIVE", gui / 2), (k, name, "GRBM_GUI_ACTIVE", gui / 2),
+                 (k, name, "SQ_VALU_MFMA_BUSY_CYCLES", busy / (1 if name == SNAKE else 4)),
+                 (k, name, "SQ_INSTS_MFMA", busy / 32 / (1 if name == SNAKE else 4))]
+    with open(d / "run_counter_collection.csv", "w", newline="") as f:
+        w = csv.writer(f)
+        w.writerow(["Dispatch_Id", "Kernel_Name", "Counter_Name", "Counter_Value", "Start_Timestamp",
+                    "End_Timestamp"])
+        for k, name, c, v in rows:
+            w.writerow([k, name, c, v, 0, 1_000_000])
+    _, tot = profsum.counters(str(d))
+    sn = tot["Snake-block convs"]
+    assert abs(sn["util"] - 0.5) < 1e-12 and abs(sn["clock_ghz"] - 2.0) < 1e-12
+    assert abs(tot["other convs (decoder, ConvT, conv_post)"]["util"] - 0.125) < 1e-12
+    assert abs(tot["all convs"]["util"] - 0.3125) < 1e-12
