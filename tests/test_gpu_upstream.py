@@ -156,6 +156,32 @@ def test_durations_vs_oracle(full_run, oracle_runs, oracle_f32_sums):
     assert np.concatenate(dev).mean() <= MEAN_FACTOR * spread.mean()
 
 
+def test_speed_scales_the_durations(full_ctx):
+    """The speed divides the duration head's sigmoid sums before rounding (src/model.rs:90-100): at
+    speeds 0.8 and 1.25 the durations are durations_from_logits of the device's own logits at that
+    speed, bit for bit; the logits do not depend on the speed (equal to a speed-1 run of the same
+    items); and each item's audio is 600 samples per frame of its own durations."""
+    from kokoro_hip import api, workloads
+    runs = {}
+    for speed in (1.0, 0.8, 1.25):
+        items = workloads.small_ids_items(47, [40, 17], speed=speed)
+        with api.Plan.full(full_ctx, items) as plan:
+            plan.run()
+            audio = plan.fetch()
+            durs = plan.durations
+            logits = [plan.tap("logits", b, (50, len(it.ids))) for b, it in enumerate(items)]
+        runs[speed] = (durs, logits)
+        for it, d, lg, a in zip(items, durs, logits, audio):
+            assert np.array_equal(d, api.durations_from_logits(np.ascontiguousarray(lg.T), speed))
+            assert a.shape == (600 * int(d.sum()),) and np.isfinite(a).all()
+        _print(f"  speed {speed}: frames {[int(d.sum()) for d in durs]}")
+    for speed in (0.8, 1.25):
+        for l1, ls in zip(runs[1.0][1], runs[speed][1]):
+            assert np.array_equal(l1, ls)
+    f = {sp: sum(int(d.sum()) for d in runs[sp][0]) for sp in runs}
+    assert f[0.8] > f[1.0] > f[1.25]
+
+
 def test_prosody_vs_oracle(full_run, oracle_runs, full_weights):
     """The shared LSTM against the oracle; the F0 / N stacks against the oracle's stacks on the GPU's
     own shared-LSTM output (the tight bar: the stacks' InstanceNorms over slowly varying channels
