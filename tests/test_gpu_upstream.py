@@ -413,6 +413,11 @@ def test_item_independent_of_batch(full_ctx):
     for b in (1, 2):
         (alone,) = full_ctx.forward_batch([items[b]])
         assert np.array_equal(alone[1], together[b][1]) and np.array_equal(alone[0], together[b][0])
+    # the batch in reverse order: every item's audio and durations unchanged (results in input order)
+    rev = full_ctx.forward_batch(items[::-1])
+    for b in range(len(items)):
+        r = rev[len(items) - 1 - b]
+        assert np.array_equal(r[0], together[b][0]) and np.array_equal(r[1], together[b][1]), b
 
 
 def test_poison_hook_changes_nothing(full_ctx):
