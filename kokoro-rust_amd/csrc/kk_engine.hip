@@ -1327,10 +1327,23 @@ struct Runner {
     // item, row xrow_at[b] of xrow [.][c]).
     void fin(const Tiles& t, int wn, int c, const MAdain& a, Coef* coef, const float* xrow = nullptr,
              const int64_t* xrow_at = nullptr) {
-        const double bytes = (double)t.count * wn * c * sizeof(StatPart) + (double)p->nb * c * (sizeof(Coef) + 8);
+        const MAdain* as[1] = {&a};
+        Coef* const cs[1] = {coef};
+        fin_n(t, wn, c, 1, as, cs, xrow, xrow_at);
+    }
+    // One finalize for the n (<= kFinMaxOuts) AdaIN layers as[k] of one tensor: its statistics once,
+    // each layer's coefficients into cs[k].
+    void fin_n(const Tiles& t, int wn, int c, int n, const MAdain* const* as, Coef* const* cs,
+               const float* xrow = nullptr, const int64_t* xrow_at = nullptr) {
+        check(n >= 1 && n <= kFinMaxOuts, "finalize outputs");
+        FinOuts fo{};
+        fo.n = n;
+        for (int k = 0; k < n; k++) fo.o[k] = FinOut{as[k]->gb_off, as[k]->nw.as<float>(), as[k]->nb.as<float>(), cs[k]};
+        const double bytes =
+            (double)t.count * wn * c * sizeof(StatPart) + (double)n * p->nb * c * (sizeof(Coef) + 8);
         launch(PC_FINALIZE, 0, bytes, [&] {
-            return launch_finalize(part(), c, wn, t.dev(), p->nb, t.max_tiles * wn, gbuf(), gb_ld(), a.gb_off,
-                                   a.nw.as<float>(), a.nb.as<float>(), coef, s, xrow, c, xrow_at);
+            return launch_finalize(part(), c, wn, t.dev(), p->nb, t.max_tiles * wn, gbuf(), gb_ld(), fo, s, xrow, c,
+                                   xrow_at);
         });
     }
     void stats_fin(const float* x, int64_t ld, int c, const Dom& d, const MAdain& a, Coef* coef) {
@@ -1461,15 +1474,13 @@ struct Runner {
                        const Tiles* yt = nullptr, int yparts = 1, bool y_refl = false, void* post_out = nullptr,
                        float post_slope = 0.f) {
         const int c = rbs[0].c, wn = kShapeWN[rbs[0].c1[0].shape];
-        // the three blocks' first AdaIN share one set of statistics of y
-        if (yt) {
-            for (int j = 0; j < 3; j++)
-                fin(*yt, yparts, c, rbs[j].a1[0], cf(2 + j), y_refl ? y : nullptr,
-                    y_refl ? d.start_d.as<int64_t>() : nullptr);
-        } else {
-            const Tiles& ts = stats(y, c, c, d);
-            for (int j = 0; j < 3; j++) fin(ts, 1, c, rbs[j].a1[0], cf(2 + j));
-        }
+        // the three blocks' first AdaIN share one set of statistics of y: one finalize for all three
+        const MAdain* a1s[3] = {&rbs[0].a1[0], &rbs[1].a1[0], &rbs[2].a1[0]};
+        Coef* const c1s[3] = {cf(2), cf(3), cf(4)};
+        if (yt)
+            fin_n(*yt, yparts, c, 3, a1s, c1s, y_refl ? y : nullptr, y_refl ? d.start_d.as<int64_t>() : nullptr);
+        else
+            fin_n(stats(y, c, c, d), 1, c, 3, a1s, c1s);
         // The three blocks are independent until the mean: blocks 0 and 1 run on the context's
         // side streams and block 2 on the main stream, each with its own h, statistics region and
         // AdaIN coefficients, and the mean (block 2's last conv) waits for the other two.  One

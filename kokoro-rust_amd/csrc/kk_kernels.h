@@ -101,10 +101,22 @@ hipError_t launch_stats_tiles(const float* x, int64_t ld, int c, TilesDev t, Sta
 // (tiles x wn), which sizes the reduction.
 // xrow (optional): one more sample per item outside the partials, row xrow_at[b] of xrow [.][xrow_ld]
 // (the reflected first row of the stage-1 ConvT output).
+// outs: the 1..kFinMaxOuts AdaIN layers that normalise this tensor, each with its style offset into
+// gb, norm weight / bias and coefficient array [nb][c].
+constexpr int kFinMaxOuts = 3;
+struct FinOut {
+    int gb_off;
+    const float* nw;
+    const float* nb;
+    Coef* coef;
+};
+struct FinOuts {
+    FinOut o[kFinMaxOuts];
+    int n;
+};
 hipError_t launch_finalize(const StatPart* part, int c, int wn, TilesDev t, int nb, int64_t max_parts,
-                           const float* gb, int64_t gb_ld, int gb_off, const float* nw, const float* nb_, Coef* coef,
-                           hipStream_t s, const float* xrow = nullptr, int64_t xrow_ld = 0,
-                           const int64_t* xrow_at = nullptr);
+                           const float* gb, int64_t gb_ld, const FinOuts& outs, hipStream_t s,
+                           const float* xrow = nullptr, int64_t xrow_ld = 0, const int64_t* xrow_at = nullptr);
 // gb[b][j] = W[j] . style[b] + bias[j] for every AdaIN layer at once.
 hipError_t launch_style_fc(const float* w, const float* bias, int rows, const float* style, int nb, float* gb,
                            hipStream_t s);

@@ -58,13 +58,14 @@ __global__ __launch_bounds__(256) void stats_tiles_kernel(const float* __restric
 // reduce in a fixed tree: deterministic, no atomics.  Each thread issues the loads of up to LOADS
 // partials before it adds any, and the launcher picks the smallest SUB (16, 32 or 64) and LOADS
 // (1, 4 or 8) that cover the largest item's partials in one such round: one memory latency per
-// launch for most layers, and no idle threads for the decoder's few partials per item.
+// launch for most layers, and no idle threads for the decoder's few partials per item.  One launch
+// serves every AdaIN layer that normalises the same tensor (outs: the three resblocks of a stage
+// read the same input): the statistics once, then each layer's coefficients.
 template <int SUB, int LOADS>
 __global__ __launch_bounds__(16 * SUB) void finalize_kernel(const StatPart* __restrict__ part, int c, int wn, TilesDev t,
-                                                            const float* __restrict__ gb, int64_t gb_ld, int gb_off,
-                                                            const float* __restrict__ nw, const float* __restrict__ nbias,
-                                                            Coef* __restrict__ coef, const float* __restrict__ xrow,
-                                                            int64_t xrow_ld, const int64_t* __restrict__ xrow_at) {
+                                                            const float* __restrict__ gb, int64_t gb_ld, FinOuts outs,
+                                                            const float* __restrict__ xrow, int64_t xrow_ld,
+                                                            const int64_t* __restrict__ xrow_at) {
     constexpr int kFinSub = SUB;
     __shared__ double sa[kFinSub][16], sb[kFinSub][16], sn[kFinSub][16];
     const int cl = threadIdx.x & 15, sub = threadIdx.x >> 4;
@@ -113,7 +114,9 @@ __global__ __launch_bounds__(16 * SUB) void finalize_kernel(const StatPart* __re
     }
     const int64_t i = (int64_t)b * c + ch;
     if (n <= 0.0) {
-        coef[i] = Coef{0.f, 0.f};
+#pragma unroll
+        for (int k = 0; k < kFinMaxOuts; k++)
+            if (k < outs.n) outs.o[k].coef[i] = Coef{0.f, 0.f};
         return;
     }
     const double dm = a1 / n;
@@ -121,10 +124,16 @@ __global__ __launch_bounds__(16 * SUB) void finalize_kernel(const StatPart* __re
     if (var < 0.0) var = 0.0;
     const float meanf = (float)(ref + dm);
     const float rstd = 1.0f / sqrtf((float)var + 1e-5f);
-    const double g1 = 1.0 + (double)gb[b * gb_ld + gb_off + ch];
-    const double beta = gb[b * gb_ld + gb_off + c + ch];
-    const double a = (double)rstd * (double)nw[ch];
-    coef[i] = Coef{(float)(a * g1), (float)(((double)nbias[ch] - (double)meanf * a) * g1 + beta)};
+    // each AdaIN layer of this tensor: its own style offset, norm weight / bias and coefficients
+#pragma unroll
+    for (int k = 0; k < kFinMaxOuts; k++) {
+        if (k >= outs.n) break;
+        const FinOut& o = outs.o[k];
+        const double g1 = 1.0 + (double)gb[b * gb_ld + o.gb_off + ch];
+        const double beta = gb[b * gb_ld + o.gb_off + c + ch];
+        const double a = (double)rstd * (double)o.nw[ch];
+        o.coef[i] = Coef{(float)(a * g1), (float)(((double)o.nb[ch] - (double)meanf * a) * g1 + beta)};
+    }
 }
 
 // ------------------------------------------------------------------ style projections
@@ -856,12 +865,13 @@ hipError_t launch_stats_tiles(const float* x, int64_t ld, int c, TilesDev t, Sta
 }
 
 hipError_t launch_finalize(const StatPart* part, int c, int wn, TilesDev t, int nb, int64_t max_parts,
-                           const float* gb, int64_t gb_ld, int gb_off, const float* nw, const float* nb_, Coef* coef,
-                           hipStream_t s, const float* xrow, int64_t xrow_ld, const int64_t* xrow_at) {
+                           const float* gb, int64_t gb_ld, const FinOuts& outs, hipStream_t s, const float* xrow,
+                           int64_t xrow_ld, const int64_t* xrow_at) {
+    if (outs.n < 1 || outs.n > kFinMaxOuts) return hipErrorInvalidValue;
     dim3 grid((unsigned)nb, (unsigned)ceil_div(c, 16));
     auto go = [&](auto kern, int sub) {
-        hipLaunchKernelGGL(kern, grid, dim3(16 * sub), 0, s, part, c, wn, t, gb, gb_ld, gb_off, nw, nb_, coef, xrow,
-                           xrow_ld, xrow_at);
+        hipLaunchKernelGGL(kern, grid, dim3(16 * sub), 0, s, part, c, wn, t, gb, gb_ld, outs, xrow, xrow_ld,
+                           xrow_at);
         return hipGetLastError();
     };
     if (max_parts <= 16) return go(finalize_kernel<16, 1>, 16);
