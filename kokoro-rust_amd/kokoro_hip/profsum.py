@@ -3,6 +3,9 @@
     python -m kokoro_hip.profsum stats <trace_dir> <steps>
         per-kernel table from a `rocprofv3 --kernel-trace` CSV run of bench.py, plus the average
         Snake-block conv duration of its profiling pass (the last <steps> steps)
+    python -m kokoro_hip.profsum serial <trace_dir> <steps>
+        per-kernel table of the trace's last <steps> runs alone (bench.py's profiling pass, every
+        kernel alone on one stream), for any workload whose runs end with the iSTFT
     python -m kokoro_hip.profsum kernels <trace_dir>
         per-kernel table (calls, total, average, share) of any `rocprofv3 --kernel-trace --stats` run
     python -m kokoro_hip.profsum layers <layers.json>
@@ -76,6 +79,27 @@ def _table(rows, dur, per_step=0):
     return lines, total
 
 
+def _serial_lines(rows, steps, dur):
+    """The per-kernel table of bench.py's profiling pass: every dispatch after the end of the run
+    before its first (each run ends with the iSTFT); empty when the trace has no such run."""
+    ist = [r for r in rows if "istft_kernel" in r["Kernel_Name"]]
+    if len(ist) <= steps:
+        return []
+    t0 = int(ist[-steps - 1]["End_Timestamp"])
+    ser = [r for r in rows if int(r["Start_Timestamp"]) > t0]
+    st, tot = _table(ser, dur, steps)
+    return [f"The profiling pass alone ({len(ser)} dispatches of the last {steps} runs, each kernel alone on "
+            f"one stream; {tot / 1e3 / steps:.3f} ms of kernels per run):", ""] + st
+
+
+def serial(trace_dir, steps):
+    """The per-kernel table of the trace's last `steps` runs alone (bench.py's profiling pass)."""
+    rows = _rows(os.path.join(trace_dir, "run_kernel_trace.csv"))
+    rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+    dur = lambda r: (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+    return "\n".join(_serial_lines(rows, steps, dur))
+
+
 def stats(trace_dir, steps):
     """Per-kernel table of the whole trace; the same table over bench.py's profiling pass alone (its
     last `steps` runs, every kernel alone on one stream: no span includes another stream's work);
@@ -84,15 +108,9 @@ def stats(trace_dir, steps):
     rows.sort(key=lambda r: int(r["Start_Timestamp"]))
     dur = lambda r: (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
     lines, _ = _table(rows, dur)
-    # the profiling pass: every dispatch after the end of the run before its first (each run ends
-    # with the iSTFT)
-    ist = [r for r in rows if "istft_kernel" in r["Kernel_Name"]]
-    if len(ist) > steps:
-        t0 = int(ist[-steps - 1]["End_Timestamp"])
-        ser = [r for r in rows if int(r["Start_Timestamp"]) > t0]
-        st, tot = _table(ser, dur, steps)
-        lines += ["", f"The profiling pass alone ({len(ser)} dispatches of the last {steps} runs, each kernel alone on "
-                      f"one stream; {tot / 1e3 / steps:.3f} ms of kernels per run):", ""] + st
+    st = _serial_lines(rows, steps, dur)
+    if st:
+        lines += [""] + st
     layers, frames = snake_layers()
     sn = [r for r in rows if SNAKE.search(r["Kernel_Name"])]
     last = sn[-steps * len(layers):]
@@ -226,6 +244,8 @@ if __name__ == "__main__":
     sys.path.insert(0, os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
     if sys.argv[1] == "stats":
         print(stats(sys.argv[2], int(sys.argv[3])))
+    elif sys.argv[1] == "serial":
+        print(serial(sys.argv[2], int(sys.argv[3])))
     elif sys.argv[1] == "kernels":
         print(kernels_table(sys.argv[2]))
     elif sys.argv[1] == "layers":

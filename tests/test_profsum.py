@@ -77,3 +77,26 @@ def test_counters_mfma_utilisation(tmp_path):
     assert abs(sn["util"] - 0.5) < 1e-12 and abs(sn["clock_ghz"] - 2.0) < 1e-12
     assert abs(tot["other convs (decoder, ConvT, conv_post)"]["util"] - 0.125) < 1e-12
     assert abs(tot["all convs"]["util"] - 0.3125) < 1e-12
+
+
+def test_serial_pass_is_the_last_runs(tmp_path):
+    """The serial table covers only the dispatches after the end of the last-but-`steps` run (each
+    run ends with the iSTFT); earlier, overlapped runs stay out of it."""
+    d = tmp_path / "trace"
+    os.makedirs(d)
+    ist = "void kk::(anonymous namespace)::istft_kernel(float const*, float*)"
+    fin = "void kk::(anonymous namespace)::finalize_kernel<16, 1>(kk::StatPart const*)"
+    # three runs: [fin 100 us, istft 10 us] each; the first two overlapped (long finalize)
+    seq = [(fin, 100), (ist, 10), (fin, 100), (ist, 10), (fin, 7), (ist, 10)]
+    with open(d / "run_kernel_trace.csv", "w", newline="") as f:
+        w = csv.writer(f)
+        w.writerow(["Kernel_Name", "Start_Timestamp", "End_Timestamp"])
+        t = 0
+        for name, us in seq:
+            w.writerow([name, t, t + us * 1000])
+            t += us * 1000 + 1000
+    out = profsum.serial(str(d), 1)
+    assert "(2 dispatches of the last 1 runs" in out
+    assert "| `finalize_kernel` | 1 | 0.01 | 7.0 |" in out
+    assert "| `istft_kernel` | 1 | 0.01 | 10.0 |" in out
+    assert profsum.serial(str(d), 3) == ""
