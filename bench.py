@@ -127,12 +127,13 @@ def cpu_baseline(weights, items, budget_s=12.0, torch_budget_s=8.0):
     return res, m
 
 
-def parity(model, it, audio, spec_gpu):
-    """Item `it`'s audio from the timed calls against the fp32 oracle, as the GPU tests compare it:
-    end to end, or -- when a spectral bin's phase is set by rounding (atan2's branch cut: a real
-    bin whose imaginary part is +-0 reads +pi on one side and -pi on the other; a real DC / Nyquist
-    bin whose sum cancels reads 0 or pi by its sign; the generator sees the jump as an input
-    change) -- against the oracle's generator run from the GPU's own spectrum."""
+def parity(model, items, audios, specs, hars):
+    """Every item's audio from the timed calls against the fp32 oracle, as the GPU tests compare it:
+    end to end for all items (max-abs and SNR), and -- for an item with a spectral bin whose phase
+    is set by rounding (atan2's branch cut: a real bin whose imaginary part is +-0 reads +pi on one
+    side and -pi on the other; a real DC / Nyquist bin whose sum cancels reads 0 or pi by its sign;
+    the generator sees the jump as an input change) -- also against the oracle's STFT and generator
+    run from the device's own harmonic-source samples (only the source substituted)."""
     import numpy as np
     from oracle import oracle as O
 
@@ -140,19 +141,59 @@ def parity(model, it, audio, spec_gpu):
         e = ((x.astype(np.float64) - ref) ** 2).sum()
         return round(float(10 * np.log10((ref.astype(np.float64) ** 2).sum() / max(e, 1e-300))), 2)
 
-    ref, spec, _ = O.synth_item(model, it, taps=True)
-    # bins whose phase input differs by > 1e-2 rad: phases set by rounding (atan2's branch cut, real
-    # DC / Nyquist bins whose sum cancels)
-    flips = int((np.abs(spec_gpu[11:].astype(np.float64) - spec[11:]) > 1e-2).sum())
-    out = {"item": 0, "n_frames": it.n_frames, "vs": "oracle/kk_oracle.c fp32", "phase_unstable_bins": flips,
-           "end_to_end": {"maxabs": float(np.abs(audio - ref).max()), "snr_db": snr(ref, audio)}}
-    if flips:
+    rows = []
+    for it, a, g, har in zip(items, audios, specs, hars):
         x = model.decoder(O.expand_tokens(it.t_en, it.dur), it.f0, it.energy, it.ref_s)
-        ref, _ = model.generator_from_spec(x, spec_gpu, it.ref_s)
-        out["from_gpu_spectrum"] = True
-    out["maxabs"] = float(np.abs(audio - ref).max())
-    out["snr_db"] = snr(ref, audio)
-    return out
+        ri, nz = O.item_noise(it)
+        ref, spec, _ = model.generator(x, it.f0, it.ref_s, ri, nz, taps=True)
+        flips = int((np.abs(g[11:].astype(np.float64) - spec[11:]) > 1e-2).sum())
+        row = [it.n_frames, flips, float(np.abs(a - ref).max()), snr(ref, a)]
+        sub = 0
+        if flips:
+            # the oracle's STFT of the device's source samples, or the device's spectrum where that STFT
+            # too reads a rounding-decided phase otherwise
+            spec_s = O.stft20(har)
+            sub = 1 if int((np.abs(g[11:].astype(np.float64) - spec_s[11:]) > 1e-2).sum()) == 0 else 2
+            ref, _ = model.generator_from_spec(x, spec_s if sub == 1 else g, it.ref_s)
+        rows.append(row + [float(np.abs(a - ref).max()), snr(ref, a), sub])
+    r = np.asarray(rows, np.float64)
+    return {"items": len(rows), "vs": "oracle/kk_oracle.c fp32",
+            "end_to_end": {"maxabs_max": float(r[:, 2].max()), "snr_db_min": float(r[:, 3].min()),
+                           "items_within_bar": int(((r[:, 2] <= 2e-3) & (r[:, 3] >= 40.0)).sum())},
+            "items_with_phase_unstable_bins": int((r[:, 1] > 0).sum()),
+            "substituted": {"source": int((r[:, 6] == 1).sum()), "spectrum": int((r[:, 6] == 2).sum())},
+            "maxabs_max": float(r[:, 4].max()), "snr_db_min": float(r[:, 5].min()),
+            "items_within_bar": int(((r[:, 4] <= 2e-3) & (r[:, 5] >= 40.0)).sum()),
+            "per_item": [[int(x[0]), int(x[1]), float("%.3g" % x[2]), x[3], float("%.3g" % x[4]), x[5]] for x in rows],
+            "per_item_fields": ["frames", "phase_unstable_bins", "e2e_maxabs", "e2e_snr_db", "maxabs", "snr_db"],
+            "note": "maxabs / snr_db: end to end, or where a phase is set by rounding from the device's source "
+                    "samples (the oracle's STFT of them), or its spectrum where that STFT reads such a phase otherwise"}
+
+
+def config5_leg(ctx, weights, steps, warmup):
+    """BASELINE config 5 (128 ragged items, generator frames log-uniform in [80, 4000], ~28 min of
+    audio) through the headline's call: host inputs in, host audio out, one kk_forward_decoder_batch
+    per step, median of `steps` after `warmup` calls."""
+    import numpy as np
+    from kokoro_hip import workloads
+    items = workloads.config5_items()
+    audio_s = sum(it.n_samples for it in items) / 24000.0
+    pb = ctx.prepare(items)
+    times = []
+    for k in range(warmup + steps):
+        t0 = time.perf_counter()
+        ctx.forward_prepared(pb)
+        if k >= warmup:
+            times.append(time.perf_counter() - t0)
+        if k + 1 < warmup + steps:
+            pb.release()
+    finite = all(np.isfinite(pb.audio(b)).all() for b in range(len(items)))
+    pb.release()
+    assert finite, "non-finite audio (config 5)"
+    ms = statistics.median(times) * 1e3
+    return {"value": round(audio_s / (ms / 1e3), 2), "unit": "audio-s/s", "ms_per_step": round(ms, 3),
+            "steps": steps, "items": len(items), "frames": sum(it.n_frames for it in items),
+            "audio_s": round(audio_s, 2), "step": "kk_forward_decoder_batch, host inputs -> host audio (median)"}
 
 
 def e2e_cpu_baseline(w, items, budget_s=15.0):
@@ -292,6 +333,9 @@ def main():
     ap.add_argument("--no-events", action="store_true", help="skip the per-launch profiling pass")
     ap.add_argument("--no-e2e", action="store_true", help="skip the ids-level (config 4) leg")
     ap.add_argument("--e2e-steps", type=int, default=5)
+    ap.add_argument("--no-config5", action="store_true", help="skip the config-5 host-in -> host-out leg")
+    ap.add_argument("--parity-items", type=int, default=-1,
+                    help="items of the batch compared with the oracle (default: all of config 3, 8 of config 5)")
     ap.add_argument("--only-e2e", action="store_true", help="run only the ids-level (config 4) leg")
     ap.add_argument("--layers", default="", help="write the profiling pass's per-launch table (JSON) here")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
@@ -348,8 +392,8 @@ def main():
         if k + 1 < args.steps:
             pb.release()
     t_region = time.perf_counter() - t_region0
-    audio0 = pb.audio(0)
-    finite = all(np.isfinite(pb.audio(b)).all() for b in range(len(items)))
+    audios = [pb.audio(b).copy() for b in range(len(items))]
+    finite = all(np.isfinite(a).all() for a in audios)
     pb.release()
     assert finite, "non-finite audio"
     ms = statistics.median(times) * 1e3
@@ -388,7 +432,18 @@ def main():
                 json.dump({"steps": args.steps, "workload": wl, "layers": per}, f, indent=1)
         prof = ctx.profile_read()
         ctx.set_profiling(False)
-    spec0 = plan.tap("spec", 0, (22, 120 * items[0].n_frames + 1))
+    plan.free()
+    # the parity leg's spectra and harmonic-source samples: one more run of a plan with the source tap
+    # (its audio equals the timed calls' bit for bit)
+    os.environ["KOKORO_HIP_TEST_TAP_SOURCE"] = "1"
+    try:
+        plan = api.Plan.decoder(ctx, items)
+    finally:
+        del os.environ["KOKORO_HIP_TEST_TAP_SOURCE"]
+    plan.run()
+    same = all(np.array_equal(a, b) for a, b in zip(plan.fetch(), audios))
+    specs = [plan.tap("spec", b, (22, 120 * it.n_frames + 1)) for b, it in enumerate(items)]
+    hars = [plan.tap("har", b, (600 * it.n_frames,)) for b, it in enumerate(items)]
     plan.free()
 
     roof, util, hbm = None, None, None
@@ -447,13 +502,19 @@ def main():
         "conv_mfma": util,
         "hbm": hbm,
     }
-    # parity of the measured batch: item 0 of the timed calls against the fp32 oracle
+    # parity of the measured batch: every item of the timed calls against the fp32 oracle
     from oracle import oracle as O
     if args.no_cpu:
         model = O.Model(weights)
     else:
         res["cpu_baseline"], model = cpu_baseline(weights, items)
-    res["parity"] = parity(model, items[0], audio0, spec0)
+    t0 = time.perf_counter()
+    k = args.parity_items if args.parity_items > 0 else (len(items) if args.config != 5 else 8)
+    res["parity"] = parity(model, items[:k], audios[:k], specs[:k], hars[:k])
+    res["parity"]["tap_plan_equals_timed_call"] = same
+    print(f"# parity leg {time.perf_counter() - t0:.1f} s", file=sys.stderr, flush=True)
+    if args.config != 5 and not args.no_config5:
+        res["config5"] = config5_leg(ctx, weights, max(3, args.steps // 4), args.warmup)
     ctx.close()
     if not args.no_e2e:
         res["e2e"] = e2e_leg(args.e2e_steps, 1, not args.no_cpu)

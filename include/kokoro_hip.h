@@ -227,7 +227,8 @@ int kk_plan_create_snake(kk_ctx* ctx, const char* prefix, const float* const* x,
  * (held from the library's first use on that device until the process ends); calls beyond
  * KK_NOALLOC_MAX_ROWS rows or KK_NOALLOC_MAX_ITEMS items are refused with KK_ERR_INVALID.  Every
  * call on one device shares that device's array: calls that overlap on one device race.  The call
- * returns when x holds the result. */
+ * returns when x holds the result; a call that fails returns only after every kernel it enqueued has
+ * finished, so x and the scratch are no longer written once the error is back. */
 #define KK_NOALLOC_MAX_ROWS 65536
 #define KK_NOALLOC_MAX_ITEMS 64
 #define KK_NOALLOC_SCRATCH_BYTES (48u << 20)
@@ -257,7 +258,8 @@ int kk_plan_fetch(kk_plan* plan, kk_output* out, char* err, size_t errlen);
  * reference's host tensors: "asr" [512][N], "decoder" [512][2N], "spec" [22][120N+1],
  * "gen0" [256][20N] (after a run until KK_STAGE_GEN0: generator stage 0's output as the next
  * layer's bf16 operand, leaky ReLU 0.1 applied, widened to f32), "post" [22][120N+1], "audio"
- * [600N]; of ids-level plans also "bert"
+ * [600N], "har" [600N] (the harmonic source's samples, the STFT's input; only for plans created
+ * with the test hook KOKORO_HIP_TEST_TAP_SOURCE=1 in the environment); of ids-level plans also "bert"
  * [768][T], "d" [640][T] (the duration encoder's output), "logits" [50][T], "t_en" [512][T],
  * "shared" [512][N], "f0" [2N], "n" [2N] (T = n_ids).  `dst` receives item `item` only; `count`
  * is its element count. */

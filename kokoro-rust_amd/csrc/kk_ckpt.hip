@@ -324,11 +324,19 @@ struct Loader {
         const int64_t total = (int64_t)(raw.second / 4);
         HostTensor t;
         t.shape = v->shape;
+        // The view's extent, overflow-checked: with a non-negative offset, sizes and strides, every
+        // element's offset lies in [offset, last], so last < total bounds every read below.
+        if (v->stride.size() != v->shape.size() || v->offset < 0) bad("tensor view of " + v->s + ": bad offset or rank");
         int64_t numel = 1, last = v->offset;
         for (size_t d = 0; d < v->shape.size(); d++) {
-            numel *= v->shape[d];
-            if (v->shape[d] > 0) last += (v->shape[d] - 1) * v->stride[d];
+            const int64_t n = v->shape[d], st = v->stride[d];
+            if (n < 0 || st < 0) bad("tensor view of " + v->s + ": negative size or stride");
+            int64_t span = 0;
+            if (__builtin_mul_overflow(numel, n, &numel) ||
+                (n > 0 && (__builtin_mul_overflow(n - 1, st, &span) || __builtin_add_overflow(last, span, &last))))
+                bad("tensor view of " + v->s + ": size overflows");
         }
+        if (numel > ((int64_t)1 << 31)) bad("tensor view of " + v->s + ": more than 2^31 elements");
         if (numel > 0 && last >= total) bad("tensor view runs past storage " + v->s);
         t.data.resize((size_t)numel);
         auto at = [&](int64_t k) {

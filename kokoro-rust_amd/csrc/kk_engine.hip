@@ -733,7 +733,7 @@ struct kk_plan {
     int64_t ln = 0;
     kk::Dom dn, d2, d20, d120, ds;
     // test hooks read at plan creation (see apply_test_hooks)
-    bool nomask = false, poison = false;
+    bool nomask = false, poison = false, tap_source = false;
     // snake plans
     const kk::MSnake* sblk = nullptr;
     int sc = 0;
@@ -744,6 +744,7 @@ struct kk_plan {
     int64_t t_rows = 0;
     // intermediates
     kk::DevBuf gb, xcat, xin_a, xin_b, hdec, pool, sc_half, dec_out, pp, spec, B[6], post, audio, audio_start;
+    kk::DevBuf har;  // the harmonic source's samples [600 ln] (only with KOKORO_HIP_TEST_TAP_SOURCE)
     kk::DevBuf xs[2], hn;  // the noise branches' outputs (d20 x 256, d120 x 128 f32) and their fp16 h
     // coef[0..1]: the Snake steps' AdaIN pair; [2..4]: the resblocks' first AdaIN; [5..8]: the pair
     // of resblock chains 0 and 1 (run on the context's side streams); [9..10]: the noise branches'
@@ -867,7 +868,9 @@ static int64_t env_i64(const char* name, int64_t dflt) {
 // - KOKORO_HIP_TEST_OOM_ABOVE=k: a batch of more than k items fails with KK_ERR_OOM before any
 //   allocation, as a device allocation failure would (the Err that Engine::synth_batch splits on,
 //   src/engine.rs:229-234);
-// - KOKORO_HIP_TEST_POISON=1: plan buffers are filled with NaN bytes instead of reused or zeroed.
+// - KOKORO_HIP_TEST_POISON=1: plan buffers are filled with NaN bytes instead of reused or zeroed;
+// - KOKORO_HIP_TEST_TAP_SOURCE=1: the harmonic source kernel also stores the samples it transforms
+//   (tap "har"), so that a test can run a CPU STFT and generator on exactly the device's source.
 static void apply_test_hooks(kk_plan* p, int n) {
     const int64_t lim = env_i64("KOKORO_HIP_TEST_OOM_ABOVE", -1);
     if (lim >= 0 && n > lim)
@@ -875,6 +878,7 @@ static void apply_test_hooks(kk_plan* p, int n) {
                              std::to_string(lim) + " (simulated device allocation failure)");
     p->nomask = std::getenv("KOKORO_BATCH_NEGCTL_NOMASK") != nullptr;
     p->poison = env_i64("KOKORO_HIP_TEST_POISON", 0) != 0;
+    p->tap_source = env_i64("KOKORO_HIP_TEST_TAP_SOURCE", 0) != 0;
 }
 
 // Resets a plan's host state for a new batch (a fresh plan, or the one-shot plan being reused).
@@ -1002,6 +1006,7 @@ static void setup_generator(kk_plan* p, const std::vector<const float*>& f0s, co
     for (int i = 0; i < 6; i++) alloc_buf(p, p->B[i], big);
     alloc_buf(p, p->post, (size_t)l120 * kPostLd * sizeof(float));
     alloc_buf(p, p->audio, (size_t)600 * ln * sizeof(float));
+    if (p->tap_source) alloc_buf(p, p->har, (size_t)600 * ln * sizeof(float));
     for (int i = 0; i < 11; i++) alloc_buf(p, p->coef[i], (size_t)nb * kXinLd * sizeof(Coef));
     alloc_buf(p, p->xs[0], (size_t)l20 * 256 * sizeof(float));
     alloc_buf(p, p->xs[1], (size_t)l120 * 128 * sizeof(float));
@@ -1644,6 +1649,7 @@ struct Runner {
         q.start120 = p->d120.start_d.as<int64_t>(), q.f_len = p->d120.len_d.as<int64_t>();
         q.blk_item = p->src_item.as<int64_t>(), q.blk_f0 = p->src_f0.as<int64_t>(), q.n_blocks = p->n_src;
         q.spec = p->spec.as<float>(), q.spec_ld = kSpecLd;
+        q.har_tap = p->tap_source ? p->har.as<float>() : nullptr;
         // reads F0 and the phases (d2), writes 22 f32 per STFT frame
         launch(PC_SOURCE, 0, n2 * 4 * (1 + kHarmonics) + nfr120 * 88, [&] { return launch_source_stft(q, s); });
     }
@@ -2082,6 +2088,17 @@ static void check_lstm_abort(kk_plan* p) {
     if (p->abort_host && *p->abort_host != 0)
         fail(KK_ERR_HIP, "BiLSTM recurrence: a block of a two-CU pair waited more than 2 s for its partner "
                           "(set KOKORO_HIP_LSTM_SINGLE=1 for the one-CU kernel)");
+}
+
+// Every path that hands an ids-level plan's results to the caller (audio, PCM, taps, sync) drains the
+// stream and fails if a recurrence of the last run gave up: its h rows would hold an earlier run's
+// values.  Plans of the other kinds run no recurrence.
+static void drain_and_check_abort(kk_plan* p) {
+    hipStream_t s = p->ctx->stream;
+    if (p->kind == PLAN_FULL && p->abort_host)
+        KK_HIP(hipMemcpyAsync(p->abort_host, p->u_lstmx.p, sizeof(uint64_t), hipMemcpyDeviceToHost, s));
+    KK_HIP(hipStreamSynchronize(s));
+    if (p->kind == PLAN_FULL) check_lstm_abort(p);
 }
 
 
@@ -2540,11 +2557,18 @@ static void snake_block_noalloc(kk_ctx* ctx, const char* prefix, float* x, int64
     Staging& st = ctx->stage;
     check(st.used <= kNaTablesBytes, "layout tables exceed the scratch");
     hipStream_t s = ctx->stream;
-    KK_HIP(hipMemcpyAsync(base + kNaTables, st.host, st.used, hipMemcpyHostToDevice, s));
-    for (const auto& r : st.refs) r.buf->view(base + kNaTables + r.off, r.bytes);
-    st.refs.clear();
-    p.frozen = true;
-    run_plan(&p, KK_STAGE_ALL);
+    try {
+        KK_HIP(hipMemcpyAsync(base + kNaTables, st.host, st.used, hipMemcpyHostToDevice, s));
+        for (const auto& r : st.refs) r.buf->view(base + kNaTables + r.off, r.bytes);
+        st.refs.clear();
+        p.frozen = true;
+        run_plan(&p, KK_STAGE_ALL);
+    } catch (...) {
+        // a failure after the first enqueue: run_plan has joined its side streams into s, so draining
+        // s leaves no kernel of this call writing x or the scratch once the error is returned
+        (void)hipStreamSynchronize(s);
+        throw;
+    }
     // x holds the result when the call returns (and the host tables outlive their copy)
     KK_HIP(hipStreamSynchronize(s));
 }
@@ -2801,7 +2825,7 @@ int kk_plan_sync(kk_plan* plan, char* err, size_t errlen) {
     }
     return guard(err, errlen, [&] {
         use_device(plan->ctx);
-        KK_HIP(hipStreamSynchronize(plan->ctx->stream));
+        drain_and_check_abort(plan);
     });
 }
 
@@ -2830,14 +2854,11 @@ static void fetch_plan(kk_plan* plan, kk_output* out, float* blk = nullptr) {
         for (int b = 0; b < plan->nb; b++) out[b] = kk_output{blk + 600 * plan->a[b], 600 * plan->nfr[b]};
     }
     if (!plan->early_issued) KK_HIP(hipMemcpyAsync(blk, plan->audio.p, bytes, hipMemcpyDeviceToHost, s));
-    if (plan->kind == PLAN_FULL)
-        KK_HIP(hipMemcpyAsync(plan->abort_host, plan->u_lstmx.p, sizeof(uint64_t), hipMemcpyDeviceToHost, s));
-    KK_HIP(hipStreamSynchronize(s));
+    drain_and_check_abort(plan);
     if (plan->early_issued) {
         KK_HIP(hipEventSynchronize(plan->out_ev[kk_plan::kOutGroups]));
         plan->early_issued = false;
     }
-    if (plan->kind == PLAN_FULL) check_lstm_abort(plan);
 }
 
 // The one-shot entries take the output block before the run, so that the run can copy each group
@@ -2879,7 +2900,7 @@ int kk_plan_fetch_pcm16(kk_plan* plan, int16_t* const* dst, int64_t* clipped, ch
         KK_HIP(launch_pcm16(plan->audio.as<float>(), plan->audio_start.as<int64_t>(), plan->pcm_len.as<int64_t>(),
                             plan->ist_item.as<int64_t>(), plan->ist_s0.as<int64_t>(), plan->n_ist,
                             plan->pcm.as<int16_t>(), plan->pcm_clip.as<unsigned long long>(), s));
-        KK_HIP(hipStreamSynchronize(s));
+        drain_and_check_abort(plan);
         for (int b = 0; b < plan->nb; b++)
             KK_HIP(hipMemcpy(dst[b], plan->pcm.as<int16_t>() + 600 * plan->a[b], sizeof(int16_t) * 600 * plan->nfr[b],
                              hipMemcpyDeviceToHost));
@@ -2961,6 +2982,8 @@ int kk_plan_fetch_pcm16_async(kk_plan* plan, int16_t* dst, int64_t* clipped, cha
         KK_HIP(hipMemcpyAsync(dst, plan->pcm.p, pcm_bytes, hipMemcpyDeviceToHost, s));
         if (clipped)
             KK_HIP(hipMemcpyAsync(clipped, plan->pcm_clip.p, sizeof(int64_t) * plan->nb, hipMemcpyDeviceToHost, s));
+        if (plan->kind == PLAN_FULL && plan->abort_host)
+            KK_HIP(hipMemcpyAsync(plan->abort_host, plan->u_lstmx.p, sizeof(uint64_t), hipMemcpyDeviceToHost, s));
         KK_HIP(hipEventRecord(plan->fetch_ev, s));
         plan->fetch_pending = true;
     });
@@ -2977,6 +3000,7 @@ int kk_plan_fetch_wait(kk_plan* plan, char* err, size_t errlen) {
         use_device(plan->ctx);
         plan->fetch_pending = false;
         KK_HIP(hipEventSynchronize(plan->fetch_ev));
+        if (plan->kind == PLAN_FULL) check_lstm_abort(plan);  // the run's abort flag came with the samples
     });
 }
 
@@ -3040,7 +3064,7 @@ int kk_plan_tap(kk_plan* plan, const char* name, int item, float* dst, int64_t c
         use_device(plan->ctx);
         check(item >= 0 && item < plan->nb, "item out of range");
         check(plan->kind != PLAN_SNAKE, "snake plans have no taps");
-        KK_HIP(hipStreamSynchronize(plan->ctx->stream));
+        drain_and_check_abort(plan);
         const std::string n(name);
         const int64_t N = plan->nfr[item], a = plan->a[item];
         auto need = [&](int64_t c) { check(count == c, "tap " + n + " holds " + std::to_string(c) + " values"); };
@@ -3073,6 +3097,10 @@ int kk_plan_tap(kk_plan* plan, const char* name, int item, float* dst, int64_t c
         } else if (n == "decoder") {
             need(512 * 2 * N);
             tap_rows(plan->dec_out.p, 512, 2 * a, 2 * N, 512, dst);
+        } else if (n == "har") {
+            check(plan->tap_source, "tap har needs KOKORO_HIP_TEST_TAP_SOURCE=1 at plan creation");
+            need(600 * N);
+            KK_HIP(hipMemcpy(dst, plan->har.as<float>() + 600 * a, sizeof(float) * 600 * N, hipMemcpyDeviceToHost));
         } else if (n == "spec") {
             need(22 * (120 * N + 1));
             tap_rows(plan->spec.p, kSpecLd, 120 * a, 120 * N + 1, 22, dst);

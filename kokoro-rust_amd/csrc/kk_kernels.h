@@ -168,6 +168,7 @@ struct SourceParams {
     int64_t n_blocks;
     float* spec;
     int64_t spec_ld;
+    float* har_tap;           // or null: the source samples at 600 a_b (a test tap)
 };
 hipError_t launch_source_stft(const SourceParams& p, hipStream_t s);
 // iSTFT frames + overlap-add, one launch over all items: audio packed at 600 a_b.

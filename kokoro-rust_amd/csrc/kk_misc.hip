@@ -667,6 +667,9 @@ __global__ __launch_bounds__(256) void source_stft_kernel(SourceParams p) {
         const int64_t pos = p0 + i;
         const int src = (int)(pos < 0 ? -pos : (pos >= s_len ? 2 * (int64_t)s_len - 2 - pos : pos));
         har[i] = har_sample(p, b, src);
+        // test tap: the item's samples in place (blocks' windows overlap by 15 samples and store
+        // the same values)
+        if (p.har_tap && pos >= 0 && pos < s_len) p.har_tap[5 * p.start120[b] + pos] = har[i];
     }
     __syncthreads();
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;

@@ -1,4 +1,7 @@
 """GPU-side comparison helpers shared by the GPU test modules (not a test module itself)."""
+import contextlib
+import os
+
 import numpy as np
 
 from conftest import snr_db
@@ -19,6 +22,10 @@ def _print(*a):
 ILL_CONDITIONED_N = (2,)
 
 
+# At most this many bins per item may carry a phase that rounding decides (measured: 0-3).
+MAX_UNSTABLE_BINS = 4
+
+
 def unstable_phase_bins(spec_gpu, spec_ref):
     """Spectral bins whose phase input to the generator differs between two spectra by more than
     1e-2 rad (raw, not wrapped: the generator reads the phase values themselves).  Two kinds occur,
@@ -29,59 +36,130 @@ def unstable_phase_bins(spec_gpu, spec_ref):
     return int((np.abs(np.asarray(spec_gpu[11:], np.float64) - spec_ref[11:]) > 1e-2).sum())
 
 
+def classify_unstable_bins(spec_gpu, spec_ref):
+    """Each bin flagged by unstable_phase_bins, classified: "cut" -- both phases within 1e-3 of
+    +-pi with opposite signs (atan2's branch cut); "real" -- bin 0 or 10 (real by construction)
+    whose magnitude on both sides is below 1e-6 of the item's largest, reading 0 on one side and pi
+    on the other; anything else is "other" (a phase error).  Returns the three counts."""
+    g, r = np.asarray(spec_gpu, np.float64), np.asarray(spec_ref, np.float64)
+    peak = max(np.abs(r[:11]).max(), 1e-30)
+    n_cut = n_real = n_other = 0
+    for k, f in zip(*np.nonzero(np.abs(g[11:] - r[11:]) > 1e-2)):
+        pg, pr = g[11 + k, f], r[11 + k, f]
+        if abs(abs(pg) - np.pi) < 1e-3 and abs(abs(pr) - np.pi) < 1e-3 and pg * pr < 0:
+            n_cut += 1
+        elif (k in (0, 10) and max(g[k, f], r[k, f]) < 1e-6 * peak
+              and min(abs(pg), abs(pr)) < 1e-3 and abs(max(abs(pg), abs(pr)) - np.pi) < 1e-3):
+            n_real += 1
+        else:
+            n_other += 1
+    return n_cut, n_real, n_other
+
+
+@contextlib.contextmanager
+def source_tap():
+    """Plans created inside store the harmonic source's samples (tap "har")."""
+    os.environ["KOKORO_HIP_TEST_TAP_SOURCE"] = "1"
+    try:
+        yield
+    finally:
+        del os.environ["KOKORO_HIP_TEST_TAP_SOURCE"]
+
+
+def check_source(oracle_model, f0, rand_ini, noise, har_gpu, spec_gpu):
+    """The device's harmonic source against the oracle's on the same F0 and noise (f32 sin of
+    large phases: a few ulp), and the device's STFT against the oracle's STFT of the device's own
+    samples: every bin, low-energy ones included -- magnitudes to the ulp of hypotf, phases to the
+    ulp of atan2f except bins of the two kinds rounding decides (classify_unstable_bins: a zero or
+    near-zero imaginary part read as +pi or -pi, or a cancelled real bin read as 0 or pi), at most
+    MAX_UNSTABLE_BINS.  Returns that oracle spectrum, the number of such bins between it and the
+    device's, and the source's max-abs difference."""
+    from oracle import oracle as O
+    har_o = O.sine_source(f0, rand_ini, noise, oracle_model.l_w, oracle_model.l_b)
+    d_har = float(np.abs(har_gpu - har_o).max())
+    assert d_har <= 1e-5, d_har
+    spec_s = O.stft20(har_gpu)
+    g = np.asarray(spec_gpu, np.float64)
+    mag = np.abs(g[:11] - spec_s[:11]).max() / max(np.abs(spec_s[:11]).max(), 1e-30)
+    assert mag <= 1e-6, mag
+    dph = np.abs(g[11:] - spec_s[11:])
+    n_cut, n_real, n_other = classify_unstable_bins(g, spec_s)
+    bad = [(int(k), int(f), float(g[11 + k, f]), float(spec_s[11 + k, f]), float(g[k, f]), float(spec_s[k, f]))
+           for k, f in zip(*np.nonzero(dph > 1e-5))]
+    _print(f"    source: maxabs {d_har:.2g}, STFT of the device's samples: mag err {mag:.2g}, phase err "
+           f"{dph[dph <= 1e-2].max():.2g} outside {len(bad)} bins (k, frame, phase gpu / cpu, mag gpu / cpu): {bad[:6]}")
+    assert n_other == 0 and n_cut + n_real <= MAX_UNSTABLE_BINS, bad
+    assert len(bad) == n_cut + n_real, bad
+    return spec_s, n_cut + n_real, d_har
+
+
 def check_vs_oracle(ctx, oracle_model, items, label):
     """Runs the items and compares each with the oracle.
 
     - Duration expansion: bit-exact.
-    - Source spectrum: magnitudes to f32 rounding, phases on the circle where a bin carries energy.
+    - Source: the device's harmonic-source samples (test tap) against the oracle's, and the
+      device's spectrum against the oracle's STFT of those samples, every bin (check_source).
+    - Source spectrum end to end: magnitudes to f32 rounding, phases on the circle where a bin
+      carries energy; the bins whose phase rounding decides (classify_unstable_bins: atan2's branch
+      cut -- the first and last frame of every item are symmetric under the reflect padding, so all
+      their bins are real -- and real DC / Nyquist bins whose sum cancels) are at most
+      MAX_UNSTABLE_BINS per item and of those two kinds only.
     - Audio with the north-star bar (max-abs <= 2e-3, SNR >= 40 dB): end to end against the oracle,
-      or against the oracle's generator run from the GPU's own spectrum when a bin's phase is set by
-      rounding (unstable_phase_bins: atan2's branch cut -- the first and last frame of every item are
-      symmetric under the reflect padding, so all their bins are real -- and real DC / Nyquist bins
-      whose sum cancels); the generator sees such a phase jump as an input change, in the reference
-      against upstream torch as here.
+      or, when a bin's phase is set by rounding (the generator sees such a jump as an input change,
+      in the reference against upstream torch as here), against the oracle's generator run from
+      the oracle's own STFT of the device's source samples -- only the source is substituted --
+      or, where that STFT too reads a rounding-decided phase otherwise, from the device's spectrum
+      (which check_source has compared with it bin for bin).
     - Two-frame items (ILL_CONDITIONED_N): the decoder output within 6 dB of the bf16-emulated
       oracle's own distance from fp32, and the audio against the oracle's generator run from the
-      GPU's decoder output and spectrum.
+      GPU's decoder output and the oracle's STFT of the device's source.
     Returns the number of items compared end to end and the audio."""
     from kokoro_hip import api
     from oracle import oracle as O
-    with api.Plan.decoder(ctx, items) as plan:
+    with source_tap(), api.Plan.decoder(ctx, items) as plan:
         plan.run()
         outs = plan.fetch()
         taps = [{"asr": plan.tap("asr", b, (512, it.n_frames)), "dec": plan.tap("decoder", b, (512, 2 * it.n_frames)),
-                 "spec": plan.tap("spec", b, (22, 120 * it.n_frames + 1))} for b, it in enumerate(items)]
+                 "spec": plan.tap("spec", b, (22, 120 * it.n_frames + 1)),
+                 "har": plan.tap("har", b, (600 * it.n_frames,))} for b, it in enumerate(items)]
     end_to_end = 0
     for it, a, tp in zip(items, outs, taps):
         assert a.shape == (600 * it.n_frames,) and np.isfinite(a).all()
         asr = O.expand_tokens(it.t_en, it.dur)
         assert np.array_equal(asr, tp["asr"])
         g = tp["spec"]
+        spec_s, s_flips, d_har = check_source(oracle_model, it.f0, *O.item_noise(it), tp["har"], g)
+        # the generator's spectrum for a substituted run: the oracle's STFT of the device's source,
+        # or, where even that reads a rounding-decided phase differently, the device's (checked
+        # against it bin for bin just above)
+        spec_sub = spec_s if s_flips == 0 else g
         ref, spec, _ = O.synth_item(oracle_model, it, taps=True)
         mag_err = np.abs(g[:11] - spec[:11]).max() / max(np.abs(spec[:11]).max(), 1e-6)
         dphi = np.angle(np.exp(1j * (g[11:].astype(np.float64) - spec[11:])))
         energetic = spec[:11] > 1e-4 * spec[:11].max()
         flips = unstable_phase_bins(g, spec)
+        n_cut, n_real, n_other = classify_unstable_bins(g, spec)
         assert mag_err < 1e-4 and np.abs(dphi[energetic]).max() < 1e-3
+        assert n_other == 0 and flips == n_cut + n_real and flips <= MAX_UNSTABLE_BINS, (n_cut, n_real, n_other)
         note = ""
         if it.n_frames in ILL_CONDITIONED_N:
             x = oracle_model.decoder(asr, it.f0, it.energy, it.ref_s)
             with O.bf16_emulation():
                 xe = oracle_model.decoder(asr, it.f0, it.energy, it.ref_s)
             d_gpu, d_emu = snr_db(x, tp["dec"]), snr_db(x, xe)
-            note = f" decoder snr {d_gpu:.1f} (emulation {d_emu:.1f}); generator from the GPU decoder and spectrum"
+            note = f" decoder snr {d_gpu:.1f} (emulation {d_emu:.1f}); generator from the GPU decoder and source"
             assert d_gpu >= min(d_emu, 40.0) - 6.0
-            ref, _ = oracle_model.generator_from_spec(tp["dec"], g, it.ref_s)
+            ref, _ = oracle_model.generator_from_spec(tp["dec"], spec_sub, it.ref_s)
         elif flips:
-            note = " (generator from the GPU spectrum)"
+            note = (f" ({n_cut} branch-cut, {n_real} cancelled real bins: generator from the GPU "
+                    f"{'source' if s_flips == 0 else 'spectrum'})")
             x = oracle_model.decoder(asr, it.f0, it.energy, it.ref_s)
-            ref, _ = oracle_model.generator_from_spec(x, g, it.ref_s)
+            ref, _ = oracle_model.generator_from_spec(x, spec_sub, it.ref_s)
         else:
             end_to_end += 1
-        _print(f"  {label} N {it.n_frames}: mag err {mag_err:.3g} phase err {np.abs(dphi[energetic]).max():.3g} "
-               f"phase-unstable bins {flips} audio snr {snr_db(ref, a):.2f} maxabs {np.abs(a - ref).max():.3g}{note}")
+        _print(f"  {label} N {it.n_frames}: source maxabs {d_har:.2g} mag err {mag_err:.3g} phase err "
+               f"{np.abs(dphi[energetic]).max():.3g} phase-unstable bins {flips} audio snr {snr_db(ref, a):.2f} "
+               f"maxabs {np.abs(a - ref).max():.3g}{note}")
         assert np.abs(a - ref).max() <= 2e-3
         assert snr_db(ref, a) >= 40.0
     return end_to_end, outs
-
-

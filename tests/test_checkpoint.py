@@ -88,6 +88,43 @@ def test_refuses_what_it_does_not_read(tmp_path):
     _expect_refusal(tmp_path / "missing.pth", ["cannot open"])
 
 
+def _patched_view(tmp_path, name, size_bytes, stride_bytes):
+    """A torch.save archive of one [8] tensor whose pickled size and stride tuples are replaced."""
+    good = tmp_path / "good8.pth"
+    torch.save({"decoder": {"w": torch.ones(8)}}, good)
+    out = tmp_path / name
+    with zipfile.ZipFile(good) as zi, zipfile.ZipFile(out, "w", zipfile.ZIP_STORED) as zo:
+        for n in zi.namelist():
+            data = zi.read(n)
+            if n.endswith("/data.pkl"):
+                # size (8,) and stride (1,): BININT1 + TUPLE1, each followed by a BINPUT of its memo slot
+                i = data.index(b"K\x08\x85q")
+                j = data.index(b"K\x01\x85q", i)
+                assert j == i + 5
+                data = data[:i] + size_bytes + data[i + 2:j] + stride_bytes + data[j + 2:]
+            zo.writestr(n, data)
+    return out
+
+
+def test_refuses_views_past_their_storage(tmp_path):
+    """A crafted size / stride must not reach past the 32-byte storage, including extents that wrap
+    int64 (the reader computes them overflow-checked, as the reference bounds every element)."""
+    def long1(v):
+        return b"\x8a\x08" + int(v).to_bytes(8, "little", signed=True)
+
+    # size 2^62 with stride 2^62: (size - 1) * stride wraps int64
+    _expect_refusal(_patched_view(tmp_path, "wrap.pth", long1(1 << 62), long1(1 << 62)), ["overflow"])
+    # size 2^40, stride 0 (an expanded view): in bounds, but beyond any tensor of the model
+    _expect_refusal(_patched_view(tmp_path, "huge.pth", long1(1 << 40), b"K\x00"), ["2^31"])
+    # negative size or stride (refused by the unpickler as non-indices already)
+    _expect_refusal(_patched_view(tmp_path, "negsize.pth", long1(-8), b"K\x01"), ["negative", "non-index"])
+    _expect_refusal(_patched_view(tmp_path, "negstride.pth", b"K\x08", long1(-1)), ["negative", "non-index"])
+    # a plain overrun: 9 elements of an 8-element storage
+    _expect_refusal(_patched_view(tmp_path, "over.pth", b"K\x09", b"K\x01"), ["past storage"])
+    # the unpatched archive reads back
+    assert np.array_equal(_read(_patched_view(tmp_path, "same.pth", b"K\x08", b"K\x01"))["decoder.w"], np.ones(8))
+
+
 def test_weight_norm():
     """The library's weight_norm equals the oracle's restatement of src/ops.rs:9-23 bit for bit, and
     torch._weight_norm within f32 rounding; a row (3, 4) has norm 5 exactly."""

@@ -8,14 +8,16 @@
   its copy in the batch.
 - Config 5 (128 items, generator frames log-uniform in [80, 4000], ~27 GiB of plan): size-
   independent properties at full size: every item finite with the right length, two items (the
-  shortest and the longest) bit-identical to runs of themselves alone, and the shortest against
-  the fp32 oracle.
+  shortest and the longest) bit-identical to runs of themselves alone, and both against the fp32
+  oracle (the longest, ~2,000 frames and 1.2 M samples, is where 64-bit offsets and long
+  overlap-add spans matter).
 """
 import numpy as np
 import pytest
 
 from conftest import snr_db
-from gpu_checks import check_vs_oracle, unstable_phase_bins
+from gpu_checks import (MAX_UNSTABLE_BINS, check_source, check_vs_oracle, classify_unstable_bins, source_tap,
+                        unstable_phase_bins)
 
 pytestmark = pytest.mark.gpu
 
@@ -25,25 +27,32 @@ def _print(*a):
 
 
 def test_config1_generator(gpu_ctx, oracle_model):
-    """End to end against the oracle, or from the GPU's own spectrum when a bin sits on atan2's
-    branch cut or a cancelled real bin (see gpu_checks.unstable_phase_bins)."""
+    """End to end against the oracle; when a bin's phase is set by rounding (atan2's branch cut or a
+    cancelled real bin, gpu_checks.classify_unstable_bins), against the oracle's generator run from
+    its own STFT of the device's source samples (gpu_checks.check_source)."""
     from kokoro_hip import api, workloads
     from oracle import oracle as O
     x, f0, style, seed = workloads.config1_generator_input()
     n = x.shape[1] // 2
-    with api.Plan.generator(gpu_ctx, [x], [f0], [style], [seed]) as plan:
+    with source_tap(), api.Plan.generator(gpu_ctx, [x], [f0], [style], [seed]) as plan:
         plan.run()
         (a,) = plan.fetch()
         g = plan.tap("spec", 0, (22, 120 * n + 1))
-    ref, spec, _ = oracle_model.generator(x, f0, style, O.rand_ini(seed), O.gen_noise(seed, 600 * n * 9), taps=True)
+        har = plan.tap("har", 0, (600 * n,))
+    ri, nz = O.rand_ini(seed), O.gen_noise(seed, 600 * n * 9)
+    spec_s, s_flips, d_har = check_source(oracle_model, f0, ri, nz, har, g)
+    ref, spec, _ = oracle_model.generator(x, f0, style, ri, nz, taps=True)
     mag_err = np.abs(g[:11] - spec[:11]).max() / max(np.abs(spec[:11]).max(), 1e-6)
     energetic = spec[:11] > 1e-4 * spec[:11].max()
     dphi = np.angle(np.exp(1j * (g[11:].astype(np.float64) - spec[11:])))
     flips = unstable_phase_bins(g, spec)
+    n_cut, n_real, n_other = classify_unstable_bins(g, spec)
     assert mag_err < 1e-4 and np.abs(dphi[energetic]).max() < 1e-3
+    assert n_other == 0 and flips <= MAX_UNSTABLE_BINS
     if flips:
-        ref, _ = oracle_model.generator_from_spec(x, g, style)
-    _print("  config 1: N", n, "phase-unstable bins", flips, "snr", snr_db(ref, a), "maxabs", np.abs(a - ref).max())
+        ref, _ = oracle_model.generator_from_spec(x, spec_s if s_flips == 0 else g, style)
+    _print("  config 1: N", n, "source maxabs", d_har, "phase-unstable bins", flips, "snr", snr_db(ref, a),
+           "maxabs", np.abs(a - ref).max())
     assert a.shape == (600 * n,)
     assert np.abs(a - ref).max() <= 2e-3
     assert snr_db(ref, a) >= 40.0
@@ -85,13 +94,11 @@ def test_config5_full_size(gpu_ctx, oracle_model):
     for it, a in zip(items, outs):
         assert a.shape == (600 * it.n_frames,) and np.isfinite(a).all()
     lo, hi = int(np.argmin(ns)), int(np.argmax(ns))
-    # the shortest item alone, against the oracle (spectrum and audio, as in the property tests)
-    _, (alone,) = check_vs_oracle(gpu_ctx, oracle_model, [items[lo]], "config 5 shortest")
-    assert np.array_equal(alone, outs[lo])
-    with api.Plan.decoder(gpu_ctx, [items[hi]]) as plan:
-        plan.run()
-        (alone,) = plan.fetch()
-    assert np.array_equal(alone, outs[hi]), f"item {hi} (N {ns[hi]})"
+    # the shortest and the longest item alone, against the oracle (source, spectrum and audio, as in
+    # the property tests), and bit-identical to their copies in the batch
+    for b, name in ((lo, "shortest"), (hi, "longest")):
+        _, (alone,) = check_vs_oracle(gpu_ctx, oracle_model, [items[b]], f"config 5 {name}")
+        assert np.array_equal(alone, outs[b]), f"item {b} (N {ns[b]})"
 
 
 def test_config3_full_size(gpu_ctx, oracle_model):
@@ -100,8 +107,8 @@ def test_config3_full_size(gpu_ctx, oracle_model):
     - every item finite with 600 N samples;
     - the shortest, the median and the longest item against the fp32 oracle at the north-star bar
       (max-abs <= 2e-3, SNR >= 40 dB) and against the bf16-emulated oracle (>= 44 dB); an item whose
-      spectrum has a phase set by rounding (gpu_checks.unstable_phase_bins) is compared through the
-      oracle's generator run from the GPU's own spectrum (see gpu_checks.check_vs_oracle);
+      spectrum has a phase set by rounding (gpu_checks.classify_unstable_bins) is compared through
+      the oracle's STFT and generator run from the device's source samples (gpu_checks.check_source);
     - the shortest and the longest item bit-identical to runs of themselves alone."""
     from kokoro_hip import api, workloads
     from oracle import oracle as O
@@ -110,27 +117,34 @@ def test_config3_full_size(gpu_ctx, oracle_model):
     _print("  config 3:", len(items), "items, frames", sum(ns))
     order = list(np.argsort(ns, kind="stable"))
     picks = [int(order[0]), int(order[len(order) // 2]), int(order[-1])]
-    with api.Plan.decoder(gpu_ctx, items) as plan:
+    with source_tap(), api.Plan.decoder(gpu_ctx, items) as plan:
         plan.run()
         outs = plan.fetch()
         specs = {b: plan.tap("spec", b, (22, 120 * ns[b] + 1)) for b in picks}
+        hars = {b: plan.tap("har", b, (600 * ns[b],)) for b in picks}
     for it, a in zip(items, outs):
         assert a.shape == (600 * it.n_frames,) and np.isfinite(a).all()
     for b in picks:
         it, a, g = items[b], outs[b], specs[b]
+        spec_s, s_flips, d_har = check_source(oracle_model, it.f0, *O.item_noise(it), hars[b], g)
+        spec_sub = spec_s if s_flips == 0 else g
         ref, spec, _ = O.synth_item(oracle_model, it, taps=True)
         with O.bf16_emulation():
             emu, _, _ = O.synth_item(oracle_model, it, taps=True)
         flips = unstable_phase_bins(g, spec)
+        n_cut, n_real, n_other = classify_unstable_bins(g, spec)
+        assert n_other == 0 and flips <= MAX_UNSTABLE_BINS
         if flips:
+            # only the source substituted (the oracle's STFT and generator from the device's samples), or
+            # the spectrum where that STFT reads a rounding-decided phase otherwise (checked above)
             asr = O.expand_tokens(it.t_en, it.dur)
             x = oracle_model.decoder(asr, it.f0, it.energy, it.ref_s)
-            ref, _ = oracle_model.generator_from_spec(x, g, it.ref_s)
+            ref, _ = oracle_model.generator_from_spec(x, spec_sub, it.ref_s)
             with O.bf16_emulation():
                 xe = oracle_model.decoder(asr, it.f0, it.energy, it.ref_s)
-                emu, _ = oracle_model.generator_from_spec(xe, g, it.ref_s)
-        _print(f"  item {b} N {ns[b]}: phase-unstable bins {flips} fp32 snr {snr_db(ref, a):.2f} "
-               f"maxabs {np.abs(a - ref).max():.3g} emu snr {snr_db(emu, a):.2f}")
+                emu, _ = oracle_model.generator_from_spec(xe, spec_sub, it.ref_s)
+        _print(f"  item {b} N {ns[b]}: source maxabs {d_har:.2g} phase-unstable bins {flips} fp32 snr "
+               f"{snr_db(ref, a):.2f} maxabs {np.abs(a - ref).max():.3g} emu snr {snr_db(emu, a):.2f}")
         assert np.abs(a - ref).max() <= 2e-3
         assert snr_db(ref, a) >= 40.0
         assert snr_db(emu, a) >= 44.0

@@ -123,7 +123,8 @@ def test_token_phase_vs_oracle(full_run, oracle_runs):
             s_plain, s_emu = snr_db(_cm(o[name]), tp[name]), snr_db(_cm(e[name]), tp[name])
             _print(f"  {name}: snr {s_plain:.1f} dB, bf16-operand emulation {s_emu:.1f} dB")
             assert s_emu >= 40.0, name
-            assert s_plain >= 25.0, name
+            # float64: 44.8-56.6 dB measured (the bf16 operand rounding itself), bar 10 dB below
+            assert s_plain >= 35.0, name
 
 
 def test_durations_vs_oracle(full_run, oracle_runs, oracle_f32_sums):
@@ -205,7 +206,10 @@ def test_prosody_vs_oracle(full_run, oracle_runs, full_weights):
                f"{np.abs(tp['f0'] - f0_g.numpy()).max():.2e} Hz), N {s_n:.1f} dB; from the oracle's own upstream: "
                f"F0 {s_f0_up:.1f} dB (oracle float64 vs bf16-operand variant: {s_f0_self:.1f} dB)")
         assert s_sh >= 40.0 and s_f0 >= 40.0 and s_n >= 40.0
-        assert s_f0_up >= 20.0
+        # from the oracle's own upstream: 29.2-33.9 dB measured, 1.3-2.3 dB above the oracle's own
+        # float64-vs-bf16 spread (27.9-31.6 dB); F0 amplifies upstream rounding (near-constant
+        # channels under InstanceNorm), so the bar is that spread, less 4 dB, and at least 24 dB
+        assert s_f0_up >= 24.0 and s_f0_up >= s_f0_self - 4.0
 
 
 def test_audio_is_the_decoder_entry_on_its_own_prosody(full_ctx, full_run):
@@ -282,6 +286,43 @@ def test_lstm_pair_wait_ends_in_an_error(full_ctx, full_run):
     res = full_ctx.forward_batch(items)
     for (a, d), a2, d2 in zip(res, audio, durs):
         assert np.array_equal(d, d2) and np.array_equal(a, a2)
+
+
+def test_lstm_abort_fails_every_result_path(full_ctx, full_run):
+    """A plan rerun whose recurrence gives up (KOKORO_HIP_TEST_LSTM_SILENT=1, read at each run) leaves
+    h rows of the previous run behind, so every path that hands results back -- sync, fetch,
+    fetch_pcm16, the asynchronous fetch's wait, taps -- fails with KK_ERR_HIP instead of returning
+    that stale audio; the next run without the hook gives the first run's audio again."""
+    from kokoro_hip import api
+    items, audio, durs, _ = full_run
+    with api.Plan.full(full_ctx, items) as plan:
+        plan.run()
+        first = plan.fetch()
+        T0 = len(items[0].ids)
+        os.environ["KOKORO_HIP_TEST_LSTM_SILENT"] = "1"
+        try:
+            plan.run()
+        finally:
+            del os.environ["KOKORO_HIP_TEST_LSTM_SILENT"]
+        calls = [("sync", plan.sync), ("fetch", plan.fetch), ("fetch_pcm16", plan.fetch_pcm16),
+                 ("tap", lambda: plan.tap("t_en", 0, (512, T0)))]
+        for name, call in calls:
+            with pytest.raises(api.KKError) as e:
+                call()
+            assert e.value.code == api.KK_ERR_HIP and "partner" in str(e.value), name
+        # the pinned destination covers the plan's whole sample layout (gaps of 2 frames included)
+        pcm = api.PinnedArray(full_ctx, 600 * sum(int(d.sum()) + 2 for d in durs), np.int16)
+        try:
+            plan.fetch_pcm16_async(pcm)
+            with pytest.raises(api.KKError) as e:
+                plan.fetch_wait()
+            assert e.value.code == api.KK_ERR_HIP and "partner" in str(e.value)
+        finally:
+            pcm.free()
+        plan.run()
+        again = plan.fetch()
+        for a, a2 in zip(again, first):
+            assert np.array_equal(a, a2)
 
 
 _SINGLE_LSTM_SCRIPT = """
