@@ -14,7 +14,7 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIBDIR = os.path.join(HERE, "lib")
 LIB = os.path.join(LIBDIR, "libkokoro_hip.so")
-SOURCES = ["kk_conv.hip", "kk_misc.hip", "kk_engine.hip", "kk_ckpt.hip", "kk_upstream.hip"]
+SOURCES = ["kk_conv.hip", "kk_misc.hip", "kk_engine.hip", "kk_ckpt.hip", "kk_upstream.hip", "kk_host.cpp"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [

@@ -23,6 +23,9 @@ struct HostTensor {
 std::map<std::string, HostTensor> read_model_checkpoint(const std::string& path);
 // Voice pack: a single tensor of shape [rows, 1, 256] (src/torchpt.rs:329-335).
 HostTensor read_voice_pack(const std::string& path);
+// The same from an archive already in memory (`path` names it in messages).
+std::map<std::string, HostTensor> read_model_checkpoint_bytes(std::vector<uint8_t> data, const std::string& path);
+HostTensor read_voice_pack_bytes(std::vector<uint8_t> data, const std::string& path);
 
 // torch._weight_norm(v, g, dim = 0): w = v * (g / ||v||), the norm over all but the first dim,
 // summed in f64 (src/ops.rs:9-23).

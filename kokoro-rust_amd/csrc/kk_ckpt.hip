@@ -296,7 +296,8 @@ struct Loader {
     std::string prefix;  // "<archive name>/"
     VP root;
 
-    explicit Loader(const std::string& path) : bytes(read_file(path)) {
+    // path: the file's name in messages (the archive is `data`, read from it or handed over)
+    Loader(std::vector<uint8_t> data, const std::string& path) : bytes(std::move(data)) {
         zip = std::make_unique<Archive>(bytes);
         std::string pkl;
         for (auto& e : zip->entries) {
@@ -336,7 +337,7 @@ struct Loader {
                 (n > 0 && (__builtin_mul_overflow(n - 1, st, &span) || __builtin_add_overflow(last, span, &last))))
                 bad("tensor view of " + v->s + ": size overflows");
         }
-        if (numel > ((int64_t)1 << 31)) bad("tensor view of " + v->s + ": more than 2^31 elements");
+        if (numel > ((int64_t)1 << 28)) bad("tensor view of " + v->s + ": more than 2^28 elements");
         if (numel > 0 && last >= total) bad("tensor view runs past storage " + v->s);
         t.data.resize((size_t)numel);
         auto at = [&](int64_t k) {
@@ -377,8 +378,8 @@ const std::string& key_str(const VP& k) {
 
 }  // namespace
 
-std::map<std::string, HostTensor> read_model_checkpoint(const std::string& path) {
-    Loader ld(path);
+std::map<std::string, HostTensor> read_model_checkpoint_bytes(std::vector<uint8_t> data, const std::string& path) {
+    Loader ld(std::move(data), path);
     if (ld.root->kind != K_DICT) bad(path + ": the root object is not a dict of state dicts");
     std::map<std::string, HostTensor> out;
     for (auto& kv : ld.root->dict) {
@@ -393,8 +394,12 @@ std::map<std::string, HostTensor> read_model_checkpoint(const std::string& path)
     return out;
 }
 
-HostTensor read_voice_pack(const std::string& path) {
-    Loader ld(path);
+std::map<std::string, HostTensor> read_model_checkpoint(const std::string& path) {
+    return read_model_checkpoint_bytes(read_file(path), path);
+}
+
+HostTensor read_voice_pack_bytes(std::vector<uint8_t> data, const std::string& path) {
+    Loader ld(std::move(data), path);
     HostTensor t = ld.tensor(ld.root);
     if (t.shape.size() != 3 || t.shape[1] != 1 || t.shape[2] != 256) {
         std::string s;
@@ -403,6 +408,8 @@ HostTensor read_voice_pack(const std::string& path) {
     }
     return t;
 }
+
+HostTensor read_voice_pack(const std::string& path) { return read_voice_pack_bytes(read_file(path), path); }
 
 void weight_norm(const float* v, const float* g, int64_t rows, int64_t per_row, float* w) {
     for (int64_t r = 0; r < rows; r++) {

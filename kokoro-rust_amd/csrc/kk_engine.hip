@@ -22,6 +22,7 @@
 
 #include "kk_ckpt.h"
 #include "kk_common.h"
+#include "kk_host.h"
 #include "kk_kernels.h"
 #include "kokoro_hip.h"
 
@@ -840,8 +841,6 @@ struct kk_plan {
 
 namespace kk {
 
-constexpr int kGapN = 2;  // GAP_N (src/gpu_batch.rs:27)
-constexpr int kGapT = 2;  // GAP_T (src/gpu_batch.rs:29)
 constexpr int64_t kXcatLd = 576, kXinLd = 1152, kSpecLd = 32, kPostLd = 32;
 
 // A plan buffer.  Every element a run reads was written earlier in the same run (convolutions and
@@ -2113,15 +2112,9 @@ static void init_full_plan(kk_plan* p, const kk_item* items, int n) {
     p->tstart.assign(n, 0), p->ntok.assign(n, 0);
     for (int b = 0; b < n; b++) {
         const kk_item& it = items[b];
-        const std::string sb = std::to_string(b);
         // src/gpu_batch.rs:182-187
-        check(it.ids != nullptr && it.ref_s != nullptr, "item " + sb + ": null input");
-        check(it.n_ids >= 2 && it.n_ids <= 512, "item " + sb + ": input_ids length outside [2, 512]");
-        check(std::isfinite(it.speed) && it.speed > 0.f, "item " + sb + ": speed must be positive and finite");
-        for (int i = 0; i < it.n_ids; i++)  // the message is built only for a failing id
-            if (it.ids[i] < 0 || it.ids[i] >= 178)
-                check(false, "item " + sb + ": token id " + std::to_string(it.ids[i]) + " out of range");
-        check(it.noise_kind == KK_NOISE_COUNTER || it.noise_kind == KK_NOISE_FIXED, "item " + sb + ": unknown noise kind");
+        const std::string e = ids_item_error(it, b);
+        check(e.empty(), e);
         p->tstart[b] = rows, p->ntok[b] = it.n_ids;
         rows += it.n_ids + kGapT;
     }
@@ -3314,61 +3307,6 @@ int kk_profile_launches(kk_ctx* ctx, kk_launch_record* out, int max, int* n_out,
         }
         *n_out = k;
     });
-}
-
-int kk_durations_from_logits(const float* logits, int t, float speed, int64_t* out) {
-    if (!logits || !out || t < 0 || !(speed > 0.f) || !std::isfinite(speed)) return KK_ERR_INVALID;
-    // src/model.rs:90-99 with src/ops.rs:49-51: f32 sigmoid, left-to-right f32 sum, ties to even
-    for (int i = 0; i < t; i++) {
-        float s = 0.f;
-        for (int j = 0; j < 50; j++) {
-            volatile float e = std::exp(-logits[i * 50 + j]);
-            s = s + 1.0f / (1.0f + (float)e);
-        }
-        const float d = std::nearbyint(s / speed);
-        const int64_t di = (int64_t)d;
-        out[i] = di < 1 ? 1 : di;
-    }
-    return KK_OK;
-}
-
-int64_t kk_layout_frames(const int64_t* nfs, int n, int64_t* a_out) {
-    if (!nfs || !a_out || n <= 0) return KK_ERR_INVALID;
-    int64_t ln = 0;
-    for (int b = 0; b < n; b++) {
-        if (nfs[b] < 0) return KK_ERR_INVALID;
-        a_out[b] = ln;
-        ln += nfs[b] + kGapN;
-    }
-    return ln;
-}
-
-int kk_layout_col_item(int64_t l, const int64_t* start, const int64_t* len, int n, int32_t* col_item) {
-    if (!start || !len || !col_item || l < 0) return KK_ERR_INVALID;
-    for (int64_t t = 0; t < l; t++) col_item[t] = -1;
-    for (int b = 0; b < n; b++) {
-        if (start[b] < 0 || len[b] < 0 || start[b] + len[b] > l) return KK_ERR_INVALID;
-        for (int64_t t = start[b]; t < start[b] + len[b]; t++) {
-            if (col_item[t] >= 0) return KK_ERR_INVALID;
-            col_item[t] = b;
-        }
-    }
-    return KK_OK;
-}
-
-int kk_layout_src_row(const int64_t* const* dur, const int32_t* n_tok, int n, const int64_t* tstart, const int64_t* a,
-                      int64_t ln, int32_t* src_row) {
-    if (!dur || !n_tok || !tstart || !a || !src_row) return KK_ERR_INVALID;
-    for (int64_t t = 0; t < ln; t++) src_row[t] = -1;
-    for (int b = 0; b < n; b++) {
-        int64_t f = a[b];
-        for (int tok = 0; tok < n_tok[b]; tok++)
-            for (int64_t r = 0; r < dur[b][tok]; r++) {
-                if (f >= ln) return KK_ERR_INVALID;
-                src_row[f++] = (int32_t)(tstart[b] + tok);
-            }
-    }
-    return KK_OK;
 }
 
 }  // extern "C"

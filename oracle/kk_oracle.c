@@ -146,7 +146,8 @@ void ko_durations_from_logits(const float* logits, int t, float speed, int64_t* 
             s = s + 1.0f / (1.0f + expf(-v));
         }
         float d = nearbyintf(s / speed); /* default rounding mode: to nearest, ties to even */
-        int64_t di = (int64_t)d;
+        /* `d as i64` saturates in Rust (src/model.rs:96): NaN -> 0, at or past 2^63 -> i64::MAX */
+        int64_t di = isnan(d) ? 0 : d >= 9.223372036854775808e18f ? INT64_MAX : (int64_t)d;
         out[i] = di < 1 ? 1 : di;
     }
 }

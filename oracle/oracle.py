@@ -12,7 +12,8 @@ import struct
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libkk_oracle.so")
+# KK_ORACLE_LIB: another build of the same source (the sanitizer test loads an ASan + UBSan build)
+LIB_PATH = os.environ.get("KK_ORACLE_LIB") or os.path.join(HERE, "libkk_oracle.so")
 
 _f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
 _i64p = np.ctypeslib.ndpointer(np.int64, flags="C_CONTIGUOUS")

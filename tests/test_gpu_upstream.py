@@ -518,6 +518,39 @@ def test_refusals(full_ctx, gpu_ctx):
     assert "stages before the decoder" in str(e.value)
 
 
+def test_fixed_noise_replay_at_ids_level(full_ctx, full_run):
+    """ItemNoise::Fixed through the whole forward_batch, as the reference's BF16x replay test passes
+    it (tests/bf16x_reference.rs:72-74): each item's counter noise expanded on the host (the oracle's
+    splitmix64 + Box-Muller: rand_ini and 600 N x 9 sine-branch samples for the item's predicted N)
+    and handed over as fixed noise gives audio and durations bit-identical to the counter-noise run,
+    items of both kinds mixed in one batch; a sine buffer that does not fit the predicted N is
+    refused with KK_ERR_INVALID (src/gpu_batch.rs:336-339), and the context stays usable."""
+    from kokoro_hip import api, workloads
+    from oracle import oracle as O
+    items, audio, durs, _ = full_run
+    fixed = []
+    for b, (it, d) in enumerate(zip(items, durs)):
+        n = int(d.sum())
+        if b == 1:  # one item keeps its counter noise
+            fixed.append(it)
+            continue
+        fixed.append(workloads.IdsItem(ids=it.ids, ref_s=it.ref_s, seed=it.seed + 1000, speed=it.speed,
+                                       rand_ini=O.rand_ini(it.seed), sine=O.gen_noise(it.seed, 600 * n * 9)))
+    res = full_ctx.forward_batch(fixed)
+    for (a, d), a2, d2 in zip(res, audio, durs):
+        assert np.array_equal(d, d2) and np.array_equal(a, a2)
+    n0 = int(durs[0].sum())
+    for n_sine in (600 * n0 * 9 - 9, 600 * (n0 + 1) * 9):
+        wrong = workloads.IdsItem(ids=items[0].ids, ref_s=items[0].ref_s, seed=1, speed=items[0].speed,
+                                  rand_ini=O.rand_ini(1), sine=np.zeros(n_sine, np.float32))
+        with pytest.raises(api.KKError) as e:
+            full_ctx.forward_batch([wrong, items[2]])
+        assert e.value.code == api.KK_ERR_INVALID and "noise" in str(e.value).lower(), str(e.value)
+    res = full_ctx.forward_batch(items)
+    for (a, d), a2, d2 in zip(res, audio, durs):
+        assert np.array_equal(d, d2) and np.array_equal(a, a2)
+
+
 def test_config4_full_size(full_ctx, full_weights, oracle_model):
     """BASELINE config 4 at full size: 64 items of 20-510 phoneme ids uniform over the vocabulary.
 

@@ -41,6 +41,16 @@ def test_durations_bit_exact():
         assert np.array_equal(api.durations_from_logits(lg, speed), O.durations_from_logits(lg, speed))
     z = np.zeros((4, 50), np.float32)
     assert list(api.durations_from_logits(z, 2.0)) == [12] * 4  # 12.5 -> 12 (ties to even)
+    # Rust's saturating `as i64` (src/model.rs:96): a NaN sum -> 0 -> clamped to 1; a sum past 2^63
+    # (a tiny speed) -> i64::MAX; -inf logits give a sum of 0 -> 1
+    odd = np.zeros((3, 50), np.float32)
+    odd[0, 7] = np.nan
+    odd[2, :] = -np.inf
+    for speed in (1.0, 1e-30):
+        got = api.durations_from_logits(odd, speed)
+        assert np.array_equal(got, O.durations_from_logits(odd, speed))
+    assert list(api.durations_from_logits(odd, 1.0)) == [1, 25, 1]
+    assert list(api.durations_from_logits(odd, 1e-30)) == [1, 2**63 - 1, 1]
 
 
 def test_layout_bit_exact():
