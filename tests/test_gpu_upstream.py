@@ -518,27 +518,45 @@ def test_refusals(full_ctx, gpu_ctx):
     assert "stages before the decoder" in str(e.value)
 
 
-def test_fixed_noise_replay_at_ids_level(full_ctx, full_run):
+def test_fixed_noise_replay_at_ids_level(full_ctx, full_run, oracle_model):
     """ItemNoise::Fixed through the whole forward_batch, as the reference's BF16x replay test passes
     it (tests/bf16x_reference.rs:72-74): each item's counter noise expanded on the host (the oracle's
     splitmix64 + Box-Muller: rand_ini and 600 N x 9 sine-branch samples for the item's predicted N)
-    and handed over as fixed noise gives audio and durations bit-identical to the counter-noise run,
-    items of both kinds mixed in one batch; a sine buffer that does not fit the predicted N is
-    refused with KK_ERR_INVALID (src/gpu_batch.rs:336-339), and the context stays usable."""
+    and handed over as fixed noise, items of both kinds mixed in one batch.
+    - durations equal to the counter-noise run's (the noise enters after them);
+    - audio bit-identical to the decoder entry's on the call's own t_en, F0 and N with the same
+      fixed noise (the ids-level plumbing of the noise), and against the oracle on those inputs at
+      the north-star bar;
+    - against the counter-noise run at the north-star bar (max-abs <= 2e-3, >= 40 dB; 48 dB
+      measured): the same noise up to the host and device libm's last-bit differences in the
+      Box-Muller cos / log, the difference every GPU-vs-oracle comparison of counter noise carries;
+    - a sine buffer that does not fit the predicted N is refused with KK_ERR_INVALID
+      (src/gpu_batch.rs:336-339), and the context stays usable."""
+    from gpu_checks import check_vs_oracle
     from kokoro_hip import api, workloads
     from oracle import oracle as O
-    items, audio, durs, _ = full_run
-    fixed = []
-    for b, (it, d) in enumerate(zip(items, durs)):
+    items, audio, durs, taps = full_run
+    fixed, dec = [], []
+    for b, (it, d, tp) in enumerate(zip(items, durs, taps)):
         n = int(d.sum())
-        if b == 1:  # one item keeps its counter noise
-            fixed.append(it)
-            continue
-        fixed.append(workloads.IdsItem(ids=it.ids, ref_s=it.ref_s, seed=it.seed + 1000, speed=it.speed,
-                                       rand_ini=O.rand_ini(it.seed), sine=O.gen_noise(it.seed, 600 * n * 9)))
+        ri, sn = (None, None) if b == 1 else (O.rand_ini(it.seed), O.gen_noise(it.seed, 600 * n * 9))
+        # item 1 keeps its counter noise
+        fixed.append(it if b == 1 else workloads.IdsItem(ids=it.ids, ref_s=it.ref_s, seed=it.seed + 1000,
+                                                         speed=it.speed, rand_ini=ri, sine=sn))
+        dec.append(workloads.DecoderItem(dur=d, t_en=tp["t_en"], f0=tp["f0"], energy=tp["n"], ref_s=it.ref_s,
+                                         seed=it.seed, rand_ini=ri, sine=sn))
     res = full_ctx.forward_batch(fixed)
-    for (a, d), a2, d2 in zip(res, audio, durs):
-        assert np.array_equal(d, d2) and np.array_equal(a, a2)
+    ref = full_ctx.forward_decoder_batch(dec)
+    for b, ((a, d), a_ctr, d_ctr, r) in enumerate(zip(res, audio, durs, ref)):
+        assert np.array_equal(d, d_ctr), b
+        assert np.array_equal(a, r), b
+        s = snr_db(a_ctr, a)
+        _print(f"  item {b}: fixed noise vs counter noise {s:.1f} dB (max diff {np.abs(a - a_ctr).max():.2e})")
+        if b == 1:
+            assert np.array_equal(a, a_ctr)
+        else:
+            assert s >= 40.0 and np.abs(a - a_ctr).max() <= 2e-3
+    check_vs_oracle(full_ctx, oracle_model, [dec[0], dec[2]], "ids-level fixed noise")
     n0 = int(durs[0].sum())
     for n_sine in (600 * n0 * 9 - 9, 600 * (n0 + 1) * 9):
         wrong = workloads.IdsItem(ids=items[0].ids, ref_s=items[0].ref_s, seed=1, speed=items[0].speed,
