@@ -179,10 +179,13 @@ typedef struct {
  * back), then the frame layout, the shared LSTM, the F0 / N stacks, the decoder, the generator and
  * the iSTFT.  Results in input order.  Kept buffers, failure release and test hooks as
  * kk_forward_decoder_batch.  Every BiLSTM recurrence runs each (item, direction) on a pair of CUs
- * that trade their halves of h each step; a block that waits more than 2 s for its partner ends
- * its launch and the call fails with KK_ERR_HIP (KOKORO_HIP_LSTM_SINGLE=1, read once per process,
- * selects the one-CU kernel instead; test hook KOKORO_HIP_TEST_LSTM_SILENT=1, read at each launch,
- * forces that failure with a 10 us wait).  ALBERT's attention runs on the f32 matrix cores;
+ * that trade their halves of h each step; a block that waits more than 2 s for its partner (held
+ * off its CU, e.g. by another process) ends its launch, and the call runs the forward again with
+ * the one-CU kernel, which waits on no other block -- contention costs time, not an error (an
+ * ids-level plan stays on the one-CU kernel for its later runs; every result path, kk_plan_sync
+ * and taps included, runs that check first).  KOKORO_HIP_LSTM_SINGLE=1 (read once per process)
+ * selects the one-CU kernel from the start; test hook KOKORO_HIP_TEST_LSTM_SILENT=1 (read at each
+ * launch) makes every pair give up after a 10 us wait.  ALBERT's attention runs on the f32 matrix cores;
  * KOKORO_HIP_ATTENTION_VALU=1 (read once per process) selects the f32 VALU kernel instead. */
 int kk_forward_batch(kk_ctx* ctx, const kk_item* items, int n, kk_result* out, char* err, size_t errlen);
 void kk_result_free(kk_result* out, int n);

@@ -735,6 +735,9 @@ struct kk_plan {
     kk::Dom dn, d2, d20, d120, ds;
     // test hooks read at plan creation (see apply_test_hooks)
     bool nomask = false, poison = false, tap_source = false;
+    // the recurrences on the one-CU kernel: set once a two-CU pair of this plan gave up (the plan's
+    // later runs stay there), reset for each new batch
+    bool lstm_single = false;
     // snake plans
     const kk::MSnake* sblk = nullptr;
     int sc = 0;
@@ -795,6 +798,8 @@ struct kk_plan {
     // kk_plan_fetch_pcm16_async: recorded after its copies; pending until kk_plan_fetch_wait
     hipEvent_t fetch_ev = nullptr;
     bool fetch_pending = false;
+    int16_t* fetch_dst = nullptr;  // the pending fetch's destinations (a fallback run fetches again)
+    int64_t* fetch_clipped = nullptr;
     void drop_events() {
         if (fetch_ev) (void)hipEventDestroy(fetch_ev);
         fetch_ev = nullptr, fetch_pending = false;
@@ -891,6 +896,7 @@ static void reset_plan(kk_plan* p, int kind, int n) {
     p->ln = 0, p->t_rows = 0, p->n_src = p->n_ist = 0;
     p->conv_flop = p->snake_flop = 0, p->launches = 0, p->last_until = -1;
     p->fetch_pending = false;
+    p->lstm_single = false;
     apply_test_hooks(p, n);
 }
 
@@ -1786,9 +1792,9 @@ struct Runner {
     // h into out[row][0:512].  Algorithmic traffic: gx read and h written once per row, W_hh once.
     // Each sequence runs on two CUs (launch_lstm_pair) with its exchange words in `region` (one per
     // stream that runs recurrences at the same time); KOKORO_HIP_LSTM_SINGLE=1 selects the one-CU
-    // kernel (W_hh partly streamed from L2 each step).  Test hook, read at each launch:
-    // KOKORO_HIP_TEST_LSTM_SILENT=1 keeps the second half of every pair from publishing and cuts the
-    // wait to 10 us, so that the run ends with the pair kernel's abort.
+    // kernel (W_hh partly streamed from L2 each step), as does a plan whose pairs gave up before
+    // (lstm_single).  Test hook, read at each launch: KOKORO_HIP_TEST_LSTM_SILENT=1 keeps the second
+    // half of every pair from publishing and cuts the wait to 10 us, so that the pairs give up.
     void recur(const MLstm& l, const float* gx, const int32_t* gx_row, const Dom& d, float* out, int64_t out_ld,
                const std::string& name, int region = 0) {
         static const bool single = env_i64("KOKORO_HIP_LSTM_SINGLE", 0) != 0;
@@ -1796,7 +1802,7 @@ struct Runner {
         const double v = (double)d.valid();
         label = name;
         launch(PC_LSTM, v * 2 * 1024 * 256 * 2, v * (2048 + 512) * 4 + 2.0 * 1024 * 257 * 4, [&] {
-            if (single)
+            if (single || p->lstm_single)
                 return launch_lstm(gx, 2048, gx_row, d.start_d.as<int64_t>(), d.len_d.as<int64_t>(), p->nb,
                                    l.whh_t.as<float>(), l.bhh.as<float>(), out, out_ld, s);
             uint64_t* x = p->u_lstmx.as<uint64_t>();
@@ -2089,14 +2095,28 @@ static void check_lstm_abort(kk_plan* p) {
                           "(set KOKORO_HIP_LSTM_SINGLE=1 for the one-CU kernel)");
 }
 
-// Every path that hands an ids-level plan's results to the caller (audio, PCM, taps, sync) drains the
-// stream and fails if a recurrence of the last run gave up: its h rows would hold an earlier run's
-// values.  Plans of the other kinds run no recurrence.
-static void drain_and_check_abort(kk_plan* p) {
+static void run_plan(kk_plan* plan, int until, bool skip_tokens = false);
+
+// Drains the stream and reads back the run's abort flag (ids-level plans).
+static bool drain_aborted(kk_plan* p) {
     hipStream_t s = p->ctx->stream;
-    if (p->kind == PLAN_FULL && p->abort_host)
-        KK_HIP(hipMemcpyAsync(p->abort_host, p->u_lstmx.p, sizeof(uint64_t), hipMemcpyDeviceToHost, s));
+    const bool full = p->kind == PLAN_FULL && p->abort_host;
+    if (full) KK_HIP(hipMemcpyAsync(p->abort_host, p->u_lstmx.p, sizeof(uint64_t), hipMemcpyDeviceToHost, s));
     KK_HIP(hipStreamSynchronize(s));
+    return full && *p->abort_host != 0;
+}
+
+// Every path that hands an ids-level plan's results to the caller (audio, PCM, taps, sync) drains the
+// stream and checks that no recurrence of the last run gave up (its h rows would hold an earlier
+// run's values).  If one did -- a two-CU pair whose partner was held off its CU past the 2 s bound,
+// e.g. by another process -- the plan switches to the one-CU kernel, which waits on no other block,
+// and runs again: contention costs time, not an error.  Plans of the other kinds run no recurrence.
+static void drain_and_check_abort(kk_plan* p) {
+    if (drain_aborted(p) && !p->lstm_single) {
+        p->lstm_single = true;
+        run_plan(p, p->last_until);
+        drain_aborted(p);
+    }
     if (p->kind == PLAN_FULL) check_lstm_abort(p);
 }
 
@@ -2187,9 +2207,17 @@ static void init_full_plan(kk_plan* p, const kk_item* items, int n) {
         KK_HIP(hipHostMalloc((void**)&p->logits_host, lg_bytes, hipHostMallocDefault));
         p->logits_cap = lg_bytes;
     }
-    KK_HIP(hipMemcpyAsync(p->logits_host, p->u_logits.p, lg_bytes, hipMemcpyDeviceToHost, ctx->stream));
-    KK_HIP(hipMemcpyAsync(p->abort_host, p->u_lstmx.p, sizeof(uint64_t), hipMemcpyDeviceToHost, ctx->stream));
-    KK_HIP(hipStreamSynchronize(ctx->stream));
+    for (int attempt = 0;; attempt++) {
+        KK_HIP(hipMemcpyAsync(p->logits_host, p->u_logits.p, lg_bytes, hipMemcpyDeviceToHost, ctx->stream));
+        KK_HIP(hipMemcpyAsync(p->abort_host, p->u_lstmx.p, sizeof(uint64_t), hipMemcpyDeviceToHost, ctx->stream));
+        KK_HIP(hipStreamSynchronize(ctx->stream));
+        if (*p->abort_host == 0 || attempt > 0 || p->lstm_single) break;
+        // a two-CU pair gave up: the token phase again with the one-CU recurrences (see
+        // drain_and_check_abort)
+        p->lstm_single = true;
+        Runner r{p, ctx, m, ctx->stream};
+        r.tokens();
+    }
     check_lstm_abort(p);
     pm.mark("token device");
     // durations_from_logits (src/model.rs:90-100) per item, the items spread over a few host
@@ -2464,7 +2492,7 @@ static_assert(kNaTotal <= KK_NOALLOC_SCRATCH_BYTES, "scratch regions exceed the 
 static __device__ __align__(256) unsigned char scratch[KK_NOALLOC_SCRATCH_BYTES];
 
 namespace kk {
-static void run_plan(kk_plan* plan, int until, bool skip_tokens = false) {
+static void run_plan(kk_plan* plan, int until, bool skip_tokens) {
     use_device(plan->ctx);
     check(plan->ctx->model.ready, "no model uploaded");
     check(plan->kind != PLAN_FULL || plan->ctx->model.up.ready, "no model with the stages before the decoder uploaded");
@@ -2846,8 +2874,11 @@ static void fetch_plan(kk_plan* plan, kk_output* out, float* blk = nullptr) {
         blk = (float*)out_block_take(bytes, plan->nb);
         for (int b = 0; b < plan->nb; b++) out[b] = kk_output{blk + 600 * plan->a[b], 600 * plan->nfr[b]};
     }
+    // ids-level plans: the run checked (and run again on the one-CU recurrences if a pair gave up)
+    // before its audio is copied; the one-shot run's early copies are issued again by that rerun
+    if (plan->kind == PLAN_FULL) drain_and_check_abort(plan);
     if (!plan->early_issued) KK_HIP(hipMemcpyAsync(blk, plan->audio.p, bytes, hipMemcpyDeviceToHost, s));
-    drain_and_check_abort(plan);
+    KK_HIP(hipStreamSynchronize(s));
     if (plan->early_issued) {
         KK_HIP(hipEventSynchronize(plan->out_ev[kk_plan::kOutGroups]));
         plan->early_issued = false;
@@ -2889,11 +2920,12 @@ int kk_plan_fetch_pcm16(kk_plan* plan, int16_t* const* dst, int64_t* clipped, ch
         check(plan->last_until >= KK_STAGE_ALL, "plan has not run to the end");
         for (int b = 0; b < plan->nb; b++) check(dst[b] != nullptr, "null destination for item " + std::to_string(b));
         hipStream_t s = plan->ctx->stream;
+        if (plan->kind == PLAN_FULL) drain_and_check_abort(plan);
         KK_HIP(launch_zero(plan->pcm_clip.p, (int64_t)plan->nb * 8, s));
         KK_HIP(launch_pcm16(plan->audio.as<float>(), plan->audio_start.as<int64_t>(), plan->pcm_len.as<int64_t>(),
                             plan->ist_item.as<int64_t>(), plan->ist_s0.as<int64_t>(), plan->n_ist,
                             plan->pcm.as<int16_t>(), plan->pcm_clip.as<unsigned long long>(), s));
-        drain_and_check_abort(plan);
+        KK_HIP(hipStreamSynchronize(s));
         for (int b = 0; b < plan->nb; b++)
             KK_HIP(hipMemcpy(dst[b], plan->pcm.as<int16_t>() + 600 * plan->a[b], sizeof(int16_t) * 600 * plan->nfr[b],
                              hipMemcpyDeviceToHost));
@@ -2950,6 +2982,18 @@ int kk_plan_item_samples(const kk_plan* plan, int item, int64_t* offset, int64_t
     return KK_OK;
 }
 
+// The PCM_16 encoding of the whole sample layout and its copies into pinned dst / clipped (or null).
+static void enqueue_pcm16_fetch(kk_plan* plan, int16_t* dst, int64_t* clipped) {
+    hipStream_t s = plan->ctx->stream;
+    KK_HIP(launch_zero(plan->pcm_clip.p, (int64_t)plan->nb * 8, s));
+    KK_HIP(launch_pcm16(plan->audio.as<float>(), plan->audio_start.as<int64_t>(), plan->pcm_len.as<int64_t>(),
+                        plan->ist_item.as<int64_t>(), plan->ist_s0.as<int64_t>(), plan->n_ist, plan->pcm.as<int16_t>(),
+                        plan->pcm_clip.as<unsigned long long>(), s));
+    KK_HIP(hipMemcpyAsync(dst, plan->pcm.p, sizeof(int16_t) * 600 * (size_t)plan->ln, hipMemcpyDeviceToHost, s));
+    if (clipped)
+        KK_HIP(hipMemcpyAsync(clipped, plan->pcm_clip.p, sizeof(int64_t) * plan->nb, hipMemcpyDeviceToHost, s));
+}
+
 int kk_plan_fetch_pcm16_async(kk_plan* plan, int16_t* dst, int64_t* clipped, char* err, size_t errlen) {
     if (!plan || !dst) return KK_ERR_INVALID;
     if (!plan->ctx) {
@@ -2968,16 +3012,12 @@ int kk_plan_fetch_pcm16_async(kk_plan* plan, int16_t* dst, int64_t* clipped, cha
               "clipped must be pinned memory from kk_host_alloc");
         hipStream_t s = plan->ctx->stream;
         if (!plan->fetch_ev) KK_HIP(hipEventCreateWithFlags(&plan->fetch_ev, hipEventDisableTiming));
-        KK_HIP(launch_zero(plan->pcm_clip.p, (int64_t)plan->nb * 8, s));
-        KK_HIP(launch_pcm16(plan->audio.as<float>(), plan->audio_start.as<int64_t>(), plan->pcm_len.as<int64_t>(),
-                            plan->ist_item.as<int64_t>(), plan->ist_s0.as<int64_t>(), plan->n_ist,
-                            plan->pcm.as<int16_t>(), plan->pcm_clip.as<unsigned long long>(), s));
-        KK_HIP(hipMemcpyAsync(dst, plan->pcm.p, pcm_bytes, hipMemcpyDeviceToHost, s));
-        if (clipped)
-            KK_HIP(hipMemcpyAsync(clipped, plan->pcm_clip.p, sizeof(int64_t) * plan->nb, hipMemcpyDeviceToHost, s));
+        enqueue_pcm16_fetch(plan, dst, clipped);
+        // ids-level plans: the run's abort flag comes back with the samples; kk_plan_fetch_wait checks it
         if (plan->kind == PLAN_FULL && plan->abort_host)
             KK_HIP(hipMemcpyAsync(plan->abort_host, plan->u_lstmx.p, sizeof(uint64_t), hipMemcpyDeviceToHost, s));
         KK_HIP(hipEventRecord(plan->fetch_ev, s));
+        plan->fetch_dst = dst, plan->fetch_clipped = clipped;
         plan->fetch_pending = true;
     });
 }
@@ -2993,7 +3033,15 @@ int kk_plan_fetch_wait(kk_plan* plan, char* err, size_t errlen) {
         use_device(plan->ctx);
         plan->fetch_pending = false;
         KK_HIP(hipEventSynchronize(plan->fetch_ev));
-        if (plan->kind == PLAN_FULL) check_lstm_abort(plan);  // the run's abort flag came with the samples
+        if (plan->kind == PLAN_FULL && plan->abort_host && *plan->abort_host != 0 && !plan->lstm_single) {
+            // a two-CU pair of the run gave up: the run again on the one-CU recurrences (see
+            // drain_and_check_abort), its samples into the same destination
+            plan->lstm_single = true;
+            run_plan(plan, plan->last_until);
+            enqueue_pcm16_fetch(plan, plan->fetch_dst, plan->fetch_clipped);
+            drain_aborted(plan);
+        }
+        if (plan->kind == PLAN_FULL) check_lstm_abort(plan);
     });
 }
 
