@@ -11,7 +11,8 @@ import os
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(os.path.dirname(HERE), "lib", "libkokoro_hip.so")
+# KK_LIB: another build of the same sources (A/B measurements of two builds on one GPU box)
+LIB_PATH = os.environ.get("KK_LIB") or os.path.join(os.path.dirname(HERE), "lib", "libkokoro_hip.so")
 
 KK_OK = 0
 KK_ERR_INVALID, KK_ERR_HIP, KK_ERR_OOM, KK_ERR_STATE = -1, -2, -3, -4

@@ -1,11 +1,12 @@
 """Summaries of rocprofv3 output for bench.py runs of the config-3 workload.
 
-    python -m kokoro_hip.profsum stats <trace_dir> <steps>
+    python -m kokoro_hip.profsum stats <trace_dir> <steps> [<trailing>]
         per-kernel table from a `rocprofv3 --kernel-trace` CSV run of bench.py, plus the average
-        Snake-block conv duration of its profiling pass (the last <steps> steps)
-    python -m kokoro_hip.profsum serial <trace_dir> <steps>
-        per-kernel table of the trace's last <steps> runs alone (bench.py's profiling pass, every
-        kernel alone on one stream), for any workload whose runs end with the iSTFT
+        Snake-block conv duration of its profiling pass (<steps> runs, followed by <trailing> other
+        runs: 1 for bench.py's config-3 leg, whose parity leg runs a plan once more)
+    python -m kokoro_hip.profsum serial <trace_dir> <steps> [<trailing>]
+        per-kernel table of bench.py's profiling pass alone (<steps> runs before the trace's last
+        <trailing>, every kernel alone on one stream), for any workload whose runs end with the iSTFT
     python -m kokoro_hip.profsum kernels <trace_dir>
         per-kernel table (calls, total, average, share) of any `rocprofv3 --kernel-trace --stats` run
     python -m kokoro_hip.profsum layers <layers.json>
@@ -79,44 +80,57 @@ def _table(rows, dur, per_step=0):
     return lines, total
 
 
-def _serial_lines(rows, steps, dur):
-    """The per-kernel table of bench.py's profiling pass: every dispatch after the end of the run
-    before its first (each run ends with the iSTFT); empty when the trace has no such run."""
+def _serial_window(rows, steps, trailing):
+    """The dispatches of bench.py's profiling pass: the `steps` runs that come before the trace's
+    last `trailing` runs (each run ends with an iSTFT): every dispatch that starts after the end of
+    the run before them and ends by the end of their last iSTFT.  None when the trace is shorter."""
     ist = [r for r in rows if "istft_kernel" in r["Kernel_Name"]]
-    if len(ist) <= steps:
+    if len(ist) <= steps + trailing:
+        return None
+    t0 = int(ist[-steps - trailing - 1]["End_Timestamp"])
+    t1 = int(ist[-trailing - 1]["End_Timestamp"])
+    return [r for r in rows if int(r["Start_Timestamp"]) > t0 and int(r["End_Timestamp"]) <= t1]
+
+
+def _serial_lines(rows, steps, dur, trailing=0):
+    """The per-kernel table of bench.py's profiling pass (`_serial_window`); empty when the trace
+    has no such run."""
+    ser = _serial_window(rows, steps, trailing)
+    if not ser:
         return []
-    t0 = int(ist[-steps - 1]["End_Timestamp"])
-    ser = [r for r in rows if int(r["Start_Timestamp"]) > t0]
     st, tot = _table(ser, dur, steps)
-    return [f"The profiling pass alone ({len(ser)} dispatches of the last {steps} runs, each kernel alone on "
+    after = f" before the trace's last {trailing}" if trailing else ""
+    return [f"The profiling pass alone ({len(ser)} dispatches of the {steps} runs{after}, each kernel alone on "
             f"one stream; {tot / 1e3 / steps:.3f} ms of kernels per run):", ""] + st
 
 
-def serial(trace_dir, steps):
-    """The per-kernel table of the trace's last `steps` runs alone (bench.py's profiling pass)."""
+def serial(trace_dir, steps, trailing=0):
+    """The per-kernel table of bench.py's profiling pass alone (`steps` runs, then `trailing` more)."""
     rows = _rows(os.path.join(trace_dir, "run_kernel_trace.csv"))
     rows.sort(key=lambda r: int(r["Start_Timestamp"]))
     dur = lambda r: (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
-    return "\n".join(_serial_lines(rows, steps, dur))
+    return "\n".join(_serial_lines(rows, steps, dur, trailing))
 
 
-def stats(trace_dir, steps):
-    """Per-kernel table of the whole trace; the same table over bench.py's profiling pass alone (its
-    last `steps` runs, every kernel alone on one stream: no span includes another stream's work);
-    and the Snake-block convs' average duration per launch in that pass."""
+def stats(trace_dir, steps, trailing=0):
+    """Per-kernel table of the whole trace; the same table over bench.py's profiling pass alone
+    (`steps` runs followed by `trailing` other runs, every kernel alone on one stream: no span
+    includes another stream's work); and the Snake-block convs' average duration per launch in that
+    pass."""
     rows = _rows(os.path.join(trace_dir, "run_kernel_trace.csv"))
     rows.sort(key=lambda r: int(r["Start_Timestamp"]))
     dur = lambda r: (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
     lines, _ = _table(rows, dur)
-    st = _serial_lines(rows, steps, dur)
+    st = _serial_lines(rows, steps, dur, trailing)
     if st:
         lines += [""] + st
     layers, frames = snake_layers()
     sn = [r for r in rows if SNAKE.search(r["Kernel_Name"])]
-    last = sn[-steps * len(layers):]
+    win = _serial_window(rows, steps, trailing)
+    last = [r for r in win if SNAKE.search(r["Kernel_Name"])] if win else sn[-steps * len(layers):]
     avg = sum(dur(r) for r in last) / len(last)
     fl = sum(l["flop"] for l in layers) / len(layers)
-    lines += ["", f"Snake-block convs of the profiling pass (the trace's last {steps} steps, {len(last)} dispatches, "
+    lines += ["", f"Snake-block convs of the profiling pass ({steps} steps, {len(last)} dispatches, "
                   f"each alone on the stream): **{avg:.1f} us** per launch on average, "
                   f"{fl / avg / 1e6:.1f} TFLOP/s algorithmic ({100 * fl / avg / 1e6 / 2500:.1f}% of 2.5 PFLOP/s); "
                   f"all {len(sn)} Snake dispatches of the trace (the timed steps overlap three chains) "
@@ -242,10 +256,11 @@ def counters(run_dir):
 
 if __name__ == "__main__":
     sys.path.insert(0, os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+    trailing = int(sys.argv[4]) if len(sys.argv) > 4 and sys.argv[1] in ("stats", "serial") else 0
     if sys.argv[1] == "stats":
-        print(stats(sys.argv[2], int(sys.argv[3])))
+        print(stats(sys.argv[2], int(sys.argv[3]), trailing))
     elif sys.argv[1] == "serial":
-        print(serial(sys.argv[2], int(sys.argv[3])))
+        print(serial(sys.argv[2], int(sys.argv[3]), trailing))
     elif sys.argv[1] == "kernels":
         print(kernels_table(sys.argv[2]))
     elif sys.argv[1] == "layers":

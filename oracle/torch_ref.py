@@ -28,28 +28,42 @@ def T(a):
 
 
 ROUND_OPERANDS = False
+ROUND_ONLY = None  # with ROUND_OPERANDS: None (every layer) or the layer-name prefixes that round
+ROUND_EXCEPT = ()  # layer-name prefixes that do not round
+ROUND_FP16 = ()    # layer-name prefixes that round to fp16 instead of bf16
 
 
 class bf16_operands:
     """Within: conv() and linear() round their input and weight to bf16 first (the GPU's MFMA
-    operands, and the reference's GLinear / BF16 convs, src/gpu.rs:280-301), accumulating in DT."""
+    operands, and the reference's GLinear / BF16 convs, src/gpu.rs:280-301), accumulating in DT.
+    only / skip / fp16: layer-name prefixes that select where it rounds (for measurements of which
+    rounding points matter)."""
+
+    def __init__(self, only=None, skip=(), fp16=()):
+        self.only, self.skip, self.fp16 = only, tuple(skip), tuple(fp16)
 
     def __enter__(self):
-        global ROUND_OPERANDS
-        ROUND_OPERANDS = True
+        global ROUND_OPERANDS, ROUND_ONLY, ROUND_EXCEPT, ROUND_FP16
+        ROUND_OPERANDS, ROUND_ONLY, ROUND_EXCEPT, ROUND_FP16 = True, self.only, self.skip, self.fp16
 
     def __exit__(self, *a):
-        global ROUND_OPERANDS
-        ROUND_OPERANDS = False
+        global ROUND_OPERANDS, ROUND_ONLY, ROUND_EXCEPT, ROUND_FP16
+        ROUND_OPERANDS, ROUND_ONLY, ROUND_EXCEPT, ROUND_FP16 = False, None, (), ()
 
 
-def _rb(t):
-    return t.to(torch.float32).to(torch.bfloat16).to(DT) if ROUND_OPERANDS else t
+def _rb(t, prefix=""):
+    if not ROUND_OPERANDS or prefix.startswith(ROUND_EXCEPT or ("\0",)):
+        return t
+    if ROUND_ONLY is not None and not prefix.startswith(tuple(ROUND_ONLY)):
+        return t
+    fmt = torch.float16 if ROUND_FP16 and prefix.startswith(ROUND_FP16) else torch.bfloat16
+    return t.to(torch.float32).to(fmt).to(DT)
 
 
 def conv(w, prefix, x, stride=1, pad=0, dil=1, bias=True):
     b = T(w[prefix + ".bias"]) if bias else None
-    return F.conv1d(_rb(x)[None], _rb(T(w[prefix + ".weight"])), b, stride=stride, padding=pad, dilation=dil)[0]
+    return F.conv1d(_rb(x, prefix)[None], _rb(T(w[prefix + ".weight"]), prefix), b, stride=stride, padding=pad,
+                    dilation=dil)[0]
 
 
 def adain(w, prefix, x, s):
@@ -196,7 +210,7 @@ HEADS, HEAD_DIM = 12, 64
 def linear(w, prefix, x):
     """Linear on row-major x [t, din] (src/nn.rs:7-23; GLinear::fwd src/gpu.rs:280-301)."""
     b = T(w[prefix + ".bias"]) if prefix + ".bias" in w else None
-    return F.linear(_rb(x), _rb(T(w[prefix + ".weight"])), b)
+    return F.linear(_rb(x, prefix), _rb(T(w[prefix + ".weight"]), prefix), b)
 
 
 def gelu_new(x):
@@ -238,7 +252,7 @@ def lstm_dir(w, prefix, sfx, x, reverse):
     wih, whh = T(w[f"{prefix}.weight_ih_l0{sfx}"]), T(w[f"{prefix}.weight_hh_l0{sfx}"])
     bih, bhh = T(w[f"{prefix}.bias_ih_l0{sfx}"]), T(w[f"{prefix}.bias_hh_l0{sfx}"])
     hd = whh.shape[1]
-    gx = F.linear(_rb(x), _rb(wih), bih)  # W_ih on the GLinear route (bf16 operands on the GPU)
+    gx = F.linear(_rb(x, prefix), _rb(wih, prefix), bih)  # W_ih on the GLinear route (bf16 operands on the GPU)
     h = torch.zeros(hd, dtype=DT)
     c = torch.zeros(hd, dtype=DT)
     out = torch.zeros(x.shape[0], hd, dtype=DT)

@@ -80,8 +80,8 @@ def test_counters_mfma_utilisation(tmp_path):
 
 
 def test_serial_pass_is_the_last_runs(tmp_path):
-    """The serial table covers only the dispatches after the end of the last-but-`steps` run (each
-    run ends with the iSTFT); earlier, overlapped runs stay out of it."""
+    """The serial table covers only the `steps` runs before the trace's last `trailing` runs (each
+    run ends with the iSTFT); earlier, overlapped runs and the trailing runs stay out of it."""
     d = tmp_path / "trace"
     os.makedirs(d)
     ist = "void kk::(anonymous namespace)::istft_kernel(float const*, float*)"
@@ -96,7 +96,12 @@ def test_serial_pass_is_the_last_runs(tmp_path):
             w.writerow([name, t, t + us * 1000])
             t += us * 1000 + 1000
     out = profsum.serial(str(d), 1)
-    assert "(2 dispatches of the last 1 runs" in out
+    assert "(2 dispatches of the 1 runs," in out
     assert "| `finalize_kernel` | 1 | 0.01 | 7.0 |" in out
     assert "| `istft_kernel` | 1 | 0.01 | 10.0 |" in out
     assert profsum.serial(str(d), 3) == ""
+    # one trailing run after the profiling pass (bench.py's parity plan): the window is the run before it
+    out = profsum.serial(str(d), 1, 1)
+    assert "(2 dispatches of the 1 runs before the trace's last 1," in out
+    assert "| `finalize_kernel` | 1 | 0.10 | 100.0 |" in out and "7.0 |" not in out
+    assert profsum.serial(str(d), 2, 1) == ""
