@@ -32,7 +32,9 @@
 //   the instance-norm statistics of the values it stores: per (tile, wave, channel) sums of
 //   (v - v_first), written to a partials buffer that finalize combines in a fixed order.
 // * The Snake blocks' conv1 output (input of conv2's AdaIN) is stored as fp16: half the HBM
-//   traffic of f32, 8x the precision of the bf16 operands; the residual stream stays f32.
+//   traffic of f32, 8x the precision of the bf16 operands.  So is the generator resblocks' residual
+//   stream (each block's running sum: conv2 adds into it in place as fp16, the next conv1 reads
+//   it, the stage's mean reads all three); the stage input it starts from stays f32.
 #include "kk_common.h"
 #include "kk_kernels.h"
 #include "kk_walk.h"
@@ -247,7 +249,7 @@ struct ConvTGeo {
 
 // Residual operands a stride-1 epilogue reads per 4 output rows.
 template <int EPI>
-constexpr int kNumRes = (EPI == EPI_MEAN3 || EPI == EPI_MEAN3_LEAKY_BF16) ? 3
+constexpr int kNumRes = EPI == EPI_MEAN3_LEAKY_BF16 ? 3
                         : (EPI == EPI_ACCUM || EPI == EPI_RESID || EPI == EPI_RESID_UP2 || EPI == EPI_ADD_FROM) ? 1
                                                                                                                  : 0;
 
@@ -259,12 +261,30 @@ struct EpiBase {
     __amdgpu_buffer_rsrc_t ry;  // y from the unit's first row, as a buffer resource (see store4)
 };
 
+// fp16 residual operands travel as their raw bits (4 halves in .x and .y) from the load to
+// finish4, which widens them: converting at the load would wait for it there.
+__device__ __forceinline__ float4 raw_h4(uint2 v) { return make_float4(__uint_as_float(v.x), __uint_as_float(v.y), 0.f, 0.f); }
+__device__ __forceinline__ float4 widen_h4(float4 raw) {
+    const f16x2_t a = __builtin_bit_cast(f16x2_t, __float_as_uint(raw.x));
+    const f16x2_t b = __builtin_bit_cast(f16x2_t, __float_as_uint(raw.y));
+    return make_float4((float)a.x, (float)a.y, (float)b.x, (float)b.y);
+}
+
 // Residual operands of output row t, channels m..m+3 (`yo`, `ro`: element offsets from the unit's
 // first row in y and r0..r2).
-template <int EPI>
+template <int EPI, bool OUT_H>
 __device__ __forceinline__ void load_res(const ConvParams& p, const EpiBase& eb, uint32_t yo, uint32_t ro, int64_t t,
                                          int m, float4* r) {
-    if constexpr (EPI == EPI_ACCUM || EPI == EPI_RESID) {
+    typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+    if constexpr (EPI == EPI_ACCUM && OUT_H) {
+        // the fp16 rows this epilogue overwrites, streamed like its stores
+        const u32x2_t v = __builtin_nontemporal_load((const u32x2_t*)((const uint16_t*)eb.y + yo));
+        r[0] = raw_h4(make_uint2(v.x, v.y));
+    } else if constexpr (EPI == EPI_MEAN3_LEAKY_BF16) {
+        r[0] = raw_h4(*(const uint2*)((const uint16_t*)eb.r0 + ro));
+        r[1] = raw_h4(*(const uint2*)((const uint16_t*)eb.r1 + ro));
+        r[2] = raw_h4(*(const uint2*)((const uint16_t*)eb.r2 + ro));
+    } else if constexpr (EPI == EPI_ACCUM || EPI == EPI_RESID) {
         // the rows this epilogue overwrites: streamed (nontemporal), like its stores
         const f32x4 v = __builtin_nontemporal_load((const f32x4*)((const float*)eb.y + yo));
         r[0] = make_float4(v.x, v.y, v.z, v.w);
@@ -272,10 +292,6 @@ __device__ __forceinline__ void load_res(const ConvParams& p, const EpiBase& eb,
         r[0] = *(const float4*)(p.r0 + (t >> 1) * p.r0_ld + m);
     } else if constexpr (EPI == EPI_ADD_FROM) {
         r[0] = *(const float4*)(eb.r0 + ro);
-    } else if constexpr (EPI == EPI_MEAN3 || EPI == EPI_MEAN3_LEAKY_BF16) {
-        r[0] = *(const float4*)(eb.r0 + ro);
-        r[1] = *(const float4*)(eb.r1 + ro);
-        r[2] = *(const float4*)(eb.r2 + ro);
     }
 }
 
@@ -301,9 +317,10 @@ __device__ __forceinline__ float4 finish4(const ConvParams& p, float4 v, const f
         pk = make_uint2(pack_bf16x2(g[0], g[1]), pack_bf16x2(g[2], g[3]));
         return v;
     } else if constexpr (EPI == EPI_MEAN3_LEAKY_BF16) {
-        // the mean of three blocks as EPI_MEAN3, then the next layer's prologue (leaky ReLU, round to
-        // nearest even bf16): the same operand bits that layer's PRO_LEAKY staging would produce
-        const float4 a = r[0], b1 = r[1], c = r[2];
+        // ((rb0 + rb1) + (rb2_resid + conv)) / 3 (src/gpu_batch.rs:395-401) from the three fp16
+        // residual streams, then the next layer's prologue (leaky ReLU, round to nearest even bf16):
+        // the same operand bits that layer's PRO_LEAKY staging would produce
+        const float4 a = widen_h4(r[0]), b1 = widen_h4(r[1]), c = widen_h4(r[2]);
         const float o[4] = {((a.x + b1.x) + (c.x + v.x)) / 3.0f, ((a.y + b1.y) + (c.y + v.y)) / 3.0f,
                             ((a.z + b1.z) + (c.z + v.z)) / 3.0f, ((a.w + b1.w) + (c.w + v.w)) / 3.0f};
         const float slope = p.slope;
@@ -312,7 +329,7 @@ __device__ __forceinline__ float4 finish4(const ConvParams& p, float4 v, const f
         for (int e = 0; e < 4; e++) w[e] = o[e] < 0.f ? o[e] * slope : o[e];
         pk = make_uint2(pack_bf16x2(w[0], w[1]), pack_bf16x2(w[2], w[3]));
         return make_float4(o[0], o[1], o[2], o[3]);
-    } else if constexpr (OUT_H) {
+    } else if constexpr (OUT_H && EPI == EPI_STORE) {
         // fp16 storage; the statistics use the f32 values, as the reference's f32 h does (the fp16
         // rounding would move the mean and variance by ~2^-12 relative, far below the next
         // layer's bf16 operand rounding)
@@ -321,17 +338,14 @@ __device__ __forceinline__ float4 finish4(const ConvParams& p, float4 v, const f
     }
     float4 o = v;
     if constexpr (EPI == EPI_ACCUM || EPI == EPI_ADD_FROM) {
-        const float4 y = r[0];
+        // an fp16 residual stream: the sum in f32, stored rounded to fp16 (statistics as above)
+        const float4 y = EPI == EPI_ACCUM && OUT_H ? widen_h4(r[0]) : r[0];
         o = make_float4(y.x + v.x, y.y + v.y, y.z + v.z, y.w + v.w);
+        if constexpr (OUT_H) pk = make_uint2(pack_f16x2(o.x, o.y), pack_f16x2(o.z, o.w));
     } else if constexpr (EPI == EPI_RESID || EPI == EPI_RESID_UP2) {
         const float4 y = r[0];
         const float s = p.scale;
         o = make_float4((v.x + y.x) * s, (v.y + y.y) * s, (v.z + y.z) * s, (v.w + y.w) * s);
-    } else if constexpr (EPI == EPI_MEAN3) {
-        // ((rb0 + rb1) + (rb2_resid + conv)) / 3   (src/gpu_batch.rs:395-401)
-        const float4 a = r[0], b1 = r[1], c = r[2];
-        o = make_float4(((a.x + b1.x) + (c.x + v.x)) / 3.0f, ((a.y + b1.y) + (c.y + v.y)) / 3.0f,
-                        ((a.z + b1.z) + (c.z + v.z)) / 3.0f, ((a.w + b1.w) + (c.w + v.w)) / 3.0f);
     }
     return o;
 }
@@ -399,6 +413,7 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
     constexpr bool CONVT = EPI == EPI_CONVT || EPI == EPI_CONVT_REFLECT;
     constexpr int NR = CONVT ? 1 : kNumRes<EPI>;
     constexpr int NRA = NR > 0 ? NR : 1;
+    constexpr bool RES_H = (EPI == EPI_ACCUM && OUT_H) || EPI == EPI_MEAN3_LEAKY_BF16;  // fp16 residuals
     constexpr int QB = NR > 1 ? 2 : (NR == 1 ? 4 : 8);  // column groups per batch
     const int l32 = lane & 31, lh = lane >> 5;
     const int cq = lane & 15, cg = lane >> 4;
@@ -438,9 +453,12 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
     if constexpr (CONVT) eb.y = p.y + ubase * p.y_ld;
     eb.ry = __builtin_amdgcn_make_buffer_rsrc(eb.y, 0, kBufRecords, kBufFormat);  // raw (stride 0) buffer
     eb.r0 = eb.r1 = eb.r2 = nullptr;
-    constexpr bool MEAN = EPI == EPI_MEAN3 || EPI == EPI_MEAN3_LEAKY_BF16;
-    if constexpr (EPI == EPI_ADD_FROM || MEAN) eb.r0 = p.r0 + n0 * p.r0_ld;
-    if constexpr (MEAN) eb.r1 = p.r1 + n0 * p.r0_ld, eb.r2 = p.r2 + n0 * p.r0_ld;
+    if constexpr (EPI == EPI_ADD_FROM) eb.r0 = p.r0 + n0 * p.r0_ld;
+    if constexpr (EPI == EPI_MEAN3_LEAKY_BF16) {  // fp16 rows, addressed as such in load_res
+        eb.r0 = (const float*)((const uint16_t*)p.r0 + n0 * p.r0_ld);
+        eb.r1 = (const float*)((const uint16_t*)p.r1 + n0 * p.r0_ld);
+        eb.r2 = (const float*)((const uint16_t*)p.r2 + n0 * p.r0_ld);
+    }
     const uint32_t yld = (uint32_t)vgpr((int)p.y_ld), rld = (uint32_t)vgpr((int)p.r0_ld);
     const uint32_t yo0 = (uint32_t)(wcol0 + cg) * yld + m, ro0 = (uint32_t)(wcol0 + cg) * rld + m;
     const uint32_t yz = u.m0, rz = u.m0;  // clamped operand of an invalid row: row 0 of the unit
@@ -464,7 +482,7 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
                 res[b % RING][qq][0] = *(const float4*)(p.r0 + d * p.r0_ld + cg_.co);
             } else {
                 const bool ok = FULL || (wcol0 + c + cg < u.nv && mok);
-                load_res<EPI>(p, eb, ok ? yo0 + __umul24(c, yld) : yz, ok ? ro0 + __umul24(c, rld) : rz,
+                load_res<EPI, OUT_H>(p, eb, ok ? yo0 + __umul24(c, yld) : yz, ok ? ro0 + __umul24(c, rld) : rz,
                               ok ? n0 + wcol0 + cg + c : n0, ok ? m : u.m0, res[b % RING][qq]);
             }
         }
@@ -500,7 +518,14 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
 #pragma unroll
                 for (int qq = 0; qq < QB; qq++)
 #pragma unroll
-                    for (int e = 0; e < NRA; e++) ready(rc[qq][e]);
+                    for (int e = 0; e < NRA; e++) {
+                        if constexpr (RES_H) {  // raw fp16 bits in .x and .y only
+                            ready(__float_as_uint(rc[qq][e].x));
+                            ready(__float_as_uint(rc[qq][e].y));
+                        } else {
+                            ready(rc[qq][e]);
+                        }
+                    }
             }
 #pragma unroll
             for (int qq = 0; qq < QB; qq++) {
@@ -855,20 +880,27 @@ hipError_t launch_conv(const ConvParams& p, int pro, int epi, int shape, bool st
 #define KK_CONV(P, E, SH, WM, WN, ST, IH, OH)                                              \
     if (pro == P && epi == E && shape == SH && stats == ST && in_h == IH && out_h == OH) \
         return launch_t<P, E, WM, WN, ST, IH, OH>(p, n_cu, s, validate_only);
-    // Snake blocks, 256 ch (stage 0) and 128 ch (stage 1): conv1 X (f32) -> h (fp16) with statistics;
-    // conv2 h -> X (ACCUM / ADD_FROM with statistics, last step without; MEAN3)
+    // Snake blocks in place on an f32 stream (the noise branches, the one-block plans), 256 ch
+    // (stage 0) and 128 ch (stage 1): conv1 X (f32) -> h (fp16) with statistics; conv2 h -> X
+    // (ACCUM with statistics, last step without)
     KK_CONV(PRO_ADAIN_SNAKE, EPI_STORE, SHAPE_256x128, 4, 1, true, false, true)
     KK_CONV(PRO_ADAIN_SNAKE, EPI_ACCUM, SHAPE_256x128, 4, 1, true, true, false)
     KK_CONV(PRO_ADAIN_SNAKE, EPI_ACCUM, SHAPE_256x128, 4, 1, false, true, false)
-    KK_CONV(PRO_ADAIN_SNAKE, EPI_ADD_FROM, SHAPE_256x128, 4, 1, true, true, false)
-    KK_CONV(PRO_ADAIN_SNAKE, EPI_MEAN3, SHAPE_256x128, 4, 1, false, true, false)
     KK_CONV(PRO_ADAIN_SNAKE, EPI_STORE, SHAPE_128x256, 2, 2, true, false, true)
     KK_CONV(PRO_ADAIN_SNAKE, EPI_ACCUM, SHAPE_128x256, 2, 2, true, true, false)
     KK_CONV(PRO_ADAIN_SNAKE, EPI_ACCUM, SHAPE_128x256, 2, 2, false, true, false)
-    KK_CONV(PRO_ADAIN_SNAKE, EPI_ADD_FROM, SHAPE_128x256, 2, 2, true, true, false)
-    KK_CONV(PRO_ADAIN_SNAKE, EPI_MEAN3, SHAPE_128x256, 2, 2, false, true, false)
-    // each stage's mean, stored as the next layer's bf16 operand (ups.1, conv_post)
+    // the generator's resblocks on fp16 residual streams: conv1 X (fp16) -> h; conv2 h -> X as
+    // ADD_FROM (from the f32 stage input) and ACCUM, with statistics but for the last step; each
+    // stage's mean of the three streams stored as the next layer's bf16 operand (ups.1, conv_post)
+    KK_CONV(PRO_ADAIN_SNAKE, EPI_STORE, SHAPE_256x128, 4, 1, true, true, true)
+    KK_CONV(PRO_ADAIN_SNAKE, EPI_ADD_FROM, SHAPE_256x128, 4, 1, true, true, true)
+    KK_CONV(PRO_ADAIN_SNAKE, EPI_ACCUM, SHAPE_256x128, 4, 1, true, true, true)
+    KK_CONV(PRO_ADAIN_SNAKE, EPI_ACCUM, SHAPE_256x128, 4, 1, false, true, true)
     KK_CONV(PRO_ADAIN_SNAKE, EPI_MEAN3_LEAKY_BF16, SHAPE_256x128, 4, 1, false, true, true)
+    KK_CONV(PRO_ADAIN_SNAKE, EPI_STORE, SHAPE_128x256, 2, 2, true, true, true)
+    KK_CONV(PRO_ADAIN_SNAKE, EPI_ADD_FROM, SHAPE_128x256, 2, 2, true, true, true)
+    KK_CONV(PRO_ADAIN_SNAKE, EPI_ACCUM, SHAPE_128x256, 2, 2, true, true, true)
+    KK_CONV(PRO_ADAIN_SNAKE, EPI_ACCUM, SHAPE_128x256, 2, 2, false, true, true)
     KK_CONV(PRO_ADAIN_SNAKE, EPI_MEAN3_LEAKY_BF16, SHAPE_128x256, 2, 2, false, true, true)
     // decoder
     KK_CONV(PRO_ADAIN_LEAKY, EPI_STORE, SHAPE_256x128, 4, 1, true, false, false)

@@ -1424,10 +1424,12 @@ struct Runner {
         const double v_in = share * (double)o.din->valid(), v_out = share * (double)o.dout->valid();
         const double es_in = (o.in_h || o.pro == PRO_BF16) ? 2 : 4, es_out = o.out_h ? 2 : 4;
         const int nres = o.convt ? 1
-                         : (o.epi == EPI_MEAN3 || o.epi == EPI_MEAN3_LEAKY_BF16) ? 3
+                         : o.epi == EPI_MEAN3_LEAKY_BF16 ? 3
                          : (o.epi == EPI_ACCUM || o.epi == EPI_RESID || o.epi == EPI_ADD_FROM) ? 1
                                                                                                  : 0;
-        double bytes = v_in * c.cin * es_in + v_out * c.cout * (es_out + 4.0 * nres);
+        // residual operands: fp16 streams for the means and fp16 accumulation, f32 otherwise
+        const double es_res = o.epi == EPI_MEAN3_LEAKY_BF16 || (o.epi == EPI_ACCUM && o.out_h) ? 2 : 4;
+        double bytes = v_in * c.cin * es_in + v_out * c.cout * (es_out + es_res * nres);
         if (o.epi == EPI_RESID_UP2) bytes += v_out / 2 * c.cout * 4;
         // the dry run (plan creation) validates the launch parameters without launching
         if (dry) {
@@ -1473,16 +1475,18 @@ struct Runner {
         }
     }
 
-    // x = (rb0(y) + rb1(y) + rb2(y)) / 3 (src/gpu_batch.rs:395-401); result in X[2].
+    // x = (rb0(y) + rb1(y) + rb2(y)) / 3 (src/gpu_batch.rs:395-401), stored in post_out as the next
+    // layer's bf16 operand (leaky ReLU with post_slope applied; nothing else reads a stage's output);
+    // post_out must not be a buffer the mean reads (X, block 2's h).
+    // Each block's running sum X[j] is an fp16 stream (half the traffic of the f32 stream the
+    // reference keeps; 2^-11 relative rounding per step against the 2^-8 of the bf16 operands that
+    // every conv reads): conv2 of step 0 adds the f32 stage input y into it, the later steps add in
+    // place, conv1 of steps 1 and 2 reads it, and the mean reads the three.
     // yt: the tiles whose partials of y its producer (the ConvT) wrote, `yparts` per tile, with the
     // reflected first row of each item (xrow_at) outside them when y_refl; null: a statistics pass.
     // hs: the fp16 h buffer of each block (distinct when the blocks run concurrently).
-    // post_out: the mean is stored there as the next layer's bf16 operand (leaky ReLU with
-    // post_slope applied) instead of as f32 in X[2] (nothing else reads a stage's output); it must not
-    // be a buffer the mean reads (X, the block 2's h)
     void resblock_mean(const MSnake* rbs, const float* y, float* X[3], float* const hs[3], const Dom& d,
-                       const Tiles* yt = nullptr, int yparts = 1, bool y_refl = false, void* post_out = nullptr,
-                       float post_slope = 0.f) {
+                       const Tiles* yt, int yparts, bool y_refl, void* post_out, float post_slope) {
         const int c = rbs[0].c, wn = kShapeWN[rbs[0].c1[0].shape];
         // the three blocks' first AdaIN share one set of statistics of y: one finalize for all three
         const MAdain* a1s[3] = {&rbs[0].a1[0], &rbs[1].a1[0], &rbs[2].a1[0]};
@@ -1516,18 +1520,17 @@ struct Runner {
             Coef* cb = side ? cf(6 + 2 * j) : cf(1);
             float* h = hs[j];  // each block its own h in both orders (the mean's output may use hs[0..1])
             for (int i = 0; i < 3; i++) {
-                const float* in = i == 0 ? y : X[j];
-                const Tiles& t =
-                    conv(blk.c1[i], snake_op(blk, d, in, h, EPI_STORE, i == 0 ? cf(2 + j) : ca, i, false, true));
+                Op o1 = snake_op(blk, d, i == 0 ? (const void*)y : X[j], h, EPI_STORE, i == 0 ? cf(2 + j) : ca, i,
+                                 false, true);
+                o1.in_h = i > 0;  // the fp16 stream from step 1 on
+                const Tiles& t = conv(blk.c1[i], o1);
                 fin(t, wn, c, blk.a2[i], cb);
                 Op o2 = snake_op(blk, d, h, X[j], EPI_ACCUM, cb, i, true, i < 2);
+                o2.out_h = true;  // X[j] in fp16
                 if (i == 0) o2.epi = EPI_ADD_FROM, o2.r0 = y, o2.r0_ld = c;
                 if (j == 2 && i == 2) {
-                    o2.epi = EPI_MEAN3, o2.r0 = X[0], o2.r1 = X[1], o2.r2 = X[2], o2.r0_ld = c;
-                    if (post_out) {
-                        o2.epi = EPI_MEAN3_LEAKY_BF16, o2.slope = post_slope, o2.y = (float*)post_out;
-                        o2.out_h = true;
-                    }
+                    o2.epi = EPI_MEAN3_LEAKY_BF16, o2.r0 = X[0], o2.r1 = X[1], o2.r2 = X[2], o2.r0_ld = c;
+                    o2.slope = post_slope, o2.y = (float*)post_out;
                     if (conc) {
                         mean_op = o2, mean_pending = true;
                         continue;

@@ -34,17 +34,18 @@ enum Prologue {
 };
 enum Epilogue {
     EPI_STORE = 0,          // y = conv + b
-    EPI_ACCUM = 1,          // y += conv + b
+    EPI_ACCUM = 1,          // y += conv + b (y fp16, read and written, when the output is fp16)
     EPI_RESID = 2,          // y = (conv + b + y) * scale
     EPI_RESID_UP2 = 3,      // y = (conv + b + r0[t/2]) * scale
-    EPI_ADD_FROM = 4,       // y = r0 + (conv + b)
-    EPI_MEAN3 = 5,          // y = ((r0 + r1) + (r2 + conv + b)) / 3
+    EPI_ADD_FROM = 4,       // y = r0 + (conv + b) (r0 f32; y f32 or fp16)
     EPI_CONVT = 6,          // polyphase ConvT scatter, y[o] = conv + b + r0[o]
     EPI_CONVT_REFLECT = 7,  // ConvT scatter with per-item ReflectionPad1d((1,0)), + r0
     EPI_GELU_BF16 = 8,      // y (bf16) = gelu_new(conv + b) (kernels/kokoro.cu:84-90), 2-byte output
-    EPI_MEAN3_LEAKY_BF16 = 9,  // y (bf16) = leaky(EPI_MEAN3's value, slope): the generator's last
-                               // Snake conv storing conv_post's input operand (2-byte output; the
-                               // slope in ConvParams.slope, which the Snake prologue does not use)
+    EPI_MEAN3_LEAKY_BF16 = 9,  // y (bf16) = leaky(((r0 + r1) + (r2 + conv + b)) / 3, slope): a
+                               // generator stage's mean of its three resblocks, stored as the next
+                               // layer's input operand (r0, r1, r2 the blocks' fp16 residual streams
+                               // with r0_ld; 2-byte output; the slope in ConvParams.slope, which the
+                               // Snake prologue does not use)
 };
 enum BlockShape {
     SHAPE_256x128 = 0,  // 4 waves (4 x 1), wave tile 64 x 128

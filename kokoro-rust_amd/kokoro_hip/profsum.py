@@ -43,11 +43,19 @@ def snake_layers():
         for blk, k in [("noise_res", nrk), ("resblock", 3), ("resblock", 7), ("resblock", 11)]:
             for d in (1, 3, 5):
                 for cv in (1, 2):
-                    # conv1 reads the f32 stream and writes fp16; conv2 reads fp16 and the f32
-                    # residual, writes f32; the last conv of the three resblocks also reads the
-                    # other two blocks' streams and writes their mean as the next layer's bf16
-                    # operand (2 + 3 x 4 + 2 bytes)
-                    per_col = 6 if cv == 1 else (16 if (blk, k, d) == ("resblock", 11, 5) else 10)
+                    # bytes per column and channel.  The noise resblock runs in place on an f32
+                    # stream: conv1 reads it and writes h in fp16 (4 + 2), conv2 reads h and the
+                    # stream and writes the stream (2 + 4 + 4).  The resblocks keep fp16 streams
+                    # started from the f32 stage input: conv1 reads the input (4 + 2) or the stream
+                    # (2 + 2); conv2 adds h to the input (2 + 4 + 2) or to the stream in place
+                    # (2 + 2 + 2); the last conv of the three reads the three streams and writes
+                    # their mean as the next layer's bf16 operand (2 + 3 x 2 + 2)
+                    if blk == "noise_res":
+                        per_col = 6 if cv == 1 else 10
+                    elif cv == 1:
+                        per_col = 6 if d == 1 else 4
+                    else:
+                        per_col = 8 if d == 1 else (10 if (k, d) == (11, 5) else 6)
                     by = c * cols * per_col
                     out.append({"name": f"stage{st} {blk} k{k} d{d} conv{cv}", "flop": 2.0 * c * c * k * cols,
                                 "bytes": by})

@@ -754,21 +754,27 @@ static void adain_act(const adain_t* a, const float* x, int t, const float* styl
     free(rstd);
 }
 
-/* snake_b (src/gpu_batch.rs:140-154). */
-static void snake_block(const snake_t* s, const float* x, int t, const float* style, float* out) {
+/* snake_b (src/gpu_batch.rs:140-154).  res16 (emulation only): the running sum is an fp16 stream
+ * on the HIP path -- rounded after each of the first `res16` steps (3 for a generator resblock
+ * whose stream the stage's mean reads, 2 for the block whose last sum the mean takes unrounded;
+ * 0: an f32 stream). */
+static void snake_block(const snake_t* s, const float* x, int t, const float* style, float* out, int res16) {
     size_t n = (size_t)s->c * t;
     float* h = (float*)malloc(n * sizeof(float));
     float* u = (float*)malloc(n * sizeof(float));
+    const int h16 = g_bf16 && (g_groups & KO_GROUP_H16);
     if (out != x) memcpy(out, x, n * sizeof(float));
     for (int i = 0; i < 3; i++) {
         adain_act(&s->a1[i], out, t, style, 1, 0.0f, s->al1[i], u);
         conv_layer(&s->c1[i], u, t, h, t);
         /* the HIP path stores conv1's output (the input of adain2) in fp16 */
-        if (g_bf16 && (g_groups & KO_GROUP_H16))
+        if (h16)
             for (size_t j = 0; j < n; j++) h[j] = ko_fp16_round(h[j]);
         adain_act(&s->a2[i], h, t, style, 1, 0.0f, s->al2[i], u);
         conv_layer(&s->c2[i], u, t, h, t);
         for (size_t j = 0; j < n; j++) out[j] = out[j] + h[j];
+        if (h16 && i < res16)
+            for (size_t j = 0; j < n; j++) out[j] = ko_fp16_round(out[j]);
     }
     free(h);
     free(u);
@@ -854,7 +860,7 @@ int ko_snake_block_forward(const ko_model* m, const char* prefix, const float* x
         if (strcmp(prefix, nm) == 0) s = &m->resblocks[i];
     }
     if (!s || t <= 0) return -1;
-    snake_block(s, x, t, style, out);
+    snake_block(s, x, t, style, out, 0);
     return 0;
 }
 
@@ -903,9 +909,9 @@ static void resblock_mean(const ko_model* m, int first, const float* y, int t, c
     int c = m->resblocks[first].c;
     size_t n = (size_t)c * t;
     float* r = (float*)malloc(n * sizeof(float));
-    snake_block(&m->resblocks[first], y, t, style, out);
+    snake_block(&m->resblocks[first], y, t, style, out, 3);
     for (int j = 1; j < 3; j++) {
-        snake_block(&m->resblocks[first + j], y, t, style, r);
+        snake_block(&m->resblocks[first + j], y, t, style, r, j < 2 ? 3 : 2);
         for (size_t i = 0; i < n; i++) out[i] = out[i] + r[i];
     }
     for (size_t i = 0; i < n; i++) out[i] = out[i] / 3.0f;
@@ -923,7 +929,7 @@ int ko_generator_from_spec(const ko_model* m, const float* x_in, const float* sp
     leaky_inplace(x, (size_t)512 * l2, 0.1f);
     float* xs = (float*)malloc((size_t)256 * t0 * sizeof(float));
     conv_layer(&m->noise_convs[0], spec, f, xs, t0);
-    snake_block(&m->noise_res[0], xs, t0, style, xs);
+    snake_block(&m->noise_res[0], xs, t0, style, xs, 0);
     float* y = (float*)malloc((size_t)256 * t0 * sizeof(float));
     convt_layer(&m->ups[0], x, l2, y, t0);
     for (size_t i = 0; i < (size_t)256 * t0; i++) y[i] = y[i] + xs[i];
@@ -937,7 +943,7 @@ int ko_generator_from_spec(const ko_model* m, const float* x_in, const float* sp
     leaky_inplace(x1, (size_t)256 * t0, 0.1f);
     float* xs1 = (float*)malloc((size_t)128 * t1 * sizeof(float));
     conv_layer(&m->noise_convs[1], spec, f, xs1, t1);
-    snake_block(&m->noise_res[1], xs1, t1, style, xs1);
+    snake_block(&m->noise_res[1], xs1, t1, style, xs1, 0);
     float* y0 = (float*)malloc((size_t)128 * (t1 - 1) * sizeof(float));
     convt_layer(&m->ups[1], x1, t0, y0, t1 - 1);
     float* y1 = (float*)malloc((size_t)128 * t1 * sizeof(float));
