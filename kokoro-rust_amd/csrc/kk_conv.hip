@@ -414,7 +414,7 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
     constexpr int NR = CONVT ? 1 : kNumRes<EPI>;
     constexpr int NRA = NR > 0 ? NR : 1;
     constexpr bool RES_H = (EPI == EPI_ACCUM && OUT_H) || EPI == EPI_MEAN3_LEAKY_BF16;  // fp16 residuals
-    constexpr int QB = NR > 1 ? 2 : (NR == 1 ? 4 : 8);  // column groups per batch
+    constexpr int QB = NR > 1 && !RES_H ? 2 : (NR >= 1 ? 4 : 8);  // column groups per batch
     const int l32 = lane & 31, lh = lane >> 5;
     const int cq = lane & 15, cg = lane >> 4;
     const int wcol0 = wn * 128;                // this wave's first column within the tile
@@ -802,9 +802,9 @@ __global__ __launch_bounds__(64 * WM * WN + kNP) void conv_mfma_kernel(ConvParam
         }
         if (last) {
             const int next_m0 = has_next ? nu.m0 : cu.m0;
-            // (not for the 256-channel accumulate-with-statistics variant: a second epilogue copy
+            // (not for the 256-channel f32 accumulate-with-statistics variant: a second epilogue copy
             // makes it spill)
-            constexpr bool kFullPath = !CONVT && !(EPI == EPI_ACCUM && WM == 4 && STATS);
+            constexpr bool kFullPath = !CONVT && !(EPI == EPI_ACCUM && !OUT_H && WM == 4 && STATS);
             if constexpr (MI == 1)
                 epilogue_m32<WN>(p, cu, acc, wm, wn, lane, scr, bias_s, next_m0);
             else if (kFullPath && cu.nv >= wn * 128 + 128 && cu.m0 + BM <= p.m)  // uniform: the common case
