@@ -290,6 +290,8 @@ __device__ __forceinline__ void load_res(const ConvParams& p, const EpiBase& eb,
         r[0] = make_float4(v.x, v.y, v.z, v.w);
     } else if constexpr (EPI == EPI_RESID_UP2) {
         r[0] = *(const float4*)(p.r0 + (t >> 1) * p.r0_ld + m);
+    } else if constexpr (EPI == EPI_ADD_FROM && OUT_H) {
+        r[0] = raw_h4(*(const uint2*)((const uint16_t*)eb.r0 + ro));
     } else if constexpr (EPI == EPI_ADD_FROM) {
         r[0] = *(const float4*)(eb.r0 + ro);
     }
@@ -339,7 +341,7 @@ __device__ __forceinline__ float4 finish4(const ConvParams& p, float4 v, const f
     float4 o = v;
     if constexpr (EPI == EPI_ACCUM || EPI == EPI_ADD_FROM) {
         // an fp16 residual stream: the sum in f32, stored rounded to fp16 (statistics as above)
-        const float4 y = EPI == EPI_ACCUM && OUT_H ? widen_h4(r[0]) : r[0];
+        const float4 y = OUT_H ? widen_h4(r[0]) : r[0];
         o = make_float4(y.x + v.x, y.y + v.y, y.z + v.z, y.w + v.w);
         if constexpr (OUT_H) pk = make_uint2(pack_f16x2(o.x, o.y), pack_f16x2(o.z, o.w));
     } else if constexpr (EPI == EPI_RESID || EPI == EPI_RESID_UP2) {
@@ -413,7 +415,8 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
     constexpr bool CONVT = EPI == EPI_CONVT || EPI == EPI_CONVT_REFLECT;
     constexpr int NR = CONVT ? 1 : kNumRes<EPI>;
     constexpr int NRA = NR > 0 ? NR : 1;
-    constexpr bool RES_H = (EPI == EPI_ACCUM && OUT_H) || EPI == EPI_MEAN3_LEAKY_BF16;  // fp16 residuals
+    // fp16 residuals: the streams of the fp16 accumulations, the means and the ConvTs' noise branch
+    constexpr bool RES_H = ((EPI == EPI_ACCUM || EPI == EPI_ADD_FROM || CONVT) && OUT_H) || EPI == EPI_MEAN3_LEAKY_BF16;
     constexpr int QB = NR > 1 && !RES_H ? 2 : (NR >= 1 ? 4 : 8);  // column groups per batch
     const int l32 = lane & 31, lh = lane >> 5;
     const int cq = lane & 15, cg = lane >> 4;
@@ -435,7 +438,12 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
         // the unit writes o = os + 1 (then stride n0 - pad - 1 <= os)
         ubase = max(cg_.os, (int64_t)p.stride_t * u.n0 - p.pad_t - 1);
         // the reflected row's residual: r0 at the item's first row
-        if constexpr (EPI == EPI_CONVT_REFLECT) rfl = *(const float4*)(p.r0 + cg_.os * p.r0_ld + cg_.co);
+        if constexpr (EPI == EPI_CONVT_REFLECT) {
+            if constexpr (OUT_H)
+                rfl = widen_h4(raw_h4(*(const uint2*)((const uint16_t*)p.r0 + cg_.os * p.r0_ld + cg_.co)));
+            else
+                rfl = *(const float4*)(p.r0 + cg_.os * p.r0_ld + cg_.co);
+        }
         ready(cb);
     }
     // ConvT output column of tile column col, whether this lane writes it, and the row written
@@ -450,10 +458,11 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
     EpiBase eb;
     const int64_t n0 = u.n0;
     eb.y = OUT_H ? (void*)((uint16_t*)p.y + n0 * p.y_ld) : (void*)(p.y + n0 * p.y_ld);
-    if constexpr (CONVT) eb.y = p.y + ubase * p.y_ld;
+    if constexpr (CONVT) eb.y = OUT_H ? (void*)((uint16_t*)p.y + ubase * p.y_ld) : (void*)(p.y + ubase * p.y_ld);
     eb.ry = __builtin_amdgcn_make_buffer_rsrc(eb.y, 0, kBufRecords, kBufFormat);  // raw (stride 0) buffer
     eb.r0 = eb.r1 = eb.r2 = nullptr;
-    if constexpr (EPI == EPI_ADD_FROM) eb.r0 = p.r0 + n0 * p.r0_ld;
+    if constexpr (EPI == EPI_ADD_FROM)
+        eb.r0 = OUT_H ? (const float*)((const uint16_t*)p.r0 + n0 * p.r0_ld) : p.r0 + n0 * p.r0_ld;
     if constexpr (EPI == EPI_MEAN3_LEAKY_BF16) {  // fp16 rows, addressed as such in load_res
         eb.r0 = (const float*)((const uint16_t*)p.r0 + n0 * p.r0_ld);
         eb.r1 = (const float*)((const uint16_t*)p.r1 + n0 * p.r0_ld);
@@ -479,7 +488,10 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
             if constexpr (CONVT) {
                 bool ok;
                 const int64_t d = convt_dest(wcol0 + c + cg, ok);
-                res[b % RING][qq][0] = *(const float4*)(p.r0 + d * p.r0_ld + cg_.co);
+                if constexpr (OUT_H)
+                    res[b % RING][qq][0] = raw_h4(*(const uint2*)((const uint16_t*)p.r0 + d * p.r0_ld + cg_.co));
+                else
+                    res[b % RING][qq][0] = *(const float4*)(p.r0 + d * p.r0_ld + cg_.co);
             } else {
                 const bool ok = FULL || (wcol0 + c + cg < u.nv && mok);
                 load_res<EPI, OUT_H>(p, eb, ok ? yo0 + __umul24(c, yld) : yz, ok ? ro0 + __umul24(c, rld) : rz,
@@ -539,16 +551,18 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
                     bool ok;
                     const int64_t d = convt_dest(col, ok);
                     const float4 w = make_float4(v[qq].x + cb.x, v[qq].y + cb.y, v[qq].z + cb.z, v[qq].w + cb.w);
-                    const float4 r = rc[qq][0];
+                    const float4 r = OUT_H ? widen_h4(rc[qq][0]) : rc[qq][0];
                     o = make_float4(w.x + r.x, w.y + r.y, w.z + r.z, w.w + r.w);
                     valid = ok;
-                    const uint2 nopk = make_uint2(0u, 0u);
-                    store4<false>(eb, (uint32_t)((d - ubase) * p.y_ld) + cg_.co, ok, o, nopk);
+                    // fp16 output: the stage input of the resblocks' fp16 streams
+                    const uint2 pk = OUT_H ? make_uint2(pack_f16x2(o.x, o.y), pack_f16x2(o.z, o.w)) : make_uint2(0u, 0u);
+                    store4<OUT_H>(eb, (uint32_t)((d - ubase) * p.y_ld) + cg_.co, ok, o, pk);
                     if constexpr (EPI == EPI_CONVT_REFLECT) {
                         // o = os + 1 also fills the item's first row (the reflected sample)
                         // (the statistics leave this row to finalize, which reads it back)
-                        store4<false>(eb, (uint32_t)((cg_.os - ubase) * p.y_ld) + cg_.co, ok && d == cg_.os + 2,
-                                      make_float4(w.x + rfl.x, w.y + rfl.y, w.z + rfl.z, w.w + rfl.w), nopk);
+                        const float4 f = make_float4(w.x + rfl.x, w.y + rfl.y, w.z + rfl.z, w.w + rfl.w);
+                        const uint2 fk = OUT_H ? make_uint2(pack_f16x2(f.x, f.y), pack_f16x2(f.z, f.w)) : make_uint2(0u, 0u);
+                        store4<OUT_H>(eb, (uint32_t)((cg_.os - ubase) * p.y_ld) + cg_.co, ok && d == cg_.os + 2, f, fk);
                     }
                     if constexpr (STATS) cnt += ok ? 1.f : 0.f;
                 } else {
@@ -889,9 +903,10 @@ hipError_t launch_conv(const ConvParams& p, int pro, int epi, int shape, bool st
     KK_CONV(PRO_ADAIN_SNAKE, EPI_STORE, SHAPE_128x256, 2, 2, true, false, true)
     KK_CONV(PRO_ADAIN_SNAKE, EPI_ACCUM, SHAPE_128x256, 2, 2, true, true, false)
     KK_CONV(PRO_ADAIN_SNAKE, EPI_ACCUM, SHAPE_128x256, 2, 2, false, true, false)
-    // the generator's resblocks on fp16 residual streams: conv1 X (fp16) -> h; conv2 h -> X as
-    // ADD_FROM (from the f32 stage input) and ACCUM, with statistics but for the last step; each
-    // stage's mean of the three streams stored as the next layer's bf16 operand (ups.1, conv_post)
+    // the generator's fp16 residual streams: conv1 X (fp16) -> h; conv2 h -> X as ADD_FROM (the
+    // resblocks' first step, from the stage input) and ACCUM, with statistics but for the last
+    // step; each stage's mean of its resblocks' three streams stored as the next layer's bf16
+    // operand (ups.1, conv_post)
     KK_CONV(PRO_ADAIN_SNAKE, EPI_STORE, SHAPE_256x128, 4, 1, true, true, true)
     KK_CONV(PRO_ADAIN_SNAKE, EPI_ADD_FROM, SHAPE_256x128, 4, 1, true, true, true)
     KK_CONV(PRO_ADAIN_SNAKE, EPI_ACCUM, SHAPE_256x128, 4, 1, true, true, true)
@@ -914,10 +929,9 @@ hipError_t launch_conv(const ConvParams& p, int pro, int epi, int shape, bool st
     KK_CONV(PRO_F32, EPI_RESID, SHAPE_256x128, 4, 1, false, false, false)
     KK_CONV(PRO_BF16, EPI_RESID, SHAPE_256x128, 4, 1, false, false, false)
     KK_CONV(PRO_F32, EPI_GELU_BF16, SHAPE_256x128, 4, 1, false, false, true)
-    // ConvT ups and conv_post
-    KK_CONV(PRO_LEAKY, EPI_CONVT, SHAPE_256x128, 4, 1, true, false, false)
-    KK_CONV(PRO_LEAKY, EPI_CONVT_REFLECT, SHAPE_256x128, 4, 1, true, false, false)
-    KK_CONV(PRO_BF16, EPI_CONVT_REFLECT, SHAPE_256x128, 4, 1, true, false, false)
+    // ConvT ups (the stage input in fp16, plus the noise branch's fp16 stream) and conv_post
+    KK_CONV(PRO_LEAKY, EPI_CONVT, SHAPE_256x128, 4, 1, true, false, true)
+    KK_CONV(PRO_BF16, EPI_CONVT_REFLECT, SHAPE_256x128, 4, 1, true, false, true)
     KK_CONV(PRO_LEAKY, EPI_STORE, SHAPE_64x256, 1, 2, false, false, false)
     // conv_post (22 output rows) on 32-row waves, from its bf16 operand (or f32 through leaky ReLU)
     if (pro == PRO_BF16 && epi == EPI_STORE && shape == SHAPE_32x256 && !stats && !in_h && !out_h)

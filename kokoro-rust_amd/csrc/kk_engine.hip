@@ -749,7 +749,7 @@ struct kk_plan {
     // intermediates
     kk::DevBuf gb, xcat, xin_a, xin_b, hdec, pool, sc_half, dec_out, pp, spec, B[6], post, audio, audio_start;
     kk::DevBuf har;  // the harmonic source's samples [600 ln] (only with KOKORO_HIP_TEST_TAP_SOURCE)
-    kk::DevBuf xs[2], hn;  // the noise branches' outputs (d20 x 256, d120 x 128 f32) and their fp16 h
+    kk::DevBuf xs[2], hn;  // the noise branches' fp16 streams (d20 x 256, d120 x 128) and their fp16 h
     // coef[0..1]: the Snake steps' AdaIN pair; [2..4]: the resblocks' first AdaIN; [5..8]: the pair
     // of resblock chains 0 and 1 (run on the context's side streams); [9..10]: the noise branches'
     kk::DevBuf part, coef[11];
@@ -1013,8 +1013,8 @@ static void setup_generator(kk_plan* p, const std::vector<const float*>& f0s, co
     alloc_buf(p, p->audio, (size_t)600 * ln * sizeof(float));
     if (p->tap_source) alloc_buf(p, p->har, (size_t)600 * ln * sizeof(float));
     for (int i = 0; i < 11; i++) alloc_buf(p, p->coef[i], (size_t)nb * kXinLd * sizeof(Coef));
-    alloc_buf(p, p->xs[0], (size_t)l20 * 256 * sizeof(float));
-    alloc_buf(p, p->xs[1], (size_t)l120 * 128 * sizeof(float));
+    alloc_buf(p, p->xs[0], (size_t)l20 * 256 * sizeof(uint16_t));
+    alloc_buf(p, p->xs[1], (size_t)l120 * 128 * sizeof(uint16_t));
     alloc_buf(p, p->hn, (size_t)std::max(l20 * 256, l120 * 128) * sizeof(uint16_t));
     // statistics partials: every partial but the last two of each item covers at least 64 columns
     // of one item (the noise convs' 64-column tiles; the convs' 128-column wave spans)
@@ -1334,8 +1334,8 @@ struct Runner {
         return t;
     }
     // Partials -> coefficients of AdaIN layer a (`wn` partials per tile; xrow: one more sample per
-    // item, row xrow_at[b] of xrow [.][c]).
-    void fin(const Tiles& t, int wn, int c, const MAdain& a, Coef* coef, const float* xrow = nullptr,
+    // item, row xrow_at[b] of xrow [.][c] fp16).
+    void fin(const Tiles& t, int wn, int c, const MAdain& a, Coef* coef, const uint16_t* xrow = nullptr,
              const int64_t* xrow_at = nullptr) {
         const MAdain* as[1] = {&a};
         Coef* const cs[1] = {coef};
@@ -1344,7 +1344,7 @@ struct Runner {
     // One finalize for the n (<= kFinMaxOuts) AdaIN layers as[k] of one tensor: its statistics once,
     // each layer's coefficients into cs[k].
     void fin_n(const Tiles& t, int wn, int c, int n, const MAdain* const* as, Coef* const* cs,
-               const float* xrow = nullptr, const int64_t* xrow_at = nullptr) {
+               const uint16_t* xrow = nullptr, const int64_t* xrow_at = nullptr) {
         check(n >= 1 && n <= kFinMaxOuts, "finalize outputs");
         FinOuts fo{};
         fo.n = n;
@@ -1427,8 +1427,9 @@ struct Runner {
                          : o.epi == EPI_MEAN3_LEAKY_BF16 ? 3
                          : (o.epi == EPI_ACCUM || o.epi == EPI_RESID || o.epi == EPI_ADD_FROM) ? 1
                                                                                                  : 0;
-        // residual operands: fp16 streams for the means and fp16 accumulation, f32 otherwise
-        const double es_res = o.epi == EPI_MEAN3_LEAKY_BF16 || (o.epi == EPI_ACCUM && o.out_h) ? 2 : 4;
+        // residual operands: fp16 streams for the means and wherever the output is an fp16 stream
+        const double es_res =
+            o.epi == EPI_MEAN3_LEAKY_BF16 || (o.out_h && (o.convt || o.epi == EPI_ACCUM || o.epi == EPI_ADD_FROM)) ? 2 : 4;
         double bytes = v_in * c.cin * es_in + v_out * c.cout * (es_out + es_res * nres);
         if (o.epi == EPI_RESID_UP2) bytes += v_out / 2 * c.cout * 4;
         // the dry run (plan creation) validates the launch parameters without launching
@@ -1455,22 +1456,30 @@ struct Runner {
         return o;
     }
 
-    // snake_b (src/gpu_batch.rs:140-154) in place on X.  The statistics of each conv's output are
-    // reduced in its epilogue; the block input's come from the kernel that produced X (`xin`: its
-    // tiles, one partial per tile and channel) or, when null, from a statistics pass here.
+    // snake_b (src/gpu_batch.rs:140-154) in place on X: an f32 stream, or an fp16 one (x16: the
+    // noise branches', which start from the noise conv's fp16 output).  The statistics of each
+    // conv's output are reduced in its epilogue; the block input's come from the kernel that
+    // produced X (`xin`: its tiles, one partial per tile and channel) or, when null, from a
+    // statistics pass here (f32 streams only).
     // ca / cb: the coefficient pair of the block's two AdaIN per step (default cf(0), cf(1)).
-    void snake_block(const MSnake& blk, float* X, float* h, const Dom& d, const Tiles* xin = nullptr,
-                     Coef* ca = nullptr, Coef* cb = nullptr) {
+    void snake_block(const MSnake& blk, void* X, float* h, const Dom& d, const Tiles* xin = nullptr,
+                     Coef* ca = nullptr, Coef* cb = nullptr, bool x16 = false) {
         const int c = blk.c, wn = kShapeWN[blk.c1[0].shape];
         if (!ca) ca = cf(0), cb = cf(1);
-        if (xin)
+        if (xin) {
             fin(*xin, 1, c, blk.a1[0], ca);
-        else
-            stats_fin(X, c, c, d, blk.a1[0], ca);
+        } else {
+            check(!x16, "an fp16 Snake stream needs its producer's statistics");
+            stats_fin((const float*)X, c, c, d, blk.a1[0], ca);
+        }
         for (int i = 0; i < 3; i++) {
-            const Tiles& t = conv(blk.c1[i], snake_op(blk, d, X, h, EPI_STORE, ca, i, false, true));
+            Op o1 = snake_op(blk, d, X, h, EPI_STORE, ca, i, false, true);
+            o1.in_h = x16;
+            const Tiles& t = conv(blk.c1[i], o1);
             fin(t, wn, c, blk.a2[i], cb);
-            conv(blk.c2[i], snake_op(blk, d, h, X, EPI_ACCUM, cb, i, true, i < 2));
+            Op o2 = snake_op(blk, d, h, (float*)X, EPI_ACCUM, cb, i, true, i < 2);
+            o2.out_h = x16;
+            conv(blk.c2[i], o2);
             if (i < 2) fin(t, wn, c, blk.a1[i + 1], ca);
         }
     }
@@ -1478,23 +1487,20 @@ struct Runner {
     // x = (rb0(y) + rb1(y) + rb2(y)) / 3 (src/gpu_batch.rs:395-401), stored in post_out as the next
     // layer's bf16 operand (leaky ReLU with post_slope applied; nothing else reads a stage's output);
     // post_out must not be a buffer the mean reads (X, block 2's h).
-    // Each block's running sum X[j] is an fp16 stream (half the traffic of the f32 stream the
-    // reference keeps; 2^-11 relative rounding per step against the 2^-8 of the bf16 operands that
-    // every conv reads): conv2 of step 0 adds the f32 stage input y into it, the later steps add in
-    // place, conv1 of steps 1 and 2 reads it, and the mean reads the three.
+    // The stage input y and each block's running sum X[j] are fp16 streams (half the traffic of the
+    // f32 streams the reference keeps; 2^-11 relative rounding per step against the 2^-8 of the
+    // bf16 operands that every conv reads): conv2 of step 0 adds y into X[j], the later steps add
+    // in place, conv1 reads y at step 0 and X[j] after, and the mean reads the three X.
     // yt: the tiles whose partials of y its producer (the ConvT) wrote, `yparts` per tile, with the
-    // reflected first row of each item (xrow_at) outside them when y_refl; null: a statistics pass.
+    // reflected first row of each item (xrow_at) outside them when y_refl.
     // hs: the fp16 h buffer of each block (distinct when the blocks run concurrently).
-    void resblock_mean(const MSnake* rbs, const float* y, float* X[3], float* const hs[3], const Dom& d,
-                       const Tiles* yt, int yparts, bool y_refl, void* post_out, float post_slope) {
+    void resblock_mean(const MSnake* rbs, const uint16_t* y, float* X[3], float* const hs[3], const Dom& d,
+                       const Tiles& yt, int yparts, bool y_refl, void* post_out, float post_slope) {
         const int c = rbs[0].c, wn = kShapeWN[rbs[0].c1[0].shape];
         // the three blocks' first AdaIN share one set of statistics of y: one finalize for all three
         const MAdain* a1s[3] = {&rbs[0].a1[0], &rbs[1].a1[0], &rbs[2].a1[0]};
         Coef* const c1s[3] = {cf(2), cf(3), cf(4)};
-        if (yt)
-            fin_n(*yt, yparts, c, 3, a1s, c1s, y_refl ? y : nullptr, y_refl ? d.start_d.as<int64_t>() : nullptr);
-        else
-            fin_n(stats(y, c, c, d), 1, c, 3, a1s, c1s);
+        fin_n(yt, yparts, c, 3, a1s, c1s, y_refl ? y : nullptr, y_refl ? d.start_d.as<int64_t>() : nullptr);
         // The three blocks are independent until the mean: blocks 0 and 1 run on the context's
         // side streams and block 2 on the main stream, each with its own h, statistics region and
         // AdaIN coefficients, and the mean (block 2's last conv) waits for the other two.  One
@@ -1522,12 +1528,12 @@ struct Runner {
             for (int i = 0; i < 3; i++) {
                 Op o1 = snake_op(blk, d, i == 0 ? (const void*)y : X[j], h, EPI_STORE, i == 0 ? cf(2 + j) : ca, i,
                                  false, true);
-                o1.in_h = i > 0;  // the fp16 stream from step 1 on
+                o1.in_h = true;  // y, then X[j]
                 const Tiles& t = conv(blk.c1[i], o1);
                 fin(t, wn, c, blk.a2[i], cb);
                 Op o2 = snake_op(blk, d, h, X[j], EPI_ACCUM, cb, i, true, i < 2);
                 o2.out_h = true;  // X[j] in fp16
-                if (i == 0) o2.epi = EPI_ADD_FROM, o2.r0 = y, o2.r0_ld = c;
+                if (i == 0) o2.epi = EPI_ADD_FROM, o2.r0 = (const float*)y, o2.r0_ld = c;
                 if (j == 2 && i == 2) {
                     o2.epi = EPI_MEAN3_LEAKY_BF16, o2.r0 = X[0], o2.r1 = X[1], o2.r2 = X[2], o2.r0_ld = c;
                     o2.slope = post_slope, o2.y = (float*)post_out;
@@ -1668,21 +1674,21 @@ struct Runner {
     void noise_branch(int i) {
         const Dom& dout = i == 0 ? p->d20 : p->d120;
         const int c = m.ups[i].cout;
-        float* xs = p->xs[i].as<float>();
+        uint16_t* xs = p->xs[i].as<uint16_t>();  // an fp16 stream from the noise conv on
         const int reg = region;
         region = 3;
         const MNoiseConv& nc = m.nc[i];
         const Tiles& tn = p->tl(dout, kNoiseTile);
         need_part(tn.count * c);
-        // reads the spectrum's valid rows once (22 f32), writes cout f32 per output row
-        const double bytes = (double)p->d120.valid() * 88 + (double)dout.valid() * c * 4;
+        // reads the spectrum's valid rows once (22 f32), writes cout fp16 per output row
+        const double bytes = (double)p->d120.valid() * 88 + (double)dout.valid() * c * 2;
         launch(i == 0 ? PC_NOISE0 : PC_NOISE1, 2.0 * 22 * nc.k * c * (double)dout.valid(), bytes, [&] {
             return launch_noise_conv(p->spec.as<float>(), kSpecLd, p->d120.l, p->d120.start_d.as<int64_t>(),
                                      p->d120.len_d.as<int64_t>(),
                                      nc.w.as<float>(), nc.wp.p ? nc.wp.as<float>() : nullptr, nc.b.as<float>(), nc.cout,
                                      nc.k, nc.stride, nc.pad, xs, c, tn.dev(), part(), s);
         });
-        snake_block(m.noise_res[i], xs, p->hn.as<float>(), dout, &tn, cf(9), cf(10));
+        snake_block(m.noise_res[i], xs, p->hn.as<float>(), dout, &tn, cf(9), cf(10), true);
         region = reg;
     }
 
@@ -1692,13 +1698,15 @@ struct Runner {
         const int c = m.ups[i].cout;
         float* B[6];
         for (int j = 0; j < 6; j++) B[j] = p->B[j].as<float>();
-        // y = ups[i](leaky_0.1(x) masked) (+ per-item reflect pad on stage 1) + xs (noise branch i)
+        // y = ups[i](leaky_0.1(x) masked) (+ per-item reflect pad on stage 1) + xs (noise branch i),
+        // both fp16 streams
         Op ou;
         // ups.1 reads stage 0's output as the bf16 operand stage 0's mean stored (leaky 0.1 applied)
         ou.pro = i == 0 ? PRO_LEAKY : PRO_BF16, ou.epi = i == 0 ? EPI_CONVT : EPI_CONVT_REFLECT, ou.slope = 0.1f;
         ou.x = i == 0 ? (const void*)p->dec_out.p : (const void*)B[2], ou.x_ld = i == 0 ? 512 : 256;
         ou.din = &din, ou.dout = &dout, ou.y = B[3], ou.y_ld = c, ou.r0 = p->xs[i].as<float>(), ou.r0_ld = c;
         ou.convt = true, ou.stride = m.ups_stride[i], ou.pad_t = m.ups_pad[i], ou.cls = PC_CONVT;
+        ou.out_h = true;
         ou.stats = true;  // partials of y per (tile, phase, wave column) for the resblocks' first AdaIN
         ou.label = "ups." + std::to_string(i);
         const Tiles& tu = conv(m.ups[i], ou);
@@ -1709,8 +1717,8 @@ struct Runner {
         // the stage's mean as the next layer's bf16 operand: stage 0's (ups.1: leaky 0.1) in B[2],
         // blocks 0 and 1's h, free after the join (not B[3]: ups.1 writes there); stage 1's
         // (conv_post: leaky 0.01) in B[3], the stage's input, free once every block's first step ran
-        resblock_mean(&m.rb[3 * i], B[3], X, hs, dout, &tu, kShapeWN[m.ups[i].shape] * ou.stride, i == 1,
-                      i == 0 ? (void*)B[2] : (void*)B[3], i == 0 ? 0.1f : 0.01f);
+        resblock_mean(&m.rb[3 * i], (const uint16_t*)B[3], X, hs, dout, tu, kShapeWN[m.ups[i].shape] * ou.stride,
+                      i == 1, i == 0 ? (void*)B[2] : (void*)B[3], i == 0 ? 0.1f : 0.01f);
     }
 
     // conv_post over the items [b0, b1) (all: b1 < 0)

@@ -115,9 +115,10 @@ struct FinOuts {
     FinOut o[kFinMaxOuts];
     int n;
 };
+// xrow (fp16 [.][xrow_ld]): one more sample per item outside the partials, row xrow_at[b].
 hipError_t launch_finalize(const StatPart* part, int c, int wn, TilesDev t, int nb, int64_t max_parts,
                            const float* gb, int64_t gb_ld, const FinOuts& outs, hipStream_t s,
-                           const float* xrow = nullptr, int64_t xrow_ld = 0, const int64_t* xrow_at = nullptr);
+                           const uint16_t* xrow = nullptr, int64_t xrow_ld = 0, const int64_t* xrow_at = nullptr);
 // gb[b][j] = W[j] . style[b] + bias[j] for every AdaIN layer at once.
 hipError_t launch_style_fc(const float* w, const float* bias, int rows, const float* style, int nb, float* gb,
                            hipStream_t s);
@@ -141,12 +142,13 @@ hipError_t launch_adain_pool(const float* x, int64_t ld, int c, const Coef* coef
 // over item-aligned tiles t (<= kNoiseTile output rows each; rows outside the tiles are not
 // written), with the statistics partial of each tile ([tile][cout], shift = bias) for the next
 // layer's AdaIN.  wt: [k][22][cout] f32 (VALU kernel); wp: the noise_convs.0 weights packed for
-// the f32 matrix cores ([32-row tile][2][32][12 taps][12] f32), or null.
+// the f32 matrix cores ([32-row tile][2][32][12 taps][12] f32), or null.  y is stored as fp16
+// (the noise branch's residual stream; the statistics describe the f32 values).
 constexpr int kNoiseTile = 64;
 hipError_t launch_noise_conv(const float* spec, int64_t spec_ld, int64_t l_in, const int64_t* in_start,
                              const int64_t* in_len,
                              const float* wt, const float* wp, const float* b, int cout, int k, int stride, int pad,
-                             float* y, int64_t y_ld, TilesDev t, StatPart* part, hipStream_t s);
+                             uint16_t* y, int64_t y_ld, TilesDev t, StatPart* part, hipStream_t s);
 // SineGen phase_pre: per item and harmonic, f64 cumulative sum of the 1/300-downsampled rad values.
 hipError_t launch_phase_pre(const float* f0, const int64_t* start2, const int64_t* len2, int nb,
                             const float* rand_ini, float* pp, int64_t pp_ld, hipStream_t s);

@@ -17,6 +17,15 @@ namespace {
 
 constexpr float kPiF = 3.14159274101257324f;  // (float)M_PI, kernels/kokoro.cu:9
 
+// Four floats rounded to fp16 (to nearest even, v_cvt_pk_f16_f32), packed for one 8-byte store.
+__device__ __forceinline__ uint2 pack_f16x4(float4 v) {
+    typedef float f32x2_t __attribute__((ext_vector_type(2)));
+    typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+    const f16x2_t a = __builtin_convertvector((f32x2_t){v.x, v.y}, f16x2_t);
+    const f16x2_t b = __builtin_convertvector((f32x2_t){v.z, v.w}, f16x2_t);
+    return make_uint2(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b));
+}
+
 // ------------------------------------------------------------------ AdaIN statistics
 // Statistics partials of x over item-aligned tiles: per (tile, channel) the sums of (v - shift) and
 // (v - shift)^2 with shift = the tile's first value (the centring of chan_stats_seg,
@@ -64,7 +73,7 @@ __global__ __launch_bounds__(256) void stats_tiles_kernel(const float* __restric
 template <int SUB, int LOADS>
 __global__ __launch_bounds__(16 * SUB) void finalize_kernel(const StatPart* __restrict__ part, int c, int wn, TilesDev t,
                                                             const float* __restrict__ gb, int64_t gb_ld, FinOuts outs,
-                                                            const float* __restrict__ xrow, int64_t xrow_ld,
+                                                            const uint16_t* __restrict__ xrow, int64_t xrow_ld,
                                                             const int64_t* __restrict__ xrow_at) {
     constexpr int kFinSub = SUB;
     __shared__ double sa[kFinSub][16], sb[kFinSub][16], sn[kFinSub][16];
@@ -108,8 +117,8 @@ __global__ __launch_bounds__(16 * SUB) void finalize_kernel(const StatPart* __re
     }
     if (sub != 0 || ch >= c) return;
     a1 = sa[0][cl], a2 = sb[0][cl], n = sn[0][cl];
-    if (xrow) {  // one more sample of the item, outside the partials: row xrow_at[b] of xrow
-        const double d = (double)xrow[xrow_at[b] * xrow_ld + ch] - ref;
+    if (xrow) {  // one more sample of the item, outside the partials: row xrow_at[b] of xrow (fp16)
+        const double d = (double)(float)__builtin_bit_cast(_Float16, xrow[xrow_at[b] * xrow_ld + ch]) - ref;
         a1 += d, a2 += d * d, n += 1.0;
     }
     const int64_t i = (int64_t)b * c + ch;
@@ -278,7 +287,7 @@ __global__ __launch_bounds__(256) void noise_conv_kernel(const float* __restrict
                                                          const int64_t* __restrict__ in_start,
                                                          const int64_t* __restrict__ in_len,
                                                          const float* __restrict__ wt, const float* __restrict__ b,
-                                                         int k, int stride, int pad, float* __restrict__ y,
+                                                         int k, int stride, int pad, uint16_t* __restrict__ y,
                                                          int64_t y_ld, TilesDev tl, StatPart* __restrict__ part) {
     constexpr int CQ = COUT / 4, TG = 256 / CQ;
     static_assert(TG * TT == kNcRows, "rows per block");
@@ -339,7 +348,7 @@ __global__ __launch_bounds__(256) void noise_conv_kernel(const float* __restrict
     for (int tt = 0; tt < TT; tt++) {
         const int r = tg * TT + tt;
         if (r < nv) {
-            *(float4*)(y + (t0 + r) * y_ld + cq * 4) = acc[tt];
+            *(uint2*)(y + (t0 + r) * y_ld + cq * 4) = pack_f16x4(acc[tt]);
             const float4 d = make_float4(acc[tt].x - bias.x, acc[tt].y - bias.y, acc[tt].z - bias.z, acc[tt].w - bias.w);
             s1.x += d.x, s1.y += d.y, s1.z += d.z, s1.w += d.w;
             s2.x = __builtin_fmaf(d.x, d.x, s2.x), s2.y = __builtin_fmaf(d.y, d.y, s2.y);
@@ -374,7 +383,7 @@ __global__ __launch_bounds__(256, 4) void noise_conv0_mfma_kernel(const float* _
                                                                int64_t l_in, const int64_t* __restrict__ in_start,
                                                                const int64_t* __restrict__ in_len,
                                                                const float4* __restrict__ wp, const float* __restrict__ b,
-                                                               int pad, float* __restrict__ y, int64_t y_ld,
+                                                               int pad, uint16_t* __restrict__ y, int64_t y_ld,
                                                                TilesDev tl, StatPart* __restrict__ part) {
     typedef float f32x16 __attribute__((ext_vector_type(16)));
     __shared__ float xs[22 * kNc0Ld];
@@ -483,8 +492,8 @@ __global__ __launch_bounds__(256, 4) void noise_conv0_mfma_kernel(const float* _
                                           acc[mi][0][4 * g + 3]);
             const float4 v1 = make_float4(acc[mi][1][4 * g], acc[mi][1][4 * g + 1], acc[mi][1][4 * g + 2],
                                           acc[mi][1][4 * g + 3]);
-            if (ok0) *(float4*)(y + (t0 + l32) * y_ld + c0) = v0;
-            if (ok1) *(float4*)(y + (t0 + 32 + l32) * y_ld + c0) = v1;
+            if (ok0) *(uint2*)(y + (t0 + l32) * y_ld + c0) = pack_f16x4(v0);
+            if (ok1) *(uint2*)(y + (t0 + 32 + l32) * y_ld + c0) = pack_f16x4(v1);
             const float4 bv = *(const float4*)(b + c0);
             const float e0[4] = {v0.x - bv.x, v0.y - bv.y, v0.z - bv.z, v0.w - bv.w};
             const float e1[4] = {v1.x - bv.x, v1.y - bv.y, v1.z - bv.z, v1.w - bv.w};
@@ -868,7 +877,7 @@ hipError_t launch_stats_tiles(const float* x, int64_t ld, int c, TilesDev t, Sta
 }
 
 hipError_t launch_finalize(const StatPart* part, int c, int wn, TilesDev t, int nb, int64_t max_parts,
-                           const float* gb, int64_t gb_ld, const FinOuts& outs, hipStream_t s, const float* xrow,
+                           const float* gb, int64_t gb_ld, const FinOuts& outs, hipStream_t s, const uint16_t* xrow,
                            int64_t xrow_ld, const int64_t* xrow_at) {
     if (outs.n < 1 || outs.n > kFinMaxOuts) return hipErrorInvalidValue;
     dim3 grid((unsigned)nb, (unsigned)ceil_div(c, 16));
@@ -926,7 +935,7 @@ hipError_t launch_adain_pool(const float* x, int64_t ld, int c, const Coef* coef
 
 hipError_t launch_noise_conv(const float* spec, int64_t spec_ld, int64_t l_in, const int64_t* in_start,
                              const int64_t* in_len, const float* wt,
-                             const float* wp, const float* b, int cout, int k, int stride, int pad, float* y,
+                             const float* wp, const float* b, int cout, int k, int stride, int pad, uint16_t* y,
                              int64_t y_ld, TilesDev t, StatPart* part, hipStream_t s) {
     const int win = (kNcRows - 1) * stride + k;
     if (win > kNcMaxWin) return hipErrorInvalidValue;

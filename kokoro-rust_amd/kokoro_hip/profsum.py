@@ -43,19 +43,12 @@ def snake_layers():
         for blk, k in [("noise_res", nrk), ("resblock", 3), ("resblock", 7), ("resblock", 11)]:
             for d in (1, 3, 5):
                 for cv in (1, 2):
-                    # bytes per column and channel.  The noise resblock runs in place on an f32
-                    # stream: conv1 reads it and writes h in fp16 (4 + 2), conv2 reads h and the
-                    # stream and writes the stream (2 + 4 + 4).  The resblocks keep fp16 streams
-                    # started from the f32 stage input: conv1 reads the input (4 + 2) or the stream
-                    # (2 + 2); conv2 adds h to the input (2 + 4 + 2) or to the stream in place
-                    # (2 + 2 + 2); the last conv of the three reads the three streams and writes
-                    # their mean as the next layer's bf16 operand (2 + 3 x 2 + 2)
-                    if blk == "noise_res":
-                        per_col = 6 if cv == 1 else 10
-                    elif cv == 1:
-                        per_col = 6 if d == 1 else 4
-                    else:
-                        per_col = 8 if d == 1 else (10 if (k, d) == (11, 5) else 6)
+                    # bytes per column and channel; every stream is fp16: conv1 reads the stream
+                    # (or the stage input) and writes h (2 + 2); conv2 reads h and adds it to the
+                    # stream (or the stage input) into the stream (2 + 2 + 2); the last conv of
+                    # the three resblocks reads the three streams and writes their mean as the next
+                    # layer's bf16 operand (2 + 3 x 2 + 2)
+                    per_col = 4 if cv == 1 else (10 if (blk, k, d) == ("resblock", 11, 5) else 6)
                     by = c * cols * per_col
                     out.append({"name": f"stage{st} {blk} k{k} d{d} conv{cv}", "flop": 2.0 * c * c * k * cols,
                                 "bytes": by})

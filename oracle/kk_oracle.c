@@ -918,7 +918,15 @@ static void resblock_mean(const ko_model* m, int first, const float* y, int t, c
     free(r);
 }
 
-/* Generator stages after the source (src/gpu_batch.rs:358-420), one item, from spec [22][120N+1]. */
+/* With the emulation of the fp16 streams (KO_GROUP_H16): x rounded to fp16 in place. */
+static void round_h16(float* x, size_t n) {
+    if (g_bf16 && (g_groups & KO_GROUP_H16))
+        for (size_t i = 0; i < n; i++) x[i] = ko_fp16_round(x[i]);
+}
+
+/* Generator stages after the source (src/gpu_batch.rs:358-420), one item, from spec [22][120N+1].
+ * The emulation rounds where the HIP path keeps fp16 streams: the noise branches (from the noise
+ * conv's output on) and each stage's input (the ConvT's output plus the noise branch). */
 int ko_generator_from_spec(const ko_model* m, const float* x_in, const float* spec, const float* style, int n,
                            float* audio, float* post_out) {
     if (n <= 0) return -1;
@@ -929,10 +937,12 @@ int ko_generator_from_spec(const ko_model* m, const float* x_in, const float* sp
     leaky_inplace(x, (size_t)512 * l2, 0.1f);
     float* xs = (float*)malloc((size_t)256 * t0 * sizeof(float));
     conv_layer(&m->noise_convs[0], spec, f, xs, t0);
-    snake_block(&m->noise_res[0], xs, t0, style, xs, 0);
+    round_h16(xs, (size_t)256 * t0);
+    snake_block(&m->noise_res[0], xs, t0, style, xs, 3);
     float* y = (float*)malloc((size_t)256 * t0 * sizeof(float));
     convt_layer(&m->ups[0], x, l2, y, t0);
     for (size_t i = 0; i < (size_t)256 * t0; i++) y[i] = y[i] + xs[i];
+    round_h16(y, (size_t)256 * t0);
     float* x1 = (float*)malloc((size_t)256 * t0 * sizeof(float));
     resblock_mean(m, 0, y, t0, style, x1);
     free(x);
@@ -943,7 +953,8 @@ int ko_generator_from_spec(const ko_model* m, const float* x_in, const float* sp
     leaky_inplace(x1, (size_t)256 * t0, 0.1f);
     float* xs1 = (float*)malloc((size_t)128 * t1 * sizeof(float));
     conv_layer(&m->noise_convs[1], spec, f, xs1, t1);
-    snake_block(&m->noise_res[1], xs1, t1, style, xs1, 0);
+    round_h16(xs1, (size_t)128 * t1);
+    snake_block(&m->noise_res[1], xs1, t1, style, xs1, 3);
     float* y0 = (float*)malloc((size_t)128 * (t1 - 1) * sizeof(float));
     convt_layer(&m->ups[1], x1, t0, y0, t1 - 1);
     float* y1 = (float*)malloc((size_t)128 * t1 * sizeof(float));
@@ -955,6 +966,7 @@ int ko_generator_from_spec(const ko_model* m, const float* x_in, const float* sp
         memcpy(dst + 1, src, (size_t)(t1 - 1) * sizeof(float));
     }
     for (size_t i = 0; i < (size_t)128 * t1; i++) y1[i] = y1[i] + xs1[i];
+    round_h16(y1, (size_t)128 * t1);
     float* x2 = (float*)malloc((size_t)128 * t1 * sizeof(float));
     resblock_mean(m, 3, y1, t1, style, x2);
     free(x1);

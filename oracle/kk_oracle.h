@@ -35,8 +35,8 @@ int ko_get_bf16_emulation(void);
 #define KO_GROUP_SNAKE 2
 #define KO_GROUP_POST 4
 #define KO_GROUP_UPS 8
-#define KO_GROUP_H16 16 /* fp16 storage of each Snake step's conv1 output and of the generator
-                           resblocks' running sums */
+#define KO_GROUP_H16 16 /* fp16 storage of each Snake step's conv1 output and of the generator's
+                           streams (noise branches, stage inputs, resblocks' running sums) */
 void ko_set_operand_formats(int groups, int fp16_groups);
 void ko_set_operand_emulation(int fmt, int groups);
 float ko_fp16_round(float x);

@@ -25,16 +25,15 @@ def _write(d, counter, rows):
 def test_snake_layers_bytes_and_flop():
     layers, frames = profsum.snake_layers()
     assert len(layers) == 48 and frames == 13501
-    # the noise resblock's conv1 moves 6 C bytes per column (f32 stream in, fp16 h out), its conv2
-    # 10 C; the resblocks' fp16 streams: conv1 4 C after the first step, conv2 8 C from the stage
-    # input, 6 C in place, the blocks' mean 10 C (three fp16 streams, the fp16 h, the next layer's
-    # bf16 operand out)
+    # fp16 streams throughout: conv1 moves 4 C bytes per column (stream in, fp16 h out), conv2 6 C
+    # (h and the stream in, the stream out), the blocks' mean 10 C (three streams and h in, the
+    # next layer's bf16 operand out)
     c0 = 20 * frames
     first = layers[0]
-    assert first["bytes"] == 256 * c0 * 6 and first["flop"] == 2.0 * 256 * 256 * 7 * c0
-    assert layers[1]["bytes"] == 256 * c0 * 10
+    assert first["bytes"] == 256 * c0 * 4 and first["flop"] == 2.0 * 256 * 256 * 7 * c0
+    assert layers[1]["bytes"] == 256 * c0 * 6
     by = {l["name"]: l["bytes"] / (256 * c0) for l in layers if l["name"].startswith("stage0 resblock k3")}
-    assert by == {"stage0 resblock k3 d1 conv1": 6, "stage0 resblock k3 d1 conv2": 8,
+    assert by == {"stage0 resblock k3 d1 conv1": 4, "stage0 resblock k3 d1 conv2": 6,
                   "stage0 resblock k3 d3 conv1": 4, "stage0 resblock k3 d3 conv2": 6,
                   "stage0 resblock k3 d5 conv1": 4, "stage0 resblock k3 d5 conv2": 6}
     means = [l for l in layers if l["name"].endswith("resblock k11 d5 conv2")]
