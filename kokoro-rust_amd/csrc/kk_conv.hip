@@ -270,6 +270,34 @@ __device__ __forceinline__ float4 widen_h4(float4 raw) {
     return make_float4((float)a.x, (float)a.y, (float)b.x, (float)b.y);
 }
 
+// h + v for the four fp16 values of a raw residual (halves 0, 1 in .x, 2, 3 in .y): one
+// v_fma_mix_f32 each, h widened in the instruction, h * one + v with one rounding -- the value that
+// widening h and adding it in f32 gives.  `one` is 1.0 held in a VGPR (a literal 1.0 would turn
+// the fma back into a widen and an add).
+__device__ __forceinline__ float4 add_h4(float4 raw, float4 v, float one) {
+    const f16x2_t a = __builtin_bit_cast(f16x2_t, __float_as_uint(raw.x));
+    const f16x2_t b = __builtin_bit_cast(f16x2_t, __float_as_uint(raw.y));
+    return make_float4(__builtin_fmaf((float)a.x, one, v.x), __builtin_fmaf((float)a.y, one, v.y),
+                       __builtin_fmaf((float)b.x, one, v.z), __builtin_fmaf((float)b.y, one, v.w));
+}
+// The same with both operands raw fp16 residuals.
+__device__ __forceinline__ float4 add_hh4(float4 raw_a, float4 raw_b, float one) {
+    const f16x2_t b0 = __builtin_bit_cast(f16x2_t, __float_as_uint(raw_b.x));
+    const f16x2_t b1 = __builtin_bit_cast(f16x2_t, __float_as_uint(raw_b.y));
+    return add_h4(raw_a, make_float4((float)b0.x, (float)b0.y, (float)b1.x, (float)b1.y), one);
+}
+
+// x / 3 rounded to nearest, equal to the division x / 3.0f for every finite x (checked over all of
+// them, tests/test_div3.py): q = x RN(1/3), the exact remainder r = x - 3 q (one FMA), then
+// Markstein's correction q + r RN(1/3) (one FMA); r = 0 keeps q, and so the sign of a zero.  Three
+// FMA-unit operations and a select instead of the ~10 of a correctly rounded division.
+__device__ __forceinline__ float div3(float x) {
+    constexpr float kThird = 1.0f / 3.0f;
+    const float q = __fmul_rn(x, kThird);
+    const float r = __builtin_fmaf(-3.0f, q, x);
+    return r != 0.0f ? __builtin_fmaf(r, kThird, q) : q;
+}
+
 // Residual operands of output row t, channels m..m+3 (`yo`, `ro`: element offsets from the unit's
 // first row in y and r0..r2).
 template <int EPI, bool OUT_H>
@@ -301,7 +329,7 @@ __device__ __forceinline__ void load_res(const ConvParams& p, const EpiBase& eb,
 // store (the statistics describe these: what the next layer reads).  With fp16 output, `pk` gets
 // the fp16 bits.
 template <int EPI, bool OUT_H>
-__device__ __forceinline__ float4 finish4(const ConvParams& p, float4 v, const float4* r, uint2& pk) {
+__device__ __forceinline__ float4 finish4(const ConvParams& p, float4 v, const float4* r, uint2& pk, float one) {
     if constexpr (EPI == EPI_GELU_BF16) {
         // gelu_new x (1 + tanh u) / 2, u = sqrt(2 / pi) (x + 0.044715 x^3), once per element, as
         // x sigmoid(2 u) = x / (1 + 2^(-2 u log2 e)): one exp2 and one reciprocal (~1 ulp each, far
@@ -322,9 +350,8 @@ __device__ __forceinline__ float4 finish4(const ConvParams& p, float4 v, const f
         // ((rb0 + rb1) + (rb2_resid + conv)) / 3 (src/gpu_batch.rs:395-401) from the three fp16
         // residual streams, then the next layer's prologue (leaky ReLU, round to nearest even bf16):
         // the same operand bits that layer's PRO_LEAKY staging would produce
-        const float4 a = widen_h4(r[0]), b1 = widen_h4(r[1]), c = widen_h4(r[2]);
-        const float o[4] = {((a.x + b1.x) + (c.x + v.x)) / 3.0f, ((a.y + b1.y) + (c.y + v.y)) / 3.0f,
-                            ((a.z + b1.z) + (c.z + v.z)) / 3.0f, ((a.w + b1.w) + (c.w + v.w)) / 3.0f};
+        const float4 ab = add_hh4(r[0], r[1], one), cv = add_h4(r[2], v, one);
+        const float o[4] = {div3(ab.x + cv.x), div3(ab.y + cv.y), div3(ab.z + cv.z), div3(ab.w + cv.w)};
         const float slope = p.slope;
         float w[4];
 #pragma unroll
@@ -341,9 +368,13 @@ __device__ __forceinline__ float4 finish4(const ConvParams& p, float4 v, const f
     float4 o = v;
     if constexpr (EPI == EPI_ACCUM || EPI == EPI_ADD_FROM) {
         // an fp16 residual stream: the sum in f32, stored rounded to fp16 (statistics as above)
-        const float4 y = OUT_H ? widen_h4(r[0]) : r[0];
-        o = make_float4(y.x + v.x, y.y + v.y, y.z + v.z, y.w + v.w);
-        if constexpr (OUT_H) pk = make_uint2(pack_f16x2(o.x, o.y), pack_f16x2(o.z, o.w));
+        if constexpr (OUT_H) {
+            o = add_h4(r[0], v, one);
+            pk = make_uint2(pack_f16x2(o.x, o.y), pack_f16x2(o.z, o.w));
+        } else {
+            const float4 y = r[0];
+            o = make_float4(y.x + v.x, y.y + v.y, y.z + v.z, y.w + v.w);
+        }
     } else if constexpr (EPI == EPI_RESID || EPI == EPI_RESID_UP2) {
         const float4 y = r[0];
         const float s = p.scale;
@@ -479,6 +510,7 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
     constexpr int BPS = 8 / QB, NB = 4 * BPS;
     constexpr int LEAD = NR > 0 ? 1 : 0, RING = LEAD + 1;
     float4 res[RING][QB][NRA];
+    const float one = CONVT ? 1.0f : vgpr_f(1.0f);  // the fp16 residuals' fma_mix multiplier (add_h4)
     // unconditional loads (invalid columns / rows read column 0 / row 0 of the tile)
     auto issue = [&](int b) {
         const int j = b / BPS, q0 = (b % BPS) * QB;
@@ -551,6 +583,7 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
                     bool ok;
                     const int64_t d = convt_dest(col, ok);
                     const float4 w = make_float4(v[qq].x + cb.x, v[qq].y + cb.y, v[qq].z + cb.z, v[qq].w + cb.w);
+                    // (the noise stream widened here: an fma_mix multiplier register would spill)
                     const float4 r = OUT_H ? widen_h4(rc[qq][0]) : rc[qq][0];
                     o = make_float4(w.x + r.x, w.y + r.y, w.z + r.z, w.w + r.w);
                     valid = ok;
@@ -567,7 +600,7 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
                     if constexpr (STATS) cnt += ok ? 1.f : 0.f;
                 } else {
                     uint2 pk;  // v = conv + bias (the accumulators started at the bias)
-                    o = finish4<EPI, OUT_H>(p, v[qq], rc[qq], pk);
+                    o = finish4<EPI, OUT_H>(p, v[qq], rc[qq], pk, one);
                     store4<OUT_H>(eb, yo0 + __umul24(j * 32 + 4 * q, yld), valid && mok, o, pk);
                 }
                 if constexpr (STATS) {
