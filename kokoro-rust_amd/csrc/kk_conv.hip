@@ -503,6 +503,13 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
     const uint32_t yo0 = (uint32_t)(wcol0 + cg) * yld + m, ro0 = (uint32_t)(wcol0 + cg) * rld + m;
     const uint32_t yz = u.m0, rz = u.m0;  // clamped operand of an invalid row: row 0 of the unit
     float s1[4] = {0.f, 0.f, 0.f, 0.f}, s2[4] = {0.f, 0.f, 0.f, 0.f}, sft[4] = {0.f, 0.f, 0.f, 0.f};
+    // fp16 outputs (h and the generator's streams): the statistics of the stored fp16 values, two
+    // columns of a channel per instruction -- the pair's shifted values d (v_pk_add_f16; exact
+    // when a value is within a factor 2 of the shift, else rounded to fp16), then sum d and sum d^2
+    // accumulated in f32 by v_dot2c_f32_f16 (products exact) -- 2 instructions per value instead of
+    // 3 in f32
+    constexpr bool HSTATS = STATS && OUT_H && !CONVT;
+    f16x2_t sftp[4] = {};  // the shift of channel r, in both halves
     float cnt = 0.f;  // ConvT: rows this lane group wrote (the statistics' count)
     // Batches of QB column groups, BPS per 32-column slice.  The residual loads of batch b + LEAD are
     // issued before batch b's stores: vector-memory counters complete in issue order (stores
@@ -571,6 +578,8 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
                         }
                     }
             }
+            uint2 pkq[QB];  // HSTATS: each column group's stored fp16 values
+            bool vq[QB];
 #pragma unroll
             for (int qq = 0; qq < QB; qq++) {
                 const int q = q0 + qq;
@@ -602,8 +611,38 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
                     uint2 pk;  // v = conv + bias (the accumulators started at the bias)
                     o = finish4<EPI, OUT_H>(p, v[qq], rc[qq], pk, one);
                     store4<OUT_H>(eb, yo0 + __umul24(j * 32 + 4 * q, yld), valid && mok, o, pk);
+                    pkq[qq] = pk, vq[qq] = valid;
+                    if constexpr (HSTATS) {
+                        if (j == 0 && q == 0) {  // the wave's first column: lanes cq of lane group 0
+                            const f16x2_t h01 = __builtin_bit_cast(f16x2_t, (uint32_t)__shfl((int)pk.x, cq, 64));
+                            const f16x2_t h23 = __builtin_bit_cast(f16x2_t, (uint32_t)__shfl((int)pk.y, cq, 64));
+                            sftp[0] = __builtin_shufflevector(h01, h01, 0, 0);
+                            sftp[1] = __builtin_shufflevector(h01, h01, 1, 1);
+                            sftp[2] = __builtin_shufflevector(h23, h23, 0, 0);
+                            sftp[3] = __builtin_shufflevector(h23, h23, 1, 1);
+#pragma unroll
+                            for (int r = 0; r < 4; r++) sft[r] = (float)sftp[r].x;
+                        }
+                        if (qq % 2 == 1) {  // the pair (qq - 1, qq): channel r of the two columns
+                            const f16x2_t a01 = __builtin_bit_cast(f16x2_t, pkq[qq - 1].x);
+                            const f16x2_t a23 = __builtin_bit_cast(f16x2_t, pkq[qq - 1].y);
+                            const f16x2_t b01 = __builtin_bit_cast(f16x2_t, pk.x), b23 = __builtin_bit_cast(f16x2_t, pk.y);
+                            f16x2_t d[4] = {__builtin_shufflevector(a01, b01, 0, 2), __builtin_shufflevector(a01, b01, 1, 3),
+                                            __builtin_shufflevector(a23, b23, 0, 2), __builtin_shufflevector(a23, b23, 1, 3)};
+                            const uint32_t keep = (vq[qq - 1] ? 0x0000ffffu : 0u) | (valid ? 0xffff0000u : 0u);
+                            const f16x2_t one2 = {(_Float16)1.0f, (_Float16)1.0f};
+#pragma unroll
+                            for (int r = 0; r < 4; r++) {
+                                d[r] = d[r] - sftp[r];
+                                if constexpr (!FULL)
+                                    d[r] = __builtin_bit_cast(f16x2_t, __builtin_bit_cast(uint32_t, d[r]) & keep);
+                                s1[r] = __builtin_amdgcn_fdot2(d[r], one2, s1[r], false);
+                                s2[r] = __builtin_amdgcn_fdot2(d[r], d[r], s2[r], false);
+                            }
+                        }
+                    }
                 }
-                if constexpr (STATS) {
+                if constexpr (STATS && !HSTATS) {
                     const float ov[4] = {o.x, o.y, o.z, o.w};
 #pragma unroll
                     for (int r = 0; r < 4; r++) {
