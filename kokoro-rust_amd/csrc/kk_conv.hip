@@ -359,8 +359,8 @@ __device__ __forceinline__ float4 finish4(const ConvParams& p, float4 v, const f
         pk = make_uint2(pack_bf16x2(w[0], w[1]), pack_bf16x2(w[2], w[3]));
         return make_float4(o[0], o[1], o[2], o[3]);
     } else if constexpr (OUT_H && EPI == EPI_STORE) {
-        // fp16 storage; the statistics use the f32 values, as the reference's f32 h does (the fp16
-        // rounding would move the mean and variance by ~2^-12 relative, far below the next
+        // fp16 storage; the statistics describe the stored fp16 values (what the next layer reads;
+        // ~2^-12 relative from the f32 values the reference's f32 h would give, far below the next
         // layer's bf16 operand rounding)
         pk = make_uint2(pack_f16x2(v.x, v.y), pack_f16x2(v.z, v.w));
         return v;
