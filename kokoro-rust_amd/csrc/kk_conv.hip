@@ -466,7 +466,7 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
         cg_.ph = mm / p.cout, cg_.co = mm - cg_.ph * p.cout;
         cb = *(const float4*)(p.bias + cg_.co);
         // rows o >= stride n0 - pad (o + 1 with the reflection pad), and the item's first row when
-        // the unit writes o = os + 1 (then stride n0 - pad - 1 <= os)
+        // the unit writes o = os + 1 (then stride n0 - pad - 1 <= os); as convt_cols computes it
         ubase = max(cg_.os, (int64_t)p.stride_t * u.n0 - p.pad_t - 1);
         // the reflected row's residual: r0 at the item's first row
         if constexpr (EPI == EPI_CONVT_REFLECT) {
@@ -477,12 +477,18 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
         }
         ready(cb);
     }
-    // ConvT output column of tile column col, whether this lane writes it, and the row written
-    auto convt_dest = [&](int col, bool& ok) -> int64_t {
-        const int64_t o = (int64_t)p.stride_t * (u.n0 + col) + cg_.ph - p.pad_t;
-        ok = col < u.nv && mok && o >= cg_.os && o < cg_.os + cg_.ol;
-        return ok ? (EPI == EPI_CONVT ? o : o + 1) : cg_.os;
-    };
+    // ConvT: the columns this lane writes, [ct_lo, ct_hi), and each one's row relative to ubase,
+    // ct_rel0 + stride col (kk_walk.h convt_cols, checked on the CPU): per column two 32-bit
+    // compares and a multiply-add.  Other columns read the residual at row ubase and store nothing.
+    int ct_lo = 0, ct_hi = 0, ct_rel0 = 0, ct_refl = -1, ct_st = 0;
+    if constexpr (CONVT) {
+        ct_st = vgpr(p.stride_t);
+        const ConvTCols cc = convt_cols(u.n0, u.nv, p.stride_t, p.pad_t, cg_.ph, cg_.os, cg_.ol,
+                                        EPI == EPI_CONVT_REFLECT, mok);
+        ct_lo = cc.lo, ct_hi = cc.hi, ct_rel0 = cc.rel0, ct_refl = cc.refl;
+    }
+    auto ct_ok = [&](int col) { return col >= ct_lo && col < ct_hi; };
+    auto ct_row = [&](int col, bool ok) { return ok ? ct_rel0 + ct_st * col : 0; };  // relative to ubase
     // Row pointers at the unit's first row (uniform) and this lane's 32-bit element offsets of its
     // first output row (column wcol0 + cg); row wcol0 + cg + c adds c * ld, one 24-bit multiply
     // with ld held in a VGPR (uniform products of every c would occupy scalar registers).
@@ -518,6 +524,9 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
     constexpr int LEAD = NR > 0 ? 1 : 0, RING = LEAD + 1;
     float4 res[RING][QB][NRA];
     const float one = CONVT ? 1.0f : vgpr_f(1.0f);  // the fp16 residuals' fma_mix multiplier (add_h4)
+    // ConvT: the residual from the unit's first writable row (its element type as y's)
+    const float* ct_r0 = !CONVT ? nullptr
+                         : OUT_H ? (const float*)((const uint16_t*)p.r0 + ubase * p.r0_ld) : p.r0 + ubase * p.r0_ld;
     // unconditional loads (invalid columns / rows read column 0 / row 0 of the tile)
     auto issue = [&](int b) {
         const int j = b / BPS, q0 = (b % BPS) * QB;
@@ -525,12 +534,12 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
         for (int qq = 0; qq < QB; qq++) {
             const int c = j * 32 + 4 * (q0 + qq);
             if constexpr (CONVT) {
-                bool ok;
-                const int64_t d = convt_dest(wcol0 + c + cg, ok);
+                const int col = wcol0 + c + cg;
+                const uint32_t off = (uint32_t)ct_row(col, ct_ok(col)) * rld + (uint32_t)cg_.co;
                 if constexpr (OUT_H)
-                    res[b % RING][qq][0] = raw_h4(*(const uint2*)((const uint16_t*)p.r0 + d * p.r0_ld + cg_.co));
+                    res[b % RING][qq][0] = raw_h4(*(const uint2*)((const uint16_t*)ct_r0 + off));
                 else
-                    res[b % RING][qq][0] = *(const float4*)(p.r0 + d * p.r0_ld + cg_.co);
+                    res[b % RING][qq][0] = *(const float4*)(ct_r0 + off);
             } else {
                 const bool ok = FULL || (wcol0 + c + cg < u.nv && mok);
                 load_res<EPI, OUT_H>(p, eb, ok ? yo0 + __umul24(c, yld) : yz, ok ? ro0 + __umul24(c, rld) : rz,
@@ -589,8 +598,8 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
                 // only the store is conditional
                 float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
                 if constexpr (CONVT) {
-                    bool ok;
-                    const int64_t d = convt_dest(col, ok);
+                    const bool ok = ct_ok(col);
+                    const uint32_t orow = (uint32_t)ct_row(col, ok);
                     const float4 w = make_float4(v[qq].x + cb.x, v[qq].y + cb.y, v[qq].z + cb.z, v[qq].w + cb.w);
                     // (the noise stream widened here: an fma_mix multiplier register would spill)
                     const float4 r = OUT_H ? widen_h4(rc[qq][0]) : rc[qq][0];
@@ -598,13 +607,14 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
                     valid = ok;
                     // fp16 output: the stage input of the resblocks' fp16 streams
                     const uint2 pk = OUT_H ? make_uint2(pack_f16x2(o.x, o.y), pack_f16x2(o.z, o.w)) : make_uint2(0u, 0u);
-                    store4<OUT_H>(eb, (uint32_t)((d - ubase) * p.y_ld) + cg_.co, ok, o, pk);
+                    store4<OUT_H>(eb, orow * yld + (uint32_t)cg_.co, ok, o, pk);
                     if constexpr (EPI == EPI_CONVT_REFLECT) {
                         // o = os + 1 also fills the item's first row (the reflected sample)
                         // (the statistics leave this row to finalize, which reads it back)
                         const float4 f = make_float4(w.x + rfl.x, w.y + rfl.y, w.z + rfl.z, w.w + rfl.w);
                         const uint2 fk = OUT_H ? make_uint2(pack_f16x2(f.x, f.y), pack_f16x2(f.z, f.w)) : make_uint2(0u, 0u);
-                        store4<OUT_H>(eb, (uint32_t)((cg_.os - ubase) * p.y_ld) + cg_.co, ok && d == cg_.os + 2, f, fk);
+                        // (ct_refl >= 0 only in the unit whose first row is os: ubase = os there)
+                        store4<OUT_H>(eb, (uint32_t)cg_.co, col == ct_refl, f, fk);
                     }
                     if constexpr (STATS) cnt += ok ? 1.f : 0.f;
                 } else {

@@ -56,4 +56,35 @@ inline int64_t walk_grid(int64_t count, int mblocks, int n_cu) {
     return units < fit ? units : fit;
 }
 
+// A ConvT unit's columns (EPI_CONVT / EPI_CONVT_REFLECT): tile column col (of nv valid, from input
+// column n0) is output row o = stride (n0 + col) + ph - pad, written -- as row o, or o + 1 with the
+// reflection pad -- when o lies in the item's output span [os, os + ol) (ol without the reflected
+// row); rows are addressed from ubase = max(os, stride n0 - pad - 1).  The columns written are
+// [lo, hi); column col's row relative to ubase is rel0 + stride col; refl is the column whose row
+// is os + 1 with the reflection pad (it also fills row os, then = ubase), or -1.  mok: this lane's
+// output channels exist (else no column is written).
+struct ConvTCols {
+    int lo, hi, rel0, refl;
+    int64_t ubase;
+};
+__host__ __device__ inline ConvTCols convt_cols(int64_t n0, int nv, int stride, int pad, int ph, int64_t os, int64_t ol,
+                                                bool reflect, bool mok) {
+    const int64_t st = stride, o0 = st * n0 + ph - pad;  // the row of column 0
+    auto ceil_div = [](int64_t a, int64_t b) { return a >= 0 ? (a + b - 1) / b : -((-a) / b); };  // b > 0
+    ConvTCols c;
+    c.ubase = os > st * n0 - pad - 1 ? os : st * n0 - pad - 1;
+    int64_t lo = ceil_div(os - o0, st), hi = ceil_div(os + ol - o0, st);
+    lo = lo > 0 ? lo : 0;
+    hi = hi < nv ? hi : nv;
+    c.lo = (int)lo;
+    c.hi = mok && hi > lo ? (int)hi : (int)lo;
+    c.rel0 = (int)(o0 + (reflect ? 1 : 0) - c.ubase);
+    c.refl = -1;
+    if (reflect) {
+        const int64_t a = os + 1 - o0;
+        if (a >= 0 && a % st == 0 && a / st >= c.lo && a / st < c.hi) c.refl = (int)(a / st);
+    }
+    return c;
+}
+
 }  // namespace kk

@@ -116,8 +116,45 @@ static long check(int64_t count, int mblocks, int k, int nsl, int64_t grid) {
     return bad;
 }
 
+// convt_cols against the per-column rule it replaces: tile column col writes output row o =
+// stride (n0 + col) + ph - pad (o + 1 with the reflection pad) when col < nv, the lane's channels
+// exist and os <= o < os + ol; written rows relative to ubase are non-negative; the reflected
+// column is the one writing row os + 1 (reflection pad) and then ubase = os.
+static long check_convt_cols() {
+    long bad = 0;
+    uint64_t st64 = 0x2545F4914F6CDD1Dull;
+    auto rnd = [&](int64_t n) { st64 = st64 * 6364136223846793005ull + 1442695040888963407ull; return (int64_t)((st64 >> 33) % (uint64_t)n); };
+    for (int it = 0; it < 200000; it++) {
+        const int stride = rnd(2) ? 6 : 10, pad = (int)(2 + rnd(6)), ph = (int)rnd(stride), nv = (int)rnd(129);
+        const bool reflect = rnd(2), mok = rnd(10) != 0;
+        const int64_t n0 = rnd(100000);
+        int64_t os = stride * n0 - pad + rnd(41) - 20;
+        if (os < 0) os = 0;
+        const int64_t ol = 1 + rnd(3000);
+        const kk::ConvTCols c = kk::convt_cols(n0, nv, stride, pad, ph, os, ol, reflect, mok);
+        if (c.ubase != (os > stride * n0 - pad - 1 ? os : stride * n0 - pad - 1)) bad++;
+        for (int col = 0; col < 128; col++) {
+            const int64_t o = (int64_t)stride * (n0 + col) + ph - pad;
+            const bool ok = col < nv && mok && o >= os && o < os + ol;
+            if (ok != (col >= c.lo && col < c.hi)) bad++;
+            if (ok) {
+                const int64_t rel = (reflect ? o + 1 : o) - c.ubase;
+                if (rel < 0 || rel != (int64_t)c.rel0 + (int64_t)stride * col) bad++;
+            }
+            if (reflect && (ok && o == os + 1) != (col == c.refl)) bad++;
+        }
+        if (c.refl >= 0 && c.ubase != os) bad++;
+    }
+    return bad;
+}
+
 int main(int argc, char** argv) {
     plant = argc > 1 && std::strcmp(argv[1], "--plant") == 0;
+    if (!plant) {
+        const long bc = check_convt_cols();
+        std::printf("convt columns violations %ld\n", bc);
+        if (bc) return 1;
+    }
     const int64_t counts[] = {1, 2, 7, 8, 9, 17, 64, 257, 1000};
     const int mbs[] = {1, 2, 3, 4};
     const int ks[] = {1, 2, 3, 5, 7, 11, 12};
