@@ -37,7 +37,7 @@ enum Epilogue {
     EPI_ACCUM = 1,          // y += conv + b (y fp16, read and written, when the output is fp16)
     EPI_RESID = 2,          // y = (conv + b + y) * scale
     EPI_RESID_UP2 = 3,      // y = (conv + b + r0[t/2]) * scale
-    EPI_ADD_FROM = 4,       // y = r0 + (conv + b) (r0 f32; y f32 or fp16)
+    EPI_ADD_FROM = 4,       // y = r0 + (conv + b) (r0 and y f32, or both fp16 with an fp16 output)
     EPI_CONVT = 6,          // polyphase ConvT scatter, y[o] = conv + b + r0[o]
     EPI_CONVT_REFLECT = 7,  // ConvT scatter with per-item ReflectionPad1d((1,0)), + r0
     EPI_GELU_BF16 = 8,      // y (bf16) = gelu_new(conv + b) (kernels/kokoro.cu:84-90), 2-byte output
