@@ -288,14 +288,16 @@ __device__ __forceinline__ float4 add_hh4(float4 raw_a, float4 raw_b, float one)
 }
 
 // x / 3 rounded to nearest, equal to the division x / 3.0f for every finite x (checked over all of
-// them, tests/test_div3.py): q = x RN(1/3), the exact remainder r = x - 3 q (one FMA), then
-// Markstein's correction q + r RN(1/3) (one FMA); r = 0 keeps q, and so the sign of a zero.  Three
-// FMA-unit operations and a select instead of the ~10 of a correctly rounded division.
+// them, tests/test_div3.py): q = x RN(1/3), the exact remainder as n = 3 q - x (one FMA), then
+// Markstein's correction q - n RN(1/3) (one FMA).  The remainder is taken negated so that a zero
+// x keeps its sign: x = -0 gives q = -0, n = +0 and -0 + -0 = -0 (with r = x - 3 q, r = +0 and
+// the correction would give +0).  Three FMA-unit operations instead of the ~10 of a correctly
+// rounded division.
 __device__ __forceinline__ float div3(float x) {
     constexpr float kThird = 1.0f / 3.0f;
     const float q = __fmul_rn(x, kThird);
-    const float r = __builtin_fmaf(-3.0f, q, x);
-    return r != 0.0f ? __builtin_fmaf(r, kThird, q) : q;
+    const float n = __builtin_fmaf(3.0f, q, -x);
+    return __builtin_fmaf(-n, kThird, q);
 }
 
 // Residual operands of output row t, channels m..m+3 (`yo`, `ro`: element offsets from the unit's
@@ -352,10 +354,12 @@ __device__ __forceinline__ float4 finish4(const ConvParams& p, float4 v, const f
         // the same operand bits that layer's PRO_LEAKY staging would produce
         const float4 ab = add_hh4(r[0], r[1], one), cv = add_h4(r[2], v, one);
         const float o[4] = {div3(ab.x + cv.x), div3(ab.y + cv.y), div3(ab.z + cv.z), div3(ab.w + cv.w)};
+        // leaky ReLU as max(o, slope o): equal to o < 0 ? slope o : o for 0 < slope <= 1 (the
+        // launch refuses other slopes), zeros' signs included
         const float slope = p.slope;
         float w[4];
 #pragma unroll
-        for (int e = 0; e < 4; e++) w[e] = o[e] < 0.f ? o[e] * slope : o[e];
+        for (int e = 0; e < 4; e++) w[e] = __builtin_fmaxf(o[e], o[e] * slope);
         pk = make_uint2(pack_bf16x2(w[0], w[1]), pack_bf16x2(w[2], w[3]));
         return make_float4(o[0], o[1], o[2], o[3]);
     } else if constexpr (OUT_H && EPI == EPI_STORE) {
@@ -400,6 +404,20 @@ __device__ __forceinline__ void store4(const EpiBase& eb, uint32_t yo, bool ok, 
     typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
     typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
     const uint32_t off = ok ? yo * (OUT_H ? 2u : 4u) : kDropOffset;
+    if constexpr (OUT_H) {
+        __builtin_amdgcn_raw_buffer_store_b64((u32x2_t){pk.x, pk.y}, eb.ry, (int)off, 0, kCpolNT);
+    } else {
+        __builtin_amdgcn_raw_buffer_store_b128(
+            (u32x4_t){__float_as_uint(o.x), __float_as_uint(o.y), __float_as_uint(o.z), __float_as_uint(o.w)}, eb.ry,
+            (int)off, 0, kCpolNT);
+    }
+}
+
+// store4 with the byte offset given (kDropOffset: no store)
+template <bool OUT_H>
+__device__ __forceinline__ void store4b(const EpiBase& eb, uint32_t off, float4 o, uint2 pk) {
+    typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+    typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
     if constexpr (OUT_H) {
         __builtin_amdgcn_raw_buffer_store_b64((u32x2_t){pk.x, pk.y}, eb.ry, (int)off, 0, kCpolNT);
     } else {
@@ -477,18 +495,29 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
         }
         ready(cb);
     }
-    // ConvT: the columns this lane writes, [ct_lo, ct_hi), and each one's row relative to ubase,
-    // ct_rel0 + stride col (kk_walk.h convt_cols, checked on the CPU): per column two 32-bit
-    // compares and a multiply-add.  Other columns read the residual at row ubase and store nothing.
-    int ct_lo = 0, ct_hi = 0, ct_rel0 = 0, ct_refl = -1, ct_st = 0;
+    // ConvT: the columns this lane writes, [lo, hi), and each one's row relative to ubase,
+    // rel0 + stride col (kk_walk.h convt_cols, checked on the CPU).  The lane's columns are
+    // wcol0 + cg + 4 k for k = 8 j + q < 32, so the valid ones are k in [ct_klo, ct_klo + ct_kn)
+    // (one subtract and one unsigned compare per column), and column k's element offsets in y and
+    // r0 are ct_y0 + k ct_dy and ct_q0 + k ct_dq (ct_dy, ct_dq uniform: one add per column).
+    // Other columns store nothing and read the residual at the unit's first row.
+    // ct_krefl: the k whose column also fills the item's first row (the reflection pad), or -1.
+    int ct_klo = 0, ct_kn = 0, ct_krefl = -1;
+    uint32_t ct_y0 = 0, ct_q0 = 0, ct_dy = 0, ct_dq = 0;
     if constexpr (CONVT) {
-        ct_st = vgpr(p.stride_t);
         const ConvTCols cc = convt_cols(u.n0, u.nv, p.stride_t, p.pad_t, cg_.ph, cg_.os, cg_.ol,
                                         EPI == EPI_CONVT_REFLECT, mok);
-        ct_lo = cc.lo, ct_hi = cc.hi, ct_rel0 = cc.rel0, ct_refl = cc.refl;
+        const int bcol = wcol0 + cg;
+        const int klo = min(max((cc.lo - bcol + 3) >> 2, 0), 32);  // ceil((lo - bcol) / 4), clamped
+        const int khi = min(max((cc.hi - bcol + 3) >> 2, 0), 32);
+        ct_klo = klo, ct_kn = max(khi - klo, 0);
+        if (cc.refl >= bcol && cc.refl - bcol < 128 && ((cc.refl - bcol) & 3) == 0) ct_krefl = (cc.refl - bcol) >> 2;
+        const uint32_t row0 = (uint32_t)(cc.rel0 + p.stride_t * bcol);  // column k = 0 (wraps when invalid)
+        ct_y0 = row0 * (uint32_t)p.y_ld + (uint32_t)cg_.co, ct_q0 = row0 * (uint32_t)p.r0_ld + (uint32_t)cg_.co;
+        ct_dy = 4u * (uint32_t)p.stride_t * (uint32_t)p.y_ld, ct_dq = 4u * (uint32_t)p.stride_t * (uint32_t)p.r0_ld;
     }
-    auto ct_ok = [&](int col) { return col >= ct_lo && col < ct_hi; };
-    auto ct_row = [&](int col, bool ok) { return ok ? ct_rel0 + ct_st * col : 0; };  // relative to ubase
+    // (FULL ConvT units lie inside their item's span with every row valid: all 32 columns write)
+    auto ct_ok = [&](int k) { return FULL || (uint32_t)(k - ct_klo) < (uint32_t)ct_kn; };
     // Row pointers at the unit's first row (uniform) and this lane's 32-bit element offsets of its
     // first output row (column wcol0 + cg); row wcol0 + cg + c adds c * ld, one 24-bit multiply
     // with ld held in a VGPR (uniform products of every c would occupy scalar registers).
@@ -523,10 +552,15 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
     constexpr int BPS = 8 / QB, NB = 4 * BPS;
     constexpr int LEAD = NR > 0 ? 1 : 0, RING = LEAD + 1;
     float4 res[RING][QB][NRA];
-    const float one = CONVT ? 1.0f : vgpr_f(1.0f);  // the fp16 residuals' fma_mix multiplier (add_h4)
-    // ConvT: the residual from the unit's first writable row (its element type as y's)
-    const float* ct_r0 = !CONVT ? nullptr
-                         : OUT_H ? (const float*)((const uint16_t*)p.r0 + ubase * p.r0_ld) : p.r0 + ubase * p.r0_ld;
+    const float one = vgpr_f(1.0f);  // the fp16 residuals' fma_mix multiplier (add_h4)
+    // ConvT: the residual from the unit's first writable row (its element type as y's), as a raw
+    // buffer
+    const __amdgpu_buffer_rsrc_t ct_r0 = __builtin_amdgcn_make_buffer_rsrc(
+        !CONVT ? nullptr
+        : OUT_H ? (void*)((const uint16_t*)p.r0 + ubase * p.r0_ld)
+                : (void*)(p.r0 + ubase * p.r0_ld),
+        0, kBufRecords, kBufFormat);
+    float4 ct_rsv = make_float4(0.f, 0.f, 0.f, 0.f);  // REFLECT: conv + bias of column ct_krefl
     // unconditional loads (invalid columns / rows read column 0 / row 0 of the tile)
     auto issue = [&](int b) {
         const int j = b / BPS, q0 = (b % BPS) * QB;
@@ -534,12 +568,19 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
         for (int qq = 0; qq < QB; qq++) {
             const int c = j * 32 + 4 * (q0 + qq);
             if constexpr (CONVT) {
-                const int col = wcol0 + c + cg;
-                const uint32_t off = (uint32_t)ct_row(col, ct_ok(col)) * rld + (uint32_t)cg_.co;
-                if constexpr (OUT_H)
-                    res[b % RING][qq][0] = raw_h4(*(const uint2*)((const uint16_t*)ct_r0 + off));
-                else
-                    res[b % RING][qq][0] = *(const float4*)(ct_r0 + off);
+                typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+                typedef float f32x4_t __attribute__((ext_vector_type(4)));
+                const int k = c / 4;
+                // (an invalid column reads the unit's first row: its value can still be the
+                // statistics' shift, which should be near the data)
+                const uint32_t off = (ct_ok(k) ? ct_q0 + (uint32_t)k * ct_dq : (uint32_t)cg_.co) * (OUT_H ? 2u : 4u);
+                if constexpr (OUT_H) {
+                    const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(ct_r0, (int)off, 0, 0);
+                    res[b % RING][qq][0] = raw_h4(make_uint2(v.x, v.y));
+                } else {
+                    const f32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(ct_r0, (int)off, 0, 0);
+                    res[b % RING][qq][0] = make_float4(v.x, v.y, v.z, v.w);
+                }
             } else {
                 const bool ok = FULL || (wcol0 + c + cg < u.nv && mok);
                 load_res<EPI, OUT_H>(p, eb, ok ? yo0 + __umul24(c, yld) : yz, ok ? ro0 + __umul24(c, rld) : rz,
@@ -598,23 +639,21 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
                 // only the store is conditional
                 float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
                 if constexpr (CONVT) {
-                    const bool ok = ct_ok(col);
-                    const uint32_t orow = (uint32_t)ct_row(col, ok);
+                    const int k = 8 * j + q;
+                    const bool ok = ct_ok(k);
                     const float4 w = make_float4(v[qq].x + cb.x, v[qq].y + cb.y, v[qq].z + cb.z, v[qq].w + cb.w);
-                    // (the noise stream widened here: an fma_mix multiplier register would spill)
-                    const float4 r = OUT_H ? widen_h4(rc[qq][0]) : rc[qq][0];
-                    o = make_float4(w.x + r.x, w.y + r.y, w.z + r.z, w.w + r.w);
+                    if constexpr (OUT_H) {
+                        o = add_h4(rc[qq][0], w, one);  // + the fp16 noise stream
+                    } else {
+                        const float4 r = rc[qq][0];
+                        o = make_float4(w.x + r.x, w.y + r.y, w.z + r.z, w.w + r.w);
+                    }
                     valid = ok;
                     // fp16 output: the stage input of the resblocks' fp16 streams
                     const uint2 pk = OUT_H ? make_uint2(pack_f16x2(o.x, o.y), pack_f16x2(o.z, o.w)) : make_uint2(0u, 0u);
-                    store4<OUT_H>(eb, orow * yld + (uint32_t)cg_.co, ok, o, pk);
-                    if constexpr (EPI == EPI_CONVT_REFLECT) {
-                        // o = os + 1 also fills the item's first row (the reflected sample)
-                        // (the statistics leave this row to finalize, which reads it back)
-                        const float4 f = make_float4(w.x + rfl.x, w.y + rfl.y, w.z + rfl.z, w.w + rfl.w);
-                        const uint2 fk = OUT_H ? make_uint2(pack_f16x2(f.x, f.y), pack_f16x2(f.z, f.w)) : make_uint2(0u, 0u);
-                        // (ct_refl >= 0 only in the unit whose first row is os: ubase = os there)
-                        store4<OUT_H>(eb, (uint32_t)cg_.co, col == ct_refl, f, fk);
+                    store4b<OUT_H>(eb, ok ? (ct_y0 + (uint32_t)k * ct_dy) * (OUT_H ? 2u : 4u) : kDropOffset, o, pk);
+                    if constexpr (EPI == EPI_CONVT_REFLECT && !FULL) {
+                        if (k == ct_krefl) ct_rsv = w;  // stored after the last column
                     }
                     if constexpr (STATS) cnt += ok ? 1.f : 0.f;
                 } else {
@@ -665,6 +704,14 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
             }
         }
         if (b % BPS == BPS - 1) __builtin_amdgcn_wave_barrier();  // the slice's LDS reads before the next writes
+    }
+    if constexpr (EPI == EPI_CONVT_REFLECT && !FULL) {
+        // column ct_krefl (o = os + 1) also fills the item's first row (the reflected sample): its
+        // conv + bias plus r0 at that row; ct_krefl >= 0 only in the unit whose first row is os
+        // (ubase = os there).  The statistics leave this row to finalize, which reads it back.
+        const float4 f = make_float4(ct_rsv.x + rfl.x, ct_rsv.y + rfl.y, ct_rsv.z + rfl.z, ct_rsv.w + rfl.w);
+        const uint2 fk = OUT_H ? make_uint2(pack_f16x2(f.x, f.y), pack_f16x2(f.z, f.w)) : make_uint2(0u, 0u);
+        store4b<OUT_H>(eb, ct_krefl >= 0 ? (uint32_t)cg_.co * (OUT_H ? 2u : 4u) : kDropOffset, f, fk);
     }
     if constexpr (STATS) {
 #pragma unroll
@@ -900,10 +947,19 @@ __global__ __launch_bounds__(64 * WM * WN + kNP) void conv_mfma_kernel(ConvParam
             const int next_m0 = has_next ? nu.m0 : cu.m0;
             // (not for the 256-channel f32 accumulate-with-statistics variant: a second epilogue copy
             // makes it spill)
-            constexpr bool kFullPath = !CONVT && !(EPI == EPI_ACCUM && !OUT_H && WM == 4 && STATS);
+            constexpr bool kFullPath = !(EPI == EPI_ACCUM && !OUT_H && WM == 4 && STATS);
+            // ConvT: full when every phase's rows of the unit lie inside the item's output span,
+            // at least two rows past its first (so no column writes the reflected row either)
+            bool interior = true;
+            if constexpr (CONVT) {
+                const int64_t os = ld_const(p.out_start, cu.item);
+                const int64_t oe = os + ld_const(p.out_len, cu.item) - (EPI == EPI_CONVT_REFLECT ? 1 : 0);
+                const int64_t o_first = (int64_t)p.stride_t * cu.n0 - p.pad_t;
+                interior = o_first >= os + 2 && o_first + (int64_t)p.stride_t * cu.nv <= oe;
+            }
             if constexpr (MI == 1)
                 epilogue_m32<WN>(p, cu, acc, wm, wn, lane, scr, bias_s, next_m0);
-            else if (kFullPath && cu.nv >= wn * 128 + 128 && cu.m0 + BM <= p.m)  // uniform: the common case
+            else if (kFullPath && cu.nv >= wn * 128 + 128 && cu.m0 + BM <= p.m && interior)  // uniform: the common case
                 epilogue<EPI, WM, WN, STATS, OUT_H, true>(p, cu, acc, wm, wn, lane, scr, bias_s, next_m0);
             else
                 epilogue<EPI, WM, WN, STATS, OUT_H, false>(p, cu, acc, wm, wn, lane, scr, bias_s, next_m0);
@@ -932,10 +988,12 @@ hipError_t launch_t(const ConvParams& p, int n_cu, hipStream_t s, bool validate_
     if (p.m_pad % BM != 0 || p.cin_pad % kCK != 0 || halo < 0 || halo > kMaxHalo || !p.bias) return hipErrorInvalidValue;
     if (!CONVT && p.m_pad > kMaxBias) return hipErrorInvalidValue;  // the bias staged in LDS
     if (PRO == PRO_ADAIN_SNAKE && p.cin % kCK != 0) return hipErrorInvalidValue;  // no channel mask there
+    if (EPI == EPI_MEAN3_LEAKY_BF16 && !(p.slope > 0.f && p.slope <= 1.f)) return hipErrorInvalidValue;  // max form
     if (p.l_in >= (int64_t)1 << 30 || p.tiles.count >= (int64_t)1 << 28) return hipErrorInvalidValue;  // 32-bit rows
     // epilogue stores: byte offsets within one unit's rows inside the buffer resource's range
     if (!CONVT && ((int64_t)BN * p.y_ld + p.m_pad) * 4 >= kBufRecords) return hipErrorInvalidValue;
-    if (CONVT && ((int64_t)p.stride_t * (BN + 1) + p.pad_t + 2) * p.y_ld * 4 >= kBufRecords) return hipErrorInvalidValue;
+    if (CONVT && ((int64_t)p.stride_t * (BN + 1) + p.pad_t + 2) * max(p.y_ld, p.r0_ld) * 4 >= kBufRecords)
+        return hipErrorInvalidValue;
     // producer loads: 32-bit byte offsets within one item's rows, rows and channels within the
     // 24-bit multiplier
     if (p.in_max_len * p.x_ld * (PRO != PRO_BF16 && !IN_H ? 4 : 2) >= (int64_t)1 << 32) return hipErrorInvalidValue;

@@ -1,6 +1,7 @@
-"""The conv epilogue's division by 3 (the generator stage means, kk_conv.hip `div3`: one multiply,
-two FMAs and a select in place of a correctly rounded division) equals x / 3.0f for every finite
-float: an exhaustive check of the same arithmetic in C with hardware FMA, on the CPU."""
+"""The conv epilogue's division by 3 (the generator stage means, kk_conv.hip `div3`: one multiply
+and two FMAs in place of a correctly rounded division) equals x / 3.0f for every finite float, and
+its leaky ReLU max(x, slope x) equals x < 0 ? slope x : x for every float at the slopes used: an
+exhaustive check of the same arithmetic in C with hardware FMA, on the CPU."""
 import os
 import subprocess
 
@@ -15,6 +16,7 @@ def test_div3_equals_division_for_every_finite_float(tmp_path):
     r = subprocess.run([exe], capture_output=True, text=True, timeout=600,
                        env=dict(os.environ, OMP_NUM_THREADS=str(min(8, os.cpu_count() or 1))))
     assert r.returncode == 0, r.stderr
-    n, bad = map(int, r.stdout.split())
+    (n, bad), (ln, lbad) = [map(int, line.split()) for line in r.stdout.split("\n")[:2]]
     assert n == 2**32 - 2**24  # every bit pattern but the infinities and NaNs
     assert bad == 0
+    assert ln == 5 * 2**32 and lbad == 0
