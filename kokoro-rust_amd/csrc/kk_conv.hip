@@ -550,7 +550,12 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
     // issued before batch b's stores: vector-memory counters complete in issue order (stores
     // included), so a load issued after a store could only be waited for together with that store.
     constexpr int BPS = 8 / QB, NB = 4 * BPS;
-    constexpr int LEAD = NR > 0 ? 1 : 0, RING = LEAD + 1;
+    // Two batches ahead for the one-residual fp16 epilogues (the ConvTs' noise stream, the
+    // resblocks' fp16 streams: rows read from HBM; the stage-1 ConvT 397 -> 373 us, kernel-only
+    // -0.13 ms on the benchmark configuration), but for the 256-channel accumulate with statistics,
+    // which would spill.
+    constexpr int LEAD = NR > 0 ? ((CONVT || (RES_H && NR == 1 && !(WM == 4 && EPI == EPI_ACCUM && STATS))) ? 2 : 1) : 0;
+    constexpr int RING = LEAD + 1;
     float4 res[RING][QB][NRA];
     const float one = vgpr_f(1.0f);  // the fp16 residuals' fma_mix multiplier (add_h4)
     // ConvT: the residual from the unit's first writable row (its element type as y's), as a raw
