@@ -428,6 +428,7 @@ __device__ __forceinline__ void store4b(const EpiBase& eb, uint32_t off, float4 
 }
 
 constexpr int kScrLd = 64 + 4;  // epilogue LDS scratch row stride (f32): one time column, 64 channels
+constexpr int kScrLd16 = 32 + 2;  // the same in 32-bit words for fp16 values (two buffers fit one f32 one)
 constexpr int kMaxBias = 1152;  // bias vector staged in LDS (output rows, M_pad)
 
 // Starts a unit's accumulators at its bias (stride-1 layers): element 4 g + r of MFMA tile (i, j)
@@ -544,6 +545,7 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
     // accumulated in f32 by v_dot2c_f32_f16 (products exact) -- 2 instructions per value instead of
     // 3 in f32
     constexpr bool HSTATS = STATS && OUT_H && !CONVT;
+    constexpr bool H16T = EPI == EPI_STORE && OUT_H && (HSTATS || !STATS);  // fp16 transpose (below)
     f16x2_t sftp[4] = {};  // the shift of channel r, in both halves
     float cnt = 0.f;  // ConvT: rows this lane group wrote (the statistics' count)
     // Batches of QB column groups, BPS per 32-column slice.  The residual loads of batch b + LEAD are
@@ -597,10 +599,27 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
 #pragma unroll
         for (int b = 0; b < LEAD; b++) issue(b);
     }
+    // Plain fp16 stores (conv1 of the Snake steps: h): the values are rounded to fp16 before the
+    // transpose (what is stored, and what the statistics describe), so a slice takes half the LDS
+    // traffic and two slices fit the scratch: slice j + 1 is written while slice j is read.
+    uint32_t* scr16 = (uint32_t*)scr;
+    auto put16 = [&](int jj) {
+        uint32_t* d = scr16 + (jj & 1) * 32 * kScrLd16 + l32 * kScrLd16 + 2 * lh;
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int g = 0; g < 4; g++)
+                *(uint2*)(d + 16 * i + 4 * g) = make_uint2(pack_f16x2(acc[i][jj][4 * g], acc[i][jj][4 * g + 1]),
+                                                           pack_f16x2(acc[i][jj][4 * g + 2], acc[i][jj][4 * g + 3]));
+    };
+    if constexpr (H16T) {
+        put16(0);
+        __builtin_amdgcn_wave_barrier();  // LDS operations of one wave execute in order
+    }
 #pragma unroll
     for (int b = 0; b < NB; b++) {
         const int j = b / BPS, q0 = (b % BPS) * QB;
-        if (b % BPS == 0) {
+        if (!H16T && b % BPS == 0) {
 #pragma unroll
             for (int i = 0; i < 2; i++)
 #pragma unroll
@@ -615,10 +634,24 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
             }
             // all LDS reads of the batch first, one wait, then the arithmetic and the stores
             float4 v[QB];
+            uint2 v16[QB];
+            if constexpr (H16T) {
+                // this slice's reads, then the next slice's writes into the other buffer (issued
+                // after the reads, so the wait below covers only the reads)
 #pragma unroll
-            for (int qq = 0; qq < QB; qq++) v[qq] = *(const float4*)(scr + (4 * (q0 + qq) + cg) * kScrLd + 4 * cq);
+                for (int qq = 0; qq < QB; qq++)
+                    v16[qq] = *(const uint2*)(scr16 + (j & 1) * 32 * kScrLd16 + (4 * (q0 + qq) + cg) * kScrLd16 + 2 * cq);
+                __builtin_amdgcn_wave_barrier();
+                if (j + 1 < 4 && b % BPS == BPS - 1) put16(j + 1);
+                __builtin_amdgcn_wave_barrier();
 #pragma unroll
-            for (int qq = 0; qq < QB; qq++) ready(v[qq]);
+                for (int qq = 0; qq < QB; qq++) ready(v16[qq].x), ready(v16[qq].y);
+            } else {
+#pragma unroll
+                for (int qq = 0; qq < QB; qq++) v[qq] = *(const float4*)(scr + (4 * (q0 + qq) + cg) * kScrLd + 4 * cq);
+#pragma unroll
+                for (int qq = 0; qq < QB; qq++) ready(v[qq]);
+            }
             float4(&rc)[QB][NRA] = res[b % RING];
             if constexpr (NR > 0) {
 #pragma unroll
@@ -663,7 +696,10 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
                     if constexpr (STATS) cnt += ok ? 1.f : 0.f;
                 } else {
                     uint2 pk;  // v = conv + bias (the accumulators started at the bias)
-                    o = finish4<EPI, OUT_H>(p, v[qq], rc[qq], pk, one);
+                    if constexpr (H16T)
+                        pk = v16[qq];  // rounded before the transpose (finish4's rule for this case)
+                    else
+                        o = finish4<EPI, OUT_H>(p, v[qq], rc[qq], pk, one);
                     store4<OUT_H>(eb, yo0 + __umul24(j * 32 + 4 * q, yld), valid && mok, o, pk);
                     pkq[qq] = pk, vq[qq] = valid;
                     if constexpr (HSTATS) {
