@@ -258,7 +258,8 @@ constexpr int kNumRes = EPI == EPI_MEAN3_LEAKY_BF16 ? 3
 struct EpiBase {
     void* y;
     const float *r0, *r1, *r2;
-    __amdgpu_buffer_rsrc_t ry;  // y from the unit's first row, as a buffer resource (see store4)
+    __amdgpu_buffer_rsrc_t ry;   // y from the unit's first row, as a buffer resource (see store4)
+    __amdgpu_buffer_rsrc_t rr0, rr1, rr2;  // EPI_ADD_FROM, EPI_MEAN3_LEAKY_BF16: r0..r2 likewise
 };
 
 // fp16 residual operands travel as their raw bits (4 halves in .x and .y) from the load to
@@ -300,6 +301,13 @@ __device__ __forceinline__ float div3(float x) {
     return __builtin_fmaf(-n, kThird, q);
 }
 
+// Raw buffer resources (stride 0) of the epilogue's rows: byte offsets are 32-bit, and an offset
+// past the range drops a store (see store4)
+constexpr int kBufRecords = 0x7fffffff;         // the resource's range in bytes
+constexpr uint32_t kDropOffset = 0x80000000u;   // past it: the store is dropped
+constexpr int kCpolNT = 2;                      // cache policy: nontemporal
+constexpr int kBufFormat = 0x00020000;          // descriptor word 3: 32-bit data format, no swizzle
+
 // Residual operands of output row t, channels m..m+3 (`yo`, `ro`: element offsets from the unit's
 // first row in y and r0..r2).
 template <int EPI, bool OUT_H>
@@ -307,13 +315,17 @@ __device__ __forceinline__ void load_res(const ConvParams& p, const EpiBase& eb,
                                          int m, float4* r) {
     typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
     if constexpr (EPI == EPI_ACCUM && OUT_H) {
-        // the fp16 rows this epilogue overwrites, streamed like its stores
-        const u32x2_t v = __builtin_nontemporal_load((const u32x2_t*)((const uint16_t*)eb.y + yo));
+        // the fp16 rows this epilogue overwrites, streamed like its stores (a buffer load: 32-bit
+        // offsets, no 64-bit address arithmetic)
+        const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(eb.ry, (int)(yo * 2u), 0, kCpolNT);
         r[0] = raw_h4(make_uint2(v.x, v.y));
     } else if constexpr (EPI == EPI_MEAN3_LEAKY_BF16) {
-        r[0] = raw_h4(*(const uint2*)((const uint16_t*)eb.r0 + ro));
-        r[1] = raw_h4(*(const uint2*)((const uint16_t*)eb.r1 + ro));
-        r[2] = raw_h4(*(const uint2*)((const uint16_t*)eb.r2 + ro));
+        const u32x2_t v0 = __builtin_amdgcn_raw_buffer_load_b64(eb.rr0, (int)(ro * 2u), 0, 0);
+        const u32x2_t v1 = __builtin_amdgcn_raw_buffer_load_b64(eb.rr1, (int)(ro * 2u), 0, 0);
+        const u32x2_t v2 = __builtin_amdgcn_raw_buffer_load_b64(eb.rr2, (int)(ro * 2u), 0, 0);
+        r[0] = raw_h4(make_uint2(v0.x, v0.y));
+        r[1] = raw_h4(make_uint2(v1.x, v1.y));
+        r[2] = raw_h4(make_uint2(v2.x, v2.y));
     } else if constexpr (EPI == EPI_ACCUM || EPI == EPI_RESID) {
         // the rows this epilogue overwrites: streamed (nontemporal), like its stores
         const f32x4 v = __builtin_nontemporal_load((const f32x4*)((const float*)eb.y + yo));
@@ -321,7 +333,8 @@ __device__ __forceinline__ void load_res(const ConvParams& p, const EpiBase& eb,
     } else if constexpr (EPI == EPI_RESID_UP2) {
         r[0] = *(const float4*)(p.r0 + (t >> 1) * p.r0_ld + m);
     } else if constexpr (EPI == EPI_ADD_FROM && OUT_H) {
-        r[0] = raw_h4(*(const uint2*)((const uint16_t*)eb.r0 + ro));
+        const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(eb.rr0, (int)(ro * 2u), 0, 0);
+        r[0] = raw_h4(make_uint2(v.x, v.y));
     } else if constexpr (EPI == EPI_ADD_FROM) {
         r[0] = *(const float4*)(eb.r0 + ro);
     }
@@ -395,10 +408,6 @@ __device__ __forceinline__ float4 finish4(const ConvParams& p, float4 v, const f
 // with that store.)  Nontemporal: the layer's output is read again only by the next launch, so it
 // streams through L2 instead of evicting the weights the A fragments reload every tap (1.4% of the
 // Snake convs' time on the benchmark configuration).
-constexpr int kBufRecords = 0x7fffffff;         // the resource's range in bytes
-constexpr uint32_t kDropOffset = 0x80000000u;   // past it: the store is dropped
-constexpr int kCpolNT = 2;                      // cache policy: nontemporal
-constexpr int kBufFormat = 0x00020000;          // descriptor word 3: 32-bit data format, no swizzle
 template <bool OUT_H>
 __device__ __forceinline__ void store4(const EpiBase& eb, uint32_t yo, bool ok, float4 o, uint2 pk) {
     typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
@@ -528,12 +537,17 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
     if constexpr (CONVT) eb.y = OUT_H ? (void*)((uint16_t*)p.y + ubase * p.y_ld) : (void*)(p.y + ubase * p.y_ld);
     eb.ry = __builtin_amdgcn_make_buffer_rsrc(eb.y, 0, kBufRecords, kBufFormat);  // raw (stride 0) buffer
     eb.r0 = eb.r1 = eb.r2 = nullptr;
-    if constexpr (EPI == EPI_ADD_FROM)
+    if constexpr (EPI == EPI_ADD_FROM) {
         eb.r0 = OUT_H ? (const float*)((const uint16_t*)p.r0 + n0 * p.r0_ld) : p.r0 + n0 * p.r0_ld;
+        eb.rr0 = __builtin_amdgcn_make_buffer_rsrc((void*)eb.r0, 0, kBufRecords, kBufFormat);
+    }
     if constexpr (EPI == EPI_MEAN3_LEAKY_BF16) {  // fp16 rows, addressed as such in load_res
         eb.r0 = (const float*)((const uint16_t*)p.r0 + n0 * p.r0_ld);
         eb.r1 = (const float*)((const uint16_t*)p.r1 + n0 * p.r0_ld);
         eb.r2 = (const float*)((const uint16_t*)p.r2 + n0 * p.r0_ld);
+        eb.rr0 = __builtin_amdgcn_make_buffer_rsrc((void*)eb.r0, 0, kBufRecords, kBufFormat);
+        eb.rr1 = __builtin_amdgcn_make_buffer_rsrc((void*)eb.r1, 0, kBufRecords, kBufFormat);
+        eb.rr2 = __builtin_amdgcn_make_buffer_rsrc((void*)eb.r2, 0, kBufRecords, kBufFormat);
     }
     const uint32_t yld = (uint32_t)vgpr((int)p.y_ld), rld = (uint32_t)vgpr((int)p.r0_ld);
     const uint32_t yo0 = (uint32_t)(wcol0 + cg) * yld + m, ro0 = (uint32_t)(wcol0 + cg) * rld + m;
@@ -545,7 +559,10 @@ __device__ __forceinline__ void epilogue(const ConvParams& p, const Unit& u, f32
     // accumulated in f32 by v_dot2c_f32_f16 (products exact) -- 2 instructions per value instead of
     // 3 in f32
     constexpr bool HSTATS = STATS && OUT_H && !CONVT;
-    constexpr bool H16T = EPI == EPI_STORE && OUT_H && (HSTATS || !STATS);  // fp16 transpose (below)
+    // fp16 transpose (below) for plain fp16 stores.  (Not for the fp16 accumulations: rounding their
+    // conv + bias to fp16 before the residual is added measured -0.07 ms and moved the audio by
+    // -46 dB, too much of the parity margin.)
+    constexpr bool H16T = OUT_H && EPI == EPI_STORE && (HSTATS || !STATS);
     f16x2_t sftp[4] = {};  // the shift of channel r, in both halves
     float cnt = 0.f;  // ConvT: rows this lane group wrote (the statistics' count)
     // Batches of QB column groups, BPS per 32-column slice.  The residual loads of batch b + LEAD are
@@ -1032,7 +1049,7 @@ hipError_t launch_t(const ConvParams& p, int n_cu, hipStream_t s, bool validate_
     if (EPI == EPI_MEAN3_LEAKY_BF16 && !(p.slope > 0.f && p.slope <= 1.f)) return hipErrorInvalidValue;  // max form
     if (p.l_in >= (int64_t)1 << 30 || p.tiles.count >= (int64_t)1 << 28) return hipErrorInvalidValue;  // 32-bit rows
     // epilogue stores: byte offsets within one unit's rows inside the buffer resource's range
-    if (!CONVT && ((int64_t)BN * p.y_ld + p.m_pad) * 4 >= kBufRecords) return hipErrorInvalidValue;
+    if (!CONVT && ((int64_t)BN * max(p.y_ld, p.r0_ld) + p.m_pad) * 4 >= kBufRecords) return hipErrorInvalidValue;
     if (CONVT && ((int64_t)p.stride_t * (BN + 1) + p.pad_t + 2) * max(p.y_ld, p.r0_ld) * 4 >= kBufRecords)
         return hipErrorInvalidValue;
     // producer loads: 32-bit byte offsets within one item's rows, rows and channels within the
