@@ -40,6 +40,7 @@
 #include "kk_walk.h"
 
 #include <algorithm>
+#include <type_traits>
 #include <atomic>
 
 namespace kk {
@@ -980,11 +981,23 @@ __global__ __launch_bounds__(64 * WM * WN + kNP) void conv_mfma_kernel(ConvParam
     for (int kc = 0; kc < 4; kc++) load_a(A[kc], cu.m0, 0, kc);
     __syncthreads();  // slab 0 and the bias staged
     init_acc<!CONVT, MI>(acc, bias_s, cu.m0, wm, lane);
+    read_b(B0, xs, 0, 0);  // slab 0's first step
     for (int g = 0; g < G; g++) {
         const uint16_t* buf = xs + (g & 1) * slab_elems;
+        const uint16_t* nbuf = xs + ((g + 1) & 1) * slab_elems;  // the next slab's buffer
         const bool last = sl + 1 == nsl;
-        read_b(B0, buf, 0, 0);
-        for (int kk = 0; kk < p.k; kk++) {
+        // One tap: 4 steps of 16 channels.  Each step reads the next step's B fragments, four reads
+        // on every path, so that the LDS wait counts of its MFMAs are static (with a skippable
+        // read the compiler waits for all of them before the step's last MFMAs, i.e. for the reads
+        // it has just issued).  The slab's last tap is a copy of its own (FINAL): at its last step
+        // every read of the slab's buffer has been issued, and the barrier (after they complete:
+        // nothing is left outstanding, on either path) hands the buffer back to the producers; the
+        // next slab's first step is then read from the other buffer, which the producers filled
+        // before the barrier, under this step's MFMAs -- or after the epilogue when one follows
+        // (those registers live through it would spill).  Past the last slab that read is of a
+        // stale buffer, in bounds and unused.
+        auto tap = [&](int kk, auto final_tap) {
+            constexpr bool FINAL = decltype(final_tap)::value;
             // the tap after this one: same slab, first tap of the next slab, or of the next unit
             // (the very last tap reloads tap 0 of this slab: a harmless load keeps the count static)
             int n_m0, n_kk, n_c16;
@@ -993,14 +1006,22 @@ __global__ __launch_bounds__(64 * WM * WN + kNP) void conv_mfma_kernel(ConvParam
             for (int kc = 0; kc < 4; kc++) {
                 bf16x8(&bc)[4] = (kc & 1) ? B1 : B0;
                 bf16x8(&bn)[4] = (kc & 1) ? B0 : B1;
-                if (kc < 3) read_b(bn, buf, kk, kc + 1);
-                else if (kk + 1 < p.k) read_b(bn, buf, kk + 1, 0);
+                if (kc < 3) {
+                    read_b(bn, buf, kk, kc + 1);
+                } else if constexpr (!FINAL) {
+                    read_b(bn, buf, kk + 1, 0);
+                } else {
+                    __syncthreads();
+                    if (!last) read_b(bn, nbuf, 0, 0);
+                }
                 __builtin_amdgcn_sched_barrier(0);
                 mfma_step(A[kc], bc);
                 __builtin_amdgcn_sched_barrier(0);
                 load_a(A[kc], n_m0, n_kk, n_c16 + kc);
             }
-        }
+        };
+        for (int kk = 0; kk + 1 < p.k; kk++) tap(kk, std::false_type{});
+        tap(p.k - 1, std::true_type{});
         if (last) {
             const int next_m0 = has_next ? nu.m0 : cu.m0;
             // (not for the 256-channel f32 accumulate-with-statistics variant: a second epilogue copy
@@ -1021,8 +1042,8 @@ __global__ __launch_bounds__(64 * WM * WN + kNP) void conv_mfma_kernel(ConvParam
                 epilogue<EPI, WM, WN, STATS, OUT_H, true>(p, cu, acc, wm, wn, lane, scr, bias_s, next_m0);
             else
                 epilogue<EPI, WM, WN, STATS, OUT_H, false>(p, cu, acc, wm, wn, lane, scr, bias_s, next_m0);
+            read_b(B0, nbuf, 0, 0);
         }
-        __syncthreads();  // hand the slab buffer back to the producers
         if (last) {
             sl = 0;
             U += gridDim.x;
