@@ -135,8 +135,9 @@ struct Slot {
         const int r0 = u.in0 - u.i_lo, rmax = u.i_hi - 1 - u.i_lo;  // row offsets from the item start
 #pragma unroll
         for (int j = 0; j < RB; j++) {
-            // rows past the slab's window re-read its first row (a cache hit, no HBM traffic)
-            const int r = rr + j * RP < tw ? rr + j * RP : 0;
+            // rows past the slab's window re-read its first row (a cache hit, no HBM traffic); the
+            // first BN / RP passes lie inside every window (tw >= BN), with no test
+            const int r = ((j + 1) * RP <= BN || rr + j * RP < tw) ? rr + j * RP : 0;
             const uint32_t row = (uint32_t)max(min(r0 + r, rmax), 0);
             const uint32_t off = (__umul24(row, ld) + (uint32_t)cl) * ES;
             if constexpr (WIDE) {
@@ -232,7 +233,8 @@ struct Slot {
             } else {
                 if (!live || n_ch <= 0) out = make_uint2(0, 0);
             }
-            if (r < tw) *(uint2*)(xrow + j * RP * kRS) = out;
+            // (a branch per row would keep the compiler from scheduling across rows)
+            if ((j + 1) * RP <= BN || r < tw) *(uint2*)(xrow + j * RP * kRS) = out;
         }
     }
 };
