@@ -963,14 +963,6 @@ __global__ __launch_bounds__(64 * WM * WN + kNP) void conv_mfma_kernel(ConvParam
         for (int i = threadIdx.x; i < p.m_pad; i += NC) bias_s[i] = i < p.m ? p.bias[i] : 0.f;
     }
     f32x16 acc[MI][4];
-    auto mfma_step = [&](const bf16x8 (&a)[MI], const bf16x8 (&b)[4]) {
-#pragma unroll
-        for (int j = 0; j < 4; j++)
-#pragma unroll
-            for (int i = 0; i < MI; i++)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
-    };
-
 
     int U = blockIdx.x, sl = 0;
     Unit cu{}, nu{};
@@ -1008,18 +1000,40 @@ __global__ __launch_bounds__(64 * WM * WN + kNP) void conv_mfma_kernel(ConvParam
             for (int kc = 0; kc < 4; kc++) {
                 bf16x8(&bc)[4] = (kc & 1) ? B1 : B0;
                 bf16x8(&bn)[4] = (kc & 1) ? B0 : B1;
-                if (kc < 3) {
-                    read_b(bn, buf, kk, kc + 1);
-                } else if constexpr (!FINAL) {
-                    read_b(bn, buf, kk + 1, 0);
-                } else {
+                if (FINAL && kc == 3) {
                     __syncthreads();
                     if (!last) read_b(bn, nbuf, 0, 0);
                 }
+                // The MFMAs fragment-major (fragment i's four, then i + 1's), each A fragment
+                // reloaded right after its last MFMA, and the loads and LDS reads issued between
+                // the MFMAs: a wave issues in order, so a load or read that waits for the memory
+                // pipeline to accept it stalls the MFMAs behind it -- issued after all of the step's
+                // MFMAs, those stalls left the matrix core idle.  (Every accumulator's sum is the
+                // same sequence of MFMAs: the outputs do not change.)
                 __builtin_amdgcn_sched_barrier(0);
-                mfma_step(A[kc], bc);
+                if (kc < 3)
+                    read_b(bn, buf, kk, kc + 1);
+                else if (!FINAL)
+                    read_b(bn, buf, kk + 1, 0);
+#pragma unroll
+                for (int i = 0; i < MI; i++) {
+#pragma unroll
+                    for (int j = 0; j < 4; j++)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A[kc][i], bc[j], acc[i][j], 0, 0, 0);
+                    A[kc][i] = w_lane[(int64_t)n_m0 * 2 + ((int64_t)n_kk * n16 + n_c16 + kc) * a_step + 64 * i];
+                }
+                // issue order: (MFMA, LDS read) x 4, A reload, (MFMA x MI*4 - 4 ... ), A reload
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
+                }
+#pragma unroll
+                for (int i = 0; i < MI; i++) {
+                    __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // global load (A fragment i)
+                    if (i + 1 < MI) __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+                }
                 __builtin_amdgcn_sched_barrier(0);
-                load_a(A[kc], n_m0, n_kk, n_c16 + kc);
             }
         };
         for (int kk = 0; kk + 1 < p.k; kk++) tap(kk, std::false_type{});
