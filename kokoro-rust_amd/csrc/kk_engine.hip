@@ -1801,14 +1801,22 @@ struct Runner {
     }
     // BiLSTM recurrence over the item spans of d (gx rows through gx_row, or the spans' own rows);
     // h into out[row][0:512].  Algorithmic traffic: gx read and h written once per row, W_hh once.
-    // Each sequence runs on two CUs (launch_lstm_pair) with its exchange words in `region` (one per
-    // stream that runs recurrences at the same time); KOKORO_HIP_LSTM_SINGLE=1 selects the one-CU
-    // kernel (W_hh partly streamed from L2 each step), as does a plan whose pairs gave up before
-    // (lstm_single).  Test hook, read at each launch: KOKORO_HIP_TEST_LSTM_SILENT=1 keeps the second
-    // half of every pair from publishing and cuts the wait to 10 us, so that the pairs give up.
+    // Each sequence runs on two CUs (launch_lstm_pair), or four for long spans (launch_lstm_quad:
+    // bit-identical), with its exchange words in `region` (one per stream that runs recurrences at
+    // the same time); KOKORO_HIP_LSTM_SINGLE=1 selects the one-CU kernel (W_hh partly streamed from
+    // L2 each step), as does a plan whose pairs or quads gave up before (lstm_single).  Test hook,
+    // read at each launch: KOKORO_HIP_TEST_LSTM_SILENT=1 keeps the second half of every pair (the
+    // second quarter of every quad) from publishing and cuts the wait to 10 us, so that they give up.
     void recur(const MLstm& l, const float* gx, const int32_t* gx_row, const Dom& d, float* out, int64_t out_ld,
                const std::string& name, int region = 0) {
         static const bool single = env_i64("KOKORO_HIP_LSTM_SINGLE", 0) != 0;
+        // four CUs per sequence when the longest span has at least kLstmQuadMinSteps steps (the
+        // quads' per-step gain outweighs their fixed cost and second wave); KOKORO_HIP_LSTM_QUAD,
+        // read at each launch: 1 always, 0 never
+        int64_t longest = 0;
+        for (int64_t v : d.len) longest = std::max(longest, v);
+        const int64_t qsel = env_i64("KOKORO_HIP_LSTM_QUAD", -1);
+        const bool quad = qsel < 0 ? longest >= kLstmQuadMinSteps : qsel != 0;
         const bool silent = env_i64("KOKORO_HIP_TEST_LSTM_SILENT", 0) != 0;
         const double v = (double)d.valid();
         label = name;
@@ -1817,6 +1825,11 @@ struct Runner {
                 return launch_lstm(gx, 2048, gx_row, d.start_d.as<int64_t>(), d.len_d.as<int64_t>(), p->nb,
                                    l.whh_t.as<float>(), l.bhh.as<float>(), out, out_ld, s);
             uint64_t* x = p->u_lstmx.as<uint64_t>();
+            if (quad)
+                return launch_lstm_quad(gx, 2048, gx_row, d.start_d.as<int64_t>(), d.len_d.as<int64_t>(), p->nb,
+                                        l.whh_t.as<float>(), l.bhh.as<float>(), out, out_ld,
+                                        x + kk_plan::kLstmXHead + (int64_t)region * 2 * p->nb * 512, (int*)x, s,
+                                        silent ? 1000 : kLstmPairWaitTicks, silent ? 1 : -1);
             return launch_lstm_pair(gx, 2048, gx_row, d.start_d.as<int64_t>(), d.len_d.as<int64_t>(), p->nb,
                                     l.whh_t.as<float>(), l.bhh.as<float>(), out, out_ld,
                                     x + kk_plan::kLstmXHead + (int64_t)region * 2 * p->nb * 512, (int*)x, s,

@@ -326,6 +326,32 @@ def test_lstm_pair_wait_falls_back_to_one_cu(full_ctx, full_run, one_cu_run):
         assert np.array_equal(d, d2) and np.array_equal(a, a2)
 
 
+def test_lstm_quad_matches_pair(full_ctx, full_run, one_cu_run):
+    """The four-CU recurrence (KOKORO_HIP_LSTM_QUAD=1 forces it for every span; by default it runs
+    spans of 1,024 steps and more, longer than this batch's): each row's dot product is summed in
+    the two-CU kernel's order, so durations and audio equal the pairs' bit for bit.  Its bounded
+    wait, forced from the host (KOKORO_HIP_TEST_LSTM_SILENT=1: the second quarter of every quad
+    publishes nothing), falls back to the one-CU kernel like the pairs'."""
+    items, audio, durs, _ = full_run
+    os.environ["KOKORO_HIP_LSTM_QUAD"] = "1"
+    try:
+        res = full_ctx.forward_batch(items)
+        for b, ((a, d), a2, d2) in enumerate(zip(res, audio, durs)):
+            assert np.array_equal(d, d2) and np.array_equal(a, a2), b
+        os.environ["KOKORO_HIP_TEST_LSTM_SILENT"] = "1"
+        try:
+            res = full_ctx.forward_batch(items)
+        finally:
+            del os.environ["KOKORO_HIP_TEST_LSTM_SILENT"]
+        for b, (a, d) in enumerate(res):
+            assert np.array_equal(d, one_cu_run[f"dur{b}"]) and np.array_equal(a, one_cu_run[f"audio{b}"]), b
+    finally:
+        del os.environ["KOKORO_HIP_LSTM_QUAD"]
+    res = full_ctx.forward_batch(items)
+    for (a, d), a2, d2 in zip(res, audio, durs):
+        assert np.array_equal(d, d2) and np.array_equal(a, a2)
+
+
 def test_lstm_abort_falls_back_in_every_result_path(full_ctx, full_run, one_cu_run):
     """A plan run whose recurrences give up (KOKORO_HIP_TEST_LSTM_SILENT=1, read at each run) would
     leave h rows of an earlier run behind; every path that hands results back -- sync, fetch,
