@@ -302,8 +302,9 @@ def e2e_leg(steps, warmup, with_cpu):
                "lstm": {"serial_ms": round(cls["lstm"]["ms"], 3), "critical_steps": lstm_steps,
                         "us_per_step": round(1e3 * cls["lstm"]["ms"] / lstm_steps, 2),
                         "note": "5 token-level BiLSTMs (longest item's ids) + the shared BiLSTM (longest item's "
-                                "frames); each (item, direction) on two CUs with all of W_hh on chip: per step "
-                                "~0.9 us of f32 FMA and the exchange of h through L2"},
+                                "frames); each (item, direction) on two CUs (four for spans of >= 1,024 steps: the shared "
+                                "BiLSTM) with all of W_hh on chip: per step ~0.9 (0.45) us of f32 FMA and the "
+                                "exchange of h through L2"},
                "attention": rate("attention", PEAK_F32_MFMA_TFLOPS),
                "linear": rate("linear", PEAK_BF16_TFLOPS),
                "prosody_conv": rate("prosody_conv", PEAK_BF16_TFLOPS),
