@@ -150,7 +150,7 @@ struct MResblk {
     int din = 0, dout = 0;
 };
 struct MNoiseConv {
-    DevBuf w, b, wp;  // wp: f32 matrix-core packing (noise_convs.0)
+    DevBuf w, b, wp;  // wp: split-bf16 matrix-core packing (noise_convs.0)
     int cout = 0, k = 0, stride = 1, pad = 0;
 };
 // A Linear [dout][din] on the MFMA conv kernel (k = 1), in pieces of at most 1024 output rows (the
@@ -559,15 +559,25 @@ static void load_model(kk_ctx* ctx, const kk_tensor* tensors, int n, bool norm_d
         c.w.upload(wt);
         c.b.upload(t.get(p + ".bias", c.cout), c.cout);
         if (c.cout == 256 && c.k == 12 && c.stride == 6) {
-            // [32-row tile mt][h][row i][tap][cp < 11, one pad] = W[32 mt + i][channel 2 cp + h][tap]
-            std::vector<float> wp((size_t)c.cout * 2 * 12 * 12, 0.f);
+            // A fragments of the split-precision kernel: [32-row tile mt][K step st][part][lane][e]
+            // = the bf16 rounding (part 0) or the bf16 rounding of the remainder (part 1) of
+            // W[32 mt + lane % 32][ci][tap], k = 16 st + 8 (lane / 32) + e = 24 tap + ci (ci >= 22: 0)
+            constexpr int kSteps = 18;
+            std::vector<uint16_t> wp((size_t)(c.cout / 32) * kSteps * 2 * 64 * 8, 0);
             for (int mt = 0; mt < c.cout / 32; mt++)
-                for (int h = 0; h < 2; h++)
-                    for (int i = 0; i < 32; i++)
-                        for (int kk = 0; kk < 12; kk++)
-                            for (int cp = 0; cp < 11; cp++)
-                                wp[((((size_t)mt * 2 + h) * 32 + i) * 12 + kk) * 12 + cp] =
-                                    w[((size_t)(32 * mt + i) * 22 + 2 * cp + h) * c.k + kk];
+                for (int st = 0; st < kSteps; st++)
+                    for (int lane = 0; lane < 64; lane++)
+                        for (int e = 0; e < 8; e++) {
+                            const int k = 16 * st + 8 * (lane / 32) + e, tap = k / 24, ci = k % 24;
+                            const float v = ci < 22 ? w[((size_t)(32 * mt + lane % 32) * 22 + ci) * c.k + tap] : 0.f;
+                            const uint16_t hi = bf16_bits(v);
+                            uint32_t hb = (uint32_t)hi << 16;
+                            float hf;
+                            std::memcpy(&hf, &hb, 4);
+                            const size_t o = ((((size_t)mt * kSteps + st) * 2) * 64 + lane) * 8 + e;
+                            wp[o] = hi;
+                            wp[o + 64 * 8] = bf16_bits(v - hf);
+                        }
             c.wp.upload(wp);
         }
     }
@@ -1685,7 +1695,7 @@ struct Runner {
         launch(i == 0 ? PC_NOISE0 : PC_NOISE1, 2.0 * 22 * nc.k * c * (double)dout.valid(), bytes, [&] {
             return launch_noise_conv(p->spec.as<float>(), kSpecLd, p->d120.l, p->d120.start_d.as<int64_t>(),
                                      p->d120.len_d.as<int64_t>(),
-                                     nc.w.as<float>(), nc.wp.p ? nc.wp.as<float>() : nullptr, nc.b.as<float>(), nc.cout,
+                                     nc.w.as<float>(), nc.wp.p ? nc.wp.as<uint16_t>() : nullptr, nc.b.as<float>(), nc.cout,
                                      nc.k, nc.stride, nc.pad, xs, c, tn.dev(), part(), s);
         });
         snake_block(m.noise_res[i], xs, p->hn.as<float>(), dout, &tn, cf(9), cf(10), true);

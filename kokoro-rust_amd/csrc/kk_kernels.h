@@ -141,13 +141,15 @@ hipError_t launch_adain_pool(const float* x, int64_t ld, int c, const Coef* coef
 // outside the tile's item span [in_start, in_start + in_len) read as 0 (the reference's gap mask),
 // over item-aligned tiles t (<= kNoiseTile output rows each; rows outside the tiles are not
 // written), with the statistics partial of each tile ([tile][cout], shift = bias) for the next
-// layer's AdaIN.  wt: [k][22][cout] f32 (VALU kernel); wp: the noise_convs.0 weights packed for
-// the f32 matrix cores ([32-row tile][2][32][12 taps][12] f32), or null.  y is stored as fp16
+// layer's AdaIN.  wt: [k][22][cout] f32 (VALU kernel); wp: the noise_convs.0 weights split into
+// bf16 roundings and remainders and packed as A fragments for the split-precision matrix-core
+// kernel ([32-row tile][18 K steps][rounding, remainder][64 lanes][8] bf16, K = 24 tap + channel
+// with channels 22 and 23 zero), or null.  y is stored as fp16
 // (the noise branch's residual stream; the statistics describe the f32 values).
 constexpr int kNoiseTile = 64;
 hipError_t launch_noise_conv(const float* spec, int64_t spec_ld, int64_t l_in, const int64_t* in_start,
                              const int64_t* in_len,
-                             const float* wt, const float* wp, const float* b, int cout, int k, int stride, int pad,
+                             const float* wt, const uint16_t* wp, const float* b, int cout, int k, int stride, int pad,
                              uint16_t* y, int64_t y_ld, TilesDev t, StatPart* part, hipStream_t s);
 // SineGen phase_pre: per item and harmonic, f64 cumulative sum of the 1/300-downsampled rad values.
 hipError_t launch_phase_pre(const float* f0, const int64_t* start2, const int64_t* len2, int nb,

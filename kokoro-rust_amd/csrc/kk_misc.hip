@@ -369,50 +369,76 @@ __global__ __launch_bounds__(256) void noise_conv_kernel(const float* __restrict
     }
 }
 
-// noise_convs.0 (22 -> 256, k 12, stride 6) on the f32 matrix cores (v_mfma_f32_32x32x2_f32:
-// exact f32 products, f32 accumulation, like the reference's f32 sgemm route).  GEMM view per
-// block: 256 output channels x 64 output columns, K = 12 taps x 22 channels = 264 in steps of 2
-// (tap, channel pair).  Wave w owns channels 64 w .. 64 w + 63 (2 x 2 tiles of 32 x 32).
-//   A (weights) lane (i = l % 32, h = l / 32) of step (tap, cp): W[row i][channel 2 cp + h][tap],
-//     pre-packed as [32-row tile][h][i][tap][12] (cp < 11, one pad) so a tap is three float4 per lane;
-//   B (input window in LDS, channel-major) lane (j, h): x[channel 2 cp + h][row 6 j + tap].
+// noise_convs.0 (22 -> 256, k 12, stride 6) on the bf16 matrix cores in split precision
+// (v_mfma_f32_32x32x16_bf16, f32 accumulation).  Every input value and weight is split into its
+// bf16 rounding and the bf16 rounding of the remainder (v = vh + vl to within 2^-17 |v|), and each
+// product is accumulated as wh xh + wh xl + wl xh: within ~2^-16 of the exact f32 product (the
+// dropped wl xl and the two remainders' own roundings), far below the fp16 rounding of the stored
+// output (2^-11).  GEMM view per block: 256 output channels x 64 output columns, K = 12 taps x 24
+// channels (22 and two zeros) = 288 in 18 steps of 16.  The window is staged row-major, [row][24]
+// bf16 in two planes (the roundings, then the remainders), so K index k = 24 tap + ci of output
+// column n is window element 144 n + k (row 6 n + tap): a B fragment (8 consecutive k) is one
+// 16-byte LDS read.  Wave w owns channels 64 w .. 64 w + 63 (2 x 2 tiles of 32 x 32).
+//   A (weights) lane (i = l % 32, h = l / 32) of step c: W[row i][k = 16 c + 8 h + e], e < 8,
+//     pre-packed as [32-row tile][step][rounding, remainder][lane] bf16x8;
+//   B lane (j, h) of step c: window[144 j + 16 c + 8 h + e].
 // Accumulators start at the bias; the epilogue stores each lane's 4 consecutive channels.
 constexpr int kNc0Win = (kNcRows - 1) * 6 + 12;  // 390 input rows per 64 output columns
-constexpr int kNc0Ld = kNc0Win + 2;               // channel-major window row stride (floats)
+constexpr int kNc0Row = 24;                       // a window row: 22 channels and two zeros
+constexpr int kNc0Plane = kNc0Win * kNc0Row;      // bf16 per plane
+constexpr int kNc0Steps = 12 * kNc0Row / 16;      // K steps of 16
+static_assert(144 * (kNcRows - 1) + 16 * kNc0Steps <= kNc0Plane, "the last column's last B fragment");
+__device__ __forceinline__ void split_bf16x4(float4 v, uint2& hi, uint2& lo) {
+    const float x[4] = {v.x, v.y, v.z, v.w};
+    uint32_t h[4], l[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        h[e] = f32_to_bf16_bits(x[e]);
+        l[e] = f32_to_bf16_bits(x[e] - __uint_as_float(h[e] << 16));
+    }
+    hi = make_uint2(h[0] | h[1] << 16, h[2] | h[3] << 16);
+    lo = make_uint2(l[0] | l[1] << 16, l[2] | l[3] << 16);
+}
 __global__ __launch_bounds__(256, 4) void noise_conv0_mfma_kernel(const float* __restrict__ spec, int64_t spec_ld,
                                                                int64_t l_in, const int64_t* __restrict__ in_start,
                                                                const int64_t* __restrict__ in_len,
-                                                               const float4* __restrict__ wp, const float* __restrict__ b,
+                                                               const bf16x8* __restrict__ wq, const float* __restrict__ b,
                                                                int pad, uint16_t* __restrict__ y, int64_t y_ld,
                                                                TilesDev tl, StatPart* __restrict__ part) {
     typedef float f32x16 __attribute__((ext_vector_type(16)));
-    __shared__ float xs[22 * kNc0Ld];
+    __shared__ __align__(16) uint16_t xs[2 * kNc0Plane];
     const int64_t t0 = tl.t0[blockIdx.x];
     const int nv = tl.n[blockIdx.x];
     const int64_t in0 = t0 * 6 - pad;
     // the tile's item: input rows outside its span are the zero padding (gap masking)
     const int item = tl.item[blockIdx.x];
     const int64_t i_lo = in_start[item], i_hi = i_lo + in_len[item];
-    // the window in batches of 12 loads per thread, each batch in flight before its first use (rows
-    // clamped, the gap / range mask applied afterwards)
-    constexpr int kPer = (kNc0Win * 22 + 255) / 256, kBatch = 12;
-#pragma unroll 1
-    for (int k0 = 0; k0 < kPer; k0 += kBatch) {
-        float sv[kBatch];
+    // the window: 6 float4 per row (channels 0-23 of the 32-float spectrum row; 22 and 23 set to 0),
+    // every load in flight before the first conversion (rows clamped, the gap / range mask applied
+    // afterwards)
+    {
+        constexpr int kQ = kNc0Win * 6, kPer = (kQ + 255) / 256;
+        float4 sv[kPer];
 #pragma unroll
-        for (int kk = 0; kk < kBatch; kk++) {
-            const int i = min((int)threadIdx.x + (k0 + kk) * 256, kNc0Win * 22 - 1);
-            const int r = i / 22, ci = i - r * 22;
+        for (int k = 0; k < kPer; k++) {
+            const int i = min((int)threadIdx.x + k * 256, kQ - 1);
+            const int r = i / 6, q = i - r * 6;
             const int64_t row = min(max(in0 + r, i_lo), i_hi - 1);
-            sv[kk] = spec[row * spec_ld + ci];
+            sv[k] = *(const float4*)(spec + row * spec_ld + 4 * q);
         }
 #pragma unroll
-        for (int kk = 0; kk < kBatch; kk++) {
-            const int i = threadIdx.x + (k0 + kk) * 256;
-            if (i < kNc0Win * 22) {
-                const int r = i / 22, ci = i - r * 22;
+        for (int k = 0; k < kPer; k++) {
+            const int i = threadIdx.x + k * 256;
+            if (i < kQ) {
+                const int r = i / 6, q = i - r * 6;
                 const int64_t row = in0 + r;
-                xs[ci * kNc0Ld + r] = (row >= i_lo && row < i_hi) ? sv[kk] : 0.f;
+                const bool in = row >= i_lo && row < i_hi;
+                float4 v = in ? sv[k] : make_float4(0.f, 0.f, 0.f, 0.f);
+                if (q == 5) v.z = 0.f, v.w = 0.f;
+                uint2 hi, lo;
+                split_bf16x4(v, hi, lo);
+                *(uint2*)(xs + r * kNc0Row + 4 * q) = hi;
+                *(uint2*)(xs + kNc0Plane + r * kNc0Row + 4 * q) = lo;
             }
         }
     }
@@ -431,44 +457,44 @@ __global__ __launch_bounds__(256, 4) void noise_conv0_mfma_kernel(const float* _
             }
         }
     }
-    // this lane's weights: tile 2 wave + mi, half h, row l32; per tap 12 floats (11 channel pairs
-    // and a pad), three float4
-    const float4* wa[2];
-#pragma unroll
-    for (int mi = 0; mi < 2; mi++) wa[mi] = wp + ((int64_t)((2 * wave + mi) * 2 + h) * 32 + l32) * 36;
-    const float* xb = xs + h * kNc0Ld + 6 * l32;  // channel h, output column l32 (ni = 0)
-    // Tap by tap: the next tap's weights are in flight while this tap's 11 steps (44 MFMAs per
-    // wave) run; scheduling barriers keep the loads where they are issued.
-    float4 ac[2][3], an[2][3];
+    // this lane's weights: tile 2 wave + mi, step c, part p at wa[((mi * steps + c) * 2 + p) * 64]
+    const bf16x8* wa = wq + (int64_t)(2 * wave) * kNc0Steps * 2 * 64 + lane;
+    const uint16_t* xb = xs + 144 * l32 + 8 * h;  // output column l32 (ni = 0); ni = 1 is 32 columns on
+    // Step by step: the next step's weights are in flight while this step's 12 MFMAs run; two
+    // register sets take turns (steps in pairs), so no copy waits for the loads.
+    static_assert(kNc0Steps % 2 == 0, "steps in pairs");
+    bf16x8 w0[2][2], w1[2][2];
 #pragma unroll
     for (int mi = 0; mi < 2; mi++)
 #pragma unroll
-        for (int q = 0; q < 3; q++) ac[mi][q] = wa[mi][q];
-#pragma unroll 1
-    for (int tap = 0; tap < 12; tap++) {
-        const int tn = min(tap + 1, 11);
+        for (int p = 0; p < 2; p++) w0[mi][p] = wa[(mi * kNc0Steps * 2 + p) * 64];
+    auto step = [&](int c, bf16x8(&cur)[2][2], bf16x8(&nxt)[2][2]) {
+        const int cn = min(c + 1, kNc0Steps - 1);
 #pragma unroll
         for (int mi = 0; mi < 2; mi++)
 #pragma unroll
-            for (int q = 0; q < 3; q++) an[mi][q] = wa[mi][3 * tn + q];
-        __builtin_amdgcn_sched_barrier(0);
+            for (int p = 0; p < 2; p++) nxt[mi][p] = wa[((mi * kNc0Steps + cn) * 2 + p) * 64];
+        __builtin_amdgcn_sched_barrier(0);  // the loads stay ahead of this step's MFMAs
+        bf16x8 bh[2], bl[2];
 #pragma unroll
-        for (int cp = 0; cp < 11; cp++) {
-            const float* xp = xb + 2 * cp * kNc0Ld + tap;
-            const float b0 = xp[0], b1 = xp[6 * 32];
-#pragma unroll
-            for (int mi = 0; mi < 2; mi++) {
-                const float4 a4 = ac[mi][cp / 4];
-                const float av = cp % 4 == 0 ? a4.x : cp % 4 == 1 ? a4.y : cp % 4 == 2 ? a4.z : a4.w;
-                acc[mi][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(av, b0, acc[mi][0], 0, 0, 0);
-                acc[mi][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(av, b1, acc[mi][1], 0, 0, 0);
-            }
+        for (int ni = 0; ni < 2; ni++) {
+            bh[ni] = *(const bf16x8*)(xb + ni * 144 * 32 + 16 * c);
+            bl[ni] = *(const bf16x8*)(xb + kNc0Plane + ni * 144 * 32 + 16 * c);
         }
-        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int mi = 0; mi < 2; mi++)
 #pragma unroll
-            for (int q = 0; q < 3; q++) ac[mi][q] = an[mi][q];
+            for (int ni = 0; ni < 2; ni++) {
+                acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(cur[mi][0], bh[ni], acc[mi][ni], 0, 0, 0);
+                acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(cur[mi][0], bl[ni], acc[mi][ni], 0, 0, 0);
+                acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(cur[mi][1], bh[ni], acc[mi][ni], 0, 0, 0);
+            }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+#pragma unroll 1
+    for (int c = 0; c < kNc0Steps; c += 2) {
+        step(c, w0, w1);
+        step(c + 1, w1, w0);
     }
     // D layout: element 4 g + r of tile (mi, ni) is channel 64 wave + 32 mi + 8 g + 4 h + r of
     // output column t0 + 32 ni + l32
@@ -478,7 +504,8 @@ __global__ __launch_bounds__(256, 4) void noise_conv0_mfma_kernel(const float* _
     // it), in order.  Each accumulator is read once.
     const bool ok0 = l32 < nv, ok1 = 32 + l32 < nv;
     constexpr int kRl = 257;  // [2 statistics][16 lane pairs][256 channels + 1]
-    static_assert(2 * 16 * kRl <= 22 * kNc0Ld, "reduction buffer");
+    static_assert(2 * 16 * kRl * 4 <= (int)sizeof(xs), "reduction buffer");
+    float* red = (float*)xs;
     auto pair_sum = [](float v) {  // v + v of lane l ^ 1 (quad_perm [1, 0, 3, 2])
         return v + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));
     };
@@ -502,15 +529,15 @@ __global__ __launch_bounds__(256, 4) void noise_conv0_mfma_kernel(const float* _
                 const float d0 = ok0 ? e0[r] : 0.f, d1 = ok1 ? e1[r] : 0.f;
                 const float p1 = pair_sum(d0 + d1), p2 = pair_sum(__builtin_fmaf(d1, d1, d0 * d0));
                 if ((l32 & 1) == 0) {
-                    xs[(l32 >> 1) * kRl + c0 + r] = p1;
-                    xs[(16 + (l32 >> 1)) * kRl + c0 + r] = p2;
+                    red[(l32 >> 1) * kRl + c0 + r] = p1;
+                    red[(16 + (l32 >> 1)) * kRl + c0 + r] = p2;
                 }
             }
             __builtin_amdgcn_sched_barrier(0);  // one group at a time: registers stay at the main loop's
         }
     __syncthreads();
     float a1 = 0.f, a2 = 0.f;
-    for (int l = 0; l < 16; l++) a1 += xs[l * kRl + threadIdx.x], a2 += xs[(16 + l) * kRl + threadIdx.x];
+    for (int l = 0; l < 16; l++) a1 += red[l * kRl + threadIdx.x], a2 += red[(16 + l) * kRl + threadIdx.x];
     part[(int64_t)blockIdx.x * 256 + threadIdx.x] = StatPart{a1, a2, b[threadIdx.x], (float)nv};
 }
 
@@ -935,7 +962,7 @@ hipError_t launch_adain_pool(const float* x, int64_t ld, int c, const Coef* coef
 
 hipError_t launch_noise_conv(const float* spec, int64_t spec_ld, int64_t l_in, const int64_t* in_start,
                              const int64_t* in_len, const float* wt,
-                             const float* wp, const float* b, int cout, int k, int stride, int pad, uint16_t* y,
+                             const uint16_t* wp, const float* b, int cout, int k, int stride, int pad, uint16_t* y,
                              int64_t y_ld, TilesDev t, StatPart* part, hipStream_t s) {
     const int win = (kNcRows - 1) * stride + k;
     if (win > kNcMaxWin) return hipErrorInvalidValue;
@@ -945,7 +972,7 @@ hipError_t launch_noise_conv(const float* spec, int64_t spec_ld, int64_t l_in, c
         // the matrix-core path: noise_convs.0's shape only, weights packed by pack_noise_conv0
         if (cout != 256 || k != 12 || stride != 6) return hipErrorInvalidValue;
         hipLaunchKernelGGL(noise_conv0_mfma_kernel, grid, dim3(256), 0, s, spec, spec_ld, l_in, in_start, in_len,
-                           (const float4*)wp, b, pad, y, y_ld, t, part);
+                           (const bf16x8*)wp, b, pad, y, y_ld, t, part);
         return hipGetLastError();
     }
     // noise_convs.0 (k 12, stride 6) stages a 390-row window; noise_convs.1 (k 1) 64 rows, small
