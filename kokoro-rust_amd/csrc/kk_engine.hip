@@ -150,7 +150,7 @@ struct MResblk {
     int din = 0, dout = 0;
 };
 struct MNoiseConv {
-    DevBuf w, b, wp;  // wp: split-bf16 matrix-core packing (noise_convs.0)
+    DevBuf b, wp;  // wp: split-bf16 matrix-core packing
     int cout = 0, k = 0, stride = 1, pad = 0;
 };
 // A Linear [dout][din] on the MFMA conv kernel (k = 1), in pieces of at most 1024 output rows (the
@@ -549,26 +549,21 @@ static void load_model(kk_ctx* ctx, const kk_tensor* tensors, int n, bool norm_d
         const std::string p = g + ".noise_convs." + std::to_string(i);
         MNoiseConv& c = m.nc[i];
         c.cout = nc_cout[i], c.k = nc_k[i], c.stride = nc_s[i], c.pad = nc_p[i];
-        // transposed to [k][22][cout] (one coalesced float4 per 4 output channels in the kernel)
         const float* w = t.get(p + ".weight", (int64_t)c.cout * 22 * c.k);
-        std::vector<float> wt((size_t)c.cout * 22 * c.k);
-        for (int co = 0; co < c.cout; co++)
-            for (int ci = 0; ci < 22; ci++)
-                for (int kk = 0; kk < c.k; kk++)
-                    wt[((size_t)kk * 22 + ci) * c.cout + co] = w[((size_t)co * 22 + ci) * c.k + kk];
-        c.w.upload(wt);
         c.b.upload(t.get(p + ".bias", c.cout), c.cout);
-        if (c.cout == 256 && c.k == 12 && c.stride == 6) {
-            // A fragments of the split-precision kernel: [32-row tile mt][K step st][part][lane][e]
+        {
+            // A fragments of the split-precision kernels: [32-row tile mt][K step st][part][lane][e]
             // = the bf16 rounding (part 0) or the bf16 rounding of the remainder (part 1) of
-            // W[32 mt + lane % 32][ci][tap], k = 16 st + 8 (lane / 32) + e = 24 tap + ci (ci >= 22: 0)
-            constexpr int kSteps = 18;
+            // W[32 mt + lane % 32][ci][tap], k = 16 st + 8 (lane / 32) + e = 24 tap + ci (ci >= 22: 0;
+            // noise_convs.1: k = ci, two steps)
+            const int kSteps = c.k == 12 ? 18 : 2;
             std::vector<uint16_t> wp((size_t)(c.cout / 32) * kSteps * 2 * 64 * 8, 0);
             for (int mt = 0; mt < c.cout / 32; mt++)
                 for (int st = 0; st < kSteps; st++)
                     for (int lane = 0; lane < 64; lane++)
                         for (int e = 0; e < 8; e++) {
-                            const int k = 16 * st + 8 * (lane / 32) + e, tap = k / 24, ci = k % 24;
+                            const int k = 16 * st + 8 * (lane / 32) + e;
+                            const int tap = c.k == 12 ? k / 24 : 0, ci = c.k == 12 ? k % 24 : k;
                             const float v = ci < 22 ? w[((size_t)(32 * mt + lane % 32) * 22 + ci) * c.k + tap] : 0.f;
                             const uint16_t hi = bf16_bits(v);
                             uint32_t hb = (uint32_t)hi << 16;
@@ -1688,15 +1683,15 @@ struct Runner {
         const int reg = region;
         region = 3;
         const MNoiseConv& nc = m.nc[i];
-        const Tiles& tn = p->tl(dout, kNoiseTile);
+        const int tile_rows = i == 0 ? kNoiseTile : kNoiseTile1;
+        const Tiles& tn = p->tl(dout, tile_rows);
         need_part(tn.count * c);
         // reads the spectrum's valid rows once (22 f32), writes cout fp16 per output row
         const double bytes = (double)p->d120.valid() * 88 + (double)dout.valid() * c * 2;
         launch(i == 0 ? PC_NOISE0 : PC_NOISE1, 2.0 * 22 * nc.k * c * (double)dout.valid(), bytes, [&] {
             return launch_noise_conv(p->spec.as<float>(), kSpecLd, p->d120.l, p->d120.start_d.as<int64_t>(),
-                                     p->d120.len_d.as<int64_t>(),
-                                     nc.w.as<float>(), nc.wp.p ? nc.wp.as<uint16_t>() : nullptr, nc.b.as<float>(), nc.cout,
-                                     nc.k, nc.stride, nc.pad, xs, c, tn.dev(), part(), s);
+                                     p->d120.len_d.as<int64_t>(), nc.wp.as<uint16_t>(), nc.b.as<float>(), nc.cout,
+                                     nc.k, nc.stride, nc.pad, xs, c, tn.dev(), tile_rows, part(), s);
         });
         snake_block(m.noise_res[i], xs, p->hn.as<float>(), dout, &tn, cf(9), cf(10), true);
         region = reg;

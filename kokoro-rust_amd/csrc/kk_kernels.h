@@ -137,20 +137,21 @@ hipError_t launch_copy_cols(const float* src, int64_t src_ld, int c, float* dst,
 hipError_t launch_adain_pool(const float* x, int64_t ld, int c, const Coef* coef, const int32_t* col_n,
                              int64_t ln, const float* pw, const float* pb, const int32_t* col_2, uint16_t* out,
                              int64_t out_ld, hipStream_t s);
-// Strided f32 conv 22 -> cout (noise_convs.0: k12 s6 p3; noise_convs.1: k1) on the spectrum, rows
-// outside the tile's item span [in_start, in_start + in_len) read as 0 (the reference's gap mask),
-// over item-aligned tiles t (<= kNoiseTile output rows each; rows outside the tiles are not
-// written), with the statistics partial of each tile ([tile][cout], shift = bias) for the next
-// layer's AdaIN.  wt: [k][22][cout] f32 (VALU kernel); wp: the noise_convs.0 weights split into
-// bf16 roundings and remainders and packed as A fragments for the split-precision matrix-core
-// kernel ([32-row tile][18 K steps][rounding, remainder][64 lanes][8] bf16, K = 24 tap + channel
-// with channels 22 and 23 zero), or null.  y is stored as fp16
+// Strided conv 22 -> cout on the spectrum at f32 accuracy (split-bf16 matrix-core products) --
+// noise_convs.0: k12 s6 p3 over item-aligned tiles of kNoiseTile output rows; noise_convs.1: k1
+// over tiles of kNoiseTile1 rows (tile_rows: the width the tiles t were built with, checked) --
+// rows outside the tile's item span [in_start, in_start + in_len) read as 0 (the reference's gap
+// mask), rows outside the tiles not written, with the statistics partial of each tile
+// ([tile][cout], shift = bias) for the next layer's AdaIN.  wp: the weights split into bf16
+// roundings and remainders, packed as A fragments ([32-row tile][K step][rounding,
+// remainder][64 lanes][8] bf16; noise_convs.0: 18 K steps, k = 24 tap + channel; noise_convs.1:
+// 2 K steps, k = channel; channels 22 and up zero).  y is stored as fp16
 // (the noise branch's residual stream; the statistics describe the f32 values).
-constexpr int kNoiseTile = 64;
+constexpr int kNoiseTile = 64, kNoiseTile1 = 128;
 hipError_t launch_noise_conv(const float* spec, int64_t spec_ld, int64_t l_in, const int64_t* in_start,
-                             const int64_t* in_len,
-                             const float* wt, const uint16_t* wp, const float* b, int cout, int k, int stride, int pad,
-                             uint16_t* y, int64_t y_ld, TilesDev t, StatPart* part, hipStream_t s);
+                             const int64_t* in_len, const uint16_t* wp, const float* b, int cout, int k, int stride,
+                             int pad, uint16_t* y, int64_t y_ld, TilesDev t, int tile_rows, StatPart* part,
+                             hipStream_t s);
 // SineGen phase_pre: per item and harmonic, f64 cumulative sum of the 1/300-downsampled rad values.
 hipError_t launch_phase_pre(const float* f0, const int64_t* start2, const int64_t* len2, int nb,
                             const float* rand_ini, float* pp, int64_t pp_ld, hipStream_t s);

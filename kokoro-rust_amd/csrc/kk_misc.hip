@@ -273,99 +273,123 @@ __global__ __launch_bounds__(256) void adain_pool_kernel(const float* __restrict
 // ------------------------------------------------------------------ noise convolutions (f32)
 // conv1d_strided / conv_direct_tiled semantics (kernels/kokoro.cu:517-617): y = b + sum_k sum_ci
 // w x with the spectrum's gap rows zeroed first (src/gpu_batch.rs:363-365).  A block computes
-// noise_convs (22 -> COUT channels, f32 like the reference's sgemm route).  A block computes 64
-// output rows x COUT channels; thread = 4 consecutive channels x TT rows, so every weight load is
-// one coalesced float4 across the wave and every input value is a wave-uniform LDS broadcast.
-// Weights are pre-transposed to [k][22][COUT].  Accumulation order per output: bias, then taps
-// ascending, channels ascending within a tap (f32 FMA).  A block computes one item-aligned tile
-// (<= 64 output rows of one item) and, for the next layer's AdaIN, the tile's statistics partial
-// per channel (sums of v - b over its rows, shift b: the bias is a value of the data's scale).
 constexpr int kNcRows = kNoiseTile;
-constexpr int kNcMaxWin = (kNcRows - 1) * 6 + 12;
-template <int COUT, int TT, int WIN>
-__global__ __launch_bounds__(256) void noise_conv_kernel(const float* __restrict__ spec, int64_t spec_ld, int64_t l_in,
-                                                         const int64_t* __restrict__ in_start,
-                                                         const int64_t* __restrict__ in_len,
-                                                         const float* __restrict__ wt, const float* __restrict__ b,
-                                                         int k, int stride, int pad, uint16_t* __restrict__ y,
-                                                         int64_t y_ld, TilesDev tl, StatPart* __restrict__ part) {
-    constexpr int CQ = COUT / 4, TG = 256 / CQ;
-    static_assert(TG * TT == kNcRows, "rows per block");
-    __shared__ float xs[WIN][22];  // the input window (its size sets how many blocks share a CU)
-    __shared__ float4 red[2][TG][CQ];
+
+// noise_convs.1 (22 -> 128, k 1) on the bf16 matrix cores in split precision, as noise_convs.0
+// (below): each value and weight split into its bf16 rounding and the rounding of the remainder,
+// products accumulated in f32 as wh xh + wh xl + wl xh.  GEMM view per block: 128 output channels
+// x the <= 128 rows of one item-aligned tile, K = 22 channels padded to 32 (two steps of 16, the
+// pad zero in both operands).  Wave w owns rows 32 w .. 32 w + 31 (one 32-column tile) and all
+// 128 channels (four 32-row tiles, taken two at a time).  A lane's B fragment of step s is 8
+// consecutive channels of its row, loaded from the spectrum as two float4 and split in registers
+// (no LDS staging); the weights are A fragments packed per lane ([32-row tile][step][rounding,
+// remainder][lane] bf16x8).  The fp16 outputs go through LDS so that the tile's rows leave as
+// contiguous 16-byte runs, and the tile's statistics partial (sums of v - b and (v - b)^2 over its
+// rows, shift b: the bias is a value of the data's scale) is summed from the stored fp16 values.
+constexpr int kNc1Ld = 128 + 8;  // LDS row stride of the output tile (fp16)
+__device__ __forceinline__ bf16x8 bf16x8_of(const uint32_t (&u)[4]) {
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    return __builtin_bit_cast(bf16x8, (u32x4){u[0], u[1], u[2], u[3]});
+}
+__global__ __launch_bounds__(256) void noise_conv1_mfma_kernel(const float* __restrict__ spec, int64_t spec_ld,
+                                                               const bf16x8* __restrict__ wq,
+                                                               const float* __restrict__ b, uint16_t* __restrict__ y,
+                                                               int64_t y_ld, TilesDev tl,
+                                                               StatPart* __restrict__ part) {
+    typedef float f32x16 __attribute__((ext_vector_type(16)));
+    __shared__ __align__(16) uint16_t ys[kNoiseTile1 * kNc1Ld];
+    __shared__ float red[2][4][128];
     const int64_t t0 = tl.t0[blockIdx.x];
     const int nv = tl.n[blockIdx.x];
-    const int win = (kNcRows - 1) * stride + k;
-    const int64_t in0 = t0 * stride - pad;
-    // the tile's item: input rows outside its span are the zero padding (gap masking)
-    const int item = tl.item[blockIdx.x];
-    const int64_t i_lo = in_start[item], i_hi = i_lo + in_len[item];
-    // Stage the input window: every load of a thread is issued before the first is used (rows
-    // clamped into the buffer, the gap / range mask applied afterwards), so the window costs one
-    // memory latency rather than one per element.
-    constexpr int kPer = (WIN * 22 + 255) / 256;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, l32 = lane & 31, h = lane >> 5;
+    // this lane's row (rows past the tile read its first row; their outputs are not stored)
+    const int r = 32 * wave + l32;
+    const float* xr = spec + (t0 + (r < nv ? r : 0)) * spec_ld + 8 * h;
+    // B fragments: step 0 channels 8 h .. 8 h + 7, step 1 channels 16 + 8 h .. (22 and up zero)
+    const float4 x0 = *(const float4*)xr, x1 = *(const float4*)(xr + 4);
+    const float4 x2 = *(const float4*)(xr + 16), x3 = *(const float4*)(xr + 20);
+    bf16x8 bh[2], bl[2];
     {
-        float sv[kPer];
+        const float v[2][8] = {{x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w},
+                               {x2.x, x2.y, x2.z, x2.w, x3.x, x3.y, 0.f, 0.f}};  // 22, 23: the pad
 #pragma unroll
-        for (int kk = 0; kk < kPer; kk++) {
-            if (kk * 256 >= win * 22) break;  // uniform
-            const int i = threadIdx.x + kk * 256;
-            const int r = i / 22, ci = i - r * 22;
-            const int64_t row = min(max(in0 + r, i_lo), i_hi - 1);
-            sv[kk] = spec[row * spec_ld + ci];
-        }
+        for (int s = 0; s < 2; s++) {
+            uint32_t hi[4], lo[4];
 #pragma unroll
-        for (int kk = 0; kk < kPer; kk++) {
-            if (kk * 256 >= win * 22) break;
-            const int i = threadIdx.x + kk * 256;
-            const int r = i / 22, ci = i - r * 22;
-            const int64_t row = in0 + r;
-            if (i < win * 22) xs[r][ci] = (row >= i_lo && row < i_hi) ? sv[kk] : 0.f;
-        }
-    }
-    __syncthreads();
-    const int cq = threadIdx.x % CQ, tg = threadIdx.x / CQ;
-    const float4 bias = *(const float4*)(b + cq * 4);
-    float4 acc[TT];
-#pragma unroll
-    for (int tt = 0; tt < TT; tt++) acc[tt] = bias;
-    const int rb = tg * TT * stride;
-    for (int kk = 0; kk < k; kk++) {
-        for (int ci = 0; ci < 22; ci++) {
-            const float4 wv = *(const float4*)(wt + ((int64_t)kk * 22 + ci) * COUT + cq * 4);
-#pragma unroll
-            for (int tt = 0; tt < TT; tt++) {
-                const float x = xs[rb + tt * stride + kk][ci];
-                acc[tt].x = __builtin_fmaf(wv.x, x, acc[tt].x);
-                acc[tt].y = __builtin_fmaf(wv.y, x, acc[tt].y);
-                acc[tt].z = __builtin_fmaf(wv.z, x, acc[tt].z);
-                acc[tt].w = __builtin_fmaf(wv.w, x, acc[tt].w);
+            for (int e = 0; e < 4; e++) {
+                float a = v[s][2 * e], c = v[s][2 * e + 1];
+                if (s == 1 && h) a = 0.f, c = 0.f;  // channels 24-31: the pad
+                const uint32_t ha = f32_to_bf16_bits(a), hc = f32_to_bf16_bits(c);
+                const uint32_t la = f32_to_bf16_bits(a - __uint_as_float(ha << 16));
+                const uint32_t lc = f32_to_bf16_bits(c - __uint_as_float(hc << 16));
+                hi[e] = ha | hc << 16, lo[e] = la | lc << 16;
             }
+            bh[s] = bf16x8_of(hi), bl[s] = bf16x8_of(lo);
         }
     }
-    float4 s1 = make_float4(0.f, 0.f, 0.f, 0.f), s2 = s1;
+    // the weights: tile mt, step s, part p at wq[((mt * 2 + s) * 2 + p) * 64 + lane]
+    const bf16x8* wa = wq + lane;
 #pragma unroll
-    for (int tt = 0; tt < TT; tt++) {
-        const int r = tg * TT + tt;
-        if (r < nv) {
-            *(uint2*)(y + (t0 + r) * y_ld + cq * 4) = pack_f16x4(acc[tt]);
-            const float4 d = make_float4(acc[tt].x - bias.x, acc[tt].y - bias.y, acc[tt].z - bias.z, acc[tt].w - bias.w);
-            s1.x += d.x, s1.y += d.y, s1.z += d.z, s1.w += d.w;
-            s2.x = __builtin_fmaf(d.x, d.x, s2.x), s2.y = __builtin_fmaf(d.y, d.y, s2.y);
-            s2.z = __builtin_fmaf(d.z, d.z, s2.z), s2.w = __builtin_fmaf(d.w, d.w, s2.w);
-        }
+    for (int mp = 0; mp < 2; mp++) {  // 32-row tiles 2 mp and 2 mp + 1
+        bf16x8 a[2][2][2];  // [tile][step][part]
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int s = 0; s < 2; s++)
+#pragma unroll
+                for (int p = 0; p < 2; p++) a[t][s][p] = wa[(((2 * mp + t) * 2 + s) * 2 + p) * 64];
+        f32x16 acc[2];
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                const float4 bv = *(const float4*)(b + 32 * (2 * mp + t) + 8 * g + 4 * h);
+                acc[t][4 * g] = bv.x, acc[t][4 * g + 1] = bv.y, acc[t][4 * g + 2] = bv.z, acc[t][4 * g + 3] = bv.w;
+            }
+#pragma unroll
+        for (int s = 0; s < 2; s++)
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[t][s][0], bh[s], acc[t], 0, 0, 0);
+                acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[t][s][0], bl[s], acc[t], 0, 0, 0);
+                acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[t][s][1], bh[s], acc[t], 0, 0, 0);
+            }
+        // D: element 4 g + e of tile t is channel 32 (2 mp + t) + 8 g + 4 h + e of row l32
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int g = 0; g < 4; g++)
+                *(uint2*)(ys + r * kNc1Ld + 32 * (2 * mp + t) + 8 * g + 4 * h) =
+                    pack_f16x4(make_float4(acc[t][4 * g], acc[t][4 * g + 1], acc[t][4 * g + 2], acc[t][4 * g + 3]));
     }
-    red[0][tg][cq] = s1, red[1][tg][cq] = s2;
-    __syncthreads();
-    if (threadIdx.x < COUT) {
-        const int c = threadIdx.x, q = c / 4, e = c % 4;
-        float a1 = 0.f, a2 = 0.f;
-        for (int g = 0; g < TG; g++) {  // row groups in order
-            const float4 u = red[0][g][q], v = red[1][g][q];
-            a1 += e == 0 ? u.x : e == 1 ? u.y : e == 2 ? u.z : u.w;
-            a2 += e == 0 ? v.x : e == 1 ? v.y : e == 2 ? v.z : v.w;
+    __builtin_amdgcn_wave_barrier();  // the wave's rows written before it reads them back
+    // the wave's 32 rows, 16 bytes per lane: 4 rows per instruction, each 256 contiguous bytes
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int rr = 32 * wave + 4 * i + (lane >> 4);
+        if (rr < nv) *(uint4*)(y + (t0 + rr) * y_ld + 8 * (lane & 15)) = *(const uint4*)(ys + rr * kNc1Ld + 8 * (lane & 15));
+    }
+    // statistics of the stored values: lane: channels 2 lane, 2 lane + 1 over the wave's rows
+    {
+        const float b0 = b[2 * lane], b1 = b[2 * lane + 1];
+        float s1a = 0.f, s2a = 0.f, s1b = 0.f, s2b = 0.f;
+        const int rn = min(max(nv - 32 * wave, 0), 32);
+        for (int i = 0; i < rn; i++) {
+            const uint32_t u = *(const uint32_t*)(ys + (32 * wave + i) * kNc1Ld + 2 * lane);
+            const float va = (float)__builtin_bit_cast(_Float16, (uint16_t)(u & 0xffffu)) - b0;
+            const float vb = (float)__builtin_bit_cast(_Float16, (uint16_t)(u >> 16)) - b1;
+            s1a += va, s2a = __builtin_fmaf(va, va, s2a);
+            s1b += vb, s2b = __builtin_fmaf(vb, vb, s2b);
         }
-        part[(int64_t)blockIdx.x * COUT + c] = StatPart{a1, a2, b[c], (float)nv};
+        red[0][wave][2 * lane] = s1a, red[0][wave][2 * lane + 1] = s1b;
+        red[1][wave][2 * lane] = s2a, red[1][wave][2 * lane + 1] = s2b;
+    }
+    __syncthreads();
+    if (threadIdx.x < 128) {  // the waves' sums in order
+        const int c = threadIdx.x;
+        const float a1 = ((red[0][0][c] + red[0][1][c]) + red[0][2][c]) + red[0][3][c];
+        const float a2 = ((red[1][0][c] + red[1][1][c]) + red[1][2][c]) + red[1][3][c];
+        part[(int64_t)blockIdx.x * 128 + c] = StatPart{a1, a2, b[c], (float)nv};
     }
 }
 
@@ -961,33 +985,24 @@ hipError_t launch_adain_pool(const float* x, int64_t ld, int c, const Coef* coef
 }
 
 hipError_t launch_noise_conv(const float* spec, int64_t spec_ld, int64_t l_in, const int64_t* in_start,
-                             const int64_t* in_len, const float* wt,
-                             const uint16_t* wp, const float* b, int cout, int k, int stride, int pad, uint16_t* y,
-                             int64_t y_ld, TilesDev t, StatPart* part, hipStream_t s) {
-    const int win = (kNcRows - 1) * stride + k;
-    if (win > kNcMaxWin) return hipErrorInvalidValue;
+                             const int64_t* in_len, const uint16_t* wp, const float* b, int cout, int k, int stride,
+                             int pad, uint16_t* y, int64_t y_ld, TilesDev t, int tile_rows, StatPart* part,
+                             hipStream_t s) {
+    if (!wp) return hipErrorInvalidValue;
     if (t.count == 0) return hipSuccess;
     const dim3 grid((unsigned)t.count);
-    if (wp) {
-        // the matrix-core path: noise_convs.0's shape only, weights packed by pack_noise_conv0
-        if (cout != 256 || k != 12 || stride != 6) return hipErrorInvalidValue;
+    if (cout == 256 && k == 12 && stride == 6) {
+        if (tile_rows != kNoiseTile) return hipErrorInvalidValue;
         hipLaunchKernelGGL(noise_conv0_mfma_kernel, grid, dim3(256), 0, s, spec, spec_ld, l_in, in_start, in_len,
                            (const bf16x8*)wp, b, pad, y, y_ld, t, part);
-        return hipGetLastError();
-    }
-    // noise_convs.0 (k 12, stride 6) stages a 390-row window; noise_convs.1 (k 1) 64 rows, small
-    // enough for 16 blocks per CU
-    if (cout == 256)
-        hipLaunchKernelGGL((noise_conv_kernel<256, 16, kNcMaxWin>), grid, dim3(256), 0, s, spec, spec_ld, l_in, in_start, in_len,
-                           wt, b, k, stride, pad, y, y_ld, t, part);
-    else if (cout == 128 && win <= kNcRows)
-        hipLaunchKernelGGL((noise_conv_kernel<128, 8, kNcRows>), grid, dim3(256), 0, s, spec, spec_ld, l_in, in_start, in_len, wt,
-                           b, k, stride, pad, y, y_ld, t, part);
-    else if (cout == 128)
-        hipLaunchKernelGGL((noise_conv_kernel<128, 8, kNcMaxWin>), grid, dim3(256), 0, s, spec, spec_ld, l_in, in_start, in_len,
-                           wt, b, k, stride, pad, y, y_ld, t, part);
-    else
+    } else if (cout == 128 && k == 1 && stride == 1 && pad == 0) {
+        // output rows are input rows: every row of a tile lies inside its item
+        if (tile_rows != kNoiseTile1 || y_ld != 128) return hipErrorInvalidValue;
+        hipLaunchKernelGGL(noise_conv1_mfma_kernel, grid, dim3(256), 0, s, spec, spec_ld, (const bf16x8*)wp, b, y, y_ld,
+                           t, part);
+    } else {
         return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 
