@@ -772,6 +772,17 @@ struct kk_plan {
         }
         return *it->second;
     }
+    // the quad recurrences' schedule over the items of domain d (built on first use, like the tiles)
+    std::map<const kk::Dom*, kk::DevBuf> lstm_sched;
+    const int32_t* lstm_sched_of(const kk::Dom& d) {
+        auto it = lstm_sched.find(&d);
+        if (it == lstm_sched.end()) {
+            kk::check(!frozen, "internal: recurrence schedule requested after plan creation");
+            kk::stage_vec(ctx, lstm_sched[&d], kk::lstm_schedule(d.len.data(), (int)d.len.size()));
+            it = lstm_sched.find(&d);
+        }
+        return it->second.as<int32_t>();
+    }
     bool frozen = false;  // tables uploaded: no more staging
     kk::DevBuf src_item, src_f0, ist_item, ist_s0;
     // ids-level plans (PLAN_FULL): the stages before the decoder.  dt: the token rows by item (the
@@ -895,7 +906,7 @@ static void reset_plan(kk_plan* p, int kind, int n) {
     p->kind = kind, p->nb = n;
     p->nfr.clear(), p->a.clear();
     p->tstart.clear(), p->ntok.clear(), p->pred.clear(), p->n_att = 0;
-    p->tiles.clear();
+    p->tiles.clear(), p->lstm_sched.clear();  // views of the previous batch's staged tables
     p->frozen = false;
     p->sblk = nullptr, p->sc = 0;
     p->ln = 0, p->t_rows = 0, p->n_src = p->n_ist = 0;
@@ -1806,18 +1817,20 @@ struct Runner {
     }
     // BiLSTM recurrence over the item spans of d (gx rows through gx_row, or the spans' own rows);
     // h into out[row][0:512].  Algorithmic traffic: gx read and h written once per row, W_hh once.
-    // Each sequence runs on two CUs (launch_lstm_pair), or four for long spans (launch_lstm_quad:
-    // bit-identical), with its exchange words in `region` (one per stream that runs recurrences at
-    // the same time); KOKORO_HIP_LSTM_SINGLE=1 selects the one-CU kernel (W_hh partly streamed from
-    // L2 each step), as does a plan whose pairs or quads gave up before (lstm_single).  Test hook,
-    // read at each launch: KOKORO_HIP_TEST_LSTM_SILENT=1 keeps the second half of every pair (the
-    // second quarter of every quad) from publishing and cuts the wait to 10 us, so that they give up.
+    // Each sequence runs on four CUs (launch_lstm_quad, at most 64 quads running scheduled lists)
+    // when the longest span has at least kLstmQuadMinSteps steps (below, the quads' per-step gain
+    // does not pay for their lists), else on two (launch_lstm_pair; bit-identical), with its
+    // exchange words in `region` (one per stream that runs recurrences at the same time);
+    // KOKORO_HIP_LSTM_SINGLE=1 selects the one-CU kernel (W_hh partly streamed from L2 each step),
+    // as does a plan whose pairs or quads gave up before (lstm_single).  Test hook, read at each
+    // launch: KOKORO_HIP_TEST_LSTM_SILENT=1 keeps the second half of every pair (the second quarter
+    // of every quad) from publishing and cuts the wait to 10 us, so that they give up.
     void recur(const MLstm& l, const float* gx, const int32_t* gx_row, const Dom& d, float* out, int64_t out_ld,
                const std::string& name, int region = 0) {
         static const bool single = env_i64("KOKORO_HIP_LSTM_SINGLE", 0) != 0;
-        // four CUs per sequence when the longest span has at least kLstmQuadMinSteps steps (the
-        // quads' per-step gain outweighs their fixed cost and second wave); KOKORO_HIP_LSTM_QUAD,
-        // read at each launch: 1 always, 0 never
+        // KOKORO_HIP_LSTM_QUAD, read at each launch: 1 quads, 0 pairs for every span
+        check((int)d.len.size() == p->nb, "internal: recurrence domain");
+        const int32_t* sched = p->lstm_sched_of(d);
         int64_t longest = 0;
         for (int64_t v : d.len) longest = std::max(longest, v);
         const int64_t qsel = env_i64("KOKORO_HIP_LSTM_QUAD", -1);
@@ -1832,7 +1845,7 @@ struct Runner {
             uint64_t* x = p->u_lstmx.as<uint64_t>();
             if (quad)
                 return launch_lstm_quad(gx, 2048, gx_row, d.start_d.as<int64_t>(), d.len_d.as<int64_t>(), p->nb,
-                                        l.whh_t.as<float>(), l.bhh.as<float>(), out, out_ld,
+                                        sched, l.whh_t.as<float>(), l.bhh.as<float>(), out, out_ld,
                                         x + kk_plan::kLstmXHead + (int64_t)region * 2 * p->nb * 512, (int*)x, s,
                                         silent ? 1000 : kLstmPairWaitTicks, silent ? 1 : -1);
             return launch_lstm_pair(gx, 2048, gx_row, d.start_d.as<int64_t>(), d.len_d.as<int64_t>(), p->nb,
@@ -2327,7 +2340,7 @@ static void init_full_plan(kk_plan* p, const kk_item* items, int n) {
 
 static void release_plan_device(kk_plan* p) {
     p->drop_events();
-    p->tiles.clear();
+    p->tiles.clear(), p->lstm_sched.clear();
     for (kk::Dom* d : {&p->dn, &p->d2, &p->d20, &p->d120, &p->ds, &p->dt, &p->dtf}) d->release();
     for (DevBuf* b : p->owned()) b->release();
     p->ctx = nullptr;

@@ -2,6 +2,8 @@
 #pragma once
 #include "kk_common.h"
 
+#include <vector>
+
 namespace kk {
 
 // ---------------------------------------------------------------- tiles
@@ -238,14 +240,22 @@ hipError_t launch_lstm_pair(const float* gx, int64_t gx_ld, const int32_t* gx_ro
                             const int64_t* len, int nb, const float* whh_t, const float* bhh, float* out, int64_t out_ld,
                             uint64_t* xbuf, int* abort, hipStream_t s, uint64_t wait_ticks = kLstmPairWaitTicks,
                             int silent_half = -1);
-// Four CUs per (item, direction), each with a quarter of h and all of its W_hh rows in registers,
-// the sequences longest first; the same arguments (xbuf 2 nb x 512 words), bit-identical outputs.
-// silent_quarter >= 0 (a test hook) keeps that quarter of every quad from publishing.
-constexpr int64_t kLstmQuadMinSteps = 1024;  // the engine's choice: quads from this many steps on
+// Four CUs per (item, direction), each with a quarter of h and all of its W_hh rows in registers;
+// the same arguments (xbuf 2 nb x 512 words), bit-identical outputs.  lstm_quads(nb) quads (one
+// block per CU) run the 2 nb sequences as lists, sched = lstm_schedule(len, nb): [nq + 1] offsets,
+// then the sequence ids (2 item + direction) of each quad's list.  silent_quarter >= 0 (a test
+// hook) keeps that quarter of every quad from publishing.
+constexpr int kLstmQuads = 64;               // 256 CUs
+constexpr int64_t kLstmQuadMinSteps = 1024;  // the engine's choice: quads when a span has this many steps
+inline int lstm_quads(int nb) { return 2 * nb < kLstmQuads ? 2 * nb : kLstmQuads; }
+// Longest processing time first: the sequences by decreasing length (items by length, ties by
+// index, both directions in turn), each to the quad with the least total length so far (ties: the
+// lowest quad).
+std::vector<int32_t> lstm_schedule(const int64_t* len, int nb);
 hipError_t launch_lstm_quad(const float* gx, int64_t gx_ld, const int32_t* gx_row, const int64_t* start,
-                            const int64_t* len, int nb, const float* whh_t, const float* bhh, float* out, int64_t out_ld,
-                            uint64_t* xbuf, int* abort, hipStream_t s, uint64_t wait_ticks = kLstmPairWaitTicks,
-                            int silent_quarter = -1);
+                            const int64_t* len, int nb, const int32_t* sched, const float* whh_t, const float* bhh,
+                            float* out, int64_t out_ld, uint64_t* xbuf, int* abort, hipStream_t s,
+                            uint64_t wait_ticks = kLstmPairWaitTicks, int silent_quarter = -1);
 // Zeroes n 64-bit words.
 hipError_t launch_clear_u64(uint64_t* x, int64_t n, hipStream_t s);
 // F0_proj / N_proj: y[r] = b + w . x[r][0:c] (c = 256) on the rows with col[r] >= 0, 0 elsewhere.

@@ -10,7 +10,11 @@
 // these kernels do not write them.
 #include "kk_kernels.h"
 
+#include <algorithm>
 #include <atomic>
+#include <functional>
+#include <queue>
+#include <utility>
 
 namespace kk {
 namespace {
@@ -594,114 +598,114 @@ __global__ void __launch_bounds__(kLstmThreads) lstm_pair_kernel(const float* gx
 // publish the block's units while threads 64..255 wait for the partners' 192.  Every row's dot
 // product is summed in the pair kernel's order (the k-quarter's 64 terms in sequence, then the four
 // quarters as ((q0 + q1) + (q2 + q3)) + b_hh): the outputs are bit-identical to it.
-// The quarters of a sequence are blocks 8 apart (the same XCD under round-robin dispatch), 32
-// consecutive blocks hold 8 complete quads, and the sequences are taken longest first (each block
-// ranks the items by length, ties by index): config 4's 128 sequences need 512 blocks, two waves
-// on 256 CUs, and the longest start in the first.  A block whose partners are not resident yet
-// waits for CUs that finishing quads release (nothing a quad waits for depends on a later one).
-// Every wait is bounded as in the pair kernel.
+// The quarters of a quad are blocks 8 apart (the same XCD under round-robin dispatch) and 32
+// consecutive blocks hold 8 complete quads; a launch has at most kLstmQuads quads (one block per
+// CU), and each quad runs a list of sequences one after another, from a schedule the host computes
+// at plan creation: longest first, each sequence to the quad with the least work so far -- the
+// longest start at once, and the short ones follow on the quads that finish first, with no second
+// wave of blocks waiting for CUs.  A quad reloads its W_hh rows only when the direction changes;
+// every sequence starts from h = c = 0 and has its own exchange words.  A block whose partners
+// are not resident yet waits for CUs that finishing quads release (nothing a quad waits for
+// depends on a later one).  Every wait is bounded as in the pair kernel.
+//   sched: [nq + 1] list offsets, then the sequence ids (2 item + direction) of the quads' lists.
 __global__ void __launch_bounds__(kLstmThreads) lstm_quad_kernel(const float* gx, int64_t gx_ld, const int32_t* gx_row,
-                                                                 const int64_t* start, const int64_t* len, int nseq,
-                                                                 const float* whh_t, const float* bhh, float* out,
-                                                                 int64_t out_ld, uint64_t* xbuf, int* abort,
-                                                                 uint64_t wait_ticks, int silent_quarter) {
+                                                                 const int64_t* start, const int64_t* len,
+                                                                 const int32_t* sched, int nq, const float* whh_t,
+                                                                 const float* bhh, float* out, int64_t out_ld,
+                                                                 uint64_t* xbuf, int* abort, uint64_t wait_ticks,
+                                                                 int silent_quarter) {
     __shared__ float part[4][256];  // partial dot products per k-quarter, local rows g 64 + u
     __shared__ float hs[kH];        // h of the previous step
-    __shared__ int gave_up, seq_s;
+    __shared__ int gave_up;
     const int B = blockIdx.x, qb = (B >> 3) & 3;
-    const int rank = (B >> 5) * 8 + (B & 7);
-    if (rank >= nseq) return;  // the quad's other quarters return too
+    const int quad = (B >> 5) * 8 + (B & 7);
+    if (quad >= nq) return;  // the quad's other quarters return too
     const int t = threadIdx.x, q = t >> 7, c = t & 127;
-    // the sequence of this rank: items by length, longest first (ties by index), both directions
-    const int nitems = nseq >> 1;
-    if (t == 0) gave_up = 0, seq_s = -1;
-    __syncthreads();
-    for (int i = t; i < nitems; i += kLstmThreads) {
-        const int64_t li = len[i];
-        int r = 0;
-        for (int j = 0; j < nitems; j++) {
-            const int64_t lj = len[j];
-            r += (lj > li || (lj == li && j < i)) ? 1 : 0;
-        }
-        if (r == (rank >> 1)) seq_s = 2 * i + (rank & 1);
-    }
-    __syncthreads();
-    const int seq = seq_s;
-    const int item = seq >> 1, dir = seq & 1;
-    const int64_t s0 = start[item], n = len[item];
+    if (t == 0) gave_up = 0;
     const int g = c >> 5, u0 = 2 * (c & 31);  // this thread's rows: gate g, units u0, u0 + 1 of the quarter
-    const float* W = whh_t + (int64_t)dir * kH * 4 * kH + g * kH + 64 * qb + u0;
-    float2 wr[64];
-#pragma unroll
-    for (int k = 0; k < 64; k++) wr[k] = *(const float2*)(W + (int64_t)(64 * q + k) * 4 * kH);
-    float cst = 0.f, bh[4];
-    if (t < 64) {
-#pragma unroll
-        for (int gg = 0; gg < 4; gg++) bh[gg] = bhh[dir * 4 * kH + gg * kH + 64 * qb + t];
-    }
-    if (t < kH) hs[t] = 0.f;
-    __syncthreads();
-    const float* hq = hs + 64 * q;
-    uint64_t* xw = xbuf + (int64_t)seq * 512 + qb * 128;  // [parity][64] this quarter's words
     // threads 64..255: the partner quarter and unit they wait for
     const int tp = t - 64, pq = (qb + 1 + tp / 64) & 3, pu = tp & 63;
-    const uint64_t* xr = xbuf + (int64_t)seq * 512 + pq * 128 + pu;
-    for (int64_t step = 0; step < n; step++) {
-        const int64_t row = s0 + (dir == 0 ? step : n - 1 - step);
-        float gxv[4];
+    const float* hq = hs + 64 * q;
+    float2 wr[64];
+    int wdir = -1;
+    const int li_end = sched[quad + 1];
+    for (int li = sched[quad]; li < li_end; li++) {
+        const int seq = sched[nq + 1 + li];
+        const int item = seq >> 1, dir = seq & 1;
+        const int64_t s0 = start[item], n = len[item];
+        if (dir != wdir) {
+            const float* W = whh_t + (int64_t)dir * kH * 4 * kH + g * kH + 64 * qb + u0;
+#pragma unroll
+            for (int k = 0; k < 64; k++) wr[k] = *(const float2*)(W + (int64_t)(64 * q + k) * 4 * kH);
+            wdir = dir;
+        }
+        float cst = 0.f, bh[4];
         if (t < 64) {
-            const int64_t grow = gx_row ? (int64_t)gx_row[row] : row;
 #pragma unroll
-            for (int gg = 0; gg < 4; gg++) gxv[gg] = gx[grow * gx_ld + dir * 4 * kH + gg * kH + 64 * qb + t];
+            for (int gg = 0; gg < 4; gg++) bh[gg] = bhh[dir * 4 * kH + gg * kH + 64 * qb + t];
         }
-        float2 acc = make_float2(0.f, 0.f);
-#pragma unroll
-        for (int k = 0; k < 64; k += 4) {
-            const float4 h4 = *(const float4*)(hq + k);
-            const float hv[4] = {h4.x, h4.y, h4.z, h4.w};
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                acc.x = fmaf(wr[k + e].x, hv[e], acc.x);
-                acc.y = fmaf(wr[k + e].y, hv[e], acc.y);
-            }
-        }
-        *(float2*)(&part[q][g * 64 + u0]) = acc;
+        if (t < kH) hs[t] = 0.f;  // every read of the previous sequence's h ended before its last barrier
         __syncthreads();
-        const uint64_t tag = (uint64_t)(step + 1) << 32;
-        if (t < 64) {
-            float gate[4];
+        uint64_t* xw = xbuf + (int64_t)seq * 512 + qb * 128;  // [parity][64] this quarter's words
+        const uint64_t* xr = xbuf + (int64_t)seq * 512 + pq * 128 + pu;
+        for (int64_t step = 0; step < n; step++) {
+            const int64_t row = s0 + (dir == 0 ? step : n - 1 - step);
+            float gxv[4];
+            if (t < 64) {
+                const int64_t grow = gx_row ? (int64_t)gx_row[row] : row;
 #pragma unroll
-            for (int gg = 0; gg < 4; gg++) {
-                const int r = gg * 64 + t;
-                gate[gg] = gxv[gg] + (((part[0][r] + part[1][r]) + (part[2][r] + part[3][r])) + bh[gg]);
+                for (int gg = 0; gg < 4; gg++) gxv[gg] = gx[grow * gx_ld + dir * 4 * kH + gg * kH + 64 * qb + t];
             }
-            const float ig = sigmoid(gate[0]), fg = sigmoid(gate[1]), gg2 = tanhf(gate[2]), og = sigmoid(gate[3]);
-            cst = fg * cst + ig * gg2;
-            const float h = og * tanhf(cst);
-            if (qb != silent_quarter)
-                __hip_atomic_store(xw + (step & 1) * 64 + t, tag | __float_as_uint(h), __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
-            hs[64 * qb + t] = h;
-            out[row * out_ld + dir * kH + 64 * qb + t] = h;
-        } else if (t < 256) {
-            const uint64_t* src = xr + (step & 1) * 64;
-            const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-            uint64_t w;
-            for (uint32_t spin = 1;; spin++) {
-                w = __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                if ((w & 0xffffffff00000000ull) == tag) break;
-                if ((spin & 255) == 0 && (__hip_atomic_load(abort, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0 ||
-                                          __builtin_amdgcn_s_memrealtime() - t0 > wait_ticks)) {
-                    gave_up = 1;
-                    break;
+            float2 acc = make_float2(0.f, 0.f);
+#pragma unroll
+            for (int k = 0; k < 64; k += 4) {
+                const float4 h4 = *(const float4*)(hq + k);
+                const float hv[4] = {h4.x, h4.y, h4.z, h4.w};
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    acc.x = fmaf(wr[k + e].x, hv[e], acc.x);
+                    acc.y = fmaf(wr[k + e].y, hv[e], acc.y);
                 }
             }
-            hs[64 * pq + pu] = __uint_as_float((uint32_t)w);
-        }
-        __syncthreads();
-        if (gave_up) {
-            if (t == 0) __hip_atomic_store(abort, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            return;
+            *(float2*)(&part[q][g * 64 + u0]) = acc;
+            __syncthreads();
+            const uint64_t tag = (uint64_t)(step + 1) << 32;
+            if (t < 64) {
+                float gate[4];
+#pragma unroll
+                for (int gg = 0; gg < 4; gg++) {
+                    const int r = gg * 64 + t;
+                    gate[gg] = gxv[gg] + (((part[0][r] + part[1][r]) + (part[2][r] + part[3][r])) + bh[gg]);
+                }
+                const float ig = sigmoid(gate[0]), fg = sigmoid(gate[1]), gg2 = tanhf(gate[2]), og = sigmoid(gate[3]);
+                cst = fg * cst + ig * gg2;
+                const float h = og * tanhf(cst);
+                if (qb != silent_quarter)
+                    __hip_atomic_store(xw + (step & 1) * 64 + t, tag | __float_as_uint(h), __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+                hs[64 * qb + t] = h;
+                out[row * out_ld + dir * kH + 64 * qb + t] = h;
+            } else if (t < 256) {
+                const uint64_t* src = xr + (step & 1) * 64;
+                const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+                uint64_t w;
+                for (uint32_t spin = 1;; spin++) {
+                    w = __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    if ((w & 0xffffffff00000000ull) == tag) break;
+                    if ((spin & 255) == 0 &&
+                        (__hip_atomic_load(abort, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0 ||
+                         __builtin_amdgcn_s_memrealtime() - t0 > wait_ticks)) {
+                        gave_up = 1;
+                        break;
+                    }
+                }
+                hs[64 * pq + pu] = __uint_as_float((uint32_t)w);
+            }
+            __syncthreads();
+            if (gave_up) {
+                if (t == 0) __hip_atomic_store(abort, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                return;
+            }
         }
     }
 }
@@ -845,18 +849,45 @@ hipError_t launch_lstm_pair(const float* gx, int64_t gx_ld, const int32_t* gx_ro
 }
 
 hipError_t launch_lstm_quad(const float* gx, int64_t gx_ld, const int32_t* gx_row, const int64_t* start,
-                            const int64_t* len, int nb, const float* whh_t, const float* bhh, float* out, int64_t out_ld,
-                            uint64_t* xbuf, int* abort, hipStream_t s, uint64_t wait_ticks, int silent_quarter) {
+                            const int64_t* len, int nb, const int32_t* sched, const float* whh_t, const float* bhh,
+                            float* out, int64_t out_ld, uint64_t* xbuf, int* abort, hipStream_t s, uint64_t wait_ticks,
+                            int silent_quarter) {
     if (nb <= 0) return hipSuccess;
-    if (!xbuf || !abort || wait_ticks == 0) return hipErrorInvalidValue;
-    const int nseq = 2 * nb;
+    if (!xbuf || !abort || !sched || wait_ticks == 0) return hipErrorInvalidValue;
+    const int nseq = 2 * nb, nq = lstm_quads(nb);
     const int64_t words = (int64_t)nseq * 512;
     hipLaunchKernelGGL(lstm_exchange_clear_kernel, dim3((unsigned)ceil_div(words, 256)), dim3(256), 0, s, xbuf, words);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(lstm_quad_kernel, dim3((unsigned)(ceil_div(nseq, 8) * 32)), dim3(kLstmThreads), 0, s, gx, gx_ld,
-                       gx_row, start, len, nseq, whh_t, bhh, out, out_ld, xbuf, abort, wait_ticks, silent_quarter);
+    hipLaunchKernelGGL(lstm_quad_kernel, dim3((unsigned)(ceil_div(nq, 8) * 32)), dim3(kLstmThreads), 0, s, gx, gx_ld,
+                       gx_row, start, len, sched, nq, whh_t, bhh, out, out_ld, xbuf, abort, wait_ticks, silent_quarter);
     return hipGetLastError();
+}
+
+std::vector<int32_t> lstm_schedule(const int64_t* len, int nb) {
+    const int nq = lstm_quads(nb);
+    std::vector<int32_t> items(nb);
+    for (int i = 0; i < nb; i++) items[i] = i;
+    std::stable_sort(items.begin(), items.end(), [&](int a, int b) { return len[a] > len[b]; });
+    typedef std::pair<int64_t, int> Load;  // (total length, quad): the least first, ties by quad
+    std::priority_queue<Load, std::vector<Load>, std::greater<Load>> free_q;
+    for (int q = 0; q < nq; q++) free_q.push(Load{0, q});
+    std::vector<std::vector<int32_t>> lists(nq);
+    for (int i : items)
+        for (int d = 0; d < 2; d++) {
+            const Load l = free_q.top();
+            free_q.pop();
+            lists[l.second].push_back(2 * i + d);
+            free_q.push(Load{l.first + len[i], l.second});
+        }
+    std::vector<int32_t> out(nq + 1 + 2 * nb);
+    int o = 0;
+    for (int q = 0; q < nq; q++) {
+        out[q] = o;
+        for (int32_t sq : lists[q]) out[nq + 1 + o++] = sq;
+    }
+    out[nq] = o;
+    return out;
 }
 
 hipError_t launch_clear_u64(uint64_t* x, int64_t n, hipStream_t s) {

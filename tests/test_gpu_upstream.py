@@ -307,18 +307,20 @@ def one_cu_run(full_run, tmp_path_factory):
 
 
 def test_lstm_pair_wait_falls_back_to_one_cu(full_ctx, full_run, one_cu_run):
-    """The two-CU recurrence's bounded wait, forced from the host: with KOKORO_HIP_TEST_LSTM_SILENT=1
-    the second half of every pair publishes nothing and the wait limit is 10 us, so every pair gives
-    up and its launch ends.  The call then runs the forward again on the one-CU kernel (which waits
-    on no other block) and succeeds: durations and audio bit-identical to a process that used the
-    one-CU kernel from the start.  The next call without the hook is back on the pairs and gives the
-    first call's audio bit for bit."""
+    """The two-CU recurrence (this batch's spans are short: the default; KOKORO_HIP_LSTM_QUAD=0 forces
+    it) and its bounded wait, forced from the host: with KOKORO_HIP_TEST_LSTM_SILENT=1 the second
+    half of every pair publishes nothing and the wait limit is 10 us, so every pair gives up and its
+    launch ends.  The call then runs the forward again on the one-CU kernel (which waits on no other
+    block) and succeeds: durations and audio bit-identical to a process that used the one-CU kernel
+    from the start.  The next call without the hooks gives the first call's audio bit for bit."""
     items, audio, durs, _ = full_run
+    os.environ["KOKORO_HIP_LSTM_QUAD"] = "0"
     os.environ["KOKORO_HIP_TEST_LSTM_SILENT"] = "1"
     try:
         res = full_ctx.forward_batch(items)
     finally:
         del os.environ["KOKORO_HIP_TEST_LSTM_SILENT"]
+        del os.environ["KOKORO_HIP_LSTM_QUAD"]
     for b, (a, d) in enumerate(res):
         assert np.array_equal(d, one_cu_run[f"dur{b}"]) and np.array_equal(a, one_cu_run[f"audio{b}"]), b
     res = full_ctx.forward_batch(items)
@@ -350,6 +352,26 @@ def test_lstm_quad_matches_pair(full_ctx, full_run, one_cu_run):
     res = full_ctx.forward_batch(items)
     for (a, d), a2, d2 in zip(res, audio, durs):
         assert np.array_equal(d, d2) and np.array_equal(a, a2)
+
+
+def test_lstm_quad_lists_match_pairs(full_ctx):
+    """More sequences than quads: 40 items are 80 sequences on 64 quads, so 16 quads run two
+    sequences one after another (the schedule gives the short ones to the quads that finish first)
+    -- some of them in the other direction, with the W_hh rows reloaded.  Durations and audio equal
+    the two-CU kernel's (every sequence on its own pair) bit for bit."""
+    from kokoro_hip import workloads
+    rng = np.random.default_rng(46)
+    items = workloads.small_ids_items(46, [int(n) for n in rng.integers(3, 40, 40)])
+    res = {}
+    for sel in ("1", "0"):  # quads, pairs
+        os.environ["KOKORO_HIP_LSTM_QUAD"] = sel
+        try:
+            res[sel] = full_ctx.forward_batch(items)
+        finally:
+            del os.environ["KOKORO_HIP_LSTM_QUAD"]
+    quads, pairs = res["1"], res["0"]
+    for b, ((a, d), (a2, d2)) in enumerate(zip(quads, pairs)):
+        assert np.array_equal(d, d2) and np.array_equal(a, a2), b
 
 
 def test_lstm_abort_falls_back_in_every_result_path(full_ctx, full_run, one_cu_run):
