@@ -521,48 +521,36 @@ __global__ __launch_bounds__(256, 4) void noise_conv0_mfma_kernel(const float* _
         step(c + 1, w1, w0);
     }
     // D layout: element 4 g + r of tile (mi, ni) is channel 64 wave + 32 mi + 8 g + 4 h + r of
-    // output column t0 + 32 ni + l32
-    // Stores, and the tile's statistics partial (sums of v - b over its rows, per channel): each
-    // lane sums its two columns and its neighbour's (a DPP lane swap); the 16 lane pairs of a
-    // channel are then added through LDS (the input window's space, once every wave is done with
-    // it), in order.  Each accumulator is read once.
-    const bool ok0 = l32 < nv, ok1 = 32 + l32 < nv;
-    constexpr int kRl = 257;  // [2 statistics][16 lane pairs][256 channels + 1]
-    static_assert(2 * 16 * kRl * 4 <= (int)sizeof(xs), "reduction buffer");
-    float* red = (float*)xs;
-    auto pair_sum = [](float v) {  // v + v of lane l ^ 1 (quad_perm [1, 0, 3, 2])
-        return v + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));
-    };
+    // output column t0 + 32 ni + l32.  The fp16 outputs go through the window's space (once every
+    // wave is done with it) so that each output row leaves as 512 contiguous bytes, and the tile's
+    // statistics partial (sums of v - b and (v - b)^2 over its rows, per channel) is summed from
+    // the stored fp16 values.
+    constexpr int kOutLd = 256 + 8;  // LDS row stride of the output tile (fp16)
+    static_assert(kNcRows * kOutLd <= 2 * kNc0Plane, "the output tile fits the window's space");
     __syncthreads();
 #pragma unroll
     for (int mi = 0; mi < 2; mi++)
 #pragma unroll
-        for (int g = 0; g < 4; g++) {
-            const int c0 = wave * 64 + mi * 32 + 8 * g + 4 * h;
-            const float4 v0 = make_float4(acc[mi][0][4 * g], acc[mi][0][4 * g + 1], acc[mi][0][4 * g + 2],
-                                          acc[mi][0][4 * g + 3]);
-            const float4 v1 = make_float4(acc[mi][1][4 * g], acc[mi][1][4 * g + 1], acc[mi][1][4 * g + 2],
-                                          acc[mi][1][4 * g + 3]);
-            if (ok0) *(uint2*)(y + (t0 + l32) * y_ld + c0) = pack_f16x4(v0);
-            if (ok1) *(uint2*)(y + (t0 + 32 + l32) * y_ld + c0) = pack_f16x4(v1);
-            const float4 bv = *(const float4*)(b + c0);
-            const float e0[4] = {v0.x - bv.x, v0.y - bv.y, v0.z - bv.z, v0.w - bv.w};
-            const float e1[4] = {v1.x - bv.x, v1.y - bv.y, v1.z - bv.z, v1.w - bv.w};
+        for (int ni = 0; ni < 2; ni++)
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const float d0 = ok0 ? e0[r] : 0.f, d1 = ok1 ? e1[r] : 0.f;
-                const float p1 = pair_sum(d0 + d1), p2 = pair_sum(__builtin_fmaf(d1, d1, d0 * d0));
-                if ((l32 & 1) == 0) {
-                    red[(l32 >> 1) * kRl + c0 + r] = p1;
-                    red[(16 + (l32 >> 1)) * kRl + c0 + r] = p2;
-                }
-            }
-            __builtin_amdgcn_sched_barrier(0);  // one group at a time: registers stay at the main loop's
-        }
+            for (int g = 0; g < 4; g++)
+                *(uint2*)(xs + (32 * ni + l32) * kOutLd + 64 * wave + 32 * mi + 8 * g + 4 * h) = pack_f16x4(
+                    make_float4(acc[mi][ni][4 * g], acc[mi][ni][4 * g + 1], acc[mi][ni][4 * g + 2], acc[mi][ni][4 * g + 3]));
     __syncthreads();
+    // rows of 512 bytes: 32 lanes of 16 bytes per row, 8 rows per pass of the block
+#pragma unroll
+    for (int i = 0; i < kNcRows / 8; i++) {
+        const int r = 8 * i + (threadIdx.x >> 5), q = threadIdx.x & 31;
+        if (r < nv) *(uint4*)(y + (t0 + r) * y_ld + 8 * q) = *(const uint4*)(xs + r * kOutLd + 8 * q);
+    }
+    // statistics: thread = channel, every row in order
+    const float bc = b[threadIdx.x];
     float a1 = 0.f, a2 = 0.f;
-    for (int l = 0; l < 16; l++) a1 += red[l * kRl + threadIdx.x], a2 += red[(16 + l) * kRl + threadIdx.x];
-    part[(int64_t)blockIdx.x * 256 + threadIdx.x] = StatPart{a1, a2, b[threadIdx.x], (float)nv};
+    for (int r = 0; r < nv; r++) {
+        const float d = (float)__builtin_bit_cast(_Float16, xs[r * kOutLd + threadIdx.x]) - bc;
+        a1 += d, a2 = __builtin_fmaf(d, d, a2);
+    }
+    part[(int64_t)blockIdx.x * 256 + threadIdx.x] = StatPart{a1, a2, bc, (float)nv};
 }
 
 // ------------------------------------------------------------------ SineGen (kernels/kokoro.cu:188-254)
