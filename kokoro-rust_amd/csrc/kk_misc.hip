@@ -635,8 +635,10 @@ __device__ __forceinline__ void noise_pair(uint64_t seed, uint64_t i, float& n0,
     const float u2 = (float)((x >> 16) & 0xFFFFFFull) * (1.0f / 16777216.0f);
     const float r = sqrtf(-2.0f * logf(u1));
     const float th = 6.2831855f * u2;
-    n0 = r * cosf(th);
-    n1 = r * sinf(th);
+    float sn, cs;
+    sincosf(th, &sn, &cs);
+    n0 = r * cs;
+    n1 = r * sn;
 }
 
 // har[t] of one item (sine_har_source, kernels/kokoro.cu:228-254).
