@@ -331,6 +331,7 @@ __global__ __launch_bounds__(256) void noise_conv1_mfma_kernel(const float* __re
     const bf16x8* wa = wq + lane;
 #pragma unroll
     for (int mp = 0; mp < 2; mp++) {  // 32-row tiles 2 mp and 2 mp + 1
+        __builtin_amdgcn_sched_barrier(0);  // one pair's weights live at a time (4 blocks per CU)
         bf16x8 a[2][2][2];  // [tile][step][part]
 #pragma unroll
         for (int t = 0; t < 2; t++)
